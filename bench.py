@@ -1,0 +1,317 @@
+#!/usr/bin/env python3
+"""Throughput of the fused per-layer kernels on one MI355X.
+
+Workload ("C5"): the memory-bound chain of one
+Llama-3-8B-shaped decoder layer in fp16 over a T=8192-token batch, in the order
+of the reference's fp16_layer_forward (src/fp16_forward.cu:167-223), GEMMs
+and attention excluded:
+
+  1. residual add + attention RMSNorm   x[8192,4096] += d; y = rmsnorm(x)
+  2. RoPE, Q and K in one launch        Q[8192,32,128], K[8192,8,128], theta 5e5, rotate-half
+  3. paged KV append                    K,V[8192,8,128] -> 512 blocks of 16 (pool of 32 layers)
+  4. residual add + FFN RMSNorm         as 1
+  5. SwiGLU                             gate, up [8192,14336] -> out
+
+One step = one pass of that chain.  Inputs are synthetic (torch.randn on the
+device), resident in HBM before timing.  Three buffer sets (~1 GB each) are
+rotated step to step so no input is still in the 256 MB MALL; the KV append
+rotates over the 32 pool layers.  value = algorithmic bytes of the chain
+(each input read once, each output written once) / wall time per step.
+
+The embedding gather (once per forward, not per layer) is timed separately and
+reported under "kernels".  The roofline entry is for the dominant kernel,
+SwiGLU fp16 [8192 x 14336]: 3 x 8192 x 14336 x 2 B = 704,643,072 B per launch.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "quant-lib_amd"))
+
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E peak, GB/s
+T, D, HQ, HKV, HD, F = 8192, 4096, 32, 8, 128, 14336
+VOCAB, THETA, EPS, L_POOL, PAGE = 32000, 5e5, 1e-5, 32, 16
+NSETS = 3
+
+BYTES = {
+    "add_rmsnorm_f16": 4 * T * D * 2 + 2 * D,                     # read x,d; write x',y; w
+    "rope_f16": 2 * T * (HQ + HKV) * HD * 2,                      # in-place read+write Q,K
+    "paged_kv_append_f16": 4 * T * HKV * HD * 2 + 4 * T,          # read K,V; write K,V; slots
+    "swiglu_f16": 3 * T * F * 2,                                  # read gate,up; write out
+    "embed_f16": 2 * T * D * 2 + 4 * T,                           # read rows; write out; ids
+}
+CHAIN = ["add_rmsnorm_f16", "rope_f16", "paged_kv_append_f16", "add_rmsnorm_f16", "swiglu_f16"]
+CHAIN_BYTES = sum(BYTES[k] for k in CHAIN)
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--breakdown-reps", type=int, default=30)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="target CPU time of the oracle baseline sample (0 = skip)")
+    ap.add_argument("--traffic-file", default=str(ROOT / "profiles" / "pmc_traffic.json"))
+    return ap.parse_args()
+
+
+class Chain:
+    """Device buffers of the C5 layer chain and the launches of one step."""
+
+    def __init__(self, ql, torch):
+        self.ql, self.torch = ql, torch
+        dev = torch.device("cuda:0")
+        g = torch.Generator(device=dev)
+        g.manual_seed(0x51A10005)
+        h = torch.float16
+
+        def randn(*shape, clip=None):
+            t = torch.randn(*shape, generator=g, device=dev, dtype=torch.float32)
+            if clip is not None:
+                t.clamp_(-clip, clip)
+            return t.to(h)
+
+        self.sets = []
+        for _ in range(NSETS):
+            s = {
+                "x": randn(T, D), "d1": randn(T, D), "d2": randn(T, D),
+                "y": torch.empty(T, D, dtype=h, device=dev),
+                "q": randn(T, HQ * HD), "k": randn(T, HKV * HD), "v": randn(T, HKV * HD),
+                "gate": randn(T, F, clip=8.0), "up": randn(T, F, clip=8.0),
+                "out": torch.empty(T, F, dtype=h, device=dev),
+            }
+            self.sets.append(s)
+        self.w_attn = (torch.rand(D, generator=g, device=dev) + 0.5).to(h)
+        self.w_ffn = (torch.rand(D, generator=g, device=dev) + 0.5).to(h)
+        # paged pool: 512 blocks of [32 layers, 16, 8, 128] fp16 (1 MiB each) per K and V
+        self.nb = T // PAGE
+        blk = L_POOL * PAGE * HKV * HD
+        self.kpool = torch.empty(self.nb * blk, dtype=h, device=dev)
+        self.vpool = torch.empty(self.nb * blk, dtype=h, device=dev)
+        self.kptrs = torch.tensor([self.kpool.data_ptr() + 2 * blk * b for b in range(self.nb)],
+                                  dtype=torch.int64, device=dev)
+        self.vptrs = torch.tensor([self.vpool.data_ptr() + 2 * blk * b for b in range(self.nb)],
+                                  dtype=torch.int64, device=dev)
+        # fresh-pool block order 0,1,2,... (LIFO allocator of src/paged_kvcache.cu:49-53)
+        self.slots = torch.arange(T, dtype=torch.int32, device=dev)
+        # embedding table and ids (gather timed separately)
+        self.table = randn(VOCAB, D)
+        self.ids = torch.randint(0, VOCAB, (T,), generator=g, device=dev, dtype=torch.int32)
+        self.emb_out = [torch.empty(T, D, dtype=h, device=dev) for _ in range(NSETS)]
+        self.stream = torch.cuda.current_stream().cuda_stream
+        self.step_no = 0
+
+    # one launch per kernel of the chain ------------------------------------------------
+    def k_add_rmsnorm(self, s, which):
+        self.ql.call("ql_add_rmsnorm_f16", s["x"].data_ptr(), s[which].data_ptr(),
+                     (self.w_attn if which == "d1" else self.w_ffn).data_ptr(), s["y"].data_ptr(),
+                     T, D, EPS, self.stream)
+
+    def k_rope(self, s):
+        self.ql.call("ql_rope_f16", s["q"].data_ptr(), s["k"].data_ptr(), T, HQ, HKV, HD, HQ * HD,
+                     HKV * HD, None, 0, THETA, self.ql.ROPE_HALF, self.stream)
+
+    def k_paged(self, s, layer):
+        self.ql.call("ql_paged_kv_append_f16", self.kptrs.data_ptr(), self.vptrs.data_ptr(), self.nb,
+                     self.slots.data_ptr(), s["k"].data_ptr(), s["v"].data_ptr(), T, layer, L_POOL,
+                     HKV, HD, self.stream)
+
+    def k_swiglu(self, s):
+        self.ql.call("ql_swiglu_f16", s["gate"].data_ptr(), s["up"].data_ptr(), s["out"].data_ptr(),
+                     T, F, self.stream)
+
+    def k_embed(self, i):
+        self.ql.call("ql_embed_f16", self.table.data_ptr(), self.ids.data_ptr(), T, VOCAB, D,
+                     self.emb_out[i % NSETS].data_ptr(), self.stream)
+
+    def step(self, ev_swiglu=None):
+        i = self.step_no
+        self.step_no += 1
+        s = self.sets[i % NSETS]
+        self.k_add_rmsnorm(s, "d1")
+        self.k_rope(s)
+        self.k_paged(s, i % L_POOL)
+        self.k_add_rmsnorm(s, "d2")
+        if ev_swiglu is not None:
+            ev_swiglu[0].record()
+        self.k_swiglu(s)
+        if ev_swiglu is not None:
+            ev_swiglu[1].record()
+
+    def kernel_launcher(self, name):
+        return {
+            "add_rmsnorm_f16": lambda i: self.k_add_rmsnorm(self.sets[i % NSETS], "d1"),
+            "rope_f16": lambda i: self.k_rope(self.sets[i % NSETS]),
+            "paged_kv_append_f16": lambda i: self.k_paged(self.sets[i % NSETS], i % L_POOL),
+            "swiglu_f16": lambda i: self.k_swiglu(self.sets[i % NSETS]),
+            "embed_f16": lambda i: self.k_embed(i),
+        }[name]
+
+
+def breakdown(chain, torch, reps):
+    """Average duration of each kernel, HIP events around every launch."""
+    out = {}
+    for name in ["add_rmsnorm_f16", "rope_f16", "paged_kv_append_f16", "swiglu_f16", "embed_f16"]:
+        launch = chain.kernel_launcher(name)
+        for i in range(3):
+            launch(i)
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(reps)]
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(evs):
+            a.record()
+            launch(i)
+            b.record()
+        torch.cuda.synchronize()
+        us = sorted(a.elapsed_time(b) * 1e3 for a, b in evs)
+        mean = sum(us) / len(us)
+        out[name] = {"us_mean": round(mean, 2), "us_median": round(us[len(us) // 2], 2),
+                     "bytes": BYTES[name], "GBps": round(BYTES[name] / (mean * 1e-6) / 1e9, 1),
+                     "frac_peak": round(BYTES[name] / (mean * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
+    return out
+
+
+def cpu_baseline(seconds):
+    """The oracle (scalar C, 1 thread) on a bounded sample of the same chain:
+    the C5 shapes restricted to 512 tokens, repeated until `seconds` elapse."""
+    import ctypes
+    import numpy as np
+    sys.path.insert(0, str(ROOT))
+    import oracle as orc
+
+    lib = orc.lib()
+    n = 512
+    r = np.random.default_rng(1)
+
+    def h(*shape, clip=None):
+        a = r.standard_normal(size=shape, dtype=np.float32)
+        if clip:
+            np.clip(a, -clip, clip, out=a)
+        return a.astype(np.float16).view(np.uint16)
+
+    x, d1, d2, y = h(n, D), h(n, D), h(n, D), np.empty((n, D), np.uint16)
+    w = (r.uniform(0.5, 1.5, D)).astype(np.float16).view(np.uint16)
+    q, k, v = h(n, HQ * HD), h(n, HKV * HD), h(n, HKV * HD)
+    gate, up, out = h(n, F, clip=8), h(n, F, clip=8), np.empty((n, F), np.uint16)
+    nb = n // PAGE
+    blk = L_POOL * PAGE * HKV * HD
+    kpool, vpool = np.empty(nb * blk, np.uint16), np.empty(nb * blk, np.uint16)
+    offs = (np.arange(nb) * blk).astype(np.int64)
+    slots = np.arange(n, dtype=np.int32)
+    P = lambda a: a.ctypes.data  # noqa: E731
+    sample_bytes = CHAIN_BYTES * n // T
+
+    def one(layer):
+        lib.or_add_rmsnorm_f16(P(x), P(d1), P(w), P(y), n, D, EPS)
+        lib.or_rope_f16(P(q), n, HQ, HD, HQ * HD, None, 0, THETA, 1)
+        lib.or_rope_f16(P(k), n, HKV, HD, HKV * HD, None, 0, THETA, 1)
+        lib.or_paged_kv_append_f16(P(kpool), P(vpool), P(offs), nb, P(slots), P(k), P(v), n, layer,
+                                   L_POOL, HKV, HD)
+        lib.or_add_rmsnorm_f16(P(x), P(d2), P(w), P(y), n, D, EPS)
+        lib.or_swiglu_f16(P(gate), P(up), P(out), n * F)
+
+    one(0)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        one(reps % L_POOL)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    gbs = sample_bytes * reps / el / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"oracle/oracle.c scalar C (gcc -O2, 1 thread) running the same 5-op chain on "
+                      f"{n} of the {T} tokens (C5 shapes), {reps} passes in {el:.1f} s; "
+                      f"{CHAIN_BYTES * n / T / 1e6:.1f} MB of algorithmic traffic per pass; "
+                      f"us_per_layer_at_T8192={el / reps * T / n * 1e6:.0f}"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
+              "every kernel is independent per token/row, see DESIGN.md for how it shards",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import quantlib_amd as ql
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    ql.lib()  # raises if the HIP library is not built
+    chain = Chain(ql, torch)
+
+    for _ in range(args.warmup):
+        chain.step()
+    torch.cuda.synchronize()
+
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    t_all0, t_all1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    t_all0.record()
+    for i in range(args.steps):
+        chain.step(evs[i])
+    t_all1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    ms_per_step = wall / args.steps * 1e3
+    ev_ms_per_step = t_all0.elapsed_time(t_all1) / args.steps
+    sw_us = sum(a.elapsed_time(b) for a, b in evs) / len(evs) * 1e3
+    sw_gbs = BYTES["swiglu_f16"] / (sw_us * 1e-6) / 1e9
+    kernels = breakdown(chain, torch, args.breakdown_reps)
+
+    traffic = None
+    tf = pathlib.Path(args.traffic_file)
+    if tf.exists():
+        try:
+            traffic = json.loads(tf.read_text()).get("swiglu_f16_c5", {}).get("hbm_bytes_per_launch")
+        except (ValueError, AttributeError):
+            traffic = None
+
+    cpu = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
+
+    line = {
+        "metric": "achieved HBM GB/s (% of MI355X peak) per fused kernel; us per decoder layer",
+        "value": round(CHAIN_BYTES / (ms_per_step * 1e-3) / 1e9, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "us_per_decoder_layer": round(ms_per_step * 1e3, 1),
+        "us_per_decoder_layer_events": round(ev_ms_per_step * 1e3, 1),
+        "frac_peak": round(CHAIN_BYTES / (ms_per_step * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (torch.randn on device; gate/up clipped to [-8,8]; w ~ U(0.5,1.5))",
+        "config": {"workload": "C5 llama3-8b-shaped fp16 decoder-layer chain: add+rmsnorm, rope q+k, "
+                               "paged kv append, add+rmsnorm, swiglu",
+                   "tokens": T, "hidden": D, "heads": HQ, "kv_heads": HKV, "head_dim": HD,
+                   "ffn": F, "rope_theta": THETA, "rope_pairing": "rotate-half", "kv_block": PAGE,
+                   "kv_pool_layers": L_POOL, "buffer_sets": NSETS,
+                   "chain_bytes_per_step": CHAIN_BYTES, "math": "fp32 with fp16 I/O"},
+        "roofline": {"kernel": "swiglu_f16 [8192 x 14336]", "bound": "hbm",
+                     "achieved": round(sw_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(sw_gbs / PEAK_HBM_GBS, 4), "traffic": traffic,
+                     "algorithmic_bytes": BYTES["swiglu_f16"], "us_per_launch": round(sw_us, 2)},
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

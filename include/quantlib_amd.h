@@ -1,0 +1,178 @@
+/*
+ * quantlib_amd.h -- C ABI of the MI355X (gfx950) fused per-layer kernels.
+ *
+ * Every entry point:
+ *   - takes plain device pointers, sizes and a hipStream_t (NULL = default stream);
+ *   - validates its arguments on the host and returns hipErrorInvalidValue before
+ *     touching the GPU when they are unusable;
+ *   - returns hipSuccess without launching anything when the problem is empty
+ *     (rows == 0, n == 0, n_tokens == 0);
+ *   - otherwise enqueues its kernel(s) on `stream` and returns the launch status.
+ *     It never synchronises, never allocates and never frees.
+ *
+ * fp16 tensors are passed as `uint16_t*` holding IEEE-754 binary16 bit patterns
+ * (the storage of `__half`).  Buffers must not alias unless an entry point says
+ * it works in place.  Fast paths use 16-byte vector accesses when every pointer
+ * (and row stride) is 16-byte aligned; other layouts take a scalar path that
+ * computes the same arithmetic.
+ *
+ * The reference names each function replaces are given as file:line of
+ * samfrazerdutton/Quant-lib.  The reference launchers use C++ linkage and
+ * return void; the drop-in shims with those exact names live in
+ * quantlib_compat.h and forward here.
+ */
+#ifndef QUANTLIB_AMD_H
+#define QUANTLIB_AMD_H
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* RoPE pairing of the head vector x[0..d).
+ * QL_ROPE_INTERLEAVED: pairs (2i, 2i+1) -- the reference's behaviour
+ *   (kernels/rope.cu:27-29,40-41; kernels/fp16_ops.cu:54,59-62).
+ * QL_ROPE_HALF: pairs (i, i + d/2) ("rotate-half", Llama/HF layout).
+ * Both use inv_freq_i = 1 / theta^(2i/d) for pair i. */
+#define QL_ROPE_INTERLEAVED 0
+#define QL_ROPE_HALF        1
+
+/* Tokens per paged-KV block (include/paged_kvcache.h:7, include/fp16_types.h:60). */
+#define QL_PAGE_SIZE 16
+
+/* Library version as 10000*major + 100*minor + patch. */
+int ql_version(void);
+
+/* ---- RMSNorm --------------------------------------------------------------
+ * out[r,i] = (x[r,i] * inv_rms_r) * w[i],  inv_rms_r = 1/sqrt(sum_i x[r,i]^2 / dim + eps)
+ * fp32 math; fp16 variant reads/writes binary16 and rounds the output RNE.
+ * Replaces launch_rmsnorm (kernels/rmsnorm.cu:51-57) and
+ * launch_fp16_rmsnorm (kernels/fp16_ops.cu:113-118). */
+hipError_t ql_rmsnorm_f32(const float* x, const float* w, float* out,
+                          int rows, int dim, float eps, hipStream_t stream);
+hipError_t ql_rmsnorm_f16(const uint16_t* x, const uint16_t* w, uint16_t* out,
+                          int rows, int dim, float eps, hipStream_t stream);
+
+/* ---- fused residual add + RMSNorm -----------------------------------------
+ * x[r,i] <- x[r,i] + d[r,i]   (in place; fp16: rounded RNE to binary16 first)
+ * out    <- rmsnorm(x_updated)  (normalises the rounded sum, so the result is
+ *                                identical to the unfused add then rmsnorm)
+ * Replaces the add_residual + launch_rmsnorm pair of src/forward.cu:228-232
+ * and the launch_fp16_add + launch_fp16_rmsnorm pair of
+ * src/fp16_forward.cu:213-216 with one pass. */
+hipError_t ql_add_rmsnorm_f32(float* x, const float* d, const float* w, float* out,
+                              int rows, int dim, float eps, hipStream_t stream);
+hipError_t ql_add_rmsnorm_f16(uint16_t* x, const uint16_t* d, const uint16_t* w,
+                              uint16_t* out, int rows, int dim, float eps,
+                              hipStream_t stream);
+
+/* ---- residual add (in place) ----------------------------------------------
+ * fp32: x += d  (add_residual_kernel, src/forward.cu:128-135)
+ * fp16: x = h(f(x) + f(d)) (fp16_add_kernel / launch_fp16_add, kernels/fp16_ops.cu:92-100,144-147) */
+hipError_t ql_add_f32(float* x, const float* d, int64_t n, hipStream_t stream);
+hipError_t ql_add_f16(uint16_t* x, const uint16_t* d, int64_t n, hipStream_t stream);
+
+/* ---- rotary position embedding (in place, Q and K in one launch) ----------
+ * q: [n_tokens rows of q_row_stride elements], head h of token t at q + t*q_row_stride + h*head_dim
+ * k: likewise with n_kv_heads heads and k_row_stride (GQA: n_kv_heads <= n_heads)
+ * Either q or k may be NULL (its head count is then ignored).
+ * position of token t = positions ? positions[t] : pos_offset + t
+ * pair i of a head:  inv_freq = 1/theta^((2i)/d) (fp32 exponent, as kernels/rope.cu:35)
+ *                    a = (float)pos * inv_freq,  c = cos(a), s = sin(a) (accurate)
+ *                    y0 = fma(x0, c, -(x1*s)),  y1 = fma(x0, s, x1*c)
+ * head_dim must be even and <= 2048.
+ * Replaces launch_rope (kernels/rope.cu:44-50) and launch_fp16_rope
+ * (kernels/fp16_ops.cu:120-127), which take one tensor per call and use
+ * position = row index. */
+hipError_t ql_rope_f32(float* q, float* k, int n_tokens, int n_heads, int n_kv_heads,
+                       int head_dim, int64_t q_row_stride, int64_t k_row_stride,
+                       const int32_t* positions, int pos_offset, float theta,
+                       int pairing, hipStream_t stream);
+hipError_t ql_rope_f16(uint16_t* q, uint16_t* k, int n_tokens, int n_heads,
+                       int n_kv_heads, int head_dim, int64_t q_row_stride,
+                       int64_t k_row_stride, const int32_t* positions, int pos_offset,
+                       float theta, int pairing, hipStream_t stream);
+
+/* ---- SwiGLU -----------------------------------------------------------------
+ * out = (g / (1 + exp(-g))) * u, elementwise over rows*ffn_dim elements.
+ * Replaces launch_swiglu (kernels/feedforward.cu:27-35) and
+ * launch_fp16_swiglu (kernels/fp16_ops.cu:129-135). */
+hipError_t ql_swiglu_f32(const float* gate, const float* up, float* out,
+                         int rows, int ffn_dim, hipStream_t stream);
+hipError_t ql_swiglu_f16(const uint16_t* gate, const uint16_t* up, uint16_t* out,
+                         int rows, int ffn_dim, hipStream_t stream);
+
+/* ---- row softmax ------------------------------------------------------------
+ * m = max(-FLT_MAX, max_c x[r,c]);  e = exp(x - m);  out = e * (1 / sum_c e)
+ * Reads each row once and writes it once.  -inf entries give exactly 0.
+ * Replaces launch_softmax (kernels/softmax.cu:88-94).  The fp16 variant has no
+ * reference kernel: it is the fp32 arithmetic with binary16 I/O (RNE output). */
+hipError_t ql_softmax_f32(const float* in, float* out, int rows, int cols,
+                          hipStream_t stream);
+hipError_t ql_softmax_f16(const uint16_t* in, uint16_t* out, int rows, int cols,
+                          hipStream_t stream);
+
+/* ---- token-embedding gather (batched) ----------------------------------------
+ * out[t, :] = table[ids[t], :] for t < n_tokens; bit-exact copy.
+ * ids outside [0, vocab) produce a zero row (the reference does no check).
+ * Replaces embed_kernel (src/forward.cu:137-141, launched :256-257) and
+ * launch_fp16_embed (kernels/fp16_ops.cu:81-89,137-142), which gather one token. */
+hipError_t ql_embed_f32(const float* table, const int32_t* ids, int n_tokens,
+                        int vocab, int dim, float* out, hipStream_t stream);
+hipError_t ql_embed_f16(const uint16_t* table, const int32_t* ids, int n_tokens,
+                        int vocab, int dim, uint16_t* out, hipStream_t stream);
+
+/* One token whose id is passed by value, as embed_kernel (src/forward.cu:137-141)
+ * and launch_fp16_embed (kernels/fp16_ops.cu:137-142) take it; no vocab bound is
+ * known, so only a negative id gives the zero row. */
+hipError_t ql_embed_token_f32(const float* table, int token_id, int dim, float* out,
+                              hipStream_t stream);
+hipError_t ql_embed_token_f16(const uint16_t* table, int token_id, int dim, uint16_t* out,
+                              hipStream_t stream);
+
+/* ---- contiguous KV-cache append ---------------------------------------------
+ * cache layout [n_layers, max_seq, n_kv_heads, head_dim]; writes n_tokens
+ * consecutive positions pos .. pos+n_tokens-1 of `layer` from
+ * k_new/v_new [n_tokens, n_kv_heads, head_dim].  Bit-exact copy.
+ * Replaces kvcache_append (src/kv_cache.cu:44-58, two cudaMemcpyAsync) and
+ * fp16_kvcache_append (src/fp16_forward.cu:148-164, one token). */
+hipError_t ql_kv_append_f32(float* k_cache, float* v_cache, const float* k_new,
+                            const float* v_new, int layer, int pos, int n_tokens,
+                            int n_kv_heads, int head_dim, int max_seq, int n_layers,
+                            hipStream_t stream);
+hipError_t ql_kv_append_f16(uint16_t* k_cache, uint16_t* v_cache, const uint16_t* k_new,
+                            const uint16_t* v_new, int layer, int pos, int n_tokens,
+                            int n_kv_heads, int head_dim, int max_seq, int n_layers,
+                            hipStream_t stream);
+
+/* ---- paged KV-cache append ----------------------------------------------------
+ * k_blocks/v_blocks: DEVICE arrays of n_blocks device pointers, one per block;
+ * each block is [n_layers, QL_PAGE_SIZE, n_kv_heads, head_dim] binary16
+ * (the pool of src/paged_kvcache.cu:26-46).
+ * slot_mapping[t] = physical_block * QL_PAGE_SIZE + offset_in_block for token t;
+ * a negative slot (padding) or a block >= n_blocks skips the token.
+ * Element (t, h, j) goes to k_blocks[b][((layer*16 + o)*n_kv_heads + h)*head_dim + j].
+ * The reference ships the pool and block tables but no append kernel. */
+hipError_t ql_paged_kv_append_f16(uint16_t* const* k_blocks, uint16_t* const* v_blocks,
+                                  int n_blocks, const int32_t* slot_mapping,
+                                  const uint16_t* k_new, const uint16_t* v_new,
+                                  int n_tokens, int layer, int n_layers, int n_kv_heads,
+                                  int head_dim, hipStream_t stream);
+
+/* Host helper: slot_mapping[i] = block_table[(start_pos+i)/16]*16 + (start_pos+i)%16
+ * for i < n_tokens (the per-sequence logical->physical block map of
+ * include/scheduler.h:17-19).  Host memory only.  Returns hipErrorInvalidValue if a
+ * needed block_table entry is negative or beyond n_table. */
+hipError_t ql_paged_slot_mapping(const int32_t* block_table, int n_table, int start_pos,
+                                 int n_tokens, int32_t* slot_mapping);
+
+/* ---- fp16 -> fp32 widening (launch_fp16_to_fp32, kernels/fp16_ops.cu:103-110,149-153) */
+hipError_t ql_f16_to_f32(const uint16_t* src, float* dst, int64_t n, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QUANTLIB_AMD_H */

@@ -1,0 +1,126 @@
+/*
+ * quantlib_compat.h -- drop-in replacements for the reference's launchers and
+ * KV-cache types, with the reference's names, argument order and meaning
+ * (cudaStream_t becomes hipStream_t).  A caller of samfrazerdutton/Quant-lib's
+ * kernels links libquantlib_amd.so instead of the .cu objects and keeps its
+ * call sites.
+ *
+ * Like the reference, the launchers return void: a launch error stays pending
+ * for the caller's next hipGetLastError()/hipStreamSynchronize() check.  An
+ * argument the reference would pass to a malformed launch (negative sizes,
+ * odd head_dim) is rejected without launching; hipGetLastError() does not
+ * report it, ql_* entry points do (quantlib_amd.h).
+ *
+ * Behaviour kept from the reference on purpose:
+ *   - launch_rope / launch_fp16_rope rotate interleaved pairs (2i, 2i+1) and
+ *     use the row index as the position (kernels/rope.cu:20,36).
+ *   - kvcache_append writes at cache->current_len; the caller advances it
+ *     (src/forward.cu:264).
+ *   - paged_kv_create hands out blocks from a LIFO free list, so a fresh pool
+ *     gives blocks 0,1,2,... (src/paged_kvcache.cu:49-53,89-93).
+ */
+#ifndef QUANTLIB_COMPAT_H
+#define QUANTLIB_COMPAT_H
+
+#include <hip/hip_runtime_api.h>
+#include <hip/hip_fp16.h>
+#include <stddef.h>
+
+/* ---- kernels/ launchers (C++ linkage, as in the reference) ------------ */
+/* kernels/rmsnorm.cu:51 */
+void launch_rmsnorm(const float* x, const float* weight, float* out, int rows, int dim,
+                    float eps, hipStream_t stream);
+/* kernels/rope.cu:44 */
+void launch_rope(float* x, int seq_len, int n_heads, int head_dim, float theta,
+                 hipStream_t stream);
+/* kernels/feedforward.cu:27 */
+void launch_swiglu(const float* gate, const float* up, float* out, int rows, int ffn_dim,
+                   hipStream_t stream);
+/* kernels/softmax.cu:88 */
+void launch_softmax(const float* input, float* output, int rows, int cols,
+                    hipStream_t stream);
+/* kernels/fp16_ops.cu:113 */
+void launch_fp16_rmsnorm(const __half* x, const __half* w, __half* out, int rows, int dim,
+                         float eps, hipStream_t stream);
+/* kernels/fp16_ops.cu:120 */
+void launch_fp16_rope(__half* x, int seq_len, int n_heads, int head_dim, float theta,
+                      hipStream_t stream);
+/* kernels/fp16_ops.cu:129 */
+void launch_fp16_swiglu(const __half* gate, const __half* up, __half* out, int rows,
+                        int ffn_dim, hipStream_t stream);
+/* kernels/fp16_ops.cu:137 */
+void launch_fp16_embed(const __half* table, __half* out, int token_id, int hidden_dim,
+                       hipStream_t stream);
+/* kernels/fp16_ops.cu:144 */
+void launch_fp16_add(__half* x, const __half* y, int n, hipStream_t stream);
+/* kernels/fp16_ops.cu:149 */
+void launch_fp16_to_fp32(const __half* src, float* dst, int n, hipStream_t stream);
+
+/* ---- inline kernels of src/forward.cu / src/fp16_forward.cu given launchers ---- */
+/* src/forward.cu:128-135 (add_residual_kernel + its static launcher) */
+void add_residual(float* x, const float* d, int n, hipStream_t stream);
+/* src/forward.cu:137-141 (embed_kernel, launched at :256-257) */
+void launch_embed(float* out, const float* tbl, int tok, int hd, hipStream_t stream);
+/* src/fp16_forward.cu:148-154 (fp16_kvcache_append, launched at :194-199) */
+void launch_fp16_kvcache_append(__half* k_cache, __half* v_cache, const __half* k_new,
+                                const __half* v_new, int layer, int pos, int n_kv_heads,
+                                int head_dim, int max_seq, int n_layers,
+                                hipStream_t stream);
+
+/* ---- fp32 contiguous KV cache (include/kv_cache.h:12-36) ------------------- */
+typedef struct {
+    float* k_cache; /* [n_layers * max_seq_len * n_heads * head_dim] */
+    float* v_cache;
+    int n_layers;
+    int max_seq_len;
+    int n_heads;
+    int head_dim;
+    int current_len;
+} KVCache;
+
+KVCache* kvcache_create(int n_layers, int max_seq_len, int n_heads, int head_dim);
+void kvcache_free(KVCache* cache);
+void kvcache_append(KVCache* cache, int layer, const float* new_k, const float* new_v,
+                    hipStream_t stream);
+float* kvcache_get_k(KVCache* cache, int layer);
+float* kvcache_get_v(KVCache* cache, int layer);
+
+/* ---- fp16 contiguous KV cache (src/fp16_forward.cu:115-145) ---------------- */
+typedef struct {
+    __half* k_cache; /* [n_layers, max_seq, n_kv_heads, head_dim] */
+    __half* v_cache;
+    int n_layers, max_seq, n_kv_heads, head_dim;
+    int current_len;
+} FP16KVCache;
+
+FP16KVCache* fp16_kvcache_create(int n_layers, int max_seq, int n_kv_heads, int head_dim);
+void fp16_kvcache_free(FP16KVCache* c);
+
+/* ---- paged KV cache (include/paged_kvcache.h:9-34) ------------------------- */
+#ifndef PAGE_SIZE
+#define PAGE_SIZE 16
+#endif
+
+typedef struct {
+    __half** k_blocks; /* [n_blocks] device array of device pointers to K blocks */
+    __half** v_blocks;
+    int n_blocks;
+    int n_layers;
+    int n_kv_heads;
+    int head_dim;
+    int* free_blocks; /* host LIFO stack of free block indices */
+    int free_count;
+    int** block_tables; /* host: seq -> block indices (-1 = unused) */
+    int max_seqs;
+    int max_blocks_per_seq;
+} PagedKVCache;
+
+extern "C" {
+PagedKVCache* paged_kv_create(int n_blocks, int n_layers, int n_kv_heads, int head_dim,
+                              int max_seqs, int max_blocks_per_seq);
+void paged_kv_free(PagedKVCache* cache);
+int paged_kv_allocate_block(PagedKVCache* cache);
+void paged_kv_free_block(PagedKVCache* cache, int block_idx);
+}
+
+#endif /* QUANTLIB_COMPAT_H */

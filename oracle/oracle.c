@@ -1,0 +1,383 @@
+/*
+ * oracle.c -- CPU restatement of the reference's hot-path arithmetic.
+ * TEST INFRASTRUCTURE ONLY (see oracle.h): the parity checker, never the
+ * thing measured or shipped.  Built with -O2 -ffp-contract=off, no fast-math,
+ * so every rounding step below happens exactly as written.
+ */
+#include "oracle.h"
+
+#include <float.h>
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---- binary16 codec --------------------------------------------------------
+ * IEEE 754 binary16 <-> binary32, round to nearest even.  The arithmetic of
+ * __float2half/__half2float used throughout kernels/fp16_ops.cu.
+ * Pinned by: exhaustive comparison with numpy float16 over all 65536 halves,
+ * every half-way point between consecutive halves, overflow and subnormal
+ * boundaries (tests/test_oracle.py::test_f16_*). */
+uint16_t or_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) /* inf / nan (quiet, top payload bits kept) */
+        return (uint16_t)(sign | 0x7c00u | (ax > 0x7f800000u ? (0x200u | ((ax >> 13) & 0x3ffu)) : 0u));
+    if (ax >= 0x477ff000u) /* >= 65520: rounds to inf */
+        return (uint16_t)(sign | 0x7c00u);
+    if (ax < 0x38800000u) { /* below 2^-14: binary16 subnormal or zero */
+        if (ax <= 0x33000000u) return (uint16_t)sign; /* <= 2^-25 rounds to 0 */
+        const uint32_t e = ax >> 23;
+        const uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+        const uint32_t shift = 126u - e; /* value / 2^-24 = m >> shift */
+        uint32_t q = m >> shift;
+        const uint32_t rem = m & ((1u << shift) - 1u);
+        const uint32_t half = 1u << (shift - 1u);
+        if (rem > half || (rem == half && (q & 1u))) q++;
+        return (uint16_t)(sign | q);
+    }
+    const uint32_t r = ax - 0x38000000u; /* rebias 127 -> 15 */
+    uint32_t h = r >> 13;
+    const uint32_t rem = r & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+    return (uint16_t)(sign | h);
+}
+
+float or_f16_to_f32(uint16_t h) {
+    const uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    uint32_t e = ((uint32_t)h >> 10) & 0x1fu;
+    uint32_t m = (uint32_t)h & 0x3ffu;
+    uint32_t bits;
+    if (e == 0) {
+        if (m == 0) {
+            bits = sign;
+        } else { /* subnormal: m * 2^-24, normalise */
+            e = 113;
+            while (!(m & 0x400u)) {
+                m <<= 1;
+                e--;
+            }
+            bits = sign | (e << 23) | ((m & 0x3ffu) << 13);
+        }
+    } else if (e == 31) {
+        bits = sign | 0x7f800000u | (m << 13);
+    } else {
+        bits = sign | ((e + 112u) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+void or_f32_to_f16_n(const float* src, uint16_t* dst, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) dst[i] = or_f32_to_f16(src[i]);
+}
+
+void or_f16_to_f32_n(const uint16_t* src, float* dst, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) dst[i] = or_f16_to_f32(src[i]);
+}
+
+/* ---- RMSNorm -----------------------------------------------------------------
+ * kernels/rmsnorm.cu:27-48 (fp32) and kernels/fp16_ops.cu:18-41 (fp16):
+ *   ss = sum x^2;  r = 1/sqrt(ss/dim + eps)  (rsqrtf in the reference);
+ *   out = (x*r)*w.
+ * ss is accumulated in double and rounded once to fp32.
+ * Pinned by: constant-row and one-hot closed forms, scale invariance
+ * (eps = 0), the eps term (all-zero row gives 0, tiny rows feel eps), weight
+ * indexing with a non-uniform w (tests/test_oracle.py::test_rmsnorm_*). */
+static float rms_inv(double ss, int dim, float eps) {
+    const float ms = (float)ss / (float)dim;
+    return 1.0f / sqrtf(ms + eps);
+}
+
+void or_rmsnorm_f32(const float* x, const float* w, float* out, int rows, int dim, float eps) {
+    for (int r = 0; r < rows; ++r) {
+        const float* xr = x + (size_t)r * dim;
+        double ss = 0.0;
+        for (int i = 0; i < dim; ++i) ss += (double)xr[i] * (double)xr[i];
+        const float inv = rms_inv(ss, dim, eps);
+        for (int i = 0; i < dim; ++i) out[(size_t)r * dim + i] = (xr[i] * inv) * w[i];
+    }
+}
+
+void or_rmsnorm_f16(const uint16_t* x, const uint16_t* w, uint16_t* out, int rows, int dim,
+                    float eps) {
+    for (int r = 0; r < rows; ++r) {
+        const uint16_t* xr = x + (size_t)r * dim;
+        double ss = 0.0;
+        for (int i = 0; i < dim; ++i) {
+            const double v = or_f16_to_f32(xr[i]);
+            ss += v * v;
+        }
+        const float inv = rms_inv(ss, dim, eps);
+        for (int i = 0; i < dim; ++i)
+            out[(size_t)r * dim + i] =
+                or_f32_to_f16((or_f16_to_f32(xr[i]) * inv) * or_f16_to_f32(w[i]));
+    }
+}
+
+/* Residual add then RMSNorm of the updated (rounded) row: the unfused chain
+ * add_residual + launch_rmsnorm (src/forward.cu:228-232) and
+ * launch_fp16_add + launch_fp16_rmsnorm (src/fp16_forward.cu:213-216).
+ * Pinned by: equality with or_add_* followed by or_rmsnorm_* (the unfused
+ * chain) and the rmsnorm pins above. */
+void or_add_rmsnorm_f32(float* x, const float* d, const float* w, float* out, int rows, int dim,
+                        float eps) {
+    or_add_f32(x, d, (int64_t)rows * dim);
+    or_rmsnorm_f32(x, w, out, rows, dim, eps);
+}
+
+void or_add_rmsnorm_f16(uint16_t* x, const uint16_t* d, const uint16_t* w, uint16_t* out,
+                        int rows, int dim, float eps) {
+    or_add_f16(x, d, (int64_t)rows * dim);
+    or_rmsnorm_f16(x, w, out, rows, dim, eps);
+}
+
+/* src/forward.cu:128-130: x += d.  kernels/fp16_ops.cu:92-100: x = h(f(x)+f(d)).
+ * Pinned by: numpy float32 / float16 addition (same rounding), exhaustive on
+ * a grid of binary16 pairs. */
+void or_add_f32(float* x, const float* d, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) x[i] = x[i] + d[i];
+}
+
+void or_add_f16(uint16_t* x, const uint16_t* d, int64_t n) {
+    for (int64_t i = 0; i < n; ++i)
+        x[i] = or_f32_to_f16(or_f16_to_f32(x[i]) + or_f16_to_f32(d[i]));
+}
+
+/* ---- RoPE ---------------------------------------------------------------------
+ * kernels/rope.cu:20-41 and kernels/fp16_ops.cu:49-62, pair i of each head:
+ *   inv_freq = 1 / theta^((2i)/d)   exponent as an fp32 division (rope.cu:35),
+ *                                   the power in double rounded to fp32
+ *   angle    = (float)pos * inv_freq                       (rope.cu:36)
+ *   c, s     = cos/sin(angle) in double rounded to fp32    (rope.cu:37-38)
+ *   y0 = fma(x0, c, -(x1*s)),  y1 = fma(x0, s, x1*c)       (rope.cu:40-41)
+ * pairing 0 = interleaved (2i, 2i+1) as the reference; 1 = rotate-half (i, i+d/2).
+ * position = positions ? positions[t] : pos_offset + t (reference: row index).
+ * Pinned by: pos = 0 identity; pair 0 has inv_freq = 1 so its angle is pos;
+ * inv_freq closed form at d = 4 (theta^-1/2); per-pair norm preservation (the
+ * reference's own test, tests/test_attention.cu:110-121); agreement with a
+ * complex-exponential formulation (x0 + i x1) e^{i angle} in float64; the
+ * interleaved/rotate-half permutation identity (tests/test_oracle.py::test_rope_*). */
+float or_rope_inv_freq(int pair, int head_dim, float theta) {
+    const float e = (2.0f * (float)pair) / (float)head_dim;
+    const float p = (float)pow((double)theta, (double)e);
+    return 1.0f / p;
+}
+
+void or_rope_cos_sin(int pos, int pair, int head_dim, float theta, float* c, float* s) {
+    const float a = (float)pos * or_rope_inv_freq(pair, head_dim, theta);
+    *c = (float)cos((double)a);
+    *s = (float)sin((double)a);
+}
+
+static void rope_pair(float x0, float x1, float c, float s, float* y0, float* y1) {
+    *y0 = fmaf(x0, c, -(x1 * s));
+    *y1 = fmaf(x0, s, x1 * c);
+}
+
+void or_rope_f32(float* x, int n_tokens, int n_heads, int head_dim, int64_t row_stride,
+                 const int32_t* positions, int pos_offset, float theta, int pairing) {
+    const int np = head_dim / 2;
+    for (int t = 0; t < n_tokens; ++t) {
+        const int pos = positions ? positions[t] : pos_offset + t;
+        for (int p = 0; p < np; ++p) {
+            float c, s;
+            or_rope_cos_sin(pos, p, head_dim, theta, &c, &s);
+            const int i0 = pairing == 0 ? 2 * p : p;
+            const int i1 = pairing == 0 ? 2 * p + 1 : p + np;
+            for (int h = 0; h < n_heads; ++h) {
+                float* v = x + (size_t)t * row_stride + (size_t)h * head_dim;
+                float y0, y1;
+                rope_pair(v[i0], v[i1], c, s, &y0, &y1);
+                v[i0] = y0;
+                v[i1] = y1;
+            }
+        }
+    }
+}
+
+void or_rope_f16(uint16_t* x, int n_tokens, int n_heads, int head_dim, int64_t row_stride,
+                 const int32_t* positions, int pos_offset, float theta, int pairing) {
+    const int np = head_dim / 2;
+    for (int t = 0; t < n_tokens; ++t) {
+        const int pos = positions ? positions[t] : pos_offset + t;
+        for (int p = 0; p < np; ++p) {
+            float c, s;
+            or_rope_cos_sin(pos, p, head_dim, theta, &c, &s);
+            const int i0 = pairing == 0 ? 2 * p : p;
+            const int i1 = pairing == 0 ? 2 * p + 1 : p + np;
+            for (int h = 0; h < n_heads; ++h) {
+                uint16_t* v = x + (size_t)t * row_stride + (size_t)h * head_dim;
+                float y0, y1;
+                rope_pair(or_f16_to_f32(v[i0]), or_f16_to_f32(v[i1]), c, s, &y0, &y1);
+                v[i0] = or_f32_to_f16(y0);
+                v[i1] = or_f32_to_f16(y1);
+            }
+        }
+    }
+}
+
+/* ---- SwiGLU ---------------------------------------------------------------------
+ * kernels/feedforward.cu:4-6,24 and kernels/fp16_ops.cu:74-77:
+ *   out = (g / (1 + exp(-g))) * u   (fp32; fp16 variant rounds the result).
+ * Pinned by: silu(0) = 0; u = 0 gives 0; silu(g) - silu(-g) = g; large |g|
+ * limits; scipy.special.expit(g) * g * u in float64 (tests/test_oracle.py::test_swiglu_*). */
+static float silu_mul(float g, float u) {
+    const float e = expf(-g);
+    return (g / (1.0f + e)) * u;
+}
+
+void or_swiglu_f32(const float* g, const float* u, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = silu_mul(g[i], u[i]);
+}
+
+void or_swiglu_f16(const uint16_t* g, const uint16_t* u, uint16_t* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i)
+        out[i] = or_f32_to_f16(silu_mul(or_f16_to_f32(g[i]), or_f16_to_f32(u[i])));
+}
+
+/* ---- softmax --------------------------------------------------------------------
+ * kernels/softmax.cu:44-85:
+ *   m = max(-FLT_MAX, x...);  e = exp(x - m);  out = e * (1/sum e)
+ * The sum is accumulated in double and rounded to fp32 before the reciprocal.
+ * The fp16 variant (no reference kernel) is the same arithmetic on widened
+ * inputs with an RNE binary16 result.
+ * Pinned by: the reference test's own check (tests/test_softmax.cu:88-106:
+ * max abs error < 1e-5 against its cpu_softmax on srand(7) inputs, row sums
+ * within 1e-5); scipy.special.softmax; shift invariance; causal row 0 = e_0;
+ * uniform row = 1/n; -inf gives exactly 0 (tests/test_oracle.py::test_softmax_*). */
+static void softmax_row(const float* x, float* e, int cols, float* out_scale) {
+    float m = -FLT_MAX;
+    for (int c = 0; c < cols; ++c) m = fmaxf(m, x[c]);
+    double s = 0.0;
+    for (int c = 0; c < cols; ++c) {
+        e[c] = expf(x[c] - m);
+        s += e[c];
+    }
+    *out_scale = 1.0f / (float)s;
+}
+
+void or_softmax_f32(const float* in, float* out, int rows, int cols) {
+    for (int r = 0; r < rows; ++r) {
+        float* o = out + (size_t)r * cols;
+        float inv;
+        softmax_row(in + (size_t)r * cols, o, cols, &inv);
+        for (int c = 0; c < cols; ++c) o[c] = o[c] * inv;
+    }
+}
+
+void or_softmax_f16(const uint16_t* in, uint16_t* out, int rows, int cols) {
+    float* x = (float*)malloc(sizeof(float) * (size_t)cols);
+    float* e = (float*)malloc(sizeof(float) * (size_t)cols);
+    for (int r = 0; r < rows; ++r) {
+        for (int c = 0; c < cols; ++c) x[c] = or_f16_to_f32(in[(size_t)r * cols + c]);
+        float inv;
+        softmax_row(x, e, cols, &inv);
+        for (int c = 0; c < cols; ++c) out[(size_t)r * cols + c] = or_f32_to_f16(e[c] * inv);
+    }
+    free(x);
+    free(e);
+}
+
+void or_softmax_reftest_cpu(const float* in, float* out, int rows, int cols) {
+    for (int r = 0; r < rows; ++r) {
+        const float* x = in + (size_t)r * cols;
+        float* o = out + (size_t)r * cols;
+        float mx = -FLT_MAX;
+        for (int c = 0; c < cols; ++c) mx = fmaxf(mx, x[c]);
+        float s = 0.0f;
+        for (int c = 0; c < cols; ++c) {
+            o[c] = expf(x[c] - mx);
+            s += o[c];
+        }
+        for (int c = 0; c < cols; ++c) o[c] /= s;
+    }
+}
+
+void or_reftest_softmax_inputs(float* out, int64_t n, unsigned seed) {
+    srand(seed);
+    for (int64_t i = 0; i < n; ++i) out[i] = (float)rand() / RAND_MAX * 4.0f - 2.0f;
+}
+
+/* ---- embedding gather -------------------------------------------------------------
+ * src/forward.cu:137-141, kernels/fp16_ops.cu:81-89: out[t,:] = table[id,:];
+ * ids outside [0, vocab) give a zero row (the build's documented choice).
+ * Pinned by: numpy fancy indexing table[ids] (tests/test_oracle.py::test_embed_*). */
+void or_embed_f32(const float* table, const int32_t* ids, int n_tokens, int vocab, int dim,
+                  float* out) {
+    for (int t = 0; t < n_tokens; ++t) {
+        const int32_t id = ids[t];
+        for (int i = 0; i < dim; ++i)
+            out[(size_t)t * dim + i] =
+                (id >= 0 && id < vocab) ? table[(size_t)id * dim + i] : 0.0f;
+    }
+}
+
+void or_embed_f16(const uint16_t* table, const int32_t* ids, int n_tokens, int vocab, int dim,
+                  uint16_t* out) {
+    for (int t = 0; t < n_tokens; ++t) {
+        const int32_t id = ids[t];
+        for (int i = 0; i < dim; ++i)
+            out[(size_t)t * dim + i] =
+                (id >= 0 && id < vocab) ? table[(size_t)id * dim + i] : (uint16_t)0;
+    }
+}
+
+/* ---- contiguous KV append ----------------------------------------------------------
+ * src/kv_cache.cu:44-58 and src/fp16_forward.cu:148-164, for n_tokens
+ * consecutive positions: cache[layer][pos + t][h][j] = new[t][h][j] with
+ * offset layer*max_seq*kv + (pos+t)*kv + h*d + j.
+ * Pinned by: the reference's readback known answer (tests/test_kvcache.cu:47-70:
+ * after 16 tokens x 32 layers, layer 0 token 7 reads k[0] = 7.0) and numpy
+ * reshape-view assignment cache.reshape(L, S, H, d)[layer, pos:pos+T] = new
+ * (tests/test_oracle.py::test_kv_*). */
+#define KV_APPEND_BODY                                                                    \
+    const size_t kv = (size_t)n_kv_heads * head_dim;                                      \
+    (void)n_layers;                                                                       \
+    for (int t = 0; t < n_tokens; ++t)                                                    \
+        for (size_t i = 0; i < kv; ++i) {                                                 \
+            const size_t o = ((size_t)layer * max_seq + (size_t)(pos + t)) * kv + i;     \
+            k_cache[o] = k_new[(size_t)t * kv + i];                                       \
+            v_cache[o] = v_new[(size_t)t * kv + i];                                       \
+        }
+
+void or_kv_append_f32(float* k_cache, float* v_cache, const float* k_new, const float* v_new,
+                      int layer, int pos, int n_tokens, int n_kv_heads, int head_dim,
+                      int max_seq, int n_layers) {
+    KV_APPEND_BODY
+}
+
+void or_kv_append_f16(uint16_t* k_cache, uint16_t* v_cache, const uint16_t* k_new,
+                      const uint16_t* v_new, int layer, int pos, int n_tokens, int n_kv_heads,
+                      int head_dim, int max_seq, int n_layers) {
+    KV_APPEND_BODY
+}
+
+/* ---- paged KV append -----------------------------------------------------------------
+ * Pool layout of src/paged_kvcache.cu:26-46 (block = [n_layers, 16, H_kv, d],
+ * include/fp16_types.h:63): element (layer, token t, head h, j) of slot s goes
+ * to block s/16, row (layer*16 + s%16).  Negative slots and blocks >= n_blocks
+ * are skipped.
+ * Pinned by: numpy view assignment pool.reshape(B, L, 16, H, d)[b, layer, o] = new
+ * for the fresh-pool LIFO block order 0,1,2,... and a permuted block map
+ * (tests/test_oracle.py::test_paged_*). */
+void or_paged_kv_append_f16(uint16_t* k_pool, uint16_t* v_pool, const int64_t* block_offset,
+                            int n_blocks, const int32_t* slots, const uint16_t* k_new,
+                            const uint16_t* v_new, int n_tokens, int layer, int n_layers,
+                            int n_kv_heads, int head_dim) {
+    const size_t kv = (size_t)n_kv_heads * head_dim;
+    (void)n_layers;
+    for (int t = 0; t < n_tokens; ++t) {
+        const int32_t s = slots[t];
+        if (s < 0) continue;
+        const int b = s / 16, o = s % 16;
+        if (b >= n_blocks) continue;
+        const size_t base = (size_t)block_offset[b] + ((size_t)layer * 16 + (size_t)o) * kv;
+        for (size_t i = 0; i < kv; ++i) {
+            k_pool[base + i] = k_new[(size_t)t * kv + i];
+            v_pool[base + i] = v_new[(size_t)t * kv + i];
+        }
+    }
+}

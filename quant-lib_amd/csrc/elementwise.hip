@@ -1,0 +1,255 @@
+// elementwise.hip -- streaming kernels for gfx950: SwiGLU, residual add,
+// binary16 -> fp32 widening, and the contiguous KV-cache append (a pair of
+// copies).
+//
+// Every kernel moves each input once and each output once with 16-byte
+// accesses.  A workgroup owns a contiguous chunk of 256*U vectors; thread t
+// touches vectors t, t+256, ... so each wavefront instruction covers one
+// contiguous 1 KiB span, and all U loads of a thread are issued before any
+// arithmetic.  Elements past the last whole vector (n % W) are handled by
+// workgroup 0.  Unaligned pointers take the same kernels with W = 1.
+#include "ql_common.hpp"
+#include "quantlib_amd.h"
+
+namespace {
+
+using namespace ql;
+
+constexpr int kUnroll = 4;
+
+// SwiGLU: out = (g / (1 + exp(-g))) * u  (kernels/feedforward.cu:4-6,24;
+// kernels/fp16_ops.cu:74-77).  The quotient is g * rcp(1 + e) with v_rcp_f32
+// (1 ulp); 1 + e >= 1 so it is well conditioned.  v_rcp_f32 flushes subnormal
+// results, so for fp32 output a divisor above 2^126 is pre-scaled by 2^-64 and
+// the product rescaled (the final multiply keeps subnormals); e = inf still
+// gives the reference's signed zero.  binary16 output cannot represent that
+// range, so its path skips the rescale.
+struct SwigluOp {
+    template <typename D>
+    __device__ static float apply(float g, float u) {
+        if constexpr (sizeof(D) == 4) {
+            const float x = 1.0f + exp_f32(-g);
+            const bool big = x > 0x1p126f;
+            float q = g * __builtin_amdgcn_rcpf(big ? x * 0x1p-64f : x);
+            q = big ? q * 0x1p-64f : q;
+            return q * u;
+        } else {
+            return (g * __builtin_amdgcn_rcpf(1.0f + exp_f32_fast(-g))) * u;
+        }
+    }
+};
+
+// Residual add: x = round_D(x + d)  (src/forward.cu:128-130; kernels/fp16_ops.cu:92-100)
+struct AddOp {
+    template <typename D>
+    __device__ static float apply(float x, float d) { return x + d; }
+};
+
+// out[i] = op(a[i], b[i]) over n elements; out may alias a (in-place add).
+template <typename D, int W, typename Op>
+__global__ __launch_bounds__(kBlock) void binary_stream(const D* a, const D* b, D* out,
+                                                        long long n) {
+    using V = Vec<D, W>;
+    const long long nvec = n / W;
+    const long long base = (long long)blockIdx.x * (kBlock * kUnroll) + threadIdx.x;
+    const V* av = reinterpret_cast<const V*>(a);
+    const V* bv = reinterpret_cast<const V*>(b);
+    V* ov = reinterpret_cast<V*>(out);
+    V ra[kUnroll], rb[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const long long i = base + (long long)u * kBlock;
+        if (i < nvec) {
+            ra[u] = av[i];
+            rb[u] = bv[i];
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const long long i = base + (long long)u * kBlock;
+        if (i < nvec) {
+            V y;
+#pragma unroll
+            for (int e = 0; e < W; ++e)
+                y.v[e] = from_f32<D>(Op::template apply<D>(to_f32(ra[u].v[e]), to_f32(rb[u].v[e])));
+            ov[i] = y;
+        }
+    }
+    if (W > 1 && blockIdx.x == 0) {
+        for (long long i = nvec * W + threadIdx.x; i < n; i += kBlock)
+            out[i] = from_f32<D>(Op::template apply<D>(to_f32(a[i]), to_f32(b[i])));
+    }
+}
+
+template <typename D, typename Op>
+hipError_t launch_binary(const D* a, const D* b, D* out, long long n, hipStream_t stream) {
+    constexpr int W = vec16<D>();
+    const bool vec_ok = qlh::aligned16(a) && qlh::aligned16(b) && qlh::aligned16(out);
+    if (vec_ok) {
+        const long long nvec = n / W;
+        const unsigned grid = nvec > 0 ? qlh::blocks_for(nvec, (long long)kBlock * kUnroll) : 1;
+        hipLaunchKernelGGL((binary_stream<D, W, Op>), dim3(grid), dim3(kBlock), 0, stream, a, b,
+                           out, n);
+    } else {
+        const unsigned grid = qlh::blocks_for(n, (long long)kBlock * kUnroll);
+        hipLaunchKernelGGL((binary_stream<D, 1, Op>), dim3(grid), dim3(kBlock), 0, stream, a, b,
+                           out, n);
+    }
+    return hipGetLastError();
+}
+
+// binary16 -> fp32 widening (kernels/fp16_ops.cu:103-110).
+template <int W>
+__global__ __launch_bounds__(kBlock) void widen_stream(const _Float16* __restrict__ src,
+                                                       float* __restrict__ dst, long long n) {
+    using VI = Vec<_Float16, W>;
+    using VO = Vec<float, W>;
+    const long long nvec = n / W;
+    const long long base = (long long)blockIdx.x * (kBlock * kUnroll) + threadIdx.x;
+    VI r[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const long long i = base + (long long)u * kBlock;
+        if (i < nvec) r[u] = reinterpret_cast<const VI*>(src)[i];
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const long long i = base + (long long)u * kBlock;
+        if (i < nvec) {
+            VO y;
+#pragma unroll
+            for (int e = 0; e < W; ++e) y.v[e] = (float)r[u].v[e];
+            reinterpret_cast<VO*>(dst)[i] = y;
+        }
+    }
+    if (W > 1 && blockIdx.x == 0)
+        for (long long i = nvec * W + threadIdx.x; i < n; i += kBlock) dst[i] = (float)src[i];
+}
+
+// Two independent copies in one launch (blockIdx.y selects the pair): the K
+// and V halves of a contiguous KV append.  Copies move 16-byte units when all
+// four pointers and the byte count allow it, else `unit`-byte elements.
+template <int UNIT>
+__global__ __launch_bounds__(kBlock) void copy_pair(char* __restrict__ d0,
+                                                    const char* __restrict__ s0,
+                                                    char* __restrict__ d1,
+                                                    const char* __restrict__ s1,
+                                                    long long nbytes) {
+    using V = Vec<char, UNIT>;
+    char* dst = blockIdx.y == 0 ? d0 : d1;
+    const char* src = blockIdx.y == 0 ? s0 : s1;
+    const long long nvec = nbytes / UNIT;
+    const long long base = (long long)blockIdx.x * (kBlock * kUnroll) + threadIdx.x;
+    V r[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const long long i = base + (long long)u * kBlock;
+        if (i < nvec) r[u] = reinterpret_cast<const V*>(src)[i];
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const long long i = base + (long long)u * kBlock;
+        if (i < nvec) reinterpret_cast<V*>(dst)[i] = r[u];
+    }
+}
+
+template <typename D>
+hipError_t kv_append_dispatch(D* kc, D* vc, const D* kn, const D* vn, int layer, int pos,
+                              int n_tokens, int hkv, int hd, int max_seq, int n_layers,
+                              hipStream_t stream) {
+    QL_CHECK_ARG(n_tokens >= 0 && hkv > 0 && hd > 0 && max_seq > 0 && n_layers > 0);
+    QL_CHECK_ARG(layer >= 0 && layer < n_layers);
+    QL_CHECK_ARG(pos >= 0 && (long long)pos + n_tokens <= max_seq);
+    if (n_tokens == 0) return hipSuccess;
+    QL_CHECK_ARG(kc && vc && kn && vn);
+    const long long kv = (long long)hkv * hd;
+    const long long off = ((long long)layer * max_seq + pos) * kv;
+    const long long nbytes = (long long)n_tokens * kv * (long long)sizeof(D);
+    char* d0 = reinterpret_cast<char*>(kc + off);
+    char* d1 = reinterpret_cast<char*>(vc + off);
+    const char* s0 = reinterpret_cast<const char*>(kn);
+    const char* s1 = reinterpret_cast<const char*>(vn);
+    const bool vec_ok = qlh::aligned16(d0) && qlh::aligned16(d1) && qlh::aligned16(s0) &&
+                        qlh::aligned16(s1) && nbytes % 16 == 0;
+    if (vec_ok) {
+        hipLaunchKernelGGL((copy_pair<16>), dim3(qlh::blocks_for(nbytes / 16, kBlock * kUnroll), 2),
+                           dim3(kBlock), 0, stream, d0, s0, d1, s1, nbytes);
+    } else {
+        constexpr int U = (int)sizeof(D);
+        hipLaunchKernelGGL((copy_pair<U>), dim3(qlh::blocks_for(nbytes / U, kBlock * kUnroll), 2),
+                           dim3(kBlock), 0, stream, d0, s0, d1, s1, nbytes);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" hipError_t ql_swiglu_f32(const float* gate, const float* up, float* out, int rows,
+                                    int ffn_dim, hipStream_t stream) {
+    QL_CHECK_ARG(rows >= 0 && ffn_dim >= 0);
+    const long long n = (long long)rows * ffn_dim;
+    if (n == 0) return hipSuccess;
+    QL_CHECK_ARG(gate && up && out);
+    return launch_binary<float, SwigluOp>(gate, up, out, n, stream);
+}
+
+extern "C" hipError_t ql_swiglu_f16(const uint16_t* gate, const uint16_t* up, uint16_t* out,
+                                    int rows, int ffn_dim, hipStream_t stream) {
+    QL_CHECK_ARG(rows >= 0 && ffn_dim >= 0);
+    const long long n = (long long)rows * ffn_dim;
+    if (n == 0) return hipSuccess;
+    QL_CHECK_ARG(gate && up && out);
+    return launch_binary<_Float16, SwigluOp>(reinterpret_cast<const _Float16*>(gate),
+                                             reinterpret_cast<const _Float16*>(up),
+                                             reinterpret_cast<_Float16*>(out), n, stream);
+}
+
+extern "C" hipError_t ql_add_f32(float* x, const float* d, int64_t n, hipStream_t stream) {
+    QL_CHECK_ARG(n >= 0);
+    if (n == 0) return hipSuccess;
+    QL_CHECK_ARG(x && d);
+    return launch_binary<float, AddOp>(x, d, x, n, stream);
+}
+
+extern "C" hipError_t ql_add_f16(uint16_t* x, const uint16_t* d, int64_t n, hipStream_t stream) {
+    QL_CHECK_ARG(n >= 0);
+    if (n == 0) return hipSuccess;
+    QL_CHECK_ARG(x && d);
+    _Float16* xh = reinterpret_cast<_Float16*>(x);
+    return launch_binary<_Float16, AddOp>(xh, reinterpret_cast<const _Float16*>(d), xh, n,
+                                          stream);
+}
+
+extern "C" hipError_t ql_f16_to_f32(const uint16_t* src, float* dst, int64_t n,
+                                    hipStream_t stream) {
+    QL_CHECK_ARG(n >= 0);
+    if (n == 0) return hipSuccess;
+    QL_CHECK_ARG(src && dst);
+    const _Float16* s = reinterpret_cast<const _Float16*>(src);
+    if (qlh::aligned16(src) && qlh::aligned16(dst)) {
+        const long long nvec = n / 8;
+        const unsigned grid = nvec > 0 ? qlh::blocks_for(nvec, (long long)kBlock * kUnroll) : 1;
+        hipLaunchKernelGGL((widen_stream<8>), dim3(grid), dim3(kBlock), 0, stream, s, dst,
+                           (long long)n);
+    } else {
+        hipLaunchKernelGGL((widen_stream<1>), dim3(qlh::blocks_for(n, (long long)kBlock * kUnroll)),
+                           dim3(kBlock), 0, stream, s, dst, (long long)n);
+    }
+    return hipGetLastError();
+}
+
+extern "C" hipError_t ql_kv_append_f32(float* k_cache, float* v_cache, const float* k_new,
+                                       const float* v_new, int layer, int pos, int n_tokens,
+                                       int n_kv_heads, int head_dim, int max_seq, int n_layers,
+                                       hipStream_t stream) {
+    return kv_append_dispatch<float>(k_cache, v_cache, k_new, v_new, layer, pos, n_tokens,
+                                     n_kv_heads, head_dim, max_seq, n_layers, stream);
+}
+
+extern "C" hipError_t ql_kv_append_f16(uint16_t* k_cache, uint16_t* v_cache,
+                                       const uint16_t* k_new, const uint16_t* v_new, int layer,
+                                       int pos, int n_tokens, int n_kv_heads, int head_dim,
+                                       int max_seq, int n_layers, hipStream_t stream) {
+    return kv_append_dispatch<uint16_t>(k_cache, v_cache, k_new, v_new, layer, pos, n_tokens,
+                                        n_kv_heads, head_dim, max_seq, n_layers, stream);
+}

@@ -1,0 +1,100 @@
+// ql_common.hpp -- shared device helpers for the gfx950 kernels.
+//
+// Element types: kernels are written against the device element type D, either
+// `float` or `_Float16` (IEEE binary16; the C ABI passes it as uint16_t bits).
+// All arithmetic is fp32; binary16 values are widened exactly and narrowed with
+// round-to-nearest-even (v_cvt_f16_f32 in the default rounding mode).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+namespace ql {
+
+constexpr int kWave = 64;      // CDNA wavefront width
+constexpr int kBlock = 256;    // default workgroup: 4 wavefronts
+
+// W contiguous elements moved as one access (16 bytes for the vector paths).
+template <typename D, int W>
+struct alignas(sizeof(D) * W) Vec {
+    D v[W];
+};
+
+// 16-byte vector width in elements of D.
+template <typename D>
+constexpr int vec16() { return 16 / (int)sizeof(D); }
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(_Float16 x) { return (float)x; }
+
+template <typename D>
+__device__ __forceinline__ D from_f32(float x);
+template <>
+__device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <>
+__device__ __forceinline__ _Float16 from_f32<_Float16>(float x) { return (_Float16)x; }
+
+// Round x to the precision of D and back (identity for float).
+template <typename D>
+__device__ __forceinline__ float round_to(float x) { return to_f32(from_f32<D>(x)); }
+
+// Butterfly reductions over the 64 lanes of a wavefront.  Lane i combines
+// with lane i^o at every step, so all lanes finish with bit-identical values
+// (a+b == b+a and max is order-free).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+// exp(y) in fp32 from the hardware base-2 exponential (v_exp_f32).
+// y*log2(e) is formed as t + err with log2(e) split into hi/lo parts and an
+// FMA residual (the classic compensated product), then
+// exp(y) = 2^t * 2^err ~= 2^t * (1 + err*ln2); the correction keeps the
+// argument error below one fp32 ulp for |y| <= 110.  Outside [-110, 110] the
+// result is 0 or +inf in fp32 anyway, so y is clamped there (comparisons keep NaN).
+__device__ __forceinline__ float exp_f32(float y) {
+    const float kL2eHi = 1.44269502162933349609375f;  // fp32(log2 e)
+    const float kL2eLo = 1.925963033500011e-08f;      // log2 e - kL2eHi
+    const float kLn2 = 0.693147180559945309f;
+    y = (y < -110.0f) ? -110.0f : y;
+    y = (y > 110.0f) ? 110.0f : y;
+    const float t = y * kL2eHi;
+    const float err = fmaf(y, kL2eHi, -t) + y * kL2eLo;
+    const float r = __builtin_amdgcn_exp2f(t);
+    return r * (1.0f + err * kLn2);
+}
+
+// exp(y) without the residual correction: relative error ~|y|*2^-24 plus the
+// v_exp_f32 error; used where the output is binary16 (2^-11 rounding).
+__device__ __forceinline__ float exp_f32_fast(float y) {
+    const float kL2e = 1.44269502162933349609375f;
+    y = (y < -110.0f) ? -110.0f : y;
+    y = (y > 110.0f) ? 110.0f : y;
+    return __builtin_amdgcn_exp2f(y * kL2e);
+}
+
+}  // namespace ql
+
+// ---- host-side helpers --------------------------------------------------------
+namespace qlh {
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+inline unsigned blocks_for(long long work, long long per_block) {
+    return (unsigned)((work + per_block - 1) / per_block);
+}
+
+}  // namespace qlh
+
+#define QL_CHECK_ARG(cond)                         \
+    do {                                           \
+        if (!(cond)) return hipErrorInvalidValue;  \
+    } while (0)

@@ -1,0 +1,202 @@
+// rmsnorm.hip -- RMSNorm and fused residual-add + RMSNorm for gfx950.
+//
+// Arithmetic (kernels/rmsnorm.cu:27-48, kernels/fp16_ops.cu:18-41):
+//   ss  = sum_i x_i^2                       (fp32)
+//   inv = 1 / sqrt(ss / dim + eps)          (correctly rounded div and sqrt)
+//   y_i = (x_i * inv) * w_i                 (fp32, then RNE to binary16 for fp16)
+// Fused add (src/fp16_forward.cu:213-216 chain): x_i <- round_D(x_i + d_i) is
+// stored and the norm is taken of that rounded value.
+//
+// Layout: rows of `dim` contiguous elements.  Fast path: the row is held in
+// registers; WPR wavefronts share a row, each lane owns NV 16-byte vectors
+// (vector index lane + k*64*WPR, so every load instruction of a wavefront is
+// one contiguous 1 KiB span).  x (and d) are read once and y (and x') written
+// once: 2 (4 fused) row transfers per row, the HBM minimum.  Rows too wide for
+// registers, or unaligned layouts, take a block-per-row loop that re-reads x.
+#include "ql_common.hpp"
+#include "quantlib_amd.h"
+
+namespace {
+
+using namespace ql;
+
+template <typename D, int NV, int WPR, bool ADD>
+__global__ __launch_bounds__(WPR <= 4 ? kBlock : kWave * WPR) void rmsnorm_rows(
+    D* x, const D* __restrict__ d, const D* __restrict__ w, D* __restrict__ out,
+    int rows, int dim, float eps) {
+    constexpr int W = vec16<D>();
+    constexpr int TPR = kWave * WPR;                       // threads per row
+    constexpr int BLOCK = WPR <= 4 ? kBlock : kWave * WPR;
+    constexpr int RPB = BLOCK / TPR;                       // rows per block
+    using V = Vec<D, W>;
+
+    const int tid = threadIdx.x;
+    const int row = blockIdx.x * RPB + tid / TPR;
+    const int rl = tid % TPR;
+    const bool row_ok = row < rows;
+    const int nvec = dim / W;
+    const size_t roff = (size_t)(row_ok ? row : 0) * (size_t)dim;
+
+    V* xr = reinterpret_cast<V*>(x + roff);
+    const V* dr = reinterpret_cast<const V*>(ADD ? d + roff : d);
+    const V* wr = reinterpret_cast<const V*>(w);
+
+    V xv[NV], wv[NV];
+    V dv[ADD ? NV : 1];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int vi = rl + k * TPR;
+        if (row_ok && vi < nvec) {
+            xv[k] = xr[vi];
+            if constexpr (ADD) dv[k] = dr[vi];
+            wv[k] = wr[vi];
+        }
+    }
+
+    // Values stay in D precision (exact for the rounded sum) to halve the
+    // register footprint of binary16 rows; they are widened again for output.
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int vi = rl + k * TPR;
+        if (row_ok && vi < nvec) {
+#pragma unroll
+            for (int e = 0; e < W; ++e) {
+                float a = to_f32(xv[k].v[e]);
+                if constexpr (ADD) {
+                    a = to_f32(dv[k].v[e]) + a;
+                    xv[k].v[e] = from_f32<D>(a);
+                    a = to_f32(xv[k].v[e]);
+                }
+                ss = fmaf(a, a, ss);
+            }
+        }
+    }
+
+    ss = wave_sum(ss);
+    if constexpr (WPR > 1) {
+        __shared__ float red[BLOCK / kWave];
+        if ((tid & (kWave - 1)) == 0) red[tid / kWave] = ss;
+        __syncthreads();
+        const int w0 = (tid / TPR) * WPR;
+        ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < WPR; ++i) ss += red[w0 + i];
+    }
+    const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+
+    V* orow = reinterpret_cast<V*>(out + roff);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int vi = rl + k * TPR;
+        if (row_ok && vi < nvec) {
+            V y;
+#pragma unroll
+            for (int e = 0; e < W; ++e)
+                y.v[e] = from_f32<D>((to_f32(xv[k].v[e]) * inv) * to_f32(wv[k].v[e]));
+            if constexpr (ADD) xr[vi] = xv[k];
+            orow[vi] = y;
+        }
+    }
+}
+
+// Block-per-row loop for any dim / alignment.  Same arithmetic; x' is written
+// in the first pass and re-read by the same thread in the second.
+template <typename D, bool ADD>
+__global__ __launch_bounds__(kBlock) void rmsnorm_rows_generic(
+    D* x, const D* __restrict__ d, const D* __restrict__ w, D* __restrict__ out,
+    int rows, int dim, float eps) {
+    const int row = blockIdx.x;  // grid.x == rows
+    (void)rows;
+    const int tid = threadIdx.x;
+    const size_t roff = (size_t)row * (size_t)dim;
+    float ss = 0.0f;
+    for (int i = tid; i < dim; i += kBlock) {
+        float a = to_f32(x[roff + i]);
+        if constexpr (ADD) {
+            a = round_to<D>(a + to_f32(d[roff + i]));
+            x[roff + i] = from_f32<D>(a);
+        }
+        ss = fmaf(a, a, ss);
+    }
+    ss = wave_sum(ss);
+    __shared__ float red[kBlock / kWave];
+    if ((tid & (kWave - 1)) == 0) red[tid / kWave] = ss;
+    __syncthreads();
+    ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kBlock / kWave; ++i) ss += red[i];
+    const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+    for (int i = tid; i < dim; i += kBlock) {
+        const float a = to_f32(x[roff + i]);
+        out[roff + i] = from_f32<D>((a * inv) * to_f32(w[i]));
+    }
+}
+
+template <typename D, int NV, int WPR, bool ADD>
+hipError_t launch_fast(D* x, const D* d, const D* w, D* out, int rows, int dim, float eps,
+                       hipStream_t stream) {
+    constexpr int BLOCK = WPR <= 4 ? kBlock : kWave * WPR;
+    constexpr int RPB = BLOCK / (kWave * WPR);
+    const unsigned grid = qlh::blocks_for(rows, RPB);
+    hipLaunchKernelGGL((rmsnorm_rows<D, NV, WPR, ADD>), dim3(grid), dim3(BLOCK), 0, stream,
+                       x, d, w, out, rows, dim, eps);
+    return hipGetLastError();
+}
+
+template <typename D, bool ADD>
+hipError_t rmsnorm_dispatch(D* x, const D* d, const D* w, D* out, int rows, int dim,
+                            float eps, hipStream_t stream) {
+    QL_CHECK_ARG(rows >= 0 && dim >= 0);
+    if (rows == 0) return hipSuccess;
+    QL_CHECK_ARG(dim > 0);
+    QL_CHECK_ARG(x && w && out && (!ADD || d));
+    constexpr int W = vec16<D>();
+    const bool vec_ok = dim % W == 0 && qlh::aligned16(x) && qlh::aligned16(w) &&
+                        qlh::aligned16(out) && (!ADD || qlh::aligned16(d));
+    const int nvec = dim / W;
+    if (vec_ok) {
+        if (nvec <= 64) return launch_fast<D, 1, 1, ADD>(x, d, w, out, rows, dim, eps, stream);
+        if (nvec <= 128) return launch_fast<D, 2, 1, ADD>(x, d, w, out, rows, dim, eps, stream);
+        if (nvec <= 256) return launch_fast<D, 4, 1, ADD>(x, d, w, out, rows, dim, eps, stream);
+        if (nvec <= 512) return launch_fast<D, 8, 1, ADD>(x, d, w, out, rows, dim, eps, stream);
+        if (nvec <= 1024) return launch_fast<D, 8, 2, ADD>(x, d, w, out, rows, dim, eps, stream);
+        if (nvec <= 2048) return launch_fast<D, 8, 4, ADD>(x, d, w, out, rows, dim, eps, stream);
+        if (nvec <= 4096) return launch_fast<D, 8, 8, ADD>(x, d, w, out, rows, dim, eps, stream);
+        if (nvec <= 8192) return launch_fast<D, 8, 16, ADD>(x, d, w, out, rows, dim, eps, stream);
+    }
+    hipLaunchKernelGGL((rmsnorm_rows_generic<D, ADD>), dim3((unsigned)rows), dim3(kBlock), 0,
+                       stream, x, d, w, out, rows, dim, eps);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" hipError_t ql_rmsnorm_f32(const float* x, const float* w, float* out, int rows,
+                                     int dim, float eps, hipStream_t stream) {
+    return rmsnorm_dispatch<float, false>(const_cast<float*>(x), nullptr, w, out, rows, dim,
+                                          eps, stream);
+}
+
+extern "C" hipError_t ql_rmsnorm_f16(const uint16_t* x, const uint16_t* w, uint16_t* out,
+                                     int rows, int dim, float eps, hipStream_t stream) {
+    return rmsnorm_dispatch<_Float16, false>(
+        reinterpret_cast<_Float16*>(const_cast<uint16_t*>(x)), nullptr,
+        reinterpret_cast<const _Float16*>(w), reinterpret_cast<_Float16*>(out), rows, dim,
+        eps, stream);
+}
+
+extern "C" hipError_t ql_add_rmsnorm_f32(float* x, const float* d, const float* w,
+                                         float* out, int rows, int dim, float eps,
+                                         hipStream_t stream) {
+    return rmsnorm_dispatch<float, true>(x, d, w, out, rows, dim, eps, stream);
+}
+
+extern "C" hipError_t ql_add_rmsnorm_f16(uint16_t* x, const uint16_t* d, const uint16_t* w,
+                                         uint16_t* out, int rows, int dim, float eps,
+                                         hipStream_t stream) {
+    return rmsnorm_dispatch<_Float16, true>(
+        reinterpret_cast<_Float16*>(x), reinterpret_cast<const _Float16*>(d),
+        reinterpret_cast<const _Float16*>(w), reinterpret_cast<_Float16*>(out), rows, dim,
+        eps, stream);
+}

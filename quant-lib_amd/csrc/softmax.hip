@@ -1,0 +1,192 @@
+// softmax.hip -- numerically stable row softmax for gfx950.
+//
+// Arithmetic (kernels/softmax.cu:44-85):
+//   m   = max(-FLT_MAX, max_c x_c)
+//   e_c = exp(x_c - m)             (-inf inputs give exactly 0)
+//   out = e_c * (1 / sum_c e_c)    (one correctly rounded division per row)
+// The reference makes three passes over the row (max; exp + write e; rescale),
+// i.e. three reads and two writes.  Here the row lives in registers: one read
+// and one write per element.  WPR wavefronts share a row; each lane holds NV
+// 16-byte vectors, lanes past the row end hold -inf (no effect on max or sum).
+// The fp16 variant (no reference kernel) is the same fp32 arithmetic with
+// binary16 input and RNE binary16 output.
+#include <float.h>
+
+#include "ql_common.hpp"
+#include "quantlib_amd.h"
+
+namespace {
+
+using namespace ql;
+
+template <typename D>
+__device__ __forceinline__ float softmax_exp(float y) {
+    // fp32 output keeps the residual-corrected exponential (1e-5 relative
+    // budget); binary16 output cannot see the difference.
+    if constexpr (sizeof(D) == 4) return exp_f32(y);
+    else return exp_f32_fast(y);
+}
+
+template <typename D, int NV, int WPR>
+__global__ __launch_bounds__(WPR <= 4 ? kBlock : kWave * WPR) void softmax_rows(
+    const D* __restrict__ in, D* __restrict__ out, int rows, int cols) {
+    constexpr int W = vec16<D>();
+    constexpr int TPR = kWave * WPR;
+    constexpr int BLOCK = WPR <= 4 ? kBlock : kWave * WPR;
+    constexpr int RPB = BLOCK / TPR;
+    using V = Vec<D, W>;
+
+    const int tid = threadIdx.x;
+    const int row = blockIdx.x * RPB + tid / TPR;
+    const int rl = tid % TPR;
+    const bool row_ok = row < rows;
+    const int nvec = cols / W;
+    const size_t roff = (size_t)(row_ok ? row : 0) * (size_t)cols;
+    const V* src = reinterpret_cast<const V*>(in + roff);
+
+    V raw[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int vi = rl + k * TPR;
+        if (row_ok && vi < nvec) raw[k] = src[vi];
+    }
+
+    float v[NV][W];
+    float m = -FLT_MAX;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int vi = rl + k * TPR;
+        const bool ok = row_ok && vi < nvec;
+#pragma unroll
+        for (int e = 0; e < W; ++e) {
+            v[k][e] = ok ? to_f32(raw[k].v[e]) : -INFINITY;
+            m = fmaxf(m, v[k][e]);
+        }
+    }
+    m = wave_max(m);
+    if constexpr (WPR > 1) {
+        __shared__ float redm[BLOCK / kWave];
+        if ((tid & (kWave - 1)) == 0) redm[tid / kWave] = m;
+        __syncthreads();
+        const int w0 = (tid / TPR) * WPR;
+        m = -FLT_MAX;
+#pragma unroll
+        for (int i = 0; i < WPR; ++i) m = fmaxf(m, redm[w0 + i]);
+    }
+
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+#pragma unroll
+        for (int e = 0; e < W; ++e) {
+            v[k][e] = softmax_exp<D>(v[k][e] - m);
+            s += v[k][e];
+        }
+    }
+    s = wave_sum(s);
+    if constexpr (WPR > 1) {
+        __shared__ float reds[BLOCK / kWave];
+        if ((tid & (kWave - 1)) == 0) reds[tid / kWave] = s;
+        __syncthreads();
+        const int w0 = (tid / TPR) * WPR;
+        s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < WPR; ++i) s += reds[w0 + i];
+    }
+    const float inv = 1.0f / s;
+
+    V* dst = reinterpret_cast<V*>(out + roff);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int vi = rl + k * TPR;
+        if (row_ok && vi < nvec) {
+            V y;
+#pragma unroll
+            for (int e = 0; e < W; ++e) y.v[e] = from_f32<D>(v[k][e] * inv);
+            dst[vi] = y;
+        }
+    }
+}
+
+// Block-per-row three-pass loop for any width / alignment (exp recomputed in
+// pass 3, bit-identical to pass 2).
+template <typename D>
+__global__ __launch_bounds__(kBlock) void softmax_rows_generic(const D* __restrict__ in,
+                                                              D* __restrict__ out, int rows,
+                                                              int cols) {
+    const int row = blockIdx.x;  // grid.x == rows
+    (void)rows;
+    const int tid = threadIdx.x;
+    const size_t roff = (size_t)row * (size_t)cols;
+    __shared__ float red[kBlock / kWave];
+
+    float m = -FLT_MAX;
+    for (int c = tid; c < cols; c += kBlock) m = fmaxf(m, to_f32(in[roff + c]));
+    m = wave_max(m);
+    if ((tid & (kWave - 1)) == 0) red[tid / kWave] = m;
+    __syncthreads();
+    m = -FLT_MAX;
+#pragma unroll
+    for (int i = 0; i < kBlock / kWave; ++i) m = fmaxf(m, red[i]);
+    __syncthreads();
+
+    float s = 0.0f;
+    for (int c = tid; c < cols; c += kBlock) s += softmax_exp<D>(to_f32(in[roff + c]) - m);
+    s = wave_sum(s);
+    if ((tid & (kWave - 1)) == 0) red[tid / kWave] = s;
+    __syncthreads();
+    s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kBlock / kWave; ++i) s += red[i];
+    const float inv = 1.0f / s;
+
+    for (int c = tid; c < cols; c += kBlock)
+        out[roff + c] = from_f32<D>(softmax_exp<D>(to_f32(in[roff + c]) - m) * inv);
+}
+
+template <typename D, int NV, int WPR>
+hipError_t launch_fast(const D* in, D* out, int rows, int cols, hipStream_t stream) {
+    constexpr int BLOCK = WPR <= 4 ? kBlock : kWave * WPR;
+    constexpr int RPB = BLOCK / (kWave * WPR);
+    hipLaunchKernelGGL((softmax_rows<D, NV, WPR>), dim3(qlh::blocks_for(rows, RPB)),
+                       dim3(BLOCK), 0, stream, in, out, rows, cols);
+    return hipGetLastError();
+}
+
+template <typename D>
+hipError_t softmax_dispatch(const D* in, D* out, int rows, int cols, hipStream_t stream) {
+    QL_CHECK_ARG(rows >= 0 && cols >= 0);
+    if (rows == 0) return hipSuccess;
+    QL_CHECK_ARG(cols > 0);
+    QL_CHECK_ARG(in && out);
+    constexpr int W = vec16<D>();
+    const bool vec_ok = cols % W == 0 && qlh::aligned16(in) && qlh::aligned16(out);
+    const int nvec = cols / W;
+    if (vec_ok) {
+        if (nvec <= 64) return launch_fast<D, 1, 1>(in, out, rows, cols, stream);
+        if (nvec <= 128) return launch_fast<D, 2, 1>(in, out, rows, cols, stream);
+        if (nvec <= 256) return launch_fast<D, 4, 1>(in, out, rows, cols, stream);
+        if (nvec <= 512) return launch_fast<D, 8, 1>(in, out, rows, cols, stream);
+        if (nvec <= 1024) return launch_fast<D, 16, 1>(in, out, rows, cols, stream);
+        if (nvec <= 2048) return launch_fast<D, 16, 2>(in, out, rows, cols, stream);
+        if (nvec <= 4096) return launch_fast<D, 16, 4>(in, out, rows, cols, stream);
+        if (nvec <= 8192) return launch_fast<D, 16, 8>(in, out, rows, cols, stream);
+        if (nvec <= 16384) return launch_fast<D, 16, 16>(in, out, rows, cols, stream);
+    }
+    hipLaunchKernelGGL((softmax_rows_generic<D>), dim3((unsigned)rows), dim3(kBlock), 0,
+                       stream, in, out, rows, cols);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" hipError_t ql_softmax_f32(const float* in, float* out, int rows, int cols,
+                                     hipStream_t stream) {
+    return softmax_dispatch<float>(in, out, rows, cols, stream);
+}
+
+extern "C" hipError_t ql_softmax_f16(const uint16_t* in, uint16_t* out, int rows, int cols,
+                                     hipStream_t stream) {
+    return softmax_dispatch<_Float16>(reinterpret_cast<const _Float16*>(in),
+                                      reinterpret_cast<_Float16*>(out), rows, cols, stream);
+}

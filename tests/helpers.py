@@ -1,0 +1,134 @@
+"""Shared test helpers: seeded inputs, device transfer, tolerance checks.
+
+Tolerances, |got - want| <= rtol*|want| + atol:
+  fp32 RMSNorm / softmax / SwiGLU : rtol 1e-5, atol 2^-126 (fp32 subnormal results)
+  fp32 RoPE                        : absolute 1e-6
+  binary16 variants                : rtol 2e-3, atol 2^-24 (one binary16 subnormal step)
+  gather / KV append               : bit-exact
+"""
+from __future__ import annotations
+
+import numpy as np
+
+RTOL_F32 = 1e-5
+ATOL_F32 = 2.0 ** -126
+ATOL_ROPE_F32 = 1e-6
+RTOL_F16 = 2e-3
+ATOL_F16 = 2.0 ** -24
+
+
+def rng(seed: int) -> np.random.Generator:
+    return np.random.default_rng(seed)
+
+
+def normal(seed: int, shape, sigma: float = 1.0, clip: float | None = None) -> np.ndarray:
+    x = rng(seed).standard_normal(size=shape, dtype=np.float32) * np.float32(sigma)
+    if clip is not None:
+        np.clip(x, -clip, clip, out=x)
+    return x
+
+
+def uniform(seed: int, shape, lo: float, hi: float) -> np.ndarray:
+    return rng(seed).uniform(lo, hi, size=shape).astype(np.float32)
+
+
+def causal_mask_inplace(x: np.ndarray) -> np.ndarray:
+    """-inf strictly above the diagonal (column > row)."""
+    rows, cols = x.shape
+    x[np.triu_indices(rows, k=1, m=cols)] = -np.inf
+    return x
+
+
+def to_f16_bits(x: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(x.astype(np.float16)).view(np.uint16)
+
+
+def f16_bits_to_f32(h: np.ndarray) -> np.ndarray:
+    return h.view(np.float16).astype(np.float32)
+
+
+def check_close(got: np.ndarray, want: np.ndarray, rtol: float, atol: float, what: str = ""):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    assert got.shape == want.shape, (got.shape, want.shape)
+    nan_g, nan_w = np.isnan(got), np.isnan(want)
+    assert np.array_equal(nan_g, nan_w), f"{what}: NaN pattern differs ({nan_g.sum()} vs {nan_w.sum()})"
+    g, w = got[~nan_w], want[~nan_w]
+    inf_w = np.isinf(w)
+    assert np.array_equal(g[inf_w], w[inf_w]), f"{what}: inf mismatch"
+    g, w = g[~inf_w], w[~inf_w]
+    err = np.abs(g - w)
+    bound = rtol * np.abs(w) + atol
+    bad = err > bound
+    if bad.any():
+        i = int(np.argmax(err - bound))
+        raise AssertionError(
+            f"{what}: {int(bad.sum())} of {g.size} elements outside rtol={rtol} atol={atol}; "
+            f"worst got={g[i]!r} want={w[i]!r} err={err[i]:.3e}")
+    return float((err / np.maximum(np.abs(w), atol)).max()) if err.size else 0.0
+
+
+def check_f16(got_bits: np.ndarray, want_bits: np.ndarray, what: str = ""):
+    return check_close(f16_bits_to_f32(got_bits), f16_bits_to_f32(want_bits), RTOL_F16, ATOL_F16,
+                       what)
+
+
+def check_abs(got: np.ndarray, want: np.ndarray, atol: float, what: str = ""):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    err = np.abs(got - want)
+    m = float(err.max()) if err.size else 0.0
+    assert m <= atol, f"{what}: max abs error {m:.3e} > {atol}"
+    return m
+
+
+# ---- device side (torch is the allocator and stream provider only) -------------------
+def dev(a: np.ndarray, offset_elems: int = 0):
+    """Copy a numpy array to cuda:0.  uint16 arrays travel as int16 bit patterns.
+    offset_elems > 0 returns a view starting that many elements into a larger
+    buffer (to exercise unaligned paths)."""
+    import torch
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    t = torch.from_numpy(a.reshape(-1))
+    if offset_elems:
+        buf = torch.empty(t.numel() + offset_elems, dtype=t.dtype)
+        buf[offset_elems:] = t
+        d = buf.to("cuda:0")[offset_elems:]
+    else:
+        d = t.to("cuda:0")
+    return d
+
+
+def host(t, dtype=None, shape=None) -> np.ndarray:
+    import torch
+    torch.cuda.synchronize()
+    a = t.detach().cpu().numpy()
+    if a.dtype == np.int16:
+        a = a.view(np.uint16)
+    if dtype is not None:
+        a = a.view(dtype)
+    if shape is not None:
+        a = a.reshape(shape)
+    return a
+
+
+def empty(shape, dtype, fill_bits: int | None = None):
+    """Device buffer; fill_bits sets every byte (guard pattern)."""
+    import torch
+    n = int(np.prod(shape))
+    tdt = {np.float32: torch.float32, np.uint16: torch.int16, np.int32: torch.int32}[dtype]
+    t = torch.empty(n, dtype=tdt, device="cuda:0")
+    if fill_bits is not None:
+        t.view(torch.uint8).fill_(fill_bits)
+    return t
+
+
+def stream() -> int:
+    import torch
+    return torch.cuda.current_stream().cuda_stream
+
+
+def ptr(t) -> int:
+    return t.data_ptr()

@@ -1,0 +1,120 @@
+"""CPU checks of the drop-in boundary: the library loads, exports every symbol
+the headers declare (C ABI and the reference-named C++ shims), and rejects bad
+arguments on the host before any GPU call (no compute is launched here)."""
+import ctypes
+import re
+import subprocess
+
+import pytest
+
+import quantlib_amd as ql
+from conftest import ROOT
+
+INVALID = ql.HIP_ERROR_INVALID_VALUE
+
+# Itanium-mangled names of the reference-named C++ shims (quantlib_compat.h).
+COMPAT_MANGLED = {
+    "launch_rmsnorm": "_Z14launch_rmsnormPKfS0_PfiifP12ihipStream_t",
+    "launch_rope": "_Z11launch_ropePfiiifP12ihipStream_t",
+    "launch_swiglu": "_Z13launch_swigluPKfS0_PfiiP12ihipStream_t",
+    "launch_softmax": "_Z14launch_softmaxPKfPfiiP12ihipStream_t",
+    "launch_fp16_rmsnorm": "_Z19launch_fp16_rmsnormPK6__halfS1_PS_iifP12ihipStream_t",
+    "launch_fp16_rope": "_Z16launch_fp16_ropeP6__halfiiifP12ihipStream_t",
+    "launch_fp16_swiglu": "_Z18launch_fp16_swigluPK6__halfS1_PS_iiP12ihipStream_t",
+    "launch_fp16_embed": "_Z17launch_fp16_embedPK6__halfPS_iiP12ihipStream_t",
+    "launch_fp16_add": "_Z15launch_fp16_addP6__halfPKS_iP12ihipStream_t",
+    "launch_fp16_to_fp32": "_Z19launch_fp16_to_fp32PK6__halfPfiP12ihipStream_t",
+    "add_residual": "_Z12add_residualPfPKfiP12ihipStream_t",
+    "launch_embed": "_Z12launch_embedPfPKfiiP12ihipStream_t",
+    "launch_fp16_kvcache_append": "_Z26launch_fp16_kvcache_appendP6__halfS0_PKS_S2_iiiiiiP12ihipStream_t",
+    "kvcache_create": "_Z14kvcache_createiiii",
+    "kvcache_free": "_Z12kvcache_freeP7KVCache",
+    "kvcache_append": "_Z14kvcache_appendP7KVCacheiPKfS2_P12ihipStream_t",
+    "kvcache_get_k": "_Z13kvcache_get_kP7KVCachei",
+    "kvcache_get_v": "_Z13kvcache_get_vP7KVCachei",
+    "fp16_kvcache_create": "_Z19fp16_kvcache_createiiii",
+    "fp16_kvcache_free": "_Z17fp16_kvcache_freeP11FP16KVCache",
+    "paged_kv_create": "paged_kv_create",
+    "paged_kv_free": "paged_kv_free",
+    "paged_kv_allocate_block": "paged_kv_allocate_block",
+    "paged_kv_free_block": "paged_kv_free_block",
+}
+
+
+def test_library_loads_and_reports_version():
+    assert ql.version() == 100
+
+
+def test_every_c_abi_symbol_declared_is_exported_and_bound():
+    declared = ql.declared_symbols()
+    assert len(declared) >= 20
+    h = ql.lib()
+    for name in declared:
+        assert hasattr(h, name), name
+    assert set(declared) == set(ql.SIGNATURES), set(declared) ^ set(ql.SIGNATURES)
+
+
+def test_every_compat_name_is_declared_and_exported():
+    text = re.sub(r"/\*.*?\*/", "", (ROOT / "include" / "quantlib_compat.h").read_text(), flags=re.S)
+    declared = set(re.findall(r"\b([a-z_0-9]+)\s*\(", text)) - {"defined"}
+    assert declared == set(COMPAT_MANGLED), declared ^ set(COMPAT_MANGLED)
+    out = subprocess.run(["nm", "-D", "--defined-only", str(ql.LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    for name, mangled in COMPAT_MANGLED.items():
+        assert mangled in exported, (name, mangled)
+
+
+# Host-side validation: each call below must return hipErrorInvalidValue
+# (or hipSuccess for an empty problem) without touching the GPU.
+P = 4096  # a non-null, 16-byte aligned dummy address: never dereferenced on these paths
+
+
+@pytest.mark.parametrize("call,expect", [
+    (("ql_rmsnorm_f32", P, P, P, -1, 16, 1e-5, None), INVALID),
+    (("ql_rmsnorm_f32", P, P, P, 4, -1, 1e-5, None), INVALID),
+    (("ql_rmsnorm_f32", P, P, P, 4, 0, 1e-5, None), INVALID),
+    (("ql_rmsnorm_f32", None, P, P, 4, 16, 1e-5, None), INVALID),
+    (("ql_rmsnorm_f16", P, None, P, 4, 16, 1e-5, None), INVALID),
+    (("ql_rmsnorm_f32", None, None, None, 0, 16, 1e-5, None), 0),
+    (("ql_add_rmsnorm_f16", P, None, P, P, 4, 16, 1e-5, None), INVALID),
+    (("ql_add_f32", P, P, -5, None), INVALID),
+    (("ql_add_f16", None, P, 5, None), INVALID),
+    (("ql_add_f16", None, None, 0, None), 0),
+    (("ql_rope_f32", P, P, 4, 8, 2, 63, 504, 126, None, 0, 1e4, 0, None), INVALID),   # odd d
+    (("ql_rope_f32", P, P, 4, 8, 2, 4096, 8 * 4096, 2 * 4096, None, 0, 1e4, 0, None), INVALID),  # d>2048
+    (("ql_rope_f16", P, P, 4, 8, 2, 64, 100, 128, None, 0, 1e4, 0, None), INVALID),  # q stride < H*d
+    (("ql_rope_f16", P, P, 4, 8, 2, 64, 512, 128, None, 0, 1e4, 2, None), INVALID),  # pairing
+    (("ql_rope_f16", P, P, 4, 8, 2, 64, 512, 128, None, 0, 0.0, 0, None), INVALID),  # theta
+    (("ql_rope_f16", None, None, 4, 8, 2, 64, 512, 128, None, 0, 1e4, 0, None), 0),  # nothing to do
+    (("ql_swiglu_f32", P, P, P, 3, -1, None), INVALID),
+    (("ql_swiglu_f16", P, None, P, 3, 8, None), INVALID),
+    (("ql_swiglu_f16", None, None, None, 0, 8, None), 0),
+    (("ql_softmax_f32", P, P, 2, 0, None), INVALID),
+    (("ql_softmax_f16", None, P, 2, 8, None), INVALID),
+    (("ql_embed_f16", P, None, 4, 100, 64, P, None), INVALID),
+    (("ql_embed_f32", P, P, -1, 100, 64, P, None), INVALID),
+    (("ql_embed_token_f16", None, 3, 64, P, None), INVALID),
+    (("ql_kv_append_f32", P, P, P, P, 2, 0, 1, 8, 128, 16, 2, None), INVALID),   # layer == n_layers
+    (("ql_kv_append_f32", P, P, P, P, 0, 15, 2, 8, 128, 16, 2, None), INVALID),  # pos+T > max_seq
+    (("ql_kv_append_f16", P, None, P, P, 0, 0, 1, 8, 128, 16, 2, None), INVALID),
+    (("ql_kv_append_f16", None, None, None, None, 0, 3, 0, 8, 128, 16, 2, None), 0),
+    (("ql_paged_kv_append_f16", P, P, 4, P, P, P, 10, 4, 4, 8, 128, None), INVALID),  # layer
+    (("ql_paged_kv_append_f16", P, None, 4, P, P, P, 10, 0, 4, 8, 128, None), INVALID),
+    (("ql_f16_to_f32", P, P, -1, None), INVALID),
+])
+def test_argument_validation(call, expect):
+    name, *args = call
+    assert ql.raw(name, *args) == expect
+
+
+def test_paged_slot_mapping_host_helper():
+    table = (ctypes.c_int32 * 3)(4, 0, 7)
+    slots = (ctypes.c_int32 * 40)()
+    assert ql.raw("ql_paged_slot_mapping", ctypes.addressof(table), 3, 5, 40, ctypes.addressof(slots)) == 0
+    want = [[4, 0, 7][(5 + i) // 16] * 16 + (5 + i) % 16 for i in range(40)]
+    assert list(slots) == want
+    # position beyond the table, or an unassigned (-1) block, is an error
+    assert ql.raw("ql_paged_slot_mapping", ctypes.addressof(table), 3, 40, 10, ctypes.addressof(slots)) == INVALID
+    bad = (ctypes.c_int32 * 2)(3, -1)
+    assert ql.raw("ql_paged_slot_mapping", ctypes.addressof(bad), 2, 10, 10, ctypes.addressof(slots)) == INVALID

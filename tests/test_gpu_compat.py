@@ -1,0 +1,230 @@
+"""The reference's own tests, rerun against the drop-in shims that keep the
+reference's names and signatures (include/quantlib_compat.h), on the GPU."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle as orc
+import quantlib_amd as ql
+from helpers import (ATOL_ROPE_F32, RTOL_F32, ATOL_F32, check_abs, check_close, check_f16, dev,
+                     empty, host, normal, ptr, stream, to_f16_bits, uniform)
+from test_abi import COMPAT_MANGLED
+
+pytestmark = pytest.mark.gpu
+
+_p, _i, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+
+
+class KVCache(ctypes.Structure):  # include/kv_cache.h:12-20
+    _fields_ = [("k_cache", _p), ("v_cache", _p), ("n_layers", _i), ("max_seq_len", _i),
+                ("n_heads", _i), ("head_dim", _i), ("current_len", _i)]
+
+
+class PagedKVCache(ctypes.Structure):  # include/paged_kvcache.h:9-25
+    _fields_ = [("k_blocks", _p), ("v_blocks", _p), ("n_blocks", _i), ("n_layers", _i),
+                ("n_kv_heads", _i), ("head_dim", _i), ("free_blocks", ctypes.POINTER(_i)),
+                ("free_count", _i), ("block_tables", ctypes.POINTER(ctypes.POINTER(_i))),
+                ("max_seqs", _i), ("max_blocks_per_seq", _i)]
+
+
+def fn(name, argtypes, restype=None):
+    f = getattr(ql.lib(), COMPAT_MANGLED[name])
+    f.argtypes, f.restype = argtypes, restype
+    return f
+
+
+def sync():
+    import torch
+    torch.cuda.synchronize()
+
+
+_hip = None
+
+
+def d2h(dst_addr: int, src_addr: int, nbytes: int) -> None:
+    global _hip
+    if _hip is None:
+        _hip = ctypes.CDLL("libamdhip64.so")
+        _hip.hipMemcpy.argtypes = [_p, _p, ctypes.c_size_t, ctypes.c_int]
+        _hip.hipMemcpy.restype = ctypes.c_int
+    assert _hip.hipMemcpy(dst_addr, src_addr, nbytes, 2) == 0  # hipMemcpyDeviceToHost
+
+
+def test_reference_test_softmax_via_launch_softmax():
+    # tests/test_softmax.cu:35-110
+    launch_softmax = fn("launch_softmax", [_p, _p, _i, _i, _p])
+    rows = cols = 2048
+    x = orc.reftest_softmax_inputs(rows, cols, 7)
+    din, dout = dev(x), empty((rows * cols,), np.float32)
+    launch_softmax(ptr(din), ptr(dout), rows, cols, stream())
+    got = host(dout, shape=(rows, cols))
+    cpu = orc.softmax_reftest_cpu(x)
+    assert np.max(np.abs(got - cpu)) < 1e-5
+    assert np.max(np.abs(got.astype(np.float64).sum(axis=1) - 1)) < 1e-5
+
+
+def test_reference_test_rope_norm_via_launch_rope():
+    # tests/test_attention.cu:60-121: srand(99)-style U(-0.5,0.5) [128,32,128], theta 1e4;
+    # the reference checks the norm to 1e-4; this also checks every element (pos = row).
+    launch_rope = fn("launch_rope", [_p, _i, _i, _i, _f, _p])
+    T, H, d = 128, 32, 128
+    q = uniform(99, (T, H * d), -0.5, 0.5)
+    dq = dev(q)
+    launch_rope(ptr(dq), T, H, d, 1e4, stream())
+    got = host(dq, shape=(T, H * d))
+    n0 = np.linalg.norm(q.reshape(T, H, d).astype(np.float64), axis=2)
+    n1 = np.linalg.norm(got.reshape(T, H, d).astype(np.float64), axis=2)
+    assert np.max(np.abs(n0 - n1)) < 1e-4
+    check_abs(got, orc.rope(q, H, d, 1e4, 0), ATOL_ROPE_F32, "launch_rope")
+
+
+def test_reference_test_kvcache_readback():
+    # tests/test_kvcache.cu:27-70 through kvcache_create / kvcache_append / kvcache_get_k
+    create = fn("kvcache_create", [_i, _i, _i, _i], ctypes.POINTER(KVCache))
+    append = fn("kvcache_append", [ctypes.POINTER(KVCache), _i, _p, _p, _p])
+    get_k = fn("kvcache_get_k", [ctypes.POINTER(KVCache), _i], _p)
+    get_v = fn("kvcache_get_v", [ctypes.POINTER(KVCache), _i], _p)
+    free = fn("kvcache_free", [ctypes.POINTER(KVCache)])
+    L, S, H, d = 32, 256, 32, 128
+    slice_ = H * d
+    c = create(L, S, H, d)
+    assert c and c.contents.current_len == 0
+    try:
+        for tok in range(16):
+            hk = np.float32(tok) + np.arange(slice_, dtype=np.float32) / np.float32(slice_)
+            hv = np.full(slice_, -tok, np.float32)
+            dk, dv = dev(hk), dev(hv)
+            for layer in range(L):
+                append(c, layer, ptr(dk), ptr(dv), stream())
+            sync()
+            c.contents.current_len += 1
+        back = np.empty(slice_, np.float32)
+        k0 = get_k(c, 0)
+        d2h(back.ctypes.data, k0 + 7 * slice_ * 4, slice_ * 4)
+        assert abs(back[0] - 7.0) < 1e-6
+        np.testing.assert_array_equal(back, np.float32(7) + np.arange(slice_, dtype=np.float32) / np.float32(slice_))
+        v5 = get_v(c, 5)
+        d2h(back.ctypes.data, v5 + 9 * slice_ * 4, slice_ * 4)
+        assert np.all(back == -9.0)
+        d2h(back.ctypes.data, k0 + 16 * slice_ * 4, slice_ * 4)
+        assert np.all(back == 0.0)  # created zeroed, untouched beyond current_len
+    finally:
+        free(c)
+
+
+def test_fp16_shims_match_oracle():
+    s = stream()
+    rows, dim = 4, 4096
+    x = to_f16_bits(normal(1, (rows, dim)))
+    w = to_f16_bits(uniform(2, dim, 0.5, 1.5))
+    dx, dw, do = dev(x), dev(w), empty((rows * dim,), np.uint16)
+    fn("launch_fp16_rmsnorm", [_p, _p, _p, _i, _i, _f, _p])(ptr(dx), ptr(dw), ptr(do), rows, dim, 1e-5, s)
+    check_f16(host(do, shape=(rows, dim)), orc.rmsnorm(x, w, 1e-5, f16=True), "launch_fp16_rmsnorm")
+
+    q = to_f16_bits(normal(3, (1, 32 * 128)))
+    dq = dev(q)
+    fn("launch_fp16_rope", [_p, _i, _i, _i, _f, _p])(ptr(dq), 1, 32, 128, 1e4, s)
+    assert np.array_equal(host(dq, shape=(1, 32 * 128)), q)  # decode: seq_len=1 -> pos 0 -> identity
+    q = to_f16_bits(normal(4, (9, 8 * 64)))
+    dq = dev(q)
+    fn("launch_fp16_rope", [_p, _i, _i, _i, _f, _p])(ptr(dq), 9, 8, 64, 1e4, s)
+    check_f16(host(dq, shape=(9, 8 * 64)), orc.rope(q, 8, 64, 1e4, 0, f16=True), "launch_fp16_rope")
+
+    g, u = to_f16_bits(normal(5, 5632, clip=8)), to_f16_bits(normal(6, 5632, clip=8))
+    dg, du, do = dev(g), dev(u), empty((5632,), np.uint16)
+    fn("launch_fp16_swiglu", [_p, _p, _p, _i, _i, _p])(ptr(dg), ptr(du), ptr(do), 1, 5632, s)
+    check_f16(host(do), orc.swiglu(g, u, f16=True), "launch_fp16_swiglu")
+
+    table = to_f16_bits(normal(7, (100, 4096)))
+    dt, do = dev(table), empty((4096,), np.uint16)
+    fn("launch_fp16_embed", [_p, _p, _i, _i, _p])(ptr(dt), ptr(do), 42, 4096, s)
+    assert np.array_equal(host(do), table[42])
+
+    a, b = to_f16_bits(normal(8, 4096)), to_f16_bits(normal(9, 4096))
+    da, db = dev(a), dev(b)
+    fn("launch_fp16_add", [_p, _p, _i, _p])(ptr(da), ptr(db), 4096, s)
+    assert np.array_equal(host(da), orc.add(a, b, f16=True))
+
+    dl, do = dev(a), empty((4096,), np.float32)
+    fn("launch_fp16_to_fp32", [_p, _p, _i, _p])(ptr(dl), ptr(do), 4096, s)
+    assert np.array_equal(host(do), orc.f16_to_f32(a))
+
+    L, S, H, d, layer, pos = 4, 32, 8, 128, 3, 11
+    kc, vc = empty((L * S * H * d,), np.uint16, fill_bits=0), empty((L * S * H * d,), np.uint16, fill_bits=0)
+    kn, vn = to_f16_bits(normal(10, H * d)), to_f16_bits(normal(11, H * d))
+    dkn, dvn = dev(kn), dev(vn)
+    fn("launch_fp16_kvcache_append", [_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p])(
+        ptr(kc), ptr(vc), ptr(dkn), ptr(dvn), layer, pos, H, d, S, L, s)
+    wk, wv = np.zeros((L, S, H, d), np.uint16), np.zeros((L, S, H, d), np.uint16)
+    orc.kv_append_inplace(wk, wv, kn.reshape(1, H, d), vn.reshape(1, H, d), layer, pos, f16=True)
+    assert np.array_equal(host(kc, shape=(L, S, H, d)), wk)
+    assert np.array_equal(host(vc, shape=(L, S, H, d)), wv)
+
+
+def test_fp32_shims_match_oracle():
+    s = stream()
+    rows, dim = 3, 2048
+    x, w = normal(20, (rows, dim)), uniform(21, dim, 0.5, 1.5)
+    dx, dw, do = dev(x), dev(w), empty((rows * dim,), np.float32)
+    fn("launch_rmsnorm", [_p, _p, _p, _i, _i, _f, _p])(ptr(dx), ptr(dw), ptr(do), rows, dim, 1e-5, s)
+    check_close(host(do, shape=(rows, dim)), orc.rmsnorm(x, w, 1e-5), RTOL_F32, ATOL_F32, "launch_rmsnorm")
+
+    g, u = normal(22, (32, 5632), clip=8), normal(23, (32, 5632), clip=8)
+    dg, du, do = dev(g), dev(u), empty((32 * 5632,), np.float32)
+    fn("launch_swiglu", [_p, _p, _p, _i, _i, _p])(ptr(dg), ptr(du), ptr(do), 32, 5632, s)
+    check_close(host(do, shape=(32, 5632)), orc.swiglu(g, u), RTOL_F32, ATOL_F32, "launch_swiglu")
+
+    a, b = normal(24, 4096), normal(25, 4096)
+    da, db = dev(a), dev(b)
+    fn("add_residual", [_p, _p, _i, _p])(ptr(da), ptr(db), 4096, s)
+    assert np.array_equal(host(da), orc.add(a, b))
+
+    table = normal(26, (50, 2048))
+    dt, do = dev(table), empty((2048,), np.float32)
+    fn("launch_embed", [_p, _p, _i, _i, _p])(ptr(do), ptr(dt), 17, 2048, s)
+    assert np.array_equal(host(do), table[17])
+
+
+def test_paged_allocator_lifo_and_pool_layout():
+    # src/paged_kvcache.cu:16-98: fresh pool hands out 0,1,2,...; -1 when empty;
+    # block i of each pool at pool + i * (n_layers*16*H_kv*d) halves.
+    create = fn("paged_kv_create", [_i, _i, _i, _i, _i, _i], ctypes.POINTER(PagedKVCache))
+    alloc = fn("paged_kv_allocate_block", [ctypes.POINTER(PagedKVCache)], _i)
+    release = fn("paged_kv_free_block", [ctypes.POINTER(PagedKVCache), _i])
+    free = fn("paged_kv_free", [ctypes.POINTER(PagedKVCache)])
+    nb, L, H, d = 6, 4, 8, 128
+    c = create(nb, L, H, d, 3, 10)
+    assert c
+    try:
+        assert [alloc(c) for _ in range(nb)] == list(range(nb))
+        assert alloc(c) == -1
+        release(c, 4)
+        release(c, 1)
+        assert alloc(c) == 1 and alloc(c) == 4
+        assert all(c.contents.block_tables[s][j] == -1 for s in range(3) for j in range(10))
+        ptrs = (ctypes.c_uint64 * nb)()
+        d2h(ctypes.addressof(ptrs), c.contents.k_blocks, 8 * nb)
+        blk_bytes = L * 16 * H * d * 2
+        assert [ptrs[i] - ptrs[0] for i in range(nb)] == [i * blk_bytes for i in range(nb)]
+
+        # append through the ql_ paged kernel into this cache's pool
+        T, layer = 40, 2
+        table = (ctypes.c_int32 * 3)(5, 0, 3)
+        slots = (ctypes.c_int32 * T)()
+        assert ql.raw("ql_paged_slot_mapping", ctypes.addressof(table), 3, 0, T, ctypes.addressof(slots)) == 0
+        slots_np = np.frombuffer(slots, np.int32).copy()
+        kn = to_f16_bits(normal(30, (T, H, d)))
+        vn = to_f16_bits(normal(31, (T, H, d)))
+        dsl, dkn, dvn = dev(slots_np), dev(kn), dev(vn)
+        ql.call("ql_paged_kv_append_f16", c.contents.k_blocks, c.contents.v_blocks, nb, ptr(dsl),
+                ptr(dkn), ptr(dvn), T, layer, L, H, d, stream())
+        sync()
+        pool = np.empty(nb * L * 16 * H * d, np.uint16)
+        d2h(pool.ctypes.data, ptrs[0], pool.nbytes)
+        pool = pool.reshape(nb, L, 16, H, d)
+        for t in range(T):
+            b, o = slots_np[t] // 16, slots_np[t] % 16
+            assert np.array_equal(pool[b, layer, o], kn[t]), t
+    finally:
+        free(c)

@@ -1,0 +1,434 @@
+"""GPU parity: every C-ABI entry point against the CPU oracle on identical
+seeded inputs, at the BASELINE configs (C1..C5) and at the edge shapes that
+select each kernel variant (register-resident widths, multi-wavefront rows,
+block-per-row fallback, unaligned pointers, ragged tails).  Outputs sit inside
+guard bands that must survive untouched.
+
+Tolerances are those of tests/helpers.py: fp32 rtol 1e-5 (RoPE: abs 1e-6),
+binary16 rtol 2e-3 (+ one subnormal step), gather/KV append bit-exact."""
+import numpy as np
+import pytest
+
+import oracle as orc
+import quantlib_amd as ql
+from helpers import (ATOL_F32, ATOL_ROPE_F32, RTOL_F32, causal_mask_inplace, check_abs,
+                     check_close, check_f16, dev, empty, f16_bits_to_f32, host, normal, ptr,
+                     stream, to_f16_bits, uniform)
+
+pytestmark = pytest.mark.gpu
+
+GUARD = 64          # elements of guard band on each side of every output
+GUARD_BYTE = 0xA5
+
+
+class Out:
+    """Device output buffer of n elements between two guard bands."""
+
+    def __init__(self, n, dtype, offset=0):
+        import torch
+        self.n, self.dtype, self.offset = n, dtype, offset
+        self.buf = empty((n + 2 * GUARD + offset,), dtype, fill_bits=GUARD_BYTE)
+        self.view = self.buf[GUARD + offset:GUARD + offset + n]
+        self.torch = torch
+
+    @property
+    def ptr(self):
+        return self.view.data_ptr()
+
+    def get(self, shape=None):
+        a = host(self.buf)
+        g0, g1 = a[:GUARD + self.offset], a[GUARD + self.offset + self.n:]
+        for g in (g0, g1):
+            assert np.all(g.view(np.uint8) == GUARD_BYTE), "write outside the output region"
+        v = a[GUARD + self.offset:GUARD + self.offset + self.n]
+        return v.reshape(shape) if shape is not None else v
+
+
+def _f16(x):
+    return to_f16_bits(x)
+
+
+# ---- RMSNorm --------------------------------------------------------------------------------
+F32_DIMS = [(2048, 2048), (1, 4), (7, 256), (5, 260), (3, 1000), (4, 4096), (3, 5000), (2, 8192),
+            (2, 16384), (2, 20000), (2, 32768), (2, 40000), (3, 1001), (1, 3)]
+F16_DIMS = [(64, 4096), (1, 8), (7, 512), (5, 520), (3, 1000), (4, 8192), (3, 10000),
+            (2, 16384), (2, 32768), (2, 65536), (2, 70000), (3, 1001), (1, 5)]
+
+
+@pytest.mark.parametrize("rows,dim", F32_DIMS)
+def test_rmsnorm_f32(rows, dim):
+    x = normal(0x51A10001 + dim, (rows, dim))
+    w = uniform(0x51A10002 + dim, dim, 0.5, 1.5)
+    out = Out(rows * dim, np.float32)
+    dx, dw = dev(x), dev(w)
+    ql.call("ql_rmsnorm_f32", ptr(dx), ptr(dw), out.ptr, rows, dim, 1e-5, stream())
+    check_close(out.get((rows, dim)), orc.rmsnorm(x, w, 1e-5), RTOL_F32, ATOL_F32,
+                f"rmsnorm f32 {rows}x{dim}")
+
+
+@pytest.mark.parametrize("rows,dim", F16_DIMS)
+def test_rmsnorm_f16(rows, dim):
+    x = _f16(normal(0x51A10011 + dim, (rows, dim)))
+    w = _f16(uniform(0x51A10012 + dim, dim, 0.5, 1.5))
+    out = Out(rows * dim, np.uint16)
+    dx, dw = dev(x), dev(w)
+    ql.call("ql_rmsnorm_f16", ptr(dx), ptr(dw), out.ptr, rows, dim, 1e-5, stream())
+    check_f16(out.get((rows, dim)), orc.rmsnorm(x, w, 1e-5, f16=True), f"rmsnorm f16 {rows}x{dim}")
+
+
+@pytest.mark.parametrize("f16", [False, True])
+def test_rmsnorm_unaligned_pointers(f16):
+    rows, dim = 9, 2048
+    x = normal(31, (rows, dim))
+    w = uniform(32, dim, 0.5, 1.5)
+    if f16:
+        x, w = _f16(x), _f16(w)
+    dt = np.uint16 if f16 else np.float32
+    out = Out(rows * dim, dt, offset=1)
+    dx, dw = dev(x, offset_elems=1), dev(w, offset_elems=3)
+    ql.call("ql_rmsnorm_f16" if f16 else "ql_rmsnorm_f32", ptr(dx), ptr(dw), out.ptr, rows, dim,
+            1e-5, stream())
+    want = orc.rmsnorm(x, w, 1e-5, f16=f16)
+    if f16:
+        check_f16(out.get((rows, dim)), want, "rmsnorm f16 unaligned")
+    else:
+        check_close(out.get((rows, dim)), want, RTOL_F32, ATOL_F32, "rmsnorm f32 unaligned")
+
+
+@pytest.mark.parametrize("rows,dim", [(8192, 4096), (3, 4096), (5, 1000), (2, 20000), (3, 1001)])
+def test_add_rmsnorm_f16(rows, dim):
+    # C5: residual + RMSNorm at T=8192, hidden 4096 (and kernel-variant shapes)
+    x = _f16(normal(0x51A10051, (rows, dim)))
+    d = _f16(normal(0x51A10052, (rows, dim)))
+    w = _f16(uniform(0x51A10053, dim, 0.5, 1.5))
+    out = Out(rows * dim, np.uint16)
+    dx, dd, dw = dev(x), dev(d), dev(w)
+    ql.call("ql_add_rmsnorm_f16", ptr(dx), ptr(dd), ptr(dw), out.ptr, rows, dim, 1e-5, stream())
+    want_x, want = orc.add_rmsnorm(x, d, w, 1e-5, f16=True)
+    # the rounded residual sum is exact arithmetic: bit-exact
+    assert np.array_equal(host(dx, shape=(rows, dim)), want_x)
+    check_f16(out.get((rows, dim)), want, f"add_rmsnorm f16 {rows}x{dim}")
+
+
+@pytest.mark.parametrize("rows,dim", [(2048, 2048), (3, 4096), (2, 50000), (3, 999)])
+def test_add_rmsnorm_f32(rows, dim):
+    x, d = normal(41, (rows, dim)), normal(42, (rows, dim))
+    w = uniform(43, dim, 0.5, 1.5)
+    out = Out(rows * dim, np.float32)
+    dx, dd, dw = dev(x), dev(d), dev(w)
+    ql.call("ql_add_rmsnorm_f32", ptr(dx), ptr(dd), ptr(dw), out.ptr, rows, dim, 1e-5, stream())
+    want_x, want = orc.add_rmsnorm(x, d, w, 1e-5)
+    assert np.array_equal(host(dx, shape=(rows, dim)), want_x)
+    check_close(out.get((rows, dim)), want, RTOL_F32, ATOL_F32, f"add_rmsnorm f32 {rows}x{dim}")
+
+
+@pytest.mark.parametrize("f16,n", [(False, 1 << 20), (True, 1 << 20), (False, 1001), (True, 1003)])
+def test_residual_add(f16, n):
+    x, d = normal(44, n), normal(45, n)
+    if f16:
+        x, d = _f16(x), _f16(d)
+    dx, dd = dev(x), dev(d)
+    ql.call("ql_add_f16" if f16 else "ql_add_f32", ptr(dx), ptr(dd), n, stream())
+    assert np.array_equal(host(dx), orc.add(x, d, f16=f16))
+
+
+# ---- RoPE -------------------------------------------------------------------------------------
+def _rope_case(f16, T, H, HK, d, theta, pairing, seed, positions=None, pos_offset=0,
+               q_extra=0, k_extra=0):
+    qs, ks = H * d + q_extra, HK * d + k_extra
+    q = normal(seed, (T, qs))
+    k = normal(seed + 1, (T, ks))
+    if f16:
+        q, k = _f16(q), _f16(k)
+    dq, dk = dev(q), dev(k)
+    dpos = dev(np.asarray(positions, np.int32)) if positions is not None else None
+    name = "ql_rope_f16" if f16 else "ql_rope_f32"
+    ql.call(name, ptr(dq), ptr(dk), T, H, HK, d, qs, ks, ptr(dpos) if dpos is not None else None,
+            pos_offset, theta, pairing, stream())
+    wq = orc.rope(q, H, d, theta, pairing, positions, pos_offset, f16=f16)
+    wk = orc.rope(k, HK, d, theta, pairing, positions, pos_offset, f16=f16)
+    gq, gk = host(dq, shape=(T, qs)), host(dk, shape=(T, ks))
+    tag = f"rope {'f16' if f16 else 'f32'} T={T} H={H}/{HK} d={d} pairing={pairing}"
+    if f16:
+        check_f16(gq, wq, tag + " Q")
+        check_f16(gk, wk, tag + " K")
+    else:
+        check_abs(gq, wq, ATOL_ROPE_F32, tag + " Q")
+        check_abs(gk, wk, ATOL_ROPE_F32, tag + " K")
+    return gq, gk, q, k
+
+
+@pytest.mark.parametrize("pairing", [ql.ROPE_INTERLEAVED, ql.ROPE_HALF])
+def test_rope_f32_c2(pairing):
+    # C2: Q[2048,32,64], K[2048,4,64], positions 0..2047, theta 1e4; norm preserved
+    gq, _, q, _ = _rope_case(False, 2048, 32, 4, 64, 1e4, pairing, 0x51A10003)
+    n0 = np.linalg.norm(q.reshape(2048, 32, 64).astype(np.float64), axis=2)
+    n1 = np.linalg.norm(gq.reshape(2048, 32, 64).astype(np.float64), axis=2)
+    assert np.max(np.abs(n0 - n1)) < 1e-5
+
+
+@pytest.mark.parametrize("pairing", [ql.ROPE_HALF, ql.ROPE_INTERLEAVED])
+def test_rope_f16_c5(pairing):
+    # C5: Q 32x128, K 8x128, T=8192, theta 5e5
+    _rope_case(True, 8192, 32, 8, 128, 5e5, pairing, 0x51A10005)
+
+
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("d", [2, 8, 16, 32, 96, 128, 256, 2048])
+def test_rope_head_dims(f16, d):
+    for pairing in (ql.ROPE_INTERLEAVED, ql.ROPE_HALF):
+        _rope_case(f16, 37, 3, 1, d, 1e4, pairing, 100 + d)
+
+
+@pytest.mark.parametrize("f16", [False, True])
+def test_rope_positions_offset_and_fused_qkv_strides(f16):
+    pos = np.random.default_rng(7).integers(0, 100_000, size=50).astype(np.int32)
+    _rope_case(f16, 50, 8, 2, 64, 5e5, ql.ROPE_HALF, 200, positions=pos)
+    _rope_case(f16, 50, 8, 2, 64, 5e5, ql.ROPE_INTERLEAVED, 210, pos_offset=4000)
+    # Q rows padded to a fused [Q|K|V] stride: the padding must stay untouched
+    gq, gk, q, k = _rope_case(f16, 40, 4, 2, 64, 1e4, ql.ROPE_HALF, 220, q_extra=256, k_extra=8)
+    assert np.array_equal(gq[:, 4 * 64:], q[:, 4 * 64:])
+    assert np.array_equal(gk[:, 2 * 64:], k[:, 2 * 64:])
+
+
+def test_rope_q_only_and_k_only():
+    T, H, d = 64, 4, 64
+    q = normal(300, (T, H * d))
+    dq = dev(q)
+    ql.call("ql_rope_f32", ptr(dq), None, T, H, 7, d, H * d, 0, None, 0, 1e4, 0, stream())
+    check_abs(host(dq, shape=(T, H * d)), orc.rope(q, H, d, 1e4, 0), ATOL_ROPE_F32, "q only")
+    dk = dev(q)
+    ql.call("ql_rope_f32", None, ptr(dk), T, 9, H, d, 0, H * d, None, 0, 1e4, 1, stream())
+    check_abs(host(dk, shape=(T, H * d)), orc.rope(q, H, d, 1e4, 1), ATOL_ROPE_F32, "k only")
+
+
+# ---- SwiGLU -------------------------------------------------------------------------------------
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("rows,ffn", [(1, 5632), (32, 5632), (128, 5632), (512, 5632), (3, 1001),
+                                      (1, 7)])
+def test_swiglu_c3(f16, rows, ffn):
+    g = normal(0x51A10004 + rows, (rows, ffn), clip=8.0)
+    u = normal(0x51A10104 + rows, (rows, ffn), clip=8.0)
+    if f16:
+        g, u = _f16(g), _f16(u)
+    out = Out(rows * ffn, np.uint16 if f16 else np.float32)
+    dg, du = dev(g), dev(u)
+    ql.call("ql_swiglu_f16" if f16 else "ql_swiglu_f32", ptr(dg), ptr(du), out.ptr, rows, ffn,
+            stream())
+    want = orc.swiglu(g, u, f16=f16)
+    if f16:
+        check_f16(out.get((rows, ffn)), want, f"swiglu f16 {rows}x{ffn}")
+    else:
+        check_close(out.get((rows, ffn)), want, RTOL_F32, ATOL_F32, f"swiglu f32 {rows}x{ffn}")
+
+
+def test_swiglu_f16_c5():
+    rows, ffn = 8192, 14336
+    g = _f16(normal(0x51A10054, (rows, ffn), clip=8.0))
+    u = _f16(normal(0x51A10055, (rows, ffn), clip=8.0))
+    out = Out(rows * ffn, np.uint16)
+    dg, du = dev(g), dev(u)
+    ql.call("ql_swiglu_f16", ptr(dg), ptr(du), out.ptr, rows, ffn, stream())
+    check_f16(out.get((rows, ffn)), orc.swiglu(g, u, f16=True), "swiglu f16 C5")
+
+
+@pytest.mark.parametrize("f16", [False, True])
+def test_swiglu_unaligned_and_extremes(f16):
+    n = 4099
+    g = normal(60, n, sigma=30.0)
+    g[:6] = [0.0, 200.0, -200.0, np.inf, -np.inf, np.nan]
+    u = normal(61, n)
+    if f16:
+        g, u = _f16(g), _f16(u)
+    out = Out(n, np.uint16 if f16 else np.float32, offset=1)
+    dg, du = dev(g, offset_elems=1), dev(u, offset_elems=2)
+    ql.call("ql_swiglu_f16" if f16 else "ql_swiglu_f32", ptr(dg), ptr(du), out.ptr, 1, n, stream())
+    want = orc.swiglu(g, u, f16=f16)
+    got = out.get()
+    if f16:
+        check_f16(got, want, "swiglu f16 extremes")
+    else:
+        check_close(got, want, RTOL_F32, ATOL_F32, "swiglu f32 extremes")
+
+
+# ---- softmax -----------------------------------------------------------------------------------
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("sigma", [2.0, 4.0])
+def test_softmax_c4_causal(f16, sigma):
+    # C4: logits[4096x4096] ~ N(0, sigma^2) with -inf above the diagonal
+    n = 4096
+    x = causal_mask_inplace(normal(0x51A10006, (n, n), sigma=sigma))
+    if f16:
+        x = _f16(x)
+    out = Out(n * n, np.uint16 if f16 else np.float32)
+    dx = dev(x)
+    ql.call("ql_softmax_f16" if f16 else "ql_softmax_f32", ptr(dx), out.ptr, n, n, stream())
+    want = orc.softmax(x, f16=f16)
+    got = out.get((n, n))
+    if f16:
+        check_f16(got, want, f"softmax f16 C4 sigma={sigma}")
+        assert np.all(got[np.triu_indices(n, 1)] == 0)
+    else:
+        check_close(got, want, RTOL_F32, ATOL_F32, f"softmax f32 C4 sigma={sigma}")
+        assert np.all(got[np.triu_indices(n, 1)] == 0) and got[0, 0] == 1.0
+
+
+def test_softmax_reference_test_thresholds():
+    # tests/test_softmax.cu:38-47,88-106 on the GPU path: srand(7) U(-2,2) 2048x2048,
+    # max abs error vs its cpu_softmax < 1e-5 and |row sum - 1| < 1e-5.
+    x = orc.reftest_softmax_inputs(2048, 2048, 7)
+    out = Out(2048 * 2048, np.float32)
+    dx = dev(x)
+    ql.call("ql_softmax_f32", ptr(dx), out.ptr, 2048, 2048, stream())
+    got = out.get((2048, 2048))
+    assert np.max(np.abs(got - orc.softmax_reftest_cpu(x))) < 1e-5
+    assert np.max(np.abs(got.astype(np.float64).sum(axis=1) - 1.0)) < 1e-5
+
+
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("rows,cols", [(5, 1), (7, 8), (9, 256), (6, 1000), (3, 8192), (3, 20000),
+                                       (2, 65536), (2, 70000), (4, 4097), (1, 3)])
+def test_softmax_widths(f16, rows, cols):
+    x = normal(500 + cols, (rows, cols), sigma=2.0)
+    if cols > 3:
+        x[0, :3] = -np.inf
+    if f16:
+        x = _f16(x)
+    out = Out(rows * cols, np.uint16 if f16 else np.float32)
+    dx = dev(x)
+    ql.call("ql_softmax_f16" if f16 else "ql_softmax_f32", ptr(dx), out.ptr, rows, cols, stream())
+    want = orc.softmax(x, f16=f16)
+    if f16:
+        check_f16(out.get((rows, cols)), want, f"softmax f16 {rows}x{cols}")
+    else:
+        check_close(out.get((rows, cols)), want, RTOL_F32, ATOL_F32, f"softmax f32 {rows}x{cols}")
+
+
+@pytest.mark.parametrize("cols", [256, 1001])
+def test_softmax_fully_masked_row_is_nan_like_reference(cols):
+    x = normal(77, (3, cols))
+    x[1] = -np.inf
+    out = Out(3 * cols, np.float32)
+    dx = dev(x)
+    ql.call("ql_softmax_f32", ptr(dx), out.ptr, 3, cols, stream())
+    got = out.get((3, cols))
+    assert np.all(np.isnan(got[1])) and not np.any(np.isnan(got[[0, 2]]))
+
+
+# ---- embedding gather -------------------------------------------------------------------------
+def test_embed_f16_c5():
+    V, D, T = 32000, 4096, 8192
+    r = np.random.default_rng(0x51A10056)
+    table = r.integers(0, 1 << 16, size=(V, D), dtype=np.uint32).astype(np.uint16)  # any bits
+    ids = r.integers(0, V, size=T).astype(np.int32)
+    out = Out(T * D, np.uint16)
+    dt, di = dev(table), dev(ids)
+    ql.call("ql_embed_f16", ptr(dt), ptr(di), T, V, D, out.ptr, stream())
+    assert np.array_equal(out.get((T, D)), table[ids])
+
+
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("dim", [1, 7, 64, 1000, 4096])
+def test_embed_ragged_and_out_of_range(f16, dim):
+    V, T = 300, 77
+    r = np.random.default_rng(dim)
+    table = normal(dim, (V, dim))
+    if f16:
+        table = _f16(table)
+    ids = r.integers(0, V, size=T).astype(np.int32)
+    ids[[0, 5, 9]] = [-1, V, 2**30]
+    out = Out(T * dim, np.uint16 if f16 else np.float32)
+    dt, di = dev(table), dev(ids)
+    ql.call("ql_embed_f16" if f16 else "ql_embed_f32", ptr(dt), ptr(di), T, V, dim, out.ptr,
+            stream())
+    assert np.array_equal(out.get((T, dim)), orc.embed(table, ids, f16=f16))
+    # single-token form (id by value), as launch_fp16_embed / embed_kernel
+    one = Out(dim, np.uint16 if f16 else np.float32)
+    ql.call("ql_embed_token_f16" if f16 else "ql_embed_token_f32", ptr(dt), 123, dim, one.ptr,
+            stream())
+    assert np.array_equal(one.get(), table[123])
+
+
+# ---- KV append ---------------------------------------------------------------------------------
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("L,S,H,d,T,layer,pos", [(4, 64, 8, 128, 1, 2, 17), (3, 9000, 8, 128, 8192, 1, 100),
+                                                 (2, 50, 3, 5, 7, 1, 40), (2, 40, 1, 2, 3, 0, 0)])
+def test_kv_append_contiguous(f16, L, S, H, d, T, layer, pos):
+    dt = np.uint16 if f16 else np.float32
+    r = np.random.default_rng(S + T)
+    kn = r.integers(0, 60000, size=(T, H, d)).astype(dt)
+    vn = r.integers(0, 60000, size=(T, H, d)).astype(dt)
+    n = L * S * H * d
+    kc, vc = Out(n, dt), Out(n, dt)
+    dkn, dvn = dev(kn), dev(vn)
+    ql.call("ql_kv_append_f16" if f16 else "ql_kv_append_f32", kc.ptr, vc.ptr, ptr(dkn), ptr(dvn),
+            layer, pos, T, H, d, S, L, stream())
+    want_k = np.full(n * np.dtype(dt).itemsize, GUARD_BYTE, np.uint8).view(dt).reshape(L, S, H, d)
+    want_v = want_k.copy()
+    orc.kv_append_inplace(want_k, want_v, kn, vn, layer, pos, f16=f16)
+    assert np.array_equal(kc.get((L, S, H, d)), want_k)
+    assert np.array_equal(vc.get((L, S, H, d)), want_v)
+
+
+def test_paged_kv_append_f16_c5_and_permuted():
+    # C5: 8192 tokens -> 512 blocks of 16; block [L,16,8,128]; fresh-pool order 0,1,2,...
+    import torch
+    T, H, d, L, layer = 8192, 8, 128, 8, 5
+    nb = T // 16
+    blk = L * 16 * H * d
+    r = np.random.default_rng(0x51A10057)
+    kn = r.integers(0, 60000, size=(T, H, d)).astype(np.uint16)
+    vn = r.integers(0, 60000, size=(T, H, d)).astype(np.uint16)
+    dkn, dvn = dev(kn), dev(vn)
+    for order in (np.arange(nb), r.permutation(nb)):
+        kpool = empty((nb * blk,), np.uint16, fill_bits=GUARD_BYTE)
+        vpool = empty((nb * blk,), np.uint16, fill_bits=GUARD_BYTE)
+        kptrs = torch.tensor([kpool.data_ptr() + 2 * blk * b for b in range(nb)], dtype=torch.int64).cuda()
+        vptrs = torch.tensor([vpool.data_ptr() + 2 * blk * b for b in range(nb)], dtype=torch.int64).cuda()
+        slots = np.array([order[t // 16] * 16 + t % 16 for t in range(T)], np.int32)
+        slots[[3, 4000]] = -1                       # padding tokens are skipped
+        dsl = dev(slots)
+        ql.call("ql_paged_kv_append_f16", ptr(kptrs), ptr(vptrs), nb, ptr(dsl), ptr(dkn), ptr(dvn),
+                T, layer, L, H, d, stream())
+        wk = np.full(nb * blk, 0xA5A5, np.uint16)
+        wv = wk.copy()
+        offs = (np.arange(nb) * blk).astype(np.int64)
+        orc.paged_kv_append_inplace(wk, wv, offs, slots, kn, vn, layer, L, H, d)
+        assert np.array_equal(host(kpool), wk)
+        assert np.array_equal(host(vpool), wv)
+
+
+def test_paged_kv_append_unaligned_rows_and_bad_slots():
+    import torch
+    T, H, d, L, layer, nb = 40, 3, 6, 2, 1, 4        # kv = 18 elements: not 16-byte rows
+    blk = L * 16 * H * d
+    r = np.random.default_rng(9)
+    kn = r.integers(0, 60000, size=(T, H, d)).astype(np.uint16)
+    vn = r.integers(0, 60000, size=(T, H, d)).astype(np.uint16)
+    kpool = empty((nb * blk,), np.uint16, fill_bits=GUARD_BYTE)
+    vpool = empty((nb * blk,), np.uint16, fill_bits=GUARD_BYTE)
+    kptrs = torch.tensor([kpool.data_ptr() + 2 * blk * b for b in range(nb)], dtype=torch.int64).cuda()
+    vptrs = torch.tensor([vpool.data_ptr() + 2 * blk * b for b in range(nb)], dtype=torch.int64).cuda()
+    slots = (np.arange(T) + 5).astype(np.int32)
+    slots[7] = nb * 16 + 3                            # block beyond the pool: skipped
+    dsl, dkn, dvn = dev(slots), dev(kn), dev(vn)
+    ql.call("ql_paged_kv_append_f16", ptr(kptrs), ptr(vptrs), nb, ptr(dsl), ptr(dkn), ptr(dvn), T,
+            layer, L, H, d, stream())
+    wk = np.full(nb * blk, 0xA5A5, np.uint16)
+    wv = wk.copy()
+    orc.paged_kv_append_inplace(wk, wv, (np.arange(nb) * blk).astype(np.int64), slots, kn, vn,
+                                layer, L, H, d)
+    assert np.array_equal(host(kpool), wk) and np.array_equal(host(vpool), wv)
+
+
+# ---- fp16 -> fp32 ------------------------------------------------------------------------------
+@pytest.mark.parametrize("n", [65536, 32000, 13])
+def test_f16_to_f32_bit_exact(n):
+    h = (np.arange(n, dtype=np.uint32) % 65536).astype(np.uint16)
+    out = Out(n, np.float32)
+    dh = dev(h)
+    ql.call("ql_f16_to_f32", ptr(dh), out.ptr, n, stream())
+    got, want = out.get(), orc.f16_to_f32(h)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))

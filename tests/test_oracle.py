@@ -1,0 +1,334 @@
+"""CPU checks that pin the oracle (oracle/oracle.c) before it is trusted as the
+parity checker.  Each test uses a closed form, an invariant, an independent
+formulation or a library routine, chosen so that a plausible slip in the
+restatement (dropped term, wrong index or sign, swapped pairing) fails."""
+import math
+
+import numpy as np
+import pytest
+import scipy.special
+
+import oracle as orc
+from helpers import normal, uniform, to_f16_bits, f16_bits_to_f32
+
+
+# ---- binary16 codec ------------------------------------------------------------------
+def test_f16_to_f32_exhaustive():
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = orc.f16_to_f32(h)
+    want = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_f16_round_trip_exhaustive():
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    f = orc.f16_to_f32(h)
+    back = orc.f32_to_f16(f)
+    nan = np.isnan(f)
+    assert np.array_equal(back[~nan], h[~nan])
+    assert np.all((back[nan] & 0x7c00) == 0x7c00) and np.all((back[nan] & 0x3ff) != 0)
+
+
+def test_f32_to_f16_midpoints_and_random():
+    # every half-way point between consecutive finite halves (ties to even)
+    h = np.arange(0, 0x7bff, dtype=np.uint16)
+    lo = h.view(np.float16).astype(np.float64)
+    hi = (h + 1).view(np.float16).astype(np.float64)
+    mid = ((lo + hi) / 2).astype(np.float32)
+    assert np.array_equal(mid.astype(np.float64), (lo + hi) / 2)  # exactly representable
+    for x in (mid, -mid, np.nextafter(mid, np.float32(np.inf)), np.nextafter(mid, np.float32(0))):
+        assert np.array_equal(orc.f32_to_f16(x), x.astype(np.float16).view(np.uint16))
+    r = np.random.default_rng(1)
+    bits = r.integers(0, 2**32, size=2_000_000, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32)
+    x = x[~np.isnan(x)]
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(orc.f32_to_f16(x), want)
+
+
+def test_f32_to_f16_boundaries():
+    cases = {65504.0: 0x7BFF, 65519.996: 0x7BFF, 65520.0: 0x7C00, 1e9: 0x7C00,
+             2.0**-24: 0x0001, 2.0**-25: 0x0000, 2.0**-25 * 1.0000001: 0x0001,
+             2.0**-14: 0x0400, -0.0: 0x8000, float("inf"): 0x7C00, float("-inf"): 0xFC00}
+    for v, want in cases.items():
+        assert int(orc.f32_to_f16(np.array([v], np.float32))[0]) == want, v
+
+
+# ---- RMSNorm ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dim", [1, 7, 64, 2048])
+def test_rmsnorm_constant_row_closed_form(dim):
+    eps = 1e-5
+    w = uniform(3, dim, 0.5, 1.5)
+    for c in (0.25, -3.0, 1e-3):
+        x = np.full((1, dim), c, np.float32)
+        got = orc.rmsnorm(x, w, eps)[0]
+        want = w.astype(np.float64) * c / math.sqrt(c * c + eps)
+        np.testing.assert_allclose(got, want, rtol=1e-6)
+
+
+def test_rmsnorm_one_hot_closed_form():
+    dim, k, a, eps = 512, 37, 5.0, 1e-5
+    w = uniform(4, dim, 0.5, 1.5)
+    x = np.zeros((1, dim), np.float32)
+    x[0, k] = a
+    got = orc.rmsnorm(x, w, eps)[0]
+    assert np.count_nonzero(got) == 1
+    np.testing.assert_allclose(got[k], w[k] * a / math.sqrt(a * a / dim + eps), rtol=1e-6)
+
+
+def test_rmsnorm_scale_invariance_exact():
+    # eps = 0 and a power-of-two scale: every rounding step scales exactly.
+    x = normal(5, (8, 300))
+    w = uniform(6, 300, 0.5, 1.5)
+    assert np.array_equal(orc.rmsnorm(x, w, 0.0), orc.rmsnorm(x * 8, w, 0.0))
+
+
+def test_rmsnorm_zero_row_and_f64():
+    w = uniform(7, 64, 0.5, 1.5)
+    assert np.all(orc.rmsnorm(np.zeros((1, 64), np.float32), w, 1e-5) == 0)
+    x = normal(8, (16, 1000))
+    w = uniform(9, 1000, 0.5, 1.5)
+    x64 = x.astype(np.float64)
+    want = x64 / np.sqrt((x64 ** 2).mean(axis=1, keepdims=True) + 1e-5) * w
+    np.testing.assert_allclose(orc.rmsnorm(x, w, 1e-5), want, rtol=1e-6)
+
+
+def test_rmsnorm_f16_is_f32_arithmetic_on_widened_values():
+    x = to_f16_bits(normal(10, (32, 4096)))
+    w = to_f16_bits(uniform(11, 4096, 0.5, 1.5))
+    got = orc.rmsnorm(x, w, 1e-5, f16=True)
+    ref32 = orc.rmsnorm(f16_bits_to_f32(x), f16_bits_to_f32(w), 1e-5)
+    assert np.array_equal(got, orc.f32_to_f16(ref32))
+
+
+def test_add_f16_matches_numpy_half_addition():
+    vals = np.arange(0, 65536, 97, dtype=np.uint32).astype(np.uint16)
+    vals = vals[~np.isnan(vals.view(np.float16))]
+    a, b = np.meshgrid(vals, vals[::7])
+    a, b = a.ravel(), b.ravel()
+    with np.errstate(over="ignore", invalid="ignore"):
+        want = (a.view(np.float16).astype(np.float32) + b.view(np.float16).astype(np.float32)).astype(np.float16)
+    got = orc.add(a, b, f16=True)
+    nan = np.isnan(want)
+    assert np.array_equal(got[~nan], want.view(np.uint16)[~nan])
+
+
+@pytest.mark.parametrize("f16", [False, True])
+def test_add_rmsnorm_equals_unfused_chain(f16):
+    conv = to_f16_bits if f16 else (lambda a: a)
+    x, d = conv(normal(12, (64, 512))), conv(normal(13, (64, 512)))
+    w = conv(uniform(14, 512, 0.5, 1.5))
+    xs, out = orc.add_rmsnorm(x, d, w, 1e-5, f16=f16)
+    x2 = orc.add(x, d, f16=f16)
+    assert np.array_equal(xs, x2)
+    assert np.array_equal(out, orc.rmsnorm(x2, w, 1e-5, f16=f16))
+
+
+# ---- RoPE ------------------------------------------------------------------------------
+def _inv_freq_numpy(i, d, theta):
+    e = np.float32(np.float32(2 * i) / np.float32(d))
+    return np.float32(np.float32(1.0) / np.float32(np.float64(theta) ** np.float64(e)))
+
+
+def test_rope_inv_freq_closed_forms():
+    assert orc.rope_inv_freq(0, 128, 5e5) == 1.0
+    assert orc.rope_inv_freq(1, 4, 1e4) == np.float32(0.01)
+    for i in range(64):
+        assert orc.rope_inv_freq(i, 128, 1e4) == _inv_freq_numpy(i, 128, 1e4)
+    c, s = orc.rope_cos_sin(2047, 0, 64, 1e4)
+    assert (c, s) == (np.float32(math.cos(2047.0)), np.float32(math.sin(2047.0)))
+
+
+@pytest.mark.parametrize("pairing", [0, 1])
+def test_rope_position_zero_is_identity(pairing):
+    x = normal(20, (1, 4 * 64))
+    assert np.array_equal(orc.rope(x, 4, 64, 1e4, pairing), x)
+
+
+@pytest.mark.parametrize("pairing", [0, 1])
+def test_rope_matches_complex_rotation(pairing):
+    T, H, d, theta = 300, 3, 64, 1e4
+    x = normal(21, (T, H * d))
+    got = orc.rope(x, H, d, theta, pairing).reshape(T, H, d).astype(np.float64)
+    xr = x.reshape(T, H, d).astype(np.float64)
+    np_ = d // 2
+    i0 = np.arange(np_) * 2 if pairing == 0 else np.arange(np_)
+    i1 = i0 + 1 if pairing == 0 else i0 + np_
+    inv = np.array([_inv_freq_numpy(i, d, theta) for i in range(np_)], np.float32)
+    ang = (np.arange(T, dtype=np.float32)[:, None] * inv[None, :]).astype(np.float64)
+    z = (xr[:, :, i0] + 1j * xr[:, :, i1]) * np.exp(1j * ang)[:, None, :]
+    np.testing.assert_allclose(got[:, :, i0], z.real, atol=1e-6)
+    np.testing.assert_allclose(got[:, :, i1], z.imag, atol=1e-6)
+
+
+def test_rope_norm_preservation_reference_invariant():
+    # tests/test_attention.cu:96-121: per (token, head) vector norm kept to 1e-4
+    T, H, d = 128, 32, 128
+    x = uniform(22, (T, H * d), -0.5, 0.5)
+    y = orc.rope(x, H, d, 1e4, 0)
+    n0 = np.linalg.norm(x.reshape(T, H, d).astype(np.float64), axis=2)
+    n1 = np.linalg.norm(y.reshape(T, H, d).astype(np.float64), axis=2)
+    assert np.max(np.abs(n0 - n1)) < 1e-5
+
+
+def test_rope_pairings_related_by_permutation():
+    T, H, d = 50, 2, 32
+    x = normal(23, (T, H * d)).reshape(T, H, d)
+    perm = np.concatenate([np.arange(0, d, 2), np.arange(1, d, 2)])  # interleaved -> halves
+    inter = orc.rope(x.reshape(T, -1), H, d, 1e4, 0).reshape(T, H, d)
+    half = orc.rope(np.ascontiguousarray(x[:, :, perm]).reshape(T, -1), H, d, 1e4, 1).reshape(T, H, d)
+    assert np.array_equal(inter[:, :, perm], half)
+
+
+def test_rope_positions_and_stride():
+    T, H, d, stride = 40, 2, 16, 2 * 16 + 8
+    x = normal(24, (T, stride))
+    pos = (np.arange(T) + 100).astype(np.int32)
+    a = orc.rope(x, H, d, 1e4, 1, positions=pos)
+    b = orc.rope(x, H, d, 1e4, 1, pos_offset=100)
+    assert np.array_equal(a, b)
+    assert np.array_equal(a[:, H * d:], x[:, H * d:])  # gap after the heads untouched
+
+
+def test_rope_f16_is_f32_arithmetic_on_widened_values():
+    x = to_f16_bits(normal(25, (64, 4 * 128)))
+    got = orc.rope(x, 4, 128, 5e5, 1, f16=True)
+    ref = orc.rope(f16_bits_to_f32(x), 4, 128, 5e5, 1)
+    assert np.array_equal(got, orc.f32_to_f16(ref))
+
+
+# ---- SwiGLU ----------------------------------------------------------------------------
+def test_swiglu_closed_forms():
+    g = np.array([0.0, 80.0, -80.0, 1.0], np.float32)
+    u = np.array([5.0, 2.0, 2.0, 0.0], np.float32)
+    out = orc.swiglu(g, u)
+    assert out[0] == 0.0 and out[1] == 160.0 and abs(out[2]) < 1e-30 and out[3] == 0.0
+
+
+def test_swiglu_odd_identity_and_scipy():
+    g = normal(30, 100_000, clip=8.0)
+    one = np.ones_like(g)
+    s_pos, s_neg = orc.swiglu(g, one), orc.swiglu(-g, one)
+    np.testing.assert_allclose(s_pos.astype(np.float64) - s_neg, g, rtol=1e-6, atol=1e-6)
+    u = normal(31, 100_000, clip=8.0)
+    want = scipy.special.expit(g.astype(np.float64)) * g * u
+    np.testing.assert_allclose(orc.swiglu(g, u), want, rtol=1e-6, atol=1e-30)
+
+
+def test_swiglu_f16_is_f32_arithmetic_on_widened_values():
+    g, u = to_f16_bits(normal(32, 50_000, clip=8)), to_f16_bits(normal(33, 50_000, clip=8))
+    got = orc.swiglu(g, u, f16=True)
+    assert np.array_equal(got, orc.f32_to_f16(orc.swiglu(f16_bits_to_f32(g), f16_bits_to_f32(u))))
+
+
+# ---- softmax ---------------------------------------------------------------------------
+def test_softmax_passes_reference_test():
+    # tests/test_softmax.cu:38-47,88-106: srand(7) U(-2,2) 2048x2048; max abs error
+    # against its cpu_softmax < 1e-5 and every row sum within 1e-5 of 1.
+    x = orc.reftest_softmax_inputs(2048, 2048, seed=7)
+    libc = __import__("ctypes").CDLL(None)
+    libc.srand(7)
+    first = [libc.rand() / 2147483647 * 4.0 - 2.0 for _ in range(3)]
+    np.testing.assert_allclose(x.ravel()[:3], np.float32(first), rtol=1e-6)  # fp32 vs double arithmetic
+    got = orc.softmax(x)
+    ref = orc.softmax_reftest_cpu(x)
+    assert np.max(np.abs(got - ref)) < 1e-5
+    assert np.max(np.abs(got.astype(np.float64).sum(axis=1) - 1.0)) < 1e-5
+
+
+def test_softmax_matches_scipy_and_shift():
+    x = normal(40, (64, 1000), sigma=2.0)
+    got = orc.softmax(x)
+    np.testing.assert_allclose(got, scipy.special.softmax(x.astype(np.float64), axis=1), rtol=2e-6, atol=1e-37)
+    np.testing.assert_allclose(orc.softmax(x + np.float32(3.0)), got, rtol=1e-5, atol=1e-37)
+
+
+def test_softmax_special_rows():
+    n = 256
+    x = np.zeros((3, n), np.float32)
+    x[1] = -np.inf
+    x[1, 0] = 0.7                       # causal row 0: only column 0 visible
+    x[2] = -np.inf                      # fully masked row: NaN, as the reference
+    out = orc.softmax(x)
+    assert np.all(out[0] == np.float32(1.0 / n))
+    assert out[1, 0] == 1.0 and np.all(out[1, 1:] == 0.0)
+    assert np.all(np.isnan(out[2]))
+
+
+def test_softmax_f16_is_f32_arithmetic_on_widened_values():
+    x = to_f16_bits(normal(41, (16, 4096), sigma=2.0))
+    got = orc.softmax(x, f16=True)
+    assert np.array_equal(got, orc.f32_to_f16(orc.softmax(f16_bits_to_f32(x))))
+
+
+# ---- gather / KV append ----------------------------------------------------------------
+@pytest.mark.parametrize("f16", [False, True])
+def test_embed_matches_numpy_indexing(f16):
+    V, D = 1000, 96
+    table = normal(50, (V, D))
+    if f16:
+        table = to_f16_bits(table)
+    ids = np.random.default_rng(51).integers(0, V, size=300).astype(np.int32)
+    ids[[3, 10]] = [-1, V]
+    got = orc.embed(table, ids, f16=f16)
+    want = table[np.clip(ids, 0, V - 1)].copy()
+    want[[3, 10]] = 0
+    assert np.array_equal(got, want)
+
+
+def test_kv_append_reference_readback_known_answer():
+    # tests/test_kvcache.cu:33-70: 32 layers, max_seq 256, 32 heads, hd 128;
+    # 16 tokens appended to every layer; layer 0 token 7 reads back k[0] = 7.0.
+    L, S, H, d = 32, 256, 32, 128
+    slice_ = H * d
+    kc = np.zeros((L, S, H, d), np.float32)
+    vc = np.zeros_like(kc)
+    for tok in range(16):
+        hk = (np.float32(tok) + np.arange(slice_, dtype=np.float32) / np.float32(slice_)).reshape(1, H, d)
+        hv = np.full((1, H, d), -tok, np.float32)
+        for layer in range(L):
+            orc.kv_append_inplace(kc, vc, hk, hv, layer, tok)
+    assert kc.reshape(L, S, -1)[0, 7, 0] == 7.0
+    assert np.all(vc[5, 9] == -9.0) and np.all(kc[:, 16:] == 0)
+
+
+@pytest.mark.parametrize("f16", [False, True])
+def test_kv_append_matches_numpy_views(f16):
+    L, S, H, d, T, layer, pos = 3, 50, 2, 24, 9, 1, 17
+    dt = np.uint16 if f16 else np.float32
+    kc = np.random.default_rng(52).integers(0, 60000, size=(L, S, H, d)).astype(dt)
+    vc = kc.copy()[::-1].copy()
+    kn = np.random.default_rng(53).integers(0, 60000, size=(T, H, d)).astype(dt)
+    vn = kn[::-1].copy()
+    ek, ev = kc.copy(), vc.copy()
+    ek[layer, pos:pos + T] = kn
+    ev[layer, pos:pos + T] = vn
+    orc.kv_append_inplace(kc, vc, kn, vn, layer, pos, f16=f16)
+    assert np.array_equal(kc, ek) and np.array_equal(vc, ev)
+
+
+@pytest.mark.parametrize("permuted", [False, True])
+def test_paged_append_matches_numpy_views(permuted):
+    B, L, H, d, T, layer = 12, 3, 2, 16, 70, 2
+    blk = L * 16 * H * d
+    r = np.random.default_rng(54)
+    order = r.permutation(B) if permuted else np.arange(B)   # physical block of logical j
+    offsets = (np.arange(B) * blk).astype(np.int64)
+    slots = np.array([order[t // 16] * 16 + t % 16 for t in range(T)], np.int32)
+    slots[5] = -1
+    kn = r.integers(0, 60000, size=(T, H, d)).astype(np.uint16)
+    vn = r.integers(0, 60000, size=(T, H, d)).astype(np.uint16)
+    kp = np.full(B * blk, 0xA5A5, np.uint16)
+    vp = kp.copy()
+    orc.paged_kv_append_inplace(kp, vp, offsets, slots, kn, vn, layer, L, H, d)
+    ek = np.full((B, L, 16, H, d), 0xA5A5, np.uint16)
+    ev = ek.copy()
+    for t in range(T):
+        if slots[t] < 0:
+            continue
+        ek[slots[t] // 16, layer, slots[t] % 16] = kn[t]
+        ev[slots[t] // 16, layer, slots[t] % 16] = vn[t]
+    assert np.array_equal(kp.reshape(ek.shape), ek) and np.array_equal(vp.reshape(ev.shape), ev)
