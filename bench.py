@@ -12,21 +12,26 @@ and attention excluded:
   4. residual add + FFN RMSNorm         as 1
   5. SwiGLU                             gate, up [8192,14336] -> out
 
-One step = one pass of that chain.  Inputs are synthetic (torch.randn on the
-device), resident in HBM before timing.  Three buffer sets (~1 GB each) are
-rotated step to step so no input is still in the 256 MB MALL; the KV append
-rotates over the 32 pool layers.  value = algorithmic bytes of the chain
-(each input read once, each output written once) / wall time per step.
+One step = one pass of that chain.  Inputs are synthetic (seeded normal values
+made on the host and uploaded once) and resident in HBM before timing.  Three
+device buffer sets (~1 GB each) are rotated step to step so no input is still
+in the 256 MB MALL; the KV append rotates over the 32 pool layers.
+value = algorithmic bytes of the chain (each input read once, each output
+written once) / wall time per step.
 
 The embedding gather (once per forward, not per layer) is timed separately and
 reported under "kernels".  The roofline entry is for the dominant kernel,
-SwiGLU fp16 [8192 x 14336]: 3 x 8192 x 14336 x 2 B = 704,643,072 B per launch.
+SwiGLU fp16 [8192 x 14336]: 3 x 8192 x 14336 x 2 B = 704,643,072 B per launch,
+timed with HIP events around each of its launches on the work stream.
+
+Device memory, the stream and events come from libamdhip64 through the
+library's own binding (quant-lib_amd/quantlib_amd.py); no framework runtime is
+loaded.
 """
 from __future__ import annotations
 
 import argparse
 import json
-import os
 import pathlib
 import sys
 import time
@@ -51,7 +56,8 @@ CHAIN_BYTES = sum(BYTES[k] for k in CHAIN)
 
 
 def parse():
-    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap = argparse.ArgumentParser(description=__doc__,
+                                 formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
@@ -65,71 +71,67 @@ def parse():
 class Chain:
     """Device buffers of the C5 layer chain and the launches of one step."""
 
-    def __init__(self, ql, torch):
-        self.ql, self.torch = ql, torch
-        dev = torch.device("cuda:0")
-        g = torch.Generator(device=dev)
-        g.manual_seed(0x51A10005)
-        h = torch.float16
+    def __init__(self, ql, np):
+        self.ql = ql
+        r = np.random.default_rng(0x51A10005)
 
         def randn(*shape, clip=None):
-            t = torch.randn(*shape, generator=g, device=dev, dtype=torch.float32)
+            a = r.standard_normal(size=shape, dtype=np.float32)
             if clip is not None:
-                t.clamp_(-clip, clip)
-            return t.to(h)
+                np.clip(a, -clip, clip, out=a)
+            return a.astype(np.float16).view(np.uint16)
 
+        up = ql.DeviceArray.from_numpy
+        # one host copy of every input, uploaded into NSETS distinct device sets
+        host = {"x": randn(T, D), "d1": randn(T, D), "d2": randn(T, D),
+                "q": randn(T, HQ * HD), "k": randn(T, HKV * HD), "v": randn(T, HKV * HD),
+                "gate": randn(T, F, clip=8.0), "up": randn(T, F, clip=8.0)}
         self.sets = []
         for _ in range(NSETS):
-            s = {
-                "x": randn(T, D), "d1": randn(T, D), "d2": randn(T, D),
-                "y": torch.empty(T, D, dtype=h, device=dev),
-                "q": randn(T, HQ * HD), "k": randn(T, HKV * HD), "v": randn(T, HKV * HD),
-                "gate": randn(T, F, clip=8.0), "up": randn(T, F, clip=8.0),
-                "out": torch.empty(T, F, dtype=h, device=dev),
-            }
+            s = {k: up(v) for k, v in host.items()}
+            s["y"] = ql.DeviceArray((T, D), np.uint16)
+            s["out"] = ql.DeviceArray((T, F), np.uint16)
             self.sets.append(s)
-        self.w_attn = (torch.rand(D, generator=g, device=dev) + 0.5).to(h)
-        self.w_ffn = (torch.rand(D, generator=g, device=dev) + 0.5).to(h)
+        del host
+        self.w_attn = up(r.uniform(0.5, 1.5, D).astype(np.float16).view(np.uint16))
+        self.w_ffn = up(r.uniform(0.5, 1.5, D).astype(np.float16).view(np.uint16))
         # paged pool: 512 blocks of [32 layers, 16, 8, 128] fp16 (1 MiB each) per K and V
         self.nb = T // PAGE
         blk = L_POOL * PAGE * HKV * HD
-        self.kpool = torch.empty(self.nb * blk, dtype=h, device=dev)
-        self.vpool = torch.empty(self.nb * blk, dtype=h, device=dev)
-        self.kptrs = torch.tensor([self.kpool.data_ptr() + 2 * blk * b for b in range(self.nb)],
-                                  dtype=torch.int64, device=dev)
-        self.vptrs = torch.tensor([self.vpool.data_ptr() + 2 * blk * b for b in range(self.nb)],
-                                  dtype=torch.int64, device=dev)
+        self.kpool = ql.DeviceArray((self.nb * blk,), np.uint16)
+        self.vpool = ql.DeviceArray((self.nb * blk,), np.uint16)
+        self.kptrs = up(np.array([self.kpool.ptr + 2 * blk * b for b in range(self.nb)], np.int64))
+        self.vptrs = up(np.array([self.vpool.ptr + 2 * blk * b for b in range(self.nb)], np.int64))
         # fresh-pool block order 0,1,2,... (LIFO allocator of src/paged_kvcache.cu:49-53)
-        self.slots = torch.arange(T, dtype=torch.int32, device=dev)
+        self.slots = up(np.arange(T, dtype=np.int32))
         # embedding table and ids (gather timed separately)
-        self.table = randn(VOCAB, D)
-        self.ids = torch.randint(0, VOCAB, (T,), generator=g, device=dev, dtype=torch.int32)
-        self.emb_out = [torch.empty(T, D, dtype=h, device=dev) for _ in range(NSETS)]
-        self.stream = torch.cuda.current_stream().cuda_stream
+        self.table = up(randn(VOCAB, D))
+        self.ids = up(r.integers(0, VOCAB, size=T).astype(np.int32))
+        self.emb_out = [ql.DeviceArray((T, D), np.uint16) for _ in range(NSETS)]
+        self.stream = ql.stream()
         self.step_no = 0
+        ql.synchronize()
 
-    # one launch per kernel of the chain ------------------------------------------------
+    # one launch per kernel of the chain --------------------------------------------------
     def k_add_rmsnorm(self, s, which):
-        self.ql.call("ql_add_rmsnorm_f16", s["x"].data_ptr(), s[which].data_ptr(),
-                     (self.w_attn if which == "d1" else self.w_ffn).data_ptr(), s["y"].data_ptr(),
-                     T, D, EPS, self.stream)
+        w = self.w_attn if which == "d1" else self.w_ffn
+        self.ql.call("ql_add_rmsnorm_f16", s["x"].ptr, s[which].ptr, w.ptr, s["y"].ptr, T, D, EPS,
+                     self.stream)
 
     def k_rope(self, s):
-        self.ql.call("ql_rope_f16", s["q"].data_ptr(), s["k"].data_ptr(), T, HQ, HKV, HD, HQ * HD,
-                     HKV * HD, None, 0, THETA, self.ql.ROPE_HALF, self.stream)
+        self.ql.call("ql_rope_f16", s["q"].ptr, s["k"].ptr, T, HQ, HKV, HD, HQ * HD, HKV * HD, None,
+                     0, THETA, self.ql.ROPE_HALF, self.stream)
 
     def k_paged(self, s, layer):
-        self.ql.call("ql_paged_kv_append_f16", self.kptrs.data_ptr(), self.vptrs.data_ptr(), self.nb,
-                     self.slots.data_ptr(), s["k"].data_ptr(), s["v"].data_ptr(), T, layer, L_POOL,
-                     HKV, HD, self.stream)
+        self.ql.call("ql_paged_kv_append_f16", self.kptrs.ptr, self.vptrs.ptr, self.nb,
+                     self.slots.ptr, s["k"].ptr, s["v"].ptr, T, layer, L_POOL, HKV, HD, self.stream)
 
     def k_swiglu(self, s):
-        self.ql.call("ql_swiglu_f16", s["gate"].data_ptr(), s["up"].data_ptr(), s["out"].data_ptr(),
-                     T, F, self.stream)
+        self.ql.call("ql_swiglu_f16", s["gate"].ptr, s["up"].ptr, s["out"].ptr, T, F, self.stream)
 
     def k_embed(self, i):
-        self.ql.call("ql_embed_f16", self.table.data_ptr(), self.ids.data_ptr(), T, VOCAB, D,
-                     self.emb_out[i % NSETS].data_ptr(), self.stream)
+        self.ql.call("ql_embed_f16", self.table.ptr, self.ids.ptr, T, VOCAB, D,
+                     self.emb_out[i % NSETS].ptr, self.stream)
 
     def step(self, ev_swiglu=None):
         i = self.step_no
@@ -140,10 +142,10 @@ class Chain:
         self.k_paged(s, i % L_POOL)
         self.k_add_rmsnorm(s, "d2")
         if ev_swiglu is not None:
-            ev_swiglu[0].record()
+            ev_swiglu[0].record(self.stream)
         self.k_swiglu(s)
         if ev_swiglu is not None:
-            ev_swiglu[1].record()
+            ev_swiglu[1].record(self.stream)
 
     def kernel_launcher(self, name):
         return {
@@ -155,33 +157,32 @@ class Chain:
         }[name]
 
 
-def breakdown(chain, torch, reps):
+def breakdown(chain, ql, reps):
     """Average duration of each kernel, HIP events around every launch."""
     out = {}
     for name in ["add_rmsnorm_f16", "rope_f16", "paged_kv_append_f16", "swiglu_f16", "embed_f16"]:
         launch = chain.kernel_launcher(name)
         for i in range(3):
             launch(i)
-        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-               for _ in range(reps)]
-        torch.cuda.synchronize()
+        evs = [(ql.Event(), ql.Event()) for _ in range(reps)]
+        ql.synchronize()
         for i, (a, b) in enumerate(evs):
-            a.record()
+            a.record(chain.stream)
             launch(i)
-            b.record()
-        torch.cuda.synchronize()
-        us = sorted(a.elapsed_time(b) * 1e3 for a, b in evs)
+            b.record(chain.stream)
+        ql.synchronize()
+        us = sorted(a.elapsed_ms(b) * 1e3 for a, b in evs)
         mean = sum(us) / len(us)
+        gbs = BYTES[name] / (mean * 1e-6) / 1e9
         out[name] = {"us_mean": round(mean, 2), "us_median": round(us[len(us) // 2], 2),
-                     "bytes": BYTES[name], "GBps": round(BYTES[name] / (mean * 1e-6) / 1e9, 1),
-                     "frac_peak": round(BYTES[name] / (mean * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
+                     "bytes": BYTES[name], "GBps": round(gbs, 1),
+                     "frac_peak": round(gbs / PEAK_HBM_GBS, 4)}
     return out
 
 
 def cpu_baseline(seconds):
     """The oracle (scalar C, 1 thread) on a bounded sample of the same chain:
     the C5 shapes restricted to 512 tokens, repeated until `seconds` elapse."""
-    import ctypes
     import numpy as np
     sys.path.insert(0, str(ROOT))
     import oracle as orc
@@ -197,7 +198,7 @@ def cpu_baseline(seconds):
         return a.astype(np.float16).view(np.uint16)
 
     x, d1, d2, y = h(n, D), h(n, D), h(n, D), np.empty((n, D), np.uint16)
-    w = (r.uniform(0.5, 1.5, D)).astype(np.float16).view(np.uint16)
+    w = r.uniform(0.5, 1.5, D).astype(np.float16).view(np.uint16)
     q, k, v = h(n, HQ * HD), h(n, HKV * HD), h(n, HKV * HD)
     gate, up, out = h(n, F, clip=8), h(n, F, clip=8), np.empty((n, F), np.uint16)
     nb = n // PAGE
@@ -205,7 +206,10 @@ def cpu_baseline(seconds):
     kpool, vpool = np.empty(nb * blk, np.uint16), np.empty(nb * blk, np.uint16)
     offs = (np.arange(nb) * blk).astype(np.int64)
     slots = np.arange(n, dtype=np.int32)
-    P = lambda a: a.ctypes.data  # noqa: E731
+
+    def P(a):
+        return a.ctypes.data
+
     sample_bytes = CHAIN_BYTES * n // T
 
     def one(layer):
@@ -229,8 +233,8 @@ def cpu_baseline(seconds):
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"oracle/oracle.c scalar C (gcc -O2, 1 thread) running the same 5-op chain on "
                       f"{n} of the {T} tokens (C5 shapes), {reps} passes in {el:.1f} s; "
-                      f"{CHAIN_BYTES * n / T / 1e6:.1f} MB of algorithmic traffic per pass; "
-                      f"us_per_layer_at_T8192={el / reps * T / n * 1e6:.0f}"}
+                      f"{sample_bytes / 1e6:.1f} MB of algorithmic traffic per pass; "
+                      f"= {el / reps * T / n * 1e6:.0f} us per decoder layer at T=8192"}
 
 
 def main():
@@ -240,36 +244,35 @@ def main():
               "every kernel is independent per token/row, see DESIGN.md for how it shards",
               file=sys.stderr)
         sys.exit(2)
-    import torch
+    import numpy as np
     import quantlib_amd as ql
 
-    if not torch.cuda.is_available():
+    ql.lib()  # raises if the HIP library is not built
+    if ql.device_count() < 1:
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
-    ql.lib()  # raises if the HIP library is not built
-    chain = Chain(ql, torch)
+    chain = Chain(ql, np)
 
     for _ in range(args.warmup):
         chain.step()
-    torch.cuda.synchronize()
+    ql.synchronize()
 
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(args.steps)]
-    t_all0, t_all1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
+    evs = [(ql.Event(), ql.Event()) for _ in range(args.steps)]
+    t_all0, t_all1 = ql.Event(), ql.Event()
+    ql.synchronize()
     t0 = time.perf_counter()
-    t_all0.record()
+    t_all0.record(chain.stream)
     for i in range(args.steps):
         chain.step(evs[i])
-    t_all1.record()
-    torch.cuda.synchronize()
+    t_all1.record(chain.stream)
+    ql.synchronize()
     wall = time.perf_counter() - t0
 
     ms_per_step = wall / args.steps * 1e3
-    ev_ms_per_step = t_all0.elapsed_time(t_all1) / args.steps
-    sw_us = sum(a.elapsed_time(b) for a, b in evs) / len(evs) * 1e3
+    ev_ms_per_step = t_all0.elapsed_ms(t_all1) / args.steps
+    sw_us = sum(a.elapsed_ms(b) for a, b in evs) / len(evs) * 1e3
     sw_gbs = BYTES["swiglu_f16"] / (sw_us * 1e-6) / 1e9
-    kernels = breakdown(chain, torch, args.breakdown_reps)
+    kernels = breakdown(chain, ql, args.breakdown_reps)
 
     traffic = None
     tf = pathlib.Path(args.traffic_file)
@@ -281,9 +284,10 @@ def main():
 
     cpu = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
 
+    chain_gbs = CHAIN_BYTES / (ms_per_step * 1e-3) / 1e9
     line = {
         "metric": "achieved HBM GB/s (% of MI355X peak) per fused kernel; us per decoder layer",
-        "value": round(CHAIN_BYTES / (ms_per_step * 1e-3) / 1e9, 1),
+        "value": round(chain_gbs, 1),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -291,12 +295,12 @@ def main():
         "ms_per_step": round(ms_per_step, 4),
         "us_per_decoder_layer": round(ms_per_step * 1e3, 1),
         "us_per_decoder_layer_events": round(ev_ms_per_step * 1e3, 1),
-        "frac_peak": round(CHAIN_BYTES / (ms_per_step * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+        "frac_peak": round(chain_gbs / PEAK_HBM_GBS, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16",
-        "data": "synthetic (torch.randn on device; gate/up clipped to [-8,8]; w ~ U(0.5,1.5))",
+        "data": "synthetic (seeded N(0,1) fp16; gate/up clipped to [-8,8]; w ~ U(0.5,1.5))",
         "config": {"workload": "C5 llama3-8b-shaped fp16 decoder-layer chain: add+rmsnorm, rope q+k, "
                                "paged kv append, add+rmsnorm, swiglu",
                    "tokens": T, "hidden": D, "heads": HQ, "kv_heads": HKV, "head_dim": HD,

@@ -115,3 +115,155 @@ def declared_symbols(header: pathlib.Path = HEADER) -> list[str]:
 
 def version() -> int:
     return lib().ql_version()
+
+
+# ---- HIP runtime plumbing -------------------------------------------------------------
+# Device memory, a stream and events come from the same libamdhip64 the library
+# links against (/opt/rocm).  A second HIP runtime in the process (e.g. the one
+# bundled with a framework wheel, loaded under another file name) must not be
+# mixed in: two runtimes on one device do not share allocations or streams.
+_hiprt = None
+_stream = None
+
+H2D, D2H, D2D = 1, 2, 3
+
+
+def hip() -> ctypes.CDLL:
+    """libamdhip64 as loaded by libquantlib_amd.so (same runtime instance)."""
+    global _hiprt
+    if _hiprt is None:
+        lib()
+        h = ctypes.CDLL("libamdhip64.so.7")
+        sig = {
+            "hipMalloc": [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t],
+            "hipFree": [_p],
+            "hipMemcpy": [_p, _p, ctypes.c_size_t, ctypes.c_int],
+            "hipMemset": [_p, ctypes.c_int, ctypes.c_size_t],
+            "hipStreamCreate": [ctypes.POINTER(ctypes.c_void_p)],
+            "hipStreamSynchronize": [_p],
+            "hipDeviceSynchronize": [],
+            "hipEventCreate": [ctypes.POINTER(ctypes.c_void_p)],
+            "hipEventDestroy": [_p],
+            "hipEventRecord": [_p, _p],
+            "hipEventSynchronize": [_p],
+            "hipEventElapsedTime": [ctypes.POINTER(ctypes.c_float), _p, _p],
+            "hipGetDeviceCount": [ctypes.POINTER(ctypes.c_int)],
+            "hipSetDevice": [ctypes.c_int],
+        }
+        for name, args in sig.items():
+            f = getattr(h, name)
+            f.argtypes = args
+            f.restype = ctypes.c_int
+        _hiprt = h
+    return _hiprt
+
+
+def hip_check(rc: int, what: str) -> None:
+    if rc != HIP_SUCCESS:
+        raise QLError(what, rc)
+
+
+def device_count() -> int:
+    n = ctypes.c_int(0)
+    rc = hip().hipGetDeviceCount(ctypes.byref(n))
+    return n.value if rc == HIP_SUCCESS else 0
+
+
+def stream() -> int:
+    """The library-wide work stream (created once, default priority)."""
+    global _stream
+    if _stream is None:
+        hip_check(hip().hipSetDevice(0), "hipSetDevice")
+        s = ctypes.c_void_p()
+        hip_check(hip().hipStreamCreate(ctypes.byref(s)), "hipStreamCreate")
+        _stream = s.value
+    return _stream
+
+
+def synchronize() -> None:
+    hip_check(hip().hipStreamSynchronize(stream()), "hipStreamSynchronize")
+
+
+class DeviceArray:
+    """A device allocation (or a window of one) with a numpy dtype and shape."""
+
+    def __init__(self, shape, dtype, _owner=None, _ptr=None):
+        import numpy as np
+        self.dtype = np.dtype(dtype)
+        self.shape = tuple(int(s) for s in (shape if isinstance(shape, (tuple, list)) else (shape,)))
+        self.size = int(np.prod(self.shape)) if self.shape else 1
+        self.nbytes = self.size * self.dtype.itemsize
+        self._owner = _owner
+        if _ptr is None:
+            p = ctypes.c_void_p()
+            hip_check(hip().hipMalloc(ctypes.byref(p), max(self.nbytes, 1)), "hipMalloc")
+            self.ptr = p.value
+            self._owns = True
+        else:
+            self.ptr = _ptr
+            self._owns = False
+
+    def data_ptr(self) -> int:
+        return self.ptr
+
+    def window(self, start: int, count: int, shape=None) -> "DeviceArray":
+        """Elements [start, start+count) as a new array sharing this memory."""
+        assert 0 <= start and start + count <= self.size
+        owner = self if self._owns else self._owner
+        return DeviceArray(shape or (count,), self.dtype, _owner=owner,
+                           _ptr=self.ptr + start * self.dtype.itemsize)
+
+    def fill_bytes(self, byte: int) -> "DeviceArray":
+        hip_check(hip().hipMemset(self.ptr, byte, self.nbytes), "hipMemset")
+        return self
+
+    def upload(self, a) -> "DeviceArray":
+        import numpy as np
+        a = np.ascontiguousarray(a)
+        assert a.nbytes == self.nbytes, (a.nbytes, self.nbytes)
+        synchronize()
+        hip_check(hip().hipMemcpy(self.ptr, a.ctypes.data, a.nbytes, H2D), "hipMemcpy H2D")
+        return self
+
+    def numpy(self):
+        import numpy as np
+        out = np.empty(self.shape, self.dtype)
+        synchronize()
+        hip_check(hip().hipMemcpy(out.ctypes.data, self.ptr, self.nbytes, D2H), "hipMemcpy D2H")
+        return out
+
+    @classmethod
+    def from_numpy(cls, a) -> "DeviceArray":
+        import numpy as np
+        a = np.ascontiguousarray(a)
+        return cls(a.shape, a.dtype).upload(a)
+
+    def __del__(self):
+        if getattr(self, "_owns", False) and _hiprt is not None:
+            try:
+                _hiprt.hipFree(self.ptr)
+            except Exception:  # interpreter shutdown
+                pass
+
+
+class Event:
+    def __init__(self):
+        e = ctypes.c_void_p()
+        hip_check(hip().hipEventCreate(ctypes.byref(e)), "hipEventCreate")
+        self.ev = e.value
+
+    def record(self, s: int | None = None) -> None:
+        hip_check(hip().hipEventRecord(self.ev, stream() if s is None else s), "hipEventRecord")
+
+    def elapsed_ms(self, end: "Event") -> float:
+        hip_check(hip().hipEventSynchronize(end.ev), "hipEventSynchronize")
+        ms = ctypes.c_float()
+        hip_check(hip().hipEventElapsedTime(ctypes.byref(ms), self.ev, end.ev), "hipEventElapsedTime")
+        return ms.value
+
+    def __del__(self):
+        if _hiprt is not None:
+            try:
+                _hiprt.hipEventDestroy(self.ev)
+            except Exception:
+                pass

@@ -82,31 +82,22 @@ def check_abs(got: np.ndarray, want: np.ndarray, atol: float, what: str = ""):
     return m
 
 
-# ---- device side (torch is the allocator and stream provider only) -------------------
+# ---- device side: HIP runtime through the library's own binding (no framework) ------
 def dev(a: np.ndarray, offset_elems: int = 0):
-    """Copy a numpy array to cuda:0.  uint16 arrays travel as int16 bit patterns.
-    offset_elems > 0 returns a view starting that many elements into a larger
-    buffer (to exercise unaligned paths)."""
-    import torch
-    a = np.ascontiguousarray(a)
-    if a.dtype == np.uint16:
-        a = a.view(np.int16)
-    t = torch.from_numpy(a.reshape(-1))
+    """Copy a numpy array to the GPU.  offset_elems > 0 places it that many
+    elements into a larger allocation (to exercise unaligned paths)."""
+    import quantlib_amd as ql
+    a = np.ascontiguousarray(a).reshape(-1)
     if offset_elems:
-        buf = torch.empty(t.numel() + offset_elems, dtype=t.dtype)
-        buf[offset_elems:] = t
-        d = buf.to("cuda:0")[offset_elems:]
-    else:
-        d = t.to("cuda:0")
-    return d
+        buf = ql.DeviceArray((a.size + offset_elems,), a.dtype)
+        d = buf.window(offset_elems, a.size)
+        d.upload(a)
+        return d
+    return ql.DeviceArray.from_numpy(a)
 
 
 def host(t, dtype=None, shape=None) -> np.ndarray:
-    import torch
-    torch.cuda.synchronize()
-    a = t.detach().cpu().numpy()
-    if a.dtype == np.int16:
-        a = a.view(np.uint16)
+    a = t.numpy().reshape(-1)
     if dtype is not None:
         a = a.view(dtype)
     if shape is not None:
@@ -116,19 +107,22 @@ def host(t, dtype=None, shape=None) -> np.ndarray:
 
 def empty(shape, dtype, fill_bits: int | None = None):
     """Device buffer; fill_bits sets every byte (guard pattern)."""
-    import torch
-    n = int(np.prod(shape))
-    tdt = {np.float32: torch.float32, np.uint16: torch.int16, np.int32: torch.int32}[dtype]
-    t = torch.empty(n, dtype=tdt, device="cuda:0")
+    import quantlib_amd as ql
+    t = ql.DeviceArray((int(np.prod(shape)),), dtype)
     if fill_bits is not None:
-        t.view(torch.uint8).fill_(fill_bits)
+        t.fill_bytes(fill_bits)
     return t
 
 
 def stream() -> int:
-    import torch
-    return torch.cuda.current_stream().cuda_stream
+    import quantlib_amd as ql
+    return ql.stream()
+
+
+def synchronize() -> None:
+    import quantlib_amd as ql
+    ql.synchronize()
 
 
 def ptr(t) -> int:
-    return t.data_ptr()
+    return t.ptr

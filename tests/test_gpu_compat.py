@@ -35,8 +35,7 @@ def fn(name, argtypes, restype=None):
 
 
 def sync():
-    import torch
-    torch.cuda.synchronize()
+    ql.synchronize()
 
 
 _hip = None

@@ -25,11 +25,9 @@ class Out:
     """Device output buffer of n elements between two guard bands."""
 
     def __init__(self, n, dtype, offset=0):
-        import torch
         self.n, self.dtype, self.offset = n, dtype, offset
         self.buf = empty((n + 2 * GUARD + offset,), dtype, fill_bits=GUARD_BYTE)
-        self.view = self.buf[GUARD + offset:GUARD + offset + n]
-        self.torch = torch
+        self.view = self.buf.window(GUARD + offset, n)
 
     @property
     def ptr(self):
@@ -372,7 +370,6 @@ def test_kv_append_contiguous(f16, L, S, H, d, T, layer, pos):
 
 def test_paged_kv_append_f16_c5_and_permuted():
     # C5: 8192 tokens -> 512 blocks of 16; block [L,16,8,128]; fresh-pool order 0,1,2,...
-    import torch
     T, H, d, L, layer = 8192, 8, 128, 8, 5
     nb = T // 16
     blk = L * 16 * H * d
@@ -383,8 +380,8 @@ def test_paged_kv_append_f16_c5_and_permuted():
     for order in (np.arange(nb), r.permutation(nb)):
         kpool = empty((nb * blk,), np.uint16, fill_bits=GUARD_BYTE)
         vpool = empty((nb * blk,), np.uint16, fill_bits=GUARD_BYTE)
-        kptrs = torch.tensor([kpool.data_ptr() + 2 * blk * b for b in range(nb)], dtype=torch.int64).cuda()
-        vptrs = torch.tensor([vpool.data_ptr() + 2 * blk * b for b in range(nb)], dtype=torch.int64).cuda()
+        kptrs = dev(np.array([kpool.ptr + 2 * blk * b for b in range(nb)], np.int64))
+        vptrs = dev(np.array([vpool.ptr + 2 * blk * b for b in range(nb)], np.int64))
         slots = np.array([order[t // 16] * 16 + t % 16 for t in range(T)], np.int32)
         slots[[3, 4000]] = -1                       # padding tokens are skipped
         dsl = dev(slots)
@@ -399,7 +396,6 @@ def test_paged_kv_append_f16_c5_and_permuted():
 
 
 def test_paged_kv_append_unaligned_rows_and_bad_slots():
-    import torch
     T, H, d, L, layer, nb = 40, 3, 6, 2, 1, 4        # kv = 18 elements: not 16-byte rows
     blk = L * 16 * H * d
     r = np.random.default_rng(9)
@@ -407,8 +403,8 @@ def test_paged_kv_append_unaligned_rows_and_bad_slots():
     vn = r.integers(0, 60000, size=(T, H, d)).astype(np.uint16)
     kpool = empty((nb * blk,), np.uint16, fill_bits=GUARD_BYTE)
     vpool = empty((nb * blk,), np.uint16, fill_bits=GUARD_BYTE)
-    kptrs = torch.tensor([kpool.data_ptr() + 2 * blk * b for b in range(nb)], dtype=torch.int64).cuda()
-    vptrs = torch.tensor([vpool.data_ptr() + 2 * blk * b for b in range(nb)], dtype=torch.int64).cuda()
+    kptrs = dev(np.array([kpool.ptr + 2 * blk * b for b in range(nb)], np.int64))
+    vptrs = dev(np.array([vpool.ptr + 2 * blk * b for b in range(nb)], np.int64))
     slots = (np.arange(T) + 5).astype(np.int32)
     slots[7] = nb * 16 + 3                            # block beyond the pool: skipped
     dsl, dkn, dvn = dev(slots), dev(kn), dev(vn)
