@@ -51,6 +51,9 @@ BYTES = {
     "swiglu_f16": 3 * T * F * 2,                                  # read gate,up; write out
     "embed_f16": 2 * T * D * 2 + 4 * T,                           # read rows; write out; ids
 }
+COPY_TOKENS = 131072                                              # 256 MiB per K and V
+COPY_ELEMS = COPY_TOKENS * HKV * HD
+BYTES["copy_calibration"] = 2 * 2 * COPY_ELEMS * 2                # read + write, K and V
 CHAIN = ["add_rmsnorm_f16", "rope_f16", "paged_kv_append_f16", "add_rmsnorm_f16", "swiglu_f16"]
 CHAIN_BYTES = sum(BYTES[k] for k in CHAIN)
 
@@ -108,6 +111,9 @@ class Chain:
         self.table = up(randn(VOCAB, D))
         self.ids = up(r.integers(0, VOCAB, size=T).astype(np.int32))
         self.emb_out = [ql.DeviceArray((T, D), np.uint16) for _ in range(NSETS)]
+        # plain-copy reference: 2 x 256 MiB copied by the contiguous KV-append kernel
+        self.cp_src = [ql.DeviceArray((COPY_ELEMS,), np.uint16) for _ in range(2)]
+        self.cp_dst = [ql.DeviceArray((COPY_ELEMS,), np.uint16) for _ in range(2)]
         self.stream = ql.stream()
         self.step_no = 0
         ql.synchronize()
@@ -133,6 +139,11 @@ class Chain:
         self.ql.call("ql_embed_f16", self.table.ptr, self.ids.ptr, T, VOCAB, D,
                      self.emb_out[i % NSETS].ptr, self.stream)
 
+    def k_copy(self):
+        # [COPY_TOKENS, 8, 128] fp16 per K and V: a pure 16-byte copy of known size
+        self.ql.call("ql_kv_append_f16", self.cp_dst[0].ptr, self.cp_dst[1].ptr, self.cp_src[0].ptr,
+                     self.cp_src[1].ptr, 0, 0, COPY_TOKENS, HKV, HD, COPY_TOKENS, 1, self.stream)
+
     def step(self, ev_swiglu=None):
         i = self.step_no
         self.step_no += 1
@@ -154,13 +165,15 @@ class Chain:
             "paged_kv_append_f16": lambda i: self.k_paged(self.sets[i % NSETS], i % L_POOL),
             "swiglu_f16": lambda i: self.k_swiglu(self.sets[i % NSETS]),
             "embed_f16": lambda i: self.k_embed(i),
+            "copy_calibration": lambda i: self.k_copy(),
         }[name]
 
 
 def breakdown(chain, ql, reps):
     """Average duration of each kernel, HIP events around every launch."""
     out = {}
-    for name in ["add_rmsnorm_f16", "rope_f16", "paged_kv_append_f16", "swiglu_f16", "embed_f16"]:
+    for name in ["add_rmsnorm_f16", "rope_f16", "paged_kv_append_f16", "swiglu_f16", "embed_f16",
+                 "copy_calibration"]:
         launch = chain.kernel_launcher(name)
         for i in range(3):
             launch(i)
