@@ -7,12 +7,13 @@ of the reference's fp16_layer_forward (src/fp16_forward.cu:167-223), GEMMs
 and attention excluded:
 
   1. residual add + attention RMSNorm   x[8192,4096] += d; y = rmsnorm(x)
-  2. RoPE, Q and K in one launch        Q[8192,32,128], K[8192,8,128], theta 5e5, rotate-half
-  3. paged KV append                    K,V[8192,8,128] -> 512 blocks of 16 (pool of 32 layers)
-  4. residual add + FFN RMSNorm         as 1
-  5. SwiGLU                             gate, up [8192,14336] -> out
+  2. RoPE on Q and K + paged KV append  Q[8192,32,128], K,V[8192,8,128], theta 5e5, rotate-half;
+     (one fused launch)                 rotated K and V -> 512 blocks of 16 (pool of 32 layers)
+  3. residual add + FFN RMSNorm         as 1
+  4. SwiGLU                             gate, up [8192,14336] -> out
 
-One step = one pass of that chain.  Inputs are synthetic (seeded normal values
+One step = one pass of that chain.  The unfused RoPE and paged-append kernels
+are timed separately under "kernels" for comparison.  Inputs are synthetic (seeded normal values
 made on the host and uploaded once) and resident in HBM before timing.  Three
 device buffer sets (~1 GB each) are rotated step to step so no input is still
 in the 256 MB MALL; the KV append rotates over the 32 pool layers.
@@ -50,11 +51,16 @@ BYTES = {
     "paged_kv_append_f16": 4 * T * HKV * HD * 2 + 4 * T,          # read K,V; write K,V; slots
     "swiglu_f16": 3 * T * F * 2,                                  # read gate,up; write out
     "embed_f16": 2 * T * D * 2 + 4 * T,                           # read rows; write out; ids
+    # Q read+write; K read, write in place, write to cache; V read, write to cache; slots
+    "rope_paged_kv_append_f16": 2 * T * HQ * HD * 2 + 5 * T * HKV * HD * 2 + 4 * T,
 }
 COPY_TOKENS = 131072                                              # 256 MiB per K and V
 COPY_ELEMS = COPY_TOKENS * HKV * HD
 BYTES["copy_calibration"] = 2 * 2 * COPY_ELEMS * 2                # read + write, K and V
-CHAIN = ["add_rmsnorm_f16", "rope_f16", "paged_kv_append_f16", "add_rmsnorm_f16", "swiglu_f16"]
+CHAIN = ["add_rmsnorm_f16", "rope_paged_kv_append_f16", "add_rmsnorm_f16", "swiglu_f16"]
+# the same layer with RoPE and the paged append as two launches (reference order)
+CHAIN_UNFUSED = ["add_rmsnorm_f16", "rope_f16", "paged_kv_append_f16", "add_rmsnorm_f16",
+                 "swiglu_f16"]
 CHAIN_BYTES = sum(BYTES[k] for k in CHAIN)
 
 
@@ -68,6 +74,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target CPU time of the oracle baseline sample (0 = skip)")
     ap.add_argument("--traffic-file", default=str(ROOT / "profiles" / "pmc_traffic.json"))
+    ap.add_argument("--all-configs", action="store_true",
+                    help="time every BASELINE config (C1..C5) and print a table instead of the JSON line")
+    ap.add_argument("--reps", type=int, default=50, help="launches per config in --all-configs")
     return ap.parse_args()
 
 
@@ -132,6 +141,11 @@ class Chain:
         self.ql.call("ql_paged_kv_append_f16", self.kptrs.ptr, self.vptrs.ptr, self.nb,
                      self.slots.ptr, s["k"].ptr, s["v"].ptr, T, layer, L_POOL, HKV, HD, self.stream)
 
+    def k_rope_paged(self, s, layer):
+        self.ql.call("ql_rope_paged_kv_append_f16", s["q"].ptr, s["k"].ptr, s["v"].ptr, T, HQ, HKV, HD,
+                     HQ * HD, HKV * HD, HKV * HD, None, 0, THETA, self.ql.ROPE_HALF, self.kptrs.ptr,
+                     self.vptrs.ptr, self.nb, self.slots.ptr, layer, L_POOL, self.stream)
+
     def k_swiglu(self, s):
         self.ql.call("ql_swiglu_f16", s["gate"].ptr, s["up"].ptr, s["out"].ptr, T, F, self.stream)
 
@@ -149,8 +163,7 @@ class Chain:
         self.step_no += 1
         s = self.sets[i % NSETS]
         self.k_add_rmsnorm(s, "d1")
-        self.k_rope(s)
-        self.k_paged(s, i % L_POOL)
+        self.k_rope_paged(s, i % L_POOL)
         self.k_add_rmsnorm(s, "d2")
         if ev_swiglu is not None:
             ev_swiglu[0].record(self.stream)
@@ -163,6 +176,7 @@ class Chain:
             "add_rmsnorm_f16": lambda i: self.k_add_rmsnorm(self.sets[i % NSETS], "d1"),
             "rope_f16": lambda i: self.k_rope(self.sets[i % NSETS]),
             "paged_kv_append_f16": lambda i: self.k_paged(self.sets[i % NSETS], i % L_POOL),
+            "rope_paged_kv_append_f16": lambda i: self.k_rope_paged(self.sets[i % NSETS], i % L_POOL),
             "swiglu_f16": lambda i: self.k_swiglu(self.sets[i % NSETS]),
             "embed_f16": lambda i: self.k_embed(i),
             "copy_calibration": lambda i: self.k_copy(),
@@ -172,8 +186,8 @@ class Chain:
 def breakdown(chain, ql, reps):
     """Average duration of each kernel, HIP events around every launch."""
     out = {}
-    for name in ["add_rmsnorm_f16", "rope_f16", "paged_kv_append_f16", "swiglu_f16", "embed_f16",
-                 "copy_calibration"]:
+    for name in ["add_rmsnorm_f16", "rope_paged_kv_append_f16", "rope_f16", "paged_kv_append_f16",
+                 "swiglu_f16", "embed_f16", "copy_calibration"]:
         launch = chain.kernel_launcher(name)
         for i in range(3):
             launch(i)
@@ -223,7 +237,7 @@ def cpu_baseline(seconds):
     def P(a):
         return a.ctypes.data
 
-    sample_bytes = CHAIN_BYTES * n // T
+    sample_bytes = CHAIN_BYTES * n // T  # the fused chain's bytes; the oracle runs rope then append
 
     def one(layer):
         lib.or_add_rmsnorm_f16(P(x), P(d1), P(w), P(y), n, D, EPS)
@@ -244,10 +258,105 @@ def cpu_baseline(seconds):
             break
     gbs = sample_bytes * reps / el / 1e9
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"oracle/oracle.c scalar C (gcc -O2, 1 thread) running the same 5-op chain on "
+            "sample": f"oracle/oracle.c scalar C (gcc -O2, 1 thread) running the same layer chain on "
                       f"{n} of the {T} tokens (C5 shapes), {reps} passes in {el:.1f} s; "
                       f"{sample_bytes / 1e6:.1f} MB of algorithmic traffic per pass; "
                       f"= {el / reps * T / n * 1e6:.0f} us per decoder layer at T=8192"}
+
+
+def all_configs(ql, np, reps):
+    """Every BASELINE config: device time per launch, back to back on one stream
+    with enough rotating buffer sets that each launch reads data last touched
+    >= 1 GiB earlier (defeats the 256 MB MALL).  Returns a list of rows."""
+    r = np.random.default_rng(7)
+    st = ql.stream()
+    rows = []
+
+    def sets_for(nbytes):
+        return max(2, min(64, -(-(1 << 30) // max(nbytes, 1))))
+
+    def upload(a):
+        return ql.DeviceArray.from_numpy(a)
+
+    def f16(a):
+        return a.astype(np.float16).view(np.uint16)
+
+    def time_it(name, cfg, nbytes, nsets, make, launch):
+        bufs = [make() for _ in range(nsets)]
+        for i in range(3):
+            launch(bufs[i % nsets])
+        ql.synchronize()
+        a, b = ql.Event(), ql.Event()
+        a.record(st)
+        for i in range(reps):
+            launch(bufs[i % nsets])
+        b.record(st)
+        us = a.elapsed_ms(b) * 1e3 / reps
+        gbs = nbytes / (us * 1e-6) / 1e9
+        rows.append({"config": cfg, "kernel": name, "bytes": nbytes, "us": round(us, 2),
+                     "GBps": round(gbs, 1), "frac_peak": round(gbs / PEAK_HBM_GBS, 4)})
+        del bufs
+
+    def randn(*shape, clip=None, sigma=1.0):
+        x = r.standard_normal(size=shape, dtype=np.float32) * np.float32(sigma)
+        if clip:
+            np.clip(x, -clip, clip, out=x)
+        return x
+
+    # C1: RMSNorm fp32 2048x2048
+    R_, C_ = 2048, 2048
+    x1, w1 = randn(R_, C_), r.uniform(0.5, 1.5, C_).astype(np.float32)
+    nb = 2 * R_ * C_ * 4 + C_ * 4
+    dw1 = upload(w1)
+    time_it("rmsnorm_f32", "C1 2048x2048", nb, sets_for(nb),
+            lambda: (upload(x1), ql.DeviceArray((R_, C_), np.float32)),
+            lambda b: ql.call("ql_rmsnorm_f32", b[0].ptr, dw1.ptr, b[1].ptr, R_, C_, 1e-5, st))
+    # C2: RoPE fp32 Q[2048,32,64] + K[2048,4,64], both pairings
+    q2, k2 = randn(2048, 32 * 64), randn(2048, 4 * 64)
+    nb = 2 * (q2.nbytes + k2.nbytes)
+    for pairing, pname in ((ql.ROPE_HALF, "rotate-half"), (ql.ROPE_INTERLEAVED, "interleaved")):
+        time_it(f"rope_f32 {pname}", "C2 Q[2048,32,64]+K[2048,4,64]", nb, sets_for(nb),
+                lambda: (upload(q2), upload(k2)),
+                lambda b, p=pairing: ql.call("ql_rope_f32", b[0].ptr, b[1].ptr, 2048, 32, 4, 64,
+                                             32 * 64, 4 * 64, None, 0, 1e4, p, st))
+    # C3: SwiGLU fp32 and fp16, rows x 5632
+    for rows_ in (1, 32, 128, 512):
+        g3, u3 = randn(rows_, 5632, clip=8.0), randn(rows_, 5632, clip=8.0)
+        for prec in ("f32", "f16"):
+            gg, uu = (g3, u3) if prec == "f32" else (f16(g3), f16(u3))
+            nb = 3 * gg.nbytes
+            time_it(f"swiglu_{prec}", f"C3 {rows_}x5632", nb, sets_for(nb),
+                    lambda gg=gg, uu=uu: (upload(gg), upload(uu), ql.DeviceArray(gg.shape, gg.dtype)),
+                    lambda b, prec=prec, rows_=rows_: ql.call(f"ql_swiglu_{prec}", b[0].ptr, b[1].ptr,
+                                                             b[2].ptr, rows_, 5632, st))
+    # C4: softmax fp32 and fp16, 4096x4096 causal, N(0, sigma=2)
+    x4 = randn(4096, 4096, sigma=2.0)
+    x4[np.triu_indices(4096, k=1)] = -np.inf
+    for prec in ("f32", "f16"):
+        xx = x4 if prec == "f32" else f16(x4)
+        nb = 2 * xx.nbytes
+        time_it(f"softmax_{prec}", "C4 4096x4096 causal", nb, sets_for(nb),
+                lambda xx=xx: (upload(xx), ql.DeviceArray(xx.shape, xx.dtype)),
+                lambda b, prec=prec: ql.call(f"ql_softmax_{prec}", b[0].ptr, b[1].ptr, 4096, 4096, st))
+    del x4
+    # C5: the layer-chain kernels (one launch each, as in the default mode)
+    chain = Chain(ql, np)
+    for name in ["embed_f16", "add_rmsnorm_f16", "rope_f16", "paged_kv_append_f16",
+                 "rope_paged_kv_append_f16", "swiglu_f16"]:
+        launch = chain.kernel_launcher(name)
+        for i in range(3):
+            launch(i)
+        ql.synchronize()
+        a, b = ql.Event(), ql.Event()
+        a.record(st)
+        for i in range(reps):
+            launch(i)
+        b.record(st)
+        us = a.elapsed_ms(b) * 1e3 / reps
+        gbs = BYTES[name] / (us * 1e-6) / 1e9
+        rows.append({"config": "C5 T=8192 llama3-8b", "kernel": name, "bytes": BYTES[name],
+                     "us": round(us, 2), "GBps": round(gbs, 1), "frac_peak": round(gbs / PEAK_HBM_GBS, 4)})
+    return rows
 
 
 def main():
@@ -264,6 +373,15 @@ def main():
     if ql.device_count() < 1:
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
+    if args.all_configs:
+        rows = all_configs(ql, np, args.reps)
+        print("| config | kernel | algorithmic bytes | us per launch | GB/s | % of 8 TB/s |")
+        print("|---|---|---|---|---|---|")
+        for r_ in rows:
+            print(f"| {r_['config']} | {r_['kernel']} | {r_['bytes']:,} | {r_['us']:.2f} | "
+                  f"{r_['GBps']:.0f} | {100 * r_['frac_peak']:.1f} |", flush=True)
+        print(json.dumps({"all_configs": rows}), flush=True)
+        return
     chain = Chain(ql, np)
 
     for _ in range(args.warmup):
@@ -314,12 +432,14 @@ def main():
         "vs_baseline": None,
         "dtype": "f16",
         "data": "synthetic (seeded N(0,1) fp16; gate/up clipped to [-8,8]; w ~ U(0.5,1.5))",
-        "config": {"workload": "C5 llama3-8b-shaped fp16 decoder-layer chain: add+rmsnorm, rope q+k, "
-                               "paged kv append, add+rmsnorm, swiglu",
+        "config": {"workload": "C5 llama3-8b-shaped fp16 decoder-layer chain: add+rmsnorm, "
+                               "rope q+k fused with paged kv append, add+rmsnorm, swiglu",
                    "tokens": T, "hidden": D, "heads": HQ, "kv_heads": HKV, "head_dim": HD,
                    "ffn": F, "rope_theta": THETA, "rope_pairing": "rotate-half", "kv_block": PAGE,
                    "kv_pool_layers": L_POOL, "buffer_sets": NSETS,
-                   "chain_bytes_per_step": CHAIN_BYTES, "math": "fp32 with fp16 I/O"},
+                   "chain_bytes_per_step": CHAIN_BYTES,
+                   "chain_bytes_unfused": sum(BYTES[k] for k in CHAIN_UNFUSED),
+                   "math": "fp32 with fp16 I/O"},
         "roofline": {"kernel": "swiglu_f16 [8192 x 14336]", "bound": "hbm",
                      "achieved": round(sw_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(sw_gbs / PEAK_HBM_GBS, 4), "traffic": traffic,

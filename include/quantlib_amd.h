@@ -95,6 +95,39 @@ hipError_t ql_rope_f16(uint16_t* q, uint16_t* k, int n_tokens, int n_heads,
                        int64_t k_row_stride, const int32_t* positions, int pos_offset,
                        float theta, int pairing, hipStream_t stream);
 
+/* ---- fused RoPE + KV-cache append ------------------------------------------
+ * One launch that does what ql_rope_f16/f32(q, k, ...) followed by the cache
+ * append of the rotated K rows and of the V rows does, with identical results:
+ * Q and K are rotated in place, and token t's rotated K row and V row
+ * (v + t*v_row_stride, n_kv_heads*head_dim elements) are written to the cache.
+ * It saves the second launch and the re-read of K.  This is the "fused KV-cache
+ * append" of the reference's layer order: launch_fp16_rope on q and k, then
+ * fp16_kvcache_append (src/fp16_forward.cu:190-199).
+ * Paged: cache arguments as ql_paged_kv_append_f16 (slot < 0 or a block
+ * >= n_blocks skips that token's cache write; Q/K are still rotated).
+ * Contiguous: cache [n_layers, max_seq, n_kv_heads, head_dim], token t at
+ * position pos + t (pos + n_tokens <= max_seq). */
+hipError_t ql_rope_paged_kv_append_f16(uint16_t* q, uint16_t* k, const uint16_t* v, int n_tokens,
+                                       int n_heads, int n_kv_heads, int head_dim,
+                                       int64_t q_row_stride, int64_t k_row_stride,
+                                       int64_t v_row_stride, const int32_t* positions,
+                                       int pos_offset, float theta, int pairing,
+                                       uint16_t* const* k_blocks, uint16_t* const* v_blocks,
+                                       int n_blocks, const int32_t* slot_mapping, int layer,
+                                       int n_layers, hipStream_t stream);
+hipError_t ql_rope_kv_append_f16(uint16_t* q, uint16_t* k, const uint16_t* v, int n_tokens,
+                                 int n_heads, int n_kv_heads, int head_dim, int64_t q_row_stride,
+                                 int64_t k_row_stride, int64_t v_row_stride,
+                                 const int32_t* positions, int pos_offset, float theta,
+                                 int pairing, uint16_t* k_cache, uint16_t* v_cache, int layer,
+                                 int pos, int max_seq, int n_layers, hipStream_t stream);
+hipError_t ql_rope_kv_append_f32(float* q, float* k, const float* v, int n_tokens, int n_heads,
+                                 int n_kv_heads, int head_dim, int64_t q_row_stride,
+                                 int64_t k_row_stride, int64_t v_row_stride,
+                                 const int32_t* positions, int pos_offset, float theta,
+                                 int pairing, float* k_cache, float* v_cache, int layer, int pos,
+                                 int max_seq, int n_layers, hipStream_t stream);
+
 /* ---- SwiGLU -----------------------------------------------------------------
  * out = (g / (1 + exp(-g))) * u, elementwise over rows*ffn_dim elements.
  * Replaces launch_swiglu (kernels/feedforward.cu:27-35) and

@@ -1,10 +1,11 @@
 // gather.hip -- token-embedding gather and paged KV-cache append for gfx950.
 //
-// Both are row copies addressed through an index: one wavefront per token
-// reads the token's index once (a wavefront-uniform scalar load) and moves the
-// row with 16-byte lane accesses, 64 lanes covering a contiguous 1 KiB span per
-// instruction and up to 8 vectors per lane in flight.  Results are bit-exact
-// copies.
+// Both are row copies addressed through an index.  A wavefront serves a small
+// group of tokens: its first lanes resolve the group's indices to row
+// addresses in one round trip, then all lanes move the rows with 16-byte
+// nontemporal accesses, 64 lanes covering a contiguous 1 KiB span per
+// instruction with up to UNR vectors per lane in flight.  Results are
+// bit-exact copies.
 #include "ql_common.hpp"
 #include "quantlib_amd.h"
 
@@ -12,20 +13,44 @@ namespace {
 
 using namespace ql;
 
-constexpr int kRowUnroll = 8;
-
-// Copy `nvec` W-element units from src to dst, one wavefront.
-template <typename V>
-__device__ __forceinline__ void wave_copy(V* __restrict__ dst, const V* __restrict__ src,
-                                          int nvec, int lane) {
-    for (int b = lane; b < nvec; b += kWave * kRowUnroll) {
-        V r[kRowUnroll];
+// Copies TPW rows of `nvec` V-units, one wavefront.  Lane r < TPW holds row
+// r's source and destination addresses (0 = none); they are broadcast with
+// cross-lane permutes so every load of the group can be in flight at once
+// (UNR per lane per pass) instead of paying the index -> address -> data
+// latency chain once per row.  A row with a destination but no source is
+// zero-filled.
+template <int TPW, int UNR, bool NT, typename V>
+__device__ __forceinline__ void wave_rows_copy(unsigned long long src_l, unsigned long long dst_l,
+                                               int nvec, int lane) {
+    const int total = TPW * nvec;
+    for (int base = 0; base < total; base += kWave * UNR) {
+        V r[UNR];
 #pragma unroll
-        for (int u = 0; u < kRowUnroll; ++u)
-            if (b + u * kWave < nvec) r[u] = src[b + u * kWave];
+        for (int u = 0; u < UNR; ++u) {
+            const int idx = base + u * kWave + lane;
+            const int row = min(idx / nvec, TPW - 1);
+            const unsigned long long sp = __shfl(src_l, row, kWave);
+            if (idx < total && sp)
+                r[u] = load<NT>(reinterpret_cast<const V*>(sp) + (idx - row * nvec));
+        }
 #pragma unroll
-        for (int u = 0; u < kRowUnroll; ++u)
-            if (b + u * kWave < nvec) dst[b + u * kWave] = r[u];
+        for (int u = 0; u < UNR; ++u) {
+            const int idx = base + u * kWave + lane;
+            const int row = min(idx / nvec, TPW - 1);
+            const unsigned long long sp = __shfl(src_l, row, kWave);
+            const unsigned long long dp = __shfl(dst_l, row, kWave);
+            if (idx < total && dp) {
+                V v;
+                if (sp) {
+                    v = r[u];
+                } else {
+#pragma unroll
+                    for (int e = 0; e < (int)(sizeof(V) / 4); ++e)
+                        reinterpret_cast<uint32_t*>(&v)[e] = 0u;
+                }
+                store<NT>(reinterpret_cast<V*>(dp) + (idx - row * nvec), v);
+            }
+        }
     }
 }
 
@@ -33,27 +58,43 @@ __device__ __forceinline__ void wave_copy(V* __restrict__ dst, const V* __restri
 // batched over tokens.  An id outside [0, vocab) writes a zero row.
 // With ids == NULL the single token `one_id` is gathered (the reference's
 // one-token launchers pass the id by value).
-template <typename D, int W>
-__global__ __launch_bounds__(kBlock) void embed_rows(const D* __restrict__ table,
-                                                     const int32_t* __restrict__ ids,
-                                                     int one_id, int n_tokens, int vocab,
-                                                     int dim, D* __restrict__ out) {
-    using V = Vec<D, W>;
+// Vector path: TPW tokens per wavefront, 16-byte units (dim*sizeof(D) % 16 == 0
+// and 16-byte aligned table/out, checked by the host).
+template <typename D, int TPW, int UNR>
+__global__ __launch_bounds__(kBlock) void embed_rows_vec(const D* __restrict__ table,
+                                                         const int32_t* __restrict__ ids,
+                                                         int one_id, int n_tokens, int vocab,
+                                                         int dim, D* __restrict__ out) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int t0 = (blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave) * TPW;
+    if (t0 >= n_tokens) return;  // wavefront-uniform
+    unsigned long long src = 0, dst = 0;
+    if (lane < TPW && t0 + lane < n_tokens) {
+        const int t = t0 + lane;
+        const int id = ids ? ids[t] : one_id;
+        dst = reinterpret_cast<unsigned long long>(out + (size_t)t * dim);
+        if (id >= 0 && id < vocab) src = reinterpret_cast<unsigned long long>(table + (size_t)id * dim);
+    }
+    wave_rows_copy<TPW, UNR, true, Vec<char, 16>>(src, dst, dim * (int)sizeof(D) / 16, lane);
+}
+
+// Any dim / alignment: one wavefront per token, element copies.
+template <typename D>
+__global__ __launch_bounds__(kBlock) void embed_rows_scalar(const D* __restrict__ table,
+                                                            const int32_t* __restrict__ ids,
+                                                            int one_id, int n_tokens, int vocab,
+                                                            int dim, D* __restrict__ out) {
     const int lane = threadIdx.x & (kWave - 1);
     const int t = blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
     if (t >= n_tokens) return;
     const int id = ids ? ids[t] : one_id;
-    const int nvec = dim / W;
-    V* dst = reinterpret_cast<V*>(out + (size_t)t * dim);
-    if (id < 0 || id >= vocab) {
-        V z;
-#pragma unroll
-        for (int e = 0; e < W; ++e) z.v[e] = D(0);
-        for (int i = lane; i < nvec; i += kWave) dst[i] = z;
-        return;
-    }
-    wave_copy(dst, reinterpret_cast<const V*>(table + (size_t)id * dim), nvec, lane);
+    const bool ok = id >= 0 && id < vocab;
+    for (int i = lane; i < dim; i += kWave)
+        out[(size_t)t * dim + i] = ok ? table[(size_t)id * dim + i] : D(0);
 }
+
+constexpr int kEmbedTPW = 1;   // tokens per wavefront (measured best at C5)
+constexpr int kEmbedUNR = 8;
 
 template <typename D>
 hipError_t embed_dispatch(const D* table, const int32_t* ids, int one_id, int n_tokens,
@@ -61,23 +102,72 @@ hipError_t embed_dispatch(const D* table, const int32_t* ids, int one_id, int n_
     QL_CHECK_ARG(n_tokens >= 0 && vocab >= 0 && dim >= 0);
     if (n_tokens == 0 || dim == 0) return hipSuccess;
     QL_CHECK_ARG(table && out && (ids || n_tokens == 1));
-    constexpr int W = vec16<D>();
-    const unsigned grid = qlh::blocks_for(n_tokens, kBlock / kWave);
-    if (dim % W == 0 && qlh::aligned16(table) && qlh::aligned16(out))
-        hipLaunchKernelGGL((embed_rows<D, W>), dim3(grid), dim3(kBlock), 0, stream, table, ids,
-                           one_id, n_tokens, vocab, dim, out);
-    else
-        hipLaunchKernelGGL((embed_rows<D, 1>), dim3(grid), dim3(kBlock), 0, stream, table, ids,
-                           one_id, n_tokens, vocab, dim, out);
+    QL_CHECK_ARG((long long)dim * (long long)sizeof(D) < (1LL << 31));
+    const int wpb = kBlock / kWave;
+    if ((dim * (int)sizeof(D)) % 16 == 0 && qlh::aligned16(table) && qlh::aligned16(out)) {
+        const unsigned grid = qlh::blocks_for(n_tokens, (long long)wpb * kEmbedTPW);
+        hipLaunchKernelGGL((embed_rows_vec<D, kEmbedTPW, kEmbedUNR>), dim3(grid), dim3(kBlock), 0,
+                           stream, table, ids, one_id, n_tokens, vocab, dim, out);
+    } else {
+        hipLaunchKernelGGL((embed_rows_scalar<D>), dim3(qlh::blocks_for(n_tokens, wpb)),
+                           dim3(kBlock), 0, stream, table, ids, one_id, n_tokens, vocab, dim, out);
+    }
     return hipGetLastError();
 }
 
 // Paged append: token t's [kv] K and V runs go to
 //   blocks[slot/16] + ((layer*16 + slot%16) * kv)
 // (pool layout of src/paged_kvcache.cu:26-46, block [n_layers,16,H_kv,d]).
-// Block pointers are read from the device table, so the 16-byte path is
-// chosen per token from the actual addresses.
-__global__ __launch_bounds__(kBlock) void paged_append_rows(
+// Vector path (kv % 8 == 0, 16-byte aligned k_new/v_new, checked by the host):
+// TPW tokens per wavefront; lanes < TPW resolve slot -> block pointer, and a
+// block pointer that is not 16-byte aligned sends that token through the
+// element loop instead.
+template <int TPW, int UNR>
+__global__ __launch_bounds__(kBlock) void paged_append_vec(
+    _Float16* const* __restrict__ kb, _Float16* const* __restrict__ vb, int n_blocks,
+    const int32_t* __restrict__ slots, const _Float16* __restrict__ kn,
+    const _Float16* __restrict__ vn, int n_tokens, int layer, int kv) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int t0 = (blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave) * TPW;
+    if (t0 >= n_tokens) return;  // wavefront-uniform
+    unsigned long long ks = 0, vs = 0, kd = 0, vd = 0;
+    bool odd = false;  // destination not 16-byte aligned
+    if (lane < TPW && t0 + lane < n_tokens) {
+        const int t = t0 + lane;
+        const int slot = slots[t];
+        if (slot >= 0 && slot / QL_PAGE_SIZE < n_blocks) {
+            const int b = slot / QL_PAGE_SIZE;
+            const size_t off = ((size_t)layer * QL_PAGE_SIZE + slot % QL_PAGE_SIZE) * (size_t)kv;
+            kd = reinterpret_cast<unsigned long long>(kb[b] + off);
+            vd = reinterpret_cast<unsigned long long>(vb[b] + off);
+            ks = reinterpret_cast<unsigned long long>(kn + (size_t)t * kv);
+            vs = reinterpret_cast<unsigned long long>(vn + (size_t)t * kv);
+            odd = ((kd | vd) & 15) != 0;
+        }
+    }
+    if (__any(odd)) {
+        // rare: some block base is misaligned -- element copies for those tokens
+        for (int r = 0; r < TPW; ++r) {
+            const bool rodd = __shfl((int)odd, r, kWave);
+            if (!rodd) continue;
+            _Float16* kdr = reinterpret_cast<_Float16*>(__shfl(kd, r, kWave));
+            _Float16* vdr = reinterpret_cast<_Float16*>(__shfl(vd, r, kWave));
+            const _Float16* ksr = reinterpret_cast<const _Float16*>(__shfl(ks, r, kWave));
+            const _Float16* vsr = reinterpret_cast<const _Float16*>(__shfl(vs, r, kWave));
+            for (int i = lane; i < kv; i += kWave) {
+                kdr[i] = ksr[i];
+                vdr[i] = vsr[i];
+            }
+        }
+        if (odd) ks = vs = kd = vd = 0;
+    }
+    const int nvec = kv / 8;
+    wave_rows_copy<TPW, UNR, true, Vec<char, 16>>(ks, kd, nvec, lane);
+    wave_rows_copy<TPW, UNR, true, Vec<char, 16>>(vs, vd, nvec, lane);
+}
+
+// Any kv / alignment: one wavefront per token, element copies.
+__global__ __launch_bounds__(kBlock) void paged_append_scalar(
     _Float16* const* __restrict__ kb, _Float16* const* __restrict__ vb, int n_blocks,
     const int32_t* __restrict__ slots, const _Float16* __restrict__ kn,
     const _Float16* __restrict__ vn, int n_tokens, int layer, int kv) {
@@ -85,43 +175,17 @@ __global__ __launch_bounds__(kBlock) void paged_append_rows(
     const int t = blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
     if (t >= n_tokens) return;
     const int slot = slots[t];
-    if (slot < 0) return;
+    if (slot < 0 || slot / QL_PAGE_SIZE >= n_blocks) return;
     const int b = slot / QL_PAGE_SIZE;
-    const int o = slot % QL_PAGE_SIZE;
-    if (b >= n_blocks) return;
-    const size_t off = ((size_t)layer * QL_PAGE_SIZE + o) * (size_t)kv;
-    _Float16* kd = kb[b] + off;
-    _Float16* vd = vb[b] + off;
-    const _Float16* ks = kn + (size_t)t * kv;
-    const _Float16* vs = vn + (size_t)t * kv;
-    const bool vec_ok = kv % 8 == 0 &&
-                        (((uintptr_t)kd | (uintptr_t)vd | (uintptr_t)ks | (uintptr_t)vs) & 15) == 0;
-    if (vec_ok) {
-        using V = Vec<_Float16, 8>;
-        const int nvec = kv / 8;
-        // K and V interleaved in one pass: 2 x up to 4 vectors in flight per lane.
-        for (int bi = lane; bi < nvec; bi += kWave * 4) {
-            V rk[4], rv[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-                if (bi + u * kWave < nvec) {
-                    rk[u] = reinterpret_cast<const V*>(ks)[bi + u * kWave];
-                    rv[u] = reinterpret_cast<const V*>(vs)[bi + u * kWave];
-                }
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-                if (bi + u * kWave < nvec) {
-                    reinterpret_cast<V*>(kd)[bi + u * kWave] = rk[u];
-                    reinterpret_cast<V*>(vd)[bi + u * kWave] = rv[u];
-                }
-        }
-    } else {
-        for (int i = lane; i < kv; i += kWave) {
-            kd[i] = ks[i];
-            vd[i] = vs[i];
-        }
+    const size_t off = ((size_t)layer * QL_PAGE_SIZE + slot % QL_PAGE_SIZE) * (size_t)kv;
+    for (int i = lane; i < kv; i += kWave) {
+        kb[b][off + i] = kn[(size_t)t * kv + i];
+        vb[b][off + i] = vn[(size_t)t * kv + i];
     }
 }
+
+constexpr int kPagedTPW = 1;   // tokens per wavefront (measured best at C5)
+constexpr int kPagedUNR = 2;
 
 }  // namespace
 
@@ -163,12 +227,21 @@ extern "C" hipError_t ql_paged_kv_append_f16(uint16_t* const* k_blocks,
     if (n_tokens == 0 || n_blocks == 0) return hipSuccess;
     QL_CHECK_ARG(k_blocks && v_blocks && slot_mapping && k_new && v_new);
     const int kv = n_kv_heads * head_dim;
-    hipLaunchKernelGGL(paged_append_rows, dim3(qlh::blocks_for(n_tokens, kBlock / kWave)),
-                       dim3(kBlock), 0, stream,
-                       reinterpret_cast<_Float16* const*>(k_blocks),
-                       reinterpret_cast<_Float16* const*>(v_blocks), n_blocks, slot_mapping,
-                       reinterpret_cast<const _Float16*>(k_new),
-                       reinterpret_cast<const _Float16*>(v_new), n_tokens, layer, kv);
+    const int wpb = kBlock / kWave;
+    if (kv % 8 == 0 && qlh::aligned16(k_new) && qlh::aligned16(v_new)) {
+        hipLaunchKernelGGL((paged_append_vec<kPagedTPW, kPagedUNR>),
+                           dim3(qlh::blocks_for(n_tokens, (long long)wpb * kPagedTPW)), dim3(kBlock),
+                           0, stream, reinterpret_cast<_Float16* const*>(k_blocks),
+                           reinterpret_cast<_Float16* const*>(v_blocks), n_blocks, slot_mapping,
+                           reinterpret_cast<const _Float16*>(k_new),
+                           reinterpret_cast<const _Float16*>(v_new), n_tokens, layer, kv);
+    } else {
+        hipLaunchKernelGGL(paged_append_scalar, dim3(qlh::blocks_for(n_tokens, wpb)), dim3(kBlock),
+                           0, stream, reinterpret_cast<_Float16* const*>(k_blocks),
+                           reinterpret_cast<_Float16* const*>(v_blocks), n_blocks, slot_mapping,
+                           reinterpret_cast<const _Float16*>(k_new),
+                           reinterpret_cast<const _Float16*>(v_new), n_tokens, layer, kv);
+    }
     return hipGetLastError();
 }
 

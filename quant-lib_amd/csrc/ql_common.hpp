@@ -25,6 +25,41 @@ struct alignas(sizeof(D) * W) Vec {
 template <typename D>
 constexpr int vec16() { return 16 / (int)sizeof(D); }
 
+// Raw carriers for nontemporal (streaming) accesses of 2..32-byte values.
+typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+template <int BYTES>
+struct RawOf;
+template <> struct RawOf<32> { using type = u32x8; };
+template <> struct RawOf<16> { using type = u32x4; };
+template <> struct RawOf<8> { using type = u32x2; };
+template <> struct RawOf<4> { using type = uint32_t; };
+template <> struct RawOf<2> { using type = uint16_t; };
+
+// Load/store with the nontemporal hint when NT: data touched once is streamed
+// past the caches instead of displacing lines other wavefronts still need.
+template <bool NT, typename V>
+__device__ __forceinline__ V load(const V* p) {
+    if constexpr (NT) {
+        using R = typename RawOf<sizeof(V)>::type;
+        return __builtin_bit_cast(V, __builtin_nontemporal_load(reinterpret_cast<const R*>(p)));
+    } else {
+        return *p;
+    }
+}
+
+template <bool NT, typename V>
+__device__ __forceinline__ void store(V* p, const V& v) {
+    if constexpr (NT) {
+        using R = typename RawOf<sizeof(V)>::type;
+        __builtin_nontemporal_store(__builtin_bit_cast(R, v), reinterpret_cast<R*>(p));
+    } else {
+        *p = v;
+    }
+}
+
 __device__ __forceinline__ float to_f32(float x) { return x; }
 __device__ __forceinline__ float to_f32(_Float16 x) { return (float)x; }
 
@@ -32,8 +67,15 @@ template <typename D>
 __device__ __forceinline__ D from_f32(float x);
 template <>
 __device__ __forceinline__ float from_f32<float>(float x) { return x; }
+// The empty asm makes x an opaque, already-rounded fp32 value: without it the
+// compiler may fold the fp32 operation that produced x and this narrowing into
+// one mixed-precision FMA (v_fma_mix*), which rounds once instead of twice and
+// so differs from "fp32 result, then RNE to binary16" in rare last-bit cases.
 template <>
-__device__ __forceinline__ _Float16 from_f32<_Float16>(float x) { return (_Float16)x; }
+__device__ __forceinline__ _Float16 from_f32<_Float16>(float x) {
+    asm("" : "+v"(x));
+    return (_Float16)x;
+}
 
 // Round x to the precision of D and back (identity for float).
 template <typename D>

@@ -11,8 +11,10 @@
 // registers; WPR wavefronts share a row, each lane owns NV 16-byte vectors
 // (vector index lane + k*64*WPR, so every load instruction of a wavefront is
 // one contiguous 1 KiB span).  x (and d) are read once and y (and x') written
-// once: 2 (4 fused) row transfers per row, the HBM minimum.  Rows too wide for
-// registers, or unaligned layouts, take a block-per-row loop that re-reads x.
+// once: 2 (4 fused) row transfers per row, the HBM minimum, with nontemporal
+// hints on the streamed rows and ordinary (cached) loads of the shared weight.
+// Rows too wide for registers, or unaligned layouts, take a block-per-row loop
+// that re-reads x.
 #include "ql_common.hpp"
 #include "quantlib_amd.h"
 
@@ -20,82 +22,105 @@ namespace {
 
 using namespace ql;
 
-template <typename D, int NV, int WPR, bool ADD>
+// A row-group of WPR wavefronts handles RPT consecutive rows: all their loads
+// are issued first, the RPT partial sums are reduced together (one LDS
+// exchange and one barrier per group), then the rows are written.
+template <typename D, int NV, int WPR, int RPT, bool ADD, bool NT = true>
 __global__ __launch_bounds__(WPR <= 4 ? kBlock : kWave * WPR) void rmsnorm_rows(
     D* x, const D* __restrict__ d, const D* __restrict__ w, D* __restrict__ out,
     int rows, int dim, float eps) {
     constexpr int W = vec16<D>();
-    constexpr int TPR = kWave * WPR;                       // threads per row
+    constexpr int TPR = kWave * WPR;                       // threads per row-group
     constexpr int BLOCK = WPR <= 4 ? kBlock : kWave * WPR;
-    constexpr int RPB = BLOCK / TPR;                       // rows per block
+    constexpr int GPB = BLOCK / TPR;                       // row-groups per block
     using V = Vec<D, W>;
 
     const int tid = threadIdx.x;
-    const int row = blockIdx.x * RPB + tid / TPR;
+    const int row0 = (blockIdx.x * GPB + tid / TPR) * RPT;
     const int rl = tid % TPR;
-    const bool row_ok = row < rows;
     const int nvec = dim / W;
-    const size_t roff = (size_t)(row_ok ? row : 0) * (size_t)dim;
-
-    V* xr = reinterpret_cast<V*>(x + roff);
-    const V* dr = reinterpret_cast<const V*>(ADD ? d + roff : d);
     const V* wr = reinterpret_cast<const V*>(w);
 
-    V xv[NV], wv[NV];
-    V dv[ADD ? NV : 1];
+    V xv[RPT][NV], wv[NV];
+    V dv[ADD ? RPT : 1][ADD ? NV : 1];
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
         const int vi = rl + k * TPR;
-        if (row_ok && vi < nvec) {
-            xv[k] = xr[vi];
-            if constexpr (ADD) dv[k] = dr[vi];
-            wv[k] = wr[vi];
+        if (vi < nvec) wv[k] = wr[vi];  // shared by every row: keep it cached
+    }
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) {
+        const int row = row0 + r;
+        const V* xr = reinterpret_cast<const V*>(x + (size_t)(row < rows ? row : 0) * dim);
+        const V* dr = reinterpret_cast<const V*>(ADD ? d + (size_t)(row < rows ? row : 0) * dim : d);
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const int vi = rl + k * TPR;
+            if (row < rows && vi < nvec) {
+                xv[r][k] = load<NT>(xr + vi);
+                if constexpr (ADD) dv[r][k] = load<NT>(dr + vi);
+            }
         }
     }
 
     // Values stay in D precision (exact for the rounded sum) to halve the
     // register footprint of binary16 rows; they are widened again for output.
-    float ss = 0.0f;
+    float ss[RPT];
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-        const int vi = rl + k * TPR;
-        if (row_ok && vi < nvec) {
+    for (int r = 0; r < RPT; ++r) {
+        ss[r] = 0.0f;
+        const bool row_ok = row0 + r < rows;
 #pragma unroll
-            for (int e = 0; e < W; ++e) {
-                float a = to_f32(xv[k].v[e]);
-                if constexpr (ADD) {
-                    a = to_f32(dv[k].v[e]) + a;
-                    xv[k].v[e] = from_f32<D>(a);
-                    a = to_f32(xv[k].v[e]);
+        for (int k = 0; k < NV; ++k) {
+            const int vi = rl + k * TPR;
+            if (row_ok && vi < nvec) {
+#pragma unroll
+                for (int e = 0; e < W; ++e) {
+                    float a = to_f32(xv[r][k].v[e]);
+                    if constexpr (ADD) {
+                        a = a + to_f32(dv[r][k].v[e]);
+                        xv[r][k].v[e] = from_f32<D>(a);
+                        a = to_f32(xv[r][k].v[e]);
+                    }
+                    ss[r] = fmaf(a, a, ss[r]);
                 }
-                ss = fmaf(a, a, ss);
             }
+        }
+        ss[r] = wave_sum(ss[r]);
+    }
+    if constexpr (WPR > 1) {
+        __shared__ float red[BLOCK / kWave][RPT];
+#pragma unroll
+        for (int r = 0; r < RPT; ++r)
+            if ((tid & (kWave - 1)) == 0) red[tid / kWave][r] = ss[r];
+        __syncthreads();
+        const int w0 = (tid / TPR) * WPR;
+#pragma unroll
+        for (int r = 0; r < RPT; ++r) {
+            ss[r] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < WPR; ++i) ss[r] += red[w0 + i][r];
         }
     }
 
-    ss = wave_sum(ss);
-    if constexpr (WPR > 1) {
-        __shared__ float red[BLOCK / kWave];
-        if ((tid & (kWave - 1)) == 0) red[tid / kWave] = ss;
-        __syncthreads();
-        const int w0 = (tid / TPR) * WPR;
-        ss = 0.0f;
 #pragma unroll
-        for (int i = 0; i < WPR; ++i) ss += red[w0 + i];
-    }
-    const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
-
-    V* orow = reinterpret_cast<V*>(out + roff);
+    for (int r = 0; r < RPT; ++r) {
+        const int row = row0 + r;
+        if (row >= rows) continue;
+        const float inv = 1.0f / sqrtf(ss[r] / (float)dim + eps);
+        V* xr = reinterpret_cast<V*>(x + (size_t)row * dim);
+        V* orow = reinterpret_cast<V*>(out + (size_t)row * dim);
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-        const int vi = rl + k * TPR;
-        if (row_ok && vi < nvec) {
-            V y;
+        for (int k = 0; k < NV; ++k) {
+            const int vi = rl + k * TPR;
+            if (vi < nvec) {
+                V y;
 #pragma unroll
-            for (int e = 0; e < W; ++e)
-                y.v[e] = from_f32<D>((to_f32(xv[k].v[e]) * inv) * to_f32(wv[k].v[e]));
-            if constexpr (ADD) xr[vi] = xv[k];
-            orow[vi] = y;
+                for (int e = 0; e < W; ++e)
+                    y.v[e] = from_f32<D>((to_f32(xv[r][k].v[e]) * inv) * to_f32(wv[k].v[e]));
+                if constexpr (ADD) store<NT>(xr + vi, xv[r][k]);
+                store<NT>(orow + vi, y);
+            }
         }
     }
 }
@@ -133,13 +158,13 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_rows_generic(
     }
 }
 
-template <typename D, int NV, int WPR, bool ADD>
+template <typename D, int NV, int WPR, bool ADD, int RPT = 1>
 hipError_t launch_fast(D* x, const D* d, const D* w, D* out, int rows, int dim, float eps,
                        hipStream_t stream) {
     constexpr int BLOCK = WPR <= 4 ? kBlock : kWave * WPR;
-    constexpr int RPB = BLOCK / (kWave * WPR);
+    constexpr int RPB = BLOCK / (kWave * WPR) * RPT;
     const unsigned grid = qlh::blocks_for(rows, RPB);
-    hipLaunchKernelGGL((rmsnorm_rows<D, NV, WPR, ADD>), dim3(grid), dim3(BLOCK), 0, stream,
+    hipLaunchKernelGGL((rmsnorm_rows<D, NV, WPR, RPT, ADD>), dim3(grid), dim3(BLOCK), 0, stream,
                        x, d, w, out, rows, dim, eps);
     return hipGetLastError();
 }
@@ -156,13 +181,16 @@ hipError_t rmsnorm_dispatch(D* x, const D* d, const D* w, D* out, int rows, int 
                         qlh::aligned16(out) && (!ADD || qlh::aligned16(d));
     const int nvec = dim / W;
     if (vec_ok) {
+        // Spread a row over as many wavefronts as it has 64-vector chunks (up
+        // to 16): one 16-byte vector per lane measured fastest (more waves in
+        // flight, shorter reduction tails).
         if (nvec <= 64) return launch_fast<D, 1, 1, ADD>(x, d, w, out, rows, dim, eps, stream);
-        if (nvec <= 128) return launch_fast<D, 2, 1, ADD>(x, d, w, out, rows, dim, eps, stream);
-        if (nvec <= 256) return launch_fast<D, 4, 1, ADD>(x, d, w, out, rows, dim, eps, stream);
-        if (nvec <= 512) return launch_fast<D, 8, 1, ADD>(x, d, w, out, rows, dim, eps, stream);
-        if (nvec <= 1024) return launch_fast<D, 8, 2, ADD>(x, d, w, out, rows, dim, eps, stream);
-        if (nvec <= 2048) return launch_fast<D, 8, 4, ADD>(x, d, w, out, rows, dim, eps, stream);
-        if (nvec <= 4096) return launch_fast<D, 8, 8, ADD>(x, d, w, out, rows, dim, eps, stream);
+        if (nvec <= 128) return launch_fast<D, 1, 2, ADD>(x, d, w, out, rows, dim, eps, stream);
+        if (nvec <= 256) return launch_fast<D, 1, 4, ADD>(x, d, w, out, rows, dim, eps, stream);
+        if (nvec <= 512) return launch_fast<D, 1, 8, ADD>(x, d, w, out, rows, dim, eps, stream);
+        if (nvec <= 1024) return launch_fast<D, 1, 16, ADD>(x, d, w, out, rows, dim, eps, stream);
+        if (nvec <= 2048) return launch_fast<D, 2, 16, ADD>(x, d, w, out, rows, dim, eps, stream);
+        if (nvec <= 4096) return launch_fast<D, 4, 16, ADD>(x, d, w, out, rows, dim, eps, stream);
         if (nvec <= 8192) return launch_fast<D, 8, 16, ADD>(x, d, w, out, rows, dim, eps, stream);
     }
     hipLaunchKernelGGL((rmsnorm_rows_generic<D, ADD>), dim3((unsigned)rows), dim3(kBlock), 0,

@@ -7,17 +7,24 @@
 //   e   = (2i) / d                       fp32 division, as the reference
 //   inv = 1 / (float)pow(theta, e)       pow in fp64, rounded to fp32
 //   a   = (float)pos * inv               fp32
-//   c   = (float)cos(a), s = (float)sin(a)   evaluated in fp64, rounded to fp32
+//   c   = cos(a), s = sin(a)             evaluated in fp64 and rounded to fp32
+//                                        (bit-identical to the CPU restatement; a
+//                                        1-ulp fp32 sincos would move outputs that
+//                                        cancel to near zero by binary16 steps)
 //   y0  = fma(x0, c, -(x1*s)),  y1 = fma(x0, s, x1*c)
 // Pairing: interleaved (2i, 2i+1) as the reference, or rotate-half (i, i+d/2).
 //
 // Fast path (d/2 <= 64 pairs, 16-byte aligned rows, head chunks that tile a
-// wavefront): one wavefront per (token, group of heads).  Lane l evaluates the
-// trig of pair l once per token in fp64 and the values are redistributed with
-// cross-lane permutes, so the fp64 work is one sincos per pair per token,
-// shared by all heads of the group.  Each lane then owns one 16-byte chunk
-// position j of the head vector and walks the heads; every wavefront access is
-// a contiguous, coalesced 16-byte-per-lane span.
+// wavefront): inv_freq is computed once per call on the host (the same libm
+// pow the CPU restatement uses) and passed by value.  One wavefront serves a
+// (token, group of heads): every lane first issues the loads of all 16-byte
+// chunks it owns (at most MAXU, or MAXU pairs of chunks for rotate-half), then
+// evaluates the trig of pair `lane` while they are in flight; the values are
+// redistributed with cross-lane permutes so each pair's sincos is computed once
+// per token and group.  Every wavefront access is a contiguous, coalesced
+// 16-byte-per-lane span, streamed with nontemporal hints.
+#include <math.h>
+
 #include "ql_common.hpp"
 #include "quantlib_amd.h"
 
@@ -25,12 +32,24 @@ namespace {
 
 using namespace ql;
 
-__device__ __forceinline__ void rope_trig(int pos, int pair, int d, float theta, float& c,
-                                          float& s) {
+struct InvFreq {
+    float v[64];
+};
+
+// inv_freq of pair i, host side, in the order of kernels/rope.cu:35.
+float host_inv_freq(int pair, int d, float theta) {
     const float e = (2.0f * (float)pair) / (float)d;
     const float p = (float)pow((double)theta, (double)e);
-    const float inv = 1.0f / p;
-    const float a = (float)pos * inv;
+    return 1.0f / p;
+}
+
+__device__ __forceinline__ float dev_inv_freq(int pair, int d, float theta) {
+    const float e = (2.0f * (float)pair) / (float)d;
+    const float p = (float)pow((double)theta, (double)e);
+    return 1.0f / p;
+}
+
+__device__ __forceinline__ void trig(float a, float& c, float& s) {
     double sd, cd;
     sincos((double)a, &sd, &cd);
     c = (float)cd;
@@ -43,104 +62,190 @@ __device__ __forceinline__ void rotate(float x0, float x1, float c, float s, flo
     y1 = fmaf(x0, s, x1 * c);
 }
 
-constexpr int kSlotsPerIter = 4;  // 16-byte chunks (pairs of chunks) in flight per lane
+// Where the fused variants put K and V: nothing (plain RoPE), the paged pool
+// (block pointer tables + slot mapping), or the contiguous cache
+// [n_layers, max_seq, n_kv_heads, head_dim] at positions pos0 + t.
+enum CacheKind { kNoCache = 0, kPagedCache = 1, kContigCache = 2 };
 
-template <typename D, int PAIRING>
+template <typename D>
+struct KvDst {
+    D* const* kb;           // paged: per-block K / V base pointers (device)
+    D* const* vb;
+    const int32_t* slots;   // paged: slot of each token (block*16 + offset), <0 = skip
+    int n_blocks;
+    D* kc;                  // contiguous: cache bases
+    D* vc;
+    int pos0;
+    int max_seq;
+    const D* v;             // new V rows [n_tokens, v_row_stride]
+    long long vs;
+    int layer;
+};
+
+// Cache row of token t for the current layer (K and V), or nullptr to skip.
+template <typename D, int CACHE>
+__device__ __forceinline__ void cache_rows(const KvDst<D>& kv, int t, int kvw, D*& kd, D*& vd) {
+    kd = vd = nullptr;
+    if constexpr (CACHE == kPagedCache) {
+        const int slot = kv.slots[t];
+        if (slot >= 0 && slot / QL_PAGE_SIZE < kv.n_blocks) {
+            const int b = slot / QL_PAGE_SIZE;
+            const size_t off = ((size_t)kv.layer * QL_PAGE_SIZE + slot % QL_PAGE_SIZE) * (size_t)kvw;
+            kd = kv.kb[b] + off;
+            vd = kv.vb[b] + off;
+        }
+    } else if constexpr (CACHE == kContigCache) {
+        const size_t off = ((size_t)kv.layer * kv.max_seq + kv.pos0 + t) * (size_t)kvw;
+        kd = kv.kc + off;
+        vd = kv.vc + off;
+    }
+}
+
+// Store a W-element chunk to a cache row that may not be 16-byte aligned
+// (paged block pointers come from a device table).
+template <typename D, typename V>
+__device__ __forceinline__ void store_cache(D* dst, const V& v, bool aligned) {
+    if (aligned) {
+        store<true>(reinterpret_cast<V*>(dst), v);
+    } else {
+#pragma unroll
+        for (int e = 0; e < (int)(sizeof(V) / sizeof(D)); ++e) dst[e] = v.v[e];
+    }
+}
+
+// Heads of a token, in order: hq Q heads, hk K heads, then (fused variants)
+// hk V heads that are copied to the cache unrotated.
+template <typename D, int PAIRING, int MAXU, int CACHE>
 __global__ __launch_bounds__(kBlock) void rope_fast(D* q, D* k, int n_tokens, int hq, int hk,
                                                     int d, long long qs, long long ks,
                                                     const int32_t* __restrict__ positions,
-                                                    int pos_offset, float theta,
-                                                    int heads_per_wave) {
+                                                    int pos_offset, InvFreq inv,
+                                                    int heads_per_wave, KvDst<D> kv) {
     constexpr int W = vec16<D>();
     constexpr int PPS = PAIRING == QL_ROPE_INTERLEAVED ? W / 2 : W;  // pairs per slot
+    constexpr bool HALF = PAIRING == QL_ROPE_HALF;
     using V = Vec<D, W>;
 
     const int lane = threadIdx.x & (kWave - 1);
     const int t = blockIdx.x * (kBlock / kWave) + (threadIdx.x / kWave);
     if (t >= n_tokens) return;  // wavefront-uniform; no barriers below
     const int npairs = d >> 1;
-    const int pos = positions ? positions[t] : pos_offset + t;
-
-    float c_own, s_own;
-    rope_trig(pos, lane % npairs, d, theta, c_own, s_own);
-
     const int S = npairs / PPS;  // slots per head; divides 64
     const int j = lane % S;
-    float c[PPS], s[PPS];
-#pragma unroll
-    for (int e = 0; e < PPS; ++e) {
-        c[e] = __shfl(c_own, j * PPS + e, kWave);
-        s[e] = __shfl(s_own, j * PPS + e, kWave);
-    }
-
+    const int hrot = hq + hk;                          // heads that rotate
+    const int htot = hrot + (CACHE != kNoCache ? hk : 0);
     const int h0 = blockIdx.y * heads_per_wave;
-    const int h1 = min(hq + hk, h0 + heads_per_wave);
-    const int nslots = (h1 - h0) * S;
+    const int h1 = min(htot, h0 + heads_per_wave);
+    const int nslots = (h1 - h0) * S;  // <= 64 * MAXU (host guarantees)
     D* qt = q ? q + (long long)t * qs : nullptr;
     D* kt = k ? k + (long long)t * ks : nullptr;
+    const D* vt = CACHE != kNoCache ? kv.v + (long long)t * kv.vs : nullptr;
 
-    for (int base = lane; base < nslots; base += kWave * kSlotsPerIter) {
-        V lo[kSlotsPerIter];
-        V hi[PAIRING == QL_ROPE_HALF ? kSlotsPerIter : 1];
-        V* plo[kSlotsPerIter];
+    D* kd = nullptr;
+    D* vd = nullptr;
+    bool cache_aligned = true;
+    if constexpr (CACHE != kNoCache) {
+        cache_rows<D, CACHE>(kv, t, hk * d, kd, vd);
+        cache_aligned = ((reinterpret_cast<uintptr_t>(kd) | reinterpret_cast<uintptr_t>(vd)) & 15) == 0;
+    }
+
+    V lo[MAXU];
+    V hi[HALF ? MAXU : 1];
+    D* src[MAXU];
+    int hs[MAXU];
 #pragma unroll
-        for (int u = 0; u < kSlotsPerIter; ++u) {
-            const int sl = base + u * kWave;
-            plo[u] = nullptr;
-            if (sl < nslots) {
-                const int h = h0 + sl / S;
-                D* head = h < hq ? qt + (long long)h * d : kt + (long long)(h - hq) * d;
-                plo[u] = reinterpret_cast<V*>(head) + j;
-                lo[u] = *plo[u];
-                if constexpr (PAIRING == QL_ROPE_HALF)
-                    hi[u] = *reinterpret_cast<V*>(reinterpret_cast<D*>(plo[u]) + npairs);
-            }
+    for (int u = 0; u < MAXU; ++u) {
+        const int sl = lane + u * kWave;
+        src[u] = nullptr;
+        hs[u] = -1;
+        if (sl < nslots) {
+            const int h = h0 + sl / S;
+            hs[u] = h;
+            // Selected as integer addresses: the equivalent nested pointer
+            // select crashes this toolchain's optimizer.
+            const uintptr_t head =
+                h < hq ? reinterpret_cast<uintptr_t>(qt) + sizeof(D) * (size_t)h * d
+                       : (h < hrot ? reinterpret_cast<uintptr_t>(kt) + sizeof(D) * (size_t)(h - hq) * d
+                                   : reinterpret_cast<uintptr_t>(vt) + sizeof(D) * (size_t)(h - hrot) * d);
+            src[u] = reinterpret_cast<D*>(head) + j * W;
+            lo[u] = load<true>(reinterpret_cast<const V*>(src[u]));
+            if constexpr (HALF) hi[u] = load<true>(reinterpret_cast<const V*>(src[u] + npairs));
         }
+    }
+
+    float c[PPS], s[PPS];
+    if (h0 < hrot) {  // wavefront-uniform: this group has heads to rotate
+        const int pos = positions ? positions[t] : pos_offset + t;
+        float c_own, s_own;
+        trig((float)pos * inv.v[lane % npairs], c_own, s_own);
 #pragma unroll
-        for (int u = 0; u < kSlotsPerIter; ++u) {
-            if (!plo[u]) continue;
-            if constexpr (PAIRING == QL_ROPE_INTERLEAVED) {
-                V y;
+        for (int e = 0; e < PPS; ++e) {
+            c[e] = __shfl(c_own, j * PPS + e, kWave);
+            s[e] = __shfl(s_own, j * PPS + e, kWave);
+        }
+    }
+
 #pragma unroll
-                for (int e = 0; e < PPS; ++e) {
-                    float y0, y1;
-                    rotate(to_f32(lo[u].v[2 * e]), to_f32(lo[u].v[2 * e + 1]), c[e], s[e], y0,
-                           y1);
-                    y.v[2 * e] = from_f32<D>(y0);
-                    y.v[2 * e + 1] = from_f32<D>(y1);
-                }
-                *plo[u] = y;
-            } else {
-                V ylo, yhi;
-#pragma unroll
-                for (int e = 0; e < PPS; ++e) {
-                    float y0, y1;
-                    rotate(to_f32(lo[u].v[e]), to_f32(hi[u].v[e]), c[e], s[e], y0, y1);
-                    ylo.v[e] = from_f32<D>(y0);
-                    yhi.v[e] = from_f32<D>(y1);
-                }
-                *plo[u] = ylo;
-                *reinterpret_cast<V*>(reinterpret_cast<D*>(plo[u]) + npairs) = yhi;
+    for (int u = 0; u < MAXU; ++u) {
+        if (!src[u]) continue;
+        const int h = hs[u];
+        if (CACHE != kNoCache && h >= hrot) {  // V head: copy into the cache
+            if (vd) {
+                D* dst = vd + (h - hrot) * d + j * W;
+                store_cache<D>(dst, lo[u], cache_aligned);
+                if constexpr (HALF) store_cache<D>(dst + npairs, hi[u], cache_aligned);
             }
+            continue;
+        }
+        V ylo, yhi;
+        if constexpr (!HALF) {
+#pragma unroll
+            for (int e = 0; e < PPS; ++e) {
+                float y0, y1;
+                rotate(to_f32(lo[u].v[2 * e]), to_f32(lo[u].v[2 * e + 1]), c[e], s[e], y0, y1);
+                ylo.v[2 * e] = from_f32<D>(y0);
+                ylo.v[2 * e + 1] = from_f32<D>(y1);
+            }
+            store<true>(reinterpret_cast<V*>(src[u]), ylo);
+        } else {
+#pragma unroll
+            for (int e = 0; e < PPS; ++e) {
+                float y0, y1;
+                rotate(to_f32(lo[u].v[e]), to_f32(hi[u].v[e]), c[e], s[e], y0, y1);
+                ylo.v[e] = from_f32<D>(y0);
+                yhi.v[e] = from_f32<D>(y1);
+            }
+            store<true>(reinterpret_cast<V*>(src[u]), ylo);
+            store<true>(reinterpret_cast<V*>(src[u] + npairs), yhi);
+        }
+        if (CACHE != kNoCache && h >= hq && kd) {  // rotated K also goes to the cache
+            D* dst = kd + (h - hq) * d + j * W;
+            store_cache<D>(dst, ylo, cache_aligned);
+            if constexpr (HALF) store_cache<D>(dst + npairs, yhi, cache_aligned);
         }
     }
 }
 
 // Any even head_dim (<= 2048), any alignment: one wavefront per token, lane =
-// pair index (strided), trig once per (token, pair), then every head.
-template <typename D, int PAIRING>
+// pair index (strided), trig once per (token, pair), then every head; fused
+// variants then copy the token's V row (and the rotated K row) to the cache.
+template <typename D, int PAIRING, int CACHE>
 __global__ __launch_bounds__(kBlock) void rope_generic(D* q, D* k, int n_tokens, int hq, int hk,
                                                        int d, long long qs, long long ks,
                                                        const int32_t* __restrict__ positions,
-                                                       int pos_offset, float theta) {
+                                                       int pos_offset, float theta,
+                                                       KvDst<D> kv) {
     const int lane = threadIdx.x & (kWave - 1);
     const int t = blockIdx.x * (kBlock / kWave) + (threadIdx.x / kWave);
     if (t >= n_tokens) return;
     const int npairs = d >> 1;
     const int pos = positions ? positions[t] : pos_offset + t;
+    D* kd = nullptr;
+    D* vd = nullptr;
+    if constexpr (CACHE != kNoCache) cache_rows<D, CACHE>(kv, t, hk * d, kd, vd);
     for (int p = lane; p < npairs; p += kWave) {
         float c, s;
-        rope_trig(pos, p, d, theta, c, s);
+        trig((float)pos * dev_inv_freq(p, d, theta), c, s);
         const int i0 = PAIRING == QL_ROPE_INTERLEAVED ? 2 * p : p;
         const int i1 = PAIRING == QL_ROPE_INTERLEAVED ? 2 * p + 1 : p + npairs;
         for (int h = 0; h < hq + hk; ++h) {
@@ -150,17 +255,38 @@ __global__ __launch_bounds__(kBlock) void rope_generic(D* q, D* k, int n_tokens,
             rotate(to_f32(head[i0]), to_f32(head[i1]), c, s, y0, y1);
             head[i0] = from_f32<D>(y0);
             head[i1] = from_f32<D>(y1);
+            if (CACHE != kNoCache && h >= hq && kd) {
+                kd[(h - hq) * d + i0] = from_f32<D>(y0);
+                kd[(h - hq) * d + i1] = from_f32<D>(y1);
+            }
+        }
+    }
+    if constexpr (CACHE != kNoCache) {
+        if (vd) {
+            const D* vt = kv.v + (long long)t * kv.vs;
+            for (int i = lane; i < hk * d; i += kWave) vd[i] = vt[i];
         }
     }
 }
 
-template <typename D>
+// Rows starting at p every stride_bytes are all 16-byte aligned (or p is unused).
+inline bool rows_aligned16(const void* p, int64_t stride_bytes) {
+    return !p || (qlh::aligned16(p) && stride_bytes % 16 == 0);
+}
+
+constexpr int kRopeMaxU = 4;        // chunks (or chunk pairs) per lane
+constexpr int kRopeTargetWaves = 16384;
+
+template <typename D, int CACHE>
 hipError_t rope_dispatch(D* q, D* k, int n_tokens, int hq, int hk, int d, int64_t qs,
                          int64_t ks, const int32_t* positions, int pos_offset, float theta,
-                         int pairing, hipStream_t stream) {
+                         int pairing, KvDst<D> kv, hipStream_t stream) {
     QL_CHECK_ARG(n_tokens >= 0 && hq >= 0 && hk >= 0);
     QL_CHECK_ARG(pairing == QL_ROPE_INTERLEAVED || pairing == QL_ROPE_HALF);
     QL_CHECK_ARG(d > 0 && d % 2 == 0 && d <= 2048);
+    if (CACHE != kNoCache) {
+        QL_CHECK_ARG(k && kv.v && hk > 0 && kv.vs >= (int64_t)hk * d);
+    }
     if (!q) hq = 0;
     if (!k) hk = 0;
     if (n_tokens == 0 || hq + hk == 0) return hipSuccess;
@@ -173,38 +299,51 @@ hipError_t rope_dispatch(D* q, D* k, int n_tokens, int hq, int hk, int d, int64_
     const int pps = pairing == QL_ROPE_INTERLEAVED ? W / 2 : W;
     const int slots = npairs % pps == 0 ? npairs / pps : 0;
     const bool tile_ok = npairs <= 64 && slots > 0 && 64 % slots == 0;
-    const bool align_ok = (!q || (qlh::aligned16(q) && (qs * (int64_t)sizeof(D)) % 16 == 0)) &&
-                          (!k || (qlh::aligned16(k) && (ks * (int64_t)sizeof(D)) % 16 == 0)) &&
-                          (d * (int)sizeof(D)) % 16 == 0;
+    bool align_ok = rows_aligned16(q, qs * (int64_t)sizeof(D)) &&
+                    rows_aligned16(k, ks * (int64_t)sizeof(D)) && (d * (int)sizeof(D)) % 16 == 0;
+    if (CACHE != kNoCache) align_ok = align_ok && rows_aligned16(kv.v, kv.vs * (int64_t)sizeof(D));
+    if (CACHE == kContigCache)
+        align_ok = align_ok && qlh::aligned16(kv.kc) && qlh::aligned16(kv.vc);
     const int tok_per_block = kBlock / kWave;
     const unsigned gx = qlh::blocks_for(n_tokens, tok_per_block);
     if (tile_ok && align_ok) {
-        // Split heads over more wavefronts when tokens alone do not give
-        // ~8K wavefronts (32 per CU on 256 CUs).
-        const int htot = hq + hk;
-        int groups = (8192 + n_tokens - 1) / n_tokens;
+        InvFreq inv;
+        for (int i = 0; i < 64; ++i) inv.v[i] = i < npairs ? host_inv_freq(i, d, theta) : 0.0f;
+        // Heads per wavefront: at most 64*kRopeMaxU chunks per wavefront, and
+        // split further while tokens alone give fewer than kRopeTargetWaves.
+        const int htot = hq + hk + (CACHE != kNoCache ? hk : 0);
+        const int hcap = (kWave * kRopeMaxU) / slots;
+        int groups = (kRopeTargetWaves + n_tokens - 1) / n_tokens;
         groups = groups < 1 ? 1 : (groups > htot ? htot : groups);
-        const int hpw = (htot + groups - 1) / groups;
+        int hpw = (htot + groups - 1) / groups;
+        hpw = hpw > hcap ? hcap : hpw;
         groups = (htot + hpw - 1) / hpw;
         if (pairing == QL_ROPE_INTERLEAVED)
-            hipLaunchKernelGGL((rope_fast<D, QL_ROPE_INTERLEAVED>), dim3(gx, groups),
-                               dim3(kBlock), 0, stream, q, k, n_tokens, hq, hk, d,
-                               (long long)qs, (long long)ks, positions, pos_offset, theta, hpw);
+            hipLaunchKernelGGL((rope_fast<D, QL_ROPE_INTERLEAVED, kRopeMaxU, CACHE>),
+                               dim3(gx, groups), dim3(kBlock), 0, stream, q, k, n_tokens, hq, hk,
+                               d, (long long)qs, (long long)ks, positions, pos_offset, inv, hpw,
+                               kv);
         else
-            hipLaunchKernelGGL((rope_fast<D, QL_ROPE_HALF>), dim3(gx, groups), dim3(kBlock), 0,
-                               stream, q, k, n_tokens, hq, hk, d, (long long)qs, (long long)ks,
-                               positions, pos_offset, theta, hpw);
+            hipLaunchKernelGGL((rope_fast<D, QL_ROPE_HALF, kRopeMaxU, CACHE>), dim3(gx, groups),
+                               dim3(kBlock), 0, stream, q, k, n_tokens, hq, hk, d, (long long)qs,
+                               (long long)ks, positions, pos_offset, inv, hpw, kv);
     } else {
         if (pairing == QL_ROPE_INTERLEAVED)
-            hipLaunchKernelGGL((rope_generic<D, QL_ROPE_INTERLEAVED>), dim3(gx), dim3(kBlock), 0,
-                               stream, q, k, n_tokens, hq, hk, d, (long long)qs, (long long)ks,
-                               positions, pos_offset, theta);
+            hipLaunchKernelGGL((rope_generic<D, QL_ROPE_INTERLEAVED, CACHE>), dim3(gx),
+                               dim3(kBlock), 0, stream, q, k, n_tokens, hq, hk, d, (long long)qs,
+                               (long long)ks, positions, pos_offset, theta, kv);
         else
-            hipLaunchKernelGGL((rope_generic<D, QL_ROPE_HALF>), dim3(gx), dim3(kBlock), 0,
+            hipLaunchKernelGGL((rope_generic<D, QL_ROPE_HALF, CACHE>), dim3(gx), dim3(kBlock), 0,
                                stream, q, k, n_tokens, hq, hk, d, (long long)qs, (long long)ks,
-                               positions, pos_offset, theta);
+                               positions, pos_offset, theta, kv);
     }
     return hipGetLastError();
+}
+
+template <typename D>
+KvDst<D> no_cache() {
+    KvDst<D> kv{};
+    return kv;
 }
 
 }  // namespace
@@ -214,8 +353,9 @@ extern "C" hipError_t ql_rope_f32(float* q, float* k, int n_tokens, int n_heads,
                                   int64_t k_row_stride, const int32_t* positions,
                                   int pos_offset, float theta, int pairing,
                                   hipStream_t stream) {
-    return rope_dispatch<float>(q, k, n_tokens, n_heads, n_kv_heads, head_dim, q_row_stride,
-                                k_row_stride, positions, pos_offset, theta, pairing, stream);
+    return rope_dispatch<float, kNoCache>(q, k, n_tokens, n_heads, n_kv_heads, head_dim,
+                                          q_row_stride, k_row_stride, positions, pos_offset,
+                                          theta, pairing, no_cache<float>(), stream);
 }
 
 extern "C" hipError_t ql_rope_f16(uint16_t* q, uint16_t* k, int n_tokens, int n_heads,
@@ -223,8 +363,76 @@ extern "C" hipError_t ql_rope_f16(uint16_t* q, uint16_t* k, int n_tokens, int n_
                                   int64_t k_row_stride, const int32_t* positions,
                                   int pos_offset, float theta, int pairing,
                                   hipStream_t stream) {
-    return rope_dispatch<_Float16>(reinterpret_cast<_Float16*>(q),
-                                   reinterpret_cast<_Float16*>(k), n_tokens, n_heads,
-                                   n_kv_heads, head_dim, q_row_stride, k_row_stride, positions,
-                                   pos_offset, theta, pairing, stream);
+    return rope_dispatch<_Float16, kNoCache>(
+        reinterpret_cast<_Float16*>(q), reinterpret_cast<_Float16*>(k), n_tokens, n_heads,
+        n_kv_heads, head_dim, q_row_stride, k_row_stride, positions, pos_offset, theta, pairing,
+        no_cache<_Float16>(), stream);
+}
+
+extern "C" hipError_t ql_rope_paged_kv_append_f16(
+    uint16_t* q, uint16_t* k, const uint16_t* v, int n_tokens, int n_heads, int n_kv_heads,
+    int head_dim, int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
+    const int32_t* positions, int pos_offset, float theta, int pairing,
+    uint16_t* const* k_blocks, uint16_t* const* v_blocks, int n_blocks,
+    const int32_t* slot_mapping, int layer, int n_layers, hipStream_t stream) {
+    QL_CHECK_ARG(n_layers > 0 && layer >= 0 && layer < n_layers && n_blocks >= 0);
+    QL_CHECK_ARG((long long)n_kv_heads * head_dim <= (1LL << 30));
+    QL_CHECK_ARG(n_tokens <= 0 || (k_blocks && v_blocks && slot_mapping));
+    KvDst<_Float16> kv{};
+    kv.kb = reinterpret_cast<_Float16* const*>(k_blocks);
+    kv.vb = reinterpret_cast<_Float16* const*>(v_blocks);
+    kv.slots = slot_mapping;
+    kv.n_blocks = n_blocks;
+    kv.v = reinterpret_cast<const _Float16*>(v);
+    kv.vs = v_row_stride;
+    kv.layer = layer;
+    return rope_dispatch<_Float16, kPagedCache>(
+        reinterpret_cast<_Float16*>(q), reinterpret_cast<_Float16*>(k), n_tokens, n_heads,
+        n_kv_heads, head_dim, q_row_stride, k_row_stride, positions, pos_offset, theta, pairing,
+        kv, stream);
+}
+
+template <typename D>
+hipError_t rope_contig_entry(D* q, D* k, const D* v, int n_tokens, int n_heads, int n_kv_heads,
+                             int head_dim, int64_t qs, int64_t ks, int64_t vs,
+                             const int32_t* positions, int pos_offset, float theta, int pairing,
+                             D* k_cache, D* v_cache, int layer, int pos, int max_seq,
+                             int n_layers, hipStream_t stream) {
+    QL_CHECK_ARG(n_layers > 0 && layer >= 0 && layer < n_layers && max_seq > 0);
+    QL_CHECK_ARG(n_tokens >= 0 && pos >= 0 && (long long)pos + n_tokens <= max_seq);
+    QL_CHECK_ARG(n_tokens == 0 || (k_cache && v_cache));
+    KvDst<D> kv{};
+    kv.kc = k_cache;
+    kv.vc = v_cache;
+    kv.pos0 = pos;
+    kv.max_seq = max_seq;
+    kv.v = v;
+    kv.vs = vs;
+    kv.layer = layer;
+    return rope_dispatch<D, kContigCache>(q, k, n_tokens, n_heads, n_kv_heads, head_dim, qs, ks,
+                                          positions, pos_offset, theta, pairing, kv, stream);
+}
+
+extern "C" hipError_t ql_rope_kv_append_f16(
+    uint16_t* q, uint16_t* k, const uint16_t* v, int n_tokens, int n_heads, int n_kv_heads,
+    int head_dim, int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
+    const int32_t* positions, int pos_offset, float theta, int pairing, uint16_t* k_cache,
+    uint16_t* v_cache, int layer, int pos, int max_seq, int n_layers, hipStream_t stream) {
+    return rope_contig_entry<_Float16>(
+        reinterpret_cast<_Float16*>(q), reinterpret_cast<_Float16*>(k),
+        reinterpret_cast<const _Float16*>(v), n_tokens, n_heads, n_kv_heads, head_dim,
+        q_row_stride, k_row_stride, v_row_stride, positions, pos_offset, theta, pairing,
+        reinterpret_cast<_Float16*>(k_cache), reinterpret_cast<_Float16*>(v_cache), layer, pos,
+        max_seq, n_layers, stream);
+}
+
+extern "C" hipError_t ql_rope_kv_append_f32(
+    float* q, float* k, const float* v, int n_tokens, int n_heads, int n_kv_heads, int head_dim,
+    int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride, const int32_t* positions,
+    int pos_offset, float theta, int pairing, float* k_cache, float* v_cache, int layer, int pos,
+    int max_seq, int n_layers, hipStream_t stream) {
+    return rope_contig_entry<float>(q, k, v, n_tokens, n_heads, n_kv_heads, head_dim,
+                                    q_row_stride, k_row_stride, v_row_stride, positions,
+                                    pos_offset, theta, pairing, k_cache, v_cache, layer, pos,
+                                    max_seq, n_layers, stream);
 }

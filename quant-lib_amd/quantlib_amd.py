@@ -37,6 +37,12 @@ SIGNATURES = {
     "ql_add_f16": [_p, _p, _i64, _p],
     "ql_rope_f32": [_p, _p, _i, _i, _i, _i, _i64, _i64, _p, _i, _f, _i, _p],
     "ql_rope_f16": [_p, _p, _i, _i, _i, _i, _i64, _i64, _p, _i, _f, _i, _p],
+    "ql_rope_paged_kv_append_f16": [_p, _p, _p, _i, _i, _i, _i, _i64, _i64, _i64, _p, _i, _f, _i,
+                                    _p, _p, _i, _p, _i, _i, _p],
+    "ql_rope_kv_append_f16": [_p, _p, _p, _i, _i, _i, _i, _i64, _i64, _i64, _p, _i, _f, _i, _p, _p,
+                              _i, _i, _i, _i, _p],
+    "ql_rope_kv_append_f32": [_p, _p, _p, _i, _i, _i, _i, _i64, _i64, _i64, _p, _i, _f, _i, _p, _p,
+                              _i, _i, _i, _i, _p],
     "ql_swiglu_f32": [_p, _p, _p, _i, _i, _p],
     "ql_swiglu_f16": [_p, _p, _p, _i, _i, _p],
     "ql_softmax_f32": [_p, _p, _i, _i, _p],

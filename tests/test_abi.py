@@ -102,6 +102,17 @@ P = 4096  # a non-null, 16-byte aligned dummy address: never dereferenced on the
     (("ql_paged_kv_append_f16", P, P, 4, P, P, P, 10, 4, 4, 8, 128, None), INVALID),  # layer
     (("ql_paged_kv_append_f16", P, None, 4, P, P, P, 10, 0, 4, 8, 128, None), INVALID),
     (("ql_f16_to_f32", P, P, -1, None), INVALID),
+    # fused RoPE + append: v missing, layer out of range, v stride too small, pos+T > max_seq
+    (("ql_rope_paged_kv_append_f16", P, P, None, 4, 8, 2, 64, 512, 128, 128, None, 0, 1e4, 1,
+      P, P, 4, P, 0, 2, None), INVALID),
+    (("ql_rope_paged_kv_append_f16", P, P, P, 4, 8, 2, 64, 512, 128, 128, None, 0, 1e4, 1,
+      P, P, 4, P, 2, 2, None), INVALID),
+    (("ql_rope_kv_append_f16", P, P, P, 4, 8, 2, 64, 512, 128, 64, None, 0, 1e4, 1,
+      P, P, 0, 0, 16, 2, None), INVALID),
+    (("ql_rope_kv_append_f32", P, P, P, 4, 8, 2, 64, 512, 128, 128, None, 0, 1e4, 1,
+      P, P, 0, 14, 16, 2, None), INVALID),
+    (("ql_rope_kv_append_f32", P, P, P, 0, 8, 2, 64, 512, 128, 128, None, 0, 1e4, 1,
+      P, P, 0, 3, 16, 2, None), 0),
 ])
 def test_argument_validation(call, expect):
     name, *args = call

@@ -428,3 +428,98 @@ def test_f16_to_f32_bit_exact(n):
     nan = np.isnan(want)
     assert np.array_equal(np.isnan(got), nan)
     assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+# ---- fused RoPE + KV-cache append ----------------------------------------------------------
+def _pool(nb, blk, misalign=0):
+    """Paged pool of nb blocks (+ slack for a misaligned table) and its device pointer table."""
+    pool = empty((nb * blk + 16,), np.uint16, fill_bits=GUARD_BYTE)
+    ptrs = dev(np.array([pool.ptr + 2 * misalign + 2 * blk * b for b in range(nb)], np.int64))
+    return pool, ptrs
+
+
+@pytest.mark.parametrize("pairing", [ql.ROPE_HALF, ql.ROPE_INTERLEAVED])
+@pytest.mark.parametrize("T,H,HK,d,misalign", [(8192, 32, 8, 128, 0), (37, 4, 2, 64, 0),
+                                               (20, 3, 1, 96, 0), (45, 4, 2, 64, 1)])
+def test_rope_paged_kv_append_fused(pairing, T, H, HK, d, misalign):
+    # One launch == ql_rope_f16 then ql_paged_kv_append_f16, bit for bit; and
+    # both agree with the oracle (C5 shape: Q 32x128, K/V 8x128, theta 5e5).
+    L, layer, theta = 4, 2, 5e5
+    nb = (T + 15) // 16 + 2
+    blk = L * 16 * HK * d
+    r = np.random.default_rng(T + d)
+    q = _f16(normal(T, (T, H * d)))
+    k = _f16(normal(T + 1, (T, HK * d)))
+    v = _f16(normal(T + 2, (T, HK * d)))
+    order = r.permutation(nb)
+    slots = np.array([order[t // 16] * 16 + t % 16 for t in range(T)], np.int32)
+    slots[T // 3] = -1
+    dsl, dv = dev(slots), dev(v)
+    # fused
+    q1, k1 = dev(q), dev(k)
+    kp1, kb1 = _pool(nb, blk, misalign)
+    vp1, vb1 = _pool(nb, blk, misalign)
+    ql.call("ql_rope_paged_kv_append_f16", q1.ptr, k1.ptr, dv.ptr, T, H, HK, d, H * d, HK * d,
+            HK * d, None, 0, theta, pairing, kb1.ptr, vb1.ptr, nb, dsl.ptr, layer, L, stream())
+    # two steps
+    q2, k2 = dev(q), dev(k)
+    kp2, kb2 = _pool(nb, blk, misalign)
+    vp2, vb2 = _pool(nb, blk, misalign)
+    ql.call("ql_rope_f16", q2.ptr, k2.ptr, T, H, HK, d, H * d, HK * d, None, 0, theta, pairing,
+            stream())
+    ql.call("ql_paged_kv_append_f16", kb2.ptr, vb2.ptr, nb, dsl.ptr, k2.ptr, dv.ptr, T, layer, L,
+            HK, d, stream())
+    gq, gk = host(q1, shape=(T, H * d)), host(k1, shape=(T, HK * d))
+    assert np.array_equal(gq, host(q2, shape=(T, H * d)))
+    assert np.array_equal(gk, host(k2, shape=(T, HK * d)))
+    assert np.array_equal(host(kp1), host(kp2)) and np.array_equal(host(vp1), host(vp2))
+    # oracle: rotation within tolerance; cache rows are exact copies of the rotated K and V
+    check_f16(gq, orc.rope(q, H, d, theta, pairing, f16=True), "fused rope q")
+    check_f16(gk, orc.rope(k, HK, d, theta, pairing, f16=True), "fused rope k")
+    wk = np.full(nb * blk + 16, 0xA5A5, np.uint16)
+    wv = wk.copy()
+    offs = (np.arange(nb) * blk + misalign).astype(np.int64)
+    orc.paged_kv_append_inplace(wk, wv, offs, slots, gk, v, layer, L, HK, d)
+    assert np.array_equal(host(kp1), wk) and np.array_equal(host(vp1), wv)
+
+
+@pytest.mark.parametrize("f16", [True, False])
+@pytest.mark.parametrize("pairing", [ql.ROPE_HALF, ql.ROPE_INTERLEAVED])
+@pytest.mark.parametrize("T,H,HK,d", [(300, 8, 2, 128), (33, 4, 4, 64), (17, 2, 1, 6)])
+def test_rope_kv_append_fused_contiguous_from_fused_qkv(f16, pairing, T, H, HK, d):
+    # Q, K, V are views into one fused [T, (H + 2*HK)*d] QKV buffer (strided rows);
+    # the cache is [L, S, HK, d], tokens written at positions pos..pos+T-1.
+    L, S, layer, pos, theta = 3, T + 40, 1, 25, 1e4
+    row = (H + 2 * HK) * d
+    qkv = normal(T * d, (T, row))
+    if f16:
+        qkv = _f16(qkv)
+    dt = np.uint16 if f16 else np.float32
+    esz = np.dtype(dt).itemsize
+    base = dev(qkv)
+    qp, kp, vp = base.ptr, base.ptr + H * d * esz, base.ptr + (H + HK) * d * esz
+    n = L * S * HK * d
+    kc, vc = Out(n, dt), Out(n, dt)
+    name = "ql_rope_kv_append_f16" if f16 else "ql_rope_kv_append_f32"
+    ql.call(name, qp, kp, vp, T, H, HK, d, row, row, row, None, pos, theta, pairing, kc.ptr, vc.ptr,
+            layer, pos, S, L, stream())
+    got = host(base, shape=(T, row))
+    # reference: contiguous copies through the two separate entry points
+    qc, kc2, vc2 = (np.ascontiguousarray(qkv[:, :H * d]), np.ascontiguousarray(qkv[:, H * d:(H + HK) * d]),
+                    np.ascontiguousarray(qkv[:, (H + HK) * d:]))
+    dq, dk, dvv = dev(qc), dev(kc2), dev(vc2)
+    ql.call("ql_rope_f16" if f16 else "ql_rope_f32", dq.ptr, dk.ptr, T, H, HK, d, H * d, HK * d,
+            None, pos, theta, pairing, stream())
+    kref, vref = Out(n, dt), Out(n, dt)
+    ql.call("ql_kv_append_f16" if f16 else "ql_kv_append_f32", kref.ptr, vref.ptr, dk.ptr, dvv.ptr,
+            layer, pos, T, HK, d, S, L, stream())
+    assert np.array_equal(got[:, :H * d], host(dq, shape=(T, H * d)))
+    assert np.array_equal(got[:, H * d:(H + HK) * d], host(dk, shape=(T, HK * d)))
+    assert np.array_equal(got[:, (H + HK) * d:], qkv[:, (H + HK) * d:])  # V untouched
+    assert np.array_equal(kc.get(), kref.get()) and np.array_equal(vc.get(), vref.get())
+    # and against the oracle
+    wq = orc.rope(qc, H, d, theta, pairing, pos_offset=pos, f16=f16)
+    if f16:
+        check_f16(got[:, :H * d], wq, "fused contiguous q")
+    else:
+        check_abs(got[:, :H * d], wq, ATOL_ROPE_F32, "fused contiguous q")
