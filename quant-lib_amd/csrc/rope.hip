@@ -274,6 +274,166 @@ inline bool rows_aligned16(const void* p, int64_t stride_bytes) {
     return !p || (qlh::aligned16(p) && stride_bytes % 16 == 0);
 }
 
+// Plane kernel for the common head sizes (HD = 64 or 128, compile time):
+// blockIdx.y selects the plane -- Q, K or (fused variants) V -- and a group of
+// its heads, so every branch on the head type is uniform over the workgroup and
+// all address arithmetic is shifts.  V planes only copy into the cache and
+// skip the trig.  Groups: gq over Q, gk over K, gk over V.
+template <typename D, int PAIRING, int HD, int MAXU, int CACHE>
+__global__ __launch_bounds__(kBlock) void rope_planes(D* q, D* k, int n_tokens, int hq, int hk,
+                                                      long long qs, long long ks,
+                                                      const int32_t* __restrict__ positions,
+                                                      int pos_offset, InvFreq inv, int gq, int gk,
+                                                      int hpw_q, int hpw_k, KvDst<D> kv) {
+    constexpr int W = vec16<D>();
+    constexpr bool HALF = PAIRING == QL_ROPE_HALF;
+    constexpr int NP = HD / 2;                                  // pairs per head
+    constexpr int PPS = HALF ? W : W / 2;                       // pairs per slot
+    constexpr int S = NP / PPS;                                 // slots per head
+    static_assert(S >= 1 && 64 % S == 0, "head chunks must tile a wavefront");
+    using V = Vec<D, W>;
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int t = blockIdx.x * (kBlock / kWave) + (threadIdx.x / kWave);
+    if (t >= n_tokens) return;  // wavefront-uniform; no barriers below
+    const int j = lane % S;
+
+    // plane and head range of this workgroup (uniform)
+    const int gy = blockIdx.y;
+    const int plane = gy < gq ? 0 : (gy < gq + gk ? 1 : 2);    // 0 Q, 1 K, 2 V
+    const int g = plane == 0 ? gy : (plane == 1 ? gy - gq : gy - gq - gk);
+    const int hpw = plane == 0 ? hpw_q : hpw_k;
+    const int nh = plane == 0 ? hq : hk;
+    const int h0 = g * hpw;
+    const int h1 = min(nh, h0 + hpw);
+    const int nslots = (h1 - h0) * S;
+    D* row = plane == 0 ? q + (long long)t * qs
+           : (plane == 1 ? k + (long long)t * ks : const_cast<D*>(kv.v) + (long long)t * kv.vs);
+
+    V lo[MAXU];
+    V hi[HALF ? MAXU : 1];
+#pragma unroll
+    for (int u = 0; u < MAXU; ++u) {
+        const int sl = lane + u * kWave;
+        if (sl < nslots) {
+            const V* p = reinterpret_cast<const V*>(row + (h0 + sl / S) * HD + j * W);
+            lo[u] = load<true>(p);
+            if constexpr (HALF) hi[u] = load<true>(reinterpret_cast<const V*>(reinterpret_cast<const D*>(p) + NP));
+        }
+    }
+
+    D* kd = nullptr;
+    D* vd = nullptr;
+    bool cache_aligned = true;
+    if constexpr (CACHE != kNoCache) {
+        if (plane != 0) {
+            cache_rows<D, CACHE>(kv, t, hk * HD, kd, vd);
+            cache_aligned = ((reinterpret_cast<uintptr_t>(kd) | reinterpret_cast<uintptr_t>(vd)) & 15) == 0;
+        }
+        if (plane == 2) {  // V: copy the rows into the cache, no rotation
+            if (vd) {
+#pragma unroll
+                for (int u = 0; u < MAXU; ++u) {
+                    const int sl = lane + u * kWave;
+                    if (sl < nslots) {
+                        D* dst = vd + (h0 + sl / S) * HD + j * W;
+                        store_cache<D>(dst, lo[u], cache_aligned);
+                        if constexpr (HALF) store_cache<D>(dst + NP, hi[u], cache_aligned);
+                    }
+                }
+            }
+            return;
+        }
+    }
+
+    const int pos = positions ? positions[t] : pos_offset + t;
+    float c_own, s_own;
+    trig((float)pos * inv.v[lane % NP], c_own, s_own);
+    float c[PPS], s[PPS];
+#pragma unroll
+    for (int e = 0; e < PPS; ++e) {
+        c[e] = __shfl(c_own, j * PPS + e, kWave);
+        s[e] = __shfl(s_own, j * PPS + e, kWave);
+    }
+
+#pragma unroll
+    for (int u = 0; u < MAXU; ++u) {
+        const int sl = lane + u * kWave;
+        if (sl >= nslots) continue;
+        const int off = (h0 + sl / S) * HD + j * W;
+        V ylo, yhi;
+        if constexpr (!HALF) {
+#pragma unroll
+            for (int e = 0; e < PPS; ++e) {
+                float y0, y1;
+                rotate(to_f32(lo[u].v[2 * e]), to_f32(lo[u].v[2 * e + 1]), c[e], s[e], y0, y1);
+                ylo.v[2 * e] = from_f32<D>(y0);
+                ylo.v[2 * e + 1] = from_f32<D>(y1);
+            }
+            store<true>(reinterpret_cast<V*>(row + off), ylo);
+        } else {
+#pragma unroll
+            for (int e = 0; e < PPS; ++e) {
+                float y0, y1;
+                rotate(to_f32(lo[u].v[e]), to_f32(hi[u].v[e]), c[e], s[e], y0, y1);
+                ylo.v[e] = from_f32<D>(y0);
+                yhi.v[e] = from_f32<D>(y1);
+            }
+            store<true>(reinterpret_cast<V*>(row + off), ylo);
+            store<true>(reinterpret_cast<V*>(row + off + NP), yhi);
+        }
+        if constexpr (CACHE != kNoCache) {
+            if (plane == 1 && kd) {
+                store_cache<D>(kd + off, ylo, cache_aligned);
+                if constexpr (HALF) store_cache<D>(kd + off + NP, yhi, cache_aligned);
+            }
+        }
+    }
+}
+
+// Launch the plane kernel: groups per plane chosen so a lane owns at most
+// MAXU chunks and there are enough wavefronts to fill the device.
+template <typename D, int PAIRING, int HD, int CACHE>
+hipError_t launch_planes(D* q, D* k, int n_tokens, int hq, int hk, long long qs, long long ks,
+                         const int32_t* positions, int pos_offset, const InvFreq& inv,
+                         const KvDst<D>& kv, hipStream_t stream) {
+    constexpr int W = vec16<D>();
+    constexpr int S = (HD / 2) / (PAIRING == QL_ROPE_HALF ? W : W / 2);
+    // a rotate-half slot is two 16-byte chunks, an interleaved slot one: keep
+    // 2 KiB per lane-set in flight either way
+    constexpr int MAXU = PAIRING == QL_ROPE_HALF ? 2 : 4;
+    const int hcap = (kWave * MAXU) / S;  // heads per wavefront at most
+    const int hpw_q = hq > 0 ? (hq < hcap ? hq : hcap) : 1;
+    const int hpw_k = hk > 0 ? (hk < hcap ? hk : hcap) : 1;
+    const int gq = hq > 0 ? (hq + hpw_q - 1) / hpw_q : 0;
+    const int gk = hk > 0 ? (hk + hpw_k - 1) / hpw_k : 0;
+    const int gy = gq + gk + (CACHE != kNoCache ? gk : 0);
+    const unsigned gx = qlh::blocks_for(n_tokens, kBlock / kWave);
+    hipLaunchKernelGGL((rope_planes<D, PAIRING, HD, MAXU, CACHE>), dim3(gx, gy), dim3(kBlock), 0,
+                       stream, q, k, n_tokens, hq, hk, qs, ks, positions, pos_offset, inv, gq, gk,
+                       hpw_q, hpw_k, kv);
+    return hipGetLastError();
+}
+
+template <typename D, int CACHE>
+hipError_t launch_planes_hd(int d, int pairing, D* q, D* k, int n_tokens, int hq, int hk,
+                            long long qs, long long ks, const int32_t* positions, int pos_offset,
+                            const InvFreq& inv, const KvDst<D>& kv, hipStream_t stream) {
+    if (d == 128) {
+        if (pairing == QL_ROPE_HALF)
+            return launch_planes<D, QL_ROPE_HALF, 128, CACHE>(q, k, n_tokens, hq, hk, qs, ks,
+                                                              positions, pos_offset, inv, kv, stream);
+        return launch_planes<D, QL_ROPE_INTERLEAVED, 128, CACHE>(q, k, n_tokens, hq, hk, qs, ks,
+                                                                 positions, pos_offset, inv, kv,
+                                                                 stream);
+    }
+    if (pairing == QL_ROPE_HALF)
+        return launch_planes<D, QL_ROPE_HALF, 64, CACHE>(q, k, n_tokens, hq, hk, qs, ks, positions,
+                                                         pos_offset, inv, kv, stream);
+    return launch_planes<D, QL_ROPE_INTERLEAVED, 64, CACHE>(q, k, n_tokens, hq, hk, qs, ks,
+                                                            positions, pos_offset, inv, kv, stream);
+}
+
 constexpr int kRopeMaxU = 4;        // chunks (or chunk pairs) per lane
 constexpr int kRopeTargetWaves = 16384;
 
@@ -309,6 +469,9 @@ hipError_t rope_dispatch(D* q, D* k, int n_tokens, int hq, int hk, int d, int64_
     if (tile_ok && align_ok) {
         InvFreq inv;
         for (int i = 0; i < 64; ++i) inv.v[i] = i < npairs ? host_inv_freq(i, d, theta) : 0.0f;
+        if (d == 64 || d == 128)
+            return launch_planes_hd<D, CACHE>(d, pairing, q, k, n_tokens, hq, hk, (long long)qs,
+                                              (long long)ks, positions, pos_offset, inv, kv, stream);
         // Heads per wavefront: at most 64*kRopeMaxU chunks per wavefront, and
         // split further while tokens alone give fewer than kRopeTargetWaves.
         const int htot = hq + hk + (CACHE != kNoCache ? hk : 0);
