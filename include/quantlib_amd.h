@@ -204,6 +204,48 @@ hipError_t ql_paged_slot_mapping(const int32_t* block_table, int n_table, int st
 /* ---- fp16 -> fp32 widening (launch_fp16_to_fp32, kernels/fp16_ops.cu:103-110,149-153) */
 hipError_t ql_f16_to_f32(const uint16_t* src, float* dst, int64_t n, hipStream_t stream);
 
+/* ---- attention (fp16 I/O, fp32 softmax state, gfx950 matrix cores) ----------------
+ * out[i, h, :] = sum_j softmax_j((q[i,h,:] . k[j,g,:]) * scale) v[j,g,:] with
+ * g = h * n_kv_heads / n_heads (grouped-query heads, kernels/flash_attention.cu:45),
+ * scale = 1/sqrtf(head_dim) (:173), normalised as O / (l + 1e-8) (:161).  Causal:
+ * key j is visible to query i when j <= its position.  head_dim must be 64 or 128;
+ * rows 16-byte aligned (strides multiples of 8 elements). */
+
+/* Replaces launch_flash_attention (kernels/flash_attention.cu:169-182): Q, out
+ * [seq_len, n_heads, head_dim]; K, V [seq_len, n_kv_heads, head_dim], query i at
+ * position i.  (The reference's tiles hold head_dim <= 64 only.) */
+hipError_t ql_flash_attention_f16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                  uint16_t* out, int seq_len, int n_heads, int n_kv_heads,
+                                  int head_dim, int causal, hipStream_t stream);
+
+/* General contiguous form: the q_len queries are the LAST q_len positions of the
+ * kv_len keys (query i sits at kv_len - q_len + i).  Decode against the contiguous
+ * cache of src/fp16_forward.cu:202-209 is q_len = 1, kv_len = pos + 1,
+ * k = k_cache + layer*max_seq*n_kv_heads*head_dim, kv_row_stride = n_kv_heads*head_dim
+ * (the reference passes its one-token Q with seq_len = ctx_len and so reads past it). */
+hipError_t ql_attention_f16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                            uint16_t* out, int q_len, int kv_len, int n_heads, int n_kv_heads,
+                            int head_dim, int64_t q_row_stride, int64_t kv_row_stride,
+                            int64_t out_row_stride, int causal, hipStream_t stream);
+
+/* Attention over the paged KV cache (pool layout of src/paged_kvcache.cu:26-46, the
+ * layout ql_paged_kv_append_f16 writes), for n_seqs sequences at once.  Device
+ * arrays: cu_q_lens[n_seqs+1] (sequence s owns query rows cu_q_lens[s] ..
+ * cu_q_lens[s+1]-1 of q/out, all < n_q_rows), ctx_lens[n_seqs] (its keys,
+ * including the new ones), block_tables[n_seqs * max_blocks_per_seq] (logical ->
+ * physical block, include/scheduler.h:17-19).  max_q_len bounds every sequence's
+ * query count (host value: it sizes the grid).  A sequence whose rows fall outside
+ * [0, n_q_rows) is skipped; a table entry outside [0, n_blocks) reads as zero
+ * keys.  Decode = one query row per sequence. */
+hipError_t ql_paged_attention_f16(const uint16_t* q, uint16_t* out, int64_t q_row_stride,
+                                  int64_t out_row_stride, int n_q_rows, int n_seqs,
+                                  const int32_t* cu_q_lens, const int32_t* ctx_lens,
+                                  int max_q_len, const int32_t* block_tables,
+                                  int max_blocks_per_seq, const uint16_t* const* k_blocks,
+                                  const uint16_t* const* v_blocks, int n_blocks, int layer,
+                                  int n_layers, int n_heads, int n_kv_heads, int head_dim,
+                                  int causal, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -44,6 +44,10 @@ _SIGS = {
     "or_kv_append_f32": ([_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i], None),
     "or_kv_append_f16": ([_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i], None),
     "or_paged_kv_append_f16": ([_p, _p, _p, _i, _p, _p, _p, _i, _i, _i, _i, _i], None),
+    "or_attention_f32": ([_p, _p, _p, _p, _i, _i, _i, _i, _i, _i64, _i64, _i64, _i], None),
+    "or_attention_f16": ([_p, _p, _p, _p, _i, _i, _i, _i, _i, _i64, _i64, _i64, _i], None),
+    "or_attention_reftest_cpu": ([_p, _p, _p, _p, _i, _i, _i], None),
+    "or_reftest_attention_inputs": ([_p, _p, _p, _i64, ctypes.c_uint], None),
 }
 
 _lib = None
@@ -210,3 +214,33 @@ def paged_kv_append_inplace(k_pool, v_pool, block_offset, slots, k_new, v_new, l
     lib().or_paged_kv_append_f16(_ptr(k_pool), _ptr(v_pool), _ptr(block_offset), block_offset.size,
                                  _ptr(slots), _ptr(k_new), _ptr(v_new), slots.size, layer,
                                  n_layers, n_kv_heads, head_dim)
+
+
+def attention(q, k, v, n_heads: int, n_kv_heads: int, causal: bool, f16: bool = False) -> np.ndarray:
+    """q: [q_len, n_heads, d]; k, v: [kv_len, n_kv_heads, d] (contiguous).  The
+    q_len queries are the last q_len positions of the kv_len keys."""
+    conv = _u16 if f16 else _f32
+    q, k, v = conv(q), conv(k), conv(v)
+    q_len, kv_len, d = q.shape[0], k.shape[0], q.shape[-1]
+    q2 = q.reshape(q_len, n_heads * d)
+    out = np.zeros_like(q2)
+    fn = lib().or_attention_f16 if f16 else lib().or_attention_f32
+    fn(_ptr(q2), _ptr(k), _ptr(v), _ptr(out), q_len, kv_len, n_heads, n_kv_heads, d,
+       n_heads * d, n_kv_heads * d, n_heads * d, int(causal))
+    return out.reshape(q.shape)
+
+
+def attention_reftest_cpu(q, k, v, n_heads: int) -> np.ndarray:
+    """tests/test_attention.cu:22-56 (fp32 loop, MHA, no mask)."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    out = np.zeros_like(q)
+    lib().or_attention_reftest_cpu(_ptr(q), _ptr(k), _ptr(v), _ptr(out), q.shape[0], n_heads,
+                                   q.shape[-1])
+    return out
+
+
+def reftest_attention_inputs(seq_len: int, n_heads: int, head_dim: int, seed: int = 99):
+    n = seq_len * n_heads * head_dim
+    q, k, v = (np.empty((seq_len, n_heads, head_dim), np.float32) for _ in range(3))
+    lib().or_reftest_attention_inputs(_ptr(q), _ptr(k), _ptr(v), n, seed)
+    return q, k, v

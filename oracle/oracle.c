@@ -381,3 +381,131 @@ void or_paged_kv_append_f16(uint16_t* k_pool, uint16_t* v_pool, const int64_t* b
         }
     }
 }
+
+/* ---- attention -----------------------------------------------------------------------
+ * kernels/flash_attention.cu:29-182 (fp16 flash attention) and
+ * kernels/attention.cu:14-97 / tests/test_attention.cu:22-56 (fp32 SDPA):
+ *   s_j  = (q . k_j) * scale, scale = 1/sqrtf(head_dim) (flash_attention.cu:173)
+ *   kv head of query head h = h * n_kv_heads / n_heads        (flash_attention.cu:45)
+ *   causal: key j is masked when j > the query's position     (flash_attention.cu:106)
+ *   out  = sum_j e^(s_j - max) v_j / (sum_j e^(s_j - max) + 1e-8)   (:161)
+ * Generalised as the kernels are: the q_len queries are the last q_len
+ * positions of a kv_len-long context (query i sits at kv_len - q_len + i), rows
+ * are strided.  Dot products, exponentials and sums in double; a query with no
+ * visible key gives 0 (0 / 1e-8), as in the reference.
+ * Pinned by: closed forms (identical keys -> mean of the visible V rows; causal
+ * query 0 -> V[0]; two keys with a known score gap -> the logistic weight;
+ * one dominant key -> its V row; the GQA head map via head-distinct V) and the
+ * reference's own test (tests/test_attention.cu:77-141: srand(99) U(-0.5,0.5)
+ * [128, 32, 128], max abs error < 1e-3 against its fp32 CPU loop, restated as
+ * or_attention_reftest_cpu) (tests/test_oracle.py::test_attention_*). */
+void or_attention_f32(const float* q, const float* k, const float* v, float* out, int q_len,
+                      int kv_len, int n_heads, int n_kv_heads, int head_dim, int64_t q_stride,
+                      int64_t kv_stride, int64_t o_stride, int causal) {
+    const double scale = (double)(1.0f / sqrtf((float)head_dim));
+    double* e = (double*)malloc(sizeof(double) * (size_t)(kv_len > 0 ? kv_len : 1));
+    double* acc = (double*)malloc(sizeof(double) * (size_t)head_dim);
+    for (int i = 0; i < q_len; ++i) {
+        const long pos = (long)kv_len - q_len + i;
+        long nk = kv_len;
+        if (causal) nk = pos + 1 < kv_len ? pos + 1 : kv_len;
+        if (nk < 0) nk = 0;
+        for (int h = 0; h < n_heads; ++h) {
+            const int kvh = (int)(((long long)h * n_kv_heads) / n_heads);
+            const float* qr = q + (size_t)i * q_stride + (size_t)h * head_dim;
+            double mx = -DBL_MAX;
+            for (long j = 0; j < nk; ++j) {
+                const float* kr = k + (size_t)j * kv_stride + (size_t)kvh * head_dim;
+                double dot = 0.0;
+                for (int d = 0; d < head_dim; ++d) dot += (double)qr[d] * (double)kr[d];
+                e[j] = dot * scale;
+                if (e[j] > mx) mx = e[j];
+            }
+            double l = 0.0;
+            for (long j = 0; j < nk; ++j) {
+                e[j] = exp(e[j] - mx);
+                l += e[j];
+            }
+            for (int d = 0; d < head_dim; ++d) acc[d] = 0.0;
+            for (long j = 0; j < nk; ++j) {
+                const float* vr = v + (size_t)j * kv_stride + (size_t)kvh * head_dim;
+                for (int d = 0; d < head_dim; ++d) acc[d] += e[j] * (double)vr[d];
+            }
+            float* orow = out + (size_t)i * o_stride + (size_t)h * head_dim;
+            for (int d = 0; d < head_dim; ++d) orow[d] = (float)(acc[d] / (l + 1e-8));
+        }
+    }
+    free(e);
+    free(acc);
+}
+
+static float* widen_rows(const uint16_t* src, int rows, int64_t stride, int width) {
+    float* f = (float*)malloc(sizeof(float) * ((size_t)(rows > 0 ? rows : 1) * (size_t)stride));
+    for (int r = 0; r < rows; ++r)
+        for (int c = 0; c < width; ++c)
+            f[(size_t)r * stride + c] = or_f16_to_f32(src[(size_t)r * stride + c]);
+    return f;
+}
+
+/* fp16 inputs widened exactly, the same double computation, then the fp32
+ * result rounded to binary16 (RNE). */
+void or_attention_f16(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out,
+                      int q_len, int kv_len, int n_heads, int n_kv_heads, int head_dim,
+                      int64_t q_stride, int64_t kv_stride, int64_t o_stride, int causal) {
+    float* qf = widen_rows(q, q_len, q_stride, n_heads * head_dim);
+    float* kf = widen_rows(k, kv_len, kv_stride, n_kv_heads * head_dim);
+    float* vf = widen_rows(v, kv_len, kv_stride, n_kv_heads * head_dim);
+    float* of = (float*)malloc(sizeof(float) * ((size_t)(q_len > 0 ? q_len : 1) * (size_t)o_stride));
+    or_attention_f32(qf, kf, vf, of, q_len, kv_len, n_heads, n_kv_heads, head_dim, q_stride,
+                     kv_stride, o_stride, causal);
+    for (int r = 0; r < q_len; ++r)
+        for (int c = 0; c < n_heads * head_dim; ++c)
+            out[(size_t)r * o_stride + c] = or_f32_to_f16(of[(size_t)r * o_stride + c]);
+    free(qf);
+    free(kf);
+    free(vf);
+    free(of);
+}
+
+/* The reference test's own CPU loop (tests/test_attention.cu:22-56): fp32
+ * sequential dot products and sums, no causal mask, n_heads K/V heads. */
+void or_attention_reftest_cpu(const float* Q, const float* K, const float* V, float* out,
+                              int seq_len, int n_heads, int head_dim) {
+    const float scale = 1.0f / sqrtf((float)head_dim);
+    float* sc = (float*)malloc(sizeof(float) * (size_t)seq_len);
+    const size_t rs = (size_t)n_heads * head_dim;
+    for (int i = 0; i < seq_len; ++i)
+        for (int h = 0; h < n_heads; ++h) {
+            float mx = -FLT_MAX;
+            for (int j = 0; j < seq_len; ++j) {
+                float dot = 0.0f;
+                for (int d = 0; d < head_dim; ++d)
+                    dot += Q[i * rs + (size_t)h * head_dim + d] * K[j * rs + (size_t)h * head_dim + d];
+                sc[j] = dot * scale;
+                if (sc[j] > mx) mx = sc[j];
+            }
+            float s = 0.0f;
+            for (int j = 0; j < seq_len; ++j) {
+                sc[j] = expf(sc[j] - mx);
+                s += sc[j];
+            }
+            for (int j = 0; j < seq_len; ++j) sc[j] /= s;
+            for (int d = 0; d < head_dim; ++d) {
+                float a = 0.0f;
+                for (int j = 0; j < seq_len; ++j) a += sc[j] * V[j * rs + (size_t)h * head_dim + d];
+                out[i * rs + (size_t)h * head_dim + d] = a;
+            }
+        }
+    free(sc);
+}
+
+/* Inputs of tests/test_attention.cu:77-82: srand(seed); per element i, in this
+ * order, Q[i], K[i], V[i] = rand()/RAND_MAX - 0.5. */
+void or_reftest_attention_inputs(float* q, float* k, float* v, int64_t n, unsigned seed) {
+    srand(seed);
+    for (int64_t i = 0; i < n; ++i) {
+        q[i] = (float)rand() / RAND_MAX - 0.5f;
+        k[i] = (float)rand() / RAND_MAX - 0.5f;
+        v[i] = (float)rand() / RAND_MAX - 0.5f;
+    }
+}

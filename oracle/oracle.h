@@ -81,6 +81,19 @@ void or_paged_kv_append_f16(uint16_t* k_pool, uint16_t* v_pool, const int64_t* b
                             const uint16_t* v_new, int n_tokens, int layer, int n_layers,
                             int n_kv_heads, int head_dim);
 
+/* Attention (fp32 / fp16 I/O, double inside): queries are the last q_len
+ * positions of a kv_len-long context; kv head of head h = h*n_kv_heads/n_heads. */
+void or_attention_f32(const float* q, const float* k, const float* v, float* out, int q_len,
+                      int kv_len, int n_heads, int n_kv_heads, int head_dim, int64_t q_stride,
+                      int64_t kv_stride, int64_t o_stride, int causal);
+void or_attention_f16(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out,
+                      int q_len, int kv_len, int n_heads, int n_kv_heads, int head_dim,
+                      int64_t q_stride, int64_t kv_stride, int64_t o_stride, int causal);
+/* The reference test's fp32 CPU loop and inputs (tests/test_attention.cu:22-56, 77-82). */
+void or_attention_reftest_cpu(const float* Q, const float* K, const float* V, float* out,
+                              int seq_len, int n_heads, int head_dim);
+void or_reftest_attention_inputs(float* q, float* k, float* v, int64_t n, unsigned seed);
+
 #ifdef __cplusplus
 }
 #endif

@@ -78,6 +78,14 @@ void launch_fp16_to_fp32(const __half* src, float* dst, int n, hipStream_t strea
     (void)ql_f16_to_f32(bits(src), dst, n, stream);
 }
 
+// kernels/flash_attention.cu:169-182
+void launch_flash_attention(const __half* Q, const __half* K, const __half* V, __half* Out,
+                            int seq_len, int n_heads, int n_kv_heads, int head_dim, int causal,
+                            hipStream_t stream) {
+    (void)ql_flash_attention_f16(bits(Q), bits(K), bits(V), bits(Out), seq_len, n_heads,
+                                 n_kv_heads, head_dim, causal, stream);
+}
+
 // src/forward.cu:128-135
 void add_residual(float* x, const float* d, int n, hipStream_t stream) {
     (void)ql_add_f32(x, d, n, stream);

@@ -126,3 +126,28 @@ def synchronize() -> None:
 
 def ptr(t) -> int:
     return t.ptr
+
+
+GUARD = 64          # elements of guard band on each side of every output
+GUARD_BYTE = 0xA5
+
+
+class Out:
+    """Device output buffer of n elements between two guard bands."""
+
+    def __init__(self, n, dtype, offset=0):
+        self.n, self.dtype, self.offset = n, dtype, offset
+        self.buf = empty((n + 2 * GUARD + offset,), dtype, fill_bits=GUARD_BYTE)
+        self.view = self.buf.window(GUARD + offset, n)
+
+    @property
+    def ptr(self):
+        return self.view.data_ptr()
+
+    def get(self, shape=None):
+        a = host(self.buf)
+        g0, g1 = a[:GUARD + self.offset], a[GUARD + self.offset + self.n:]
+        for g in (g0, g1):
+            assert np.all(g.view(np.uint8) == GUARD_BYTE), "write outside the output region"
+        v = a[GUARD + self.offset:GUARD + self.offset + self.n]
+        return v.reshape(shape) if shape is not None else v

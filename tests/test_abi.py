@@ -24,6 +24,7 @@ COMPAT_MANGLED = {
     "launch_fp16_embed": "_Z17launch_fp16_embedPK6__halfPS_iiP12ihipStream_t",
     "launch_fp16_add": "_Z15launch_fp16_addP6__halfPKS_iP12ihipStream_t",
     "launch_fp16_to_fp32": "_Z19launch_fp16_to_fp32PK6__halfPfiP12ihipStream_t",
+    "launch_flash_attention": "_Z22launch_flash_attentionPK6__halfS1_S1_PS_iiiiiP12ihipStream_t",
     "add_residual": "_Z12add_residualPfPKfiP12ihipStream_t",
     "launch_embed": "_Z12launch_embedPfPKfiiP12ihipStream_t",
     "launch_fp16_kvcache_append": "_Z26launch_fp16_kvcache_appendP6__halfS0_PKS_S2_iiiiiiP12ihipStream_t",
@@ -113,6 +114,25 @@ P = 4096  # a non-null, 16-byte aligned dummy address: never dereferenced on the
       P, P, 0, 14, 16, 2, None), INVALID),
     (("ql_rope_kv_append_f32", P, P, P, 0, 8, 2, 64, 512, 128, 128, None, 0, 1e4, 1,
       P, P, 0, 3, 16, 2, None), 0),
+    # attention: head_dim 96 unsupported, kv heads > heads, empty problem
+    (("ql_flash_attention_f16", P, P, P, P, 4, 8, 2, 96, 1, None), INVALID),
+    (("ql_flash_attention_f16", P, P, P, P, 4, 2, 8, 64, 1, None), INVALID),
+    (("ql_flash_attention_f16", None, None, None, None, 0, 8, 2, 64, 1, None), 0),
+    # q stride too small, stride not a multiple of 8, misaligned base, missing K
+    (("ql_attention_f16", P, P, P, P, 1, 9, 8, 2, 64, 500, 128, 512, 1, None), INVALID),
+    (("ql_attention_f16", P, P, P, P, 1, 9, 8, 2, 64, 516, 128, 512, 1, None), INVALID),
+    (("ql_attention_f16", P + 2, P, P, P, 1, 9, 8, 2, 64, 512, 128, 512, 1, None), INVALID),
+    (("ql_attention_f16", P, None, P, P, 1, 9, 8, 2, 64, 512, 128, 512, 1, None), INVALID),
+    (("ql_attention_f16", None, None, None, None, 0, 9, 8, 2, 64, 512, 128, 512, 1, None), 0),
+    # paged: layer out of range, head_dim 80, missing block tables, no sequences
+    (("ql_paged_attention_f16", P, P, 512, 512, 4, 2, P, P, 2, P, 4, P, P, 8, 2, 2, 8, 2, 64, 1,
+      None), INVALID),
+    (("ql_paged_attention_f16", P, P, 640, 640, 4, 2, P, P, 2, P, 4, P, P, 8, 0, 2, 8, 2, 80, 1,
+      None), INVALID),
+    (("ql_paged_attention_f16", P, P, 512, 512, 4, 2, P, P, 2, None, 4, P, P, 8, 0, 2, 8, 2, 64, 1,
+      None), INVALID),
+    (("ql_paged_attention_f16", None, None, 512, 512, 0, 0, None, None, 0, None, 0, None, None, 0,
+      0, 2, 8, 2, 64, 1, None), 0),
 ])
 def test_argument_validation(call, expect):
     name, *args = call

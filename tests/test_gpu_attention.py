@@ -1,0 +1,246 @@
+"""GPU parity of the fp16 attention entry points (ql_flash_attention_f16,
+ql_attention_f16, ql_paged_attention_f16 and the launch_flash_attention shim)
+against the CPU oracle (double-precision softmax . V) on the same seeded
+binary16 inputs.
+
+Tolerance, |got - want| <= RTOL_ATTN*|want| + ATOL_ATTN*max|V|: the kernel
+multiplies V by the probabilities rounded to binary16 (relative error <= 2^-11
+each; the row sum uses the same rounded values, so the output is a convex
+combination whose weights are off by <= 2^-10 relative, i.e. <= 2^-10*max|V|
+absolute), accumulates in fp32 and rounds the result to binary16 (2^-11
+relative).  Probabilities below the binary16 subnormal range add at most
+kv_len*2^-25 of weight, well inside the bound at these sizes.
+
+Paged and contiguous K/V run the same arithmetic, so their outputs must agree
+bit for bit.  At the C5 shape (8192 tokens, 32 query heads, 8 KV heads,
+head_dim 128, causal) the oracle checks sampled rows: query i of a causal
+prefill equals a one-query problem over keys 0..i."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle as orc
+import quantlib_amd as ql
+from helpers import (GUARD_BYTE, Out, check_close, dev, empty, f16_bits_to_f32, host, normal,
+                     ptr, stream, to_f16_bits)
+from test_abi import COMPAT_MANGLED
+
+pytestmark = pytest.mark.gpu
+
+RTOL_ATTN = 2e-3
+ATOL_ATTN = 2e-3   # times max|V|
+
+
+def check_attn(got, want, v, what):
+    vmax = float(np.abs(f16_bits_to_f32(v)).max()) if v.size else 1.0
+    return check_close(f16_bits_to_f32(got), f16_bits_to_f32(want), RTOL_ATTN,
+                       ATOL_ATTN * max(vmax, 1e-3), what)
+
+
+def qkv(seed, q_len, kv_len, h, hkv, d, q_sigma=1.0):
+    return (to_f16_bits(normal(seed, (q_len, h, d), q_sigma)),
+            to_f16_bits(normal(seed + 1, (kv_len, hkv, d))),
+            to_f16_bits(normal(seed + 2, (kv_len, hkv, d))))
+
+
+# ---- reference semantics (launch_flash_attention) -------------------------------------------
+@pytest.mark.parametrize("seq,h,hkv,d,causal,q_sigma", [
+    (1, 4, 2, 64, 1, 1.0), (7, 4, 1, 128, 1, 1.0), (64, 8, 2, 64, 0, 1.0),
+    (100, 32, 8, 128, 1, 1.0), (129, 6, 4, 64, 1, 3.0), (257, 4, 4, 128, 0, 3.0),
+    (300, 8, 8, 128, 1, 0.3), (513, 32, 8, 128, 1, 1.0), (200, 32, 4, 64, 1, 1.0)])
+def test_flash_attention_matches_oracle(seq, h, hkv, d, causal, q_sigma):
+    q, k, v = qkv(seq * 7 + d, seq, seq, h, hkv, d, q_sigma)
+    out = Out(seq * h * d, np.uint16)
+    dq, dk, dv = dev(q), dev(k), dev(v)
+    ql.call("ql_flash_attention_f16", ptr(dq), ptr(dk), ptr(dv), out.ptr, seq, h, hkv, d, causal,
+            stream())
+    want = orc.attention(q, k, v, h, hkv, bool(causal), f16=True)
+    check_attn(out.get((seq, h, d)), want, v, f"flash attention seq={seq} h={h}/{hkv} d={d}")
+
+
+def test_flash_attention_passes_reference_test():
+    # tests/test_attention.cu:60-141: srand(99) U(-0.5,0.5) [128, 32, 128], no mask,
+    # max abs error < 1e-3 against its fp32 CPU loop (inputs here rounded to binary16)
+    seq, h, d = 128, 32, 128
+    q, k, v = orc.reftest_attention_inputs(seq, h, d, 99)
+    qb, kb, vb = to_f16_bits(q), to_f16_bits(k), to_f16_bits(v)
+    out = Out(seq * h * d, np.uint16)
+    dq, dk, dv = dev(qb), dev(kb), dev(vb)
+    ql.call("ql_flash_attention_f16", ptr(dq), ptr(dk), ptr(dv), out.ptr, seq, h, h, d, 0, stream())
+    got = out.get((seq, h, d))
+    err = float(np.abs(f16_bits_to_f32(got) - orc.attention_reftest_cpu(q, k, v, h)).max())
+    assert err < 1e-3, err
+    check_attn(got, orc.attention(qb, kb, vb, h, h, False, f16=True), vb, "reference test")
+
+
+def test_launch_flash_attention_shim_tinyllama_shape():
+    # the reference's own shape: TinyLlama 32 query heads, 4 KV heads, head_dim 64
+    seq, h, hkv, d = 77, 32, 4, 64
+    f = getattr(ql.lib(), COMPAT_MANGLED["launch_flash_attention"])
+    f.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int] * 5 + [ctypes.c_void_p]
+    f.restype = None
+    q, k, v = qkv(77, seq, seq, h, hkv, d)
+    dq, dk, dv = dev(q), dev(k), dev(v)
+    o1, o2 = Out(seq * h * d, np.uint16), Out(seq * h * d, np.uint16)
+    f(ptr(dq), ptr(dk), ptr(dv), o1.ptr, seq, h, hkv, d, 1, stream())
+    ql.call("ql_flash_attention_f16", ptr(dq), ptr(dk), ptr(dv), o2.ptr, seq, h, hkv, d, 1,
+            stream())
+    g1 = o1.get((seq, h, d))
+    assert np.array_equal(g1, o2.get((seq, h, d)))
+    check_attn(g1, orc.attention(q, k, v, h, hkv, True, f16=True), v, "launch_flash_attention")
+
+
+# ---- decode / chunked prefill over a contiguous cache, strided rows -----------------------
+@pytest.mark.parametrize("q_len,kv_len", [(1, 1), (1, 1000), (5, 77), (130, 333), (64, 64),
+                                          (3, 0)])
+@pytest.mark.parametrize("causal", [1, 0])
+def test_attention_last_positions_strided(q_len, kv_len, causal):
+    # Q rows inside a fused [q_len, (H + 2*HK)*d] QKV buffer; K/V one layer of a
+    # [L, S, HK, d] cache; out rows padded (the padding must stay untouched)
+    h, hkv, d, L, S, layer = 8, 2, 128, 3, max(kv_len, 1) + 16, 1
+    qrow = (h + 2 * hkv) * d
+    orow = h * d + 64
+    qkvbuf = to_f16_bits(normal(q_len + kv_len, (q_len, qrow)))
+    kc = to_f16_bits(normal(kv_len + 1, (L, S, hkv, d)))
+    vc = to_f16_bits(normal(kv_len + 2, (L, S, hkv, d)))
+    dq, dk, dv = dev(qkvbuf), dev(kc), dev(vc)
+    layer_off = 2 * layer * S * hkv * d
+    out = Out(q_len * orow, np.uint16)
+    ql.call("ql_attention_f16", ptr(dq), ptr(dk) + layer_off, ptr(dv) + layer_off, out.ptr, q_len,
+            kv_len, h, hkv, d, qrow, hkv * d, orow, causal, stream())
+    got = out.get((q_len, orow))
+    assert np.all(got[:, h * d:].view(np.uint8) == GUARD_BYTE), "padding columns written"
+    q = np.ascontiguousarray(qkvbuf[:, :h * d]).reshape(q_len, h, d)
+    k, v = kc[layer, :kv_len], vc[layer, :kv_len]
+    want = orc.attention(q, k, v, h, hkv, bool(causal), f16=True)
+    check_attn(got[:, :h * d].reshape(q_len, h, d), want, v, f"attention q={q_len} kv={kv_len}")
+
+
+# ---- paged KV cache -------------------------------------------------------------------------
+class PagedPool:
+    """Device pool of nb blocks [L, 16, HK, d] (K and V), written through
+    ql_paged_kv_append_f16 from per-sequence block tables."""
+
+    def __init__(self, nb, L, hkv, d):
+        self.nb, self.L, self.hkv, self.d = nb, L, hkv, d
+        self.blk = L * 16 * hkv * d
+        self.kpool = empty((nb * self.blk,), np.uint16, fill_bits=GUARD_BYTE)
+        self.vpool = empty((nb * self.blk,), np.uint16, fill_bits=GUARD_BYTE)
+        self.kptrs = dev(np.array([self.kpool.ptr + 2 * self.blk * b for b in range(nb)], np.int64))
+        self.vptrs = dev(np.array([self.vpool.ptr + 2 * self.blk * b for b in range(nb)], np.int64))
+
+    def append(self, table, k, v, layer):
+        n = k.shape[0]
+        if n == 0:
+            return
+        slots = np.array([table[t // 16] * 16 + t % 16 for t in range(n)], np.int32)
+        dsl, dk, dv = dev(slots), dev(k), dev(v)
+        ql.call("ql_paged_kv_append_f16", self.kptrs.ptr, self.vptrs.ptr, self.nb, dsl.ptr, dk.ptr,
+                dv.ptr, n, layer, self.L, self.hkv, self.d, stream())
+
+
+@pytest.mark.parametrize("h,hkv,d", [(32, 8, 128), (8, 2, 64), (4, 4, 128)])
+def test_paged_attention_varlen_matches_contiguous_and_oracle(h, hkv, d):
+    # three sequences in one launch: a 200-token prefill, a decode step at
+    # context 333, a 17-token chunk at context 150; permuted physical blocks
+    L, layer = 4, 3
+    ctx = [200, 333, 150]
+    qn = [200, 1, 17]
+    r = np.random.default_rng(h * d)
+    need = [(c + 15) // 16 for c in ctx]
+    nb = sum(need) + 3
+    perm = r.permutation(nb)
+    tables, o = [], 0
+    for n in need:
+        tables.append(perm[o:o + n])
+        o += n
+    max_blocks = max(need) + 2
+    bt = np.full((len(ctx), max_blocks), -1, np.int32)
+    for s, t in enumerate(tables):
+        bt[s, :len(t)] = t
+    pool = PagedPool(nb, L, hkv, d)
+    ks, vs, qs = [], [], []
+    for s, c in enumerate(ctx):
+        k = to_f16_bits(normal(100 + s, (c, hkv, d)))
+        v = to_f16_bits(normal(200 + s, (c, hkv, d)))
+        pool.append(bt[s], k, v, layer)
+        ks.append(k)
+        vs.append(v)
+        qs.append(to_f16_bits(normal(300 + s, (qn[s], h, d))))
+    cu = np.concatenate([[0], np.cumsum(qn)]).astype(np.int32)
+    rows = int(cu[-1])
+    qall = np.concatenate(qs)
+    dq = dev(qall)
+    out = Out(rows * h * d, np.uint16)
+    dcu, dctx, dbt = dev(cu), dev(np.array(ctx, np.int32)), dev(bt)
+    ql.call("ql_paged_attention_f16", dq.ptr, out.ptr, h * d, h * d, rows, len(ctx), dcu.ptr,
+            dctx.ptr, max(qn), dbt.ptr, max_blocks, pool.kptrs.ptr, pool.vptrs.ptr, nb, layer, L,
+            h, hkv, d, 1, stream())
+    got = out.get((rows, h, d))
+    for s in range(len(ctx)):
+        mine = got[cu[s]:cu[s + 1]]
+        # same sequence through the contiguous entry point: bit-identical
+        dqs, dks, dvs = dev(qs[s]), dev(ks[s]), dev(vs[s])
+        ref = Out(qn[s] * h * d, np.uint16)
+        ql.call("ql_attention_f16", dqs.ptr, dks.ptr, dvs.ptr, ref.ptr, qn[s], ctx[s], h, hkv, d,
+                h * d, hkv * d, h * d, 1, stream())
+        assert np.array_equal(mine, ref.get((qn[s], h, d))), f"paged != contiguous, sequence {s}"
+        want = orc.attention(qs[s], ks[s], vs[s], h, hkv, True, f16=True)
+        check_attn(mine, want, vs[s], f"paged attention sequence {s}")
+
+
+def test_paged_attention_skips_bad_rows_and_missing_blocks():
+    # sequence 0 claims rows beyond n_q_rows: skipped (its rows keep the guard);
+    # sequence 1's table has a hole (-1): those 16 keys read as zero rows
+    h, hkv, d, L, layer = 4, 2, 64, 1, 0
+    pool = PagedPool(4, L, hkv, d)
+    k = to_f16_bits(normal(1, (40, hkv, d)))
+    v = to_f16_bits(normal(2, (40, hkv, d)))
+    table = np.array([2, 0, 3], np.int32)
+    pool.append(table, k, v, layer)
+    bt = np.array([[1, -1, -1], [2, -1, 3]], np.int32)
+    cu = np.array([3, 9, 4], np.int32)     # seq 0: rows 3..8 (> n_q_rows 4); seq 1: rows 9..3 (empty)
+    q = to_f16_bits(normal(3, (4, h, d)))
+    dq, dcu = dev(q), dev(cu)
+    dctx, dbt = dev(np.array([40, 40], np.int32)), dev(bt)
+    out = Out(4 * h * d, np.uint16)
+    ql.call("ql_paged_attention_f16", dq.ptr, out.ptr, h * d, h * d, 4, 2, dcu.ptr, dctx.ptr, 8,
+            dbt.ptr, 3, pool.kptrs.ptr, pool.vptrs.ptr, 4, layer, L, h, hkv, d, 1, stream())
+    assert np.all(out.get().view(np.uint8) == GUARD_BYTE)
+    # one valid sequence over the holed table: keys 16..31 are zeros
+    cu = np.array([0, 4], np.int32)
+    dcu = dev(cu)
+    dbt = dev(np.array([[2, -1, 3]], np.int32))
+    ql.call("ql_paged_attention_f16", dq.ptr, out.ptr, h * d, h * d, 4, 1, dcu.ptr, dctx.ptr, 4,
+            dbt.ptr, 3, pool.kptrs.ptr, pool.vptrs.ptr, 4, layer, L, h, hkv, d, 1, stream())
+    kz, vz = k.copy(), v.copy()
+    kz[16:32] = 0
+    vz[16:32] = 0
+    check_attn(out.get((4, h, d)), orc.attention(q, kz, vz, h, hkv, True, f16=True), v, "holed table")
+
+
+# ---- C5 shape: 8192-token causal prefill, GQA 32/8, head_dim 128 ---------------------------
+def test_attention_c5_prefill_sampled_rows_and_paged_equivalence():
+    T, h, hkv, d, L, layer = 8192, 32, 8, 128, 2, 1
+    q, k, v = qkv(0x51A10070, T, T, h, hkv, d)
+    dq, dk, dv = dev(q), dev(k), dev(v)
+    out = Out(T * h * d, np.uint16)
+    ql.call("ql_flash_attention_f16", ptr(dq), ptr(dk), ptr(dv), out.ptr, T, h, hkv, d, 1,
+            stream())
+    got = out.get((T, h, d))
+    rows = [0, 1, 31, 32, 63, 64, 127, 128, 1000, 4095, 4096, 6143, 8190, 8191]
+    rows += list(np.random.default_rng(5).integers(0, T, 6))
+    for i in rows:
+        want = orc.attention(q[i:i + 1], k[:i + 1], v[:i + 1], h, hkv, True, f16=True)
+        check_attn(got[i:i + 1], want, v, f"C5 prefill row {i}")
+    # the same K/V in a paged pool (fresh-pool block order) gives identical bits
+    nb = T // 16
+    pool = PagedPool(nb, L, hkv, d)
+    table = np.arange(nb, dtype=np.int32)
+    pool.append(table, k, v, layer)
+    out2 = Out(T * h * d, np.uint16)
+    dcu, dctx, dbt = dev(np.array([0, T], np.int32)), dev(np.array([T], np.int32)), dev(table)
+    ql.call("ql_paged_attention_f16", dq.ptr, out2.ptr, h * d, h * d, T, 1, dcu.ptr, dctx.ptr, T,
+            dbt.ptr, nb, pool.kptrs.ptr, pool.vptrs.ptr, nb, layer, L, h, hkv, d, 1, stream())
+    assert np.array_equal(out2.get((T, h, d)), got)

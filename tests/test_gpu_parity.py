@@ -11,36 +11,11 @@ import pytest
 
 import oracle as orc
 import quantlib_amd as ql
-from helpers import (ATOL_F32, ATOL_ROPE_F32, RTOL_F32, causal_mask_inplace, check_abs,
-                     check_close, check_f16, dev, empty, f16_bits_to_f32, host, normal, ptr,
-                     stream, to_f16_bits, uniform)
+from helpers import (ATOL_F32, ATOL_ROPE_F32, GUARD, GUARD_BYTE, RTOL_F32, Out,
+                     causal_mask_inplace, check_abs, check_close, check_f16, dev, empty,
+                     f16_bits_to_f32, host, normal, ptr, stream, to_f16_bits, uniform)
 
 pytestmark = pytest.mark.gpu
-
-GUARD = 64          # elements of guard band on each side of every output
-GUARD_BYTE = 0xA5
-
-
-class Out:
-    """Device output buffer of n elements between two guard bands."""
-
-    def __init__(self, n, dtype, offset=0):
-        self.n, self.dtype, self.offset = n, dtype, offset
-        self.buf = empty((n + 2 * GUARD + offset,), dtype, fill_bits=GUARD_BYTE)
-        self.view = self.buf.window(GUARD + offset, n)
-
-    @property
-    def ptr(self):
-        return self.view.data_ptr()
-
-    def get(self, shape=None):
-        a = host(self.buf)
-        g0, g1 = a[:GUARD + self.offset], a[GUARD + self.offset + self.n:]
-        for g in (g0, g1):
-            assert np.all(g.view(np.uint8) == GUARD_BYTE), "write outside the output region"
-        v = a[GUARD + self.offset:GUARD + self.offset + self.n]
-        return v.reshape(shape) if shape is not None else v
-
 
 def _f16(x):
     return to_f16_bits(x)

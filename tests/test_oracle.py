@@ -332,3 +332,93 @@ def test_paged_append_matches_numpy_views(permuted):
         ek[slots[t] // 16, layer, slots[t] % 16] = kn[t]
         ev[slots[t] // 16, layer, slots[t] % 16] = vn[t]
     assert np.array_equal(kp.reshape(ek.shape), ek) and np.array_equal(vp.reshape(ev.shape), ev)
+
+
+# ---- attention ---------------------------------------------------------------------------
+def _qkv(seed, q_len, kv_len, h, hkv, d, sigma=1.0):
+    return (normal(seed, (q_len, h, d), sigma), normal(seed + 1, (kv_len, hkv, d)),
+            normal(seed + 2, (kv_len, hkv, d)))
+
+
+@pytest.mark.parametrize("q_len,kv_len", [(9, 9), (3, 11), (1, 17)])
+def test_attention_identical_keys_give_mean_of_visible_values(q_len, kv_len):
+    # equal scores -> uniform weights over the visible keys: a prefix mean under
+    # the causal mask (query i at position kv_len - q_len + i), the full mean without
+    q, _, v = _qkv(11, q_len, kv_len, 4, 2, 16)
+    k = np.broadcast_to(normal(5, (1, 2, 16)), (kv_len, 2, 16)).copy()
+    for causal in (True, False):
+        out = orc.attention(q, k, v, 4, 2, causal)
+        for i in range(q_len):
+            n = kv_len - q_len + i + 1 if causal else kv_len
+            for h in range(4):
+                want = v[:n, h * 2 // 4].astype(np.float64).mean(axis=0)
+                np.testing.assert_allclose(out[i, h], want, rtol=1e-6, atol=1e-7)
+
+
+def test_attention_causal_first_query_is_first_value_row():
+    q, k, v = _qkv(21, 6, 6, 2, 2, 8, sigma=3.0)
+    out = orc.attention(q, k, v, 2, 2, True)
+    assert np.array_equal(out[0], v[0])
+
+
+def test_attention_two_keys_logistic_weight_pins_scale():
+    # q . k0 = 0 and q . k1 = a*b, so the weight of v1 is sigmoid(a*b/sqrt(d))
+    d = 64
+    for a, b in [(1.0, 2.0), (3.0, -1.5), (0.5, 7.0)]:
+        q = np.zeros((2, 1, d), np.float32)
+        q[:, 0, 0] = a
+        k = np.zeros((2, 1, d), np.float32)
+        k[1, 0, 0] = b
+        v = np.zeros((2, 1, d), np.float32)
+        v[0, 0, :] = 1.0
+        v[1, 0, :] = -2.0
+        out = orc.attention(q, k, v, 1, 1, False)
+        w1 = scipy.special.expit(a * b / math.sqrt(d))
+        np.testing.assert_allclose(out[1, 0], (1 - w1) * 1.0 + w1 * -2.0, rtol=1e-6)
+
+
+def test_attention_dominant_key_selects_its_value_row():
+    d, n = 32, 40
+    q = np.zeros((1, 1, d), np.float32)
+    q[0, 0, 3] = 50.0
+    k = normal(31, (n, 1, d), 0.1)
+    k[17, 0, 3] = 20.0   # score 1000/sqrt(32) ~ 177 above the rest
+    v = normal(32, (n, 1, d))
+    out = orc.attention(q, k, v, 1, 1, False)
+    np.testing.assert_allclose(out[0, 0], v[17, 0], rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("h,hkv", [(8, 2), (6, 4), (32, 8), (4, 4)])
+def test_attention_gqa_head_map(h, hkv):
+    # V of kv head g is the constant g+1, so out[:, head] = head*hkv//h + 1 exactly
+    q, k, _ = _qkv(41, 5, 5, h, hkv, 16)
+    v = np.broadcast_to(np.arange(1, hkv + 1, dtype=np.float32)[None, :, None], (5, hkv, 16)).copy()
+    out = orc.attention(q, k, v, h, hkv, True)
+    for head in range(h):
+        assert np.all(out[:, head] == np.float32(head * hkv // h + 1)), head
+
+
+def test_attention_no_visible_key_gives_zero():
+    q, k, v = _qkv(51, 4, 2, 2, 1, 8)   # q_len > kv_len: the first queries see nothing
+    out = orc.attention(q, k, v, 2, 1, True)
+    assert np.all(out[:2] == 0.0) and np.all(np.abs(out[2:]).sum(axis=-1) > 0)
+
+
+def test_attention_passes_reference_test():
+    # tests/test_attention.cu:60-141: srand(99), U(-0.5, 0.5), [128, 32, 128], MHA,
+    # no mask; max abs error < 1e-3 against the reference's own fp32 CPU loop
+    q, k, v = orc.reftest_attention_inputs(128, 32, 128, 99)
+    assert np.float32(q[0, 0, 0]) == np.float32(q.ravel()[0])
+    ours = orc.attention(q, k, v, 32, 32, False)
+    theirs = orc.attention_reftest_cpu(q, k, v, 32)
+    err = float(np.abs(ours - theirs).max())
+    assert err < 1e-5, err        # the reference's bar is 1e-3; fp32 vs double loops
+    assert float(np.abs(ours).max()) > 0.01
+
+
+def test_attention_f16_is_f32_arithmetic_on_widened_values():
+    q, k, v = _qkv(61, 7, 7, 4, 2, 64)
+    qh, kh, vh = to_f16_bits(q), to_f16_bits(k), to_f16_bits(v)
+    got = orc.attention(qh, kh, vh, 4, 2, True, f16=True)
+    want = orc.attention(f16_bits_to_f32(qh), f16_bits_to_f32(kh), f16_bits_to_f32(vh), 4, 2, True)
+    assert np.array_equal(got, orc.f32_to_f16(want))
