@@ -27,9 +27,14 @@
 // operand is two 8-byte LDS reads per MFMA.
 //
 // Precision: Q, K, V, P in fp16 (exact products), fp32 accumulation and
-// softmax state; p = 2^(s*c - m*c) with c = scale*log2(e) from v_exp_f32; the
-// row sum l adds the fp16-rounded p, so O/l is an exact convex combination of
-// the fp16 weights that multiplied V.
+// softmax state; p = 2^(s*c - m*c) with c = scale*log2(e) from v_exp_f32, m a
+// running offset that is raised only when a query's maximum grows by more than
+// 2^8 (so p <= 256; the offset cancels in O/l); the row sum l adds the
+// fp16-rounded p (v_dot2 with ones, fp32 accumulation), so O/l is an exact
+// convex combination of the fp16 weights that multiplied V.
+//
+// Workgroups are mapped XCD-aware: ids go to the 8 XCDs round-robin, and each
+// XCD is handed a contiguous run of query heads (and so of KV heads).
 #include "ql_common.hpp"
 #include "quantlib_amd.h"
 
@@ -109,16 +114,32 @@ __device__ __forceinline__ uintptr_t key_row(const AttnArgs& a, const _Float16* 
     }
 }
 
-// 8 halfs at p (0 = missing row -> zeros); a base that is not 16-byte aligned
-// (possible for caller-provided page pointers) is read element by element.
-__device__ __forceinline__ half8 load8(uintptr_t p) {
-    if (p == 0) return half8{};
-    if ((p & 15) == 0) return *reinterpret_cast<const half8*>(p);
-    const _Float16* e = reinterpret_cast<const _Float16*>(p);
-    half8 r;
+typedef const __attribute__((address_space(1))) half8* GlobalHalf8Ptr;
+
+// 16 bytes of chunk ch of a key row (row == 0: missing key -> zeros).  Loads
+// always target a valid address (dummy stands in for a missing row) and the
+// value is selected afterwards, so the fast path has no branches; loads are
+// issued in the global address space so they count only against the vector
+// memory counter (LDS waits do not wait for them).  A page pointer that is not
+// 16-byte aligned (caller-provided pools) sends the wavefront through an
+// element-wise path.
+template <bool PAGED>
+__device__ __forceinline__ half8 load_chunk(uintptr_t row, int ch, uintptr_t dummy) {
+    const bool ok = row != 0;
+    const uintptr_t src = (ok ? row : dummy) + 16 * (uintptr_t)ch;
+    if constexpr (PAGED) {
+        if (__any((src & 15) != 0)) {
+            half8 r{};
+            if (ok) {
+                const _Float16* e = reinterpret_cast<const _Float16*>(src);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) r[i] = e[i];
-    return r;
+                for (int i = 0; i < 8; ++i) r[i] = e[i];
+            }
+            return r;
+        }
+    }
+    const half8 x = *(GlobalHalf8Ptr)src;
+    return ok ? x : half8{};
 }
 
 template <int HD, bool PAGED>
@@ -131,7 +152,8 @@ struct TileRegs {
 // beyond kv_len read as zeros; they are masked anyway).
 template <int HD, bool PAGED>
 __device__ __forceinline__ void fetch_tile(TileRegs<HD, PAGED>& r, const AttnArgs& a,
-                                           const int32_t* table, int kvh, int kv0, int kv_len) {
+                                           const int32_t* table, int kvh, int kv0, int kv_len,
+                                           uintptr_t dummy) {
     using T = Tile<HD>;
     const int tid = threadIdx.x;
 #pragma unroll
@@ -140,14 +162,14 @@ __device__ __forceinline__ void fetch_tile(TileRegs<HD, PAGED>& r, const AttnArg
         const int key = idx / T::KCH, ch = idx % T::KCH;
         const int j = kv0 + key;
         const uintptr_t row = j < kv_len ? key_row<PAGED>(a, a.k, a.kb, table, kvh, j, HD) : 0;
-        r.k[i] = load8(row ? row + 16 * ch : 0);
+        r.k[i] = load_chunk<PAGED>(row, ch, dummy);
     }
     const int g = tid % T::VGROUPS, ch = tid / T::VGROUPS;
 #pragma unroll
     for (int i = 0; i < T::KPT; ++i) {
         const int j = kv0 + g * T::KPT + i;
         const uintptr_t row = j < kv_len ? key_row<PAGED>(a, a.v, a.vb, table, kvh, j, HD) : 0;
-        r.v[i] = load8(row ? row + 16 * ch : 0);
+        r.v[i] = load_chunk<PAGED>(row, ch, dummy);
     }
 }
 
@@ -181,7 +203,21 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
     constexpr int NDB = HD / 32;   // 32-row blocks of O^T
     __shared__ _Float16 smem[2 * T::STAGE];
 
-    const int head = blockIdx.y;
+    // Work item (query head, query tile).  Consecutive workgroup ids go to the
+    // 8 XCDs in turn; when the heads split evenly over the XCDs, each XCD is
+    // given its own contiguous run of heads (so the K/V rows of their shared KV
+    // heads stay in that XCD's L2).  Causal: heavy (late) query tiles first.
+    const int n_qt = (int)gridDim.x / a.n_heads;
+    int head, t;
+    if (a.n_heads % 8 == 0) {
+        const int hpx = a.n_heads / 8, xcd = (int)blockIdx.x & 7, j = (int)blockIdx.x >> 3;
+        head = xcd * hpx + j % hpx;
+        t = j / hpx;
+    } else {
+        head = (int)blockIdx.x % a.n_heads;
+        t = (int)blockIdx.x / a.n_heads;
+    }
+    const int qt = a.causal ? n_qt - 1 - t : t;
     const int kvh = (int)(((long long)head * a.n_kv_heads) / a.n_heads);
     int q_begin = 0, q_len = a.q_len, kv_len = a.kv_len;
     const int32_t* table = nullptr;
@@ -194,8 +230,6 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
         if (kv_len > a.max_blocks * QL_PAGE_SIZE) kv_len = a.max_blocks * QL_PAGE_SIZE;
         table = a.block_tables + (size_t)s * a.max_blocks;
     }
-    // causal: heavy (late) query tiles first
-    const int qt = a.causal ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x;
     const int q0 = qt * kBQ;
     if (q0 >= q_len) return;   // workgroup-uniform
     if (kv_len < 0) kv_len = 0;
@@ -235,9 +269,12 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
     float m_run = -FLT_MAX, l_run = 0.0f;
     const float cl2 = a.cl2;
 
+    // a valid, aligned address for the loads of missing key rows: this
+    // sequence's first query row
+    const uintptr_t dummy = reinterpret_cast<uintptr_t>(a.q + (size_t)q_begin * a.q_stride);
     TileRegs<HD, PAGED> regs;
     if (n_tiles > 0) {
-        fetch_tile<HD, PAGED>(regs, a, table, kvh, 0, kv_len);
+        fetch_tile<HD, PAGED>(regs, a, table, kvh, 0, kv_len, dummy);
         stash_tile<HD, PAGED>(regs, smem, smem + T::K_ELEMS);
     }
     __syncthreads();
@@ -245,7 +282,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
     for (int t = 0; t < n_tiles; ++t) {
         const int kv0 = t * kBK;
         const bool more = t + 1 < n_tiles;
-        if (more) fetch_tile<HD, PAGED>(regs, a, table, kvh, kv0 + kBK, kv_len);
+        if (more) fetch_tile<HD, PAGED>(regs, a, table, kvh, kv0 + kBK, kv_len, dummy);
         const _Float16* sk = smem + (t & 1) * T::STAGE;
         const _Float16* sv = sk + T::K_ELEMS;
 
@@ -280,26 +317,40 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
                 }
             }
             mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
-            const float m_new = fmaxf(m_run, mt);
-            const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * cl2);
-            const float moff = m_new * cl2;
+            // Rescale only when some query's max grew by more than 2^8 in the
+            // exponent: until then the stale offset keeps p <= 256 (exact
+            // enough in binary16) and O/l is unchanged, since the offset cancels.
+            const float m_cand = fmaxf(m_run, mt);
+            if (__any((m_cand - m_run) * cl2 > 8.0f)) {
+                const float alpha = __builtin_amdgcn_exp2f((m_run - m_cand) * cl2);
+#pragma unroll
+                for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+                l_run *= alpha;
+                m_run = m_cand;
+            }
+            const float moff = m_run * cl2;
             half8 pf[2][2];
-            float lsum = 0.0f;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     const float p = __builtin_amdgcn_exp2f(fmaf(s[kb][i], cl2, -moff));
-                    const _Float16 ph = from_f32<_Float16>(p);
-                    lsum += (float)ph;
-                    pf[kb][i >> 3][i & 7] = ph;
+                    pf[kb][i >> 3][i & 7] = from_f32<_Float16>(p);
                 }
             }
-            l_run = fmaf(l_run, alpha, lsum);
-            m_run = m_new;
+            // row sum of the binary16 weights, accumulated in fp32 (v_dot2 with ones)
+            float lsum = l_run;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int c = 0; c < 2; ++c)
+#pragma unroll
+                    for (int e = 0; e < 8; e += 2)
+                        lsum = __builtin_amdgcn_fdot2(half2v{pf[kb][c][e], pf[kb][c][e + 1]},
+                                                      half2v{1.0f16, 1.0f16}, lsum, false);
+            l_run = lsum;
 #pragma unroll
             for (int db = 0; db < NDB; ++db) {
-                o[db] *= alpha;
                 const _Float16* vrow = sv + (db * 32 + col) * T::VS + 4 * hh;
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb) {
@@ -341,7 +392,8 @@ float scale_log2e(int head_dim) {
 
 template <bool PAGED>
 hipError_t launch_attn(const AttnArgs& a, int head_dim, unsigned gx, unsigned gz, hipStream_t stream) {
-    const dim3 grid(gx, (unsigned)a.n_heads, gz);
+    QL_CHECK_ARG((long long)gx * a.n_heads <= INT32_MAX);
+    const dim3 grid(gx * (unsigned)a.n_heads, 1, gz);
     if (head_dim == 128) {
         hipLaunchKernelGGL((attn_fwd<128, PAGED>), grid, dim3(kAttnThreads), 0, stream, a);
     } else {
