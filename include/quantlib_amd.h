@@ -222,7 +222,8 @@ hipError_t ql_flash_attention_f16(const uint16_t* q, const uint16_t* k, const ui
  * kv_len keys (query i sits at kv_len - q_len + i).  Decode against the contiguous
  * cache of src/fp16_forward.cu:202-209 is q_len = 1, kv_len = pos + 1,
  * k = k_cache + layer*max_seq*n_kv_heads*head_dim, kv_row_stride = n_kv_heads*head_dim
- * (the reference passes its one-token Q with seq_len = ctx_len and so reads past it). */
+ * (the reference passes its one-token Q with seq_len = ctx_len and so reads past it).
+ * q_len == 1 runs the decode kernel (the query heads of a KV head share one pass). */
 hipError_t ql_attention_f16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                             uint16_t* out, int q_len, int kv_len, int n_heads, int n_kv_heads,
                             int head_dim, int64_t q_row_stride, int64_t kv_row_stride,
@@ -236,7 +237,8 @@ hipError_t ql_attention_f16(const uint16_t* q, const uint16_t* k, const uint16_t
  * physical block, include/scheduler.h:17-19).  max_q_len bounds every sequence's
  * query count (host value: it sizes the grid).  A sequence whose rows fall outside
  * [0, n_q_rows) is skipped; a table entry outside [0, n_blocks) reads as zero
- * keys.  Decode = one query row per sequence. */
+ * keys.  max_q_len == 1 (every sequence decodes one token) runs the decode kernel
+ * (see ql_paged_decode_attention_f16) in one pass. */
 hipError_t ql_paged_attention_f16(const uint16_t* q, uint16_t* out, int64_t q_row_stride,
                                   int64_t out_row_stride, int n_q_rows, int n_seqs,
                                   const int32_t* cu_q_lens, const int32_t* ctx_lens,
@@ -245,6 +247,29 @@ hipError_t ql_paged_attention_f16(const uint16_t* q, uint16_t* out, int64_t q_ro
                                   const uint16_t* const* v_blocks, int n_blocks, int layer,
                                   int n_layers, int n_heads, int n_kv_heads, int head_dim,
                                   int causal, hipStream_t stream);
+
+/* Decode over the paged KV cache: sequence s (< n_seqs) has ONE query, row s of q,
+ * at position ctx_lens[s] - 1, and its output goes to row s of out (the attention
+ * step of the per-token decode in src/fp16_forward.cu:202-209 and
+ * src/continuous_batch.cu:104-127, batched over sequences).  The query heads
+ * that share a KV head read its K/V rows once.  With a workspace of
+ * ql_paged_decode_workspace_size() bytes the keys of each sequence are split over
+ * more workgroups (partials in the workspace, then a combine kernel); a smaller or
+ * NULL workspace uses fewer splits (down to one pass, no workspace).  max_ctx_len
+ * is a host-side bound of ctx_lens used to size the split.  Results for a given
+ * workspace size are deterministic.  Calls that share a workspace must be ordered
+ * on one stream. */
+hipError_t ql_paged_decode_workspace_size(int n_seqs, int n_heads, int n_kv_heads, int head_dim,
+                                          int max_ctx_len, size_t* bytes);
+hipError_t ql_paged_decode_attention_f16(const uint16_t* q, uint16_t* out, int64_t q_row_stride,
+                                         int64_t out_row_stride, int n_seqs,
+                                         const int32_t* ctx_lens, int max_ctx_len,
+                                         const int32_t* block_tables, int max_blocks_per_seq,
+                                         const uint16_t* const* k_blocks,
+                                         const uint16_t* const* v_blocks, int n_blocks,
+                                         int layer, int n_layers, int n_heads, int n_kv_heads,
+                                         int head_dim, void* workspace, size_t workspace_bytes,
+                                         hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -93,23 +93,88 @@ struct AttnArgs {
     const int32_t* ctx_lens;       // [n_seqs] keys of each sequence
     int n_q_rows;                  // rows available in q / out
     int layer;
+    // decode (one query row per sequence)
+    int n_split;                   // key splits per (sequence, KV head)
+    float* ws;                     // [n_seqs, n_heads, n_split, head_dim + 2] partials
+};
+
+// Page bases of up to 4 consecutive 16-key pages: the address of (block,
+// layer, slot 0, this KV head) for K and V, or 0 where the table entry is
+// missing or out of range.  The lookups use VECTOR loads whose results are
+// broadcast with v_readlane: scalar loads would share the LDS wait counter, so
+// every LDS wait would also wait for the lookup.
+struct Pages {
+    uintptr_t k[4], v[4];
+    bool misaligned;
+};
+
+__device__ __forceinline__ uintptr_t readlane64(uintptr_t x, int l) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(x >> 32), l);
+    return ((uintptr_t)hi << 32) | lo;
+}
+
+// Three-stage lookup of the page bases of COUNT consecutive pages: (1) lane p
+// loads table entry first+p, (2) it loads the two block pointers, (3) the
+// results are broadcast with v_readlane.  Each stage's result is consumed one
+// tile later, at a point where the kernel waits for its K/V loads anyway, so the
+// dependent table -> pointer chain never stalls the tile in flight.
+template <bool PAGED, int COUNT>
+struct PagePipe {
+    int b = -1;                 // stage 1: table entry of page first + lane%4 (or -1)
+    uintptr_t kp = 0, vp = 0;   // stage 2: block pointers (0 = missing)
+
+    __device__ __forceinline__ void entries(const AttnArgs& a, const int32_t* table, int first) {
+        if constexpr (PAGED) {
+            const int p = (int)(threadIdx.x & 3);
+            const int t = first + p;
+            int e = -1;
+            if (p < COUNT && t < a.max_blocks) e = table[t];
+            b = e;
+        }
+    }
+    __device__ __forceinline__ void pointers(const AttnArgs& a, int kvh, int hd) {
+        if constexpr (PAGED) {
+            const size_t head_off = ((size_t)a.layer * QL_PAGE_SIZE * a.n_kv_heads + kvh) * hd;
+            uintptr_t k = 0, v = 0;
+            if (b >= 0 && b < a.n_blocks) {
+                k = reinterpret_cast<uintptr_t>(a.kb[b] + head_off);
+                v = reinterpret_cast<uintptr_t>(a.vb[b] + head_off);
+            }
+            kp = k;
+            vp = v;
+        }
+    }
+    __device__ __forceinline__ Pages bases() const {
+        Pages pg{};
+        if constexpr (PAGED) {
+            uintptr_t any = 0;
+#pragma unroll
+            for (int q = 0; q < COUNT; ++q) {
+                pg.k[q] = readlane64(kp, q);
+                pg.v[q] = readlane64(vp, q);
+                any |= pg.k[q] | pg.v[q];
+            }
+            pg.misaligned = (any & 15) != 0;
+        }
+        return pg;
+    }
 };
 
 // Address of key row j (its d values are contiguous) for this KV head, or 0
-// when the key has no backing block.
+// when the key has no backing block.  kv0 = first key of the tile j is in.
 template <bool PAGED>
 __device__ __forceinline__ uintptr_t key_row(const AttnArgs& a, const _Float16* base,
-                                             const _Float16* const* blocks, const int32_t* table,
-                                             int kvh, int j, int hd) {
+                                             const uintptr_t* pages, int kvh, int kv0, int j,
+                                             int hd) {
     if constexpr (PAGED) {
-        const int t = j >> 4;
-        if (t >= a.max_blocks) return 0;
-        const int b = table[t];
-        if (b < 0 || b >= a.n_blocks) return 0;
-        const size_t off = (((size_t)a.layer * QL_PAGE_SIZE + (j & (QL_PAGE_SIZE - 1))) *
-                                (size_t)a.n_kv_heads + kvh) * hd;
-        return reinterpret_cast<uintptr_t>(blocks[b] + off);
+        const int p = (j - kv0) >> 4;
+        const uintptr_t pb = p == 0 ? pages[0] : p == 1 ? pages[1] : p == 2 ? pages[2] : pages[3];
+        const uintptr_t row_bytes = (uintptr_t)a.n_kv_heads * hd * sizeof(_Float16);
+        return pb ? pb + (uintptr_t)(j & (QL_PAGE_SIZE - 1)) * row_bytes : 0;
     } else {
+        (void)pages;
+        (void)kv0;
         return reinterpret_cast<uintptr_t>(base + (size_t)j * a.kv_stride + (size_t)kvh * hd);
     }
 }
@@ -118,28 +183,26 @@ typedef const __attribute__((address_space(1))) half8* GlobalHalf8Ptr;
 
 // 16 bytes of chunk ch of a key row (row == 0: missing key -> zeros).  Loads
 // always target a valid address (dummy stands in for a missing row) and the
-// value is selected afterwards, so the fast path has no branches; loads are
-// issued in the global address space so they count only against the vector
-// memory counter (LDS waits do not wait for them).  A page pointer that is not
-// 16-byte aligned (caller-provided pools) sends the wavefront through an
-// element-wise path.
-template <bool PAGED>
+// value is selected afterwards, so there are no branches; loads are issued in
+// the global address space so they count only against the vector memory
+// counter (LDS waits do not wait for them).
 __device__ __forceinline__ half8 load_chunk(uintptr_t row, int ch, uintptr_t dummy) {
     const bool ok = row != 0;
     const uintptr_t src = (ok ? row : dummy) + 16 * (uintptr_t)ch;
-    if constexpr (PAGED) {
-        if (__any((src & 15) != 0)) {
-            half8 r{};
-            if (ok) {
-                const _Float16* e = reinterpret_cast<const _Float16*>(src);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) r[i] = e[i];
-            }
-            return r;
-        }
-    }
     const half8 x = *(GlobalHalf8Ptr)src;
     return ok ? x : half8{};
+}
+
+// The same for page pointers that are not 16-byte aligned (caller-provided
+// pools): element-wise loads.  Used for a whole tile, chosen once per tile.
+__device__ __noinline__ half8 load_chunk_unaligned(uintptr_t row, int ch) {
+    half8 r{};
+    if (row != 0) {
+        const _Float16* e = reinterpret_cast<const _Float16*>(row + 16 * (uintptr_t)ch);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r[i] = e[i];
+    }
+    return r;
 }
 
 template <int HD, bool PAGED>
@@ -148,29 +211,100 @@ struct TileRegs {
     half8 v[Tile<HD>::KPT];
 };
 
+// Per-thread constants of the tile loader: which tile key each of the thread's
+// K and V chunks belongs to, the page it lies in, and its byte offset from that
+// page's base (paged) or from the tile's first key row (contiguous).
+template <int HD, bool PAGED>
+struct TilePlan {
+    using T = Tile<HD>;
+    uint32_t k_off[T::KLOADS], v_off[T::KPT];
+    int k_page[T::KLOADS], v_page;
+
+    __device__ __forceinline__ TilePlan(const AttnArgs& a, int kvh) {
+        const int tid = (int)threadIdx.x;
+        const uint32_t row_bytes = PAGED ? (uint32_t)(a.n_kv_heads * HD * sizeof(_Float16))
+                                         : (uint32_t)(a.kv_stride * sizeof(_Float16));
+        const uint32_t head_bytes = PAGED ? 0u : (uint32_t)(kvh * HD * sizeof(_Float16));
+#pragma unroll
+        for (int i = 0; i < T::KLOADS; ++i) {
+            const int key = tid / T::KCH + (kAttnThreads / T::KCH) * i, ch = tid % T::KCH;
+            k_page[i] = key >> 4;
+            k_off[i] = (uint32_t)(PAGED ? (key & 15) : key) * row_bytes + head_bytes + 16u * ch;
+        }
+        const int g = tid % T::VGROUPS, ch = tid / T::VGROUPS;
+        v_page = (g * T::KPT) >> 4;
+#pragma unroll
+        for (int i = 0; i < T::KPT; ++i) {
+            const int key = g * T::KPT + i;
+            v_off[i] = (uint32_t)(PAGED ? (key & 15) : key) * row_bytes + head_bytes + 16u * ch;
+        }
+    }
+};
+
+__device__ __forceinline__ uintptr_t pick4(const uintptr_t* v, int i) {
+    return i == 0 ? v[0] : i == 1 ? v[1] : i == 2 ? v[2] : v[3];
+}
+
 // Fetch key tile [kv0, kv0+64) of this KV head into registers (keys at or
-// beyond kv_len read as zeros; they are masked anyway).
+// beyond kv_len read as zeros; they are masked anyway).  A full tile whose
+// pages are all present and aligned takes the branch-free path; the last
+// tile, holes in the block table and misaligned pages take the checked path.
 template <int HD, bool PAGED>
 __device__ __forceinline__ void fetch_tile(TileRegs<HD, PAGED>& r, const AttnArgs& a,
-                                           const int32_t* table, int kvh, int kv0, int kv_len,
-                                           uintptr_t dummy) {
+                                           const TilePlan<HD, PAGED>& plan, const Pages& pg,
+                                           int kvh, int kv0, int kv_len, uintptr_t dummy) {
     using T = Tile<HD>;
+    bool clean = kv0 + kBK <= kv_len;
+    if constexpr (PAGED)
+        clean = clean && !pg.misaligned && pg.k[0] && pg.k[1] && pg.k[2] && pg.k[3] && pg.v[0] &&
+                pg.v[1] && pg.v[2] && pg.v[3];
+    if (clean) {   // workgroup-uniform
+        uintptr_t kbase[4], vbase;
+        if constexpr (PAGED) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) kbase[i] = pg.k[i];
+            vbase = pick4(pg.v, plan.v_page);
+        } else {
+            const uintptr_t step = (uintptr_t)kv0 * (uintptr_t)a.kv_stride * sizeof(_Float16);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) kbase[i] = reinterpret_cast<uintptr_t>(a.k) + step;
+            vbase = reinterpret_cast<uintptr_t>(a.v) + step;
+        }
+#pragma unroll
+        for (int i = 0; i < T::KLOADS; ++i) {
+            const uintptr_t kb = PAGED ? pick4(kbase, plan.k_page[i]) : kbase[0];
+            r.k[i] = *(GlobalHalf8Ptr)(kb + plan.k_off[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < T::KPT; ++i) r.v[i] = *(GlobalHalf8Ptr)(vbase + plan.v_off[i]);
+        return;
+    }
     const int tid = threadIdx.x;
+    uintptr_t krow[T::KLOADS], vrow[T::KPT];
 #pragma unroll
     for (int i = 0; i < T::KLOADS; ++i) {
-        const int idx = tid + kAttnThreads * i;
-        const int key = idx / T::KCH, ch = idx % T::KCH;
-        const int j = kv0 + key;
-        const uintptr_t row = j < kv_len ? key_row<PAGED>(a, a.k, a.kb, table, kvh, j, HD) : 0;
-        r.k[i] = load_chunk<PAGED>(row, ch, dummy);
+        const int j = kv0 + (tid + kAttnThreads * i) / T::KCH;
+        krow[i] = j < kv_len ? key_row<PAGED>(a, a.k, pg.k, kvh, kv0, j, HD) : 0;
     }
-    const int g = tid % T::VGROUPS, ch = tid / T::VGROUPS;
+    const int g = tid % T::VGROUPS, vch = tid / T::VGROUPS;
 #pragma unroll
     for (int i = 0; i < T::KPT; ++i) {
         const int j = kv0 + g * T::KPT + i;
-        const uintptr_t row = j < kv_len ? key_row<PAGED>(a, a.v, a.vb, table, kvh, j, HD) : 0;
-        r.v[i] = load_chunk<PAGED>(row, ch, dummy);
+        vrow[i] = j < kv_len ? key_row<PAGED>(a, a.v, pg.v, kvh, kv0, j, HD) : 0;
     }
+    if (PAGED && pg.misaligned) {   // workgroup-uniform
+#pragma unroll
+        for (int i = 0; i < T::KLOADS; ++i)
+            r.k[i] = load_chunk_unaligned(krow[i], (tid + kAttnThreads * i) % T::KCH);
+#pragma unroll
+        for (int i = 0; i < T::KPT; ++i) r.v[i] = load_chunk_unaligned(vrow[i], vch);
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < T::KLOADS; ++i)
+        r.k[i] = load_chunk(krow[i], (tid + kAttnThreads * i) % T::KCH, dummy);
+#pragma unroll
+    for (int i = 0; i < T::KPT; ++i) r.v[i] = load_chunk(vrow[i], vch, dummy);
 }
 
 // Registers -> LDS stage: K row-major [key][d], V transposed [d][key].
@@ -273,8 +407,21 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
     // sequence's first query row
     const uintptr_t dummy = reinterpret_cast<uintptr_t>(a.q + (size_t)q_begin * a.q_stride);
     TileRegs<HD, PAGED> regs;
+    const TilePlan<HD, PAGED> plan(a, kvh);
+    constexpr int kTilePages = kBK / QL_PAGE_SIZE;
+    PagePipe<PAGED, kTilePages> pp;
+    Pages pg_next{};
     if (n_tiles > 0) {
-        fetch_tile<HD, PAGED>(regs, a, table, kvh, 0, kv_len, dummy);
+        pp.entries(a, table, 0);
+        pp.pointers(a, kvh, HD);
+        const Pages pg0 = pp.bases();
+        if (n_tiles > 1) {
+            pp.entries(a, table, kTilePages);
+            pp.pointers(a, kvh, HD);
+            pg_next = pp.bases();
+        }
+        if (n_tiles > 2) pp.entries(a, table, 2 * kTilePages);
+        fetch_tile<HD, PAGED>(regs, a, plan, pg0, kvh, 0, kv_len, dummy);
         stash_tile<HD, PAGED>(regs, smem, smem + T::K_ELEMS);
     }
     __syncthreads();
@@ -282,7 +429,9 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
     for (int t = 0; t < n_tiles; ++t) {
         const int kv0 = t * kBK;
         const bool more = t + 1 < n_tiles;
-        if (more) fetch_tile<HD, PAGED>(regs, a, table, kvh, kv0 + kBK, kv_len, dummy);
+        if (more) fetch_tile<HD, PAGED>(regs, a, plan, pg_next, kvh, kv0 + kBK, kv_len, dummy);
+        if (t + 2 < n_tiles) pp.pointers(a, kvh, HD);                          // tile t+2
+        if (t + 3 < n_tiles) pp.entries(a, table, (t + 3) * kTilePages);       // tile t+3
         const _Float16* sk = smem + (t & 1) * T::STAGE;
         const _Float16* sv = sk + T::K_ELEMS;
 
@@ -366,6 +515,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
         }
         if (more) stash_tile<HD, PAGED>(regs, smem + ((t + 1) & 1) * T::STAGE,
                                         smem + ((t + 1) & 1) * T::STAGE + T::K_ELEMS);
+        if (t + 2 < n_tiles) pg_next = pp.bases();
         __syncthreads();
     }
 
@@ -383,6 +533,345 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
             *reinterpret_cast<half4*>(orow + db * 32 + 8 * g + 4 * hh) = r;
         }
     }
+}
+
+// ---- decode: one query row per sequence ------------------------------------------------
+//
+// One workgroup = (sequence, KV head, key split, chunk of <= 16 query heads).
+// The query heads that share the KV head are the 16 columns of
+// v_mfma_f32_16x16x32_f16 products, so each K/V row is read once for all of
+// them.  The 4 wavefronts stream disjoint 32-key steps of the split: K rows are
+// the A operand exactly as loaded (double-buffered in registers, no LDS); V
+// rows are transposed into a wavefront-private, double-buffered LDS area (LDS
+// operations of one wavefront complete in order, so no barrier is needed
+// there).  S^T = K.Q^T and O^T += V^T.P^T as in the prefill kernel; the
+// wavefronts are merged through LDS at the end.  With several splits the
+// merged partial (offset m, sum l, unnormalised O) goes to the workspace and
+// attn_decode_combine finishes each row.
+constexpr int kDecStep = 32;
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+template <int HD>
+struct Dec {
+    static constexpr int VS = kDecStep + 4;          // V^T row stride in LDS (halfs)
+    static constexpr int VBUF = HD * VS;              // one V^T stage (halfs)
+    static constexpr int WAVE_V = 2 * VBUF;           // double-buffered, per wavefront
+    static constexpr int NKK = HD / 32;               // k-steps over d for S^T
+    static constexpr int NDB = HD / 16;               // 16-row blocks of O^T
+    static constexpr int CH = HD / 8;                 // 16-byte chunks per row
+    static constexpr int KPL = HD / 16;               // V keys per lane per step
+    static constexpr int KG = kWave / CH;             // key groups in the V loader
+    static_assert(KG * KPL == kDecStep, "V step split");
+    static_assert(KPL % 4 == 0, "V^T writes are 4 keys wide");
+    static constexpr int PART = kAttnWaves * 16 * (HD + 2);   // floats of the merge area
+    static constexpr int SMEM_BYTES =
+        kAttnWaves * WAVE_V * 2 > PART * 4 ? kAttnWaves * WAVE_V * 2 : PART * 4;
+};
+
+template <int HD>
+struct DecK {
+    half8 k[2 * Dec<HD>::NKK];
+};
+template <int HD>
+struct DecV {
+    half8 v[Dec<HD>::KPL];
+};
+
+// K rows: lane feeds key k0 + 16*kb + lane%16, d = 32*kk + 8*(lane/16) .. +8.
+template <int HD, bool PAGED>
+__device__ __forceinline__ void dec_fetch_k(DecK<HD>& r, const AttnArgs& a, const Pages& pg,
+                                            int kvh, int k0, int k_end, uintptr_t dummy, int lane) {
+    using T = Dec<HD>;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+        const int j = k0 + 16 * kb + (lane & 15);
+        const uintptr_t row = j < k_end ? key_row<PAGED>(a, a.k, pg.k, kvh, k0, j, HD) : 0;
+        if (PAGED && pg.misaligned) {   // wavefront-uniform
+#pragma unroll
+            for (int kk = 0; kk < T::NKK; ++kk)
+                r.k[kb * T::NKK + kk] = load_chunk_unaligned(row, 4 * kk + (lane >> 4));
+        } else {
+#pragma unroll
+            for (int kk = 0; kk < T::NKK; ++kk)
+                r.k[kb * T::NKK + kk] = load_chunk(row, 4 * kk + (lane >> 4), dummy);
+        }
+    }
+}
+
+// V rows: lane owns chunk lane%CH of keys k0 + KPL*(lane/CH) + i.
+template <int HD, bool PAGED>
+__device__ __forceinline__ void dec_fetch_v(DecV<HD>& r, const AttnArgs& a, const Pages& pg,
+                                            int kvh, int k0, int k_end, uintptr_t dummy, int lane) {
+    using T = Dec<HD>;
+    const int ch = lane % T::CH, kg = lane / T::CH;
+    uintptr_t rows[T::KPL];
+#pragma unroll
+    for (int i = 0; i < T::KPL; ++i) {
+        const int j = k0 + T::KPL * kg + i;
+        rows[i] = j < k_end ? key_row<PAGED>(a, a.v, pg.v, kvh, k0, j, HD) : 0;
+    }
+    if (PAGED && pg.misaligned) {   // wavefront-uniform
+#pragma unroll
+        for (int i = 0; i < T::KPL; ++i) r.v[i] = load_chunk_unaligned(rows[i], ch);
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < T::KPL; ++i) r.v[i] = load_chunk(rows[i], ch, dummy);
+}
+
+// V^T stage: row d, keys KPL*kg + i.
+template <int HD>
+__device__ __forceinline__ void dec_stage_v(const DecV<HD>& r, _Float16* sv, int lane) {
+    using T = Dec<HD>;
+    const int ch = lane % T::CH, kg = lane / T::CH;
+#pragma unroll
+    for (int i = 0; i < T::KPL; i += 4)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            *reinterpret_cast<half4*>(sv + (ch * 8 + e) * T::VS + T::KPL * kg + i) =
+                half4{r.v[i][e], r.v[i + 1][e], r.v[i + 2][e], r.v[i + 3][e]};
+}
+
+struct DecState {
+    float m_run, l_run;
+};
+
+// One 32-key step: K operands in `kr`, V^T staged at sv.
+template <int HD>
+__device__ __forceinline__ void dec_step(const DecK<HD>& kr, const half8* qf, floatx4* o,
+                                         DecState& st, const _Float16* sv, int k0, int k_end,
+                                         int lane, float cl2) {
+    using T = Dec<HD>;
+    const int col = lane & 15, hq = lane >> 4;
+    floatx4 sc[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+        sc[kb] = floatx4{};
+#pragma unroll
+        for (int kk = 0; kk < T::NKK; ++kk)
+            sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kr.k[kb * T::NKK + kk], qf[kk], sc[kb],
+                                                            0, 0, 0);
+    }
+    // lane holds S^T[key = k0 + 16*kb + 4*hq + i][column col]
+    float mt = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (k0 + kDecStep > k_end) {
+                const int j = k0 + 16 * kb + 4 * hq + i;
+                sc[kb][i] = j < k_end ? sc[kb][i] : -INFINITY;
+            }
+            mt = fmaxf(mt, sc[kb][i]);
+        }
+    mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
+    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+    const float m_cand = fmaxf(st.m_run, mt);
+    if (__any((m_cand - st.m_run) * cl2 > 8.0f)) {
+        const float alpha = __builtin_amdgcn_exp2f((st.m_run - m_cand) * cl2);
+#pragma unroll
+        for (int db = 0; db < T::NDB; ++db) o[db] *= alpha;
+        st.l_run *= alpha;
+        st.m_run = m_cand;
+    }
+    const float moff = st.m_run * cl2;
+    half8 pf;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            pf[4 * kb + i] = from_f32<_Float16>(__builtin_amdgcn_exp2f(fmaf(sc[kb][i], cl2, -moff)));
+    float lsum = st.l_run;
+#pragma unroll
+    for (int e = 0; e < 8; e += 2)
+        lsum = __builtin_amdgcn_fdot2(half2v{pf[e], pf[e + 1]}, half2v{1.0f16, 1.0f16}, lsum, false);
+    st.l_run = lsum;
+    // O^T[d][col] += V^T[d][keys] P^T[keys][col]; MFMA k index 8*hq + e maps to
+    // key 4*hq + e (e < 4) and 16 + 4*hq + e - 4 (e >= 4), as in pf
+#pragma unroll
+    for (int db = 0; db < T::NDB; ++db) {
+        const _Float16* vrow = sv + (16 * db + col) * T::VS + 4 * hq;
+        const half4 lo = *reinterpret_cast<const half4*>(vrow);
+        const half4 hi = *reinterpret_cast<const half4*>(vrow + 16);
+        const half8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, o[db], 0, 0, 0);
+    }
+}
+
+// Query row, key count and block table of sequence s; false = nothing to do.
+template <bool PAGED>
+__device__ __forceinline__ bool dec_sequence(const AttnArgs& a, int s, int& q_row, int& kv_len,
+                                             const int32_t*& table) {
+    q_row = 0;
+    kv_len = a.kv_len;
+    table = nullptr;
+    if constexpr (PAGED) {
+        q_row = s;
+        if (a.cu_q) {
+            q_row = a.cu_q[s];
+            if (a.cu_q[s + 1] - q_row != 1) return false;
+        }
+        if (q_row < 0 || q_row >= a.n_q_rows) return false;
+        kv_len = a.ctx_lens[s];
+        if (kv_len > a.max_blocks * QL_PAGE_SIZE) kv_len = a.max_blocks * QL_PAGE_SIZE;
+        table = a.block_tables + (size_t)s * a.max_blocks;
+    }
+    if (kv_len < 0) kv_len = 0;
+    return true;
+}
+
+template <int HD, bool PAGED>
+__global__ __launch_bounds__(kAttnThreads, 2) void attn_decode(AttnArgs a) {
+    using T = Dec<HD>;
+    __shared__ __attribute__((aligned(16))) char smem_raw[T::SMEM_BYTES];
+    const int s = blockIdx.z, kvh = blockIdx.y;
+    const int sp = (int)blockIdx.x % a.n_split, cg = (int)blockIdx.x / a.n_split;
+    // query heads h with h*n_kv_heads/n_heads == kvh: [ceil(kvh*H/Hkv), ceil((kvh+1)*H/Hkv))
+    const long long H = a.n_heads, HK = a.n_kv_heads;
+    const int h_lo = (int)((kvh * H + HK - 1) / HK);
+    const int h_hi = (int)(((kvh + 1) * H + HK - 1) / HK);
+    const int hb = h_lo + 16 * cg;
+    const int G = min(h_hi, hb + 16) - hb;
+    if (G <= 0) return;   // workgroup-uniform
+    int q_row, kv_len;
+    const int32_t* table;
+    if (!dec_sequence<PAGED>(a, s, q_row, kv_len, table)) return;
+    const int per = (kv_len + a.n_split - 1) / a.n_split;
+    const int chunk = (per + kAttnWaves * kDecStep - 1) / (kAttnWaves * kDecStep) * (kAttnWaves * kDecStep);
+    const int k_begin = sp * chunk;
+    const int k_end = min(kv_len, k_begin + chunk);
+    const int n_steps = k_end > k_begin ? (k_end - k_begin + kDecStep - 1) / kDecStep : 0;
+
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int col = lane & 15, hq = lane >> 4;
+    const bool col_ok = col < G;
+    half8 qf[T::NKK];
+    {
+        const _Float16* qrow = a.q + (size_t)q_row * a.q_stride + (size_t)(hb + (col_ok ? col : 0)) * HD;
+#pragma unroll
+        for (int kk = 0; kk < T::NKK; ++kk)
+            qf[kk] = col_ok ? *reinterpret_cast<const half8*>(qrow + 32 * kk + 8 * hq) : half8{};
+    }
+    floatx4 o[T::NDB];
+#pragma unroll
+    for (int i = 0; i < T::NDB; ++i) o[i] = floatx4{};
+    DecState st{-FLT_MAX, 0.0f};
+    const float cl2 = a.cl2;
+    _Float16* sv = reinterpret_cast<_Float16*>(smem_raw) + wave * T::WAVE_V;
+    const uintptr_t dummy = reinterpret_cast<uintptr_t>(a.q + (size_t)q_row * a.q_stride);
+
+    // wavefront w takes steps w, w+4, w+8, ...: K registers ping-pong between ka
+    // and kb; V goes through one register set into the other LDS stage; page
+    // bases flow through the 3-stage lookup, one step per stage
+    constexpr int kStride = kAttnWaves * kDecStep;
+    constexpr int kStepPages = kDecStep / QL_PAGE_SIZE;
+    DecK<HD> ka, kb;
+    DecV<HD> vr;
+    PagePipe<PAGED, kStepPages> pp;
+    int step = wave, stage = 0;
+    Pages pg_next{};
+    auto page_of = [&](int sidx) { return (k_begin + sidx * kDecStep) >> 4; };
+    if (step < n_steps) {
+        const int k0 = k_begin + step * kDecStep;
+        pp.entries(a, table, page_of(step));
+        pp.pointers(a, kvh, HD);
+        const Pages pg = pp.bases();
+        if (step + kAttnWaves < n_steps) {
+            pp.entries(a, table, page_of(step + kAttnWaves));
+            pp.pointers(a, kvh, HD);
+            pg_next = pp.bases();
+        }
+        if (step + 2 * kAttnWaves < n_steps) pp.entries(a, table, page_of(step + 2 * kAttnWaves));
+        dec_fetch_k<HD, PAGED>(ka, a, pg, kvh, k0, k_end, dummy, lane);
+        dec_fetch_v<HD, PAGED>(vr, a, pg, kvh, k0, k_end, dummy, lane);
+        dec_stage_v<HD>(vr, sv, lane);
+    }
+    // one step with K operands in `use`, prefetching the wavefront's next step into `fill`
+    auto run_step = [&](DecK<HD>& use, DecK<HD>& fill) -> bool {
+        const int k0 = k_begin + step * kDecStep;
+        const bool more = step + kAttnWaves < n_steps;
+        if (more) {
+            dec_fetch_k<HD, PAGED>(fill, a, pg_next, kvh, k0 + kStride, k_end, dummy, lane);
+            dec_fetch_v<HD, PAGED>(vr, a, pg_next, kvh, k0 + kStride, k_end, dummy, lane);
+        }
+        if (step + 2 * kAttnWaves < n_steps) pp.pointers(a, kvh, HD);
+        if (step + 3 * kAttnWaves < n_steps) pp.entries(a, table, page_of(step + 3 * kAttnWaves));
+        dec_step<HD>(use, qf, o, st, sv + stage * T::VBUF, k0, k_end, lane, cl2);
+        if (!more) return false;
+        stage ^= 1;
+        dec_stage_v<HD>(vr, sv + stage * T::VBUF, lane);
+        if (step + 2 * kAttnWaves < n_steps) pg_next = pp.bases();
+        step += kAttnWaves;
+        return true;
+    };
+    while (step < n_steps) {
+        if (!run_step(ka, kb)) break;
+        if (!run_step(kb, ka)) break;
+    }
+
+    // merge the wavefronts: the 4 lanes of a column share m_run, so their sums add
+    float l_tot = st.l_run + __shfl_xor(st.l_run, 16, kWave);
+    l_tot += __shfl_xor(l_tot, 32, kWave);
+    __syncthreads();   // every wavefront is done with its V^T staging
+    float* part = reinterpret_cast<float*>(smem_raw);   // [wave][column][HD + 2]
+    {
+        float* pw = part + (wave * 16 + col) * (HD + 2);
+#pragma unroll
+        for (int db = 0; db < T::NDB; ++db)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) pw[16 * db + 4 * hq + i] = o[db][i];
+        if (hq == 0) {
+            pw[HD] = st.m_run;
+            pw[HD + 1] = l_tot;
+        }
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < G * HD; e += kAttnThreads) {
+        const int c = e / HD, d = e % HD;
+        float mstar = -FLT_MAX;
+#pragma unroll
+        for (int w = 0; w < kAttnWaves; ++w) mstar = fmaxf(mstar, part[(w * 16 + c) * (HD + 2) + HD]);
+        float acc = 0.0f, lsum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kAttnWaves; ++w) {
+            const float* pp = part + (w * 16 + c) * (HD + 2);
+            const float f = __builtin_amdgcn_exp2f((pp[HD] - mstar) * cl2);
+            acc = fmaf(f, pp[d], acc);
+            lsum = fmaf(f, pp[HD + 1], lsum);
+        }
+        const int h = hb + c;
+        if (a.n_split == 1) {
+            a.out[(size_t)q_row * a.o_stride + (size_t)h * HD + d] = from_f32<_Float16>(acc / (lsum + 1e-8f));
+        } else {
+            float* w = a.ws + (((size_t)s * a.n_heads + h) * a.n_split + sp) * (HD + 2);
+            w[d] = acc;
+            if (d == 0) {
+                w[HD] = mstar;
+                w[HD + 1] = lsum;
+            }
+        }
+    }
+}
+
+// Finish split decode rows: out = sum_s 2^((m_s - m*)c) O_s / (sum_s 2^((m_s - m*)c) l_s + 1e-8).
+template <int HD, bool PAGED>
+__global__ __launch_bounds__(HD) void attn_decode_combine(AttnArgs a) {
+    const int h = blockIdx.x, s = blockIdx.y, d = threadIdx.x;
+    int q_row, kv_len;
+    const int32_t* table;
+    if (!dec_sequence<PAGED>(a, s, q_row, kv_len, table)) return;
+    const float* w = a.ws + ((size_t)s * a.n_heads + h) * a.n_split * (HD + 2);
+    float mstar = -FLT_MAX;
+    for (int sp = 0; sp < a.n_split; ++sp) mstar = fmaxf(mstar, w[sp * (HD + 2) + HD]);
+    float acc = 0.0f, lsum = 0.0f;
+    for (int sp = 0; sp < a.n_split; ++sp) {
+        const float* pp = w + sp * (HD + 2);
+        const float f = __builtin_amdgcn_exp2f((pp[HD] - mstar) * a.cl2);
+        acc = fmaf(f, pp[d], acc);
+        lsum = fmaf(f, pp[HD + 1], lsum);
+    }
+    a.out[(size_t)q_row * a.o_stride + (size_t)h * HD + d] = from_f32<_Float16>(acc / (lsum + 1e-8f));
 }
 
 float scale_log2e(int head_dim) {
@@ -406,6 +895,45 @@ bool aligned_rows(const void* p, int64_t stride) {
     return qlh::aligned16(p) && stride % 8 == 0;
 }
 
+// Decode launch shape: chunks of <= 16 query heads per KV head, and key splits
+// so that about 512 workgroups are in flight (2 per CU), each split covering
+// at least 256 keys.
+int dec_col_chunks(int n_heads, int n_kv_heads) {
+    const int gmax = (n_heads + n_kv_heads - 1) / n_kv_heads;
+    return (gmax + 15) / 16;
+}
+
+int dec_splits(int n_seqs, int n_kv_heads, int n_cg, int max_ctx) {
+    const long long base = (long long)n_seqs * n_kv_heads * n_cg;
+    const long long want = (512 + base - 1) / base;
+    const long long cap = ((long long)max_ctx + 255) / 256;
+    long long n = want < cap ? want : cap;
+    if (n > 128) n = 128;
+    return n < 1 ? 1 : (int)n;
+}
+
+size_t dec_ws_bytes(int n_seqs, int n_heads, int head_dim, int n_split) {
+    return n_split > 1 ? (size_t)n_seqs * n_heads * n_split * (head_dim + 2) * sizeof(float) : 0;
+}
+
+template <bool PAGED>
+hipError_t launch_decode(const AttnArgs& a, int head_dim, int n_seqs, hipStream_t stream) {
+    const int n_cg = dec_col_chunks(a.n_heads, a.n_kv_heads);
+    QL_CHECK_ARG((long long)a.n_split * n_cg <= INT32_MAX);
+    const dim3 grid((unsigned)(a.n_split * n_cg), (unsigned)a.n_kv_heads, (unsigned)n_seqs);
+    const dim3 cgrid((unsigned)a.n_heads, (unsigned)n_seqs);
+    if (head_dim == 128) {
+        hipLaunchKernelGGL((attn_decode<128, PAGED>), grid, dim3(kAttnThreads), 0, stream, a);
+        if (a.n_split > 1)
+            hipLaunchKernelGGL((attn_decode_combine<128, PAGED>), cgrid, dim3(128), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL((attn_decode<64, PAGED>), grid, dim3(kAttnThreads), 0, stream, a);
+        if (a.n_split > 1)
+            hipLaunchKernelGGL((attn_decode_combine<64, PAGED>), cgrid, dim3(64), 0, stream, a);
+    }
+    return hipGetLastError();
+}
+
 }  // namespace
 
 extern "C" hipError_t ql_attention_f16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
@@ -419,6 +947,7 @@ extern "C" hipError_t ql_attention_f16(const uint16_t* q, const uint16_t* k, con
     QL_CHECK_ARG(q_row_stride >= (int64_t)n_heads * head_dim);
     QL_CHECK_ARG(out_row_stride >= (int64_t)n_heads * head_dim);
     QL_CHECK_ARG(kv_row_stride >= (int64_t)n_kv_heads * head_dim);
+    QL_CHECK_ARG(kv_row_stride < (int64_t)1 << 24);   // 64 key rows span < 4 GiB (32-bit offsets)
     if (q_len == 0) return hipSuccess;
     QL_CHECK_ARG(q && out && (kv_len == 0 || (k && v)));
     QL_CHECK_ARG(aligned_rows(q, q_row_stride) && aligned_rows(out, out_row_stride));
@@ -437,6 +966,10 @@ extern "C" hipError_t ql_attention_f16(const uint16_t* q, const uint16_t* k, con
     a.k = reinterpret_cast<const _Float16*>(k);
     a.v = reinterpret_cast<const _Float16*>(v);
     a.kv_stride = kv_row_stride;
+    if (q_len == 1) {   // decode: the query heads of a KV head share one pass over K/V
+        a.n_split = 1;
+        return launch_decode<false>(a, head_dim, 1, stream);
+    }
     return launch_attn<false>(a, head_dim, qlh::blocks_for(q_len, kBQ), 1, stream);
 }
 
@@ -486,5 +1019,65 @@ extern "C" hipError_t ql_paged_attention_f16(
     a.ctx_lens = ctx_lens;
     a.n_q_rows = n_q_rows;
     a.layer = layer;
+    if (max_q_len == 1) {   // every sequence decodes one token
+        a.n_split = 1;
+        return launch_decode<true>(a, head_dim, n_seqs, stream);
+    }
     return launch_attn<true>(a, head_dim, qlh::blocks_for(max_q_len, kBQ), (unsigned)n_seqs, stream);
+}
+
+extern "C" hipError_t ql_paged_decode_workspace_size(int n_seqs, int n_heads, int n_kv_heads,
+                                                     int head_dim, int max_ctx_len, size_t* bytes) {
+    QL_CHECK_ARG(bytes && n_seqs >= 0 && n_heads > 0 && n_kv_heads > 0 && n_kv_heads <= n_heads);
+    QL_CHECK_ARG((head_dim == 64 || head_dim == 128) && max_ctx_len >= 0);
+    *bytes = 0;
+    if (n_seqs == 0) return hipSuccess;
+    const int n_split = dec_splits(n_seqs, n_kv_heads, dec_col_chunks(n_heads, n_kv_heads), max_ctx_len);
+    *bytes = dec_ws_bytes(n_seqs, n_heads, head_dim, n_split);
+    return hipSuccess;
+}
+
+extern "C" hipError_t ql_paged_decode_attention_f16(
+    const uint16_t* q, uint16_t* out, int64_t q_row_stride, int64_t out_row_stride, int n_seqs,
+    const int32_t* ctx_lens, int max_ctx_len, const int32_t* block_tables, int max_blocks_per_seq,
+    const uint16_t* const* k_blocks, const uint16_t* const* v_blocks, int n_blocks, int layer,
+    int n_layers, int n_heads, int n_kv_heads, int head_dim, void* workspace,
+    size_t workspace_bytes, hipStream_t stream) {
+    QL_CHECK_ARG(n_seqs >= 0 && n_seqs <= 65535 && max_ctx_len >= 0);
+    QL_CHECK_ARG(n_heads > 0 && n_kv_heads > 0 && n_kv_heads <= n_heads && n_heads <= 65535);
+    QL_CHECK_ARG(head_dim == 64 || head_dim == 128);
+    QL_CHECK_ARG(n_layers > 0 && layer >= 0 && layer < n_layers);
+    QL_CHECK_ARG(max_blocks_per_seq >= 0 && max_blocks_per_seq <= (INT32_MAX / QL_PAGE_SIZE));
+    QL_CHECK_ARG(n_blocks >= 0);
+    QL_CHECK_ARG(q_row_stride >= (int64_t)n_heads * head_dim);
+    QL_CHECK_ARG(out_row_stride >= (int64_t)n_heads * head_dim);
+    QL_CHECK_ARG(workspace_bytes == 0 || workspace);
+    if (n_seqs == 0) return hipSuccess;
+    QL_CHECK_ARG(q && out && ctx_lens);
+    QL_CHECK_ARG(max_blocks_per_seq == 0 || (block_tables && k_blocks && v_blocks));
+    QL_CHECK_ARG(aligned_rows(q, q_row_stride) && aligned_rows(out, out_row_stride));
+    AttnArgs a{};
+    a.q = reinterpret_cast<const _Float16*>(q);
+    a.out = reinterpret_cast<_Float16*>(out);
+    a.q_stride = q_row_stride;
+    a.o_stride = out_row_stride;
+    a.n_heads = n_heads;
+    a.n_kv_heads = n_kv_heads;
+    a.cl2 = scale_log2e(head_dim);
+    a.causal = 1;
+    a.kb = reinterpret_cast<const _Float16* const*>(k_blocks);
+    a.vb = reinterpret_cast<const _Float16* const*>(v_blocks);
+    a.n_blocks = n_blocks;
+    a.block_tables = block_tables;
+    a.max_blocks = max_blocks_per_seq;
+    a.cu_q = nullptr;   // sequence s owns query row s
+    a.ctx_lens = ctx_lens;
+    a.n_q_rows = n_seqs;
+    a.layer = layer;
+    // as many key splits as wanted and the workspace holds (1 = no workspace used)
+    int n_split = dec_splits(n_seqs, n_kv_heads, dec_col_chunks(n_heads, n_kv_heads), max_ctx_len);
+    while (n_split > 1 && dec_ws_bytes(n_seqs, n_heads, head_dim, n_split) > workspace_bytes) --n_split;
+    a.n_split = n_split;
+    a.ws = n_split > 1 ? static_cast<float*>(workspace) : nullptr;
+    return launch_decode<true>(a, head_dim, n_seqs, stream);
 }

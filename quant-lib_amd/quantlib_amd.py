@@ -60,6 +60,9 @@ SIGNATURES = {
     "ql_attention_f16": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _i64, _i64, _i64, _i, _p],
     "ql_paged_attention_f16": [_p, _p, _i64, _i64, _i, _i, _p, _p, _i, _p, _i, _p, _p, _i, _i, _i,
                                _i, _i, _i, _i, _p],
+    "ql_paged_decode_workspace_size": [_i, _i, _i, _i, _i, _p],
+    "ql_paged_decode_attention_f16": [_p, _p, _i64, _i64, _i, _p, _i, _p, _i, _p, _p, _i, _i, _i,
+                                      _i, _i, _i, _p, ctypes.c_size_t, _p],
 }
 
 HIP_SUCCESS = 0

@@ -133,10 +133,30 @@ P = 4096  # a non-null, 16-byte aligned dummy address: never dereferenced on the
       None), INVALID),
     (("ql_paged_attention_f16", None, None, 512, 512, 0, 0, None, None, 0, None, 0, None, None, 0,
       0, 2, 8, 2, 64, 1, None), 0),
+    # paged decode: workspace bytes without a pointer, head_dim 96, no sequences
+    (("ql_paged_decode_attention_f16", P, P, 512, 512, 2, P, 100, P, 8, P, P, 8, 0, 1, 8, 2, 64,
+      None, 4096, None), INVALID),
+    (("ql_paged_decode_attention_f16", P, P, 768, 768, 2, P, 100, P, 8, P, P, 8, 0, 1, 8, 2, 96,
+      None, 0, None), INVALID),
+    (("ql_paged_decode_attention_f16", None, None, 512, 512, 0, None, 0, None, 0, None, None, 0, 0,
+      1, 8, 2, 64, None, 0, None), 0),
+    (("ql_paged_decode_workspace_size", 4, 8, 2, 64, 100, None), INVALID),
 ])
 def test_argument_validation(call, expect):
     name, *args = call
     assert ql.raw(name, *args) == expect
+
+
+def test_decode_workspace_size_host_query():
+    size = ctypes.c_size_t(123)
+    assert ql.raw("ql_paged_decode_workspace_size", 0, 32, 8, 128, 4096, ctypes.addressof(size)) == 0
+    assert size.value == 0
+    # one sequence, 8 KV heads: split so ~512 workgroups run; each split >= 256 keys
+    assert ql.raw("ql_paged_decode_workspace_size", 1, 32, 8, 128, 8192, ctypes.addressof(size)) == 0
+    assert size.value == 1 * 32 * 32 * 130 * 4
+    # enough sequences to fill the GPU in one pass: no workspace
+    assert ql.raw("ql_paged_decode_workspace_size", 64, 32, 8, 128, 8192, ctypes.addressof(size)) == 0
+    assert size.value == 0
 
 
 def test_paged_slot_mapping_host_helper():

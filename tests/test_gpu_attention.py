@@ -185,7 +185,8 @@ def test_paged_attention_varlen_matches_contiguous_and_oracle(h, hkv, d):
         ref = Out(qn[s] * h * d, np.uint16)
         ql.call("ql_attention_f16", dqs.ptr, dks.ptr, dvs.ptr, ref.ptr, qn[s], ctx[s], h, hkv, d,
                 h * d, hkv * d, h * d, 1, stream())
-        assert np.array_equal(mine, ref.get((qn[s], h, d))), f"paged != contiguous, sequence {s}"
+        if qn[s] > 1:   # (a one-query call runs the decode kernel: compared to the oracle only)
+            assert np.array_equal(mine, ref.get((qn[s], h, d))), f"paged != contiguous, sequence {s}"
         want = orc.attention(qs[s], ks[s], vs[s], h, hkv, True, f16=True)
         check_attn(mine, want, vs[s], f"paged attention sequence {s}")
 
@@ -244,3 +245,91 @@ def test_attention_c5_prefill_sampled_rows_and_paged_equivalence():
     ql.call("ql_paged_attention_f16", dq.ptr, out2.ptr, h * d, h * d, T, 1, dcu.ptr, dctx.ptr, T,
             dbt.ptr, nb, pool.kptrs.ptr, pool.vptrs.ptr, nb, layer, L, h, hkv, d, 1, stream())
     assert np.array_equal(out2.get((T, h, d)), got)
+
+
+# ---- decode (one query per sequence) ------------------------------------------------------
+@pytest.mark.parametrize("h,hkv,d", [(32, 8, 128), (32, 1, 128), (6, 4, 64), (4, 4, 64),
+                                     (40, 8, 128)])
+@pytest.mark.parametrize("kv_len", [1, 31, 32, 33, 500, 2049])
+def test_decode_contiguous_gqa_groups(h, hkv, d, kv_len):
+    # q_len = 1 runs the decode kernel: query heads grouped per KV head (32/1: two
+    # 16-head column chunks; 6/4: groups of 2,1,2,1 heads; 40/8: 5 per group)
+    q, k, v = qkv(kv_len * 3 + h, 1, kv_len, h, hkv, d, 2.0)
+    out = Out(h * d, np.uint16)
+    dq, dk, dv = dev(q), dev(k), dev(v)
+    ql.call("ql_attention_f16", ptr(dq), ptr(dk), ptr(dv), out.ptr, 1, kv_len, h, hkv, d, h * d,
+            hkv * d, h * d, 1, stream())
+    check_attn(out.get((1, h, d)), orc.attention(q, k, v, h, hkv, True, f16=True), v,
+               f"decode h={h}/{hkv} d={d} kv={kv_len}")
+
+
+def _decode_setup(ctx, h, hkv, d, L, layer, seed):
+    r = np.random.default_rng(seed)
+    need = [(c + 15) // 16 for c in ctx]
+    nb = sum(need) + 2
+    perm = r.permutation(nb)
+    max_blocks = max(need + [1])
+    bt = np.full((len(ctx), max_blocks), -1, np.int32)
+    o = 0
+    pool = PagedPool(nb, L, hkv, d)
+    ks, vs = [], []
+    for s, c in enumerate(ctx):
+        bt[s, :need[s]] = perm[o:o + need[s]]
+        o += need[s]
+        k = to_f16_bits(normal(seed + 10 * s + 1, (c, hkv, d)))
+        v = to_f16_bits(normal(seed + 10 * s + 2, (c, hkv, d)))
+        pool.append(bt[s], k, v, layer)
+        ks.append(k)
+        vs.append(v)
+    q = to_f16_bits(normal(seed + 5, (len(ctx), h, d), 2.0))
+    return pool, bt, ks, vs, q
+
+
+@pytest.mark.parametrize("h,hkv,d", [(32, 8, 128), (8, 2, 64), (32, 1, 128)])
+def test_paged_decode_splits_and_one_pass_agree_with_oracle(h, hkv, d):
+    ctx = [0, 1, 17, 100, 1000, 4096, 33, 130]
+    L, layer = 3, 2
+    pool, bt, ks, vs, q = _decode_setup(ctx, h, hkv, d, L, layer, h * d + hkv)
+    S, max_blocks = len(ctx), bt.shape[1]
+    dq, dctx, dbt = dev(q), dev(np.array(ctx, np.int32)), dev(bt)
+    size = ctypes.c_size_t()
+    ql.call("ql_paged_decode_workspace_size", S, h, hkv, d, max(ctx), ctypes.addressof(size))
+    assert size.value > 0
+    results = {}
+    for label, nbytes in [("one pass", 0), ("full", size.value), ("partial", size.value // 3)]:
+        ws = empty((max(nbytes, 1),), np.uint8, fill_bits=0x7F) if nbytes else None
+        out = Out(S * h * d, np.uint16)
+        ql.call("ql_paged_decode_attention_f16", dq.ptr, out.ptr, h * d, h * d, S, dctx.ptr,
+                max(ctx), dbt.ptr, max_blocks, pool.kptrs.ptr, pool.vptrs.ptr, pool.nb, layer, L,
+                h, hkv, d, ws.ptr if ws else None, nbytes, stream())
+        got = out.get((S, h, d))
+        for s in range(S):
+            want = orc.attention(q[s:s + 1], ks[s], vs[s], h, hkv, True, f16=True)
+            check_attn(got[s:s + 1], want, vs[s], f"decode {label} seq {s} ctx {ctx[s]}")
+        results[label] = got
+    # the varlen entry point with one query per sequence runs the same one-pass kernel
+    out = Out(S * h * d, np.uint16)
+    dcu = dev(np.arange(S + 1, dtype=np.int32))
+    ql.call("ql_paged_attention_f16", dq.ptr, out.ptr, h * d, h * d, S, S, dcu.ptr, dctx.ptr, 1,
+            dbt.ptr, max_blocks, pool.kptrs.ptr, pool.vptrs.ptr, pool.nb, layer, L, h, hkv, d, 1,
+            stream())
+    assert np.array_equal(out.get((S, h, d)), results["one pass"])
+
+
+def test_paged_decode_batch_c5_heads_long_context():
+    # 16 sequences x 4096-token contexts, Llama-3-8B heads, split over the workspace
+    S, C, h, hkv, d, L, layer = 16, 4096, 32, 8, 128, 2, 1
+    ctx = [C - 37 * i for i in range(S)]
+    pool, bt, ks, vs, q = _decode_setup(ctx, h, hkv, d, L, layer, 0x51A10080)
+    dq, dctx, dbt = dev(q), dev(np.array(ctx, np.int32)), dev(bt)
+    size = ctypes.c_size_t()
+    ql.call("ql_paged_decode_workspace_size", S, h, hkv, d, C, ctypes.addressof(size))
+    ws = empty((size.value,), np.uint8)
+    out = Out(S * h * d, np.uint16)
+    ql.call("ql_paged_decode_attention_f16", dq.ptr, out.ptr, h * d, h * d, S, dctx.ptr, C,
+            dbt.ptr, bt.shape[1], pool.kptrs.ptr, pool.vptrs.ptr, pool.nb, layer, L, h, hkv, d,
+            ws.ptr, size.value, stream())
+    got = out.get((S, h, d))
+    for s in range(S):
+        check_attn(got[s:s + 1], orc.attention(q[s:s + 1], ks[s], vs[s], h, hkv, True, f16=True),
+                   vs[s], f"decode seq {s}")
