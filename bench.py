@@ -25,6 +25,13 @@ reported under "kernels".  The roofline entry is for the dominant kernel,
 SwiGLU fp16 [8192 x 14336]: 3 x 8192 x 14336 x 2 B = 704,643,072 B per launch,
 timed with HIP events around each of its launches on the work stream.
 
+`--all-configs` times every BASELINE config (C1-C5) one kernel at a time and
+adds the attention that consumes the path's output: causal prefill over the
+8192 tokens (contiguous, and over the paged pool the chain writes), reported in
+TFLOP/s against the dense fp16 matrix peak, and paged decode (64 sequences x
+4096 tokens; 1 sequence x 8192 tokens with the key-split workspace), HBM-bound
+on the K/V rows.
+
 Device memory, the stream and events come from libamdhip64 through the
 library's own binding (quant-lib_amd/quantlib_amd.py); no framework runtime is
 loaded.
@@ -32,6 +39,7 @@ loaded.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import pathlib
 import sys
@@ -41,6 +49,7 @@ ROOT = pathlib.Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "quant-lib_amd"))
 
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E peak, GB/s
+PEAK_MFMA_F16_TFLOPS = 2500.0  # MI355X dense fp16 matrix peak, TFLOP/s
 T, D, HQ, HKV, HD, F = 8192, 4096, 32, 8, 128, 14336
 VOCAB, THETA, EPS, L_POOL, PAGE = 32000, 5e5, 1e-5, 32, 16
 NSETS = 3
@@ -356,6 +365,84 @@ def all_configs(ql, np, reps):
         gbs = BYTES[name] / (us * 1e-6) / 1e9
         rows.append({"config": "C5 T=8192 llama3-8b", "kernel": name, "bytes": BYTES[name],
                      "us": round(us, 2), "GBps": round(gbs, 1), "frac_peak": round(gbs / PEAK_HBM_GBS, 4)})
+    rows += attention_rows(ql, np, chain, reps)
+    return rows
+
+
+def attention_rows(ql, np, chain, reps):
+    """Attention over the C5 shapes: causal prefill of the 8192 tokens (contiguous
+    Q/K/V and the paged pool the chain writes) -- MFMA-bound, reported in TFLOP/s
+    against the dense fp16 peak -- and paged decode, HBM-bound on the K/V rows."""
+    st = chain.stream
+    rows = []
+
+    def timed(launch, n):
+        for i in range(3):
+            launch(i)
+        ql.synchronize()
+        a, b = ql.Event(), ql.Event()
+        a.record(st)
+        for i in range(n):
+            launch(i)
+        b.record(st)
+        return a.elapsed_ms(b) * 1e3 / n
+
+    for layer in range(L_POOL):   # every layer of the pool holds K/V rows
+        chain.k_paged(chain.sets[layer % NSETS], layer)
+    flops = 4.0 * (T * (T + 1) / 2) * HD * HQ
+    io = 2 * T * HQ * HD * 2 + 2 * T * HKV * HD * 2
+    out = [ql.DeviceArray((T, HQ * HD), np.uint16) for _ in range(2)]
+    up = ql.DeviceArray.from_numpy
+    cu, ctx, table = up(np.array([0, T], np.int32)), up(np.array([T], np.int32)), \
+        up(np.arange(chain.nb, dtype=np.int32))
+    n_att = max(3, reps // 10)
+    us = timed(lambda i: ql.call("ql_flash_attention_f16", chain.sets[i % NSETS]["q"].ptr,
+                                 chain.sets[i % NSETS]["k"].ptr, chain.sets[i % NSETS]["v"].ptr,
+                                 out[i % 2].ptr, T, HQ, HKV, HD, 1, st), n_att)
+    rows.append({"config": "C5 attention prefill T=8192 causal", "kernel": "flash_attention_f16",
+                 "bytes": io, "us": round(us, 2), "GBps": round(io / (us * 1e-6) / 1e9, 1),
+                 "frac_peak": round(io / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+                 "tflops": round(flops / (us * 1e-6) / 1e12, 1),
+                 "frac_mfma_peak": round(flops / (us * 1e-6) / 1e12 / PEAK_MFMA_F16_TFLOPS, 4)})
+    us = timed(lambda i: ql.call("ql_paged_attention_f16", chain.sets[i % NSETS]["q"].ptr,
+                                 out[i % 2].ptr, HQ * HD, HQ * HD, T, 1, cu.ptr, ctx.ptr, T, table.ptr,
+                                 chain.nb, chain.kptrs.ptr, chain.vptrs.ptr, chain.nb, i % L_POOL,
+                                 L_POOL, HQ, HKV, HD, 1, st), n_att)
+    rows.append({"config": "C5 attention prefill T=8192 causal", "kernel": "paged_attention_f16",
+                 "bytes": io, "us": round(us, 2), "GBps": round(io / (us * 1e-6) / 1e9, 1),
+                 "frac_peak": round(io / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+                 "tflops": round(flops / (us * 1e-6) / 1e12, 1),
+                 "frac_mfma_peak": round(flops / (us * 1e-6) / 1e12 / PEAK_MFMA_F16_TFLOPS, 4)})
+    del out
+    # decode: S sequences x C context tokens, Llama-3-8B heads, pool of L_POOL layers
+    r = np.random.default_rng(11)
+    for S, C in ((64, 4096), (1, 8192)):
+        nbs = C // PAGE
+        nb = S * nbs
+        blk = L_POOL * PAGE * HKV * HD
+        kpool = ql.DeviceArray((nb * blk,), np.uint16)
+        vpool = ql.DeviceArray((nb * blk,), np.uint16)
+        kpool.fill_bytes(0x3C)   # every element 1.0078125: finite, no NaN from unwritten rows
+        vpool.fill_bytes(0x3C)
+        kp = up(np.array([kpool.ptr + 2 * blk * b for b in range(nb)], np.int64))
+        vp = up(np.array([vpool.ptr + 2 * blk * b for b in range(nb)], np.int64))
+        q = up(r.standard_normal((S, HQ * HD), dtype=np.float32).astype(np.float16).view(np.uint16))
+        o = ql.DeviceArray((S, HQ * HD), np.uint16)
+        ctxs = up(np.full(S, C, np.int32))
+        bt = up(r.permutation(nb).astype(np.int32).reshape(S, nbs))
+        size = ctypes.c_size_t()
+        ql.call("ql_paged_decode_workspace_size", S, HQ, HKV, HD, C, ctypes.addressof(size))
+        ws = ql.DeviceArray((max(size.value, 16),), np.uint8)
+        kv_bytes = S * C * HKV * HD * 2 * 2
+        us = timed(lambda i: ql.call("ql_paged_decode_attention_f16", q.ptr, o.ptr, HQ * HD, HQ * HD, S,
+                                     ctxs.ptr, C, bt.ptr, nbs, kp.ptr, vp.ptr, nb, i % L_POOL, L_POOL,
+                                     HQ, HKV, HD, ws.ptr, size.value, st), max(3, reps // 5))
+        gbs = (kv_bytes + 2 * S * HQ * HD * 2) / (us * 1e-6) / 1e9
+        rows.append({"config": f"decode {S} seq x {C} ctx (paged, {L_POOL}-layer blocks)",
+                     "kernel": "paged_decode_attention_f16", "bytes": kv_bytes + 2 * S * HQ * HD * 2,
+                     "us": round(us, 2), "GBps": round(gbs, 1), "frac_peak": round(gbs / PEAK_HBM_GBS, 4),
+                     "splits_workspace_bytes": size.value})
+        del kpool, vpool, ws
     return rows
 
 
@@ -378,7 +465,9 @@ def main():
         print("| config | kernel | algorithmic bytes | us per launch | GB/s | % of 8 TB/s |")
         print("|---|---|---|---|---|---|")
         for r_ in rows:
-            print(f"| {r_['config']} | {r_['kernel']} | {r_['bytes']:,} | {r_['us']:.2f} | "
+            extra = (f" ({r_['tflops']:.0f} TFLOP/s, {100 * r_['frac_mfma_peak']:.1f}% of fp16 MFMA peak)"
+                     if "tflops" in r_ else "")
+            print(f"| {r_['config']} | {r_['kernel']}{extra} | {r_['bytes']:,} | {r_['us']:.2f} | "
                   f"{r_['GBps']:.0f} | {100 * r_['frac_peak']:.1f} |", flush=True)
         print(json.dumps({"all_configs": rows}), flush=True)
         return

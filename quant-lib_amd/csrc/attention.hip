@@ -195,7 +195,7 @@ __device__ __forceinline__ half8 load_chunk(uintptr_t row, int ch, uintptr_t dum
 
 // The same for page pointers that are not 16-byte aligned (caller-provided
 // pools): element-wise loads.  Used for a whole tile, chosen once per tile.
-__device__ __noinline__ half8 load_chunk_unaligned(uintptr_t row, int ch) {
+__device__ __forceinline__ half8 load_chunk_unaligned(uintptr_t row, int ch) {
     half8 r{};
     if (row != 0) {
         const _Float16* e = reinterpret_cast<const _Float16*>(row + 16 * (uintptr_t)ch);
@@ -578,11 +578,55 @@ struct DecV {
     half8 v[Dec<HD>::KPL];
 };
 
+// Per-lane constants of the decode loaders: byte offsets of the lane's K and V
+// chunks from their page base (paged) or from the step's first key row
+// (contiguous), and the page of the lane's V keys.
+template <int HD, bool PAGED>
+struct DecPlan {
+    using T = Dec<HD>;
+    uint32_t row_bytes;   // uniform
+    uint32_t k_off, v_off;  // the lane's first V key; key i adds i * row_bytes
+    int v_page;
+
+    __device__ __forceinline__ DecPlan(const AttnArgs& a, int kvh, int lane) {
+        row_bytes = PAGED ? (uint32_t)(a.n_kv_heads * HD * sizeof(_Float16))
+                          : (uint32_t)(a.kv_stride * sizeof(_Float16));
+        const uint32_t head_bytes = PAGED ? 0u : (uint32_t)(kvh * HD * sizeof(_Float16));
+        k_off = (uint32_t)(lane & 15) * row_bytes + head_bytes + 16u * (uint32_t)(lane >> 4);
+        const int ch = lane % T::CH, kg = lane / T::CH;
+        const int key = T::KPL * kg;   // its KPL keys stay inside one page
+        v_page = key >> 4;
+        v_off = (uint32_t)(PAGED ? (key & 15) : key) * row_bytes + head_bytes + 16u * ch;
+    }
+};
+
+// A full 32-key step whose two pages are present and aligned: no checks.
+template <bool PAGED>
+__device__ __forceinline__ bool dec_clean(const Pages& pg, int k0, int k_end) {
+    bool clean = k0 + kDecStep <= k_end;
+    if constexpr (PAGED) clean = clean && !pg.misaligned && pg.k[0] && pg.k[1] && pg.v[0] && pg.v[1];
+    return clean;
+}
+
 // K rows: lane feeds key k0 + 16*kb + lane%16, d = 32*kk + 8*(lane/16) .. +8.
 template <int HD, bool PAGED>
-__device__ __forceinline__ void dec_fetch_k(DecK<HD>& r, const AttnArgs& a, const Pages& pg,
-                                            int kvh, int k0, int k_end, uintptr_t dummy, int lane) {
+__device__ __forceinline__ void dec_fetch_k(DecK<HD>& r, const AttnArgs& a, const DecPlan<HD, PAGED>& plan,
+                                            const Pages& pg, int kvh, int k0, int k_end,
+                                            uintptr_t dummy, int lane) {
     using T = Dec<HD>;
+    if (dec_clean<PAGED>(pg, k0, k_end)) {   // wavefront-uniform
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            const uintptr_t base =
+                PAGED ? pg.k[kb]
+                      : reinterpret_cast<uintptr_t>(a.k) +
+                            (uintptr_t)(k0 + 16 * kb) * (uintptr_t)a.kv_stride * sizeof(_Float16);
+#pragma unroll
+            for (int kk = 0; kk < T::NKK; ++kk)
+                r.k[kb * T::NKK + kk] = *(GlobalHalf8Ptr)(base + plan.k_off + 64u * kk);
+        }
+        return;
+    }
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
         const int j = k0 + 16 * kb + (lane & 15);
@@ -601,26 +645,36 @@ __device__ __forceinline__ void dec_fetch_k(DecK<HD>& r, const AttnArgs& a, cons
 
 // V rows: lane owns chunk lane%CH of keys k0 + KPL*(lane/CH) + i.
 template <int HD, bool PAGED>
-__device__ __forceinline__ void dec_fetch_v(DecV<HD>& r, const AttnArgs& a, const Pages& pg,
-                                            int kvh, int k0, int k_end, uintptr_t dummy, int lane) {
+__device__ __forceinline__ void dec_fetch_v(DecV<HD>& r, const AttnArgs& a, const DecPlan<HD, PAGED>& plan,
+                                            const Pages& pg, int kvh, int k0, int k_end,
+                                            uintptr_t dummy, int lane) {
     using T = Dec<HD>;
+    if (dec_clean<PAGED>(pg, k0, k_end)) {   // wavefront-uniform
+        const uintptr_t base =
+            PAGED ? (plan.v_page == 0 ? pg.v[0] : pg.v[1])
+                  : reinterpret_cast<uintptr_t>(a.v) +
+                        (uintptr_t)k0 * (uintptr_t)a.kv_stride * sizeof(_Float16);
+#pragma unroll
+        for (int i = 0; i < T::KPL; ++i)
+            r.v[i] = *(GlobalHalf8Ptr)(base + plan.v_off + (uintptr_t)i * plan.row_bytes);
+        return;
+    }
     const int ch = lane % T::CH, kg = lane / T::CH;
-    uintptr_t rows[T::KPL];
+    const bool unaligned = PAGED && pg.misaligned;   // wavefront-uniform
 #pragma unroll
     for (int i = 0; i < T::KPL; ++i) {
         const int j = k0 + T::KPL * kg + i;
-        rows[i] = j < k_end ? key_row<PAGED>(a, a.v, pg.v, kvh, k0, j, HD) : 0;
+        const uintptr_t row = j < k_end ? key_row<PAGED>(a, a.v, pg.v, kvh, k0, j, HD) : 0;
+        r.v[i] = unaligned ? load_chunk_unaligned(row, ch) : load_chunk(row, ch, dummy);
     }
-    if (PAGED && pg.misaligned) {   // wavefront-uniform
-#pragma unroll
-        for (int i = 0; i < T::KPL; ++i) r.v[i] = load_chunk_unaligned(rows[i], ch);
-        return;
-    }
-#pragma unroll
-    for (int i = 0; i < T::KPL; ++i) r.v[i] = load_chunk(rows[i], ch, dummy);
 }
 
-// V^T stage: row d, keys KPL*kg + i.
+// V^T stage: row d, keys KPL*kg + i.  The 8-byte unit u (4 keys) of row r is
+// stored at unit u ^ ((r >> 4) & 7): with the 72-byte row stride both these
+// 4-key writes and the operand reads of dec_step hit 16 distinct bank pairs
+// per 16 lanes.
+__device__ __forceinline__ int vt_unit(int r, int u) { return u ^ ((r >> 4) & 7); }
+
 template <int HD>
 __device__ __forceinline__ void dec_stage_v(const DecV<HD>& r, _Float16* sv, int lane) {
     using T = Dec<HD>;
@@ -628,9 +682,11 @@ __device__ __forceinline__ void dec_stage_v(const DecV<HD>& r, _Float16* sv, int
 #pragma unroll
     for (int i = 0; i < T::KPL; i += 4)
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-            *reinterpret_cast<half4*>(sv + (ch * 8 + e) * T::VS + T::KPL * kg + i) =
+        for (int e = 0; e < 8; ++e) {
+            const int row = ch * 8 + e;
+            *reinterpret_cast<half4*>(sv + row * T::VS + 4 * vt_unit(row, (T::KPL * kg + i) >> 2)) =
                 half4{r.v[i][e], r.v[i + 1][e], r.v[i + 2][e], r.v[i + 3][e]};
+        }
 }
 
 struct DecState {
@@ -691,9 +747,10 @@ __device__ __forceinline__ void dec_step(const DecK<HD>& kr, const half8* qf, fl
     // key 4*hq + e (e < 4) and 16 + 4*hq + e - 4 (e >= 4), as in pf
 #pragma unroll
     for (int db = 0; db < T::NDB; ++db) {
-        const _Float16* vrow = sv + (16 * db + col) * T::VS + 4 * hq;
-        const half4 lo = *reinterpret_cast<const half4*>(vrow);
-        const half4 hi = *reinterpret_cast<const half4*>(vrow + 16);
+        const int row = 16 * db + col;
+        const _Float16* vrow = sv + row * T::VS;
+        const half4 lo = *reinterpret_cast<const half4*>(vrow + 4 * vt_unit(row, hq));
+        const half4 hi = *reinterpret_cast<const half4*>(vrow + 4 * vt_unit(row, 4 + hq));
         const half8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, o[db], 0, 0, 0);
     }
@@ -768,6 +825,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_decode(AttnArgs a) {
     constexpr int kStepPages = kDecStep / QL_PAGE_SIZE;
     DecK<HD> ka, kb;
     DecV<HD> vr;
+    const DecPlan<HD, PAGED> plan(a, kvh, lane);
     PagePipe<PAGED, kStepPages> pp;
     int step = wave, stage = 0;
     Pages pg_next{};
@@ -783,8 +841,8 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_decode(AttnArgs a) {
             pg_next = pp.bases();
         }
         if (step + 2 * kAttnWaves < n_steps) pp.entries(a, table, page_of(step + 2 * kAttnWaves));
-        dec_fetch_k<HD, PAGED>(ka, a, pg, kvh, k0, k_end, dummy, lane);
-        dec_fetch_v<HD, PAGED>(vr, a, pg, kvh, k0, k_end, dummy, lane);
+        dec_fetch_k<HD, PAGED>(ka, a, plan, pg, kvh, k0, k_end, dummy, lane);
+        dec_fetch_v<HD, PAGED>(vr, a, plan, pg, kvh, k0, k_end, dummy, lane);
         dec_stage_v<HD>(vr, sv, lane);
     }
     // one step with K operands in `use`, prefetching the wavefront's next step into `fill`
@@ -792,8 +850,8 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_decode(AttnArgs a) {
         const int k0 = k_begin + step * kDecStep;
         const bool more = step + kAttnWaves < n_steps;
         if (more) {
-            dec_fetch_k<HD, PAGED>(fill, a, pg_next, kvh, k0 + kStride, k_end, dummy, lane);
-            dec_fetch_v<HD, PAGED>(vr, a, pg_next, kvh, k0 + kStride, k_end, dummy, lane);
+            dec_fetch_k<HD, PAGED>(fill, a, plan, pg_next, kvh, k0 + kStride, k_end, dummy, lane);
+            dec_fetch_v<HD, PAGED>(vr, a, plan, pg_next, kvh, k0 + kStride, k_end, dummy, lane);
         }
         if (step + 2 * kAttnWaves < n_steps) pp.pointers(a, kvh, HD);
         if (step + 3 * kAttnWaves < n_steps) pp.entries(a, table, page_of(step + 3 * kAttnWaves));
@@ -855,23 +913,47 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_decode(AttnArgs a) {
 }
 
 // Finish split decode rows: out = sum_s 2^((m_s - m*)c) O_s / (sum_s 2^((m_s - m*)c) l_s + 1e-8).
+// One workgroup per (sequence, head): thread s < n_split reads split s's (m, l),
+// the weights go through LDS, then thread d sums its column with independent loads.
+constexpr int kMaxSplits = 128;
+
 template <int HD, bool PAGED>
-__global__ __launch_bounds__(HD) void attn_decode_combine(AttnArgs a) {
-    const int h = blockIdx.x, s = blockIdx.y, d = threadIdx.x;
+__global__ __launch_bounds__(kMaxSplits) void attn_decode_combine(AttnArgs a) {
+    __shared__ float wsc[kMaxSplits];
+    __shared__ float red[kMaxSplits];
+    __shared__ float lden;
+    const int h = blockIdx.x, s = blockIdx.y, tid = threadIdx.x;
     int q_row, kv_len;
     const int32_t* table;
     if (!dec_sequence<PAGED>(a, s, q_row, kv_len, table)) return;
-    const float* w = a.ws + ((size_t)s * a.n_heads + h) * a.n_split * (HD + 2);
-    float mstar = -FLT_MAX;
-    for (int sp = 0; sp < a.n_split; ++sp) mstar = fmaxf(mstar, w[sp * (HD + 2) + HD]);
-    float acc = 0.0f, lsum = 0.0f;
-    for (int sp = 0; sp < a.n_split; ++sp) {
-        const float* pp = w + sp * (HD + 2);
-        const float f = __builtin_amdgcn_exp2f((pp[HD] - mstar) * a.cl2);
-        acc = fmaf(f, pp[d], acc);
-        lsum = fmaf(f, pp[HD + 1], lsum);
+    const int ns = a.n_split;
+    const float* w = a.ws + ((size_t)s * a.n_heads + h) * ns * (HD + 2);
+    const float m_s = tid < ns ? w[tid * (HD + 2) + HD] : -FLT_MAX;
+    const float l_s = tid < ns ? w[tid * (HD + 2) + HD + 1] : 0.0f;
+    red[tid] = m_s;
+    __syncthreads();
+    for (int o = kMaxSplits / 2; o > 0; o >>= 1) {
+        if (tid < o) red[tid] = fmaxf(red[tid], red[tid + o]);
+        __syncthreads();
     }
-    a.out[(size_t)q_row * a.o_stride + (size_t)h * HD + d] = from_f32<_Float16>(acc / (lsum + 1e-8f));
+    const float mstar = red[0];
+    __syncthreads();
+    const float f = __builtin_amdgcn_exp2f((m_s - mstar) * a.cl2);
+    wsc[tid] = tid < ns ? f : 0.0f;
+    red[tid] = tid < ns ? f * l_s : 0.0f;
+    __syncthreads();
+    for (int o = kMaxSplits / 2; o > 0; o >>= 1) {
+        if (tid < o) red[tid] += red[tid + o];
+        __syncthreads();
+    }
+    if (tid == 0) lden = red[0] + 1e-8f;
+    __syncthreads();
+    for (int d = tid; d < HD; d += kMaxSplits) {
+        float acc = 0.0f;
+#pragma unroll 8
+        for (int sp = 0; sp < ns; ++sp) acc = fmaf(wsc[sp], w[sp * (HD + 2) + d], acc);
+        a.out[(size_t)q_row * a.o_stride + (size_t)h * HD + d] = from_f32<_Float16>(acc / lden);
+    }
 }
 
 float scale_log2e(int head_dim) {
@@ -908,7 +990,7 @@ int dec_splits(int n_seqs, int n_kv_heads, int n_cg, int max_ctx) {
     const long long want = (512 + base - 1) / base;
     const long long cap = ((long long)max_ctx + 255) / 256;
     long long n = want < cap ? want : cap;
-    if (n > 128) n = 128;
+    if (n > kMaxSplits) n = kMaxSplits;
     return n < 1 ? 1 : (int)n;
 }
 
@@ -925,11 +1007,11 @@ hipError_t launch_decode(const AttnArgs& a, int head_dim, int n_seqs, hipStream_
     if (head_dim == 128) {
         hipLaunchKernelGGL((attn_decode<128, PAGED>), grid, dim3(kAttnThreads), 0, stream, a);
         if (a.n_split > 1)
-            hipLaunchKernelGGL((attn_decode_combine<128, PAGED>), cgrid, dim3(128), 0, stream, a);
+            hipLaunchKernelGGL((attn_decode_combine<128, PAGED>), cgrid, dim3(kMaxSplits), 0, stream, a);
     } else {
         hipLaunchKernelGGL((attn_decode<64, PAGED>), grid, dim3(kAttnThreads), 0, stream, a);
         if (a.n_split > 1)
-            hipLaunchKernelGGL((attn_decode_combine<64, PAGED>), cgrid, dim3(64), 0, stream, a);
+            hipLaunchKernelGGL((attn_decode_combine<64, PAGED>), cgrid, dim3(kMaxSplits), 0, stream, a);
     }
     return hipGetLastError();
 }
