@@ -271,6 +271,79 @@ hipError_t ql_paged_decode_attention_f16(const uint16_t* q, uint16_t* out, int64
                                          int head_dim, void* workspace, size_t workspace_bytes,
                                          hipStream_t stream);
 
+/* ---- continuous batching over the paged pool (host only, no GPU calls) -------------
+ * The bookkeeping of the reference scheduler (scheduler_create / scheduler_add_request
+ * / scheduler_step, src/continuous_batch.cu:48-174, include/scheduler.h:6-54) over the
+ * LIFO block allocator of src/paged_kvcache.cu:49-53,89-98, with the model step left
+ * to the caller and every active sequence served by ONE batched step:
+ *   ql_batcher_plan   admits pending requests (FIFO; the head waits until
+ *                     ceil(prompt_len/16) blocks are free and fewer than max_active
+ *                     run -- head-of-line blocking), gives a decoding sequence a new
+ *                     block when its next position starts one (evicting it, finished
+ *                     early, when none is free), and lists the step's work: per
+ *                     sequence in active order its query rows (whole prompt for a
+ *                     prefill, the newest token for a decode) with token ids,
+ *                     positions and KV slots, plus cu_q_lens / ctx_lens /
+ *                     block_tables for ql_paged_attention_f16 and slot_mapping for
+ *                     ql_rope_paged_kv_append_f16 / ql_paged_kv_append_f16;
+ *   ql_batcher_commit takes the sampled token of each planned sequence (the logits
+ *                     of row sample_rows[i]), finishes sequences at prompt_len + max_gen
+ *                     tokens or at eos_token, and returns their blocks (table order,
+ *                     swap-with-last removal from the active list, as the reference).
+ * Plans and commits alternate.  Plan arrays are host memory owned by the batcher,
+ * valid until the next ql_batcher_plan.  Difference from the reference: the token
+ * sampled after the prefill is kept as the first generated token (the reference's
+ * stub forward discards it), so a request finishes one step earlier; growth and
+ * eviction happen at the same positions. */
+#define QL_FINISH_LENGTH  0   /* reached prompt_len + max_gen tokens */
+#define QL_FINISH_EOS     1   /* sampled eos_token */
+#define QL_FINISH_EVICTED 2   /* no free block for its next position */
+
+typedef struct ql_batcher ql_batcher;
+
+typedef struct {
+    int n_seqs;                   /* sequences that run this step */
+    int n_rows;                   /* query rows (tokens) in this step */
+    int max_q_len;                /* largest rows of one sequence */
+    int max_ctx_len;              /* largest ctx_lens[i] */
+    int max_blocks;               /* row length of block_tables */
+    const int32_t* req_ids;       /* [n_seqs] */
+    const int32_t* is_prefill;    /* [n_seqs] 1 = prompt rows, 0 = one decode row */
+    const int32_t* cu_q_lens;     /* [n_seqs + 1] rows of sequence i: cu[i] .. cu[i+1]-1 */
+    const int32_t* ctx_lens;      /* [n_seqs] keys after this step's rows are appended */
+    const int32_t* block_tables;  /* [n_seqs * max_blocks] physical blocks, -1 padded */
+    const int32_t* token_ids;     /* [n_rows] token of each row (embedding input) */
+    const int32_t* positions;     /* [n_rows] its position (RoPE) */
+    const int32_t* slot_mapping;  /* [n_rows] its KV slot = block*16 + position%16 */
+    const int32_t* sample_rows;   /* [n_seqs] row whose logits give the next token */
+} ql_step_plan;
+
+typedef struct {
+    int n_active, n_pending, free_blocks, n_finished;
+} ql_batcher_counts;
+
+typedef struct {
+    int req_id, reason, prompt_len, n_tokens;   /* n_tokens = prompt + generated */
+} ql_finished;
+
+/* A batcher owning an allocator of n_blocks (fresh-pool LIFO order 0, 1, 2, ...). */
+hipError_t ql_batcher_create(int n_blocks, int max_active, int eos_token, ql_batcher** out);
+/* A batcher using an existing LIFO stack of free block indices (e.g. PagedKVCache's
+ * free_blocks / free_count): blocks are popped and pushed exactly as
+ * paged_kv_allocate_block / paged_kv_free_block do. */
+hipError_t ql_batcher_create_on_stack(int* free_blocks, int* free_count, int n_blocks,
+                                      int max_active, int eos_token, ql_batcher** out);
+hipError_t ql_batcher_destroy(ql_batcher* b);
+/* prompt_len > 0, max_gen > 0; the prompt is copied. */
+hipError_t ql_batcher_add_request(ql_batcher* b, int req_id, const int32_t* prompt,
+                                  int prompt_len, int max_gen);
+hipError_t ql_batcher_plan(ql_batcher* b, ql_step_plan* plan);
+hipError_t ql_batcher_commit(ql_batcher* b, const int32_t* sampled, int n_seqs);
+hipError_t ql_batcher_stats(const ql_batcher* b, ql_batcher_counts* counts);
+/* Oldest finished request: *got = 1 and up to cap of its tokens copied, or *got = 0. */
+hipError_t ql_batcher_pop_finished(ql_batcher* b, ql_finished* ev, int32_t* tokens, int cap,
+                                   int* got);
+
 #ifdef __cplusplus
 }
 #endif

@@ -61,6 +61,14 @@ SIGNATURES = {
     "ql_paged_attention_f16": [_p, _p, _i64, _i64, _i, _i, _p, _p, _i, _p, _i, _p, _p, _i, _i, _i,
                                _i, _i, _i, _i, _p],
     "ql_paged_decode_workspace_size": [_i, _i, _i, _i, _i, _p],
+    "ql_batcher_create": [_i, _i, _i, _p],
+    "ql_batcher_create_on_stack": [_p, _p, _i, _i, _i, _p],
+    "ql_batcher_destroy": [_p],
+    "ql_batcher_add_request": [_p, _i, _p, _i, _i],
+    "ql_batcher_plan": [_p, _p],
+    "ql_batcher_commit": [_p, _p, _i],
+    "ql_batcher_stats": [_p, _p],
+    "ql_batcher_pop_finished": [_p, _p, _p, _i, _p],
     "ql_paged_decode_attention_f16": [_p, _p, _i64, _i64, _i, _p, _i, _p, _i, _p, _p, _i, _i, _i,
                                       _i, _i, _i, _p, ctypes.c_size_t, _p],
 }
@@ -280,3 +288,93 @@ class Event:
                 _hiprt.hipEventDestroy(self.ev)
             except Exception:
                 pass
+
+
+# ---- continuous batching (host only) ---------------------------------------------------
+FINISH_LENGTH, FINISH_EOS, FINISH_EVICTED = 0, 1, 2
+_i32p = ctypes.POINTER(ctypes.c_int32)
+
+
+class StepPlan(ctypes.Structure):
+    """ql_step_plan (include/quantlib_amd.h)."""
+    _fields_ = [("n_seqs", _i), ("n_rows", _i), ("max_q_len", _i), ("max_ctx_len", _i),
+                ("max_blocks", _i), ("req_ids", _i32p), ("is_prefill", _i32p),
+                ("cu_q_lens", _i32p), ("ctx_lens", _i32p), ("block_tables", _i32p),
+                ("token_ids", _i32p), ("positions", _i32p), ("slot_mapping", _i32p),
+                ("sample_rows", _i32p)]
+
+
+class BatcherCounts(ctypes.Structure):
+    _fields_ = [("n_active", _i), ("n_pending", _i), ("free_blocks", _i), ("n_finished", _i)]
+
+
+class Finished(ctypes.Structure):
+    _fields_ = [("req_id", _i), ("reason", _i), ("prompt_len", _i), ("n_tokens", _i)]
+
+
+class Batcher:
+    """Thin wrapper of the ql_batcher_* C ABI; plan() returns numpy copies."""
+
+    def __init__(self, n_blocks: int, max_active: int, eos_token: int = 2, stack=None,
+                 free_count=None):
+        import numpy as np
+        self._np = np
+        h = ctypes.c_void_p()
+        if stack is None:
+            call("ql_batcher_create", n_blocks, max_active, eos_token, ctypes.byref(h))
+        else:   # borrow an external LIFO stack (numpy int32 array + 1-element count array)
+            self._stack, self._count = stack, free_count
+            call("ql_batcher_create_on_stack", stack.ctypes.data, free_count.ctypes.data, n_blocks,
+                 max_active, eos_token, ctypes.byref(h))
+        self.h = h.value
+
+    def close(self):
+        if self.h:
+            call("ql_batcher_destroy", self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def add(self, req_id: int, prompt, max_gen: int):
+        p = self._np.ascontiguousarray(prompt, self._np.int32)
+        call("ql_batcher_add_request", self.h, req_id, p.ctypes.data, p.size, max_gen)
+
+    def plan(self) -> dict:
+        np = self._np
+        pl = StepPlan()
+        call("ql_batcher_plan", self.h, ctypes.byref(pl))
+        n, r, mb = pl.n_seqs, pl.n_rows, pl.max_blocks
+
+        def arr(ptr, count):
+            return np.ctypeslib.as_array(ptr, shape=(count,)).copy() if count else np.zeros(0, np.int32)
+        return {"n_seqs": n, "n_rows": r, "max_q_len": pl.max_q_len, "max_ctx_len": pl.max_ctx_len,
+                "max_blocks": mb, "req_ids": arr(pl.req_ids, n), "is_prefill": arr(pl.is_prefill, n),
+                "cu_q_lens": arr(pl.cu_q_lens, n + 1), "ctx_lens": arr(pl.ctx_lens, n),
+                "block_tables": arr(pl.block_tables, n * mb).reshape(n, mb),
+                "token_ids": arr(pl.token_ids, r), "positions": arr(pl.positions, r),
+                "slot_mapping": arr(pl.slot_mapping, r), "sample_rows": arr(pl.sample_rows, n)}
+
+    def commit(self, sampled):
+        s = self._np.ascontiguousarray(sampled, self._np.int32)
+        call("ql_batcher_commit", self.h, s.ctypes.data if s.size else None, s.size)
+
+    def counts(self) -> dict:
+        c = BatcherCounts()
+        call("ql_batcher_stats", self.h, ctypes.byref(c))
+        return {"n_active": c.n_active, "n_pending": c.n_pending, "free_blocks": c.free_blocks,
+                "n_finished": c.n_finished}
+
+    def pop_finished(self):
+        """(req_id, reason, prompt_len, tokens) of the oldest finished request, or None."""
+        np = self._np
+        ev, got = Finished(), ctypes.c_int(0)
+        buf = np.zeros(1 << 16, np.int32)
+        call("ql_batcher_pop_finished", self.h, ctypes.byref(ev), buf.ctypes.data, buf.size,
+             ctypes.byref(got))
+        if not got.value:
+            return None
+        return ev.req_id, ev.reason, ev.prompt_len, buf[:min(ev.n_tokens, buf.size)].copy()
