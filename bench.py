@@ -30,7 +30,8 @@ adds the attention that consumes the path's output: causal prefill over the
 8192 tokens (contiguous, and over the paged pool the chain writes), reported in
 TFLOP/s against the dense fp16 matrix peak, and paged decode (64 sequences x
 4096 tokens; 1 sequence x 8192 tokens with the key-split workspace), HBM-bound
-on the K/V rows.
+on the K/V rows, and one whole decoder layer through the engine (hipBLASLt
+GEMMs + the fused kernels + attention) for that prefill and that decode step.
 
 Device memory, the stream and events come from libamdhip64 through the
 library's own binding (quant-lib_amd/quantlib_amd.py); no framework runtime is
@@ -366,6 +367,82 @@ def all_configs(ql, np, reps):
         rows.append({"config": "C5 T=8192 llama3-8b", "kernel": name, "bytes": BYTES[name],
                      "us": round(us, 2), "GBps": round(gbs, 1), "frac_peak": round(gbs / PEAK_HBM_GBS, 4)})
     rows += attention_rows(ql, np, chain, reps)
+    rows += layer_rows(ql, np, chain, reps)
+    return rows
+
+
+def layer_rows(ql, np, chain, reps):
+    """One whole Llama-3-8B-shaped fp16 decoder layer through the engine
+    (ql_engine_layer_f16: hipBLASLt GEMMs + the fused kernels + attention):
+    a 8192-token prefill of one sequence and a decode step of 64 sequences at
+    4096 keys.  Weights are seeded N(0, 1/fan_in), uploaded once."""
+    st = chain.stream
+    up = ql.DeviceArray.from_numpy
+    r = np.random.default_rng(21)
+
+    def w(shape, fan_in):
+        return up((r.standard_normal(shape, dtype=np.float32) * np.float32(fan_in ** -0.5))
+                  .astype(np.float16).view(np.uint16))
+
+    QKV = (HQ + 2 * HKV) * HD
+    wts = {"attn_norm": up(np.ones(D, np.float16).view(np.uint16)), "wqkv": w((QKV, D), D),
+           "wo": w((D, HQ * HD), HQ * HD), "ffn_norm": up(np.ones(D, np.float16).view(np.uint16)),
+           "w_gate": w((F, D), D), "w_up": w((F, D), D), "w_down": w((D, F), F)}
+    lw = ql.LayerWeights(*(wts[k].ptr for k in ("attn_norm", "wqkv", "wo", "ffn_norm", "w_gate", "w_up",
+                                                "w_down")))
+    dims = ql.LayerDims(D, HQ, HKV, HD, F, THETA, EPS, ql.ROPE_HALF)
+    rows = []
+    gemm_flops = lambda m: 2.0 * m * D * (QKV + HQ * HD + 3 * F)
+    for label, S, C, q_len in (("prefill 1 seq x 8192 tokens", 1, T, T),
+                               ("decode 64 seq x 4096 ctx", 64, 4096, 1)):
+        nbs = C // PAGE
+        nb = S * nbs
+        blk = L_POOL * PAGE * HKV * HD
+        kpool = ql.DeviceArray((nb * blk,), np.uint16)
+        vpool = ql.DeviceArray((nb * blk,), np.uint16)
+        kpool.fill_bytes(0x3C)
+        vpool.fill_bytes(0x3C)
+        kp = up(np.array([kpool.ptr + 2 * blk * b for b in range(nb)], np.int64))
+        vp = up(np.array([vpool.ptr + 2 * blk * b for b in range(nb)], np.int64))
+        n_rows = S * q_len
+        if q_len == 1:   # one decode row per sequence at position C-1
+            pos = np.full(S, C - 1, np.int32)
+            tables = r.permutation(nb).astype(np.int32).reshape(S, nbs)
+            slots = (tables[:, (C - 1) // PAGE] * PAGE + (C - 1) % PAGE).astype(np.int32)
+        else:
+            pos = np.arange(C, dtype=np.int32)
+            tables = np.arange(nb, dtype=np.int32).reshape(1, nb)
+            slots = (tables[0, pos // PAGE] * PAGE + pos % PAGE).astype(np.int32)
+        arrs = {"pos": up(pos), "slots": up(slots), "cu": up(np.arange(S + 1, dtype=np.int32) * q_len),
+                "ctx": up(np.full(S, C, np.int32)), "bt": up(tables.reshape(-1))}
+        sd = ql.StepDevice(n_rows, S, q_len, C, nbs, arrs["pos"].ptr, arrs["slots"].ptr, arrs["cu"].ptr,
+                           arrs["ctx"].ptr, arrs["bt"].ptr, kp.ptr, vp.ptr, nb, L_POOL)
+        eng = ctypes.c_void_p()
+        ql.call("ql_engine_create", ctypes.byref(dims), n_rows, S, C, ctypes.byref(eng))
+        x = up(r.standard_normal((n_rows, D), dtype=np.float32).astype(np.float16).view(np.uint16))
+        deltas = [ql.DeviceArray((n_rows, D), np.uint16) for _ in range(2)]
+
+        def launch(i):
+            ql.call("ql_engine_layer_f16", eng, ctypes.byref(lw), i % L_POOL, x.ptr,
+                    deltas[(i + 1) % 2].ptr if i else None, deltas[i % 2].ptr, ctypes.byref(sd), st)
+        for i in range(3):
+            launch(i)
+        ql.synchronize()
+        n = max(3, reps // 10)
+        a, b = ql.Event(), ql.Event()
+        a.record(st)
+        for i in range(n):
+            launch(i + 3)
+        b.record(st)
+        us = a.elapsed_ms(b) * 1e3 / n
+        fl = gemm_flops(n_rows) + (4.0 * (C * (C + 1) / 2) * HD * HQ if q_len > 1 else 4.0 * S * C * HD * HQ)
+        rows.append({"config": f"C5 decoder layer, {label}", "kernel": "engine_layer_f16",
+                     "bytes": 0, "us": round(us, 2), "GBps": 0.0, "frac_peak": 0.0,
+                     "tflops": round(fl / (us * 1e-6) / 1e12, 1),
+                     "frac_mfma_peak": round(fl / (us * 1e-6) / 1e12 / PEAK_MFMA_F16_TFLOPS, 4),
+                     "tokens_per_s_per_layer": round(n_rows / (us * 1e-6), 1)})
+        ql.call("ql_engine_destroy", eng)
+        del kpool, vpool
     return rows
 
 

@@ -344,6 +344,76 @@ hipError_t ql_batcher_stats(const ql_batcher* b, ql_batcher_counts* counts);
 hipError_t ql_batcher_pop_finished(ql_batcher* b, ql_finished* ev, int32_t* tokens, int cap,
                                    int* got);
 
+/* ---- greedy sampling ----------------------------------------------------------------
+ * out[r] = the first index of the maximum of row r (logits + r*ld, cols values): the
+ * strict-">" scan of argmax_kernel (src/continuous_batch.cu:12-25,
+ * src/fp16_forward.cu:259-283), batched over rows.  NaN never wins; a row with no
+ * value above -inf gives 0. */
+hipError_t ql_argmax_f32(const float* logits, int rows, int cols, int64_t ld, int32_t* out,
+                         hipStream_t stream);
+hipError_t ql_argmax_f16(const uint16_t* logits, int rows, int cols, int64_t ld, int32_t* out,
+                         hipStream_t stream);
+
+/* ---- decoder-layer engine (fp16; hipBLASLt GEMMs + the kernels above) -----------------
+ * One fp16 decoder layer for every row of a batched step, in the order of
+ * fp16_layer_forward (src/fp16_forward.cu:167-223):
+ *   x += delta_in; y = rmsnorm(x)*attn_norm; qkv = y Wqkv^T; RoPE + paged KV append;
+ *   a = attention over the paged pool; x += a Wo^T; y = rmsnorm(x)*ffn_norm;
+ *   delta_out = (silu(y Wg^T) * (y Wu^T)) Wd^T
+ * delta_in = NULL for the first layer; delta_out is added by the next layer (or by
+ * ql_engine_logits_f16).  Weights are row-major [out_features, in_features] fp16;
+ * wqkv stacks the Q rows (n_heads*head_dim), then K, then V (n_kv_heads*head_dim
+ * each).  The step arrays are a ql_step_plan's, on the device.  A step whose rows
+ * are all single-token decodes (max_q_len == 1, n_rows == n_seqs) uses the split
+ * decode with the engine's workspace.  The engine owns its activation buffers and
+ * workspaces (allocated once by ql_engine_create, sized for max_rows rows,
+ * max_seqs sequences and max_ctx_len keys); the per-step calls allocate nothing.
+ * GEMM plans are cached per (rows, out, in) shape; use an engine from one host
+ * thread at a time. */
+typedef struct {
+    int hidden, n_heads, n_kv_heads, head_dim, ffn;
+    float rope_theta, rms_eps;
+    int rope_pairing;
+} ql_layer_dims;
+
+typedef struct {
+    const uint16_t* attn_norm;   /* [hidden] */
+    const uint16_t* wqkv;        /* [(n_heads + 2*n_kv_heads)*head_dim, hidden] */
+    const uint16_t* wo;          /* [hidden, n_heads*head_dim] */
+    const uint16_t* ffn_norm;    /* [hidden] */
+    const uint16_t* w_gate;      /* [ffn, hidden] */
+    const uint16_t* w_up;        /* [ffn, hidden] */
+    const uint16_t* w_down;      /* [hidden, ffn] */
+} ql_layer_weights;
+
+typedef struct {
+    int n_rows, n_seqs, max_q_len, max_ctx_len, max_blocks;
+    const int32_t* positions;     /* device [n_rows] */
+    const int32_t* slot_mapping;  /* device [n_rows] */
+    const int32_t* cu_q_lens;     /* device [n_seqs + 1] */
+    const int32_t* ctx_lens;      /* device [n_seqs] */
+    const int32_t* block_tables;  /* device [n_seqs * max_blocks] */
+    uint16_t* const* k_blocks;    /* device block-pointer tables of the pool */
+    uint16_t* const* v_blocks;
+    int n_blocks, n_layers;
+} ql_step_device;
+
+typedef struct ql_engine ql_engine;
+
+hipError_t ql_engine_create(const ql_layer_dims* dims, int max_rows, int max_seqs, int max_ctx_len,
+                            ql_engine** out);
+hipError_t ql_engine_destroy(ql_engine* e);
+hipError_t ql_engine_layer_f16(ql_engine* e, const ql_layer_weights* w, int layer, uint16_t* x,
+                               const uint16_t* delta_in, uint16_t* delta_out,
+                               const ql_step_device* step, hipStream_t stream);
+/* x += delta_in over all n_rows rows, final RMSNorm, gather the n_sample rows
+ * sample_rows[] (device), logits = rows lm_head^T ([n_sample, vocab] fp16) and, if
+ * tokens is not NULL, tokens[i] = argmax of logits row i (device). */
+hipError_t ql_engine_logits_f16(ql_engine* e, uint16_t* x, const uint16_t* delta_in,
+                                const uint16_t* final_norm, const uint16_t* lm_head, int vocab,
+                                const int32_t* sample_rows, int n_sample, int n_rows,
+                                uint16_t* logits, int32_t* tokens, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

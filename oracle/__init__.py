@@ -48,6 +48,8 @@ _SIGS = {
     "or_attention_f16": ([_p, _p, _p, _p, _i, _i, _i, _i, _i, _i64, _i64, _i64, _i], None),
     "or_attention_reftest_cpu": ([_p, _p, _p, _p, _i, _i, _i], None),
     "or_reftest_attention_inputs": ([_p, _p, _p, _i64, ctypes.c_uint], None),
+    "or_matmul_f16": ([_p, _p, _p, _i, _i, _i], None),
+    "or_argmax_f32": ([_p, _i, _i, _p], None),
 }
 
 _lib = None
@@ -244,3 +246,21 @@ def reftest_attention_inputs(seq_len: int, n_heads: int, head_dim: int, seed: in
     q, k, v = (np.empty((seq_len, n_heads, head_dim), np.float32) for _ in range(3))
     lib().or_reftest_attention_inputs(_ptr(q), _ptr(k), _ptr(v), n, seed)
     return q, k, v
+
+
+def matmul(x, w) -> np.ndarray:
+    """y = x W^T for binary16 x [M, K], w [N, K] -> binary16 [M, N]."""
+    x, w = _u16(x), _u16(w)
+    M, K = x.shape
+    N = w.shape[0]
+    y = np.empty((M, N), np.uint16)
+    lib().or_matmul_f16(_ptr(x), _ptr(w), _ptr(y), M, N, K)
+    return y
+
+
+def argmax(x) -> np.ndarray:
+    x = _f32(x)
+    x2 = x.reshape(-1, x.shape[-1])
+    out = np.empty(x2.shape[0], np.int32)
+    lib().or_argmax_f32(_ptr(x2), x2.shape[0], x2.shape[1], _ptr(out))
+    return out.reshape(x.shape[:-1])

@@ -509,3 +509,46 @@ void or_reftest_attention_inputs(float* q, float* k, float* v, int64_t n, unsign
         v[i] = (float)rand() / RAND_MAX - 0.5f;
     }
 }
+
+/* ---- linear layer and greedy sampling ---------------------------------------------------
+ * y[m, n] = sum_k x[m, k] w[n, k] (weights [out, in], y = x W^T), the projections of
+ * src/fp16_forward.cu:184-186,204,211,219-221 (hgemm with fp32 accumulation);
+ * products and sum in double, result rounded to binary16.
+ * Pinned by: numpy float64 matmul of the widened values; identity and permutation
+ * weights reproduce / permute x exactly (tests/test_oracle.py::test_matmul_*). */
+void or_matmul_f16(const uint16_t* x, const uint16_t* w, uint16_t* y, int M, int N, int K) {
+    float* wf = (float*)malloc(sizeof(float) * (size_t)N * (size_t)K);
+    for (size_t i = 0; i < (size_t)N * (size_t)K; ++i) wf[i] = or_f16_to_f32(w[i]);
+    double* xr = (double*)malloc(sizeof(double) * (size_t)(K > 0 ? K : 1));
+    for (int m = 0; m < M; ++m) {
+        for (int k = 0; k < K; ++k) xr[k] = or_f16_to_f32(x[(size_t)m * K + k]);
+        for (int n = 0; n < N; ++n) {
+            const float* wr = wf + (size_t)n * K;
+            double acc = 0.0;
+            for (int k = 0; k < K; ++k) acc += xr[k] * (double)wr[k];
+            y[(size_t)m * N + n] = or_f32_to_f16((float)acc);
+        }
+    }
+    free(wf);
+    free(xr);
+}
+
+/* argmax_kernel (src/continuous_batch.cu:12-25): the first index whose value is
+ * strictly greater than all earlier ones; NaN never is; a row without a value
+ * above -inf gives 0.
+ * Pinned by: numpy argmax (first occurrence) on NaN-free rows; ties, all -inf and
+ * NaN rows by closed forms (tests/test_oracle.py::test_argmax_*). */
+void or_argmax_f32(const float* x, int rows, int cols, int32_t* out) {
+    for (int r = 0; r < rows; ++r) {
+        float best = -INFINITY;
+        int32_t idx = 0;
+        for (int c = 0; c < cols; ++c) {
+            const float v = x[(size_t)r * cols + c];
+            if (v > best) {
+                best = v;
+                idx = c;
+            }
+        }
+        out[r] = idx;
+    }
+}

@@ -94,6 +94,11 @@ void or_attention_reftest_cpu(const float* Q, const float* K, const float* V, fl
                               int seq_len, int n_heads, int head_dim);
 void or_reftest_attention_inputs(float* q, float* k, float* v, int64_t n, unsigned seed);
 
+/* y = x W^T (weights [out, in]), double accumulation, binary16 result. */
+void or_matmul_f16(const uint16_t* x, const uint16_t* w, uint16_t* y, int M, int N, int K);
+/* First index of the row maximum (strict >, NaN ignored, 0 if none above -inf). */
+void or_argmax_f32(const float* x, int rows, int cols, int32_t* out);
+
 #ifdef __cplusplus
 }
 #endif

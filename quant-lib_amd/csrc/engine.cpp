@@ -1,0 +1,229 @@
+// engine.cpp -- one fp16 decoder layer (and the logits of the sampled rows) for a
+// batched step, composed from the library's kernels and hipBLASLt GEMMs.
+//
+// The layer order of fp16_layer_forward (src/fp16_forward.cu:167-223), with
+// the reference's per-token, per-op launches replaced by one batched step over
+// every row a ql_batcher plan lists (prefills and decodes together):
+//
+//   x += delta_in; y = rmsnorm(x) * attn_norm        ql_add_rmsnorm_f16 (fused)
+//   qkv = y Wqkv^T                                    hipBLASLt (Q, K, V in one GEMM)
+//   rope(q, k); k, v -> paged pool                    ql_rope_paged_kv_append_f16 (fused)
+//   a = attention(q, paged K/V)                       ql_paged_attention_f16, or the
+//                                                     split decode for all-decode steps
+//   x += a Wo^T; y = rmsnorm(x) * ffn_norm            hipBLASLt + ql_add_rmsnorm_f16
+//   delta_out = swiglu(y Wg^T, y Wu^T) Wd^T           hipBLASLt x2, ql_swiglu_f16, hipBLASLt
+//
+// The MLP output is returned as delta_out and added by the next layer's fused
+// add+RMSNorm (or by ql_engine_logits_f16 after the last layer).  Weights are
+// row-major [out_features, in_features] fp16 (y = x W^T).  GEMMs accumulate in
+// fp32 and write fp16.  The engine owns its activation buffers, the GEMM
+// workspace and the split-decode workspace, all allocated once at creation;
+// the per-step calls allocate nothing.
+#include "quantlib_amd.h"
+
+#include <hipblaslt/hipblaslt.h>
+
+#include <map>
+#include <new>
+#include <tuple>
+
+namespace {
+
+constexpr size_t kGemmWorkspace = 64u << 20;
+
+struct GemmPlan {
+    hipblasLtMatmulDesc_t desc = nullptr;
+    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
+    hipblasLtMatmulAlgo_t algo{};
+    bool ok = false;
+};
+
+size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+}  // namespace
+
+struct ql_engine {
+    ql_layer_dims dims{};
+    int max_rows = 0, max_seqs = 0, max_ctx = 0;
+    hipblasLtHandle_t lt = nullptr;
+    void* gemm_ws = nullptr;
+    void* arena = nullptr;
+    uint16_t *y = nullptr, *qkv = nullptr, *attn = nullptr, *o = nullptr, *g = nullptr, *u = nullptr,
+             *mid = nullptr;
+    void* dec_ws = nullptr;
+    size_t dec_ws_bytes = 0;
+    std::map<std::tuple<int, int, int>, GemmPlan> gemms;
+
+    // y[M, N] = x[M, K] W[N, K]^T  (row-major, fp16 in/out, fp32 accumulate)
+    hipError_t gemm(const uint16_t* x, const uint16_t* w, uint16_t* out, int M, int N, int K,
+                    hipStream_t stream) {
+        GemmPlan& p = gemms[std::make_tuple(M, N, K)];
+        if (!p.ok) {
+            // column-major view: out^T (N x M) = op(A) op(B), A = W stored K x N (transposed),
+            // B = x stored K x M
+            const hipblasOperation_t opT = HIPBLAS_OP_T, opN = HIPBLAS_OP_N;
+            if (hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS ||
+                hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opT, sizeof(opT)) !=
+                    HIPBLAS_STATUS_SUCCESS ||
+                hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opN, sizeof(opN)) !=
+                    HIPBLAS_STATUS_SUCCESS ||
+                hipblasLtMatrixLayoutCreate(&p.a, HIP_R_16F, (uint64_t)K, (uint64_t)N, K) != HIPBLAS_STATUS_SUCCESS ||
+                hipblasLtMatrixLayoutCreate(&p.b, HIP_R_16F, (uint64_t)K, (uint64_t)M, K) != HIPBLAS_STATUS_SUCCESS ||
+                hipblasLtMatrixLayoutCreate(&p.c, HIP_R_16F, (uint64_t)N, (uint64_t)M, N) != HIPBLAS_STATUS_SUCCESS)
+                return hipErrorUnknown;
+            hipblasLtMatmulPreference_t pref = nullptr;
+            if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return hipErrorUnknown;
+            const uint64_t ws = kGemmWorkspace;
+            hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws,
+                                                  sizeof(ws));
+            hipblasLtMatmulHeuristicResult_t res{};
+            int n = 0;
+            const hipblasStatus_t st = hipblasLtMatmulAlgoGetHeuristic(lt, p.desc, p.a, p.b, p.c, p.c, pref,
+                                                                       1, &res, &n);
+            hipblasLtMatmulPreferenceDestroy(pref);
+            if (st != HIPBLAS_STATUS_SUCCESS || n < 1 || res.workspaceSize > kGemmWorkspace)
+                return hipErrorNotSupported;
+            p.algo = res.algo;
+            p.ok = true;
+        }
+        const float alpha = 1.0f, beta = 0.0f;
+        const hipblasStatus_t st = hipblasLtMatmul(lt, p.desc, &alpha, w, p.a, x, p.b, &beta, out, p.c,
+                                                   out, p.c, &p.algo, gemm_ws, kGemmWorkspace, stream);
+        return st == HIPBLAS_STATUS_SUCCESS ? hipSuccess : hipErrorLaunchFailure;
+    }
+
+    ~ql_engine() {
+        for (auto& kv : gemms) {
+            if (kv.second.a) hipblasLtMatrixLayoutDestroy(kv.second.a);
+            if (kv.second.b) hipblasLtMatrixLayoutDestroy(kv.second.b);
+            if (kv.second.c) hipblasLtMatrixLayoutDestroy(kv.second.c);
+            if (kv.second.desc) hipblasLtMatmulDescDestroy(kv.second.desc);
+        }
+        if (lt) hipblasLtDestroy(lt);
+        if (gemm_ws) (void)hipFree(gemm_ws);
+        if (arena) (void)hipFree(arena);
+    }
+};
+
+#define QL_TRY(expr)                          \
+    do {                                      \
+        const hipError_t e_ = (expr);         \
+        if (e_ != hipSuccess) return e_;      \
+    } while (0)
+
+extern "C" hipError_t ql_engine_create(const ql_layer_dims* d, int max_rows, int max_seqs,
+                                       int max_ctx_len, ql_engine** out) {
+    if (!out || !d || max_rows <= 0 || max_seqs <= 0 || max_ctx_len < 0) return hipErrorInvalidValue;
+    if (d->hidden <= 0 || d->n_heads <= 0 || d->n_kv_heads <= 0 || d->n_kv_heads > d->n_heads ||
+        (d->head_dim != 64 && d->head_dim != 128) || d->ffn <= 0 || d->hidden % 8 || d->ffn % 8 ||
+        !(d->rope_theta > 0.0f) || (d->rope_pairing != QL_ROPE_INTERLEAVED && d->rope_pairing != QL_ROPE_HALF))
+        return hipErrorInvalidValue;
+    *out = nullptr;
+    ql_engine* e = new (std::nothrow) ql_engine();
+    if (!e) return hipErrorOutOfMemory;
+    e->dims = *d;
+    e->max_rows = max_rows;
+    e->max_seqs = max_seqs;
+    e->max_ctx = max_ctx_len;
+    const size_t R = (size_t)max_rows, D = (size_t)d->hidden, F = (size_t)d->ffn;
+    const size_t Q = (size_t)d->n_heads * d->head_dim, KV = (size_t)d->n_kv_heads * d->head_dim;
+    size_t ws = 0;
+    if (ql_paged_decode_workspace_size(max_seqs, d->n_heads, d->n_kv_heads, d->head_dim, max_ctx_len, &ws) !=
+        hipSuccess) {
+        delete e;
+        return hipErrorInvalidValue;
+    }
+    e->dec_ws_bytes = ws;
+    const size_t sizes[] = {R * D, R * (Q + 2 * KV), R * Q, R * D, R * F, R * F, R * F};
+    size_t total = 0;
+    for (size_t s : sizes) total += align256(s * sizeof(uint16_t));
+    total += align256(ws);
+    if (hipMalloc(&e->arena, total) != hipSuccess || hipMalloc(&e->gemm_ws, kGemmWorkspace) != hipSuccess ||
+        hipblasLtCreate(&e->lt) != HIPBLAS_STATUS_SUCCESS) {
+        delete e;
+        return hipErrorOutOfMemory;
+    }
+    char* p = static_cast<char*>(e->arena);
+    uint16_t** bufs[] = {&e->y, &e->qkv, &e->attn, &e->o, &e->g, &e->u, &e->mid};
+    for (int i = 0; i < 7; ++i) {
+        *bufs[i] = reinterpret_cast<uint16_t*>(p);
+        p += align256(sizes[i] * sizeof(uint16_t));
+    }
+    e->dec_ws = ws ? p : nullptr;
+    *out = e;
+    return hipSuccess;
+}
+
+extern "C" hipError_t ql_engine_destroy(ql_engine* e) {
+    delete e;
+    return hipSuccess;
+}
+
+extern "C" hipError_t ql_engine_layer_f16(ql_engine* e, const ql_layer_weights* w, int layer,
+                                          uint16_t* x, const uint16_t* delta_in, uint16_t* delta_out,
+                                          const ql_step_device* s, hipStream_t stream) {
+    if (!e || !w || !x || !delta_out || !s) return hipErrorInvalidValue;
+    const ql_layer_dims& d = e->dims;
+    const int T = s->n_rows;
+    if (T < 0 || T > e->max_rows || s->n_seqs < 0 || s->n_seqs > e->max_seqs ||
+        s->max_ctx_len > e->max_ctx || layer < 0 || layer >= s->n_layers)
+        return hipErrorInvalidValue;
+    if (T == 0) return hipSuccess;
+    if (!w->attn_norm || !w->wqkv || !w->wo || !w->ffn_norm || !w->w_gate || !w->w_up || !w->w_down)
+        return hipErrorInvalidValue;
+    const int H = d.n_heads, HK = d.n_kv_heads, HD = d.head_dim, D = d.hidden, F = d.ffn;
+    const int QKV = (H + 2 * HK) * HD;
+    // attention sublayer
+    if (delta_in)
+        QL_TRY(ql_add_rmsnorm_f16(x, delta_in, w->attn_norm, e->y, T, D, d.rms_eps, stream));
+    else
+        QL_TRY(ql_rmsnorm_f16(x, w->attn_norm, e->y, T, D, d.rms_eps, stream));
+    QL_TRY(e->gemm(e->y, w->wqkv, e->qkv, T, QKV, D, stream));
+    uint16_t* q = e->qkv;
+    uint16_t* k = e->qkv + (size_t)H * HD;
+    const uint16_t* v = e->qkv + (size_t)(H + HK) * HD;
+    QL_TRY(ql_rope_paged_kv_append_f16(q, k, v, T, H, HK, HD, QKV, QKV, QKV, s->positions, 0,
+                                       d.rope_theta, d.rope_pairing, s->k_blocks, s->v_blocks,
+                                       s->n_blocks, s->slot_mapping, layer, s->n_layers, stream));
+    const uint16_t* const* kb = reinterpret_cast<const uint16_t* const*>(s->k_blocks);
+    const uint16_t* const* vb = reinterpret_cast<const uint16_t* const*>(s->v_blocks);
+    if (s->max_q_len == 1 && T == s->n_seqs) {   // every sequence decodes: row i = sequence i
+        QL_TRY(ql_paged_decode_attention_f16(q, e->attn, QKV, (int64_t)H * HD, s->n_seqs, s->ctx_lens,
+                                             s->max_ctx_len, s->block_tables, s->max_blocks, kb, vb,
+                                             s->n_blocks, layer, s->n_layers, H, HK, HD, e->dec_ws,
+                                             e->dec_ws_bytes, stream));
+    } else {
+        QL_TRY(ql_paged_attention_f16(q, e->attn, QKV, (int64_t)H * HD, T, s->n_seqs, s->cu_q_lens,
+                                      s->ctx_lens, s->max_q_len, s->block_tables, s->max_blocks, kb, vb,
+                                      s->n_blocks, layer, s->n_layers, H, HK, HD, 1, stream));
+    }
+    QL_TRY(e->gemm(e->attn, w->wo, e->o, T, D, H * HD, stream));
+    // MLP sublayer
+    QL_TRY(ql_add_rmsnorm_f16(x, e->o, w->ffn_norm, e->y, T, D, d.rms_eps, stream));
+    QL_TRY(e->gemm(e->y, w->w_gate, e->g, T, F, D, stream));
+    QL_TRY(e->gemm(e->y, w->w_up, e->u, T, F, D, stream));
+    QL_TRY(ql_swiglu_f16(e->g, e->u, e->mid, T, F, stream));
+    QL_TRY(e->gemm(e->mid, w->w_down, delta_out, T, D, F, stream));
+    return hipSuccess;
+}
+
+extern "C" hipError_t ql_engine_logits_f16(ql_engine* e, uint16_t* x, const uint16_t* delta_in,
+                                           const uint16_t* final_norm, const uint16_t* lm_head,
+                                           int vocab, const int32_t* sample_rows, int n_sample,
+                                           int n_rows, uint16_t* logits, int32_t* tokens,
+                                           hipStream_t stream) {
+    if (!e || !x || !final_norm || !lm_head || !sample_rows || !logits || vocab <= 0 || vocab % 8 ||
+        n_sample < 0 || n_sample > e->max_rows || n_rows < 0 || n_rows > e->max_rows)
+        return hipErrorInvalidValue;
+    if (n_sample == 0) return hipSuccess;
+    const int D = e->dims.hidden;
+    // finish the residual stream of every row, then gather the rows to sample
+    if (delta_in)
+        QL_TRY(ql_add_rmsnorm_f16(x, delta_in, final_norm, e->y, n_rows, D, e->dims.rms_eps, stream));
+    else
+        QL_TRY(ql_rmsnorm_f16(x, final_norm, e->y, n_rows, D, e->dims.rms_eps, stream));
+    QL_TRY(ql_embed_f16(e->y, sample_rows, n_sample, n_rows, D, e->o, stream));
+    QL_TRY(e->gemm(e->o, lm_head, logits, n_sample, vocab, D, stream));
+    if (tokens) QL_TRY(ql_argmax_f16(logits, n_sample, vocab, vocab, tokens, stream));
+    return hipSuccess;
+}

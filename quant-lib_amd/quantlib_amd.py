@@ -69,6 +69,12 @@ SIGNATURES = {
     "ql_batcher_commit": [_p, _p, _i],
     "ql_batcher_stats": [_p, _p],
     "ql_batcher_pop_finished": [_p, _p, _p, _i, _p],
+    "ql_argmax_f32": [_p, _i, _i, _i64, _p, _p],
+    "ql_argmax_f16": [_p, _i, _i, _i64, _p, _p],
+    "ql_engine_create": [_p, _i, _i, _i, _p],
+    "ql_engine_destroy": [_p],
+    "ql_engine_layer_f16": [_p, _p, _i, _p, _p, _p, _p, _p],
+    "ql_engine_logits_f16": [_p, _p, _p, _p, _p, _i, _p, _i, _i, _p, _p, _p],
     "ql_paged_decode_attention_f16": [_p, _p, _i64, _i64, _i, _p, _i, _p, _i, _p, _p, _i, _i, _i,
                                       _i, _i, _i, _p, ctypes.c_size_t, _p],
 }
@@ -378,3 +384,24 @@ class Batcher:
         if not got.value:
             return None
         return ev.req_id, ev.reason, ev.prompt_len, buf[:min(ev.n_tokens, buf.size)].copy()
+
+
+# ---- decoder-layer engine ----------------------------------------------------------------
+class LayerDims(ctypes.Structure):
+    """ql_layer_dims (include/quantlib_amd.h)."""
+    _fields_ = [("hidden", _i), ("n_heads", _i), ("n_kv_heads", _i), ("head_dim", _i), ("ffn", _i),
+                ("rope_theta", _f), ("rms_eps", _f), ("rope_pairing", _i)]
+
+
+class LayerWeights(ctypes.Structure):
+    """ql_layer_weights: device addresses of one layer's fp16 weights."""
+    _fields_ = [("attn_norm", _p), ("wqkv", _p), ("wo", _p), ("ffn_norm", _p), ("w_gate", _p),
+                ("w_up", _p), ("w_down", _p)]
+
+
+class StepDevice(ctypes.Structure):
+    """ql_step_device: a step plan's arrays on the device plus the paged pool."""
+    _fields_ = [("n_rows", _i), ("n_seqs", _i), ("max_q_len", _i), ("max_ctx_len", _i),
+                ("max_blocks", _i), ("positions", _p), ("slot_mapping", _p), ("cu_q_lens", _p),
+                ("ctx_lens", _p), ("block_tables", _p), ("k_blocks", _p), ("v_blocks", _p),
+                ("n_blocks", _i), ("n_layers", _i)]

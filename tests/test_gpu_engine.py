@@ -1,0 +1,161 @@
+"""GPU parity of greedy sampling (ql_argmax_*) and of the decoder-layer engine
+(ql_engine_*): a small fp16 Llama-style layer run on batcher steps (a mixed
+prefill step, then an all-decode step that takes the split-decode path) against
+the oracle composed in the same order -- rmsnorm, x W^T, RoPE at the step's
+positions, causal attention over each sequence's K/V history, residual add,
+SwiGLU -- with a binary16 rounding after every stage, as the engine stores them.
+
+Layer tolerance, |got - want| <= 2e-2*|want| + 1e-2*max|want|: both sides round
+every stage to binary16 (2^-11 relative) but accumulate GEMMs in different
+orders (fp32 in hipBLASLt, double in the oracle), so single-ulp differences in
+intermediate values propagate through up to six dependent stages."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle as orc
+import quantlib_amd as ql
+from helpers import check_close, dev, empty, f16_bits_to_f32, host, normal, stream, to_f16_bits
+from test_gpu_attention import PagedPool
+
+pytestmark = pytest.mark.gpu
+
+
+# ---- argmax --------------------------------------------------------------------------------
+@pytest.mark.parametrize("rows,cols,pad", [(1, 5, 0), (7, 32000, 0), (3, 128256, 0), (5, 1001, 3),
+                                           (64, 4096, 8)])
+@pytest.mark.parametrize("f16", [False, True])
+def test_argmax_matches_oracle(rows, cols, pad, f16):
+    ld = cols + pad
+    x = normal(rows * cols + pad, (rows, ld), 3.0)
+    if rows >= 3:
+        x[0, :] = -np.inf
+        x[1, :cols // 2] = np.nan
+        x[2, 7 % cols] = x[2, (cols - 1)] = 50.0          # tie: first index wins
+    if f16:
+        xb = to_f16_bits(x)
+        want = orc.argmax(f16_bits_to_f32(xb)[:, :cols])
+    else:
+        xb = x
+        want = orc.argmax(x[:, :cols])
+    out = empty((rows,), np.int32)
+    d = dev(xb)
+    ql.call("ql_argmax_f16" if f16 else "ql_argmax_f32", d.ptr, rows, cols, ld, out.ptr, stream())
+    assert list(host(out)) == list(want)
+
+
+# ---- decoder layer -------------------------------------------------------------------------
+H, HK, HD, DM, FF = 4, 2, 64, 256, 512
+THETA, EPS, PAIR = 1e4, 1e-5, ql.ROPE_HALF
+
+
+def layer_weights(seed):
+    r = lambda s, shape, scale: to_f16_bits(normal(seed + s, shape, scale))
+    qkv_out = (H + 2 * HK) * HD
+    return {"attn_norm": to_f16_bits(np.random.default_rng(seed).uniform(0.5, 1.5, DM).astype(np.float32)),
+            "wqkv": r(1, (qkv_out, DM), DM ** -0.5), "wo": r(2, (DM, H * HD), (H * HD) ** -0.5),
+            "ffn_norm": to_f16_bits(np.random.default_rng(seed + 3).uniform(0.5, 1.5, DM).astype(np.float32)),
+            "w_gate": r(4, (FF, DM), DM ** -0.5), "w_up": r(5, (FF, DM), DM ** -0.5),
+            "w_down": r(6, (DM, FF), FF ** -0.5)}
+
+
+def oracle_layer(x, delta_in, w, plan, hist):
+    """One layer on the host; hist[req] holds (K rows, V rows) of earlier steps."""
+    if delta_in is None:
+        x1, y = x, orc.rmsnorm(x, w["attn_norm"], EPS, f16=True)
+    else:
+        x1, y = orc.add_rmsnorm(x, delta_in, w["attn_norm"], EPS, f16=True)
+    qkv = orc.matmul(y, w["wqkv"])
+    q = np.ascontiguousarray(qkv[:, :H * HD])
+    k = np.ascontiguousarray(qkv[:, H * HD:(H + HK) * HD])
+    v = np.ascontiguousarray(qkv[:, (H + HK) * HD:])
+    pos = plan["positions"]
+    q = orc.rope(q, H, HD, THETA, PAIR, positions=pos, f16=True)
+    k = orc.rope(k, HK, HD, THETA, PAIR, positions=pos, f16=True)
+    attn = np.zeros((plan["n_rows"], H * HD), np.uint16)
+    cu = plan["cu_q_lens"]
+    for i, rid in enumerate(plan["req_ids"]):
+        sl = slice(cu[i], cu[i + 1])
+        ks, vs = hist.setdefault(int(rid), ([], []))
+        ks.extend(k[sl])
+        vs.extend(v[sl])
+        kk = np.stack(ks).reshape(-1, HK, HD)
+        vv = np.stack(vs).reshape(-1, HK, HD)
+        attn[sl] = orc.attention(q[sl].reshape(-1, H, HD), kk, vv, H, HK, True, f16=True).reshape(-1, H * HD)
+    o = orc.matmul(attn, w["wo"])
+    x2 = orc.add(x1, o, f16=True)
+    y2 = orc.rmsnorm(x2, w["ffn_norm"], EPS, f16=True)
+    mid = orc.swiglu(orc.matmul(y2, w["w_gate"]), orc.matmul(y2, w["w_up"]), f16=True)
+    return x2, orc.matmul(mid, w["w_down"])
+
+
+def check_layer(got, want, what):
+    g, wv = f16_bits_to_f32(got), f16_bits_to_f32(want)
+    check_close(g, wv, 2e-2, 1e-2 * float(np.abs(wv).max()), what)
+
+
+def step_device(plan, pool, L, keep):
+    arrs = {k: dev(np.ascontiguousarray(plan[k], np.int32)) for k in
+            ("positions", "slot_mapping", "cu_q_lens", "ctx_lens")}
+    arrs["block_tables"] = dev(np.ascontiguousarray(plan["block_tables"], np.int32).reshape(-1))
+    keep.append(arrs)
+    return ql.StepDevice(plan["n_rows"], plan["n_seqs"], plan["max_q_len"], plan["max_ctx_len"],
+                         plan["max_blocks"], arrs["positions"].ptr, arrs["slot_mapping"].ptr,
+                         arrs["cu_q_lens"].ptr, arrs["ctx_lens"].ptr, arrs["block_tables"].ptr,
+                         pool.kptrs.ptr, pool.vptrs.ptr, pool.nb, L)
+
+
+def test_engine_layers_steps_and_logits_match_oracle():
+    L, nblk, vocab = 2, 32, 512
+    weights = [layer_weights(100 * (l + 1)) for l in range(L)]
+    dw = [{k: dev(v) for k, v in w.items()} for w in weights]
+    lw = [ql.LayerWeights(*(d[k].ptr for k in ("attn_norm", "wqkv", "wo", "ffn_norm", "w_gate", "w_up",
+                                               "w_down"))) for d in dw]
+    final_norm = to_f16_bits(np.random.default_rng(9).uniform(0.5, 1.5, DM).astype(np.float32))
+    lm_head = to_f16_bits(normal(10, (vocab, DM), DM ** -0.5))
+    d_final, d_lm = dev(final_norm), dev(lm_head)
+    dims = ql.LayerDims(DM, H, HK, HD, FF, THETA, EPS, PAIR)
+    eng = ctypes.c_void_p()
+    ql.call("ql_engine_create", ctypes.byref(dims), 64, 8, 256, ctypes.byref(eng))
+    pool = PagedPool(nblk, L, HK, HD)
+    b = ql.Batcher(nblk, 4)
+    prompts = {0: 20, 1: 33, 2: 5}
+    for rid, n in prompts.items():
+        b.add(rid, np.arange(n, dtype=np.int32), 8)
+    hist = [dict() for _ in range(L)]
+    keep = []
+    try:
+        for step in range(3):
+            plan = b.plan()
+            T = plan["n_rows"]
+            sd = step_device(plan, pool, L, keep)
+            x = to_f16_bits(normal(500 + step, (T, DM)))
+            dx = dev(x)
+            deltas = [empty((T * DM,), np.uint16) for _ in range(L)]
+            xo, delta = x, None
+            for l in range(L):
+                ql.call("ql_engine_layer_f16", eng, ctypes.byref(lw[l]), l, dx.ptr,
+                        deltas[l - 1].ptr if l else None, deltas[l].ptr, ctypes.byref(sd), stream())
+                xo, delta = oracle_layer(xo, delta, weights[l], plan, hist[l])
+                check_layer(host(dx, shape=(T, DM)), xo, f"step {step} layer {l} residual")
+                check_layer(host(deltas[l], shape=(T, DM)), delta, f"step {step} layer {l} mlp out")
+                xo = host(dx, shape=(T, DM)).copy()      # continue from the GPU's stream
+                delta = host(deltas[l], shape=(T, DM)).copy()
+            # logits of the sampled rows and greedy tokens
+            n = plan["n_seqs"]
+            rows_d = dev(plan["sample_rows"])
+            logits = empty((n * vocab,), np.uint16)
+            toks = empty((n,), np.int32)
+            ql.call("ql_engine_logits_f16", eng, dx.ptr, deltas[-1].ptr, d_final.ptr, d_lm.ptr, vocab,
+                    rows_d.ptr, n, T, logits.ptr, toks.ptr, stream())
+            xf = orc.add(xo, delta, f16=True)
+            yf = orc.rmsnorm(xf, final_norm, EPS, f16=True)
+            want = orc.matmul(yf[plan["sample_rows"]], lm_head)
+            got = host(logits, shape=(n, vocab))
+            check_layer(got, want, f"step {step} logits")
+            assert list(host(toks)) == list(orc.argmax(f16_bits_to_f32(got)))
+            b.commit(host(toks))
+            assert step == 0 or plan["max_q_len"] == 1        # later steps are all decodes
+    finally:
+        ql.call("ql_engine_destroy", eng)

@@ -422,3 +422,31 @@ def test_attention_f16_is_f32_arithmetic_on_widened_values():
     got = orc.attention(qh, kh, vh, 4, 2, True, f16=True)
     want = orc.attention(f16_bits_to_f32(qh), f16_bits_to_f32(kh), f16_bits_to_f32(vh), 4, 2, True)
     assert np.array_equal(got, orc.f32_to_f16(want))
+
+
+# ---- linear layer and greedy sampling --------------------------------------------------
+def test_matmul_matches_float64_numpy():
+    x = to_f16_bits(normal(71, (9, 40)))
+    w = to_f16_bits(normal(72, (13, 40), 0.2))
+    want = f16_bits_to_f32(x).astype(np.float64) @ f16_bits_to_f32(w).astype(np.float64).T
+    got = orc.matmul(x, w)
+    assert np.array_equal(got, orc.f32_to_f16(want.astype(np.float32)))
+
+
+def test_matmul_identity_and_permutation_weights():
+    x = to_f16_bits(normal(73, (5, 16)))
+    eye = to_f16_bits(np.eye(16, dtype=np.float32))
+    assert np.array_equal(orc.matmul(x, eye), x)
+    perm = np.random.default_rng(1).permutation(16)
+    assert np.array_equal(orc.matmul(x, eye[perm]), x[:, perm])
+
+
+def test_argmax_first_maximum_and_special_rows():
+    x = normal(74, (6, 50))
+    assert list(orc.argmax(x)) == list(np.argmax(x, axis=1))
+    row = np.array([[1.0, 3.0, 3.0, -1.0]], np.float32)
+    assert orc.argmax(row)[0] == 1                      # first of equal maxima
+    assert orc.argmax(np.full((1, 4), -np.inf, np.float32))[0] == 0
+    nan = np.array([[np.nan, 2.0, np.nan, 5.0, np.nan]], np.float32)
+    assert orc.argmax(nan)[0] == 3                      # NaN never wins
+    assert orc.argmax(np.full((1, 3), np.nan, np.float32))[0] == 0
