@@ -354,6 +354,55 @@ hipError_t ql_argmax_f32(const float* logits, int rows, int cols, int64_t ld, in
 hipError_t ql_argmax_f16(const uint16_t* logits, int rows, int cols, int64_t ld, int32_t* out,
                          hipStream_t stream);
 
+/* ---- fp16 library GEMM ------------------------------------------------------------------
+ * y[M, N] = x[M, K] W[N, K]^T (row-major, weights [out_features, in_features]), fp16
+ * in/out, fp32 accumulation, on hipBLASLt -- the hgemm/cuBLAS projections of
+ * src/fp16_forward.cu:184-186,204,211,219-221.  A per-device library context
+ * (handle, per-(M,N,K) plans, a 64 MB workspace per stream) is created on first use
+ * and kept until the process ends. */
+hipError_t ql_gemm_f16(const uint16_t* x, const uint16_t* w, uint16_t* y, int M, int N, int K,
+                       hipStream_t stream);
+
+/* ---- FP8 weight codec and FP8-weight GEMM (quantlib) ------------------------------------
+ * quantlib_fp16_to_fp8_e4m3/e5m2, quantlib_fp8_to_fp16, quantlib_fp8_gemm
+ * (quantlib_src/include/quantlib.h:10-28, kernels/fp8_convert.cu:15-173,
+ * kernels/fp8_gemm.cu:34-139).  Scales per group of the row-major [rows, cols] matrix
+ * (per-tensor: all of it; per-channel: one row; per-group: runs of group_size
+ * elements): scale = fmax / max|x| (max < 1e-8 -> 1), fmax 448 (E4M3) / 57344 (E5M2);
+ * q = encode(x * scale); dequant = binary16(decode(q) / scale).
+ * QL_FP8_MODE_REFERENCE: the reference's algorithm in IEEE arithmetic -- its max
+ *   reduction sees only the elements at offsets < 32 mod 128 of each group, and its
+ *   encoder truncates the mantissa, flushes subnormals to zero and clamps.
+ * QL_FP8_MODE_OCP: the whole group's max and the OCP E4M3FN / E5M2 encodings (round
+ *   to nearest even, subnormals, saturation to +-fmax), on gfx950's FP8 conversions. */
+#define QL_FP8_E4M3 0
+#define QL_FP8_E5M2 1
+#define QL_FP8_MODE_REFERENCE 0
+#define QL_FP8_MODE_OCP 1
+#define QL_QUANT_PER_TENSOR 0    /* QuantGranularity values of quant_types.h:17-21 */
+#define QL_QUANT_PER_CHANNEL 1
+#define QL_QUANT_PER_GROUP 2
+
+/* number of scales for a [rows, cols] matrix (host) */
+hipError_t ql_fp8_num_scales(int rows, int cols, int granularity, int group_size, int* n_scales);
+hipError_t ql_fp8_scales(const uint16_t* src, int rows, int cols, int format, int granularity,
+                         int group_size, int mode, float* scales, hipStream_t stream);
+/* scales (device, n_scales floats) are computed and written too */
+hipError_t ql_fp8_quantize(const uint16_t* src, int rows, int cols, int format, int granularity,
+                           int group_size, int mode, uint8_t* dst, float* scales,
+                           hipStream_t stream);
+hipError_t ql_fp8_dequantize(const uint8_t* src, const float* scales, int rows, int cols,
+                             int format, int granularity, int group_size, int mode,
+                             uint16_t* dst, hipStream_t stream);
+/* C[M, N] = A[M, K] (dequant W[N, K])^T, fp32 accumulation, fp16 out.  M <= 64 with
+ * N % 16 == 0, K % 64 == 0 and 16 | group length streams W once and dequantizes in
+ * registers (multiplying by 1/scale); otherwise W is dequantized into workspace
+ * (N*K*2 bytes, 16-byte aligned) and ql_gemm_f16 runs. */
+hipError_t ql_fp8_gemm_f16(const uint16_t* A, const uint8_t* W, const float* scales, int M, int N,
+                           int K, int format, int granularity, int group_size, int mode,
+                           uint16_t* C, void* workspace, size_t workspace_bytes,
+                           hipStream_t stream);
+
 /* ---- decoder-layer engine (fp16; hipBLASLt GEMMs + the kernels above) -----------------
  * One fp16 decoder layer for every row of a batched step, in the order of
  * fp16_layer_forward (src/fp16_forward.cu:167-223):

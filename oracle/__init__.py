@@ -50,6 +50,14 @@ _SIGS = {
     "or_reftest_attention_inputs": ([_p, _p, _p, _i64, ctypes.c_uint], None),
     "or_matmul_f16": ([_p, _p, _p, _i, _i, _i], None),
     "or_argmax_f32": ([_p, _i, _i, _p], None),
+    "or_fp8_encode_ref": ([_f, _i], ctypes.c_uint8),
+    "or_fp8_decode_ref": ([ctypes.c_uint8, _i], ctypes.c_float),
+    "or_fp8_encode_ocp": ([_f, _i], ctypes.c_uint8),
+    "or_fp8_decode_ocp": ([ctypes.c_uint8, _i], ctypes.c_float),
+    "or_fp8_num_scales": ([_i, _i, _i, _i], ctypes.c_int),
+    "or_fp8_scales": ([_p, _i, _i, _i, _i, _i, _i, _p], None),
+    "or_fp8_quantize": ([_p, _i, _i, _i, _i, _i, _i, _p, _p], None),
+    "or_fp8_dequantize": ([_p, _p, _i, _i, _i, _i, _i, _i, _p], None),
 }
 
 _lib = None
@@ -264,3 +272,35 @@ def argmax(x) -> np.ndarray:
     out = np.empty(x2.shape[0], np.int32)
     lib().or_argmax_f32(_ptr(x2), x2.shape[0], x2.shape[1], _ptr(out))
     return out.reshape(x.shape[:-1])
+
+
+# ---- FP8 codec (fmt 0 = E4M3, 1 = E5M2; mode 0 = reference, 1 = OCP) -------------------
+def fp8_encode(v: float, fmt: int, mode: int) -> int:
+    return (lib().or_fp8_encode_ocp if mode else lib().or_fp8_encode_ref)(float(v), fmt)
+
+
+def fp8_decode(q: int, fmt: int, mode: int) -> float:
+    return (lib().or_fp8_decode_ocp if mode else lib().or_fp8_decode_ref)(int(q), fmt)
+
+
+def fp8_num_scales(rows, cols, gran, group_size) -> int:
+    return lib().or_fp8_num_scales(rows, cols, gran, group_size)
+
+
+def fp8_quantize(x, fmt: int, gran: int, group_size: int, mode: int):
+    """x: binary16 [rows, cols] -> (codes uint8 [rows, cols], scales float32)."""
+    x = _u16(x)
+    rows, cols = x.shape
+    q = np.empty((rows, cols), np.uint8)
+    sc = np.empty(fp8_num_scales(rows, cols, gran, group_size), np.float32)
+    lib().or_fp8_quantize(_ptr(x), rows, cols, fmt, gran, group_size, mode, _ptr(q), _ptr(sc))
+    return q, sc
+
+
+def fp8_dequantize(q, scales, fmt: int, gran: int, group_size: int, mode: int) -> np.ndarray:
+    q = np.ascontiguousarray(q, np.uint8)
+    scales = _f32(scales)
+    rows, cols = q.shape
+    out = np.empty((rows, cols), np.uint16)
+    lib().or_fp8_dequantize(_ptr(q), _ptr(scales), rows, cols, fmt, gran, group_size, mode, _ptr(out))
+    return out

@@ -552,3 +552,143 @@ void or_argmax_f32(const float* x, int rows, int cols, int32_t* out) {
         out[r] = idx;
     }
 }
+
+/* ---- FP8 weight codec (quantlib) ----------------------------------------------------
+ * Two modes.
+ * REFERENCE (quantlib_src/include/quant_types.h:47-84, kernels/fp8_convert.cu:15-89):
+ *   scale  = fmax / m, m = max |x| over the elements the reference's reduction sees
+ *            (128 threads stride the group, only warp 0's lanes are reduced: the
+ *            elements whose offset within the group is < 32 mod 128); m < 1e-8 -> 1;
+ *   encode = clamp to +-fmax, rebias the exponent, TRUNCATE the mantissa, exponent
+ *            <= 0 -> signed zero, above the top -> top code;
+ *   decode = (1 + m/2^M) * 2^(e - bias), code with e = m = 0 -> +0;
+ *   dequant = decode(q) / scale, rounded to binary16.
+ * OCP (E4M3FN / E5M2 of the OCP 8-bit floating point spec): scale from the max over
+ *   the whole group; encode = round to nearest even with subnormals, saturating to
+ *   +-fmax (NaN stays NaN); decode per the spec.
+ * fmax = 448 (E4M3) or 57344 (E5M2).  Groups are runs of group_size elements of
+ * the row-major matrix (per-tensor: rows*cols, per-channel: cols).
+ * Pinned by: exhaustive code tables against the formats' closed forms, round trips
+ * of every code, brute-force nearest-value search for the OCP encoder, the
+ * reference's own truncation examples, and the reference test's max abs error
+ * bar (tests/test_oracle.py::test_fp8_*). */
+static float fp8_fmax(int fmt) { return fmt == 0 ? 448.0f : 57344.0f; }
+
+uint8_t or_fp8_encode_ref(float v, int fmt) {
+    const float fm = fp8_fmax(fmt);
+    v = v > fm ? fm : (v < -fm ? -fm : v);
+    uint32_t bits;
+    memcpy(&bits, &v, 4);
+    const uint8_t sign = (uint8_t)((bits >> 31) & 1);
+    const int mbits = fmt == 0 ? 3 : 2, bias = fmt == 0 ? 7 : 15, emax = fmt == 0 ? 15 : 31;
+    int e = (int)((bits >> 23) & 0xFF) - 127 + bias;
+    uint8_t m = (uint8_t)((bits >> (23 - mbits)) & ((1u << mbits) - 1));
+    if (e <= 0) return (uint8_t)(sign << 7);
+    if (e > emax) {
+        e = emax;
+        m = (uint8_t)((1u << mbits) - 1);
+    }
+    return (uint8_t)((sign << 7) | (e << mbits) | m);
+}
+
+float or_fp8_decode_ref(uint8_t q, int fmt) {
+    const int mbits = fmt == 0 ? 3 : 2, bias = fmt == 0 ? 7 : 15;
+    const int e = (q >> mbits) & (fmt == 0 ? 0xF : 0x1F);
+    const int m = q & ((1 << mbits) - 1);
+    if (e == 0 && m == 0) return 0.0f;
+    const float r = ldexpf(1.0f + (float)m / (float)(1 << mbits), e - bias);
+    return (q >> 7) ? -r : r;
+}
+
+float or_fp8_decode_ocp(uint8_t q, int fmt) {
+    const int mbits = fmt == 0 ? 3 : 2, bias = fmt == 0 ? 7 : 15;
+    const int emask = fmt == 0 ? 0xF : 0x1F;
+    const int e = (q >> mbits) & emask, m = q & ((1 << mbits) - 1);
+    const int s = q >> 7;
+    float r;
+    if (fmt == 0 && e == 0xF && m == 7) return NAN;                 /* E4M3FN: only NaN */
+    if (fmt == 1 && e == 0x1F) r = m ? NAN : INFINITY;               /* E5M2: IEEE-like */
+    else if (e == 0) r = ldexpf((float)m / (float)(1 << mbits), 1 - bias);
+    else r = ldexpf(1.0f + (float)m / (float)(1 << mbits), e - bias);
+    return s ? -r : r;
+}
+
+/* Round to nearest even onto the format grid, saturating at +-fmax. */
+uint8_t or_fp8_encode_ocp(float v, int fmt) {
+    const int mbits = fmt == 0 ? 3 : 2, bias = fmt == 0 ? 7 : 15;
+    if (isnan(v)) return fmt == 0 ? 0x7F : 0x7E;
+    const uint8_t sign = signbit(v) ? 0x80 : 0;
+    double a = fabs((double)v);
+    const double fm = fp8_fmax(fmt);
+    if (a >= fm) return (uint8_t)(sign | (fmt == 0 ? 0x7E : 0x7B));
+    /* quantum at a's binade (subnormal quantum below the first normal binade) */
+    int ex;
+    frexp(a, &ex);                     /* a = f * 2^ex, f in [0.5, 1) */
+    int e_unb = ex - 1;                /* a in [2^e_unb, 2^(e_unb+1)) */
+    if (e_unb < 1 - bias) e_unb = 1 - bias;
+    const double quantum = ldexp(1.0, e_unb - mbits);
+    double n = a / quantum;            /* exact: power-of-two quantum */
+    double fl = floor(n);
+    double r = n - fl;
+    if (r > 0.5 || (r == 0.5 && fmod(fl, 2.0) != 0.0)) fl += 1.0;
+    const double val = fl * quantum;
+    if (val >= fm) return (uint8_t)(sign | (fmt == 0 ? 0x7E : 0x7B));
+    if (val == 0.0) return sign;
+    /* encode val */
+    int ev;
+    frexp(val, &ev);
+    int e = ev - 1 + bias;
+    int m;
+    if (e <= 0) {
+        e = 0;
+        m = (int)(val / ldexp(1.0, 1 - bias - mbits));
+    } else {
+        m = (int)((val / ldexp(1.0, ev - 1) - 1.0) * (1 << mbits));
+    }
+    return (uint8_t)(sign | (e << mbits) | m);
+}
+
+int or_fp8_num_scales(int rows, int cols, int gran, int group_size) {
+    const long long n = (long long)rows * cols;
+    if (gran == 0) return 1;
+    if (gran == 1) return rows;
+    return (int)((n + group_size - 1) / group_size);
+}
+
+static long long fp8_group(int rows, int cols, int gran, int group_size) {
+    return gran == 0 ? (long long)rows * cols : (gran == 1 ? cols : group_size);
+}
+
+void or_fp8_scales(const uint16_t* src, int rows, int cols, int fmt, int gran, int group_size,
+                   int mode, float* scales) {
+    const long long n = (long long)rows * cols, gs = fp8_group(rows, cols, gran, group_size);
+    const int ns = or_fp8_num_scales(rows, cols, gran, group_size);
+    for (int g = 0; g < ns; ++g) {
+        float mx = 0.0f;
+        for (long long i = 0; i < gs && g * gs + i < n; ++i) {
+            if (mode == 0 && (i % 128) >= 32) continue;   /* lanes the reference reduces */
+            const float a = fabsf(or_f16_to_f32(src[g * gs + i]));
+            mx = fmaxf(mx, a);
+        }
+        scales[g] = mx < 1e-8f ? 1.0f : fp8_fmax(fmt) / mx;
+    }
+}
+
+void or_fp8_quantize(const uint16_t* src, int rows, int cols, int fmt, int gran, int group_size,
+                     int mode, uint8_t* dst, float* scales) {
+    or_fp8_scales(src, rows, cols, fmt, gran, group_size, mode, scales);
+    const long long n = (long long)rows * cols, gs = fp8_group(rows, cols, gran, group_size);
+    for (long long i = 0; i < n; ++i) {
+        const float v = or_f16_to_f32(src[i]) * scales[i / gs];
+        dst[i] = mode == 0 ? or_fp8_encode_ref(v, fmt) : or_fp8_encode_ocp(v, fmt);
+    }
+}
+
+void or_fp8_dequantize(const uint8_t* src, const float* scales, int rows, int cols, int fmt,
+                       int gran, int group_size, int mode, uint16_t* dst) {
+    const long long n = (long long)rows * cols, gs = fp8_group(rows, cols, gran, group_size);
+    for (long long i = 0; i < n; ++i) {
+        const float d = mode == 0 ? or_fp8_decode_ref(src[i], fmt) : or_fp8_decode_ocp(src[i], fmt);
+        dst[i] = or_f32_to_f16(d / scales[i / gs]);
+    }
+}

@@ -99,6 +99,21 @@ void or_matmul_f16(const uint16_t* x, const uint16_t* w, uint16_t* y, int M, int
 /* First index of the row maximum (strict >, NaN ignored, 0 if none above -inf). */
 void or_argmax_f32(const float* x, int rows, int cols, int32_t* out);
 
+/* FP8 codec: fmt 0 = E4M3, 1 = E5M2; mode 0 = the reference's (warp-0 scale,
+ * truncating), 1 = OCP (full-group scale, RNE, saturating); gran 0/1/2 =
+ * per-tensor / per-channel / per-group. */
+uint8_t or_fp8_encode_ref(float v, int fmt);
+float or_fp8_decode_ref(uint8_t q, int fmt);
+uint8_t or_fp8_encode_ocp(float v, int fmt);
+float or_fp8_decode_ocp(uint8_t q, int fmt);
+int or_fp8_num_scales(int rows, int cols, int gran, int group_size);
+void or_fp8_scales(const uint16_t* src, int rows, int cols, int fmt, int gran, int group_size,
+                   int mode, float* scales);
+void or_fp8_quantize(const uint16_t* src, int rows, int cols, int fmt, int gran, int group_size,
+                     int mode, uint8_t* dst, float* scales);
+void or_fp8_dequantize(const uint8_t* src, const float* scales, int rows, int cols, int fmt,
+                       int gran, int group_size, int mode, uint16_t* dst);
+
 #ifdef __cplusplus
 }
 #endif

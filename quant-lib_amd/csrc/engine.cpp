@@ -16,27 +16,14 @@
 // The MLP output is returned as delta_out and added by the next layer's fused
 // add+RMSNorm (or by ql_engine_logits_f16 after the last layer).  Weights are
 // row-major [out_features, in_features] fp16 (y = x W^T).  GEMMs accumulate in
-// fp32 and write fp16.  The engine owns its activation buffers, the GEMM
-// workspace and the split-decode workspace, all allocated once at creation;
-// the per-step calls allocate nothing.
+// fp32 and write fp16 (ql_gemm_f16).  The engine owns its activation buffers and
+// the split-decode workspace, allocated once at creation; the per-step calls
+// allocate nothing (the GEMM library context is created on the first GEMM).
 #include "quantlib_amd.h"
 
-#include <hipblaslt/hipblaslt.h>
-
-#include <map>
 #include <new>
-#include <tuple>
 
 namespace {
-
-constexpr size_t kGemmWorkspace = 64u << 20;
-
-struct GemmPlan {
-    hipblasLtMatmulDesc_t desc = nullptr;
-    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
-    hipblasLtMatmulAlgo_t algo{};
-    bool ok = false;
-};
 
 size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
@@ -45,62 +32,18 @@ size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 struct ql_engine {
     ql_layer_dims dims{};
     int max_rows = 0, max_seqs = 0, max_ctx = 0;
-    hipblasLtHandle_t lt = nullptr;
-    void* gemm_ws = nullptr;
     void* arena = nullptr;
     uint16_t *y = nullptr, *qkv = nullptr, *attn = nullptr, *o = nullptr, *g = nullptr, *u = nullptr,
              *mid = nullptr;
     void* dec_ws = nullptr;
     size_t dec_ws_bytes = 0;
-    std::map<std::tuple<int, int, int>, GemmPlan> gemms;
 
-    // y[M, N] = x[M, K] W[N, K]^T  (row-major, fp16 in/out, fp32 accumulate)
     hipError_t gemm(const uint16_t* x, const uint16_t* w, uint16_t* out, int M, int N, int K,
                     hipStream_t stream) {
-        GemmPlan& p = gemms[std::make_tuple(M, N, K)];
-        if (!p.ok) {
-            // column-major view: out^T (N x M) = op(A) op(B), A = W stored K x N (transposed),
-            // B = x stored K x M
-            const hipblasOperation_t opT = HIPBLAS_OP_T, opN = HIPBLAS_OP_N;
-            if (hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS ||
-                hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opT, sizeof(opT)) !=
-                    HIPBLAS_STATUS_SUCCESS ||
-                hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opN, sizeof(opN)) !=
-                    HIPBLAS_STATUS_SUCCESS ||
-                hipblasLtMatrixLayoutCreate(&p.a, HIP_R_16F, (uint64_t)K, (uint64_t)N, K) != HIPBLAS_STATUS_SUCCESS ||
-                hipblasLtMatrixLayoutCreate(&p.b, HIP_R_16F, (uint64_t)K, (uint64_t)M, K) != HIPBLAS_STATUS_SUCCESS ||
-                hipblasLtMatrixLayoutCreate(&p.c, HIP_R_16F, (uint64_t)N, (uint64_t)M, N) != HIPBLAS_STATUS_SUCCESS)
-                return hipErrorUnknown;
-            hipblasLtMatmulPreference_t pref = nullptr;
-            if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return hipErrorUnknown;
-            const uint64_t ws = kGemmWorkspace;
-            hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws,
-                                                  sizeof(ws));
-            hipblasLtMatmulHeuristicResult_t res{};
-            int n = 0;
-            const hipblasStatus_t st = hipblasLtMatmulAlgoGetHeuristic(lt, p.desc, p.a, p.b, p.c, p.c, pref,
-                                                                       1, &res, &n);
-            hipblasLtMatmulPreferenceDestroy(pref);
-            if (st != HIPBLAS_STATUS_SUCCESS || n < 1 || res.workspaceSize > kGemmWorkspace)
-                return hipErrorNotSupported;
-            p.algo = res.algo;
-            p.ok = true;
-        }
-        const float alpha = 1.0f, beta = 0.0f;
-        const hipblasStatus_t st = hipblasLtMatmul(lt, p.desc, &alpha, w, p.a, x, p.b, &beta, out, p.c,
-                                                   out, p.c, &p.algo, gemm_ws, kGemmWorkspace, stream);
-        return st == HIPBLAS_STATUS_SUCCESS ? hipSuccess : hipErrorLaunchFailure;
+        return ql_gemm_f16(x, w, out, M, N, K, stream);
     }
 
     ~ql_engine() {
-        for (auto& kv : gemms) {
-            if (kv.second.a) hipblasLtMatrixLayoutDestroy(kv.second.a);
-            if (kv.second.b) hipblasLtMatrixLayoutDestroy(kv.second.b);
-            if (kv.second.c) hipblasLtMatrixLayoutDestroy(kv.second.c);
-            if (kv.second.desc) hipblasLtMatmulDescDestroy(kv.second.desc);
-        }
-        if (lt) hipblasLtDestroy(lt);
-        if (gemm_ws) (void)hipFree(gemm_ws);
         if (arena) (void)hipFree(arena);
     }
 };
@@ -138,8 +81,7 @@ extern "C" hipError_t ql_engine_create(const ql_layer_dims* d, int max_rows, int
     size_t total = 0;
     for (size_t s : sizes) total += align256(s * sizeof(uint16_t));
     total += align256(ws);
-    if (hipMalloc(&e->arena, total) != hipSuccess || hipMalloc(&e->gemm_ws, kGemmWorkspace) != hipSuccess ||
-        hipblasLtCreate(&e->lt) != HIPBLAS_STATUS_SUCCESS) {
+    if (hipMalloc(&e->arena, total) != hipSuccess) {
         delete e;
         return hipErrorOutOfMemory;
     }

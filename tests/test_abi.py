@@ -141,6 +141,17 @@ P = 4096  # a non-null, 16-byte aligned dummy address: never dereferenced on the
     (("ql_paged_decode_attention_f16", None, None, 512, 512, 0, None, 0, None, 0, None, None, 0, 0,
       1, 8, 2, 64, None, 0, None), 0),
     (("ql_paged_decode_workspace_size", 4, 8, 2, 64, 100, None), INVALID),
+    # FP8: bad format / mode / granularity / group size; empty problems; GEMM without workspace
+    (("ql_fp8_quantize", P, 4, 64, 2, 0, 0, 0, P, P, None), INVALID),
+    (("ql_fp8_quantize", P, 4, 64, 0, 0, 0, 3, P, P, None), INVALID),
+    (("ql_fp8_quantize", P, 4, 64, 0, 5, 0, 0, P, P, None), INVALID),
+    (("ql_fp8_quantize", P, 4, 64, 0, 2, 0, 0, P, P, None), INVALID),
+    (("ql_fp8_quantize", None, 0, 64, 0, 2, 128, 0, None, None, None), 0),
+    (("ql_fp8_dequantize", P, None, 4, 64, 0, 2, 128, 1, P, None), INVALID),
+    (("ql_fp8_gemm_f16", P, P, P, 100, 64, 64, 0, 2, 128, 1, P, None, 0, None), INVALID),
+    (("ql_fp8_gemm_f16", None, None, None, 0, 64, 64, 0, 2, 128, 1, None, None, 0, None), 0),
+    (("ql_gemm_f16", P, P, P, -1, 4, 4, None), INVALID),
+    (("ql_gemm_f16", None, None, None, 0, 4, 4, None), 0),
 ])
 def test_argument_validation(call, expect):
     name, *args = call

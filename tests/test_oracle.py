@@ -450,3 +450,100 @@ def test_argmax_first_maximum_and_special_rows():
     nan = np.array([[np.nan, 2.0, np.nan, 5.0, np.nan]], np.float32)
     assert orc.argmax(nan)[0] == 3                      # NaN never wins
     assert orc.argmax(np.full((1, 3), np.nan, np.float32))[0] == 0
+
+
+# ---- FP8 codec ----------------------------------------------------------------------------
+E4M3, E5M2, REF, OCP = 0, 1, 0, 1
+
+
+def spec_value(q, fmt):
+    """Closed form of each OCP 8-bit code (the OCP FP8 specification's tables)."""
+    mb, bias = (3, 7) if fmt == E4M3 else (2, 15)
+    s, e, m = q >> 7, (q >> mb) & ((1 << (7 - mb)) - 1), q & ((1 << mb) - 1)
+    if fmt == E4M3 and e == 15 and m == 7:
+        return math.nan
+    if fmt == E5M2 and e == 31:
+        return math.nan if m else (-math.inf if s else math.inf)
+    v = (m / (1 << mb)) * 2.0 ** (1 - bias) if e == 0 else (1 + m / (1 << mb)) * 2.0 ** (e - bias)
+    return -v if s else v
+
+
+@pytest.mark.parametrize("fmt", [E4M3, E5M2])
+def test_fp8_ocp_decode_table_and_round_trip(fmt):
+    for q in range(256):
+        want, got = spec_value(q, fmt), orc.fp8_decode(q, fmt, OCP)
+        if math.isnan(want):
+            assert math.isnan(got)
+            continue
+        assert got == want, (q, got, want)
+        if math.isfinite(want):
+            enc = orc.fp8_encode(want, fmt, OCP)
+            assert enc == q or (want == 0 and enc & 0x7F == 0), (q, enc)
+
+
+@pytest.mark.parametrize("fmt", [E4M3, E5M2])
+def test_fp8_ocp_encode_is_nearest_even_saturating(fmt):
+    grid = sorted({spec_value(q, fmt) for q in range(128) if math.isfinite(spec_value(q, fmt))})
+    fmax = grid[-1]
+    xs = np.concatenate([np.linspace(0, fmax * 1.1, 4001), (np.array(grid[:-1]) + np.array(grid[1:])) / 2])
+    for x in xs.astype(np.float32):
+        x = float(x)
+        q = orc.fp8_encode(x, fmt, OCP)
+        got = spec_value(q, fmt)
+        if x >= fmax:
+            assert got == fmax
+            continue
+        d = [abs(g - x) for g in grid]
+        best = min(d)
+        cands = [g for g, dd in zip(grid, d) if dd == best]
+        if len(cands) == 2:   # tie: even mantissa (code LSB 0)
+            assert orc.fp8_encode(cands[0], fmt, OCP) & 1 == 0 and got == cands[0] or \
+                orc.fp8_encode(cands[1], fmt, OCP) & 1 == 0 and got == cands[1]
+        else:
+            assert got == cands[0], (x, got, cands)
+        assert orc.fp8_encode(-x, fmt, OCP) == (q | 0x80 if x else orc.fp8_encode(-x, fmt, OCP))
+
+
+@pytest.mark.parametrize("fmt", [E4M3, E5M2])
+def test_fp8_reference_codec_truncates(fmt):
+    fmax = 448.0 if fmt == E4M3 else 57344.0
+    mb = 3 if fmt == E4M3 else 2
+    # known answers of the truncating encoder (quant_types.h:47-84)
+    assert orc.fp8_encode(1.0, fmt, REF) == (0x38 if fmt == E4M3 else 0x3C)
+    assert orc.fp8_encode(fmax * 4, fmt, REF) == (0x7E if fmt == E4M3 else 0x7B)
+    assert orc.fp8_encode(-1e-30, fmt, REF) == 0x80                  # underflow -> signed zero
+    assert orc.fp8_decode(0x80, fmt, REF) == 0.0                      # e = m = 0 -> +0
+    h = np.arange(0, 0x7C00, 7, dtype=np.uint32).astype(np.uint16)   # positive halves
+    for x in f16_bits_to_f32(h):
+        x = float(x)
+        q = orc.fp8_encode(x, fmt, REF)
+        d = orc.fp8_decode(q, fmt, REF)
+        if x >= fmax:
+            assert d == fmax
+        elif q == 0:
+            assert x < 2.0 ** (1 - (7 if fmt == E4M3 else 15))       # below the smallest normal
+        else:   # truncation: never above x, within one quantum of the binade
+            assert d <= x < d + 2.0 ** (math.floor(math.log2(d)) - mb)
+
+
+@pytest.mark.parametrize("mode", [REF, OCP])
+@pytest.mark.parametrize("gran,gs", [(0, 0), (1, 0), (2, 128), (2, 100)])
+def test_fp8_quantize_scales_and_reference_error_bar(mode, gran, gs):
+    # the reference test's inputs and bar (quantlib_src/tests/test_fp8.cu:24-58):
+    # U(-1, 1) weights, max abs dequantization error < 0.25
+    x = to_f16_bits(uniform(81, (64, 256), -1.0, 1.0))
+    for fmt in (E4M3, E5M2):
+        q, sc = orc.fp8_quantize(x, fmt, gran, gs, mode)
+        g = 64 * 256 if gran == 0 else (256 if gran == 1 else gs)
+        assert sc.size == -(-x.size // g)
+        xf = f16_bits_to_f32(x).ravel()
+        for i in range(sc.size):   # the scale rule of each mode
+            grp = np.abs(xf[i * g:(i + 1) * g])
+            seen = grp if mode == OCP else grp[(np.arange(grp.size) % 128) < 32]
+            assert sc[i] == np.float32(np.float32(448.0 if fmt == E4M3 else 57344.0) / np.float32(seen.max()))
+        back = f16_bits_to_f32(orc.fp8_dequantize(q, sc, fmt, gran, gs, mode))
+        err = float(np.abs(back - f16_bits_to_f32(x)).max())
+        assert err < 0.25, err
+        if mode == OCP:   # nearest-even with a full-group scale: half a quantum
+            rel = np.abs(back - f16_bits_to_f32(x)) / np.maximum(np.abs(f16_bits_to_f32(x)), 1e-3)
+            assert float(np.median(rel)) < (2 ** -4 if fmt == E4M3 else 2 ** -3)
