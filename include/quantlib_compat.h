@@ -127,4 +127,48 @@ int paged_kv_allocate_block(PagedKVCache* cache);
 void paged_kv_free_block(PagedKVCache* cache, int block_idx);
 }
 
+/* ---- quantlib FP8 (quantlib_src/include/quant_types.h:15-45, quantlib.h:10-43) -----
+ * Same types and names; the conversions run the reference's algorithm
+ * (QL_FP8_MODE_REFERENCE of quantlib_amd.h) and, like the reference, allocate the
+ * QuantMatrix's device buffers (freed by quantlib_free).  quantlib_fp8_gemm with
+ * M > 64 dequantizes into a process-wide device buffer that grows on demand. */
+typedef uint8_t fp8_e4m3_t;
+typedef uint8_t fp8_e5m2_t;
+
+typedef enum {
+    QUANT_PER_TENSOR = 0,
+    QUANT_PER_CHANNEL = 1,
+    QUANT_PER_GROUP = 2
+} QuantGranularity;
+
+typedef struct {
+    float* scales;
+    float* zeros;
+    int group_size;
+    QuantGranularity granularity;
+    int n_scales;
+} QuantParams;
+
+typedef struct {
+    void* data;
+    QuantParams params;
+    int rows;
+    int cols;
+    int bits;
+    char format[16];
+} QuantMatrix;
+
+extern "C" {
+QuantMatrix quantlib_fp16_to_fp8_e4m3(const __half* src, int rows, int cols, QuantGranularity gran,
+                                      int group_size, hipStream_t stream);
+QuantMatrix quantlib_fp16_to_fp8_e5m2(const __half* src, int rows, int cols, QuantGranularity gran,
+                                      int group_size, hipStream_t stream);
+void quantlib_fp8_to_fp16(const QuantMatrix* qm, __half* dst, hipStream_t stream);
+void quantlib_fp8_gemm(const __half* A, const QuantMatrix* W, __half* C, int M, int N, int K,
+                       hipStream_t stream);
+void quantlib_free(QuantMatrix* qm);
+float quantlib_quant_error(const __half* original, const __half* dequantized, int n_elements);
+void quantlib_print_stats(const QuantMatrix* qm);
+}
+
 #endif /* QUANTLIB_COMPAT_H */

@@ -58,6 +58,7 @@ _SIGS = {
     "or_fp8_scales": ([_p, _i, _i, _i, _i, _i, _i, _p], None),
     "or_fp8_quantize": ([_p, _i, _i, _i, _i, _i, _i, _p, _p], None),
     "or_fp8_dequantize": ([_p, _p, _i, _i, _i, _i, _i, _i, _p], None),
+    "or_reftest_fp8_inputs": ([_p, _i64, ctypes.c_uint], None),
 }
 
 _lib = None
@@ -303,4 +304,10 @@ def fp8_dequantize(q, scales, fmt: int, gran: int, group_size: int, mode: int) -
     rows, cols = q.shape
     out = np.empty((rows, cols), np.uint16)
     lib().or_fp8_dequantize(_ptr(q), _ptr(scales), rows, cols, fmt, gran, group_size, mode, _ptr(out))
+    return out
+
+
+def reftest_fp8_inputs(rows: int, cols: int, seed: int = 1) -> np.ndarray:
+    out = np.empty((rows, cols), np.float32)
+    lib().or_reftest_fp8_inputs(_ptr(out), out.size, seed)
     return out

@@ -692,3 +692,10 @@ void or_fp8_dequantize(const uint8_t* src, const float* scales, int rows, int co
         dst[i] = or_f32_to_f16(d / scales[i / gs]);
     }
 }
+
+/* Inputs of quantlib_src/tests/test_fp8.cu:27-29 (glibc rand, default seed 1):
+ * x = ((float)rand() / RAND_MAX) * 2 - 1. */
+void or_reftest_fp8_inputs(float* out, int64_t n, unsigned seed) {
+    srand(seed);
+    for (int64_t i = 0; i < n; ++i) out[i] = ((float)rand() / RAND_MAX) * 2.0f - 1.0f;
+}

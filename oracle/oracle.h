@@ -114,6 +114,9 @@ void or_fp8_quantize(const uint16_t* src, int rows, int cols, int fmt, int gran,
 void or_fp8_dequantize(const uint8_t* src, const float* scales, int rows, int cols, int fmt,
                        int gran, int group_size, int mode, uint16_t* dst);
 
+/* Inputs of quantlib_src/tests/test_fp8.cu:27-29. */
+void or_reftest_fp8_inputs(float* out, int64_t n, unsigned seed);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,10 +1,16 @@
 // compat.cpp -- the reference's launcher names and KV-cache host API on top of
 // the ql_* C ABI (declarations and behaviour notes in quantlib_compat.h).
 //
-// Host code only: it validates nothing beyond what the ql_* calls check and
-// never synchronises, matching the reference launchers' fire-and-forget style.
+// Host code only: it validates nothing beyond what the ql_* calls check and,
+// like the reference, only the quantlib helpers that copy to the host (or grow
+// the FP8 GEMM's dequantization buffer) synchronise.
+#include <math.h>
+#include <stdio.h>
 #include <stdlib.h>
+
 #include <string.h>
+
+#include <mutex>
 
 #include <hip/hip_runtime_api.h>
 
@@ -15,6 +21,16 @@ namespace {
 
 uint16_t* bits(__half* p) { return reinterpret_cast<uint16_t*>(p); }
 const uint16_t* bits(const __half* p) { return reinterpret_cast<const uint16_t*>(p); }
+
+// IEEE binary16 -> float (exact)
+float half_to_float(uint16_t h) {
+    const int e = (h >> 10) & 0x1F, m = h & 0x3FF;
+    float v;
+    if (e == 0) v = ldexpf((float)m, -24);
+    else if (e == 31) v = m ? NAN : INFINITY;
+    else v = ldexpf((float)(m | 0x400), e - 25);
+    return (h & 0x8000) ? -v : v;
+}
 
 }  // namespace
 
@@ -284,4 +300,134 @@ extern "C" void paged_kv_free_block(PagedKVCache* cache, int block_idx) {
         return;
     cache->free_blocks[cache->free_count] = block_idx;
     cache->free_count++;
+}
+
+// ---- quantlib FP8 (quantlib_src/src/quantlib.cu:26-143, kernels/fp8_convert.cu:91-173) ----
+namespace {
+
+int fp8_format_of(const QuantMatrix* qm) {
+    return (qm->format[0] == 'E' && qm->format[1] == '5') ? QL_FP8_E5M2 : QL_FP8_E4M3;
+}
+
+QuantMatrix fp16_to_fp8(const __half* src, int rows, int cols, QuantGranularity gran,
+                        int group_size, int fmt, hipStream_t stream) {
+    QuantMatrix qm;
+    memset(&qm, 0, sizeof(qm));
+    qm.rows = rows;
+    qm.cols = cols;
+    qm.bits = 8;
+    snprintf(qm.format, sizeof(qm.format), "%s", fmt == QL_FP8_E4M3 ? "E4M3" : "E5M2");
+    const long long n = (long long)rows * cols;
+    // group_size as the reference stores it (quantlib_src/kernels/fp8_convert.cu:111-112)
+    qm.params.granularity = gran;
+    qm.params.group_size = gran == QUANT_PER_TENSOR ? (int)n : (gran == QUANT_PER_CHANNEL ? cols : group_size);
+    int ns = 0;
+    if (ql_fp8_num_scales(rows, cols, (int)gran, group_size, &ns) != hipSuccess || n <= 0) return qm;
+    qm.params.n_scales = ns;
+    if (hipMalloc(&qm.data, (size_t)n) != hipSuccess) {
+        qm.data = nullptr;
+        return qm;
+    }
+    if (hipMalloc(reinterpret_cast<void**>(&qm.params.scales), (size_t)ns * sizeof(float)) != hipSuccess) {
+        (void)hipFree(qm.data);
+        qm.data = nullptr;
+        qm.params.scales = nullptr;
+        return qm;
+    }
+    (void)ql_fp8_quantize(bits(src), rows, cols, fmt, (int)gran, group_size, QL_FP8_MODE_REFERENCE,
+                          static_cast<uint8_t*>(qm.data), qm.params.scales, stream);
+    return qm;
+}
+
+std::mutex g_ws_mu;
+void* g_ws = nullptr;
+size_t g_ws_bytes = 0;
+
+}  // namespace
+
+extern "C" QuantMatrix quantlib_fp16_to_fp8_e4m3(const __half* src, int rows, int cols,
+                                                 QuantGranularity gran, int group_size,
+                                                 hipStream_t stream) {
+    return fp16_to_fp8(src, rows, cols, gran, group_size, QL_FP8_E4M3, stream);
+}
+
+extern "C" QuantMatrix quantlib_fp16_to_fp8_e5m2(const __half* src, int rows, int cols,
+                                                 QuantGranularity gran, int group_size,
+                                                 hipStream_t stream) {
+    return fp16_to_fp8(src, rows, cols, gran, group_size, QL_FP8_E5M2, stream);
+}
+
+extern "C" void quantlib_fp8_to_fp16(const QuantMatrix* qm, __half* dst, hipStream_t stream) {
+    if (!qm || qm->bits != 8) return;
+    (void)ql_fp8_dequantize(static_cast<const uint8_t*>(qm->data), qm->params.scales, qm->rows, qm->cols,
+                            fp8_format_of(qm), (int)qm->params.granularity, qm->params.group_size,
+                            QL_FP8_MODE_REFERENCE, bits(dst), stream);
+}
+
+extern "C" void quantlib_fp8_gemm(const __half* A, const QuantMatrix* W, __half* C, int M, int N,
+                                  int K, hipStream_t stream) {
+    if (!W || W->bits != 8) return;
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    if (M > 64 && N > 0 && K > 0) {
+        std::lock_guard<std::mutex> lock(g_ws_mu);
+        const size_t need = (size_t)N * (size_t)K * sizeof(uint16_t);
+        if (g_ws_bytes < need) {
+            if (g_ws) {
+                (void)hipStreamSynchronize(stream);
+                (void)hipFree(g_ws);
+            }
+            if (hipMalloc(&g_ws, need) != hipSuccess) {
+                g_ws = nullptr;
+                g_ws_bytes = 0;
+                return;
+            }
+            g_ws_bytes = need;
+        }
+        ws = g_ws;
+        ws_bytes = g_ws_bytes;
+    }
+    (void)ql_fp8_gemm_f16(bits(A), static_cast<const uint8_t*>(W->data), W->params.scales, M, N, K,
+                          fp8_format_of(W), (int)W->params.granularity, W->params.group_size,
+                          QL_FP8_MODE_REFERENCE, bits(C), ws, ws_bytes, stream);
+}
+
+extern "C" void quantlib_free(QuantMatrix* qm) {
+    if (!qm) return;
+    if (qm->data) (void)hipFree(qm->data);
+    if (qm->params.scales) (void)hipFree(qm->params.scales);
+    if (qm->params.zeros) (void)hipFree(qm->params.zeros);
+    qm->data = nullptr;
+    qm->params.scales = nullptr;
+    qm->params.zeros = nullptr;
+}
+
+extern "C" float quantlib_quant_error(const __half* original, const __half* dequantized,
+                                      int n_elements) {
+    if (n_elements <= 0) return 0.0f;
+    uint16_t* a = static_cast<uint16_t*>(malloc((size_t)n_elements * 2));
+    uint16_t* b = static_cast<uint16_t*>(malloc((size_t)n_elements * 2));
+    float max_err = 0.0f;
+    if (a && b && hipMemcpy(a, original, (size_t)n_elements * 2, hipMemcpyDeviceToHost) == hipSuccess &&
+        hipMemcpy(b, dequantized, (size_t)n_elements * 2, hipMemcpyDeviceToHost) == hipSuccess) {
+        for (int i = 0; i < n_elements; ++i) {
+            const float e = fabsf(half_to_float(a[i]) - half_to_float(b[i]));
+            if (e > max_err) max_err = e;
+        }
+    }
+    free(a);
+    free(b);
+    return max_err;
+}
+
+extern "C" void quantlib_print_stats(const QuantMatrix* qm) {
+    if (!qm) return;
+    const size_t raw = (size_t)qm->rows * qm->cols * 2;
+    const size_t quant = qm->bits == 8 ? (size_t)qm->rows * qm->cols : ((size_t)qm->rows * qm->cols + 1) / 2;
+    printf("QuantMatrix [%s]  %d x %d  bits=%d\n", qm->format, qm->rows, qm->cols, qm->bits);
+    printf("  FP16 size    : %.2f MB\n", raw / 1e6f);
+    printf("  Quant size   : %.2f MB\n", quant / 1e6f);
+    printf("  Compression  : %.2fx\n", quant ? (float)raw / quant : 0.0f);
+    printf("  Scales       : %d  (granularity=%d  group=%d)\n", qm->params.n_scales,
+           (int)qm->params.granularity, qm->params.group_size);
 }

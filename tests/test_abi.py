@@ -39,6 +39,13 @@ COMPAT_MANGLED = {
     "paged_kv_free": "paged_kv_free",
     "paged_kv_allocate_block": "paged_kv_allocate_block",
     "paged_kv_free_block": "paged_kv_free_block",
+    "quantlib_fp16_to_fp8_e4m3": "quantlib_fp16_to_fp8_e4m3",
+    "quantlib_fp16_to_fp8_e5m2": "quantlib_fp16_to_fp8_e5m2",
+    "quantlib_fp8_to_fp16": "quantlib_fp8_to_fp16",
+    "quantlib_fp8_gemm": "quantlib_fp8_gemm",
+    "quantlib_free": "quantlib_free",
+    "quantlib_quant_error": "quantlib_quant_error",
+    "quantlib_print_stats": "quantlib_print_stats",
 }
 
 

@@ -8,7 +8,7 @@ import pytest
 import oracle as orc
 import quantlib_amd as ql
 from helpers import (ATOL_ROPE_F32, RTOL_F32, ATOL_F32, check_abs, check_close, check_f16, dev,
-                     empty, host, normal, ptr, stream, to_f16_bits, uniform)
+                     empty, f16_bits_to_f32, host, normal, ptr, stream, to_f16_bits, uniform)
 from test_abi import COMPAT_MANGLED
 
 pytestmark = pytest.mark.gpu
@@ -227,3 +227,70 @@ def test_paged_allocator_lifo_and_pool_layout():
             assert np.array_equal(pool[b, layer, o], kn[t]), t
     finally:
         free(c)
+
+
+# ---- quantlib FP8 (quantlib_src/tests/test_fp8.cu) -------------------------------------------
+class QuantParams(ctypes.Structure):   # quant_types.h:23-29
+    _fields_ = [("scales", _p), ("zeros", _p), ("group_size", _i), ("granularity", _i),
+                ("n_scales", _i)]
+
+
+class QuantMatrix(ctypes.Structure):   # quant_types.h:32-39
+    _fields_ = [("data", _p), ("params", QuantParams), ("rows", _i), ("cols", _i), ("bits", _i),
+                ("format", ctypes.c_char * 16)]
+
+
+def test_reference_fp8_test_via_quantlib_shims():
+    # quantlib_src/tests/test_fp8.cu:24-100: 1024x1024 U(-1,1) weights (rand(), default
+    # seed), E4M3 per-group 128, E5M2 per-channel, E4M3 per-tensor; max abs error < 0.25.
+    to_e4m3 = fn("quantlib_fp16_to_fp8_e4m3", [_p, _i, _i, _i, _i, _p], QuantMatrix)
+    to_e5m2 = fn("quantlib_fp16_to_fp8_e5m2", [_p, _i, _i, _i, _i, _p], QuantMatrix)
+    to_f16 = fn("quantlib_fp8_to_fp16", [ctypes.POINTER(QuantMatrix), _p, _p])
+    qerr = fn("quantlib_quant_error", [_p, _p, _i], ctypes.c_float)
+    qfree = fn("quantlib_free", [ctypes.POINTER(QuantMatrix)])
+    stats = fn("quantlib_print_stats", [ctypes.POINTER(QuantMatrix)])
+    rows = cols = 1024
+    x = to_f16_bits(orc.reftest_fp8_inputs(rows, cols, 1))
+    dx = dev(x)
+    deq = empty((rows * cols,), np.uint16)
+    for conv, fmt, gran, gs in [(to_e4m3, 0, 2, 128), (to_e5m2, 1, 1, 0), (to_e4m3, 0, 0, 0)]:
+        qm = conv(ptr(dx), rows, cols, gran, gs, stream())
+        assert qm.bits == 8 and qm.format == (b"E4M3" if fmt == 0 else b"E5M2")
+        stats(ctypes.byref(qm))
+        to_f16(ctypes.byref(qm), ptr(deq), stream())
+        sync()
+        err = qerr(ptr(dx), ptr(deq), rows * cols)
+        assert err < 0.25, err
+        q_want, sc_want = orc.fp8_quantize(x, fmt, gran, gs, 0)   # the reference's algorithm
+        codes = np.empty(rows * cols, np.uint8)
+        scales = np.empty(qm.params.n_scales, np.float32)
+        d2h(codes.ctypes.data, qm.data, codes.nbytes)
+        d2h(scales.ctypes.data, qm.params.scales, scales.nbytes)
+        assert np.array_equal(scales, sc_want) and np.array_equal(codes.reshape(rows, cols), q_want)
+        assert np.array_equal(host(deq, shape=(rows, cols)),
+                              orc.fp8_dequantize(q_want, sc_want, fmt, gran, gs, 0))
+        assert abs(err - float(np.abs(f16_bits_to_f32(host(deq)) - f16_bits_to_f32(x).ravel()).max())) == 0
+        qfree(ctypes.byref(qm))
+        assert qm.data is None and qm.params.scales is None
+
+
+@pytest.mark.parametrize("M", [16, 128])
+def test_quantlib_fp8_gemm_shim(M):
+    to_e4m3 = fn("quantlib_fp16_to_fp8_e4m3", [_p, _i, _i, _i, _i, _p], QuantMatrix)
+    gemm = fn("quantlib_fp8_gemm", [_p, ctypes.POINTER(QuantMatrix), _p, _i, _i, _i, _p])
+    qfree = fn("quantlib_free", [ctypes.POINTER(QuantMatrix)])
+    N, K = 256, 512
+    w = to_f16_bits(normal(5, (N, K), K ** -0.5))
+    a = to_f16_bits(normal(6, (M, K)))
+    dw, da = dev(w), dev(a)
+    qm = to_e4m3(ptr(dw), N, K, 2, 128, stream())
+    out = empty((M * N,), np.uint16)
+    gemm(ptr(da), ctypes.byref(qm), ptr(out), M, N, K, stream())
+    sync()
+    q, sc = orc.fp8_quantize(w, 0, 2, 128, 0)
+    wd = orc.fp8_dequantize(q, sc, 0, 2, 128, 0)
+    want = orc.matmul(a, wd)
+    bound = 2.0 ** -10 * (np.abs(f16_bits_to_f32(want)) +
+                          np.abs(f16_bits_to_f32(a)).astype(np.float64) @ np.abs(f16_bits_to_f32(wd)).T)
+    assert np.all(np.abs(f16_bits_to_f32(host(out, shape=(M, N))) - f16_bits_to_f32(want)) <= bound)
+    qfree(ctypes.byref(qm))
