@@ -394,10 +394,16 @@ hipError_t ql_fp8_quantize(const uint16_t* src, int rows, int cols, int format, 
 hipError_t ql_fp8_dequantize(const uint8_t* src, const float* scales, int rows, int cols,
                              int format, int granularity, int group_size, int mode,
                              uint16_t* dst, hipStream_t stream);
-/* C[M, N] = A[M, K] (dequant W[N, K])^T, fp32 accumulation, fp16 out.  M <= 64 with
- * N % 16 == 0, K % 64 == 0 and 16 | group length streams W once and dequantizes in
- * registers (multiplying by 1/scale); otherwise W is dequantized into workspace
- * (N*K*2 bytes, 16-byte aligned) and ql_gemm_f16 runs. */
+/* C[M, N] = A[M, K] (dequant W[N, K])^T, fp32 accumulation, fp16 out
+ * (quantlib_src/kernels/fp8_gemm.cu:34-139, quantlib_fp8_gemm).  M <= 64 with
+ * N % 16 == 0, K % 64 == 0, 16 | group length and 16-byte aligned A and W streams W
+ * once and dequantizes in registers (multiplying by 1/scale); there the workspace
+ * is optional and, when it holds ql_fp8_gemm_workspace_size bytes (16-byte aligned,
+ * C 8-byte aligned), splits K over more workgroups with fp32 partials summed in a
+ * fixed order.  Otherwise W is dequantized into workspace (N*K*2 bytes, 16-byte
+ * aligned) and ql_gemm_f16 runs. */
+hipError_t ql_fp8_gemm_workspace_size(int M, int N, int K, int granularity, int group_size,
+                                      size_t* bytes);
 hipError_t ql_fp8_gemm_f16(const uint16_t* A, const uint8_t* W, const float* scales, int M, int N,
                            int K, int format, int granularity, int group_size, int mode,
                            uint16_t* C, void* workspace, size_t workspace_bytes,

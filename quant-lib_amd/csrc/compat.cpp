@@ -368,10 +368,12 @@ extern "C" void quantlib_fp8_gemm(const __half* A, const QuantMatrix* W, __half*
                                   int K, hipStream_t stream) {
     if (!W || W->bits != 8) return;
     void* ws = nullptr;
-    size_t ws_bytes = 0;
-    if (M > 64 && N > 0 && K > 0) {
+    size_t ws_bytes = 0, need = 0;
+    if (ql_fp8_gemm_workspace_size(M, N, K, (int)W->params.granularity, W->params.group_size, &need) !=
+        hipSuccess)
+        return;
+    if (need > 0) {
         std::lock_guard<std::mutex> lock(g_ws_mu);
-        const size_t need = (size_t)N * (size_t)K * sizeof(uint16_t);
         if (g_ws_bytes < need) {
             if (g_ws) {
                 (void)hipStreamSynchronize(stream);

@@ -26,6 +26,9 @@
 
 #include <math.h>
 #include <float.h>
+#include <stdint.h>
+
+#include <algorithm>
 
 namespace {
 
@@ -82,12 +85,13 @@ __device__ __forceinline__ uint32_t enc_ocp2(float a, float b) {
     return lo | (hi << 8);
 }
 
-template <int FMT>
-__device__ __forceinline__ float2v dec_ocp2(uint32_t w) {   // the two low bytes of w
+// the two bytes of w's low (HI = false) or high 16-bit word
+template <int FMT, bool HI = false>
+__device__ __forceinline__ float2v dec_ocp2(uint32_t w) {
     if constexpr (FMT == QL_FP8_E4M3)
-        return __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+        return __builtin_amdgcn_cvt_pk_f32_fp8((int)w, HI);
     else
-        return __builtin_amdgcn_cvt_pk_f32_bf8((int)w, false);
+        return __builtin_amdgcn_cvt_pk_f32_bf8((int)w, HI);
 }
 
 // ---- scales ----------------------------------------------------------------------------
@@ -211,85 +215,306 @@ __global__ __launch_bounds__(kBlock) void dequantize_kernel(const uint8_t* __res
 }
 
 // ---- skinny GEMM: C[M,N] = A[M,K] (dequant W[N,K])^T, M <= 64 --------------------------
-// Workgroup: 16 weight rows (n), all M tokens; wavefront w sums K-range w of 4.
-// Per 64-k chunk a lane holds 16 codes of row n0 + lane%16 at k = 16*(lane/16) ..,
-// used as the A operand of two 16x16x32 steps (k order permuted identically in
-// the B operand: token rows A[m][same k]).
+// Computed as C^T = W' A^T with v_mfma_f32_16x16x32_f16: the weights are the A
+// operand (16 rows x 32 k), the tokens the B operand (32 k x 16 tokens).
+// Workgroup (4 wavefronts): R row tiles of 16 weight rows x all M tokens (MT tiles
+// of 16) over one K-split's range of 64-k chunks; wavefront w takes chunks
+// w, w+4, ... of that range, so the four read adjacent halves of each row's cache
+// lines together.  Per chunk a lane loads 16 codes of row (tile base + lane%16) at
+// k = 16*(lane/16) .. +15 and the same 16 k of token (16t + lane%16) -- the k order
+// inside a chunk is permuted identically for both operands, so the products pair
+// up -- and each token fragment serves all R row tiles.  Chunks stream through a
+// ring of 3-4 register stages.  Token rows past M load row M-1 (in bounds): they
+// only feed C^T columns that are never written.  The wavefronts' partial tiles are
+// summed in LDS; with several K-splits the split's fp32 partial goes to
+// part[split][M][N] and splitk_reduce sums the splits in order (deterministic).
 constexpr int kGemmWaves = 4;
 
-template <int FMT, int MODE>
-__device__ __forceinline__ void dequant16(uint4 codes, float inv, half8& lo, half8& hi) {
-    const uint32_t w[4] = {codes.x, codes.y, codes.z, codes.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        float f[4];
-        if constexpr (MODE == QL_FP8_MODE_REFERENCE) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) f[e] = dec_ref<FMT>((w[j] >> (8 * e)) & 0xFFu);
-        } else {
-            const float2v a = dec_ocp2<FMT>(w[j]);
-            const float2v b = dec_ocp2<FMT>(w[j] >> 16);
-            f[0] = a[0];
-            f[1] = a[1];
-            f[2] = b[0];
-            f[3] = b[1];
-        }
-        half8& dst = j < 2 ? lo : hi;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) dst[4 * (j & 1) + e] = from_f32<_Float16>(f[e] * inv);
+// scale lookup of the register path: one scale (tensor), one per weight row, per
+// group with K % gs == 0 from the workgroup's LDS table of inverses (GroupLds) or
+// from global memory (Group), and groups that straddle rows (Any)
+enum ScaleKind { kScaleTensor = 0, kScaleRow = 1, kScaleGroupLds = 2, kScaleGroup = 3, kScaleAny = 4 };
+
+// bytes of 4 reference-mode codes whose reference decode differs from the OCP
+// decode: E4M3 exponent 0 with a non-zero mantissa (the reference reads it as a
+// normal number) and |code| 0x7F (the reference's 480, OCP's NaN); E5M2 exponent 0
+// with a non-zero mantissa and exponent 31 (finite in the reference).  Bytewise
+// sums of 7-bit values never carry into the next byte.
+template <int FMT>
+__device__ __forceinline__ uint32_t ref_special(uint32_t w) {
+    const uint32_t low7 = w & 0x7F7F7F7Fu;
+    const uint32_t nz = (low7 + 0x7F7F7F7Fu) & 0x80808080u;
+    if constexpr (FMT == QL_FP8_E4M3) {
+        const uint32_t ge8 = (low7 + 0x78787878u) & 0x80808080u;
+        const uint32_t is7f = (low7 + 0x01010101u) & 0x80808080u;
+        return (nz & ~ge8) | is7f;
+    } else {
+        const uint32_t ge4 = (low7 + 0x7C7C7C7Cu) & 0x80808080u;
+        const uint32_t ge7c = (low7 + 0x04040404u) & 0x80808080u;
+        return (nz & ~ge4) | ge7c;
     }
 }
 
-template <int FMT, int MODE, int MT>
-__global__ __launch_bounds__(kGemmWaves * kWave) void fp8_gemm_skinny(
-    const _Float16* __restrict__ A, const uint8_t* __restrict__ W, const float* __restrict__ scales,
-    _Float16* __restrict__ C, int M, int N, int K, long long gs) {
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    const int n0 = blockIdx.x * 16;
-    const int row = n0 + (lane & 15);             // weight row this lane loads
-    const int kq = lane >> 4;                     // which 16-k slice of a 64-k chunk
-    const int n_chunks = K / 64;
-    const int per = (n_chunks + kGemmWaves - 1) / kGemmWaves;
-    const int c_begin = wave * per, c_end = min(n_chunks, c_begin + per);
-    floatx4 acc[MT];
+// 16 codes -> two fp16 fragments of binary16(decode(code) * inv).  The hardware
+// decode is exact for every OCP code; in reference mode it is used when none of a
+// lane's 16 codes is one of the codes whose reference value differs (the reference
+// encoder only writes such a code for a NaN input) and the lane falls back to the
+// bitwise reference decode otherwise.  SCALED = false leaves the scale out (the
+// caller applies it to the accumulated products): every FP8 value is exact in
+// binary16, so the fragments then hold the decoded codes themselves.
+template <int FMT, int MODE, bool SCALED>
+__device__ __forceinline__ void dequant16(uint4 codes, float inv, half8& lo, half8& hi) {
+    const uint32_t w[4] = {codes.x, codes.y, codes.z, codes.w};
+    float f[16];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) acc[t] = floatx4{};
-    const uint8_t* wrow = W + (size_t)row * K;
-    const long long wbase = (long long)row * K;
-    for (int c = c_begin; c < c_end; ++c) {
-        const int k = c * 64 + 16 * kq;
-        const uint4 codes = *reinterpret_cast<const uint4*>(wrow + k);
-        const float inv = 1.0f / scales[(wbase + k) / gs];
-        half8 wlo, whi;
-        dequant16<FMT, MODE>(codes, inv, wlo, whi);
+    for (int j = 0; j < 4; ++j) {
+        const float2v a = dec_ocp2<FMT>(w[j]);
+        const float2v b = dec_ocp2<FMT, true>(w[j]);
+        f[4 * j] = a[0];
+        f[4 * j + 1] = a[1];
+        f[4 * j + 2] = b[0];
+        f[4 * j + 3] = b[1];
+    }
+    if constexpr (MODE == QL_FP8_MODE_REFERENCE) {
+        const uint32_t special = ref_special<FMT>(w[0]) | ref_special<FMT>(w[1]) | ref_special<FMT>(w[2]) |
+                                 ref_special<FMT>(w[3]);
+        if (special) {
 #pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            const int m = 16 * t + (lane & 15);
-            const _Float16* arow = A + (size_t)(m < M ? m : 0) * K + k;
-            half8 alo = *reinterpret_cast<const half8*>(arow);
-            half8 ahi = *reinterpret_cast<const half8*>(arow + 8);
-            if (m >= M) {
-                alo = half8{};
-                ahi = half8{};
-            }
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wlo, alo, acc[t], 0, 0, 0);
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(whi, ahi, acc[t], 0, 0, 0);
+            for (int e = 0; e < 16; ++e) f[e] = dec_ref<FMT>((w[e >> 2] >> (8 * (e & 3))) & 0xFFu);
         }
     }
-    // sum the wavefronts' partial C^T tiles: lane holds C^T[n0 + 4*(lane/16) + i][16t + lane%16]
-    __shared__ float part[kGemmWaves][MT * 16][17];
 #pragma unroll
-    for (int t = 0; t < MT; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) part[wave][16 * t + (lane & 15)][4 * (lane >> 4) + i] = acc[t][i];
-    __syncthreads();
-    for (int e = threadIdx.x; e < MT * 16 * 16; e += kGemmWaves * kWave) {
-        const int m = e / 16, nn = e % 16;
-        float s = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kGemmWaves; ++w) s += part[w][m][nn];
-        if (m < M && n0 + nn < N) C[(size_t)m * N + n0 + nn] = from_f32<_Float16>(s);
+    for (int e = 0; e < 8; ++e) {
+        lo[e] = (_Float16)(SCALED ? f[e] * inv : f[e]);
+        hi[e] = (_Float16)(SCALED ? f[8 + e] * inv : f[8 + e]);
     }
+}
+
+struct SkinnyArgs {
+    const char* A;        // byte views: every offset below 2^32 (checked on the host)
+    const char* W;
+    const float* scales;
+    _Float16* C;
+    float* part;          // [splits][M][N] fp32 partials (splits > 1)
+    int M, N, K;
+    int chunks_per_split;
+    long long gs;         // group length in elements
+    int groups_per_row;   // K / gs (kScaleGroup)
+    int g_step, r_step;   // 256 / gs, 256 % gs: a wavefront's next chunk starts 256 k on
+};
+
+template <int MT, int R>
+struct SkStage {
+    uint4 w[R];
+    half8 a[MT][2];
+    float s[R];
+};
+
+// Per-tensor and per-row scales are applied once to the accumulated products
+// instead of to every weight, except for reference-mode E5M2, whose exponent-31
+// codes decode beyond the binary16 range before scaling.
+template <int FMT, int MODE, int SK>
+constexpr bool fold_scale() {
+    return SK <= kScaleRow && !(MODE == QL_FP8_MODE_REFERENCE && FMT == QL_FP8_E5M2);
+}
+
+template <int SK>
+__device__ __forceinline__ float scale_at(const SkinnyArgs& p, int row, int k) {
+    if constexpr (SK == kScaleTensor) return p.scales[0];
+    else if constexpr (SK == kScaleRow) return p.scales[row];
+    else if constexpr (SK == kScaleAny) return p.scales[((long long)row * p.K + k) / p.gs];
+    else return p.scales[row * p.groups_per_row + (int)((unsigned)k / (unsigned)p.gs)];
+}
+
+// kScaleGroup(Lds): the group of a lane's next chunk, advanced by 256 k per load
+// (the loads of a wavefront run through its chunks in order, 4 apart) and clamped
+// to the group of its last chunk (the loads past the end repeat that chunk).
+struct GroupCursor {
+    int g, rem, g_last;
+    const float* lds;     // kScaleGroupLds: [NR][ng] inverse scales of groups g0 .. g0+ng-1
+    int ng, g0;
+};
+
+template <int MT, int R, int SK>
+__device__ __forceinline__ void sk_load(SkStage<MT, R>& st, const SkinnyArgs& p, const uint32_t (&woff)[R],
+                                        const int (&row)[R], const uint32_t (&aoff)[MT], int c, int kq,
+                                        GroupCursor& gc) {
+    const uint32_t k = (uint32_t)c * 64u;
+#pragma unroll
+    for (int r = 0; r < R; ++r) st.w[r] = *reinterpret_cast<const uint4*>(p.W + (woff[r] + k));
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        st.a[t][0] = *reinterpret_cast<const half8*>(p.A + (aoff[t] + 2u * k));
+        st.a[t][1] = *reinterpret_cast<const half8*>(p.A + (aoff[t] + 2u * k + 16u));
+    }
+    if constexpr (SK == kScaleGroupLds || SK == kScaleGroup) {
+        const int g = min(gc.g, gc.g_last);
+        const int lane16 = threadIdx.x & 15;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if constexpr (SK == kScaleGroupLds) st.s[r] = gc.lds[(16 * r + lane16) * gc.ng + g - gc.g0];
+            else st.s[r] = p.scales[row[r] * p.groups_per_row + g];
+        }
+        gc.g += p.g_step;
+        gc.rem += p.r_step;
+        if (gc.rem >= (int)p.gs) {
+            gc.rem -= (int)p.gs;
+            ++gc.g;
+        }
+    } else if constexpr (SK == kScaleAny) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) st.s[r] = scale_at<SK>(p, row[r], (int)k + 16 * kq);
+    }
+}
+
+template <int FMT, int MODE, int MT, int R, int SK>
+__device__ __forceinline__ void sk_compute(const SkStage<MT, R>& st, const float (&inv_fixed)[R],
+                                           floatx4 (&acc)[R][MT]) {
+    constexpr bool kFold = fold_scale<FMT, MODE, SK>();
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        // v_rcp_f32 (1 ulp): the weight is rounded to binary16 right after
+        const float inv = SK <= kScaleRow ? inv_fixed[r]
+                                          : (SK == kScaleGroupLds ? st.s[r] : __builtin_amdgcn_rcpf(st.s[r]));
+        half8 wlo, whi;
+        dequant16<FMT, MODE, !kFold>(st.w[r], inv, wlo, whi);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            acc[r][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wlo, st.a[t][0], acc[r][t], 0, 0, 0);
+            acc[r][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(whi, st.a[t][1], acc[r][t], 0, 0, 0);
+        }
+    }
+}
+
+// floats of the skinny kernel's LDS: the four wavefronts' partial tiles, and at
+// least 16 KB for the inverse-scale table
+__host__ __device__ constexpr int skinny_smem_floats(int nr, int mc, int sk) {
+    return sk == kScaleGroupLds && kGemmWaves * nr * (mc + 1) < 4096 ? 4096 : kGemmWaves * nr * (mc + 1);
+}
+
+template <int FMT, int MODE, int MT, int R, int SK>
+__global__ __launch_bounds__(kGemmWaves * kWave) void fp8_gemm_skinny(SkinnyArgs p) {
+    constexpr int NR = 16 * R, MC = 16 * MT;
+    constexpr bool kFold = fold_scale<FMT, MODE, SK>();
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int n0 = blockIdx.x * NR;
+    const int kq = lane >> 4;
+    const int n_chunks = p.K / 64;
+    const int c_begin = blockIdx.y * p.chunks_per_split;
+    const int c_end = min(n_chunks, c_begin + p.chunks_per_split);
+    uint32_t woff[R];
+    int row[R];
+    float inv_fixed[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        row[r] = n0 + 16 * r + (lane & 15);
+        woff[r] = (uint32_t)row[r] * (uint32_t)p.K + 16u * kq;
+        inv_fixed[r] = 1.0f;
+        if constexpr (SK <= kScaleRow && !kFold) inv_fixed[r] = 1.0f / scale_at<SK>(p, row[r], 0);
+    }
+    uint32_t aoff[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) aoff[t] = 2u * ((uint32_t)min(16 * t + (lane & 15), p.M - 1) * (uint32_t)p.K + 16u * kq);
+    floatx4 acc[R][MT];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) acc[r][t] = floatx4{};
+
+    // LDS: the inverse-scale table during the loop (kScaleGroupLds; the host checks
+    // that NR * ng fits), then the partial tiles
+    constexpr int kSmemFloats = skinny_smem_floats(NR, MC, SK);
+    __shared__ float smem[kSmemFloats];
+    GroupCursor gc{0, 0, 0, nullptr, 0, 0};
+    if constexpr (SK == kScaleGroupLds) {
+        const int gs = (int)p.gs;
+        gc.g0 = c_begin * 64 / gs;
+        gc.ng = (c_end * 64 - 1) / gs + 1 - gc.g0;
+        for (int i = threadIdx.x; i < NR * gc.ng; i += kGemmWaves * kWave) {
+            const int rr = i / gc.ng, gg = i - rr * gc.ng;
+            smem[i] = 1.0f / p.scales[(n0 + rr) * p.groups_per_row + gc.g0 + gg];
+        }
+        gc.lds = smem;
+        __syncthreads();
+    }
+
+    // ring of NS register stages: stage s holds chunk first + 4*(s + NS*j); while one
+    // is dequantized and multiplied the loads of the other NS - 1 are in flight.
+    // Loads past the wavefront's last chunk repeat that chunk (in bounds, never
+    // used), so every round issues the same loads and the waits count them exactly.
+    constexpr int NS = MT == 4 ? 3 : 4;
+    const int first = c_begin + wave;              // wave-uniform
+    if (first < c_end) {
+        const int last = first + kGemmWaves * ((c_end - 1 - first) / kGemmWaves);
+        if constexpr (SK == kScaleGroupLds || SK == kScaleGroup) {
+            const int k0 = first * 64 + 16 * kq;
+            gc.g = k0 / (int)p.gs;
+            gc.rem = k0 - gc.g * (int)p.gs;
+            gc.g_last = (last * 64 + 16 * kq) / (int)p.gs;
+        }
+        SkStage<MT, R> st[NS];
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+            sk_load<MT, R, SK>(st[s], p, woff, row, aoff, min(first + kGemmWaves * s, last), kq, gc);
+        for (int c0 = first; c0 <= last; c0 += kGemmWaves * NS) {
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                const int cs = c0 + kGemmWaves * s;
+                if (cs <= last) sk_compute<FMT, MODE, MT, R, SK>(st[s], inv_fixed, acc);
+                sk_load<MT, R, SK>(st[s], p, woff, row, aoff, min(cs + kGemmWaves * NS, last), kq, gc);
+            }
+        }
+    }
+    if constexpr (SK == kScaleGroupLds) __syncthreads();   // the table's space is reused below
+    // lane holds C^T[16r + 4*(lane/16) + i][16t + lane%16]; sum the four wavefronts
+    // (the folded scale is per weight row, i.e. per i)
+    float (*part)[NR][MC + 1] = reinterpret_cast<float (*)[NR][MC + 1]>(smem);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float rs[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+        if constexpr (kFold) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) rs[i] = 1.0f / scale_at<SK>(p, n0 + 16 * r + 4 * kq + i, 0);
+        }
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                part[wave][16 * r + 4 * kq + i][16 * t + (lane & 15)] = kFold ? acc[r][t][i] * rs[i] : acc[r][t][i];
+    }
+    __syncthreads();
+    const int m_end = min(p.M, MC);
+    for (int e = threadIdx.x; e < NR * m_end; e += kGemmWaves * kWave) {
+        const int m = e / NR, nn = e % NR;
+        float s = part[0][nn][m];
+#pragma unroll
+        for (int w = 1; w < kGemmWaves; ++w) s += part[w][nn][m];
+        const size_t o = (size_t)m * p.N + n0 + nn;
+        if (gridDim.y == 1) p.C[o] = from_f32<_Float16>(s);
+        else p.part[(size_t)blockIdx.y * p.M * p.N + o] = s;
+    }
+}
+
+// C = binary16(sum over splits of part[s]), 4 outputs per thread (M*N % 4 == 0)
+__global__ __launch_bounds__(kBlock) void splitk_reduce(const float* __restrict__ part,
+                                                        _Float16* __restrict__ C, int splits,
+                                                        long long mn) {
+    const long long i = ((long long)blockIdx.x * kBlock + threadIdx.x) * 4;
+    if (i >= mn) return;
+    float4 s = *reinterpret_cast<const float4*>(part + i);
+    for (int k = 1; k < splits; ++k) {
+        const float4 v = *reinterpret_cast<const float4*>(part + (size_t)k * mn + i);
+        s.x += v.x;
+        s.y += v.y;
+        s.z += v.z;
+        s.w += v.w;
+    }
+    Vec<_Float16, 4> o;
+    o.v[0] = from_f32<_Float16>(s.x);
+    o.v[1] = from_f32<_Float16>(s.y);
+    o.v[2] = from_f32<_Float16>(s.z);
+    o.v[3] = from_f32<_Float16>(s.w);
+    store<true>(reinterpret_cast<Vec<_Float16, 4>*>(C + i), o);
 }
 
 // ---- host helpers ----------------------------------------------------------------------
@@ -328,19 +553,80 @@ void launch_dequantize(const uint8_t* q, const Geom& g, const float* s, _Float16
                            dim3(kBlock), 0, st, q, g, s, y);
 }
 
+// Skinny GEMM launch shape: MT token tiles, R = 4 row tiles per workgroup (64
+// weight rows: each wavefront streams 64 contiguous rows' 64-byte chunks, and the
+// token fragments serve four row tiles) when N allows, and K-splits only while
+// there are fewer row blocks than CUs: floor(256 / row blocks), at least two chunks
+// per wavefront, and splits*M*N*4 bytes of workspace for the fp32 partials.
+// (Measured on MI355X with weights streamed from HBM: one split at 224 row blocks,
+// two at 96, four at 64.)
+constexpr int kSkinnyTargetWgs = 256;
+
+struct SkinnyPlan {
+    int mt, r, splits, chunks_per_split;
+};
+
+SkinnyPlan skinny_plan(int M, int N, int K, size_t ws_bytes) {
+    SkinnyPlan s;
+    s.mt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+    s.r = 4;
+    while (s.r > 1 && (N / 16) % s.r) s.r /= 2;
+    const int row_blocks = N / (16 * s.r);
+    const int n_chunks = K / 64;
+    int splits = row_blocks >= kSkinnyTargetWgs ? 1 : kSkinnyTargetWgs / row_blocks;
+    splits = std::min(splits, std::max(1, n_chunks / (2 * kGemmWaves)));
+    while (splits > 1 && (size_t)splits * (size_t)M * (size_t)N * sizeof(float) > ws_bytes) --splits;
+    s.chunks_per_split = (n_chunks + splits - 1) / splits;
+    s.splits = (n_chunks + s.chunks_per_split - 1) / s.chunks_per_split;
+    return s;
+}
+
+int scale_kind(const Geom& g, int K, const SkinnyPlan& pl) {
+    if (g.n_groups == 1) return kScaleTensor;
+    if (g.gs == K) return kScaleRow;
+    if (K % g.gs) return kScaleAny;
+    // the largest group range of a K-split must fit the LDS table
+    const int n_chunks = K / 64;
+    int ng_max = 0;
+    for (int s = 0; s < pl.splits; ++s) {
+        const int cb = s * pl.chunks_per_split, ce = std::min(n_chunks, cb + pl.chunks_per_split);
+        ng_max = std::max(ng_max, (int)((ce * 64LL - 1) / g.gs + 1 - cb * 64LL / g.gs));
+    }
+    const int nr = 16 * pl.r, mc = 16 * pl.mt;
+    return (long long)nr * ng_max <= skinny_smem_floats(nr, mc, kScaleGroupLds) ? kScaleGroupLds : kScaleGroup;
+}
+
+template <int FMT, int MODE, int MT, int R>
+void launch_skinny_rs(const SkinnyArgs& a, int kind, dim3 grid, hipStream_t st) {
+    const dim3 block(kGemmWaves * kWave);
+    switch (kind) {
+    case kScaleTensor: hipLaunchKernelGGL((fp8_gemm_skinny<FMT, MODE, MT, R, kScaleTensor>), grid, block, 0, st, a); break;
+    case kScaleRow: hipLaunchKernelGGL((fp8_gemm_skinny<FMT, MODE, MT, R, kScaleRow>), grid, block, 0, st, a); break;
+    case kScaleGroupLds: hipLaunchKernelGGL((fp8_gemm_skinny<FMT, MODE, MT, R, kScaleGroupLds>), grid, block, 0, st, a); break;
+    case kScaleGroup: hipLaunchKernelGGL((fp8_gemm_skinny<FMT, MODE, MT, R, kScaleGroup>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((fp8_gemm_skinny<FMT, MODE, MT, R, kScaleAny>), grid, block, 0, st, a); break;
+    }
+}
+
 template <int FMT, int MODE, int MT>
-void launch_skinny(const _Float16* A, const uint8_t* W, const float* s, _Float16* C, int M, int N,
-                   int K, long long gs, hipStream_t st) {
-    hipLaunchKernelGGL((fp8_gemm_skinny<FMT, MODE, MT>), dim3((unsigned)(N / 16)),
-                       dim3(kGemmWaves * kWave), 0, st, A, W, s, C, M, N, K, gs);
+void launch_skinny_mt(const SkinnyArgs& a, const SkinnyPlan& pl, int kind, dim3 grid, hipStream_t st) {
+    if (pl.r == 4) launch_skinny_rs<FMT, MODE, MT, 4>(a, kind, grid, st);
+    else if (pl.r == 2) launch_skinny_rs<FMT, MODE, MT, 2>(a, kind, grid, st);
+    else launch_skinny_rs<FMT, MODE, MT, 1>(a, kind, grid, st);
 }
 
 template <int FMT, int MODE>
-void launch_skinny_mt(const _Float16* A, const uint8_t* W, const float* s, _Float16* C, int M, int N,
-                      int K, long long gs, hipStream_t st) {
-    if (M <= 16) launch_skinny<FMT, MODE, 1>(A, W, s, C, M, N, K, gs, st);
-    else if (M <= 32) launch_skinny<FMT, MODE, 2>(A, W, s, C, M, N, K, gs, st);
-    else launch_skinny<FMT, MODE, 4>(A, W, s, C, M, N, K, gs, st);
+void launch_skinny(const SkinnyArgs& a, const SkinnyPlan& pl, int kind, hipStream_t st) {
+    const dim3 grid((unsigned)(a.N / (16 * pl.r)), (unsigned)pl.splits);
+    if (pl.mt == 1) launch_skinny_mt<FMT, MODE, 1>(a, pl, kind, grid, st);
+    else if (pl.mt == 2) launch_skinny_mt<FMT, MODE, 2>(a, pl, kind, grid, st);
+    else launch_skinny_mt<FMT, MODE, 4>(a, pl, kind, grid, st);
+}
+
+// the register path addresses W and A with 32-bit byte offsets
+bool skinny_ok(int M, int N, int K, const Geom& g) {
+    return M <= 64 && N % 16 == 0 && K % 64 == 0 && g.gs % 16 == 0 && (uint64_t)N * (uint64_t)K < (1ull << 32) &&
+           (uint64_t)M * (uint64_t)K * 2u < (1ull << 32);
 }
 
 #define QL_FP8_DISPATCH(fmt, mode, FN, ...)                                                   \
@@ -424,6 +710,21 @@ extern "C" hipError_t ql_fp8_dequantize(const uint8_t* src, const float* scales,
     return hipGetLastError();
 }
 
+extern "C" hipError_t ql_fp8_gemm_workspace_size(int M, int N, int K, int granularity, int group_size,
+                                                 size_t* bytes) {
+    Geom g;
+    QL_CHECK_ARG(bytes && M >= 0 && N >= 0 && K >= 0 && geom_for(N, K, granularity, group_size, g));
+    *bytes = 0;
+    if (M == 0 || N == 0 || K == 0) return hipSuccess;
+    if (skinny_ok(M, N, K, g)) {
+        const SkinnyPlan pl = skinny_plan(M, N, K, SIZE_MAX);
+        *bytes = pl.splits > 1 ? (size_t)pl.splits * (size_t)M * (size_t)N * sizeof(float) : 0;
+    } else {
+        *bytes = (size_t)N * (size_t)K * sizeof(uint16_t);
+    }
+    return hipSuccess;
+}
+
 extern "C" hipError_t ql_fp8_gemm_f16(const uint16_t* A, const uint8_t* W, const float* scales,
                                       int M, int N, int K, int format, int granularity,
                                       int group_size, int mode, uint16_t* C, void* workspace,
@@ -433,11 +734,29 @@ extern "C" hipError_t ql_fp8_gemm_f16(const uint16_t* A, const uint8_t* W, const
     QL_CHECK_ARG(geom_for(N, K, granularity, group_size, g));
     if (M == 0 || N == 0) return hipSuccess;
     QL_CHECK_ARG(A && W && scales && C && K > 0);
-    const bool skinny = M <= 64 && N % 16 == 0 && K % 64 == 0 && g.gs % 16 == 0 &&
-                        qlh::aligned16(A) && qlh::aligned16(W) && N / 16 <= 0x7fffffff;
-    if (skinny) {
-        QL_FP8_DISPATCH(format, mode, launch_skinny_mt, reinterpret_cast<const _Float16*>(A), W, scales,
-                        reinterpret_cast<_Float16*>(C), M, N, K, g.gs, stream);
+    if (skinny_ok(M, N, K, g) && qlh::aligned16(A) && qlh::aligned16(W)) {
+        const bool ws_ok = workspace && qlh::aligned16(workspace) && ((uintptr_t)C & 7) == 0;
+        const SkinnyPlan pl = skinny_plan(M, N, K, ws_ok ? workspace_bytes : 0);
+        SkinnyArgs a;
+        a.A = reinterpret_cast<const char*>(A);
+        a.W = reinterpret_cast<const char*>(W);
+        a.scales = scales;
+        a.C = reinterpret_cast<_Float16*>(C);
+        a.part = static_cast<float*>(workspace);
+        a.M = M;
+        a.N = N;
+        a.K = K;
+        a.chunks_per_split = pl.chunks_per_split;
+        a.gs = g.gs;
+        a.groups_per_row = K % g.gs == 0 ? (int)(K / g.gs) : 0;
+        a.g_step = (int)(256 / g.gs);
+        a.r_step = (int)(256 % g.gs);
+        QL_FP8_DISPATCH(format, mode, launch_skinny, a, pl, scale_kind(g, K, pl), stream);
+        if (pl.splits > 1) {
+            const long long mn = (long long)M * N;
+            hipLaunchKernelGGL(splitk_reduce, dim3(qlh::blocks_for(mn / 4, kBlock)), dim3(kBlock), 0, stream,
+                               a.part, a.C, pl.splits, mn);
+        }
         return hipGetLastError();
     }
     // dequantize into the workspace, then the fp16 library GEMM

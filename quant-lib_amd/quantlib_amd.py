@@ -76,6 +76,7 @@ SIGNATURES = {
     "ql_fp8_scales": [_p, _i, _i, _i, _i, _i, _i, _p, _p],
     "ql_fp8_quantize": [_p, _i, _i, _i, _i, _i, _i, _p, _p, _p],
     "ql_fp8_dequantize": [_p, _p, _i, _i, _i, _i, _i, _i, _p, _p],
+    "ql_fp8_gemm_workspace_size": [_i, _i, _i, _i, _i, _p],
     "ql_fp8_gemm_f16": [_p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p, _p, ctypes.c_size_t, _p],
     "ql_engine_create": [_p, _i, _i, _i, _p],
     "ql_engine_destroy": [_p],

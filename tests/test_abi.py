@@ -177,6 +177,25 @@ def test_decode_workspace_size_host_query():
     assert size.value == 0
 
 
+def test_fp8_gemm_workspace_size_host_query():
+    size = ctypes.c_size_t(123)
+    q = lambda *a: ql.raw("ql_fp8_gemm_workspace_size", *a, ctypes.addressof(size))
+    # 4096 x 14336 weights: 64 row blocks of 64 rows, four K-splits of fp32 partials
+    assert q(64, 4096, 14336, 1, 0) == 0 and size.value == 4 * 64 * 4096 * 4
+    assert q(1, 4096, 14336, 2, 128) == 0 and size.value == 4 * 1 * 4096 * 4
+    assert q(16, 6144, 4096, 0, 0) == 0 and size.value == 2 * 16 * 6144 * 4      # 96 blocks: two
+    # enough row blocks (224 of 64 rows): no split, no workspace
+    assert q(1, 14336, 4096, 2, 128) == 0 and size.value == 0
+    assert q(64, 14336, 4096, 0, 0) == 0 and size.value == 0
+    # K too short to split (two chunks per wavefront)
+    assert q(16, 1024, 512, 2, 128) == 0 and size.value == 0
+    # more than 64 rows, or a shape the register path does not take: dequantized copy
+    assert q(65, 512, 512, 2, 128) == 0 and size.value == 512 * 512 * 2
+    assert q(16, 100, 256, 1, 0) == 0 and size.value == 100 * 256 * 2
+    assert q(0, 512, 512, 2, 128) == 0 and size.value == 0
+    assert q(1, 512, 512, 2, 0) == INVALID
+
+
 def test_paged_slot_mapping_host_helper():
     table = (ctypes.c_int32 * 3)(4, 0, 7)
     slots = (ctypes.c_int32 * 40)()

@@ -5,8 +5,11 @@ including exhaustive encode and decode tables), of the FP8-weight GEMM
 
 GEMM tolerance, |got - want| <= 2^-10*|want| + 2^-10 * sum_k |a_k w_k|: the
 oracle accumulates in double from the codec's dequantized weights; the kernels
-accumulate in fp32, and the skinny path dequantizes with a multiply by 1/scale,
-which can move a weight by one binary16 step (2^-11 relative)."""
+accumulate in fp32.  The register path either multiplies each decoded weight by
+1/scale before rounding it to binary16, which can move a weight by one binary16
+step (2^-11 relative), or, for per-tensor and per-row scales, multiplies the fp32
+sums of the exactly decoded codes by 1/scale, which skips the weight rounding
+altogether (at most 2^-11 relative from the oracle's rounded weights)."""
 import ctypes
 
 import numpy as np
@@ -101,25 +104,81 @@ def check_gemm(got, want, bound, what):
     assert not bad.any(), f"{what}: {int(bad.sum())} elements out of bound, worst {float((err - bound).max()):.3e}"
 
 
-@pytest.mark.parametrize("mode", MODES)
-@pytest.mark.parametrize("fmt", FMTS)
-@pytest.mark.parametrize("M,N,K,gran,gs", [
+def gpu_fp8_gemm(a, q, sc, M, N, K, fmt, gran, gs, mode, workspace):
+    """workspace: "query" (ql_fp8_gemm_workspace_size bytes), "none", or a byte count."""
+    if workspace == "query":
+        size = ctypes.c_size_t()
+        ql.call("ql_fp8_gemm_workspace_size", M, N, K, gran, gs, ctypes.byref(size))
+        nbytes = size.value
+    else:
+        nbytes = 0 if workspace == "none" else workspace
+    da, dq, ds = dev(a), dev(q), dev(sc)
+    out = empty((M * N,), np.uint16)
+    ws = empty((max(nbytes, 16),), np.uint8)
+    ql.call("ql_fp8_gemm_f16", da.ptr, dq.ptr, ds.ptr, M, N, K, fmt, gran, gs, mode, out.ptr,
+            ws.ptr if nbytes else None, nbytes, stream())
+    return host(out, shape=(M, N))
+
+
+GEMM_CASES = [
     (1, 4096, 4096, ql.QUANT_PER_GROUP, 128), (7, 256, 14336, ql.QUANT_PER_CHANNEL, 0),
     (33, 1024, 1024, ql.QUANT_PER_TENSOR, 0), (64, 512, 512, ql.QUANT_PER_GROUP, 64),
     (65, 512, 512, ql.QUANT_PER_GROUP, 128), (200, 96, 320, ql.QUANT_PER_GROUP, 100),
-    (16, 100, 256, ql.QUANT_PER_CHANNEL, 0)])
+    (16, 100, 256, ql.QUANT_PER_CHANNEL, 0),
+    (64, 1024, 4096, ql.QUANT_PER_GROUP, 48),      # groups straddle rows: general scale index
+    (24, 208, 1024, ql.QUANT_PER_GROUP, 16),       # 13 row tiles: one tile per workgroup
+    (48, 480, 2048, ql.QUANT_PER_GROUP, 32),       # 30 row tiles: two per workgroup
+    (16, 512, 3072, ql.QUANT_PER_GROUP, 48),       # K-splits start inside a group
+    (8, 256, 4096, ql.QUANT_PER_GROUP, 16),        # unsplit: too many groups for the LDS table
+    (64, 1024, 8192, ql.QUANT_PER_GROUP, 16),
+    (20, 512, 1024, ql.QUANT_PER_CHANNEL, 0),      # two token tiles, four row tiles
+    (3, 480, 512, ql.QUANT_PER_GROUP, 64),         # one token tile, two row tiles
+    (5, 208, 256, ql.QUANT_PER_TENSOR, 0)]         # one token tile, one row tile
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("M,N,K,gran,gs", GEMM_CASES)
 def test_fp8_gemm_matches_oracle(mode, fmt, M, N, K, gran, gs):
     a = to_f16_bits(normal(M + N + K, (M, K)))
     w = to_f16_bits(normal(M * N + K, (N, K), K ** -0.5))
     q, sc = orc.fp8_quantize(w, fmt, gran, gs, mode)
     w_deq = orc.fp8_dequantize(q, sc, fmt, gran, gs, mode)
     want = orc.matmul(a, w_deq)
-    da, dq, ds = dev(a), dev(q), dev(sc)
-    out = empty((M * N,), np.uint16)
-    ws = empty((N * K,), np.uint16)
-    ql.call("ql_fp8_gemm_f16", da.ptr, dq.ptr, ds.ptr, M, N, K, fmt, gran, gs, mode, out.ptr, ws.ptr,
-            N * K * 2, stream())
-    check_gemm(host(out, shape=(M, N)), want, gemm_bound(a, w_deq, want), f"fp8 gemm {M}x{N}x{K}")
+    bound = gemm_bound(a, w_deq, want)
+    # with the queried workspace (K split over workgroups when the register path
+    # runs), then without one where the register path runs
+    size = ctypes.c_size_t()
+    ql.call("ql_fp8_gemm_workspace_size", M, N, K, gran, gs, ctypes.byref(size))
+    register_path = size.value != N * K * 2
+    assert register_path == (M <= 64 and N % 16 == 0 and K % 64 == 0)
+    for workspace in ("query",) + (("none",) if register_path else ()):
+        got = gpu_fp8_gemm(a, q, sc, M, N, K, fmt, gran, gs, mode, workspace)
+        check_gemm(got, want, bound, f"fp8 gemm {M}x{N}x{K} workspace {workspace}")
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("M,gran", [(1, ql.QUANT_PER_GROUP), (64, ql.QUANT_PER_GROUP), (5, ql.QUANT_PER_CHANNEL)])
+def test_fp8_gemm_every_code(mode, fmt, M, gran):
+    # raw codes, not encoder output: every byte appears in every 16-code run of some
+    # rows, including the codes whose reference decode is not the OCP one (exponent 0
+    # with a mantissa, 0x7F, E5M2 exponent 31); OCP mode leaves out its NaN / inf codes
+    N, K = 256, 512
+    rng = np.random.default_rng(7 + M + 2 * fmt + 4 * mode)
+    codes = np.arange(256, dtype=np.uint8)
+    if mode == ql.FP8_MODE_OCP:
+        bad = (codes & 0x7F) == 0x7F if fmt == ql.FP8_E4M3 else (codes & 0x7C) == 0x7C
+        codes = codes[~bad]
+    q = rng.choice(codes, size=(N, K)).astype(np.uint8)
+    q[:128, :] = np.resize(codes, (128, K))               # every code in order
+    gs = 128 if gran == ql.QUANT_PER_GROUP else 0
+    sc = rng.uniform(2.0, 8.0, N * K // 128 if gs else N).astype(np.float32)
+    a = to_f16_bits(normal(M + 11, (M, K)))
+    w_deq = orc.fp8_dequantize(q, sc, fmt, gran, gs, mode)
+    want = orc.matmul(a, w_deq)
+    got = gpu_fp8_gemm(a, q, sc, M, N, K, fmt, gran, gs, mode, "query")
+    check_gemm(got, want, gemm_bound(a, w_deq, want), f"fp8 gemm codes fmt {fmt} mode {mode} M {M} gran {gran}")
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (64, 6144, 4096), (300, 512, 1000), (8192, 256, 512)])
