@@ -461,6 +461,36 @@ hipError_t ql_engine_destroy(ql_engine* e);
 hipError_t ql_engine_layer_f16(ql_engine* e, const ql_layer_weights* w, int layer, uint16_t* x,
                                const uint16_t* delta_in, uint16_t* delta_out,
                                const ql_step_device* step, hipStream_t stream);
+/* ---- the same layer on FP8 weights (W8A16) --------------------------------------------
+ * The quantized forward of the reference: quantize_model
+ * (src/quant_forward.cu:57-101) stores every weight matrix as FP8 codes + scales
+ * and the layer GEMMs run through quantlib_fp8_gemm (src/forward.cu:52-70,
+ * 185-238).  Here each layer GEMM is ql_fp8_gemm_f16 (the register path for steps
+ * of <= 64 rows); the norms stay fp16.  The five matrices share one format,
+ * granularity, group size and mode; wqkv is the row-wise stack of the Q, K and V
+ * matrices, whose per-channel or per-group (group_size dividing hidden) codes and
+ * scales are those of the three matrices quantized separately.
+ * ql_engine_create_fp8 is ql_engine_create plus the FP8 GEMM workspace for that
+ * granularity and group size; such an engine runs both layer kinds. */
+typedef struct {
+    const uint8_t* codes;   /* [out_features, in_features] FP8 codes */
+    const float* scales;    /* ql_fp8_num_scales(out_features, in_features, ...) floats */
+} ql_fp8_weight;
+
+typedef struct {
+    const uint16_t* attn_norm;
+    ql_fp8_weight wqkv, wo;
+    const uint16_t* ffn_norm;
+    ql_fp8_weight w_gate, w_up, w_down;
+    int format, granularity, group_size, mode;   /* QL_FP8_*, QL_QUANT_*, QL_FP8_MODE_* */
+} ql_layer_weights_fp8;
+
+hipError_t ql_engine_create_fp8(const ql_layer_dims* dims, int max_rows, int max_seqs,
+                                int max_ctx_len, int granularity, int group_size, ql_engine** out);
+hipError_t ql_engine_layer_fp8(ql_engine* e, const ql_layer_weights_fp8* w, int layer, uint16_t* x,
+                               const uint16_t* delta_in, uint16_t* delta_out,
+                               const ql_step_device* step, hipStream_t stream);
+
 /* x += delta_in over all n_rows rows, final RMSNorm, gather the n_sample rows
  * sample_rows[] (device), logits = rows lm_head^T ([n_sample, vocab] fp16) and, if
  * tokens is not NULL, tokens[i] = argmax of logits row i (device). */

@@ -81,6 +81,8 @@ SIGNATURES = {
     "ql_engine_create": [_p, _i, _i, _i, _p],
     "ql_engine_destroy": [_p],
     "ql_engine_layer_f16": [_p, _p, _i, _p, _p, _p, _p, _p],
+    "ql_engine_create_fp8": [_p, _i, _i, _i, _i, _i, _p],
+    "ql_engine_layer_fp8": [_p, _p, _i, _p, _p, _p, _p, _p],
     "ql_engine_logits_f16": [_p, _p, _p, _p, _p, _i, _p, _i, _i, _p, _p, _p],
     "ql_paged_decode_attention_f16": [_p, _p, _i64, _i64, _i, _p, _i, _p, _i, _p, _p, _i, _i, _i,
                                       _i, _i, _i, _p, ctypes.c_size_t, _p],
@@ -407,6 +409,18 @@ class LayerWeights(ctypes.Structure):
     """ql_layer_weights: device addresses of one layer's fp16 weights."""
     _fields_ = [("attn_norm", _p), ("wqkv", _p), ("wo", _p), ("ffn_norm", _p), ("w_gate", _p),
                 ("w_up", _p), ("w_down", _p)]
+
+
+class FP8Weight(ctypes.Structure):
+    """ql_fp8_weight: device addresses of one matrix's FP8 codes and its scales."""
+    _fields_ = [("codes", _p), ("scales", _p)]
+
+
+class LayerWeightsFP8(ctypes.Structure):
+    """ql_layer_weights_fp8: one layer's fp16 norms and FP8 matrices."""
+    _fields_ = [("attn_norm", _p), ("wqkv", FP8Weight), ("wo", FP8Weight), ("ffn_norm", _p),
+                ("w_gate", FP8Weight), ("w_up", FP8Weight), ("w_down", FP8Weight), ("format", _i),
+                ("granularity", _i), ("group_size", _i), ("mode", _i)]
 
 
 class StepDevice(ctypes.Structure):

@@ -4,6 +4,8 @@ prefill step, then an all-decode step that takes the split-decode path) against
 the oracle composed in the same order -- rmsnorm, x W^T, RoPE at the step's
 positions, causal attention over each sequence's K/V history, residual add,
 SwiGLU -- with a binary16 rounding after every stage, as the engine stores them.
+The FP8-weight layer (ql_engine_layer_fp8) is checked the same way against the
+oracle layer on the oracle codec's dequantized weights.
 
 Layer tolerance, |got - want| <= 2e-2*|want| + 1e-2*max|want|: both sides round
 every stage to binary16 (2^-11 relative) but accumulate GEMMs in different
@@ -106,56 +108,100 @@ def step_device(plan, pool, L, keep):
                          pool.kptrs.ptr, pool.vptrs.ptr, pool.nb, L)
 
 
+def run_engine_steps(eng, layer_call, weights, prompts, n_steps, max_gen=8):
+    """Batcher steps through the engine's layers (layer_call(l, x, delta_in, delta_out, sd))
+    and logits, each stage checked against the oracle layer on `weights` (fp16 bits)."""
+    L, nblk, vocab = len(weights), 32, 512
+    final_norm = to_f16_bits(np.random.default_rng(9).uniform(0.5, 1.5, DM).astype(np.float32))
+    lm_head = to_f16_bits(normal(10, (vocab, DM), DM ** -0.5))
+    d_final, d_lm = dev(final_norm), dev(lm_head)
+    pool = PagedPool(nblk, L, HK, HD)
+    b = ql.Batcher(nblk, 4)
+    for rid, n in prompts.items():
+        b.add(rid, np.arange(n, dtype=np.int32), max_gen)
+    hist = [dict() for _ in range(L)]
+    keep = []
+    for step in range(n_steps):
+        plan = b.plan()
+        T = plan["n_rows"]
+        sd = step_device(plan, pool, L, keep)
+        x = to_f16_bits(normal(500 + step, (T, DM)))
+        dx = dev(x)
+        deltas = [empty((T * DM,), np.uint16) for _ in range(L)]
+        xo, delta = x, None
+        for l in range(L):
+            layer_call(l, dx.ptr, deltas[l - 1].ptr if l else None, deltas[l].ptr, sd)
+            xo, delta = oracle_layer(xo, delta, weights[l], plan, hist[l])
+            check_layer(host(dx, shape=(T, DM)), xo, f"step {step} layer {l} residual")
+            check_layer(host(deltas[l], shape=(T, DM)), delta, f"step {step} layer {l} mlp out")
+            xo = host(dx, shape=(T, DM)).copy()      # continue from the GPU's stream
+            delta = host(deltas[l], shape=(T, DM)).copy()
+        # logits of the sampled rows and greedy tokens
+        n = plan["n_seqs"]
+        rows_d = dev(plan["sample_rows"])
+        logits = empty((n * vocab,), np.uint16)
+        toks = empty((n,), np.int32)
+        ql.call("ql_engine_logits_f16", eng, dx.ptr, deltas[-1].ptr, d_final.ptr, d_lm.ptr, vocab,
+                rows_d.ptr, n, T, logits.ptr, toks.ptr, stream())
+        xf = orc.add(xo, delta, f16=True)
+        yf = orc.rmsnorm(xf, final_norm, EPS, f16=True)
+        want = orc.matmul(yf[plan["sample_rows"]], lm_head)
+        got = host(logits, shape=(n, vocab))
+        check_layer(got, want, f"step {step} logits")
+        assert list(host(toks)) == list(orc.argmax(f16_bits_to_f32(got)))
+        b.commit(host(toks))
+        assert step == 0 or plan["max_q_len"] == 1        # later steps are all decodes
+
+
 def test_engine_layers_steps_and_logits_match_oracle():
-    L, nblk, vocab = 2, 32, 512
+    L = 2
     weights = [layer_weights(100 * (l + 1)) for l in range(L)]
     dw = [{k: dev(v) for k, v in w.items()} for w in weights]
     lw = [ql.LayerWeights(*(d[k].ptr for k in ("attn_norm", "wqkv", "wo", "ffn_norm", "w_gate", "w_up",
                                                "w_down"))) for d in dw]
-    final_norm = to_f16_bits(np.random.default_rng(9).uniform(0.5, 1.5, DM).astype(np.float32))
-    lm_head = to_f16_bits(normal(10, (vocab, DM), DM ** -0.5))
-    d_final, d_lm = dev(final_norm), dev(lm_head)
     dims = ql.LayerDims(DM, H, HK, HD, FF, THETA, EPS, PAIR)
     eng = ctypes.c_void_p()
     ql.call("ql_engine_create", ctypes.byref(dims), 64, 8, 256, ctypes.byref(eng))
-    pool = PagedPool(nblk, L, HK, HD)
-    b = ql.Batcher(nblk, 4)
-    prompts = {0: 20, 1: 33, 2: 5}
-    for rid, n in prompts.items():
-        b.add(rid, np.arange(n, dtype=np.int32), 8)
-    hist = [dict() for _ in range(L)]
-    keep = []
     try:
-        for step in range(3):
-            plan = b.plan()
-            T = plan["n_rows"]
-            sd = step_device(plan, pool, L, keep)
-            x = to_f16_bits(normal(500 + step, (T, DM)))
-            dx = dev(x)
-            deltas = [empty((T * DM,), np.uint16) for _ in range(L)]
-            xo, delta = x, None
-            for l in range(L):
-                ql.call("ql_engine_layer_f16", eng, ctypes.byref(lw[l]), l, dx.ptr,
-                        deltas[l - 1].ptr if l else None, deltas[l].ptr, ctypes.byref(sd), stream())
-                xo, delta = oracle_layer(xo, delta, weights[l], plan, hist[l])
-                check_layer(host(dx, shape=(T, DM)), xo, f"step {step} layer {l} residual")
-                check_layer(host(deltas[l], shape=(T, DM)), delta, f"step {step} layer {l} mlp out")
-                xo = host(dx, shape=(T, DM)).copy()      # continue from the GPU's stream
-                delta = host(deltas[l], shape=(T, DM)).copy()
-            # logits of the sampled rows and greedy tokens
-            n = plan["n_seqs"]
-            rows_d = dev(plan["sample_rows"])
-            logits = empty((n * vocab,), np.uint16)
-            toks = empty((n,), np.int32)
-            ql.call("ql_engine_logits_f16", eng, dx.ptr, deltas[-1].ptr, d_final.ptr, d_lm.ptr, vocab,
-                    rows_d.ptr, n, T, logits.ptr, toks.ptr, stream())
-            xf = orc.add(xo, delta, f16=True)
-            yf = orc.rmsnorm(xf, final_norm, EPS, f16=True)
-            want = orc.matmul(yf[plan["sample_rows"]], lm_head)
-            got = host(logits, shape=(n, vocab))
-            check_layer(got, want, f"step {step} logits")
-            assert list(host(toks)) == list(orc.argmax(f16_bits_to_f32(got)))
-            b.commit(host(toks))
-            assert step == 0 or plan["max_q_len"] == 1        # later steps are all decodes
+        run_engine_steps(eng, lambda l, x, di, do, sd: ql.call(
+            "ql_engine_layer_f16", eng, ctypes.byref(lw[l]), l, x, di, do, ctypes.byref(sd), stream()),
+            weights, {0: 20, 1: 33, 2: 5}, 3)
+    finally:
+        ql.call("ql_engine_destroy", eng)
+
+
+MATS = ("wqkv", "wo", "w_gate", "w_up", "w_down")
+
+
+@pytest.mark.parametrize("fmt,gran,gs,mode,prompts", [
+    # the reference's quantize_model: E4M3, groups of 128, its own codec; a 58-row prefill
+    (ql.FP8_E4M3, ql.QUANT_PER_GROUP, 128, ql.FP8_MODE_REFERENCE, {0: 20, 1: 33, 2: 5}),
+    # per-channel OCP codes; a 100-row prefill takes the dequantize + library GEMM path
+    (ql.FP8_E4M3, ql.QUANT_PER_CHANNEL, 0, ql.FP8_MODE_OCP, {0: 70, 1: 30})])
+def test_engine_fp8_layers_match_oracle(fmt, gran, gs, mode, prompts):
+    L = 2
+    src = [layer_weights(100 * (l + 1)) for l in range(L)]
+    deq, keep, lw = [], [], []
+    for w in src:
+        d = dict(w)
+        fw = {}
+        for k in MATS:
+            q, sc = orc.fp8_quantize(w[k], fmt, gran, gs, mode)
+            d[k] = orc.fp8_dequantize(q, sc, fmt, gran, gs, mode)
+            dq, ds = dev(q), dev(sc)
+            keep += [dq, ds]
+            fw[k] = ql.FP8Weight(dq.ptr, ds.ptr)
+        deq.append(d)
+        dn, fn = dev(w["attn_norm"]), dev(w["ffn_norm"])
+        keep += [dn, fn]
+        lw.append(ql.LayerWeightsFP8(dn.ptr, fw["wqkv"], fw["wo"], fn.ptr, fw["w_gate"], fw["w_up"],
+                                     fw["w_down"], fmt, gran, gs, mode))
+    dims = ql.LayerDims(DM, H, HK, HD, FF, THETA, EPS, PAIR)
+    eng = ctypes.c_void_p()
+    ql.call("ql_engine_create_fp8", ctypes.byref(dims), 128, 8, 256, gran, gs, ctypes.byref(eng))
+    try:
+        run_engine_steps(eng, lambda l, x, di, do, sd: ql.call(
+            "ql_engine_layer_fp8", eng, ctypes.byref(lw[l]), l, x, di, do, ctypes.byref(sd), stream()),
+            deq, prompts, 3)
     finally:
         ql.call("ql_engine_destroy", eng)
