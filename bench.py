@@ -31,7 +31,10 @@ adds the attention that consumes the path's output: causal prefill over the
 TFLOP/s against the dense fp16 matrix peak, and paged decode (64 sequences x
 4096 tokens; 1 sequence x 8192 tokens with the key-split workspace), HBM-bound
 on the K/V rows, and one whole decoder layer through the engine (hipBLASLt
-GEMMs + the fused kernels + attention) for that prefill and that decode step.
+GEMMs + the fused kernels + attention) for that prefill and those decode steps,
+on fp16 weights and on FP8 weights (the reference's quantized forward), plus
+the FP8-weight GEMM at decode row counts against the fp16 GEMM and the FP8
+codec.
 
 Device memory, the stream and events come from libamdhip64 through the
 library's own binding (quant-lib_amd/quantlib_amd.py); no framework runtime is
@@ -368,33 +371,54 @@ def all_configs(ql, np, reps):
                      "us": round(us, 2), "GBps": round(gbs, 1), "frac_peak": round(gbs / PEAK_HBM_GBS, 4)})
     rows += attention_rows(ql, np, chain, reps)
     rows += layer_rows(ql, np, chain, reps)
+    del chain
+    rows += fp8_rows(ql, np, reps)
     return rows
 
 
 def layer_rows(ql, np, chain, reps):
-    """One whole Llama-3-8B-shaped fp16 decoder layer through the engine
-    (ql_engine_layer_f16: hipBLASLt GEMMs + the fused kernels + attention):
-    a 8192-token prefill of one sequence and a decode step of 64 sequences at
-    4096 keys.  Weights are seeded N(0, 1/fan_in), uploaded once."""
+    """One whole Llama-3-8B-shaped decoder layer through the engine -- fp16 weights
+    (ql_engine_layer_f16: hipBLASLt GEMMs + the fused kernels + attention) and FP8
+    weights (ql_engine_layer_fp8: the reference's quantize_model config, E4M3 in
+    groups of 128 with its own codec) -- for a 8192-token prefill of one sequence,
+    a decode step of 64 sequences at 4096 keys and a one-sequence decode step
+    (the reference's quantized generation).  Weights are seeded N(0, 1/fan_in);
+    the step rotates over several weight sets (>= 600 MB) so that none is still
+    in the 256 MB MALL, as the layers of a model stream theirs."""
     st = chain.stream
     up = ql.DeviceArray.from_numpy
     r = np.random.default_rng(21)
-
-    def w(shape, fan_in):
-        return up((r.standard_normal(shape, dtype=np.float32) * np.float32(fan_in ** -0.5))
-                  .astype(np.float16).view(np.uint16))
-
     QKV = (HQ + 2 * HKV) * HD
-    wts = {"attn_norm": up(np.ones(D, np.float16).view(np.uint16)), "wqkv": w((QKV, D), D),
-           "wo": w((D, HQ * HD), HQ * HD), "ffn_norm": up(np.ones(D, np.float16).view(np.uint16)),
-           "w_gate": w((F, D), D), "w_up": w((F, D), D), "w_down": w((D, F), F)}
-    lw = ql.LayerWeights(*(wts[k].ptr for k in ("attn_norm", "wqkv", "wo", "ffn_norm", "w_gate", "w_up",
-                                                "w_down")))
+    shapes = {"wqkv": (QKV, D), "wo": (D, HQ * HD), "w_gate": (F, D), "w_up": (F, D), "w_down": (D, F)}
+    host = {k: (r.standard_normal(sh, dtype=np.float32) * np.float32(sh[1] ** -0.5)).astype(np.float16)
+            .view(np.uint16) for k, sh in shapes.items()}
+    norm = up(np.ones(D, np.float16).view(np.uint16))
+    f16_sets = [{k: up(v) for k, v in host.items()} for _ in range(3)]
+    del host
+    lw16 = [ql.LayerWeights(norm.ptr, w["wqkv"].ptr, w["wo"].ptr, norm.ptr, w["w_gate"].ptr, w["w_up"].ptr,
+                            w["w_down"].ptr) for w in f16_sets]
+    fmt, gran, gs, mode = ql.FP8_E4M3, ql.QUANT_PER_GROUP, 128, ql.FP8_MODE_REFERENCE
+    fp8_sets, lw8 = [], []
+    for i in range(6):
+        src = f16_sets[i % 3]
+        w8 = {}
+        for k, (n_, k_) in shapes.items():
+            codes = ql.DeviceArray((n_ * k_,), np.uint8)
+            scales = ql.DeviceArray((n_ * k_ // gs,), np.float32)
+            ql.call("ql_fp8_quantize", src[k].ptr, n_, k_, fmt, gran, gs, mode, codes.ptr, scales.ptr, st)
+            w8[k] = (codes, scales)
+        fp8_sets.append(w8)
+        fw = {k: ql.FP8Weight(c.ptr, sc.ptr) for k, (c, sc) in w8.items()}
+        lw8.append(ql.LayerWeightsFP8(norm.ptr, fw["wqkv"], fw["wo"], norm.ptr, fw["w_gate"], fw["w_up"],
+                                      fw["w_down"], fmt, gran, gs, mode))
+    ql.synchronize()
     dims = ql.LayerDims(D, HQ, HKV, HD, F, THETA, EPS, ql.ROPE_HALF)
     rows = []
     gemm_flops = lambda m: 2.0 * m * D * (QKV + HQ * HD + 3 * F)
+    w_bytes = sum(n_ * k_ for n_, k_ in shapes.values())
     for label, S, C, q_len in (("prefill 1 seq x 8192 tokens", 1, T, T),
-                               ("decode 64 seq x 4096 ctx", 64, 4096, 1)):
+                               ("decode 64 seq x 4096 ctx", 64, 4096, 1),
+                               ("decode 1 seq x 4096 ctx", 1, 4096, 1)):
         nbs = C // PAGE
         nb = S * nbs
         blk = L_POOL * PAGE * HKV * HD
@@ -418,31 +442,118 @@ def layer_rows(ql, np, chain, reps):
         sd = ql.StepDevice(n_rows, S, q_len, C, nbs, arrs["pos"].ptr, arrs["slots"].ptr, arrs["cu"].ptr,
                            arrs["ctx"].ptr, arrs["bt"].ptr, kp.ptr, vp.ptr, nb, L_POOL)
         eng = ctypes.c_void_p()
-        ql.call("ql_engine_create", ctypes.byref(dims), n_rows, S, C, ctypes.byref(eng))
+        ql.call("ql_engine_create_fp8", ctypes.byref(dims), n_rows, S, C, gran, gs, ctypes.byref(eng))
         x = up(r.standard_normal((n_rows, D), dtype=np.float32).astype(np.float16).view(np.uint16))
         deltas = [ql.DeviceArray((n_rows, D), np.uint16) for _ in range(2)]
+        for kind, fn, lws, wb in (("fp16", "ql_engine_layer_f16", lw16, 2 * w_bytes),
+                                  ("fp8 e4m3 g128", "ql_engine_layer_fp8", lw8, w_bytes + 4 * w_bytes // gs)):
+            def launch(i, fn=fn, lws=lws):
+                ql.call(fn, eng, ctypes.byref(lws[i % len(lws)]), i % L_POOL, x.ptr,
+                        deltas[(i + 1) % 2].ptr if i else None, deltas[i % 2].ptr, ctypes.byref(sd), st)
+            for i in range(3):
+                launch(i)
+            ql.synchronize()
+            n = max(6, reps // 10)
+            a, b = ql.Event(), ql.Event()
+            a.record(st)
+            for i in range(n):
+                launch(i + 3)
+            b.record(st)
+            us = a.elapsed_ms(b) * 1e3 / n
+            fl = gemm_flops(n_rows) + (4.0 * (C * (C + 1) / 2) * HD * HQ if q_len > 1 else 4.0 * S * C * HD * HQ)
+            rows.append({"config": f"C5 decoder layer, {label}, {kind} weights", "kernel": fn[3:],
+                         "bytes": 0, "us": round(us, 2), "GBps": 0.0, "frac_peak": 0.0,
+                         "weight_bytes": wb,
+                         "tflops": round(fl / (us * 1e-6) / 1e12, 1),
+                         "frac_mfma_peak": round(fl / (us * 1e-6) / 1e12 / PEAK_MFMA_F16_TFLOPS, 4),
+                         "tokens_per_s_per_layer": round(n_rows / (us * 1e-6), 1)})
+        ql.call("ql_engine_destroy", eng)
+        del kpool, vpool
+    del f16_sets, fp8_sets
+    return rows
 
-        def launch(i):
-            ql.call("ql_engine_layer_f16", eng, ctypes.byref(lw), i % L_POOL, x.ptr,
-                    deltas[(i + 1) % 2].ptr if i else None, deltas[i % 2].ptr, ctypes.byref(sd), st)
+
+def fp8_rows(ql, np, reps):
+    """The FP8 weight path on Llama-3-8B FFN shapes: the skinny FP8-weight GEMM
+    (ql_fp8_gemm_f16) at decode row counts next to the fp16 library GEMM on the
+    same shape, and the codec (quantize = scales + encode, dequantize) on a
+    14336 x 4096 matrix.  Each launch reads a weight copy last touched >= 600 MB
+    earlier (rotating copies), so the weights stream from HBM.  Algorithmic bytes:
+    codes (1 B per weight) + scales + activations in + outputs out."""
+    st = ql.stream()
+    r = np.random.default_rng(31)
+    rows = []
+
+    def rotating(n_bytes):
+        return max(2, -(-(640 << 20) // n_bytes))
+
+    def timed(launch, n):
         for i in range(3):
             launch(i)
         ql.synchronize()
-        n = max(3, reps // 10)
         a, b = ql.Event(), ql.Event()
         a.record(st)
         for i in range(n):
             launch(i + 3)
         b.record(st)
-        us = a.elapsed_ms(b) * 1e3 / n
-        fl = gemm_flops(n_rows) + (4.0 * (C * (C + 1) / 2) * HD * HQ if q_len > 1 else 4.0 * S * C * HD * HQ)
-        rows.append({"config": f"C5 decoder layer, {label}", "kernel": "engine_layer_f16",
-                     "bytes": 0, "us": round(us, 2), "GBps": 0.0, "frac_peak": 0.0,
-                     "tflops": round(fl / (us * 1e-6) / 1e12, 1),
-                     "frac_mfma_peak": round(fl / (us * 1e-6) / 1e12 / PEAK_MFMA_F16_TFLOPS, 4),
-                     "tokens_per_s_per_layer": round(n_rows / (us * 1e-6), 1)})
-        ql.call("ql_engine_destroy", eng)
-        del kpool, vpool
+        return a.elapsed_ms(b) * 1e3 / n
+
+    for N, K, what in ((F, D, "gate/up 14336x4096"), (D, F, "down 4096x14336")):
+        w16 = (r.standard_normal((N, K), dtype=np.float32) * np.float32(K ** -0.5)).astype(np.float16)
+        d16 = [ql.DeviceArray.from_numpy(w16.view(np.uint16)) for _ in range(rotating(2 * N * K))]
+        del w16
+        for M in (1, 64):
+            a = ql.DeviceArray.from_numpy(r.standard_normal((M, K), dtype=np.float32).astype(np.float16)
+                                          .view(np.uint16))
+            out = ql.DeviceArray((M, N), np.uint16)
+            us16 = timed(lambda i: ql.call("ql_gemm_f16", a.ptr, d16[i % len(d16)].ptr, out.ptr, M, N, K, st),
+                         max(6, reps // 5))
+            for fmt, gran, gs, mode, label in (
+                    (ql.FP8_E4M3, ql.QUANT_PER_GROUP, 128, ql.FP8_MODE_REFERENCE, "e4m3 g128 reference codec"),
+                    (ql.FP8_E4M3, ql.QUANT_PER_CHANNEL, 0, ql.FP8_MODE_OCP, "e4m3 per-channel OCP")):
+                n_sc = N * K // 128 if gs else N
+                codes = [(ql.DeviceArray((N * K,), np.uint8), ql.DeviceArray((n_sc,), np.float32))
+                         for _ in range(rotating(N * K))]
+                for i, (c, sc) in enumerate(codes):
+                    ql.call("ql_fp8_quantize", d16[i % len(d16)].ptr, N, K, fmt, gran, gs, mode, c.ptr, sc.ptr, st)
+                size = ctypes.c_size_t()
+                ql.call("ql_fp8_gemm_workspace_size", M, N, K, gran, gs, ctypes.byref(size))
+                ws = ql.DeviceArray((max(size.value, 16),), np.uint8)
+                us = timed(lambda i: ql.call("ql_fp8_gemm_f16", a.ptr, codes[i % len(codes)][0].ptr,
+                                             codes[i % len(codes)][1].ptr, M, N, K, fmt, gran, gs, mode,
+                                             out.ptr, ws.ptr, size.value, st), max(6, reps // 5))
+                nbytes = N * K + 4 * n_sc + 2 * M * K + 2 * M * N
+                gbs = nbytes / (us * 1e-6) / 1e9
+                rows.append({"config": f"FP8 GEMM {what}, {M} rows, {label}", "kernel": "fp8_gemm_f16",
+                             "bytes": nbytes, "us": round(us, 2), "GBps": round(gbs, 1),
+                             "frac_peak": round(gbs / PEAK_HBM_GBS, 4), "fp16_gemm_us": round(us16, 2),
+                             "speedup_vs_fp16": round(us16 / us, 2), "workspace_bytes": size.value})
+                del codes, ws
+        del d16
+    # codec on one 14336 x 4096 matrix
+    N, K = F, D
+    x = (r.standard_normal((N, K), dtype=np.float32)).astype(np.float16).view(np.uint16)
+    xs = [ql.DeviceArray.from_numpy(x) for _ in range(rotating(2 * N * K))]
+    del x
+    nsets = len(xs)
+    qs = [(ql.DeviceArray((N * K,), np.uint8), ql.DeviceArray((N * K // 128,), np.float32)) for _ in range(nsets)]
+    for mode, mname in ((ql.FP8_MODE_REFERENCE, "reference codec"), (ql.FP8_MODE_OCP, "OCP")):
+        us = timed(lambda i: ql.call("ql_fp8_quantize", xs[i % nsets].ptr, N, K, ql.FP8_E4M3,
+                                     ql.QUANT_PER_GROUP, 128, mode, qs[i % nsets][0].ptr, qs[i % nsets][1].ptr, st),
+                   max(6, reps // 5))
+        nbytes = 3 * N * K + 4 * N * K // 128
+        gbs = nbytes / (us * 1e-6) / 1e9
+        rows.append({"config": f"FP8 quantize 14336x4096 e4m3 g128, {mname}", "kernel": "fp8_quantize",
+                     "bytes": nbytes, "us": round(us, 2), "GBps": round(gbs, 1),
+                     "frac_peak": round(gbs / PEAK_HBM_GBS, 4)})
+        us = timed(lambda i: ql.call("ql_fp8_dequantize", qs[i % nsets][0].ptr, qs[i % nsets][1].ptr, N, K,
+                                     ql.FP8_E4M3, ql.QUANT_PER_GROUP, 128, mode, xs[(i + 1) % nsets].ptr, st),
+                   max(6, reps // 5))
+        gbs = nbytes / (us * 1e-6) / 1e9
+        rows.append({"config": f"FP8 dequantize 14336x4096 e4m3 g128, {mname}", "kernel": "fp8_dequantize",
+                     "bytes": nbytes, "us": round(us, 2), "GBps": round(gbs, 1),
+                     "frac_peak": round(gbs / PEAK_HBM_GBS, 4)})
+    del xs, qs
     return rows
 
 

@@ -133,7 +133,9 @@ GEMM_CASES = [
     (64, 1024, 8192, ql.QUANT_PER_GROUP, 16),
     (20, 512, 1024, ql.QUANT_PER_CHANNEL, 0),      # two token tiles, four row tiles
     (3, 480, 512, ql.QUANT_PER_GROUP, 64),         # one token tile, two row tiles
-    (5, 208, 256, ql.QUANT_PER_TENSOR, 0)]         # one token tile, one row tile
+    (5, 208, 256, ql.QUANT_PER_TENSOR, 0),         # one token tile, one row tile
+    (30, 480, 512, ql.QUANT_PER_CHANNEL, 0),       # two token tiles, two row tiles
+    (40, 208, 512, ql.QUANT_PER_GROUP, 64)]        # four token tiles, one row tile
 
 
 @pytest.mark.parametrize("mode", MODES)
