@@ -32,9 +32,9 @@ TFLOP/s against the dense fp16 matrix peak, and paged decode (64 sequences x
 4096 tokens; 1 sequence x 8192 tokens with the key-split workspace), HBM-bound
 on the K/V rows, and one whole decoder layer through the engine (hipBLASLt
 GEMMs + the fused kernels + attention) for that prefill and those decode steps,
-on fp16 weights and on FP8 weights (the reference's quantized forward), plus
-the FP8-weight GEMM at decode row counts against the fp16 GEMM and the FP8
-codec.
+on fp16 weights and on FP8 weights (the reference's quantized forward; the
+decode steps also as a 32-layer step captured in one HIP graph), plus the
+FP8-weight GEMM at decode row counts against the fp16 GEMM and the FP8 codec.
 
 Device memory, the stream and events come from libamdhip64 through the
 library's own binding (quant-lib_amd/quantlib_amd.py); no framework runtime is
@@ -467,6 +467,34 @@ def layer_rows(ql, np, chain, reps):
                          "tflops": round(fl / (us * 1e-6) / 1e12, 1),
                          "frac_mfma_peak": round(fl / (us * 1e-6) / 1e12 / PEAK_MFMA_F16_TFLOPS, 4),
                          "tokens_per_s_per_layer": round(n_rows / (us * 1e-6), 1)})
+            if q_len == 1:
+                # the whole 32-layer decode step captured once and replayed
+                # (ql_graph_*): one submission instead of ~16 launches per layer
+                graph = ctypes.c_void_p()
+                ql.call("ql_graph_begin", st)
+                try:
+                    for l in range(L_POOL):
+                        launch(l)
+                finally:
+                    ql.call("ql_graph_end", st, ctypes.byref(graph))
+                for _ in range(2):
+                    ql.call("ql_graph_launch", graph, st)
+                ql.synchronize()
+                ng = max(3, reps // 20)
+                a, b = ql.Event(), ql.Event()
+                a.record(st)
+                for _ in range(ng):
+                    ql.call("ql_graph_launch", graph, st)
+                b.record(st)
+                us_g = a.elapsed_ms(b) * 1e3 / (ng * L_POOL)
+                ql.call("ql_graph_destroy", graph)
+                rows.append({"config": f"C5 decoder layer, {label}, {kind} weights, {L_POOL}-layer step "
+                                       "in one HIP graph (per layer)", "kernel": fn[3:],
+                             "bytes": 0, "us": round(us_g, 2), "GBps": 0.0, "frac_peak": 0.0,
+                             "weight_bytes": wb, "weight_GBps": round(wb / (us_g * 1e-6) / 1e9, 1),
+                             "tflops": round(fl / (us_g * 1e-6) / 1e12, 1),
+                             "frac_mfma_peak": round(fl / (us_g * 1e-6) / 1e12 / PEAK_MFMA_F16_TFLOPS, 4),
+                             "tokens_per_s_per_layer": round(n_rows / (us_g * 1e-6), 1)})
         ql.call("ql_engine_destroy", eng)
         del kpool, vpool
     del f16_sets, fp8_sets

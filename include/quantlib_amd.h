@@ -491,6 +491,21 @@ hipError_t ql_engine_layer_fp8(ql_engine* e, const ql_layer_weights_fp8* w, int 
                                const uint16_t* delta_in, uint16_t* delta_out,
                                const ql_step_device* step, hipStream_t stream);
 
+/* ---- HIP graphs of library calls ----------------------------------------------------------
+ * No counterpart in the reference (it launches every op of every token from the host).
+ * ql_graph_begin starts capturing `stream` (not the null stream; thread-local mode, so
+ * an allocation or synchronisation on this thread during capture fails); the library
+ * calls that follow are recorded, not run; ql_graph_end instantiates them.
+ * ql_graph_launch replays them on any stream.  Capturable: every entry point above
+ * once each GEMM shape has run eagerly (plan and workspace created).  Values read
+ * from device memory (positions, slots, ctx_lens, block tables, inputs) may change
+ * between replays; host arguments and pointers are those of the capture. */
+typedef struct ql_graph ql_graph;
+hipError_t ql_graph_begin(hipStream_t stream);
+hipError_t ql_graph_end(hipStream_t stream, ql_graph** out);
+hipError_t ql_graph_launch(ql_graph* g, hipStream_t stream);
+hipError_t ql_graph_destroy(ql_graph* g);
+
 /* x += delta_in over all n_rows rows, final RMSNorm, gather the n_sample rows
  * sample_rows[] (device), logits = rows lm_head^T ([n_sample, vocab] fp16) and, if
  * tokens is not NULL, tokens[i] = argmax of logits row i (device). */

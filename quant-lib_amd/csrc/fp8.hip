@@ -231,28 +231,28 @@ __global__ __launch_bounds__(kBlock) void dequantize_kernel(const uint8_t* __res
 constexpr int kGemmWaves = 4;
 
 // scale lookup of the register path: one scale (tensor), one per weight row, per
-// group with K % gs == 0 from the workgroup's LDS table of inverses (GroupLds) or
-// from global memory (Group), and groups that straddle rows (Any)
-enum ScaleKind { kScaleTensor = 0, kScaleRow = 1, kScaleGroupLds = 2, kScaleGroup = 3, kScaleAny = 4 };
+// group with K % gs == 0 from the workgroup's LDS table of inverses -- applied to
+// each 64-k chunk's sums when gs % 64 == 0 (GroupFold), else to each weight
+// (GroupLds) -- or from global memory (Group), and groups that straddle rows (Any)
+enum ScaleKind {
+    kScaleTensor = 0, kScaleRow = 1, kScaleGroupFold = 2, kScaleGroupLds = 3, kScaleGroup = 4, kScaleAny = 5
+};
 
 // bytes of 4 reference-mode codes whose reference decode differs from the OCP
-// decode: E4M3 exponent 0 with a non-zero mantissa (the reference reads it as a
-// normal number) and |code| 0x7F (the reference's 480, OCP's NaN); E5M2 exponent 0
-// with a non-zero mantissa and exponent 31 (finite in the reference).  Bytewise
-// sums of 7-bit values never carry into the next byte.
+// decode (bit 7 of each byte of the result): E4M3 exponent 0 with a non-zero
+// mantissa (the reference reads it as a normal number) and |code| 0x7F (the
+// reference's 480, OCP's NaN); E5M2 exponent 0 with a non-zero mantissa and
+// exponent 31 (finite in the reference).  With l = |code| (7 bits) per byte,
+// l + 0x7F has bit 7 iff l >= 1, 0x87 - l (or 0x83 - l) iff l <= 7 (l <= 3), and
+// l + 0x01 (l + 0x04) iff l == 0x7F (l >= 0x7C); none of these carries or borrows
+// across bytes.  The caller masks the OR of several words with 0x80808080.
 template <int FMT>
 __device__ __forceinline__ uint32_t ref_special(uint32_t w) {
-    const uint32_t low7 = w & 0x7F7F7F7Fu;
-    const uint32_t nz = (low7 + 0x7F7F7F7Fu) & 0x80808080u;
-    if constexpr (FMT == QL_FP8_E4M3) {
-        const uint32_t ge8 = (low7 + 0x78787878u) & 0x80808080u;
-        const uint32_t is7f = (low7 + 0x01010101u) & 0x80808080u;
-        return (nz & ~ge8) | is7f;
-    } else {
-        const uint32_t ge4 = (low7 + 0x7C7C7C7Cu) & 0x80808080u;
-        const uint32_t ge7c = (low7 + 0x04040404u) & 0x80808080u;
-        return (nz & ~ge4) | ge7c;
-    }
+    const uint32_t l = w & 0x7F7F7F7Fu;
+    const uint32_t ge1 = l + 0x7F7F7F7Fu;
+    const uint32_t le_m = (FMT == QL_FP8_E4M3 ? 0x87878787u : 0x83838383u) - l;
+    const uint32_t top = l + (FMT == QL_FP8_E4M3 ? 0x01010101u : 0x04040404u);
+    return (ge1 & le_m) | top;
 }
 
 // 16 codes -> two fp16 fragments of binary16(decode(code) * inv).  The hardware
@@ -276,8 +276,8 @@ __device__ __forceinline__ void dequant16(uint4 codes, float inv, half8& lo, hal
         f[4 * j + 3] = b[1];
     }
     if constexpr (MODE == QL_FP8_MODE_REFERENCE) {
-        const uint32_t special = ref_special<FMT>(w[0]) | ref_special<FMT>(w[1]) | ref_special<FMT>(w[2]) |
-                                 ref_special<FMT>(w[3]);
+        const uint32_t special = (ref_special<FMT>(w[0]) | ref_special<FMT>(w[1]) | ref_special<FMT>(w[2]) |
+                                  ref_special<FMT>(w[3])) & 0x80808080u;
         if (special) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) f[e] = dec_ref<FMT>((w[e >> 2] >> (8 * (e & 3))) & 0xFFu);
@@ -308,6 +308,7 @@ struct SkStage {
     uint4 w[R];
     half8 a[MT][2];
     float s[R];
+    int gi;               // kScaleGroupFold: the chunk's group, relative to the table
 };
 
 // Per-tensor and per-row scales are applied once to the accumulated products
@@ -326,13 +327,14 @@ __device__ __forceinline__ float scale_at(const SkinnyArgs& p, int row, int k) {
     else return p.scales[row * p.groups_per_row + (int)((unsigned)k / (unsigned)p.gs)];
 }
 
-// kScaleGroup(Lds): the group of a lane's next chunk, advanced by 256 k per load
-// (the loads of a wavefront run through its chunks in order, 4 apart) and clamped
-// to the group of its last chunk (the loads past the end repeat that chunk).
+// kScaleGroup*: the group of a lane's next chunk, advanced by 256 k per load (the
+// loads of a wavefront run through its chunks in order, 4 apart) and clamped to
+// the group of its last chunk (the loads past the end repeat that chunk).  For
+// kScaleGroupFold the whole chunk lies in one group, so the cursor is uniform.
 struct GroupCursor {
     int g, rem, g_last;
-    const float* lds;     // kScaleGroupLds: [NR][ng] inverse scales of groups g0 .. g0+ng-1
-    int ng, g0;
+    const float* lds;     // inverse scales of groups g0 .. g0+ng-1: [NR][ng] (GroupLds),
+    int ng, g0;           // [ng][NR] (GroupFold)
 };
 
 template <int MT, int R, int SK>
@@ -347,13 +349,14 @@ __device__ __forceinline__ void sk_load(SkStage<MT, R>& st, const SkinnyArgs& p,
         st.a[t][0] = *reinterpret_cast<const half8*>(p.A + (aoff[t] + 2u * k));
         st.a[t][1] = *reinterpret_cast<const half8*>(p.A + (aoff[t] + 2u * k + 16u));
     }
-    if constexpr (SK == kScaleGroupLds || SK == kScaleGroup) {
+    if constexpr (SK == kScaleGroupFold || SK == kScaleGroupLds || SK == kScaleGroup) {
         const int g = min(gc.g, gc.g_last);
         const int lane16 = threadIdx.x & 15;
+        if constexpr (SK == kScaleGroupFold) st.gi = g - gc.g0;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             if constexpr (SK == kScaleGroupLds) st.s[r] = gc.lds[(16 * r + lane16) * gc.ng + g - gc.g0];
-            else st.s[r] = p.scales[row[r] * p.groups_per_row + g];
+            else if constexpr (SK == kScaleGroup) st.s[r] = p.scales[row[r] * p.groups_per_row + g];
         }
         gc.g += p.g_step;
         gc.rem += p.r_step;
@@ -369,8 +372,28 @@ __device__ __forceinline__ void sk_load(SkStage<MT, R>& st, const SkinnyArgs& p,
 
 template <int FMT, int MODE, int MT, int R, int SK>
 __device__ __forceinline__ void sk_compute(const SkStage<MT, R>& st, const float (&inv_fixed)[R],
-                                           floatx4 (&acc)[R][MT]) {
+                                           const float* table, int kq, floatx4 (&acc)[R][MT]) {
     constexpr bool kFold = fold_scale<FMT, MODE, SK>();
+    if constexpr (SK == kScaleGroupFold) {
+        // the chunk's products of decoded codes, then one multiply-add per output
+        // by the inverse scale of its weight row (lane rows 16r + 4*kq + i)
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            half8 wlo, whi;
+            dequant16<FMT, MODE, false>(st.w[r], 1.0f, wlo, whi);
+            const float4 inv = *reinterpret_cast<const float4*>(table + st.gi * (16 * R) + 16 * r + 4 * kq);
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                floatx4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(wlo, st.a[t][0], floatx4{}, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(whi, st.a[t][1], c, 0, 0, 0);
+                acc[r][t][0] = fmaf(c[0], inv.x, acc[r][t][0]);
+                acc[r][t][1] = fmaf(c[1], inv.y, acc[r][t][1]);
+                acc[r][t][2] = fmaf(c[2], inv.z, acc[r][t][2]);
+                acc[r][t][3] = fmaf(c[3], inv.w, acc[r][t][3]);
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         // v_rcp_f32 (1 ulp): the weight is rounded to binary16 right after
@@ -389,7 +412,9 @@ __device__ __forceinline__ void sk_compute(const SkStage<MT, R>& st, const float
 // floats of the skinny kernel's LDS: the four wavefronts' partial tiles, and at
 // least 16 KB for the inverse-scale table
 __host__ __device__ constexpr int skinny_smem_floats(int nr, int mc, int sk) {
-    return sk == kScaleGroupLds && kGemmWaves * nr * (mc + 1) < 4096 ? 4096 : kGemmWaves * nr * (mc + 1);
+    return (sk == kScaleGroupLds || sk == kScaleGroupFold) && kGemmWaves * nr * (mc + 1) < 4096
+               ? 4096
+               : kGemmWaves * nr * (mc + 1);
 }
 
 template <int FMT, int MODE, int MT, int R, int SK>
@@ -426,12 +451,19 @@ __global__ __launch_bounds__(kGemmWaves * kWave) void fp8_gemm_skinny(SkinnyArgs
     constexpr int kSmemFloats = skinny_smem_floats(NR, MC, SK);
     __shared__ float smem[kSmemFloats];
     GroupCursor gc{0, 0, 0, nullptr, 0, 0};
-    if constexpr (SK == kScaleGroupLds) {
+    if constexpr (SK == kScaleGroupLds || SK == kScaleGroupFold) {
         const int gs = (int)p.gs;
         gc.g0 = c_begin * 64 / gs;
         gc.ng = (c_end * 64 - 1) / gs + 1 - gc.g0;
         for (int i = threadIdx.x; i < NR * gc.ng; i += kGemmWaves * kWave) {
-            const int rr = i / gc.ng, gg = i - rr * gc.ng;
+            int rr, gg;
+            if constexpr (SK == kScaleGroupFold) {   // group-major: a lane's 4 rows are adjacent
+                gg = i / NR;
+                rr = i - gg * NR;
+            } else {
+                rr = i / gc.ng;
+                gg = i - rr * gc.ng;
+            }
             smem[i] = 1.0f / p.scales[(n0 + rr) * p.groups_per_row + gc.g0 + gg];
         }
         gc.lds = smem;
@@ -446,11 +478,12 @@ __global__ __launch_bounds__(kGemmWaves * kWave) void fp8_gemm_skinny(SkinnyArgs
     const int first = c_begin + wave;              // wave-uniform
     if (first < c_end) {
         const int last = first + kGemmWaves * ((c_end - 1 - first) / kGemmWaves);
-        if constexpr (SK == kScaleGroupLds || SK == kScaleGroup) {
-            const int k0 = first * 64 + 16 * kq;
+        if constexpr (SK == kScaleGroupFold || SK == kScaleGroupLds || SK == kScaleGroup) {
+            const int kl = SK == kScaleGroupFold ? 0 : 16 * kq;
+            const int k0 = first * 64 + kl;
             gc.g = k0 / (int)p.gs;
             gc.rem = k0 - gc.g * (int)p.gs;
-            gc.g_last = (last * 64 + 16 * kq) / (int)p.gs;
+            gc.g_last = (last * 64 + kl) / (int)p.gs;
         }
         SkStage<MT, R> st[NS];
 #pragma unroll
@@ -460,12 +493,13 @@ __global__ __launch_bounds__(kGemmWaves * kWave) void fp8_gemm_skinny(SkinnyArgs
 #pragma unroll
             for (int s = 0; s < NS; ++s) {
                 const int cs = c0 + kGemmWaves * s;
-                if (cs <= last) sk_compute<FMT, MODE, MT, R, SK>(st[s], inv_fixed, acc);
+                if (cs <= last) sk_compute<FMT, MODE, MT, R, SK>(st[s], inv_fixed, gc.lds, kq, acc);
                 sk_load<MT, R, SK>(st[s], p, woff, row, aoff, min(cs + kGemmWaves * NS, last), kq, gc);
             }
         }
     }
-    if constexpr (SK == kScaleGroupLds) __syncthreads();   // the table's space is reused below
+    if constexpr (SK == kScaleGroupLds || SK == kScaleGroupFold)
+        __syncthreads();   // the table's space is reused below
     // lane holds C^T[16r + 4*(lane/16) + i][16t + lane%16]; sum the four wavefronts
     // (the folded scale is per weight row, i.e. per i)
     float (*part)[NR][MC + 1] = reinterpret_cast<float (*)[NR][MC + 1]>(smem);
@@ -581,10 +615,14 @@ SkinnyPlan skinny_plan(int M, int N, int K, size_t ws_bytes) {
     return s;
 }
 
-int scale_kind(const Geom& g, int K, const SkinnyPlan& pl) {
+int scale_kind(const Geom& g, int K, const SkinnyPlan& pl, int format, int mode) {
     if (g.n_groups == 1) return kScaleTensor;
     if (g.gs == K) return kScaleRow;
     if (K % g.gs) return kScaleAny;
+    // chunk sums need every decoded code in binary16 range (not reference-mode E5M2);
+    // with 4 token tiles the 16 multiply-adds per row tile cost more than scaling
+    // the 16 weights
+    const bool fold = g.gs % 64 == 0 && pl.mt <= 2 && !(format == QL_FP8_E5M2 && mode == QL_FP8_MODE_REFERENCE);
     // the largest group range of a K-split must fit the LDS table
     const int n_chunks = K / 64;
     int ng_max = 0;
@@ -593,7 +631,8 @@ int scale_kind(const Geom& g, int K, const SkinnyPlan& pl) {
         ng_max = std::max(ng_max, (int)((ce * 64LL - 1) / g.gs + 1 - cb * 64LL / g.gs));
     }
     const int nr = 16 * pl.r, mc = 16 * pl.mt;
-    return (long long)nr * ng_max <= skinny_smem_floats(nr, mc, kScaleGroupLds) ? kScaleGroupLds : kScaleGroup;
+    if ((long long)nr * ng_max > skinny_smem_floats(nr, mc, kScaleGroupLds)) return kScaleGroup;
+    return fold ? kScaleGroupFold : kScaleGroupLds;
 }
 
 template <int FMT, int MODE, int MT, int R>
@@ -602,6 +641,7 @@ void launch_skinny_rs(const SkinnyArgs& a, int kind, dim3 grid, hipStream_t st) 
     switch (kind) {
     case kScaleTensor: hipLaunchKernelGGL((fp8_gemm_skinny<FMT, MODE, MT, R, kScaleTensor>), grid, block, 0, st, a); break;
     case kScaleRow: hipLaunchKernelGGL((fp8_gemm_skinny<FMT, MODE, MT, R, kScaleRow>), grid, block, 0, st, a); break;
+    case kScaleGroupFold: hipLaunchKernelGGL((fp8_gemm_skinny<FMT, MODE, MT, R, kScaleGroupFold>), grid, block, 0, st, a); break;
     case kScaleGroupLds: hipLaunchKernelGGL((fp8_gemm_skinny<FMT, MODE, MT, R, kScaleGroupLds>), grid, block, 0, st, a); break;
     case kScaleGroup: hipLaunchKernelGGL((fp8_gemm_skinny<FMT, MODE, MT, R, kScaleGroup>), grid, block, 0, st, a); break;
     default: hipLaunchKernelGGL((fp8_gemm_skinny<FMT, MODE, MT, R, kScaleAny>), grid, block, 0, st, a); break;
@@ -751,7 +791,7 @@ extern "C" hipError_t ql_fp8_gemm_f16(const uint16_t* A, const uint8_t* W, const
         a.groups_per_row = K % g.gs == 0 ? (int)(K / g.gs) : 0;
         a.g_step = (int)(256 / g.gs);
         a.r_step = (int)(256 % g.gs);
-        QL_FP8_DISPATCH(format, mode, launch_skinny, a, pl, scale_kind(g, K, pl), stream);
+        QL_FP8_DISPATCH(format, mode, launch_skinny, a, pl, scale_kind(g, K, pl, format, mode), stream);
         if (pl.splits > 1) {
             const long long mn = (long long)M * N;
             hipLaunchKernelGGL(splitk_reduce, dim3(qlh::blocks_for(mn / 4, kBlock)), dim3(kBlock), 0, stream,

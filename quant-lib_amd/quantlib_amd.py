@@ -82,6 +82,10 @@ SIGNATURES = {
     "ql_engine_destroy": [_p],
     "ql_engine_layer_f16": [_p, _p, _i, _p, _p, _p, _p, _p],
     "ql_engine_create_fp8": [_p, _i, _i, _i, _i, _i, _p],
+    "ql_graph_begin": [_p],
+    "ql_graph_end": [_p, _p],
+    "ql_graph_launch": [_p, _p],
+    "ql_graph_destroy": [_p],
     "ql_engine_layer_fp8": [_p, _p, _i, _p, _p, _p, _p, _p],
     "ql_engine_logits_f16": [_p, _p, _p, _p, _p, _i, _p, _i, _i, _p, _p, _p],
     "ql_paged_decode_attention_f16": [_p, _p, _i64, _i64, _i, _p, _i, _p, _i, _p, _p, _i, _i, _i,

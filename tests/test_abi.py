@@ -157,6 +157,10 @@ P = 4096  # a non-null, 16-byte aligned dummy address: never dereferenced on the
     (("ql_fp8_dequantize", P, None, 4, 64, 0, 2, 128, 1, P, None), INVALID),
     (("ql_engine_create_fp8", None, 16, 4, 64, 2, 128, P), INVALID),
     (("ql_engine_layer_fp8", None, P, 0, P, None, P, P, None), INVALID),
+    (("ql_graph_begin", None), INVALID),
+    (("ql_graph_end", None, P), INVALID),
+    (("ql_graph_launch", None, None), INVALID),
+    (("ql_graph_destroy", None), 0),
     (("ql_fp8_gemm_f16", P, P, P, 100, 64, 64, 0, 2, 128, 1, P, None, 0, None), INVALID),
     (("ql_fp8_gemm_f16", None, None, None, 0, 64, 64, 0, 2, 128, 1, None, None, 0, None), 0),
     (("ql_gemm_f16", P, P, P, -1, 4, 4, None), INVALID),

@@ -205,3 +205,92 @@ def test_engine_fp8_layers_match_oracle(fmt, gran, gs, mode, prompts):
             deq, prompts, 3)
     finally:
         ql.call("ql_engine_destroy", eng)
+
+
+def fp8_layer(w, keep, fmt=ql.FP8_E4M3, gran=ql.QUANT_PER_GROUP, gs=128, mode=ql.FP8_MODE_REFERENCE):
+    """ql_layer_weights_fp8 of one layer's fp16 weights, quantized by the oracle codec."""
+    fw = {}
+    for k in MATS:
+        q, sc = orc.fp8_quantize(w[k], fmt, gran, gs, mode)
+        dq, ds = dev(q), dev(sc)
+        keep += [dq, ds]
+        fw[k] = ql.FP8Weight(dq.ptr, ds.ptr)
+    dn, fn = dev(w["attn_norm"]), dev(w["ffn_norm"])
+    keep += [dn, fn]
+    return ql.LayerWeightsFP8(dn.ptr, fw["wqkv"], fw["wo"], fn.ptr, fw["w_gate"], fw["w_up"], fw["w_down"],
+                              fmt, gran, gs, mode)
+
+
+@pytest.mark.parametrize("kind", ["f16", "fp8"])
+def test_decode_step_graph_replays_match_eager(kind):
+    """A 2-layer decode step captured with ql_graph_begin/end and replayed three
+    times, with eager work and synchronisations between the replays: every
+    replay reproduces the eager step bit for bit (residual stream, MLP outputs)."""
+    L = 2
+    weights = [layer_weights(100 * (l + 1)) for l in range(L)]
+    keep = []
+    if kind == "f16":
+        dw = [{k: dev(v) for k, v in w.items()} for w in weights]
+        keep += dw
+        lw = [ql.LayerWeights(*(d[k].ptr for k in ("attn_norm", "wqkv", "wo", "ffn_norm", "w_gate", "w_up",
+                                                   "w_down"))) for d in dw]
+        fn = "ql_engine_layer_f16"
+    else:
+        lw = [fp8_layer(w, keep) for w in weights]
+        fn = "ql_engine_layer_fp8"
+    dims = ql.LayerDims(DM, H, HK, HD, FF, THETA, EPS, PAIR)
+    eng = ctypes.c_void_p()
+    ql.call("ql_engine_create_fp8", ctypes.byref(dims), 64, 8, 256, ql.QUANT_PER_GROUP, 128, ctypes.byref(eng))
+    pool = PagedPool(32, L, HK, HD)
+    b = ql.Batcher(32, 4)
+    for rid, n in {0: 20, 1: 33, 2: 5}.items():
+        b.add(rid, np.arange(n, dtype=np.int32), 8)
+    st = stream()
+    graph = ctypes.c_void_p()
+
+    def run_step(sd, dx, deltas):
+        for l in range(L):
+            ql.call(fn, eng, ctypes.byref(lw[l]), l, dx.ptr, deltas[l - 1].ptr if l else None, deltas[l].ptr,
+                    ctypes.byref(sd), st)
+    try:
+        # prefill step, eagerly (fills the K/V history)
+        plan = b.plan()
+        sd = step_device(plan, pool, L, keep)
+        dx = dev(to_f16_bits(normal(1, (plan["n_rows"], DM))))
+        deltas = [empty((plan["n_rows"] * DM,), np.uint16) for _ in range(L)]
+        run_step(sd, dx, deltas)
+        b.commit(np.zeros(plan["n_seqs"], np.int32))
+        # decode step: eager reference (also the warm-up of its GEMM shapes)
+        plan = b.plan()
+        assert plan["max_q_len"] == 1
+        T = plan["n_rows"]
+        sd = step_device(plan, pool, L, keep)
+        x0 = to_f16_bits(normal(2, (T, DM)))
+        dx = dev(x0)
+        deltas = [empty((T * DM,), np.uint16) for _ in range(L)]
+        run_step(sd, dx, deltas)
+        want_x = host(dx, shape=(T, DM)).copy()
+        want_d = [host(d, shape=(T, DM)).copy() for d in deltas]
+        # capture the same step
+        dx.upload(x0)
+        ql.call("ql_graph_begin", st)
+        try:
+            run_step(sd, dx, deltas)
+        finally:
+            ql.call("ql_graph_end", st, ctypes.byref(graph))
+        scratch = [dev(to_f16_bits(normal(3, (T, FF)))) for _ in range(3)]
+        for rep in range(3):
+            dx.upload(x0)
+            for d in deltas:
+                d.fill_bytes(0)
+            # eager work between replays on the same stream
+            ql.call("ql_swiglu_f16", scratch[0].ptr, scratch[1].ptr, scratch[2].ptr, T, FF, st)
+            ql.call("ql_graph_launch", graph, st)
+            ql.synchronize()
+            assert np.array_equal(host(dx, shape=(T, DM)), want_x), f"replay {rep}: residual stream"
+            for l in range(L):
+                assert np.array_equal(host(deltas[l], shape=(T, DM)), want_d[l]), f"replay {rep}: layer {l}"
+    finally:
+        if graph.value:
+            ql.call("ql_graph_destroy", graph)
+        ql.call("ql_engine_destroy", eng)

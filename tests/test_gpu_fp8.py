@@ -7,9 +7,10 @@ GEMM tolerance, |got - want| <= 2^-10*|want| + 2^-10 * sum_k |a_k w_k|: the
 oracle accumulates in double from the codec's dequantized weights; the kernels
 accumulate in fp32.  The register path either multiplies each decoded weight by
 1/scale before rounding it to binary16, which can move a weight by one binary16
-step (2^-11 relative), or, for per-tensor and per-row scales, multiplies the fp32
-sums of the exactly decoded codes by 1/scale, which skips the weight rounding
-altogether (at most 2^-11 relative from the oracle's rounded weights)."""
+step (2^-11 relative), or, for per-tensor and per-row scales and for groups of a
+multiple of 64, multiplies the fp32 sums of the exactly decoded codes by 1/scale,
+which skips the weight rounding altogether (at most 2^-11 relative from the
+oracle's rounded weights)."""
 import ctypes
 
 import numpy as np
