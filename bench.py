@@ -90,6 +90,9 @@ def parse():
     ap.add_argument("--all-configs", action="store_true",
                     help="time every BASELINE config (C1..C5) and print a table instead of the JSON line")
     ap.add_argument("--reps", type=int, default=50, help="launches per config in --all-configs")
+    ap.add_argument("--only", default="",
+                    help="--all-configs row groups to time, comma-separated: "
+                         "configs, attention, layer, fp8 (default: all)")
     return ap.parse_args()
 
 
@@ -277,13 +280,16 @@ def cpu_baseline(seconds):
                       f"= {el / reps * T / n * 1e6:.0f} us per decoder layer at T=8192"}
 
 
-def all_configs(ql, np, reps):
+def all_configs(ql, np, reps, only=()):
     """Every BASELINE config: device time per launch, back to back on one stream
     with enough rotating buffer sets that each launch reads data last touched
     >= 1 GiB earlier (defeats the 256 MB MALL).  Returns a list of rows."""
     r = np.random.default_rng(7)
     st = ql.stream()
     rows = []
+    want = lambda group: not only or group in only
+    if not want("configs") and not want("attention") and not want("layer"):
+        return fp8_rows(ql, np, reps) if want("fp8") else rows
 
     def sets_for(nbytes):
         return max(2, min(64, -(-(1 << 30) // max(nbytes, 1))))
@@ -316,6 +322,12 @@ def all_configs(ql, np, reps):
             np.clip(x, -clip, clip, out=x)
         return x
 
+    chain = Chain(ql, np)
+    if not want("configs"):
+        rows += attention_rows(ql, np, chain, reps) if want("attention") else []
+        rows += layer_rows(ql, np, chain, reps) if want("layer") else []
+        del chain
+        return rows + (fp8_rows(ql, np, reps) if want("fp8") else [])
     # C1: RMSNorm fp32 2048x2048
     R_, C_ = 2048, 2048
     x1, w1 = randn(R_, C_), r.uniform(0.5, 1.5, C_).astype(np.float32)
@@ -353,7 +365,6 @@ def all_configs(ql, np, reps):
                 lambda b, prec=prec: ql.call(f"ql_softmax_{prec}", b[0].ptr, b[1].ptr, 4096, 4096, st))
     del x4
     # C5: the layer-chain kernels (one launch each, as in the default mode)
-    chain = Chain(ql, np)
     for name in ["embed_f16", "add_rmsnorm_f16", "rope_f16", "paged_kv_append_f16",
                  "rope_paged_kv_append_f16", "swiglu_f16"]:
         launch = chain.kernel_launcher(name)
@@ -369,10 +380,10 @@ def all_configs(ql, np, reps):
         gbs = BYTES[name] / (us * 1e-6) / 1e9
         rows.append({"config": "C5 T=8192 llama3-8b", "kernel": name, "bytes": BYTES[name],
                      "us": round(us, 2), "GBps": round(gbs, 1), "frac_peak": round(gbs / PEAK_HBM_GBS, 4)})
-    rows += attention_rows(ql, np, chain, reps)
-    rows += layer_rows(ql, np, chain, reps)
+    rows += attention_rows(ql, np, chain, reps) if want("attention") else []
+    rows += layer_rows(ql, np, chain, reps) if want("layer") else []
     del chain
-    rows += fp8_rows(ql, np, reps)
+    rows += fp8_rows(ql, np, reps) if want("fp8") else []
     return rows
 
 
@@ -677,7 +688,7 @@ def main():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
     if args.all_configs:
-        rows = all_configs(ql, np, args.reps)
+        rows = all_configs(ql, np, args.reps, tuple(g for g in args.only.split(",") if g))
         print("| config | kernel | algorithmic bytes | us per launch | GB/s | % of 8 TB/s |")
         print("|---|---|---|---|---|---|")
         for r_ in rows:

@@ -8,8 +8,10 @@
 //   x += delta_in; y = rmsnorm(x) * attn_norm        ql_add_rmsnorm_f16 (fused)
 //   qkv = y Wqkv^T                                    hipBLASLt (Q, K, V in one GEMM)
 //   rope(q, k); k, v -> paged pool                    ql_rope_paged_kv_append_f16 (fused)
-//   a = attention(q, paged K/V)                       ql_paged_attention_f16, or the
-//                                                     split decode for all-decode steps
+//   a = attention(q, paged K/V)                       ql_paged_attention_f16, the split
+//                                                     decode for all-decode steps, or
+//                                                     ql_attention_f16 on the QKV rows
+//                                                     for one fresh prompt
 //   x += a Wo^T; y = rmsnorm(x) * ffn_norm            hipBLASLt + ql_add_rmsnorm_f16
 //   delta_out = swiglu(y Wg^T, y Wu^T) Wd^T           hipBLASLt x2, ql_swiglu_f16, hipBLASLt
 //
@@ -184,7 +186,12 @@ hipError_t layer_forward(ql_engine* e, const uint16_t* attn_norm, const uint16_t
                                        s->n_blocks, s->slot_mapping, layer, s->n_layers, stream));
     const uint16_t* const* kb = reinterpret_cast<const uint16_t* const*>(s->k_blocks);
     const uint16_t* const* vb = reinterpret_cast<const uint16_t* const*>(s->v_blocks);
-    if (s->max_q_len == 1 && T == s->n_seqs) {   // every sequence decodes: row i = sequence i
+    if (s->n_seqs == 1 && s->max_q_len == T && s->max_ctx_len == T && T > 1) {
+        // one fresh prompt: its keys are exactly this step's rows, still in the QKV
+        // buffer (rotated in place), so the contiguous kernel reads them through the
+        // row stride instead of the pool (same arithmetic, no page lookups)
+        QL_TRY(ql_attention_f16(q, k, v, e->attn, T, T, H, HK, HD, QKV, QKV, (int64_t)H * HD, 1, stream));
+    } else if (s->max_q_len == 1 && T == s->n_seqs) {   // every sequence decodes: row i = sequence i
         QL_TRY(ql_paged_decode_attention_f16(q, e->attn, QKV, (int64_t)H * HD, s->n_seqs, s->ctx_lens,
                                              s->max_ctx_len, s->block_tables, s->max_blocks, kb, vb,
                                              s->n_blocks, layer, s->n_layers, H, HK, HD, e->dec_ws,

@@ -153,7 +153,9 @@ def run_engine_steps(eng, layer_call, weights, prompts, n_steps, max_gen=8):
         assert step == 0 or plan["max_q_len"] == 1        # later steps are all decodes
 
 
-def test_engine_layers_steps_and_logits_match_oracle():
+@pytest.mark.parametrize("prompts", [{0: 20, 1: 33, 2: 5},    # mixed prefill, then decodes
+                                     {0: 45}])                 # one fresh prompt: contiguous attention
+def test_engine_layers_steps_and_logits_match_oracle(prompts):
     L = 2
     weights = [layer_weights(100 * (l + 1)) for l in range(L)]
     dw = [{k: dev(v) for k, v in w.items()} for w in weights]
@@ -165,7 +167,7 @@ def test_engine_layers_steps_and_logits_match_oracle():
     try:
         run_engine_steps(eng, lambda l, x, di, do, sd: ql.call(
             "ql_engine_layer_f16", eng, ctypes.byref(lw[l]), l, x, di, do, ctypes.byref(sd), stream()),
-            weights, {0: 20, 1: 33, 2: 5}, 3)
+            weights, prompts, 3)
     finally:
         ql.call("ql_engine_destroy", eng)
 
