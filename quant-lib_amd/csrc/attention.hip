@@ -540,11 +540,14 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
 // One workgroup = (sequence, KV head, key split, chunk of <= 16 query heads).
 // The query heads that share the KV head are the 16 columns of
 // v_mfma_f32_16x16x32_f16 products, so each K/V row is read once for all of
-// them.  The 4 wavefronts stream disjoint 32-key steps of the split: K rows are
-// the A operand exactly as loaded (double-buffered in registers, no LDS); V
-// rows are transposed into a wavefront-private, double-buffered LDS area (LDS
-// operations of one wavefront complete in order, so no barrier is needed
-// there).  S^T = K.Q^T and O^T += V^T.P^T as in the prefill kernel; the
+// them.  The 4 wavefronts stream disjoint 32-key steps of the split.  K and V
+// rows are loaded whole: each load instruction covers complete 256-byte head
+// rows (16 lanes per row), which streams the pool's interleaved head rows
+// markedly faster than the MFMA fragment shape (16 rows x 64 bytes).  The
+// rows are double-buffered in registers, then re-laid through wavefront-private
+// LDS areas: K row-major with 16-byte slots XOR-swizzled by key (conflict-free
+// fragment reads), V transposed (LDS operations of one wavefront complete in
+// order, so no barrier is needed there).  S^T = K.Q^T and O^T += V^T.P^T as in the prefill kernel; the
 // wavefronts are merged through LDS at the end.  With several splits the
 // merged partial (offset m, sum l, unnormalised O) goes to the workspace and
 // attn_decode_combine finishes each row.
@@ -556,13 +559,14 @@ template <int HD>
 struct Dec {
     static constexpr int VS = kDecStep + 4;          // V^T row stride in LDS (halfs)
     static constexpr int VBUF = HD * VS;              // one V^T stage (halfs)
-    static constexpr int WAVE_V = 2 * VBUF;           // double-buffered, per wavefront
+    static constexpr int KBUF = kDecStep * HD;        // one K stage (halfs), swizzled rows
+    static constexpr int WAVE_V = VBUF + KBUF;        // LDS per wavefront (halfs)
     static constexpr int NKK = HD / 32;               // k-steps over d for S^T
     static constexpr int NDB = HD / 16;               // 16-row blocks of O^T
     static constexpr int CH = HD / 8;                 // 16-byte chunks per row
-    static constexpr int KPL = HD / 16;               // V keys per lane per step
+    static constexpr int KPL = HD / 16;               // K/V keys per lane per step
     static constexpr int KG = kWave / CH;             // key groups in the V loader
-    static_assert(KG * KPL == kDecStep, "V step split");
+    static_assert(KG * KPL == kDecStep, "K/V step split");
     static_assert(KPL % 4 == 0, "V^T writes are 4 keys wide");
     static constexpr int PART = kAttnWaves * 16 * (HD + 2);   // floats of the merge area
     static constexpr int SMEM_BYTES =
@@ -571,28 +575,27 @@ struct Dec {
 
 template <int HD>
 struct DecK {
-    half8 k[2 * Dec<HD>::NKK];
+    half8 k[Dec<HD>::KPL];   // rows as loaded: chunk lane%CH of keys KPL*(lane/CH) + i
 };
 template <int HD>
 struct DecV {
     half8 v[Dec<HD>::KPL];
 };
 
-// Per-lane constants of the decode loaders: byte offsets of the lane's K and V
-// chunks from their page base (paged) or from the step's first key row
-// (contiguous), and the page of the lane's V keys.
+// Per-lane constants of the decode loaders: byte offset of the lane's K/V chunk
+// from its page base (paged) or from the step's first key row (contiguous), and
+// the page of the lane's keys.
 template <int HD, bool PAGED>
 struct DecPlan {
     using T = Dec<HD>;
     uint32_t row_bytes;   // uniform
-    uint32_t k_off, v_off;  // the lane's first V key; key i adds i * row_bytes
+    uint32_t v_off;       // the lane's first key; key i adds i * row_bytes
     int v_page;
 
     __device__ __forceinline__ DecPlan(const AttnArgs& a, int kvh, int lane) {
         row_bytes = PAGED ? (uint32_t)(a.n_kv_heads * HD * sizeof(_Float16))
                           : (uint32_t)(a.kv_stride * sizeof(_Float16));
         const uint32_t head_bytes = PAGED ? 0u : (uint32_t)(kvh * HD * sizeof(_Float16));
-        k_off = (uint32_t)(lane & 15) * row_bytes + head_bytes + 16u * (uint32_t)(lane >> 4);
         const int ch = lane % T::CH, kg = lane / T::CH;
         const int key = T::KPL * kg;   // its KPL keys stay inside one page
         v_page = key >> 4;
@@ -608,38 +611,49 @@ __device__ __forceinline__ bool dec_clean(const Pages& pg, int k0, int k_end) {
     return clean;
 }
 
-// K rows: lane feeds key k0 + 16*kb + lane%16, d = 32*kk + 8*(lane/16) .. +8.
+// K rows, loaded like V: lane owns chunk lane%CH of keys k0 + KPL*(lane/CH) + i.
 template <int HD, bool PAGED>
 __device__ __forceinline__ void dec_fetch_k(DecK<HD>& r, const AttnArgs& a, const DecPlan<HD, PAGED>& plan,
                                             const Pages& pg, int kvh, int k0, int k_end,
                                             uintptr_t dummy, int lane) {
     using T = Dec<HD>;
     if (dec_clean<PAGED>(pg, k0, k_end)) {   // wavefront-uniform
+        const uintptr_t base =
+            PAGED ? (plan.v_page == 0 ? pg.k[0] : pg.k[1])
+                  : reinterpret_cast<uintptr_t>(a.k) +
+                        (uintptr_t)k0 * (uintptr_t)a.kv_stride * sizeof(_Float16);
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            const uintptr_t base =
-                PAGED ? pg.k[kb]
-                      : reinterpret_cast<uintptr_t>(a.k) +
-                            (uintptr_t)(k0 + 16 * kb) * (uintptr_t)a.kv_stride * sizeof(_Float16);
-#pragma unroll
-            for (int kk = 0; kk < T::NKK; ++kk)
-                r.k[kb * T::NKK + kk] = *(GlobalHalf8Ptr)(base + plan.k_off + 64u * kk);
-        }
+        for (int i = 0; i < T::KPL; ++i)
+            r.k[i] = *(GlobalHalf8Ptr)(base + plan.v_off + (uintptr_t)i * plan.row_bytes);
         return;
     }
+    const int ch = lane % T::CH, kg = lane / T::CH;
+    const bool unaligned = PAGED && pg.misaligned;   // wavefront-uniform
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-        const int j = k0 + 16 * kb + (lane & 15);
+    for (int i = 0; i < T::KPL; ++i) {
+        const int j = k0 + T::KPL * kg + i;
         const uintptr_t row = j < k_end ? key_row<PAGED>(a, a.k, pg.k, kvh, k0, j, HD) : 0;
-        if (PAGED && pg.misaligned) {   // wavefront-uniform
+        r.k[i] = unaligned ? load_chunk_unaligned(row, ch) : load_chunk(row, ch, dummy);
+    }
+}
+
+// K stage: row `key` holds its 16-byte chunk c in slot kt_slot(key, c).  Fragment
+// reads (16 lanes = keys 16*kb .. +15, one chunk) then hit 16 distinct bank groups:
+// 256-byte rows alias every bank, so the slot varies with key & 15; 128-byte rows
+// alternate bank halves, so it varies with (key >> 1) & 7.
+template <int HD>
+__device__ __forceinline__ int kt_slot(int key, int c) {
+    return HD == 128 ? (c ^ (key & 15)) : (c ^ ((key >> 1) & 7));
+}
+
+template <int HD>
+__device__ __forceinline__ void dec_stage_k(const DecK<HD>& r, _Float16* sk, int lane) {
+    using T = Dec<HD>;
+    const int ch = lane % T::CH, kg = lane / T::CH;
 #pragma unroll
-            for (int kk = 0; kk < T::NKK; ++kk)
-                r.k[kb * T::NKK + kk] = load_chunk_unaligned(row, 4 * kk + (lane >> 4));
-        } else {
-#pragma unroll
-            for (int kk = 0; kk < T::NKK; ++kk)
-                r.k[kb * T::NKK + kk] = load_chunk(row, 4 * kk + (lane >> 4), dummy);
-        }
+    for (int i = 0; i < T::KPL; ++i) {
+        const int key = T::KPL * kg + i;
+        *reinterpret_cast<half8*>(sk + key * HD + 8 * kt_slot<HD>(key, ch)) = r.k[i];
     }
 }
 
@@ -693,9 +707,9 @@ struct DecState {
     float m_run, l_run;
 };
 
-// One 32-key step: K operands in `kr`, V^T staged at sv.
+// One 32-key step: K staged at sk (row-major, swizzled), V^T staged at sv.
 template <int HD>
-__device__ __forceinline__ void dec_step(const DecK<HD>& kr, const half8* qf, floatx4* o,
+__device__ __forceinline__ void dec_step(const _Float16* sk, const half8* qf, floatx4* o,
                                          DecState& st, const _Float16* sv, int k0, int k_end,
                                          int lane, float cl2) {
     using T = Dec<HD>;
@@ -704,10 +718,13 @@ __device__ __forceinline__ void dec_step(const DecK<HD>& kr, const half8* qf, fl
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
         sc[kb] = floatx4{};
+        const int key = 16 * kb + col;
 #pragma unroll
-        for (int kk = 0; kk < T::NKK; ++kk)
-            sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kr.k[kb * T::NKK + kk], qf[kk], sc[kb],
-                                                            0, 0, 0);
+        for (int kk = 0; kk < T::NKK; ++kk) {
+            // A operand: key, d = 32*kk + 8*hq .. +8 (chunk 4*kk + hq)
+            const half8 kf = *reinterpret_cast<const half8*>(sk + key * HD + 8 * kt_slot<HD>(key, 4 * kk + hq));
+            sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[kk], sc[kb], 0, 0, 0);
+        }
     }
     // lane holds S^T[key = k0 + 16*kb + 4*hq + i][column col]
     float mt = -INFINITY;
@@ -816,18 +833,21 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_decode(AttnArgs a) {
     DecState st{-FLT_MAX, 0.0f};
     const float cl2 = a.cl2;
     _Float16* sv = reinterpret_cast<_Float16*>(smem_raw) + wave * T::WAVE_V;
+    _Float16* sk = sv + T::VBUF;
     const uintptr_t dummy = reinterpret_cast<uintptr_t>(a.q + (size_t)q_row * a.q_stride);
 
-    // wavefront w takes steps w, w+4, w+8, ...: K registers ping-pong between ka
-    // and kb; V goes through one register set into the other LDS stage; page
-    // bases flow through the 3-stage lookup, one step per stage
+    // wavefront w takes steps w, w+4, w+8, ...: each step stages its K rows
+    // (loaded one step earlier) into LDS, then reuses those registers for the
+    // next step's K rows; V goes through one register set and is staged as soon
+    // as the step has read the previous stage; page bases flow through the
+    // 3-stage lookup, one step per stage
     constexpr int kStride = kAttnWaves * kDecStep;
     constexpr int kStepPages = kDecStep / QL_PAGE_SIZE;
-    DecK<HD> ka, kb;
+    DecK<HD> kr;
     DecV<HD> vr;
     const DecPlan<HD, PAGED> plan(a, kvh, lane);
     PagePipe<PAGED, kStepPages> pp;
-    int step = wave, stage = 0;
+    int step = wave;
     Pages pg_next{};
     auto page_of = [&](int sidx) { return (k_begin + sidx * kDecStep) >> 4; };
     if (step < n_steps) {
@@ -841,32 +861,31 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_decode(AttnArgs a) {
             pg_next = pp.bases();
         }
         if (step + 2 * kAttnWaves < n_steps) pp.entries(a, table, page_of(step + 2 * kAttnWaves));
-        dec_fetch_k<HD, PAGED>(ka, a, plan, pg, kvh, k0, k_end, dummy, lane);
+        dec_fetch_k<HD, PAGED>(kr, a, plan, pg, kvh, k0, k_end, dummy, lane);
         dec_fetch_v<HD, PAGED>(vr, a, plan, pg, kvh, k0, k_end, dummy, lane);
         dec_stage_v<HD>(vr, sv, lane);
     }
-    // one step with K operands in `use`, prefetching the wavefront's next step into `fill`
-    auto run_step = [&](DecK<HD>& use, DecK<HD>& fill) -> bool {
+    // one step: stage its K rows, prefetch the wavefront's next step into the
+    // registers, multiply, then stage the next step's V rows
+    auto run_step = [&]() -> bool {
         const int k0 = k_begin + step * kDecStep;
         const bool more = step + kAttnWaves < n_steps;
+        dec_stage_k<HD>(kr, sk, lane);   // after the previous step's K reads (in order)
         if (more) {
-            dec_fetch_k<HD, PAGED>(fill, a, plan, pg_next, kvh, k0 + kStride, k_end, dummy, lane);
+            dec_fetch_k<HD, PAGED>(kr, a, plan, pg_next, kvh, k0 + kStride, k_end, dummy, lane);
             dec_fetch_v<HD, PAGED>(vr, a, plan, pg_next, kvh, k0 + kStride, k_end, dummy, lane);
         }
         if (step + 2 * kAttnWaves < n_steps) pp.pointers(a, kvh, HD);
         if (step + 3 * kAttnWaves < n_steps) pp.entries(a, table, page_of(step + 3 * kAttnWaves));
-        dec_step<HD>(use, qf, o, st, sv + stage * T::VBUF, k0, k_end, lane, cl2);
+        dec_step<HD>(sk, qf, o, st, sv, k0, k_end, lane, cl2);
         if (!more) return false;
-        stage ^= 1;
-        dec_stage_v<HD>(vr, sv + stage * T::VBUF, lane);
+        dec_stage_v<HD>(vr, sv, lane);    // after this step's V^T reads (in order)
         if (step + 2 * kAttnWaves < n_steps) pg_next = pp.bases();
         step += kAttnWaves;
         return true;
     };
-    while (step < n_steps) {
-        if (!run_step(ka, kb)) break;
-        if (!run_step(kb, ka)) break;
-    }
+    while (step < n_steps)
+        if (!run_step()) break;
 
     // merge the wavefronts: the 4 lanes of a column share m_run, so their sums add
     float l_tot = st.l_run + __shfl_xor(st.l_run, 16, kWave);
