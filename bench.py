@@ -45,6 +45,7 @@ from __future__ import annotations
 import argparse
 import ctypes
 import json
+import os
 import pathlib
 import sys
 import time
@@ -223,59 +224,81 @@ def breakdown(chain, ql, reps):
     return out
 
 
-def cpu_baseline(seconds):
-    """The oracle (scalar C, 1 thread) on a bounded sample of the same chain:
-    the C5 shapes restricted to 512 tokens, repeated until `seconds` elapse."""
+def cpu_baseline(seconds, threads=1):
+    """The oracle (scalar C) on a bounded sample of the same chain: the C5 shapes
+    restricted to 512 tokens per thread, repeated until `seconds` elapse.  With
+    threads > 1 every thread runs its own 512-token slice (own buffers) at the
+    same time; ctypes releases the interpreter lock during each C call, so the
+    slices run on separate host cores."""
+    import threading
     import numpy as np
     sys.path.insert(0, str(ROOT))
     import oracle as orc
 
     lib = orc.lib()
     n = 512
-    r = np.random.default_rng(1)
-
-    def h(*shape, clip=None):
-        a = r.standard_normal(size=shape, dtype=np.float32)
-        if clip:
-            np.clip(a, -clip, clip, out=a)
-        return a.astype(np.float16).view(np.uint16)
-
-    x, d1, d2, y = h(n, D), h(n, D), h(n, D), np.empty((n, D), np.uint16)
-    w = r.uniform(0.5, 1.5, D).astype(np.float16).view(np.uint16)
-    q, k, v = h(n, HQ * HD), h(n, HKV * HD), h(n, HKV * HD)
-    gate, up, out = h(n, F, clip=8), h(n, F, clip=8), np.empty((n, F), np.uint16)
-    nb = n // PAGE
-    blk = L_POOL * PAGE * HKV * HD
-    kpool, vpool = np.empty(nb * blk, np.uint16), np.empty(nb * blk, np.uint16)
-    offs = (np.arange(nb) * blk).astype(np.int64)
-    slots = np.arange(n, dtype=np.int32)
+    sample_bytes = CHAIN_BYTES * n // T  # the fused chain's bytes; the oracle runs rope then append
 
     def P(a):
         return a.ctypes.data
 
-    sample_bytes = CHAIN_BYTES * n // T  # the fused chain's bytes; the oracle runs rope then append
+    def make(seed):
+        r = np.random.default_rng(seed)
 
-    def one(layer):
-        lib.or_add_rmsnorm_f16(P(x), P(d1), P(w), P(y), n, D, EPS)
-        lib.or_rope_f16(P(q), n, HQ, HD, HQ * HD, None, 0, THETA, 1)
-        lib.or_rope_f16(P(k), n, HKV, HD, HKV * HD, None, 0, THETA, 1)
-        lib.or_paged_kv_append_f16(P(kpool), P(vpool), P(offs), nb, P(slots), P(k), P(v), n, layer,
-                                   L_POOL, HKV, HD)
-        lib.or_add_rmsnorm_f16(P(x), P(d2), P(w), P(y), n, D, EPS)
-        lib.or_swiglu_f16(P(gate), P(up), P(out), n * F)
+        def h(*shape, clip=None):
+            a = r.standard_normal(size=shape, dtype=np.float32)
+            if clip:
+                np.clip(a, -clip, clip, out=a)
+            return a.astype(np.float16).view(np.uint16)
 
-    one(0)
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        one(reps % L_POOL)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
+        nb = n // PAGE
+        blk = L_POOL * PAGE * HKV * HD
+        b = {"x": h(n, D), "d1": h(n, D), "d2": h(n, D), "y": np.empty((n, D), np.uint16),
+             "w": r.uniform(0.5, 1.5, D).astype(np.float16).view(np.uint16),
+             "q": h(n, HQ * HD), "k": h(n, HKV * HD), "v": h(n, HKV * HD),
+             "gate": h(n, F, clip=8), "up": h(n, F, clip=8), "out": np.empty((n, F), np.uint16),
+             "kpool": np.empty(nb * blk, np.uint16), "vpool": np.empty(nb * blk, np.uint16),
+             "offs": (np.arange(nb) * blk).astype(np.int64), "slots": np.arange(n, dtype=np.int32)}
+        b["nb"] = nb
+        return b
+
+    def one(b, layer):
+        lib.or_add_rmsnorm_f16(P(b["x"]), P(b["d1"]), P(b["w"]), P(b["y"]), n, D, EPS)
+        lib.or_rope_f16(P(b["q"]), n, HQ, HD, HQ * HD, None, 0, THETA, 1)
+        lib.or_rope_f16(P(b["k"]), n, HKV, HD, HKV * HD, None, 0, THETA, 1)
+        lib.or_paged_kv_append_f16(P(b["kpool"]), P(b["vpool"]), P(b["offs"]), b["nb"], P(b["slots"]),
+                                   P(b["k"]), P(b["v"]), n, layer, L_POOL, HKV, HD)
+        lib.or_add_rmsnorm_f16(P(b["x"]), P(b["d2"]), P(b["w"]), P(b["y"]), n, D, EPS)
+        lib.or_swiglu_f16(P(b["gate"]), P(b["up"]), P(b["out"]), n * F)
+
+    bufs = [make(1 + i) for i in range(threads)]
+    for b in bufs:
+        one(b, 0)
+    passes = [0] * threads
+    start = threading.Barrier(threads + 1)
+    stop = [0.0]
+
+    def worker(i):
+        start.wait()
+        while time.perf_counter() < stop[0]:
+            one(bufs[i], passes[i] % L_POOL)
+            passes[i] += 1
+
+    ts = [threading.Thread(target=worker, args=(i,)) for i in range(threads)]
+    for t in ts:
+        t.start()
+    t0 = time.perf_counter()
+    stop[0] = t0 + seconds
+    start.wait()
+    for t in ts:
+        t.join()
+    el = time.perf_counter() - t0
+    reps = sum(passes)
     gbs = sample_bytes * reps / el / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"oracle/oracle.c scalar C (gcc -O2, 1 thread) running the same layer chain on "
-                      f"{n} of the {T} tokens (C5 shapes), {reps} passes in {el:.1f} s; "
+    how = "1 thread" if threads == 1 else f"{threads} threads, one 512-token slice each"
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"oracle/oracle.c scalar C (gcc -O2, {how}) running the same layer chain on "
+                      f"{n}-token slices of the {T} tokens (C5 shapes), {reps} passes in {el:.1f} s; "
                       f"{sample_bytes / 1e6:.1f} MB of algorithmic traffic per pass; "
                       f"= {el / reps * T / n * 1e6:.0f} us per decoder layer at T=8192"}
 
@@ -730,6 +753,9 @@ def main():
             traffic = None
 
     cpu = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
+    # all host cores, labelled separately (the GPU box's share is 16 cores)
+    n_cores = min(16, os.cpu_count() or 1)
+    cpu_all = cpu_baseline(args.cpu_seconds, n_cores) if args.cpu_seconds > 0 and n_cores > 1 else None
 
     chain_gbs = CHAIN_BYTES / (ms_per_step * 1e-3) / 1e9
     line = {
@@ -762,6 +788,7 @@ def main():
                      "algorithmic_bytes": BYTES["swiglu_f16"], "us_per_launch": round(sw_us, 2)},
         "kernels": kernels,
         "cpu_baseline": cpu,
+        "cpu_baseline_all_cores": cpu_all,
     }
     print(json.dumps(line), flush=True)
 
