@@ -200,6 +200,13 @@ class Chain:
         }[name]
 
 
+def percentiles(us):
+    """Median, p10 and p90 of a list of durations (us)."""
+    v = sorted(us)
+    at = lambda f: v[min(len(v) - 1, int(f * len(v)))]
+    return {"us_median": round(at(0.5), 2), "us_p10": round(at(0.1), 2), "us_p90": round(at(0.9), 2)}
+
+
 def breakdown(chain, ql, reps):
     """Average duration of each kernel, HIP events around every launch."""
     out = {}
@@ -218,9 +225,8 @@ def breakdown(chain, ql, reps):
         us = sorted(a.elapsed_ms(b) * 1e3 for a, b in evs)
         mean = sum(us) / len(us)
         gbs = BYTES[name] / (mean * 1e-6) / 1e9
-        out[name] = {"us_mean": round(mean, 2), "us_median": round(us[len(us) // 2], 2),
-                     "bytes": BYTES[name], "GBps": round(gbs, 1),
-                     "frac_peak": round(gbs / PEAK_HBM_GBS, 4)}
+        out[name] = {"us_mean": round(mean, 2), **percentiles(us), "bytes": BYTES[name],
+                     "GBps": round(gbs, 1), "frac_peak": round(gbs / PEAK_HBM_GBS, 4)}
     return out
 
 
@@ -728,11 +734,12 @@ def main():
     ql.synchronize()
 
     evs = [(ql.Event(), ql.Event()) for _ in range(args.steps)]
-    t_all0, t_all1 = ql.Event(), ql.Event()
+    ev_steps = [ql.Event() for _ in range(args.steps + 1)]   # step boundaries
+    t_all0, t_all1 = ev_steps[0], ev_steps[-1]
     ql.synchronize()
     t0 = time.perf_counter()
-    t_all0.record(chain.stream)
     for i in range(args.steps):
+        ev_steps[i].record(chain.stream)
         chain.step(evs[i])
     t_all1.record(chain.stream)
     ql.synchronize()
@@ -740,7 +747,9 @@ def main():
 
     ms_per_step = wall / args.steps * 1e3
     ev_ms_per_step = t_all0.elapsed_ms(t_all1) / args.steps
-    sw_us = sum(a.elapsed_ms(b) for a, b in evs) / len(evs) * 1e3
+    sw_all = [a.elapsed_ms(b) * 1e3 for a, b in evs]
+    sw_us = sum(sw_all) / len(sw_all)
+    step_all = [ev_steps[i].elapsed_ms(ev_steps[i + 1]) * 1e3 for i in range(args.steps)]
     sw_gbs = BYTES["swiglu_f16"] / (sw_us * 1e-6) / 1e9
     kernels = breakdown(chain, ql, args.breakdown_reps)
 
@@ -768,6 +777,7 @@ def main():
         "ms_per_step": round(ms_per_step, 4),
         "us_per_decoder_layer": round(ms_per_step * 1e3, 1),
         "us_per_decoder_layer_events": round(ev_ms_per_step * 1e3, 1),
+        "step_events": percentiles(step_all),
         "frac_peak": round(chain_gbs / PEAK_HBM_GBS, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -785,7 +795,8 @@ def main():
         "roofline": {"kernel": "swiglu_f16 [8192 x 14336]", "bound": "hbm",
                      "achieved": round(sw_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(sw_gbs / PEAK_HBM_GBS, 4), "traffic": traffic,
-                     "algorithmic_bytes": BYTES["swiglu_f16"], "us_per_launch": round(sw_us, 2)},
+                     "algorithmic_bytes": BYTES["swiglu_f16"], "us_per_launch": round(sw_us, 2),
+                     **percentiles(sw_all)},
         "kernels": kernels,
         "cpu_baseline": cpu,
         "cpu_baseline_all_cores": cpu_all,

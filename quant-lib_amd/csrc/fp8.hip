@@ -120,6 +120,36 @@ __global__ __launch_bounds__(kBlock) void absmax_wave(const _Float16* __restrict
     if (lane == 0) mx[grp] = m;
 }
 
+// groups of GL*8 elements (GL = 2..64 lanes, a power of two), n % 8 == 0, 16-byte
+// aligned: each lane reads 8 consecutive elements with one 16-byte load, the GL
+// lanes of a group (a group starts at a lane multiple of GL, since every
+// wavefront starts at a multiple of 64 vectors) reduce with shuffles, and each
+// wavefront walks kAbsIters consecutive spans of 64 vectors.  In reference mode a
+// lane whose 8 elements sit at offsets >= 32 mod 128 of their group loads nothing.
+constexpr int kAbsIters = 8;
+
+template <int GL>
+__global__ __launch_bounds__(kBlock) void absmax_vec(const _Float16* __restrict__ x, Geom g, int mode,
+                                                     float* __restrict__ mx) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const long long n_vec = g.n / 8;
+    const long long w0 = ((long long)blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave) * kAbsIters * kWave;
+#pragma unroll
+    for (int it = 0; it < kAbsIters; ++it) {
+        const long long v = w0 + (long long)it * kWave + lane;
+        const long long off = (v * 8) % (8 * GL);                 // offset inside the group
+        float m = 0.0f;
+        if (v < n_vec && seen(mode, off)) {
+            const Vec<_Float16, 8> h = load<true>(reinterpret_cast<const Vec<_Float16, 8>*>(x) + v);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf((float)h.v[e]));
+        }
+#pragma unroll
+        for (int o = 1; o < GL; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
+        if ((lane & (GL - 1)) == 0 && v < n_vec) mx[v / GL] = m;
+    }
+}
+
 // large groups: blocks stride their group and combine with an atomic max on the
 // bit pattern (non-negative floats order like their bits); mx pre-zeroed
 __global__ __launch_bounds__(kBlock) void absmax_blocks(const _Float16* __restrict__ x, Geom g,
@@ -705,7 +735,18 @@ extern "C" hipError_t ql_fp8_scales(const uint16_t* src, int rows, int cols, int
     QL_CHECK_ARG(src && scales);
     const _Float16* x = reinterpret_cast<const _Float16*>(src);
     const unsigned sblocks = qlh::blocks_for(g.n_groups, kBlock);
-    if (g.gs <= 8192) {
+    const bool vec = g.n % 8 == 0 && qlh::aligned16(src);
+    if (vec && (g.gs == 16 || g.gs == 32 || g.gs == 64 || g.gs == 128 || g.gs == 256 || g.gs == 512)) {
+        const unsigned blocks = qlh::blocks_for(g.n / 8, (long long)kAbsIters * kBlock);
+        switch (g.gs) {
+        case 16: hipLaunchKernelGGL(absmax_vec<2>, dim3(blocks), dim3(kBlock), 0, stream, x, g, mode, scales); break;
+        case 32: hipLaunchKernelGGL(absmax_vec<4>, dim3(blocks), dim3(kBlock), 0, stream, x, g, mode, scales); break;
+        case 64: hipLaunchKernelGGL(absmax_vec<8>, dim3(blocks), dim3(kBlock), 0, stream, x, g, mode, scales); break;
+        case 128: hipLaunchKernelGGL(absmax_vec<16>, dim3(blocks), dim3(kBlock), 0, stream, x, g, mode, scales); break;
+        case 256: hipLaunchKernelGGL(absmax_vec<32>, dim3(blocks), dim3(kBlock), 0, stream, x, g, mode, scales); break;
+        default: hipLaunchKernelGGL(absmax_vec<64>, dim3(blocks), dim3(kBlock), 0, stream, x, g, mode, scales); break;
+        }
+    } else if (g.gs <= 8192) {
         hipLaunchKernelGGL(absmax_wave, dim3(qlh::blocks_for(g.n_groups, kBlock / kWave)), dim3(kBlock),
                            0, stream, x, g, mode, scales);
     } else {

@@ -61,7 +61,10 @@ def same_f16(a, b):
     (1024, 1024, ql.QUANT_PER_GROUP, 128),     # the reference test's shape and grouping
     (1024, 1024, ql.QUANT_PER_CHANNEL, 0), (1024, 1024, ql.QUANT_PER_TENSOR, 0),
     (64, 256, ql.QUANT_PER_GROUP, 100), (3, 1000, ql.QUANT_PER_GROUP, 7), (5, 33, ql.QUANT_PER_CHANNEL, 0),
-    (4096, 4096, ql.QUANT_PER_TENSOR, 0)])      # one group larger than a wavefront pass
+    (4096, 4096, ql.QUANT_PER_TENSOR, 0),       # one group larger than a wavefront pass
+    # power-of-two groups take the vector scales pass: every lane count, a partial last group
+    (16, 512, ql.QUANT_PER_GROUP, 16), (5, 96, ql.QUANT_PER_GROUP, 32), (7, 64, ql.QUANT_PER_GROUP, 64),
+    (8, 1024, ql.QUANT_PER_GROUP, 256), (16, 512, ql.QUANT_PER_GROUP, 512), (3, 200, ql.QUANT_PER_GROUP, 128)])
 def test_fp8_codec_bit_exact(mode, fmt, rows, cols, gran, gs):
     x = to_f16_bits(uniform(rows + cols + gs, (rows, cols), -1.0, 1.0) *
                     np.float32(1.0 if fmt == ql.FP8_E4M3 else 300.0))
