@@ -187,7 +187,10 @@ def test_fp8_gemm_every_code(mode, fmt, M, gran):
     check_gemm(got, want, gemm_bound(a, w_deq, want), f"fp8 gemm codes fmt {fmt} mode {mode} M {M} gran {gran}")
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (64, 6144, 4096), (300, 512, 1000), (8192, 256, 512)])
+@pytest.mark.parametrize("M,N,K", [
+    (1, 4096, 4096), (64, 6144, 4096), (300, 512, 1000), (8192, 256, 512),
+    # few rows, odd widths
+    (2, 4096, 4096), (16, 14336, 4096), (7, 1024, 14336), (9, 480, 512), (5, 100, 256), (3, 512, 1000)])
 def test_gemm_f16_matches_oracle(M, N, K):
     a = to_f16_bits(normal(M + K, (M, K)))
     w = to_f16_bits(normal(N + K, (N, K), K ** -0.5))
