@@ -22,6 +22,7 @@
 // dequant multiplies by 1/scale.  Larger M dequantizes into a workspace with the
 // codec and runs the fp16 library GEMM.
 #include "ql_common.hpp"
+#include <type_traits>
 #include "quantlib_amd.h"
 
 #include <math.h>
@@ -92,6 +93,17 @@ __device__ __forceinline__ float2v dec_ocp2(uint32_t w) {
         return __builtin_amdgcn_cvt_pk_f32_fp8((int)w, HI);
     else
         return __builtin_amdgcn_cvt_pk_f32_bf8((int)w, HI);
+}
+
+// two codes (the low or high half of w) -> two binary16, exact (every E4M3 / E5M2
+// value is a binary16 value; the scale operand 1.0 leaves them as decoded)
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+template <int FMT, bool HI = false>
+__device__ __forceinline__ half2v dec_ocp2_h(uint32_t w) {
+    if constexpr (FMT == QL_FP8_E4M3)
+        return __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, HI);
+    else
+        return __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(w, 1.0f, HI);
 }
 
 // ---- scales ----------------------------------------------------------------------------
@@ -291,10 +303,36 @@ __device__ __forceinline__ uint32_t ref_special(uint32_t w) {
 // encoder only writes such a code for a NaN input) and the lane falls back to the
 // bitwise reference decode otherwise.  SCALED = false leaves the scale out (the
 // caller applies it to the accumulated products): every FP8 value is exact in
-// binary16, so the fragments then hold the decoded codes themselves.
+// binary16, so the fragments then hold the decoded codes themselves, converted
+// two at a time straight to binary16 (callers keep reference-mode E5M2, whose
+// exponent-31 codes exceed the binary16 range, on SCALED = true).
 template <int FMT, int MODE, bool SCALED>
 __device__ __forceinline__ void dequant16(uint4 codes, float inv, half8& lo, half8& hi) {
     const uint32_t w[4] = {codes.x, codes.y, codes.z, codes.w};
+    if constexpr (!SCALED) {
+        // straight to binary16: one conversion per two codes
+        half2v h[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            h[2 * j] = dec_ocp2_h<FMT>(w[j]);
+            h[2 * j + 1] = dec_ocp2_h<FMT, true>(w[j]);
+        }
+        if constexpr (MODE == QL_FP8_MODE_REFERENCE) {
+            const uint32_t special = (ref_special<FMT>(w[0]) | ref_special<FMT>(w[1]) | ref_special<FMT>(w[2]) |
+                                      ref_special<FMT>(w[3])) & 0x80808080u;
+            if (special) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    h[e >> 1][e & 1] = (_Float16)dec_ref<FMT>((w[e >> 2] >> (8 * (e & 3))) & 0xFFu);
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            lo[e] = h[e >> 1][e & 1];
+            hi[e] = h[4 + (e >> 1)][e & 1];
+        }
+        return;
+    }
     float f[16];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -315,8 +353,8 @@ __device__ __forceinline__ void dequant16(uint4 codes, float inv, half8& lo, hal
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        lo[e] = (_Float16)(SCALED ? f[e] * inv : f[e]);
-        hi[e] = (_Float16)(SCALED ? f[8 + e] * inv : f[8 + e]);
+        lo[e] = (_Float16)(f[e] * inv);
+        hi[e] = (_Float16)(f[8 + e] * inv);
     }
 }
 
@@ -581,6 +619,192 @@ __global__ __launch_bounds__(kBlock) void splitk_reduce(const float* __restrict_
     store<true>(reinterpret_cast<Vec<_Float16, 4>*>(C + i), o);
 }
 
+// ---- one token tile (M <= 16): whole-row weight loads -----------------------------------
+// Workgroup = RW x KW wavefronts over 16*RW weight rows and one K-split: wavefront
+// w owns row tile w % RW and every KW-th chunk of 256 codes from w / RW on.  One
+// load instruction covers 4 complete 256-byte row segments (16 lanes per row): that
+// shape streams the matrix markedly faster than 16 rows x 64 bytes.  Each chunk is
+// re-laid through a wavefront-private LDS tile (16-byte slots XOR-swizzled by row,
+// conflict-free both ways; LDS operations of one wavefront complete in order, so
+// no barrier) into MFMA fragments: lane (row l%16, q = l/16) takes piece p = 0..3
+// from slot 4p + q, i.e. codes 64p + 16q .. +15 of the chunk, and the token
+// fragments use the same k order, so MFMA pair p covers k = 64p .. 64p + 63 of the
+// chunk -- inside one scale group when the group length is a multiple of 64.
+// Token rows come through a buffer resource that ends at row M: lanes of tokens
+// past M read zeros without touching memory.  Scales: per tensor / per row applied
+// once to the sums; per group (length a multiple of 64, dividing K) one multiply-add
+// per output per piece with the inverse from the workgroup's LDS table.  The KW
+// partial tiles of a row tile are summed in LDS in wavefront order.
+constexpr int kRowsChunk = 256;
+#ifndef QL_ROWS_STAGES
+#define QL_ROWS_STAGES 2
+#endif
+constexpr int kRowsStages = QL_ROWS_STAGES;   // register ring depth (chunks in flight)
+constexpr int kRowsMaxTokens = 8;              // more tokens: the register path is faster
+constexpr int kRowsOcpWaves = 1024;            // wavefront budgets of the launch shape
+constexpr int kRowsRefWaves = 2048;
+constexpr int kRowsTableFloats = 4096;
+constexpr uint32_t kBufferWord3 = 0x00020000u;          // raw buffer, 32-bit dwords (gfx9)
+
+struct RowsStage {
+    u32x4 w[4];        // instruction i: row 4i + lane/16, bytes 16*(lane%16) .. of the chunk
+    half8 a[4][2];     // piece p: token k = 64p + 16q .. +7 and +8 .. +15 of the chunk
+};
+
+__device__ __forceinline__ void rows_load_w(RowsStage& st, const SkinnyArgs& p, const uint32_t (&woff)[4], int c) {
+    const uint32_t kb = (uint32_t)c * kRowsChunk;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st.w[i] = *reinterpret_cast<const u32x4*>(p.W + (woff[i] + kb));
+}
+
+__device__ __forceinline__ void rows_load_a(RowsStage& st, __amdgpu_buffer_rsrc_t ra, uint32_t aoff, int c) {
+    const uint32_t kb = 2u * (uint32_t)c * kRowsChunk;
+#pragma unroll
+    for (int pc = 0; pc < 4; ++pc) {
+        const u32x4 lo = __builtin_amdgcn_raw_buffer_load_b128(ra, aoff + kb + 128u * pc, 0, 0);
+        const u32x4 hi = __builtin_amdgcn_raw_buffer_load_b128(ra, aoff + kb + 128u * pc + 16u, 0, 0);
+        st.a[pc][0] = __builtin_bit_cast(half8, lo);
+        st.a[pc][1] = __builtin_bit_cast(half8, hi);
+    }
+}
+
+template <int FMT, int MODE, int SK, int RW, int KW>
+__global__ __launch_bounds__(RW * KW * kWave) void fp8_gemm_rows(SkinnyArgs p) {
+    constexpr int NW = RW * KW, NR = 16 * RW;
+    // the wavefront index in a scalar register: the chunk loop's branches are uniform
+    const int lane = threadIdx.x & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int rt = wave % RW, kp = wave / RW;
+    const int q = lane >> 4, r16 = lane & 15;
+    const int n0 = blockIdx.x * NR;
+    const int rbase = n0 + 16 * rt;
+    const int n_chunks = p.K / kRowsChunk;
+    const int c_begin = blockIdx.y * p.chunks_per_split;
+    const int c_end = min(n_chunks, c_begin + p.chunks_per_split);
+    uint32_t woff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) woff[i] = (uint32_t)(rbase + 4 * i + q) * (uint32_t)p.K + 16u * r16;
+    // byte offsets into the token rows; rows past M start at the resource's end
+    // (the host checks (M + 1) * K * 2 < 2^32)
+    const uint32_t a_bytes = 2u * (uint32_t)p.M * (uint32_t)p.K;
+    const uint32_t aoff = (r16 < p.M ? 2u * (uint32_t)r16 * (uint32_t)p.K : a_bytes) + 32u * q;
+    const __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(p.A), (short)0, (int)a_bytes, (int)kBufferWord3);
+
+    __shared__ u32x4 tile[NW][16][16];
+    __shared__ float table[SK == kScaleGroupFold ? kRowsTableFloats : 1];   // [group - g0][NR rows]
+    __shared__ floatx4 red[KW > 1 ? NW : 1][kWave];
+    int g0 = 0;
+    if constexpr (SK == kScaleGroupFold) {
+        const int gs = (int)p.gs;
+        g0 = c_begin * kRowsChunk / gs;
+        const int ng = (c_end * kRowsChunk - 1) / gs + 1 - g0;   // the host checks NR * ng fits
+        for (int i = threadIdx.x; i < NR * ng; i += NW * kWave) {
+            const int gg = i / NR, rr = i - NR * gg;
+            table[i] = 1.0f / p.scales[(n0 + rr) * p.groups_per_row + g0 + gg];
+        }
+        __syncthreads();
+    }
+
+    floatx4 acc = floatx4{};
+    // one chunk from stage st: re-lay, decode, multiply; with LOAD, the stage is
+    // refilled with chunk c_next (weights as soon as they are in LDS, tokens after
+    // the products)
+    auto step = [&](RowsStage& st, int c, int c_next, auto load) {
+        // re-lay the chunk: row 4i + q, slot r16 -> position r16 ^ row
+#pragma unroll
+        for (int i = 0; i < 4; ++i) tile[wave][4 * i + q][r16 ^ (4 * i + q)] = st.w[i];
+        if constexpr (decltype(load)::value) rows_load_w(st, p, woff, c_next);
+        // orders the compiler only: one wavefront's LDS operations execute in order
+        __builtin_amdgcn_wave_barrier();
+        const u32x4 codes4[4] = {tile[wave][r16][q ^ r16], tile[wave][r16][(4 + q) ^ r16],
+                                 tile[wave][r16][(8 + q) ^ r16], tile[wave][r16][(12 + q) ^ r16]};
+        __builtin_amdgcn_wave_barrier();
+        // pieces of one scale group (groups of 64 codes: every piece; 128: pairs;
+        // 256 and longer: the whole chunk) share one partial and one multiply-add
+        const int gp = SK == kScaleGroupFold ? min(4, (int)p.gs / 64) : 4;   // 1, 2 or 4 (gs % 64 == 0)
+        floatx4 part = floatx4{};
+#pragma unroll
+        for (int pc = 0; pc < 4; ++pc) {
+            const u32x4 cv = codes4[pc];
+            half8 wlo, whi;
+            dequant16<FMT, MODE, false>(uint4{cv[0], cv[1], cv[2], cv[3]}, 1.0f, wlo, whi);
+            if constexpr (SK == kScaleGroupFold) {
+                part = __builtin_amdgcn_mfma_f32_16x16x32_f16(wlo, st.a[pc][0], part, 0, 0, 0);
+                part = __builtin_amdgcn_mfma_f32_16x16x32_f16(whi, st.a[pc][1], part, 0, 0, 0);
+                if ((pc + 1) % gp == 0) {   // wave-uniform
+                    const int g = (c * kRowsChunk + 64 * pc) / (int)p.gs - g0;
+                    const float4 inv = *reinterpret_cast<const float4*>(table + g * NR + 16 * rt + 4 * q);
+                    acc[0] = fmaf(part[0], inv.x, acc[0]);
+                    acc[1] = fmaf(part[1], inv.y, acc[1]);
+                    acc[2] = fmaf(part[2], inv.z, acc[2]);
+                    acc[3] = fmaf(part[3], inv.w, acc[3]);
+                    part = floatx4{};
+                }
+            } else {
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(wlo, st.a[pc][0], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(whi, st.a[pc][1], acc, 0, 0, 0);
+            }
+        }
+        if constexpr (decltype(load)::value) rows_load_a(st, ra, aoff, c_next);
+    };
+    // ring of NS stages: stage s holds the wavefront's chunks s, s + NS, ...  Whole
+    // rounds refill every stage (loads past the last chunk repeat it: in bounds,
+    // never used, and the waits count every round's loads exactly); the remaining
+    // chunks are computed without refills.
+    constexpr int NS = kRowsStages;
+    const int first = c_begin + kp;   // wave-uniform
+    if (first < c_end) {
+        const int n_mine = (c_end - 1 - first) / KW + 1;
+        const int last = first + KW * (n_mine - 1);
+        RowsStage st[NS];
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            rows_load_w(st[s], p, woff, min(first + KW * s, last));
+            rows_load_a(st[s], ra, aoff, min(first + KW * s, last));
+        }
+        const int rounds = n_mine / NS;
+        int c = first;
+        for (int r = 0; r < rounds; ++r) {
+#pragma unroll
+            for (int s = 0; s < NS; ++s, c += KW) step(st[s], c, min(c + KW * NS, last), std::true_type{});
+        }
+#pragma unroll
+        for (int s = 0; s < NS - 1; ++s, c += KW)
+            if (s < n_mine - rounds * NS) step(st[s], c, 0, std::false_type{});
+    }
+    // lane holds C^T[rbase + 4q + i][token r16]; the KW wavefronts of a row tile
+    // are summed in order by the first
+    if constexpr (KW > 1) {
+        red[wave][lane] = acc;
+        __syncthreads();
+        if (kp != 0) return;
+#pragma unroll
+        for (int j = 1; j < KW; ++j) {
+            const floatx4 o = red[rt + RW * j][lane];
+            acc[0] += o[0];
+            acc[1] += o[1];
+            acc[2] += o[2];
+            acc[3] += o[3];
+        }
+    }
+    if constexpr (SK == kScaleTensor || SK == kScaleRow) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] *= 1.0f / scale_at<SK>(p, rbase + 4 * q + i, 0);
+    }
+    if (r16 < p.M) {
+        const size_t o = (size_t)r16 * p.N + rbase + 4 * q;
+        if (gridDim.y == 1) {
+            Vec<_Float16, 4> h;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) h.v[i] = from_f32<_Float16>(acc[i]);
+            *reinterpret_cast<Vec<_Float16, 4>*>(p.C + o) = h;
+        } else {
+            *reinterpret_cast<float4*>(p.part + (size_t)blockIdx.y * p.M * p.N + o) =
+                float4{acc[0], acc[1], acc[2], acc[3]};
+        }
+    }
+}
+
 // ---- host helpers ----------------------------------------------------------------------
 bool geom_for(int rows, int cols, int gran, int group_size, Geom& g) {
     if (rows < 0 || cols < 0) return false;
@@ -628,6 +852,7 @@ constexpr int kSkinnyTargetWgs = 256;
 
 struct SkinnyPlan {
     int mt, r, splits, chunks_per_split;
+    int rw = 0, kw = 0;   // whole-row path: row tiles per workgroup, wavefronts per row tile
 };
 
 SkinnyPlan skinny_plan(int M, int N, int K, size_t ws_bytes) {
@@ -691,6 +916,79 @@ void launch_skinny(const SkinnyArgs& a, const SkinnyPlan& pl, int kind, hipStrea
     if (pl.mt == 1) launch_skinny_mt<FMT, MODE, 1>(a, pl, kind, grid, st);
     else if (pl.mt == 2) launch_skinny_mt<FMT, MODE, 2>(a, pl, kind, grid, st);
     else launch_skinny_mt<FMT, MODE, 4>(a, pl, kind, grid, st);
+}
+
+// Whole-row path for one token tile: chunks of 256 codes, scales per tensor, per
+// row or per group of a multiple of 64 codes dividing K (the group table of a split
+// must fit LDS).  It multiplies decoded codes and scales the sums, so
+// reference-mode E5M2 (whose exponent-31 codes decode beyond the binary16 range)
+// stays on the register path.
+int rows_kind(const Geom& g, int M, int N, int K, int format, int mode) {
+    if (M > kRowsMaxTokens || N % 16 || K % kRowsChunk || (format == QL_FP8_E5M2 && mode == QL_FP8_MODE_REFERENCE) ||
+        (uint64_t)(M + 1) * (uint64_t)K * 2u >= (1ull << 32))
+        return -1;
+    if (g.n_groups == 1) return kScaleTensor;
+    if (g.gs == K) return kScaleRow;
+    if (K % g.gs || g.gs % 64) return -1;
+    return kScaleGroupFold;
+}
+
+// Shape of the whole-row launch: KW (wavefronts sharing a row tile, splitting its
+// chunks) is the largest of 1, 2, 4, 8 that keeps N/16 * KW wavefronts within
+// max_waves and gives every wavefront at least a ring of chunks; RW = 4 / KW row
+// tiles per workgroup (1 for KW >= 4), lowered until N divides.  K-splits over
+// launches (fp32 partials + splitk_reduce) only when KW = 8 leaves the chip
+// short of wavefronts.  Measured on MI355X with weights streamed from HBM:
+// about 1024 wavefronts suit the OCP decode, about 2048 the reference-mode decode
+// (its check of every code needs more wavefronts to hide).
+SkinnyPlan rows_plan(int M, int N, int K, int mode, size_t ws_bytes) {
+    const int max_waves = mode == QL_FP8_MODE_REFERENCE ? kRowsRefWaves : kRowsOcpWaves;
+    SkinnyPlan s;
+    const int tiles = N / 16;
+    const int n_chunks = K / kRowsChunk;
+    s.kw = 1;
+    while (s.kw < 8 && tiles * 2 * s.kw <= max_waves && n_chunks / (2 * s.kw) >= kRowsStages) s.kw *= 2;
+    s.rw = s.kw >= 4 ? 1 : 4 / s.kw;
+    while (tiles % s.rw) s.rw /= 2;
+    s.mt = 1;
+    s.r = s.rw;
+    int splits = 1;
+    if (s.kw == 8 && tiles * 16 <= max_waves)
+        splits = std::min(max_waves / (tiles * 8), std::max(1, n_chunks / (8 * kRowsStages)));
+    while (splits > 1 && (size_t)splits * (size_t)M * (size_t)N * sizeof(float) > ws_bytes) --splits;
+    s.chunks_per_split = (n_chunks + splits - 1) / splits;
+    s.splits = (n_chunks + s.chunks_per_split - 1) / s.chunks_per_split;
+    return s;
+}
+
+// largest number of scale groups one K-split of the plan touches
+int rows_groups_per_split(const SkinnyPlan& pl, int K, long long gs) {
+    const int n_chunks = K / kRowsChunk;
+    int ng_max = 0;
+    for (int s = 0; s < pl.splits; ++s) {
+        const int cb = s * pl.chunks_per_split, ce = std::min(n_chunks, cb + pl.chunks_per_split);
+        ng_max = std::max(ng_max, (int)((ce * (long long)kRowsChunk - 1) / gs + 1 - cb * (long long)kRowsChunk / gs));
+    }
+    return ng_max;
+}
+
+template <int FMT, int MODE, int RW, int KW>
+void launch_rows_shape(const SkinnyArgs& a, const SkinnyPlan& pl, int kind, hipStream_t st) {
+    const dim3 grid((unsigned)(a.N / (16 * RW)), (unsigned)pl.splits), block(RW * KW * kWave);
+    if (kind == kScaleTensor) hipLaunchKernelGGL((fp8_gemm_rows<FMT, MODE, kScaleTensor, RW, KW>), grid, block, 0, st, a);
+    else if (kind == kScaleRow) hipLaunchKernelGGL((fp8_gemm_rows<FMT, MODE, kScaleRow, RW, KW>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((fp8_gemm_rows<FMT, MODE, kScaleGroupFold, RW, KW>), grid, block, 0, st, a);
+}
+
+template <int FMT, int MODE>
+void launch_rows(const SkinnyArgs& a, const SkinnyPlan& pl, int kind, hipStream_t st) {
+    if (pl.kw == 8) launch_rows_shape<FMT, MODE, 1, 8>(a, pl, kind, st);
+    else if (pl.kw == 4) launch_rows_shape<FMT, MODE, 1, 4>(a, pl, kind, st);
+    else if (pl.kw == 2 && pl.rw == 2) launch_rows_shape<FMT, MODE, 2, 2>(a, pl, kind, st);
+    else if (pl.kw == 2) launch_rows_shape<FMT, MODE, 1, 2>(a, pl, kind, st);
+    else if (pl.rw == 4) launch_rows_shape<FMT, MODE, 4, 1>(a, pl, kind, st);
+    else if (pl.rw == 2) launch_rows_shape<FMT, MODE, 2, 1>(a, pl, kind, st);
+    else launch_rows_shape<FMT, MODE, 1, 1>(a, pl, kind, st);
 }
 
 // the register path addresses W and A with 32-bit byte offsets
@@ -798,8 +1096,14 @@ extern "C" hipError_t ql_fp8_gemm_workspace_size(int M, int N, int K, int granul
     *bytes = 0;
     if (M == 0 || N == 0 || K == 0) return hipSuccess;
     if (skinny_ok(M, N, K, g)) {
+        // the format and mode only narrow the whole-row path's group case; the
+        // reservation covers either path
         const SkinnyPlan pl = skinny_plan(M, N, K, SIZE_MAX);
-        *bytes = pl.splits > 1 ? (size_t)pl.splits * (size_t)M * (size_t)N * sizeof(float) : 0;
+        size_t splits = (size_t)pl.splits;
+        if (rows_kind(g, M, N, K, QL_FP8_E4M3, QL_FP8_MODE_OCP) >= 0)
+            for (int mode : {QL_FP8_MODE_REFERENCE, QL_FP8_MODE_OCP})
+                splits = std::max(splits, (size_t)rows_plan(M, N, K, mode, SIZE_MAX).splits);
+        *bytes = splits > 1 ? splits * (size_t)M * (size_t)N * sizeof(float) : 0;
     } else {
         *bytes = (size_t)N * (size_t)K * sizeof(uint16_t);
     }
@@ -817,7 +1121,13 @@ extern "C" hipError_t ql_fp8_gemm_f16(const uint16_t* A, const uint8_t* W, const
     QL_CHECK_ARG(A && W && scales && C && K > 0);
     if (skinny_ok(M, N, K, g) && qlh::aligned16(A) && qlh::aligned16(W)) {
         const bool ws_ok = workspace && qlh::aligned16(workspace) && ((uintptr_t)C & 7) == 0;
-        const SkinnyPlan pl = skinny_plan(M, N, K, ws_ok ? workspace_bytes : 0);
+        const size_t ws = ws_ok ? workspace_bytes : 0;
+        int rkind = rows_kind(g, M, N, K, format, mode);
+        SkinnyPlan pl = rkind >= 0 ? rows_plan(M, N, K, mode, ws) : skinny_plan(M, N, K, ws);
+        if (rkind == kScaleGroupFold && 16LL * pl.rw * rows_groups_per_split(pl, K, g.gs) > kRowsTableFloats) {
+            rkind = -1;
+            pl = skinny_plan(M, N, K, ws);
+        }
         SkinnyArgs a;
         a.A = reinterpret_cast<const char*>(A);
         a.W = reinterpret_cast<const char*>(W);
@@ -832,7 +1142,10 @@ extern "C" hipError_t ql_fp8_gemm_f16(const uint16_t* A, const uint8_t* W, const
         a.groups_per_row = K % g.gs == 0 ? (int)(K / g.gs) : 0;
         a.g_step = (int)(256 / g.gs);
         a.r_step = (int)(256 % g.gs);
-        QL_FP8_DISPATCH(format, mode, launch_skinny, a, pl, scale_kind(g, K, pl, format, mode), stream);
+        if (rkind >= 0)
+            QL_FP8_DISPATCH(format, mode, launch_rows, a, pl, rkind, stream);
+        else
+            QL_FP8_DISPATCH(format, mode, launch_skinny, a, pl, scale_kind(g, K, pl, format, mode), stream);
         if (pl.splits > 1) {
             const long long mn = (long long)M * N;
             hipLaunchKernelGGL(splitk_reduce, dim3(qlh::blocks_for(mn / 4, kBlock)), dim3(kBlock), 0, stream,

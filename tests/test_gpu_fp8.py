@@ -136,10 +136,21 @@ GEMM_CASES = [
     (8, 256, 4096, ql.QUANT_PER_GROUP, 16),        # unsplit: too many groups for the LDS table
     (64, 1024, 8192, ql.QUANT_PER_GROUP, 16),
     (20, 512, 1024, ql.QUANT_PER_CHANNEL, 0),      # two token tiles, four row tiles
-    (3, 480, 512, ql.QUANT_PER_GROUP, 64),         # one token tile, two row tiles
-    (5, 208, 256, ql.QUANT_PER_TENSOR, 0),         # one token tile, one row tile
+    (3, 480, 448, ql.QUANT_PER_GROUP, 64),         # one token tile, two row tiles
+    (5, 208, 320, ql.QUANT_PER_TENSOR, 0),         # one token tile, one row tile
     (30, 480, 512, ql.QUANT_PER_CHANNEL, 0),       # two token tiles, two row tiles
-    (40, 208, 512, ql.QUANT_PER_GROUP, 64)]        # four token tiles, one row tile
+    (40, 208, 512, ql.QUANT_PER_GROUP, 64),        # four token tiles, one row tile
+    # at most 8 tokens and K a multiple of 256: whole-row loads
+    (4, 1024, 512, ql.QUANT_PER_GROUP, 128),       # 4 row tiles per workgroup, one wavefront each
+    (8, 480, 512, ql.QUANT_PER_CHANNEL, 0),        # 30 row tiles: 2 per workgroup
+    (5, 208, 256, ql.QUANT_PER_TENSOR, 0),         # 13 row tiles: 1 per workgroup, one chunk
+    (1, 512, 768, ql.QUANT_PER_CHANNEL, 0),        # 3 chunks: a ring round and a remainder
+    (8, 512, 1024, ql.QUANT_PER_GROUP, 256),       # 2 wavefronts per row tile
+    (2, 256, 2048, ql.QUANT_PER_GROUP, 64),        # 4 wavefronts per row tile
+    (3, 512, 4096, ql.QUANT_PER_GROUP, 512),       # 8 wavefronts per row tile
+    (2, 256, 8192, ql.QUANT_PER_TENSOR, 0),        # 8 wavefronts per row tile and K-splits
+    (1, 64, 32768, ql.QUANT_PER_GROUP, 64),        # without a workspace: group table too large
+    (7, 1536, 1280, ql.QUANT_PER_GROUP, 128)]      # 5 chunks over 2 wavefronts
 
 
 @pytest.mark.parametrize("mode", MODES)
@@ -165,7 +176,8 @@ def test_fp8_gemm_matches_oracle(mode, fmt, M, N, K, gran, gs):
 
 @pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize("fmt", FMTS)
-@pytest.mark.parametrize("M,gran", [(1, ql.QUANT_PER_GROUP), (64, ql.QUANT_PER_GROUP), (5, ql.QUANT_PER_CHANNEL)])
+@pytest.mark.parametrize("M,gran", [(1, ql.QUANT_PER_GROUP), (12, ql.QUANT_PER_GROUP), (64, ql.QUANT_PER_GROUP),
+                                    (5, ql.QUANT_PER_CHANNEL)])
 def test_fp8_gemm_every_code(mode, fmt, M, gran):
     # raw codes, not encoder output: every byte appears in every 16-code run of some
     # rows, including the codes whose reference decode is not the OCP one (exponent 0
