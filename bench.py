@@ -449,8 +449,12 @@ def layer_rows(ql, np, chain, reps):
             w8[k] = (codes, scales)
         fp8_sets.append(w8)
         fw = {k: ql.FP8Weight(c.ptr, sc.ptr) for k, (c, sc) in w8.items()}
+        # static weights: decode as QL_FP8_MODE_REFERENCE_CLEAN when the scan finds
+        # none of the codes whose reference decode differs (same results)
+        dmode = ql.FP8_MODE_REFERENCE_CLEAN if all(
+            ref_special_count(ql, np, w8[k][0], n_ * k_, fmt, st) == 0 for k, (n_, k_) in shapes.items()) else mode
         lw8.append(ql.LayerWeightsFP8(norm.ptr, fw["wqkv"], fw["wo"], norm.ptr, fw["w_gate"], fw["w_up"],
-                                      fw["w_down"], fmt, gran, gs, mode))
+                                      fw["w_down"], fmt, gran, gs, dmode))
     ql.synchronize()
     dims = ql.LayerDims(D, HQ, HKV, HD, F, THETA, EPS, ql.ROPE_HALF)
     rows = []
@@ -485,8 +489,10 @@ def layer_rows(ql, np, chain, reps):
         ql.call("ql_engine_create_fp8", ctypes.byref(dims), n_rows, S, C, gran, gs, ctypes.byref(eng))
         x = up(r.standard_normal((n_rows, D), dtype=np.float32).astype(np.float16).view(np.uint16))
         deltas = [ql.DeviceArray((n_rows, D), np.uint16) for _ in range(2)]
+        fp8_kind = "fp8 e4m3 g128" + (" (reference codes, checked clean)"
+                                      if lw8[0].mode == ql.FP8_MODE_REFERENCE_CLEAN else "")
         for kind, fn, lws, wb in (("fp16", "ql_engine_layer_f16", lw16, 2 * w_bytes),
-                                  ("fp8 e4m3 g128", "ql_engine_layer_fp8", lw8, w_bytes + 4 * w_bytes // gs)):
+                                  (fp8_kind, "ql_engine_layer_fp8", lw8, w_bytes + 4 * w_bytes // gs)):
             def launch(i, fn=fn, lws=lws):
                 ql.call(fn, eng, ctypes.byref(lws[i % len(lws)]), i % L_POOL, x.ptr,
                         deltas[(i + 1) % 2].ptr if i else None, deltas[i % 2].ptr, ctypes.byref(sd), st)
@@ -541,6 +547,14 @@ def layer_rows(ql, np, chain, reps):
     return rows
 
 
+def ref_special_count(ql, np, codes, n, fmt, st):
+    """ql_fp8_count_ref_special of n codes (device), read back."""
+    cnt = ql.DeviceArray((1,), np.uint64)
+    ql.call("ql_fp8_count_ref_special", codes.ptr, n, fmt, cnt.ptr, st)
+    ql.synchronize()
+    return int(cnt.numpy()[0])
+
+
 def fp8_rows(ql, np, reps):
     """The FP8 weight path on Llama-3-8B FFN shapes: the skinny FP8-weight GEMM
     (ql_fp8_gemm_f16) at decode row counts next to the fp16 library GEMM on the
@@ -578,12 +592,17 @@ def fp8_rows(ql, np, reps):
                          max(6, reps // 5))
             for fmt, gran, gs, mode, label in (
                     (ql.FP8_E4M3, ql.QUANT_PER_GROUP, 128, ql.FP8_MODE_REFERENCE, "e4m3 g128 reference codec"),
+                    (ql.FP8_E4M3, ql.QUANT_PER_GROUP, 128, ql.FP8_MODE_REFERENCE_CLEAN,
+                     "e4m3 g128 reference codes, checked clean"),
                     (ql.FP8_E4M3, ql.QUANT_PER_CHANNEL, 0, ql.FP8_MODE_OCP, "e4m3 per-channel OCP")):
                 n_sc = N * K // 128 if gs else N
                 codes = [(ql.DeviceArray((N * K,), np.uint8), ql.DeviceArray((n_sc,), np.float32))
                          for _ in range(rotating(N * K))]
+                qmode = ql.FP8_MODE_REFERENCE if mode == ql.FP8_MODE_REFERENCE_CLEAN else mode
                 for i, (c, sc) in enumerate(codes):
-                    ql.call("ql_fp8_quantize", d16[i % len(d16)].ptr, N, K, fmt, gran, gs, mode, c.ptr, sc.ptr, st)
+                    ql.call("ql_fp8_quantize", d16[i % len(d16)].ptr, N, K, fmt, gran, gs, qmode, c.ptr, sc.ptr, st)
+                if mode == ql.FP8_MODE_REFERENCE_CLEAN:
+                    assert all(ref_special_count(ql, np, c, N * K, fmt, st) == 0 for c, _ in codes)
                 size = ctypes.c_size_t()
                 ql.call("ql_fp8_gemm_workspace_size", M, N, K, gran, gs, ctypes.byref(size))
                 ws = ql.DeviceArray((max(size.value, 16),), np.uint8)

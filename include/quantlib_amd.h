@@ -379,6 +379,15 @@ hipError_t ql_gemm_f16(const uint16_t* x, const uint16_t* w, uint16_t* y, int M,
 #define QL_FP8_E5M2 1
 #define QL_FP8_MODE_REFERENCE 0
 #define QL_FP8_MODE_OCP 1
+/* Decoding only (ql_fp8_dequantize, ql_fp8_gemm_f16, the FP8 engine layers):
+ * reference-mode codes that ql_fp8_count_ref_special found free of the codes whose
+ * reference decode differs from the OCP decode (the reference encoder writes them
+ * only for NaN inputs).  Such codes decode to the same values either way (0x80:
+ * -0 against the reference's +0, which no product or sum sees), so the GEMM skips
+ * the per-code check of QL_FP8_MODE_REFERENCE and gives its results;
+ * ql_fp8_dequantize runs the reference decoder as for QL_FP8_MODE_REFERENCE.  No
+ * counterpart in the reference: for callers that hold static weights. */
+#define QL_FP8_MODE_REFERENCE_CLEAN 2
 #define QL_QUANT_PER_TENSOR 0    /* QuantGranularity values of quant_types.h:17-21 */
 #define QL_QUANT_PER_CHANNEL 1
 #define QL_QUANT_PER_GROUP 2
@@ -394,6 +403,12 @@ hipError_t ql_fp8_quantize(const uint16_t* src, int rows, int cols, int format, 
 hipError_t ql_fp8_dequantize(const uint8_t* src, const float* scales, int rows, int cols,
                              int format, int granularity, int group_size, int mode,
                              uint16_t* dst, hipStream_t stream);
+/* *count (device) = the number of the n codes (16-byte aligned) whose reference decode
+ * differs from the OCP decode: E4M3 exponent 0 with a mantissa and |code| 0x7F, E5M2
+ * exponent 0 with a mantissa and exponent 31.  Zero: the codes may be decoded with
+ * QL_FP8_MODE_REFERENCE_CLEAN.  No counterpart in the reference. */
+hipError_t ql_fp8_count_ref_special(const uint8_t* codes, size_t n, int format,
+                                    unsigned long long* count, hipStream_t stream);
 /* C[M, N] = A[M, K] (dequant W[N, K])^T, fp32 accumulation, fp16 out
  * (quantlib_src/kernels/fp8_gemm.cu:34-139, quantlib_fp8_gemm).  M <= 64 with
  * N % 16 == 0, K % 64 == 0, 16 | group length and 16-byte aligned A and W streams W

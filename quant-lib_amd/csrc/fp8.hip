@@ -641,8 +641,17 @@ constexpr int kRowsChunk = 256;
 #endif
 constexpr int kRowsStages = QL_ROWS_STAGES;   // register ring depth (chunks in flight)
 constexpr int kRowsMaxTokens = 8;              // more tokens: the register path is faster
-constexpr int kRowsOcpWaves = 1024;            // wavefront budgets of the launch shape
-constexpr int kRowsRefWaves = 2048;
+#ifndef QL_ROWS_CONTIG
+#define QL_ROWS_CONTIG 1
+#endif
+#ifndef QL_ROWS_OCP_WAVES
+#define QL_ROWS_OCP_WAVES 1024
+#endif
+#ifndef QL_ROWS_REF_WAVES
+#define QL_ROWS_REF_WAVES 2048
+#endif
+constexpr int kRowsOcpWaves = QL_ROWS_OCP_WAVES;   // wavefront budgets of the launch shape
+constexpr int kRowsRefWaves = QL_ROWS_REF_WAVES;
 constexpr int kRowsTableFloats = 4096;
 constexpr uint32_t kBufferWord3 = 0x00020000u;          // raw buffer, 32-bit dwords (gfx9)
 
@@ -752,24 +761,34 @@ __global__ __launch_bounds__(RW * KW * kWave) void fp8_gemm_rows(SkinnyArgs p) {
     // never used, and the waits count every round's loads exactly); the remaining
     // chunks are computed without refills.
     constexpr int NS = kRowsStages;
-    const int first = c_begin + kp;   // wave-uniform
-    if (first < c_end) {
-        const int n_mine = (c_end - 1 - first) / KW + 1;
-        const int last = first + KW * (n_mine - 1);
+#if QL_ROWS_CONTIG
+    // wavefront kp of a row tile takes the kp-th contiguous run of the split's chunks
+    constexpr int CS = 1;
+    const int per_w = (c_end - c_begin + KW - 1) / KW;
+    const int first = c_begin + kp * per_w;   // wave-uniform
+    const int w_end = min(c_end, first + per_w);
+#else
+    constexpr int CS = KW;
+    const int first = c_begin + kp;           // wave-uniform
+    const int w_end = c_end;
+#endif
+    if (first < w_end) {
+        const int n_mine = (w_end - 1 - first) / CS + 1;
+        const int last = first + CS * (n_mine - 1);
         RowsStage st[NS];
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-            rows_load_w(st[s], p, woff, min(first + KW * s, last));
-            rows_load_a(st[s], ra, aoff, min(first + KW * s, last));
+            rows_load_w(st[s], p, woff, min(first + CS * s, last));
+            rows_load_a(st[s], ra, aoff, min(first + CS * s, last));
         }
         const int rounds = n_mine / NS;
         int c = first;
         for (int r = 0; r < rounds; ++r) {
 #pragma unroll
-            for (int s = 0; s < NS; ++s, c += KW) step(st[s], c, min(c + KW * NS, last), std::true_type{});
+            for (int s = 0; s < NS; ++s, c += CS) step(st[s], c, min(c + CS * NS, last), std::true_type{});
         }
 #pragma unroll
-        for (int s = 0; s < NS - 1; ++s, c += KW)
+        for (int s = 0; s < NS - 1; ++s, c += CS)
             if (s < n_mine - rounds * NS) step(st[s], c, 0, std::false_type{});
     }
     // lane holds C^T[rbase + 4q + i][token r16]; the KW wavefronts of a row tile
@@ -1014,6 +1033,36 @@ bool fmt_mode_ok(int fmt, int mode) {
            (mode == QL_FP8_MODE_REFERENCE || mode == QL_FP8_MODE_OCP);
 }
 
+// decoding entries also take QL_FP8_MODE_REFERENCE_CLEAN: codes without any of the
+// codes whose reference decode differs decode to the same values with the OCP
+// decode (up to the sign of zero for 0x80, which no product or sum sees)
+bool decode_mode_ok(int fmt, int mode) {
+    return fmt_mode_ok(fmt, mode) || ((fmt == QL_FP8_E4M3 || fmt == QL_FP8_E5M2) && mode == QL_FP8_MODE_REFERENCE_CLEAN);
+}
+int decode_mode(int mode) { return mode == QL_FP8_MODE_REFERENCE_CLEAN ? QL_FP8_MODE_OCP : mode; }
+
+// number of codes (16 per thread per step) whose reference decode differs from the
+// OCP decode; one 64-bit atomic add per wavefront
+template <int FMT>
+__global__ __launch_bounds__(kBlock) void count_ref_special(const uint8_t* __restrict__ q, size_t n,
+                                                           unsigned long long* __restrict__ count) {
+    const size_t n16 = n / 16;
+    const size_t stride = (size_t)gridDim.x * kBlock;
+    unsigned c = 0;
+    for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < n16; i += stride) {
+        const uint4 v = reinterpret_cast<const uint4*>(q)[i];
+        c += __popc(ref_special<FMT>(v.x) & 0x80808080u) + __popc(ref_special<FMT>(v.y) & 0x80808080u) +
+             __popc(ref_special<FMT>(v.z) & 0x80808080u) + __popc(ref_special<FMT>(v.w) & 0x80808080u);
+    }
+    if (blockIdx.x == 0 && threadIdx.x < n - 16 * n16)   // the last n % 16 codes
+        c += __popc(ref_special<FMT>(q[16 * n16 + threadIdx.x]) & 0x80u);
+#pragma unroll
+    for (int o = kWave / 2; o > 0; o >>= 1) c += __shfl_xor(c, o, kWave);
+    if ((threadIdx.x & (kWave - 1)) == 0 && c) atomicAdd(count, (unsigned long long)c);
+}
+
+__global__ void clear_u64(unsigned long long* p) { *p = 0; }
+
 }  // namespace
 
 extern "C" hipError_t ql_fp8_num_scales(int rows, int cols, int granularity, int group_size,
@@ -1080,9 +1129,11 @@ extern "C" hipError_t ql_fp8_dequantize(const uint8_t* src, const float* scales,
                                         int format, int granularity, int group_size, int mode,
                                         uint16_t* dst, hipStream_t stream) {
     Geom g;
-    QL_CHECK_ARG(fmt_mode_ok(format, mode) && geom_for(rows, cols, granularity, group_size, g));
+    QL_CHECK_ARG(decode_mode_ok(format, mode) && geom_for(rows, cols, granularity, group_size, g));
     if (g.n == 0) return hipSuccess;
     QL_CHECK_ARG(src && scales && dst);
+    // the reference's decoder throughout (its +0 for code 0x80 included): cheap here
+    if (mode == QL_FP8_MODE_REFERENCE_CLEAN) mode = QL_FP8_MODE_REFERENCE;
     const bool vec = g.n % 8 == 0 && g.gs % 8 == 0 && qlh::aligned16(dst) && ((uintptr_t)src & 7) == 0;
     QL_FP8_DISPATCH(format, mode, launch_dequantize, src, g, scales, reinterpret_cast<_Float16*>(dst),
                     vec, stream);
@@ -1115,10 +1166,11 @@ extern "C" hipError_t ql_fp8_gemm_f16(const uint16_t* A, const uint8_t* W, const
                                       int group_size, int mode, uint16_t* C, void* workspace,
                                       size_t workspace_bytes, hipStream_t stream) {
     Geom g;
-    QL_CHECK_ARG(fmt_mode_ok(format, mode) && M >= 0 && N >= 0 && K >= 0);
+    QL_CHECK_ARG(decode_mode_ok(format, mode) && M >= 0 && N >= 0 && K >= 0);
     QL_CHECK_ARG(geom_for(N, K, granularity, group_size, g));
     if (M == 0 || N == 0) return hipSuccess;
     QL_CHECK_ARG(A && W && scales && C && K > 0);
+    mode = decode_mode(mode);
     if (skinny_ok(M, N, K, g) && qlh::aligned16(A) && qlh::aligned16(W)) {
         const bool ws_ok = workspace && qlh::aligned16(workspace) && ((uintptr_t)C & 7) == 0;
         const size_t ws = ws_ok ? workspace_bytes : 0;
@@ -1160,4 +1212,18 @@ extern "C" hipError_t ql_fp8_gemm_f16(const uint16_t* A, const uint8_t* W, const
     const hipError_t e = ql_fp8_dequantize(W, scales, N, K, format, granularity, group_size, mode, wf, stream);
     if (e != hipSuccess) return e;
     return ql_gemm_f16(A, wf, C, M, N, K, stream);
+}
+
+extern "C" hipError_t ql_fp8_count_ref_special(const uint8_t* codes, size_t n, int format,
+                                               unsigned long long* count, hipStream_t stream) {
+    QL_CHECK_ARG((format == QL_FP8_E4M3 || format == QL_FP8_E5M2) && count);
+    QL_CHECK_ARG(n == 0 || (codes && qlh::aligned16(codes)));
+    hipLaunchKernelGGL(clear_u64, dim3(1), dim3(1), 0, stream, count);
+    if (n == 0) return hipGetLastError();
+    const unsigned blocks = (unsigned)std::max<size_t>(1, std::min<size_t>(2048, (n / 16 + kBlock - 1) / kBlock));
+    if (format == QL_FP8_E4M3)
+        hipLaunchKernelGGL(count_ref_special<QL_FP8_E4M3>, dim3(blocks), dim3(kBlock), 0, stream, codes, n, count);
+    else
+        hipLaunchKernelGGL(count_ref_special<QL_FP8_E5M2>, dim3(blocks), dim3(kBlock), 0, stream, codes, n, count);
+    return hipGetLastError();
 }

@@ -78,6 +78,7 @@ SIGNATURES = {
     "ql_fp8_dequantize": [_p, _p, _i, _i, _i, _i, _i, _i, _p, _p],
     "ql_fp8_gemm_workspace_size": [_i, _i, _i, _i, _i, _p],
     "ql_fp8_gemm_f16": [_p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p, _p, ctypes.c_size_t, _p],
+    "ql_fp8_count_ref_special": [_p, ctypes.c_size_t, _i, _p, _p],
     "ql_engine_create": [_p, _i, _i, _i, _p],
     "ql_engine_destroy": [_p],
     "ql_engine_layer_f16": [_p, _p, _i, _p, _p, _p, _p, _p],
@@ -95,7 +96,7 @@ SIGNATURES = {
 HIP_SUCCESS = 0
 HIP_ERROR_INVALID_VALUE = 1
 FP8_E4M3, FP8_E5M2 = 0, 1
-FP8_MODE_REFERENCE, FP8_MODE_OCP = 0, 1
+FP8_MODE_REFERENCE, FP8_MODE_OCP, FP8_MODE_REFERENCE_CLEAN = 0, 1, 2
 QUANT_PER_TENSOR, QUANT_PER_CHANNEL, QUANT_PER_GROUP = 0, 1, 2
 
 

@@ -155,6 +155,13 @@ P = 4096  # a non-null, 16-byte aligned dummy address: never dereferenced on the
     (("ql_fp8_quantize", P, 4, 64, 0, 2, 0, 0, P, P, None), INVALID),
     (("ql_fp8_quantize", None, 0, 64, 0, 2, 128, 0, None, None, None), 0),
     (("ql_fp8_dequantize", P, None, 4, 64, 0, 2, 128, 1, P, None), INVALID),
+    (("ql_fp8_dequantize", P, P, 4, 64, 0, 2, 128, 3, P, None), INVALID),      # no mode 3
+    (("ql_fp8_quantize", P, 4, 64, 0, 2, 128, 2, P, P, None), INVALID),        # clean: decode only
+    (("ql_fp8_scales", P, 4, 64, 0, 2, 128, 2, P, None), INVALID),
+    (("ql_fp8_count_ref_special", P, 64, 2, P, None), INVALID),                 # format
+    (("ql_fp8_count_ref_special", P, 64, 0, None, None), INVALID),              # no count
+    (("ql_fp8_count_ref_special", P + 8, 64, 0, P, None), INVALID),             # unaligned codes
+    (("ql_fp8_count_ref_special", None, 64, 0, P, None), INVALID),
     (("ql_engine_create_fp8", None, 16, 4, 64, 2, 128, P), INVALID),
     (("ql_engine_layer_fp8", None, P, 0, P, None, P, P, None), INVALID),
     (("ql_graph_begin", None), INVALID),
@@ -163,6 +170,8 @@ P = 4096  # a non-null, 16-byte aligned dummy address: never dereferenced on the
     (("ql_graph_destroy", None), 0),
     (("ql_fp8_gemm_f16", P, P, P, 100, 64, 64, 0, 2, 128, 1, P, None, 0, None), INVALID),
     (("ql_fp8_gemm_f16", None, None, None, 0, 64, 64, 0, 2, 128, 1, None, None, 0, None), 0),
+    (("ql_fp8_gemm_f16", None, None, None, 0, 64, 64, 1, 2, 128, 2, None, None, 0, None), 0),
+    (("ql_fp8_gemm_f16", P, P, P, 4, 64, 64, 0, 2, 128, 3, P, None, 0, None), INVALID),
     (("ql_gemm_f16", P, P, P, -1, 4, 4, None), INVALID),
     (("ql_gemm_f16", None, None, None, 0, 4, 4, None), 0),
 ])

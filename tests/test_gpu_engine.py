@@ -179,18 +179,25 @@ MATS = ("wqkv", "wo", "w_gate", "w_up", "w_down")
     # the reference's quantize_model: E4M3, groups of 128, its own codec; a 58-row prefill
     (ql.FP8_E4M3, ql.QUANT_PER_GROUP, 128, ql.FP8_MODE_REFERENCE, {0: 20, 1: 33, 2: 5}),
     # per-channel OCP codes; a 100-row prefill takes the dequantize + library GEMM path
-    (ql.FP8_E4M3, ql.QUANT_PER_CHANNEL, 0, ql.FP8_MODE_OCP, {0: 70, 1: 30})])
+    (ql.FP8_E4M3, ql.QUANT_PER_CHANNEL, 0, ql.FP8_MODE_OCP, {0: 70, 1: 30}),
+    # reference codes checked free of the codes whose reference decode differs
+    (ql.FP8_E4M3, ql.QUANT_PER_GROUP, 128, ql.FP8_MODE_REFERENCE_CLEAN, {0: 9, 1: 4})])
 def test_engine_fp8_layers_match_oracle(fmt, gran, gs, mode, prompts):
     L = 2
     src = [layer_weights(100 * (l + 1)) for l in range(L)]
+    qmode = ql.FP8_MODE_REFERENCE if mode == ql.FP8_MODE_REFERENCE_CLEAN else mode
+    count = empty((1,), np.uint64)
     deq, keep, lw = [], [], []
     for w in src:
         d = dict(w)
         fw = {}
         for k in MATS:
-            q, sc = orc.fp8_quantize(w[k], fmt, gran, gs, mode)
-            d[k] = orc.fp8_dequantize(q, sc, fmt, gran, gs, mode)
+            q, sc = orc.fp8_quantize(w[k], fmt, gran, gs, qmode)
+            d[k] = orc.fp8_dequantize(q, sc, fmt, gran, gs, qmode)
             dq, ds = dev(q), dev(sc)
+            if mode == ql.FP8_MODE_REFERENCE_CLEAN:
+                ql.call("ql_fp8_count_ref_special", dq.ptr, q.size, fmt, count.ptr, stream())
+                assert int(host(count)[0]) == 0
             keep += [dq, ds]
             fw[k] = ql.FP8Weight(dq.ptr, ds.ptr)
         deq.append(d)

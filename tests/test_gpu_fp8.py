@@ -199,6 +199,68 @@ def test_fp8_gemm_every_code(mode, fmt, M, gran):
     check_gemm(got, want, gemm_bound(a, w_deq, want), f"fp8 gemm codes fmt {fmt} mode {mode} M {M} gran {gran}")
 
 
+def special_codes(fmt):
+    """Codes whose reference decode differs from the OCP decode, from the oracle's two
+    decoders (scale 4 keeps the reference's E5M2 exponent-31 values finite)."""
+    q = np.arange(256, dtype=np.uint8).reshape(1, 256)
+    sc = np.array([4.0], np.float32)
+    ref = f16_bits_to_f32(orc.fp8_dequantize(q, sc, fmt, ql.QUANT_PER_TENSOR, 0, ql.FP8_MODE_REFERENCE))
+    ocp = f16_bits_to_f32(orc.fp8_dequantize(q, sc, fmt, ql.QUANT_PER_TENSOR, 0, ql.FP8_MODE_OCP))
+    same = (ref == ocp) | (np.isnan(ref) & np.isnan(ocp))
+    return np.flatnonzero(~same.reshape(-1)).astype(np.uint8)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_count_ref_special_matches_oracle_decoders(fmt):
+    sp = special_codes(fmt)
+    # E4M3: exponent 0 with a mantissa and 0x7F, both signs; E5M2: also exponent 31
+    assert len(sp) == (16 if fmt == ql.FP8_E4M3 else 14)
+    rng = np.random.default_rng(3 + fmt)
+    count = empty((1,), np.uint64)
+    for n, n_planted in ((0, 0), (7, 3), (4096, 0), (1_000_013, 57)):
+        ok = np.setdiff1d(np.arange(256, dtype=np.uint8), sp)
+        q = rng.choice(ok, size=n).astype(np.uint8)
+        if n_planted:
+            pos = rng.choice(n, n_planted, replace=False)
+            q[pos] = rng.choice(sp, n_planted)
+            q[-1] = sp[0]                                 # one in the last n % 16 codes
+        want = int(np.isin(q, sp).sum())
+        dq = dev(q) if n else empty((16,), np.uint8)
+        ql.call("ql_fp8_count_ref_special", dq.ptr, n, fmt, count.ptr, stream())
+        assert int(host(count)[0]) == want, (n, want)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("M,N,K,gran,gs", [
+    (1, 4096, 4096, ql.QUANT_PER_GROUP, 128), (8, 1024, 2048, ql.QUANT_PER_CHANNEL, 0),
+    (33, 512, 512, ql.QUANT_PER_GROUP, 64), (100, 256, 512, ql.QUANT_PER_TENSOR, 0)])
+def test_fp8_gemm_clean_reference_codes(fmt, M, N, K, gran, gs):
+    """Reference-encoded weights hold none of the codes whose decode differs; decoding
+    them as QL_FP8_MODE_REFERENCE_CLEAN gives the reference-mode product (within the
+    GEMM bound: the launch shape, hence the summation order, may differ) and the
+    reference-mode dequantization bit for bit."""
+    a = to_f16_bits(normal(M + 5, (M, K)))
+    w = to_f16_bits(normal(N + 7, (N, K), K ** -0.5))
+    q, sc = orc.fp8_quantize(w, fmt, gran, gs, ql.FP8_MODE_REFERENCE)
+    count = empty((1,), np.uint64)
+    dq = dev(q)
+    ql.call("ql_fp8_count_ref_special", dq.ptr, q.size, fmt, count.ptr, stream())
+    assert int(host(count)[0]) == int(np.isin(q, special_codes(fmt)).sum()) == 0
+    w_deq = orc.fp8_dequantize(q, sc, fmt, gran, gs, ql.FP8_MODE_REFERENCE)
+    want = orc.matmul(a, w_deq)
+    ref = gpu_fp8_gemm(a, q, sc, M, N, K, fmt, gran, gs, ql.FP8_MODE_REFERENCE, "query")
+    clean = gpu_fp8_gemm(a, q, sc, M, N, K, fmt, gran, gs, ql.FP8_MODE_REFERENCE_CLEAN, "query")
+    for got, what in ((ref, "reference"), (clean, "clean")):
+        check_gemm(got, want, gemm_bound(a, w_deq, want), f"{what} fp8 gemm {M}x{N}x{K}")
+    # dequantize: identical codes decode identically
+    outs = []
+    for mode in (ql.FP8_MODE_REFERENCE, ql.FP8_MODE_REFERENCE_CLEAN):
+        y = empty((N * K,), np.uint16)
+        ql.call("ql_fp8_dequantize", dq.ptr, dev(sc).ptr, N, K, fmt, gran, gs, mode, y.ptr, stream())
+        outs.append(host(y).copy())
+    np.testing.assert_array_equal(outs[0], outs[1])
+
+
 @pytest.mark.parametrize("M,N,K", [
     (1, 4096, 4096), (64, 6144, 4096), (300, 512, 1000), (8192, 256, 512),
     # few rows, odd widths
