@@ -46,23 +46,25 @@ struct AddOp {
 };
 
 // out[i] = op(a[i], b[i]) over n elements; out may alias a (in-place add).
-// U vectors per thread, NT = nontemporal loads and stores.  Measured on MI355X
-// (C5 SwiGLU, 705 MB): one 16-byte vector per thread with nontemporal access
-// streams fastest (~6.5 TB/s); unrolling further lowers occupancy without
-// adding useful bytes in flight.
-template <typename D, int W, int U, bool NT, typename Op>
-__global__ __launch_bounds__(kBlock) void binary_stream(const D* a, const D* b, D* out,
-                                                        long long n) {
+// BS threads per workgroup, U vectors per thread, NT = nontemporal loads and
+// stores.  Measured on MI355X (C5 SwiGLU, 705 MB, buffers rotated past the
+// MALL): one 16-byte vector per thread with nontemporal access streams
+// fastest; unrolling further lowers occupancy without adding useful bytes in
+// flight, and 128-thread workgroups stream a 2-read/1-write mix ~3% faster
+// than 256-thread ones.
+template <typename D, int W, int U, bool NT, typename Op, int BS = kBlock>
+__global__ __launch_bounds__(BS) void binary_stream(const D* a, const D* b, D* out,
+                                                    long long n) {
     using V = Vec<D, W>;
     const long long nvec = n / W;
-    const long long base = (long long)blockIdx.x * (kBlock * U) + threadIdx.x;
+    const long long base = (long long)blockIdx.x * (BS * U) + threadIdx.x;
     const V* av = reinterpret_cast<const V*>(a);
     const V* bv = reinterpret_cast<const V*>(b);
     V* ov = reinterpret_cast<V*>(out);
     V ra[U], rb[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const long long i = base + (long long)u * kBlock;
+        const long long i = base + (long long)u * BS;
         if (i < nvec) {
             ra[u] = load<NT>(av + i);
             rb[u] = load<NT>(bv + i);
@@ -70,7 +72,7 @@ __global__ __launch_bounds__(kBlock) void binary_stream(const D* a, const D* b, 
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const long long i = base + (long long)u * kBlock;
+        const long long i = base + (long long)u * BS;
         if (i < nvec) {
             V y;
 #pragma unroll
@@ -80,12 +82,13 @@ __global__ __launch_bounds__(kBlock) void binary_stream(const D* a, const D* b, 
         }
     }
     if (W > 1 && blockIdx.x == 0) {
-        for (long long i = nvec * W + threadIdx.x; i < n; i += kBlock)
+        for (long long i = nvec * W + threadIdx.x; i < n; i += BS)
             out[i] = from_f32<D>(Op::template apply<D>(to_f32(a[i]), to_f32(b[i])));
     }
 }
 
 constexpr int kStreamU = 1;
+constexpr int kStreamBlock = 128;
 
 template <typename D, typename Op>
 hipError_t launch_binary(const D* a, const D* b, D* out, long long n, hipStream_t stream) {
@@ -93,9 +96,10 @@ hipError_t launch_binary(const D* a, const D* b, D* out, long long n, hipStream_
     const bool vec_ok = qlh::aligned16(a) && qlh::aligned16(b) && qlh::aligned16(out);
     if (vec_ok) {
         const long long nvec = n / W;
-        const unsigned grid = nvec > 0 ? qlh::blocks_for(nvec, (long long)kBlock * kStreamU) : 1;
-        hipLaunchKernelGGL((binary_stream<D, W, kStreamU, true, Op>), dim3(grid), dim3(kBlock), 0,
-                           stream, a, b, out, n);
+        const unsigned grid =
+            nvec > 0 ? qlh::blocks_for(nvec, (long long)kStreamBlock * kStreamU) : 1;
+        hipLaunchKernelGGL((binary_stream<D, W, kStreamU, true, Op, kStreamBlock>), dim3(grid),
+                           dim3(kStreamBlock), 0, stream, a, b, out, n);
     } else {
         const unsigned grid = qlh::blocks_for(n, (long long)kBlock * kUnroll);
         hipLaunchKernelGGL((binary_stream<D, 1, kUnroll, false, Op>), dim3(grid), dim3(kBlock), 0,

@@ -256,7 +256,8 @@ def test_fp8_gemm_clean_reference_codes(fmt, M, N, K, gran, gs):
     outs = []
     for mode in (ql.FP8_MODE_REFERENCE, ql.FP8_MODE_REFERENCE_CLEAN):
         y = empty((N * K,), np.uint16)
-        ql.call("ql_fp8_dequantize", dq.ptr, dev(sc).ptr, N, K, fmt, gran, gs, mode, y.ptr, stream())
+        dsc = dev(sc)
+        ql.call("ql_fp8_dequantize", dq.ptr, dsc.ptr, N, K, fmt, gran, gs, mode, y.ptr, stream())
         outs.append(host(y).copy())
     np.testing.assert_array_equal(outs[0], outs[1])
 

@@ -44,18 +44,24 @@ def _pool(nb, blk, guard):
 def test_golden_fixture(name):
     p, a = mg.load(name)
     op, tol, s = p["op"], p["tol"], stream()
+    held = []           # device inputs stay allocated until the test ends
+
+    def D(arr):
+        t = dev(arr)
+        held.append(t)
+        return t.ptr
 
     if op in ("rmsnorm_f32", "rmsnorm_f16"):
         x = a["in_x"]
         out = Out(x.size, x.dtype)
-        ql.call(f"ql_{op}", ptr(dev(x)), ptr(dev(a["in_w"])), out.ptr, x.shape[0], x.shape[1],
+        ql.call(f"ql_{op}", D(x), D(a["in_w"]), out.ptr, x.shape[0], x.shape[1],
                 p["eps"], s)
         _check(out.get(x.shape), a["want_out"], tol, name)
 
     elif op in ("add_rmsnorm_f32", "add_rmsnorm_f16"):
         x = a["in_x"]
         dx, out = dev(x), Out(x.size, x.dtype)
-        ql.call(f"ql_{op}", ptr(dx), ptr(dev(a["in_d"])), ptr(dev(a["in_w"])), out.ptr, x.shape[0],
+        ql.call(f"ql_{op}", ptr(dx), D(a["in_d"]), D(a["in_w"]), out.ptr, x.shape[0],
                 x.shape[1], p["eps"], s)
         _check(host(dx, shape=x.shape), a["want_x"], "exact", f"{name} x'")
         _check(out.get(x.shape), a["want_out"], tol, name)
@@ -73,13 +79,13 @@ def test_golden_fixture(name):
     elif op in ("swiglu_f32", "swiglu_f16"):
         g = a["in_gate"]
         out = Out(g.size, g.dtype)
-        ql.call(f"ql_{op}", ptr(dev(g)), ptr(dev(a["in_up"])), out.ptr, g.shape[0], g.shape[1], s)
+        ql.call(f"ql_{op}", D(g), D(a["in_up"]), out.ptr, g.shape[0], g.shape[1], s)
         _check(out.get(g.shape), a["want_out"], tol, name)
 
     elif op in ("softmax_f32", "softmax_f16"):
         x = a["in_x"]
         out = Out(x.size, x.dtype)
-        ql.call(f"ql_{op}", ptr(dev(x)), out.ptr, x.shape[0], x.shape[1], s)
+        ql.call(f"ql_{op}", D(x), out.ptr, x.shape[0], x.shape[1], s)
         got = out.get(x.shape)
         _check(got, a["want_out"], tol, name)
         if "want_reftest_cpu" in a:       # tests/test_softmax.cu:88-106
@@ -89,7 +95,7 @@ def test_golden_fixture(name):
     elif op in ("embed_f16", "embed_f32"):
         t, ids = a["in_table"], a["in_ids"]
         out = Out(ids.size * t.shape[1], t.dtype)
-        ql.call(f"ql_{op}", ptr(dev(t)), ptr(dev(ids)), ids.size, t.shape[0], t.shape[1], out.ptr, s)
+        ql.call(f"ql_{op}", D(t), D(ids), ids.size, t.shape[0], t.shape[1], out.ptr, s)
         _check(out.get((ids.size, t.shape[1])), a["want_out"], tol, name)
 
     elif op == "kv_append_f32_tokens":
@@ -113,7 +119,7 @@ def test_golden_fixture(name):
         kc.upload(np.full(n, p["guard"], np.uint16))
         vc.upload(np.full(n, p["guard"], np.uint16))
         kn = a["in_k"]
-        ql.call("ql_kv_append_f16", kc.ptr, vc.ptr, ptr(dev(kn)), ptr(dev(a["in_v"])), p["layer"],
+        ql.call("ql_kv_append_f16", kc.ptr, vc.ptr, D(kn), D(a["in_v"]), p["layer"],
                 p["pos"], kn.shape[0], H, d, S, L, s)
         _check(host(kc, shape=(L, S, H, d)), a["want_k_cache"], tol, f"{name} k")
         _check(host(vc, shape=(L, S, H, d)), a["want_v_cache"], tol, f"{name} v")
@@ -122,8 +128,8 @@ def test_golden_fixture(name):
         nb, L, H, d = p["n_blocks"], p["n_layers"], p["n_kv_heads"], p["head_dim"]
         kp, vp, kptr, vptr = _pool(nb, L * 16 * H * d, p["guard"])
         kn = a["in_k"]
-        ql.call("ql_paged_kv_append_f16", kptr.ptr, vptr.ptr, nb, ptr(dev(a["in_slots"])),
-                ptr(dev(kn)), ptr(dev(a["in_v"])), kn.shape[0], p["layer"], L, H, d, s)
+        ql.call("ql_paged_kv_append_f16", kptr.ptr, vptr.ptr, nb, D(a["in_slots"]),
+                D(kn), D(a["in_v"]), kn.shape[0], p["layer"], L, H, d, s)
         _check(host(kp), a["want_k_pool"], tol, f"{name} k pool")
         _check(host(vp), a["want_v_pool"], tol, f"{name} v pool")
 
@@ -133,9 +139,9 @@ def test_golden_fixture(name):
         kp, vp, kptr, vptr = _pool(nb, L * 16 * HK * d, p["guard"])
         q, k, v = a["in_q"], a["in_k"], a["in_v"]
         dq, dk = dev(q), dev(k)
-        ql.call("ql_rope_paged_kv_append_f16", dq.ptr, dk.ptr, ptr(dev(v)), q.shape[0], H, HK, d,
-                q.shape[1], k.shape[1], v.shape[1], ptr(dev(a["in_positions"])), 0, p["theta"],
-                p["pairing"], kptr.ptr, vptr.ptr, nb, ptr(dev(a["in_slots"])), p["layer"], L, s)
+        ql.call("ql_rope_paged_kv_append_f16", dq.ptr, dk.ptr, D(v), q.shape[0], H, HK, d,
+                q.shape[1], k.shape[1], v.shape[1], D(a["in_positions"]), 0, p["theta"],
+                p["pairing"], kptr.ptr, vptr.ptr, nb, D(a["in_slots"]), p["layer"], L, s)
         _check(host(dq, shape=q.shape), a["want_q"], tol, f"{name} q")
         got_k = host(dk, shape=k.shape)
         _check(got_k, a["want_k"], tol, f"{name} k")
@@ -151,7 +157,7 @@ def test_golden_fixture(name):
     elif op == "f16_to_f32":
         x = a["in_x"]
         out = Out(x.size, np.float32)
-        ql.call("ql_f16_to_f32", ptr(dev(x)), out.ptr, x.size, s)
+        ql.call("ql_f16_to_f32", D(x), out.ptr, x.size, s)
         got, want = out.get(), a["want_out"]
         nan = np.isnan(want)
         assert np.array_equal(np.isnan(got), nan)
@@ -160,7 +166,7 @@ def test_golden_fixture(name):
     elif op == "flash_attention_f16":
         q, k, v = a["in_q"], a["in_k"], a["in_v"]
         out = Out(q.size, np.uint16)
-        ql.call("ql_flash_attention_f16", ptr(dev(q)), ptr(dev(k)), ptr(dev(v)), out.ptr,
+        ql.call("ql_flash_attention_f16", D(q), D(k), D(v), out.ptr,
                 q.shape[0], p["n_heads"], p["n_kv_heads"], p["head_dim"], p["causal"], s)
         _check(out.get(q.shape), a["want_out"], tol, name,
                vmax=float(np.abs(f16_bits_to_f32(v)).max()))
