@@ -429,17 +429,14 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
     for (int t = 0; t < n_tiles; ++t) {
         const int kv0 = t * kBK;
         const bool more = t + 1 < n_tiles;
-        if (more) fetch_tile<HD, PAGED>(regs, a, plan, pg_next, kvh, kv0 + kBK, kv_len, dummy);
-        if (t + 2 < n_tiles) pp.pointers(a, kvh, HD);                          // tile t+2
-        if (t + 3 < n_tiles) pp.entries(a, table, (t + 3) * kTilePages);       // tile t+3
         const _Float16* sk = smem + (t & 1) * T::STAGE;
         const _Float16* sv = sk + T::K_ELEMS;
 
         // a wavefront with no queries, or whose queries all precede this tile,
         // has nothing to add
         const bool active = wave_has_q && (!a.causal || kv0 <= wave_last_pos);
+        floatx16 s[2];
         if (active) {
-            floatx16 s[2];
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
                 s[kb] = floatx16{};
@@ -450,21 +447,35 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
                     s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[kk], s[kb], 0, 0, 0);
                 }
             }
+        }
+        // The next tile's loads are issued after this tile's score products: issued
+        // before them, the products waited for the loads (measured 4% slower).
+        if (more) fetch_tile<HD, PAGED>(regs, a, plan, pg_next, kvh, kv0 + kBK, kv_len, dummy);
+        if (t + 2 < n_tiles) pp.pointers(a, kvh, HD);                          // tile t+2
+        if (t + 3 < n_tiles) pp.entries(a, table, (t + 3) * kTilePages);       // tile t+3
+        if (active) {
             // mask: lane holds S^T[key = kv0 + 32*kb + 8*(i/4) + 4*hh + i%4][query col]
             const bool need_mask = kv0 + kBK > kv_len || (a.causal && kv0 + kBK - 1 > pos_base + q0 + wave * 32);
-            float mt = -INFINITY;
+            if (need_mask) {
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
+                for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    if (need_mask) {
+                    for (int i = 0; i < 16; ++i) {
                         const int j = kv0 + 32 * kb + 8 * (i >> 2) + 4 * hh + (i & 3);
                         const bool ok = j < kv_len && (!a.causal || j <= qpos);
                         s[kb][i] = ok ? s[kb][i] : -INFINITY;
                     }
-                    mt = fmaxf(mt, s[kb][i]);
                 }
             }
+            // maximum as a tree: four independent chains of eight, then combined
+            float mq[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                mq[c] = fmaxf(s[c >> 1][8 * (c & 1)], s[c >> 1][8 * (c & 1) + 1]);
+#pragma unroll
+                for (int i = 2; i < 8; ++i) mq[c] = fmaxf(mq[c], s[c >> 1][8 * (c & 1) + i]);
+            }
+            float mt = fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]));
             mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
             // Rescale only when some query's max grew by more than 2^8 in the
             // exponent: until then the stale offset keeps p <= 256 (exact
