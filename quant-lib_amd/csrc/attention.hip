@@ -180,6 +180,13 @@ __device__ __forceinline__ uintptr_t key_row(const AttnArgs& a, const _Float16* 
 }
 
 typedef const __attribute__((address_space(1))) half8* GlobalHalf8Ptr;
+typedef uint32_t u32x4g __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(1))) u32x4g* GlobalU4Ptr;
+
+// Streaming (nontemporal) 16-byte global load.
+__device__ __forceinline__ half8 load_nt16(uintptr_t p) {
+    return __builtin_bit_cast(half8, __builtin_nontemporal_load((GlobalU4Ptr)p));
+}
 
 // 16 bytes of chunk ch of a key row (row == 0: missing key -> zeros).  Loads
 // always target a valid address (dummy stands in for a missing row) and the
@@ -198,7 +205,10 @@ __device__ __forceinline__ half8 load_chunk(uintptr_t row, int ch, uintptr_t dum
 __device__ __forceinline__ half8 load_chunk_unaligned(uintptr_t row, int ch) {
     half8 r{};
     if (row != 0) {
-        const _Float16* e = reinterpret_cast<const _Float16*>(row + 16 * (uintptr_t)ch);
+        // global address space: generic (flat) loads would also count against the
+        // LDS counter, so every later LDS wait would wait for them
+        const __attribute__((address_space(1))) _Float16* e =
+            reinterpret_cast<const __attribute__((address_space(1))) _Float16*>(row + 16 * (uintptr_t)ch);
 #pragma unroll
         for (int i = 0; i < 8; ++i) r[i] = e[i];
     }
@@ -622,22 +632,13 @@ __device__ __forceinline__ bool dec_clean(const Pages& pg, int k0, int k_end) {
     return clean;
 }
 
-// K rows, loaded like V: lane owns chunk lane%CH of keys k0 + KPL*(lane/CH) + i.
+// K rows of a step that is not clean (last step, holes in the table, misaligned
+// pages): lane owns chunk lane%CH of keys k0 + KPL*(lane/CH) + i, checked loads.
 template <int HD, bool PAGED>
-__device__ __forceinline__ void dec_fetch_k(DecK<HD>& r, const AttnArgs& a, const DecPlan<HD, PAGED>& plan,
-                                            const Pages& pg, int kvh, int k0, int k_end,
-                                            uintptr_t dummy, int lane) {
+__device__ __forceinline__ void dec_fetch_k_checked(DecK<HD>& r, const AttnArgs& a, const Pages& pg,
+                                                    int kvh, int k0, int k_end, uintptr_t dummy,
+                                                    int lane) {
     using T = Dec<HD>;
-    if (dec_clean<PAGED>(pg, k0, k_end)) {   // wavefront-uniform
-        const uintptr_t base =
-            PAGED ? (plan.v_page == 0 ? pg.k[0] : pg.k[1])
-                  : reinterpret_cast<uintptr_t>(a.k) +
-                        (uintptr_t)k0 * (uintptr_t)a.kv_stride * sizeof(_Float16);
-#pragma unroll
-        for (int i = 0; i < T::KPL; ++i)
-            r.k[i] = *(GlobalHalf8Ptr)(base + plan.v_off + (uintptr_t)i * plan.row_bytes);
-        return;
-    }
     const int ch = lane % T::CH, kg = lane / T::CH;
     const bool unaligned = PAGED && pg.misaligned;   // wavefront-uniform
 #pragma unroll
@@ -668,22 +669,12 @@ __device__ __forceinline__ void dec_stage_k(const DecK<HD>& r, _Float16* sk, int
     }
 }
 
-// V rows: lane owns chunk lane%CH of keys k0 + KPL*(lane/CH) + i.
+// V rows of a step that is not clean, as the K rows.
 template <int HD, bool PAGED>
-__device__ __forceinline__ void dec_fetch_v(DecV<HD>& r, const AttnArgs& a, const DecPlan<HD, PAGED>& plan,
-                                            const Pages& pg, int kvh, int k0, int k_end,
-                                            uintptr_t dummy, int lane) {
+__device__ __forceinline__ void dec_fetch_v_checked(DecV<HD>& r, const AttnArgs& a, const Pages& pg,
+                                                    int kvh, int k0, int k_end, uintptr_t dummy,
+                                                    int lane) {
     using T = Dec<HD>;
-    if (dec_clean<PAGED>(pg, k0, k_end)) {   // wavefront-uniform
-        const uintptr_t base =
-            PAGED ? (plan.v_page == 0 ? pg.v[0] : pg.v[1])
-                  : reinterpret_cast<uintptr_t>(a.v) +
-                        (uintptr_t)k0 * (uintptr_t)a.kv_stride * sizeof(_Float16);
-#pragma unroll
-        for (int i = 0; i < T::KPL; ++i)
-            r.v[i] = *(GlobalHalf8Ptr)(base + plan.v_off + (uintptr_t)i * plan.row_bytes);
-        return;
-    }
     const int ch = lane % T::CH, kg = lane / T::CH;
     const bool unaligned = PAGED && pg.misaligned;   // wavefront-uniform
 #pragma unroll
@@ -692,6 +683,38 @@ __device__ __forceinline__ void dec_fetch_v(DecV<HD>& r, const AttnArgs& a, cons
         const uintptr_t row = j < k_end ? key_row<PAGED>(a, a.v, pg.v, kvh, k0, j, HD) : 0;
         r.v[i] = unaligned ? load_chunk_unaligned(row, ch) : load_chunk(row, ch, dummy);
     }
+}
+
+// K and V rows of one step: lane owns chunk lane%CH of keys k0 + KPL*(lane/CH) + i.
+// A clean step issues all 2*KPL loads back to back, nontemporal (each row is
+// read by one workgroup), in one straight-line block: with the K and V paths as
+// separate branches the compiler waited for the K loads before issuing the V
+// loads.
+template <int HD, bool PAGED>
+__device__ __forceinline__ void dec_fetch_kv(DecK<HD>& rk, DecV<HD>& rv, const AttnArgs& a,
+                                             const DecPlan<HD, PAGED>& plan, const Pages& pg, int kvh,
+                                             int k0, int k_end, uintptr_t dummy, int lane) {
+    using T = Dec<HD>;
+    if (dec_clean<PAGED>(pg, k0, k_end)) {   // wavefront-uniform
+        uintptr_t kbase, vbase;
+        if constexpr (PAGED) {
+            kbase = plan.v_page == 0 ? pg.k[0] : pg.k[1];
+            vbase = plan.v_page == 0 ? pg.v[0] : pg.v[1];
+        } else {
+            const uintptr_t step = (uintptr_t)k0 * (uintptr_t)a.kv_stride * sizeof(_Float16);
+            kbase = reinterpret_cast<uintptr_t>(a.k) + step;
+            vbase = reinterpret_cast<uintptr_t>(a.v) + step;
+        }
+#pragma unroll
+        for (int i = 0; i < T::KPL; ++i)
+            rk.k[i] = load_nt16(kbase + plan.v_off + (uintptr_t)i * plan.row_bytes);
+#pragma unroll
+        for (int i = 0; i < T::KPL; ++i)
+            rv.v[i] = load_nt16(vbase + plan.v_off + (uintptr_t)i * plan.row_bytes);
+        return;
+    }
+    dec_fetch_k_checked<HD, PAGED>(rk, a, pg, kvh, k0, k_end, dummy, lane);
+    dec_fetch_v_checked<HD, PAGED>(rv, a, pg, kvh, k0, k_end, dummy, lane);
 }
 
 // V^T stage: row d, keys KPL*kg + i.  The 8-byte unit u (4 keys) of row r is
@@ -872,8 +895,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_decode(AttnArgs a) {
             pg_next = pp.bases();
         }
         if (step + 2 * kAttnWaves < n_steps) pp.entries(a, table, page_of(step + 2 * kAttnWaves));
-        dec_fetch_k<HD, PAGED>(kr, a, plan, pg, kvh, k0, k_end, dummy, lane);
-        dec_fetch_v<HD, PAGED>(vr, a, plan, pg, kvh, k0, k_end, dummy, lane);
+        dec_fetch_kv<HD, PAGED>(kr, vr, a, plan, pg, kvh, k0, k_end, dummy, lane);
         dec_stage_v<HD>(vr, sv, lane);
     }
     // one step: stage its K rows, prefetch the wavefront's next step into the
@@ -882,12 +904,11 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_decode(AttnArgs a) {
         const int k0 = k_begin + step * kDecStep;
         const bool more = step + kAttnWaves < n_steps;
         dec_stage_k<HD>(kr, sk, lane);   // after the previous step's K reads (in order)
-        if (more) {
-            dec_fetch_k<HD, PAGED>(kr, a, plan, pg_next, kvh, k0 + kStride, k_end, dummy, lane);
-            dec_fetch_v<HD, PAGED>(vr, a, plan, pg_next, kvh, k0 + kStride, k_end, dummy, lane);
-        }
+        // page lookups first: issued after the K/V rows, their waits would also
+        // wait for the rows
         if (step + 2 * kAttnWaves < n_steps) pp.pointers(a, kvh, HD);
         if (step + 3 * kAttnWaves < n_steps) pp.entries(a, table, page_of(step + 3 * kAttnWaves));
+        if (more) dec_fetch_kv<HD, PAGED>(kr, vr, a, plan, pg_next, kvh, k0 + kStride, k_end, dummy, lane);
         dec_step<HD>(sk, qf, o, st, sv, k0, k_end, lane, cl2);
         if (!more) return false;
         dec_stage_v<HD>(vr, sv, lane);    // after this step's V^T reads (in order)
