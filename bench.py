@@ -491,8 +491,15 @@ def layer_rows(ql, np, chain, reps):
         deltas = [ql.DeviceArray((n_rows, D), np.uint16) for _ in range(2)]
         fp8_kind = "fp8 e4m3 g128" + (" (reference codes, checked clean)"
                                       if lw8[0].mode == ql.FP8_MODE_REFERENCE_CLEAN else "")
-        for kind, fn, lws, wb in (("fp16", "ql_engine_layer_f16", lw16, 2 * w_bytes),
-                                  (fp8_kind, "ql_engine_layer_fp8", lw8, w_bytes + 4 * w_bytes // gs)):
+        passes = [("fp16", "ql_engine_layer_f16", lw16, 2 * w_bytes, False),
+                  (fp8_kind, "ql_engine_layer_fp8", lw8, w_bytes + 4 * w_bytes // gs, False)]
+        if q_len == 1:   # decode steps again after ql_engine_tune picked the GEMM plans
+            passes.insert(1, ("fp16", "ql_engine_layer_f16", lw16, 2 * w_bytes, True))
+        for kind, fn, lws, wb, tuned in passes:
+            if tuned:
+                ql.call("ql_engine_tune", eng, n_rows, st)
+                kind += " (GEMM plans tuned)"
+
             def launch(i, fn=fn, lws=lws):
                 ql.call(fn, eng, ctypes.byref(lws[i % len(lws)]), i % L_POOL, x.ptr,
                         deltas[(i + 1) % 2].ptr if i else None, deltas[i % 2].ptr, ctypes.byref(sd), st)

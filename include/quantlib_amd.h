@@ -362,6 +362,18 @@ hipError_t ql_argmax_f16(const uint16_t* logits, int rows, int cols, int64_t ld,
  * and kept until the process ends. */
 hipError_t ql_gemm_f16(const uint16_t* x, const uint16_t* w, uint16_t* y, int M, int N, int K,
                        hipStream_t stream);
+/* Replaces the cached plan's algorithm for (M, N, K) by the fastest of the library
+ * heuristic's first 32 candidates, timed on scratch operands by the host's clock
+ * from launch to completion, launch costs included (the weights rotate
+ * over copies of >= 512 MB in total, so they stream from HBM as in a multi-layer
+ * step).  The fastest four are re-timed with the heuristic's first choice in three
+ * alternating rounds, and the first choice is kept unless one of them is more than
+ * 3% faster over those rounds.  Setup only: allocates and frees scratch, synchronizes `stream`, and must
+ * not run under graph capture.  Later ql_gemm_f16 calls of that shape use the
+ * chosen algorithm; results stay within the GEMM's fp32-accumulation tolerance
+ * but may differ in the last bits from the untuned plan.  No counterpart in the
+ * reference (its cuBLAS calls take the library default). */
+hipError_t ql_gemm_tune_f16(int M, int N, int K, hipStream_t stream);
 
 /* ---- FP8 weight codec and FP8-weight GEMM (quantlib) ------------------------------------
  * quantlib_fp16_to_fp8_e4m3/e5m2, quantlib_fp8_to_fp16, quantlib_fp8_gemm
@@ -476,6 +488,10 @@ hipError_t ql_engine_destroy(ql_engine* e);
 hipError_t ql_engine_layer_f16(ql_engine* e, const ql_layer_weights* w, int layer, uint16_t* x,
                                const uint16_t* delta_in, uint16_t* delta_out,
                                const ql_step_device* step, hipStream_t stream);
+/* ql_gemm_tune_f16 for the four fp16 layer GEMM shapes of a step of `rows` rows
+ * (1 <= rows <= max_rows): QKV, O, gate/up, down.  Setup only (see
+ * ql_gemm_tune_f16).  No counterpart in the reference. */
+hipError_t ql_engine_tune(ql_engine* e, int rows, hipStream_t stream);
 /* ---- the same layer on FP8 weights (W8A16) --------------------------------------------
  * The quantized forward of the reference: quantize_model
  * (src/quant_forward.cu:57-101) stores every weight matrix as FP8 codes + scales

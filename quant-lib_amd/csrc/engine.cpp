@@ -283,3 +283,16 @@ extern "C" hipError_t ql_engine_logits_f16(ql_engine* e, uint16_t* x, const uint
     if (tokens) QL_TRY(ql_argmax_f16(logits, n_sample, vocab, vocab, tokens, stream));
     return hipSuccess;
 }
+
+extern "C" hipError_t ql_engine_tune(ql_engine* e, int rows, hipStream_t stream) {
+    if (!e || rows < 1 || rows > e->max_rows) return hipErrorInvalidValue;
+    const ql_layer_dims& d = e->dims;
+    const int qkv = (d.n_heads + 2 * d.n_kv_heads) * d.head_dim, att = d.n_heads * d.head_dim;
+    const int shapes[4][2] = {{qkv, d.hidden}, {d.hidden, att}, {d.ffn, d.hidden}, {d.hidden, d.ffn}};
+    for (const auto& sh : shapes) {
+        const hipError_t r = ql_gemm_tune_f16(rows, sh[0], sh[1], stream);
+        if (r != hipSuccess) return r;
+    }
+    return hipSuccess;
+}
+

@@ -72,6 +72,8 @@ SIGNATURES = {
     "ql_argmax_f32": [_p, _i, _i, _i64, _p, _p],
     "ql_argmax_f16": [_p, _i, _i, _i64, _p, _p],
     "ql_gemm_f16": [_p, _p, _p, _i, _i, _i, _p],
+    "ql_gemm_tune_f16": [_i, _i, _i, _p],
+    "ql_engine_tune": [_p, _i, _p],
     "ql_fp8_num_scales": [_i, _i, _i, _i, _p],
     "ql_fp8_scales": [_p, _i, _i, _i, _i, _i, _i, _p, _p],
     "ql_fp8_quantize": [_p, _i, _i, _i, _i, _i, _i, _p, _p, _p],

@@ -303,3 +303,53 @@ def test_decode_step_graph_replays_match_eager(kind):
         if graph.value:
             ql.call("ql_graph_destroy", graph)
         ql.call("ql_engine_destroy", eng)
+
+
+# ---- tuned library GEMM plans ----------------------------------------------------------------
+@pytest.mark.parametrize("M,N,K", [(1, 1536, 512), (5, 512, 1536), (64, 1024, 256)])
+def test_gemm_tune_keeps_results_within_tolerance(M, N, K):
+    x = to_f16_bits(normal(71 + M, (M, K)))
+    w = to_f16_bits(normal(72 + N, (N, K)) * np.float32(K ** -0.5))
+    dx, dw = dev(x), dev(w)
+    want = orc.matmul(x, w)
+    outs = []
+    # the untuned plan, then tuned twice in a row (timing may pick another candidate
+    # the second time), then the last plan once more
+    for tune in (False, True, True, False):
+        if tune:
+            ql.call("ql_gemm_tune_f16", M, N, K, stream())
+        y = empty((M * N,), np.uint16)
+        ql.call("ql_gemm_f16", dx.ptr, dw.ptr, y.ptr, M, N, K, stream())
+        got = host(y, shape=(M, N))
+        # fp32 accumulation in any order, one binary16 rounding of the result
+        bound = 2.0 ** -10 * np.abs(f16_bits_to_f32(want)) + 2.0 ** -10 * (
+            np.abs(f16_bits_to_f32(x)).astype(np.float64) @ np.abs(f16_bits_to_f32(w)).T.astype(np.float64))
+        err = np.abs(f16_bits_to_f32(got).astype(np.float64) - f16_bits_to_f32(want))
+        assert np.all(err <= bound), f"gemm {M}x{N}x{K} tuned={tune}: max err {err.max():.3e}"
+        outs.append(got)
+    assert np.array_equal(outs[2], outs[3])   # one plan: identical results
+    for bad in ((0, N, K), (M, -1, K), (M, N, 0)):
+        with pytest.raises(ql.QLError):
+            ql.call("ql_gemm_tune_f16", *bad, stream())
+
+
+def test_engine_layers_after_tuning_match_oracle():
+    L = 2
+    prompts = {0: 20, 1: 33, 2: 5}           # a 58-row prefill, then 3-row decodes
+    weights = [layer_weights(100 * (l + 1)) for l in range(L)]
+    dw = [{k: dev(v) for k, v in w.items()} for w in weights]
+    lw = [ql.LayerWeights(*(d[k].ptr for k in ("attn_norm", "wqkv", "wo", "ffn_norm", "w_gate", "w_up",
+                                               "w_down"))) for d in dw]
+    dims = ql.LayerDims(DM, H, HK, HD, FF, THETA, EPS, PAIR)
+    eng = ctypes.c_void_p()
+    ql.call("ql_engine_create", ctypes.byref(dims), 64, 8, 256, ctypes.byref(eng))
+    try:
+        for rows in (58, 3):
+            ql.call("ql_engine_tune", eng, rows, stream())
+        with pytest.raises(ql.QLError):
+            ql.call("ql_engine_tune", eng, 65, stream())    # beyond the engine's max_rows
+        run_engine_steps(eng, lambda l, x, di, do, sd: ql.call(
+            "ql_engine_layer_f16", eng, ctypes.byref(lw[l]), l, x, di, do, ctypes.byref(sd), stream()),
+            weights, prompts, 3)
+    finally:
+        ql.call("ql_engine_destroy", eng)
