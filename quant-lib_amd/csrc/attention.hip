@@ -340,19 +340,14 @@ __device__ __forceinline__ void stash_tile(const TileRegs<HD, PAGED>& r, _Float1
     }
 }
 
-template <int HD, bool PAGED>
-__global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
-    using T = Tile<HD>;
-    constexpr int NKK = HD / 16;   // MFMA steps over d for S^T
-    constexpr int NDB = HD / 32;   // 32-row blocks of O^T
-    __shared__ _Float16 smem[2 * T::STAGE];
-
-    // Work item (query head, query tile).  Consecutive workgroup ids go to the
-    // 8 XCDs in turn; when the heads split evenly over the XCDs, each XCD is
-    // given its own contiguous run of heads (so the K/V rows of their shared KV
-    // heads stay in that XCD's L2).  Causal: heavy (late) query tiles first.
+// Work item of a prefill workgroup: (query head, query tile).  Consecutive
+// workgroup ids go to the 8 XCDs in turn; when the heads split evenly over the
+// XCDs, each XCD is given its own contiguous run of heads (so the K/V rows of
+// their shared KV heads stay in that XCD's L2).  Causal: heavy (late) query
+// tiles first.
+__device__ __forceinline__ void prefill_item(const AttnArgs& a, int& head, int& qt) {
     const int n_qt = (int)gridDim.x / a.n_heads;
-    int head, t;
+    int t;
     if (a.n_heads % 8 == 0) {
         const int hpx = a.n_heads / 8, xcd = (int)blockIdx.x & 7, j = (int)blockIdx.x >> 3;
         head = xcd * hpx + j % hpx;
@@ -361,7 +356,119 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
         head = (int)blockIdx.x % a.n_heads;
         t = (int)blockIdx.x / a.n_heads;
     }
-    const int qt = a.causal ? n_qt - 1 - t : t;
+    qt = a.causal ? n_qt - 1 - t : t;
+}
+
+// Q^T operand: lane holds Q[query][d = 16*kk + 8*hh + 0..7] (zeros past the last query).
+template <int HD>
+__device__ __forceinline__ void load_q_operand(half8 (&qf)[HD / 16], const _Float16* qrow, bool valid, int hh) {
+#pragma unroll
+    for (int kk = 0; kk < HD / 16; ++kk)
+        qf[kk] = valid ? *reinterpret_cast<const half8*>(qrow + 16 * kk + 8 * hh) : half8{};
+}
+
+// One wavefront's online-softmax step over a 64-key tile, given its scores
+// s[kb] = S^T block kb (lane holds S^T[key = kv0 + 32*kb + 8*(i/4) + 4*hh + i%4]
+// [its query]): masks keys past kv_len and (causal) after the query, raises the
+// running maximum when needed, forms the binary16 weights, adds their fp32 sum to
+// l_run and accumulates P V into O^T.  v_operand(db, kb, c) returns the V^T
+// operand of rows d = 32*db + 0..31 over the keys of pf[kb][c].
+template <int HD, class VOperand>
+__device__ __forceinline__ void softmax_pv(floatx16 (&s)[2], floatx16 (&o)[HD / 32], float& m_run, float& l_run,
+                                           float cl2, bool causal, int kv0, int kv_len, int qpos,
+                                           int wave_first_pos, int hh, VOperand v_operand) {
+    constexpr int NDB = HD / 32;
+    const bool need_mask = kv0 + kBK > kv_len || (causal && kv0 + kBK - 1 > wave_first_pos);
+    if (need_mask) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int j = kv0 + 32 * kb + 8 * (i >> 2) + 4 * hh + (i & 3);
+                const bool ok = j < kv_len && (!causal || j <= qpos);
+                s[kb][i] = ok ? s[kb][i] : -INFINITY;
+            }
+        }
+    }
+    // maximum as a tree: four independent chains of eight, then combined
+    float mq[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        mq[c] = fmaxf(s[c >> 1][8 * (c & 1)], s[c >> 1][8 * (c & 1) + 1]);
+#pragma unroll
+        for (int i = 2; i < 8; ++i) mq[c] = fmaxf(mq[c], s[c >> 1][8 * (c & 1) + i]);
+    }
+    float mt = fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]));
+    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+    // Rescale only when some query's max grew by more than 2^8 in the
+    // exponent: until then the stale offset keeps p <= 256 (exact
+    // enough in binary16) and O/l is unchanged, since the offset cancels.
+    const float m_cand = fmaxf(m_run, mt);
+    if (__any((m_cand - m_run) * cl2 > 8.0f)) {
+        const float alpha = __builtin_amdgcn_exp2f((m_run - m_cand) * cl2);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+        l_run *= alpha;
+        m_run = m_cand;
+    }
+    const float moff = m_run * cl2;
+    half8 pf[2][2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float p = __builtin_amdgcn_exp2f(fmaf(s[kb][i], cl2, -moff));
+            pf[kb][i >> 3][i & 7] = from_f32<_Float16>(p);
+        }
+    }
+    // row sum of the binary16 weights, accumulated in fp32 (v_dot2 with ones)
+    float lsum = l_run;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int e = 0; e < 8; e += 2)
+                lsum = __builtin_amdgcn_fdot2(half2v{pf[kb][c][e], pf[kb][c][e + 1]},
+                                              half2v{1.0f16, 1.0f16}, lsum, false);
+    l_run = lsum;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(v_operand(db, kb, c), pf[kb][c], o[db], 0, 0, 0);
+        }
+    }
+}
+
+// O = O^T / l for the lane's query (both 8-key halves of the sum combined).
+template <int HD>
+__device__ __forceinline__ void store_o(const floatx16 (&o)[HD / 32], float l_run, _Float16* orow, int hh) {
+    const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
+    const float inv_den = 1.0f / (l_tot + 1e-8f);
+#pragma unroll
+    for (int db = 0; db < HD / 32; ++db) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            half4 r;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) r[e] = from_f32<_Float16>(o[db][4 * g + e] * inv_den);
+            *reinterpret_cast<half4*>(orow + db * 32 + 8 * g + 4 * hh) = r;
+        }
+    }
+}
+
+template <int HD, bool PAGED>
+__global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
+    using T = Tile<HD>;
+    constexpr int NKK = HD / 16;   // MFMA steps over d for S^T
+    constexpr int NDB = HD / 32;   // 32-row blocks of O^T
+    __shared__ _Float16 smem[2 * T::STAGE];
+
+    int head, qt;
+    prefill_item(a, head, qt);
     const int kvh = (int)(((long long)head * a.n_kv_heads) / a.n_heads);
     int q_begin = 0, q_len = a.q_len, kv_len = a.kv_len;
     const int32_t* table = nullptr;
@@ -398,14 +505,9 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
     const int wave_last_pos = pos_base + min(q0 + wave * 32 + 31, q_len - 1);
     const bool wave_has_q = q0 + wave * 32 < q_len;
 
-    // Q^T operand: lane holds Q[query=col][d = 16*kk + 8*hh + 0..7]
     half8 qf[NKK];
-    {
-        const _Float16* qrow = a.q + (size_t)(q_begin + (q_valid ? qi : 0)) * a.q_stride + (size_t)head * HD;
-#pragma unroll
-        for (int kk = 0; kk < NKK; ++kk)
-            qf[kk] = q_valid ? *reinterpret_cast<const half8*>(qrow + 16 * kk + 8 * hh) : half8{};
-    }
+    load_q_operand<HD>(qf, a.q + (size_t)(q_begin + (q_valid ? qi : 0)) * a.q_stride + (size_t)head * HD,
+                       q_valid, hh);
 
     floatx16 o[NDB];
 #pragma unroll
@@ -464,75 +566,15 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
         if (t + 2 < n_tiles) pp.pointers(a, kvh, HD);                          // tile t+2
         if (t + 3 < n_tiles) pp.entries(a, table, (t + 3) * kTilePages);       // tile t+3
         if (active) {
-            // mask: lane holds S^T[key = kv0 + 32*kb + 8*(i/4) + 4*hh + i%4][query col]
-            const bool need_mask = kv0 + kBK > kv_len || (a.causal && kv0 + kBK - 1 > pos_base + q0 + wave * 32);
-            if (need_mask) {
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        const int j = kv0 + 32 * kb + 8 * (i >> 2) + 4 * hh + (i & 3);
-                        const bool ok = j < kv_len && (!a.causal || j <= qpos);
-                        s[kb][i] = ok ? s[kb][i] : -INFINITY;
-                    }
-                }
-            }
-            // maximum as a tree: four independent chains of eight, then combined
-            float mq[4];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                mq[c] = fmaxf(s[c >> 1][8 * (c & 1)], s[c >> 1][8 * (c & 1) + 1]);
-#pragma unroll
-                for (int i = 2; i < 8; ++i) mq[c] = fmaxf(mq[c], s[c >> 1][8 * (c & 1) + i]);
-            }
-            float mt = fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]));
-            mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
-            // Rescale only when some query's max grew by more than 2^8 in the
-            // exponent: until then the stale offset keeps p <= 256 (exact
-            // enough in binary16) and O/l is unchanged, since the offset cancels.
-            const float m_cand = fmaxf(m_run, mt);
-            if (__any((m_cand - m_run) * cl2 > 8.0f)) {
-                const float alpha = __builtin_amdgcn_exp2f((m_run - m_cand) * cl2);
-#pragma unroll
-                for (int db = 0; db < NDB; ++db) o[db] *= alpha;
-                l_run *= alpha;
-                m_run = m_cand;
-            }
-            const float moff = m_run * cl2;
-            half8 pf[2][2];
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const float p = __builtin_amdgcn_exp2f(fmaf(s[kb][i], cl2, -moff));
-                    pf[kb][i >> 3][i & 7] = from_f32<_Float16>(p);
-                }
-            }
-            // row sum of the binary16 weights, accumulated in fp32 (v_dot2 with ones)
-            float lsum = l_run;
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int c = 0; c < 2; ++c)
-#pragma unroll
-                    for (int e = 0; e < 8; e += 2)
-                        lsum = __builtin_amdgcn_fdot2(half2v{pf[kb][c][e], pf[kb][c][e + 1]},
-                                                      half2v{1.0f16, 1.0f16}, lsum, false);
-            l_run = lsum;
-#pragma unroll
-            for (int db = 0; db < NDB; ++db) {
-                const _Float16* vrow = sv + (db * 32 + col) * T::VS + 4 * hh;
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-                    for (int c = 0; c < 2; ++c) {
-                        const half4 lo = *reinterpret_cast<const half4*>(vrow + 32 * kb + 16 * c);
-                        const half4 hi = *reinterpret_cast<const half4*>(vrow + 32 * kb + 16 * c + 8);
-                        const half8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[kb][c], o[db], 0, 0, 0);
-                    }
-                }
-            }
+            // V^T operand from the transposed stage: lane holds V[keys 32*kb + 16*c + 4*hh
+            // + 0..3 and + 8..11][d = 32*db + col]
+            softmax_pv<HD>(s, o, m_run, l_run, cl2, a.causal, kv0, kv_len, qpos, pos_base + q0 + wave * 32, hh,
+                           [&](int db, int kb, int c) {
+                               const _Float16* vrow = sv + (db * 32 + col) * T::VS + 4 * hh + 32 * kb + 16 * c;
+                               const half4 lo = *reinterpret_cast<const half4*>(vrow);
+                               const half4 hi = *reinterpret_cast<const half4*>(vrow + 8);
+                               return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                           });
         }
         if (more) stash_tile<HD, PAGED>(regs, smem + ((t + 1) & 1) * T::STAGE,
                                         smem + ((t + 1) & 1) * T::STAGE + T::K_ELEMS);
@@ -541,19 +583,161 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
     }
 
     if (!q_valid) return;
-    const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
-    const float inv_den = 1.0f / (l_tot + 1e-8f);
-    _Float16* orow = a.out + (size_t)(q_begin + qi) * a.o_stride + (size_t)head * HD;
+    store_o<HD>(o, l_run, a.out + (size_t)(q_begin + qi) * a.o_stride + (size_t)head * HD, hh);
+}
+
+// ---- prefill over contiguous K/V with direct-to-LDS tile loads ----------------------------
+//
+// The work decomposition and arithmetic of attn_fwd, but the K and V tiles go
+// from global memory straight into LDS (gfx950 global_load_lds_dwordx4: lane l
+// of one load instruction writes its 16 bytes at the instruction's LDS base +
+// 16*l), so no registers hold a tile in flight and nothing is copied from
+// registers to LDS.  Both tiles are stored row-major with unpadded rows; the
+// 16-byte chunk c of key row r sits in slot c ^ dma_swz(r), so the fragment
+// reads of 16 consecutive keys spread over all banks.  The V^T operand comes
+// from the transposing LDS read (ds_read_b64_tr_b16).  Keys at or past kv_len
+// load a row of zeros (kZeroRow).  The two stages are two distinct arrays and
+// the tile loop is unrolled by two, so no wait for the loads into one stage is
+// placed before the reads of the other.  Contiguous K/V only: the pool rows of
+// the paged layout go through attn_fwd.
+__device__ _Float16 kZeroRow[128] = {};
+
+template <int HD>
+__device__ __forceinline__ int dma_swz(int r) {
+    return HD == 128 ? (r & 15) : ((r >> 1) & 7);
+}
+
+template <int HD>
+struct DmaTile {
+    static constexpr int CH = HD / 8;                          // 16-byte chunks per key row
+    static constexpr int ELEMS = kBK * HD;                     // one K (or V) tile, halfs
+    static constexpr int LOADS = kBK * CH / kAttnThreads;      // chunks per thread per tile
+    static_assert(LOADS * kAttnThreads == kBK * CH, "tile split");
+    static_assert(HD <= 128, "kZeroRow covers one key row");
+};
+
+typedef short short4v __attribute__((ext_vector_type(4)));
+
+// Transposing LDS read: in each 16-lane group, lane i receives element i%4 of
+// the 8 bytes addressed by lanes 4e + i/4, e = 0..3.
+__device__ __forceinline__ half4 lds_read_tr4(const _Float16* p) {
+    const short4v r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) short4v*)(p));
+    return __builtin_bit_cast(half4, r);
+}
+
+// Issue the loads of key tile [kv0, kv0 + 64) of KV head kvh into sk (K) and sv (V).
+template <int HD>
+__device__ __forceinline__ void dma_tile(_Float16* sk, _Float16* sv, const AttnArgs& a, int kvh, int kv0,
+                                         int kv_len, int wave, int lane) {
+    using T = DmaTile<HD>;
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            half4 r;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) r[e] = from_f32<_Float16>(o[db][4 * g + e] * inv_den);
-            *reinterpret_cast<half4*>(orow + db * 32 + 8 * g + 4 * hh) = r;
-        }
+    for (int i = 0; i < T::LOADS; ++i) {
+        const int base = (i * kAttnWaves + wave) * kWave;      // first slot of this instruction
+        const int slot = base + lane;
+        const int r = slot / T::CH, c = (slot % T::CH) ^ dma_swz<HD>(r);
+        const int j = kv0 + r;
+        const size_t off = (size_t)j * (size_t)a.kv_stride + (size_t)kvh * HD + (size_t)c * 8;
+        const _Float16* kg = j < kv_len ? a.k + off : kZeroRow + c * 8;
+        const _Float16* vg = j < kv_len ? a.v + off : kZeroRow + c * 8;
+        __builtin_amdgcn_global_load_lds(kg, (__attribute__((address_space(3))) void*)(sk + base * 8), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vg, (__attribute__((address_space(3))) void*)(sv + base * 8), 16, 0, 0);
     }
+}
+
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima): this thread's
+// direct-to-LDS loads have landed.
+__device__ __forceinline__ void wait_tile_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd_dma(AttnArgs a) {
+    using T = DmaTile<HD>;
+    constexpr int NKK = HD / 16;
+    constexpr int NDB = HD / 32;
+    __shared__ __attribute__((aligned(16))) _Float16 sk0[T::ELEMS];
+    __shared__ __attribute__((aligned(16))) _Float16 sv0[T::ELEMS];
+    __shared__ __attribute__((aligned(16))) _Float16 sk1[T::ELEMS];
+    __shared__ __attribute__((aligned(16))) _Float16 sv1[T::ELEMS];
+
+    int head, qt;
+    prefill_item(a, head, qt);
+    const int kvh = (int)(((long long)head * a.n_kv_heads) / a.n_heads);
+    const int q_len = a.q_len;
+    const int kv_len = a.kv_len;
+    const int q0 = qt * kBQ;
+    if (q0 >= q_len) return;   // workgroup-uniform
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int col = lane & 31;
+    const int hh = lane >> 5;
+    const int qi = q0 + wave * 32 + col;
+    const int pos_base = kv_len - q_len;
+    const int qpos = pos_base + qi;
+    const bool q_valid = qi < q_len;
+
+    int kv_hi = kv_len;
+    if (a.causal) kv_hi = min(kv_len, pos_base + min(q_len, q0 + kBQ));
+    if (kv_hi < 0) kv_hi = 0;
+    const int n_tiles = (kv_hi + kBK - 1) / kBK;
+    const int wave_first_pos = pos_base + q0 + wave * 32;
+    const int wave_last_pos = pos_base + min(q0 + wave * 32 + 31, q_len - 1);
+    const bool wave_has_q = q0 + wave * 32 < q_len;
+
+    half8 qf[NKK];
+    load_q_operand<HD>(qf, a.q + (size_t)(q_valid ? qi : 0) * a.q_stride + (size_t)head * HD, q_valid, hh);
+    floatx16 o[NDB];
+#pragma unroll
+    for (int i = 0; i < NDB; ++i) o[i] = floatx16{};
+    float m_run = -FLT_MAX, l_run = 0.0f;
+    const int s16 = lane & 15, grp = (lane >> 4) & 1;
+
+    auto compute = [&](const _Float16* sk, const _Float16* sv, int kv0) {
+        if (!(wave_has_q && (!a.causal || kv0 <= wave_last_pos))) return;
+        floatx16 s[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            s[kb] = floatx16{};
+            const int key = kb * 32 + col;
+            const _Float16* krow = sk + key * HD;
+            const int sw = dma_swz<HD>(key);
+#pragma unroll
+            for (int kk = 0; kk < NKK; ++kk) {
+                const half8 kf = *reinterpret_cast<const half8*>(krow + 8 * ((2 * kk + hh) ^ sw));
+                s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[kk], s[kb], 0, 0, 0);
+            }
+        }
+        // V^T operand: lane s16 of its 16-lane group addresses V[key r][d .. d+3] with
+        // key r = 32*kb + 16*c + 4*hh + s16/4 (+8 for the upper half) and
+        // d = 32*db + 16*grp + 4*(s16%4); the transposing read hands each lane its column.
+        softmax_pv<HD>(s, o, m_run, l_run, a.cl2, a.causal, kv0, kv_len, qpos, wave_first_pos, hh,
+                       [&](int db, int kb, int c) {
+                           const int d = 32 * db + 16 * grp + 4 * (s16 & 3);
+                           const int r0 = 32 * kb + 16 * c + 4 * hh + (s16 >> 2), r1 = r0 + 8;
+                           const half4 lo = lds_read_tr4(sv + r0 * HD + 8 * ((d >> 3) ^ dma_swz<HD>(r0)) + (d & 7));
+                           const half4 hi = lds_read_tr4(sv + r1 * HD + 8 * ((d >> 3) ^ dma_swz<HD>(r1)) + (d & 7));
+                           return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                       });
+    };
+
+    if (n_tiles > 0) dma_tile<HD>(sk0, sv0, a, kvh, 0, kv_len, wave, lane);
+    wait_tile_loads();
+    __syncthreads();
+    for (int t = 0; t < n_tiles; t += 2) {
+        const int kv0 = t * kBK;
+        if (t + 1 < n_tiles) dma_tile<HD>(sk1, sv1, a, kvh, kv0 + kBK, kv_len, wave, lane);
+        compute(sk0, sv0, kv0);
+        wait_tile_loads();
+        __syncthreads();
+        if (t + 1 >= n_tiles) break;
+        if (t + 2 < n_tiles) dma_tile<HD>(sk0, sv0, a, kvh, kv0 + 2 * kBK, kv_len, wave, lane);
+        compute(sk1, sv1, kv0 + kBK);
+        wait_tile_loads();
+        __syncthreads();
+    }
+
+    if (!q_valid) return;
+    store_o<HD>(o, l_run, a.out + (size_t)qi * a.o_stride + (size_t)head * HD, hh);
 }
 
 // ---- decode: one query row per sequence ------------------------------------------------
@@ -1016,10 +1200,16 @@ template <bool PAGED>
 hipError_t launch_attn(const AttnArgs& a, int head_dim, unsigned gx, unsigned gz, hipStream_t stream) {
     QL_CHECK_ARG((long long)gx * a.n_heads <= INT32_MAX);
     const dim3 grid(gx * (unsigned)a.n_heads, 1, gz);
-    if (head_dim == 128) {
-        hipLaunchKernelGGL((attn_fwd<128, PAGED>), grid, dim3(kAttnThreads), 0, stream, a);
-    } else {
-        hipLaunchKernelGGL((attn_fwd<64, PAGED>), grid, dim3(kAttnThreads), 0, stream, a);
+    if constexpr (PAGED) {
+        if (head_dim == 128)
+            hipLaunchKernelGGL((attn_fwd<128, true>), grid, dim3(kAttnThreads), 0, stream, a);
+        else
+            hipLaunchKernelGGL((attn_fwd<64, true>), grid, dim3(kAttnThreads), 0, stream, a);
+    } else {   // contiguous rows, 16-byte aligned (checked by the callers)
+        if (head_dim == 128)
+            hipLaunchKernelGGL(attn_fwd_dma<128>, grid, dim3(kAttnThreads), 0, stream, a);
+        else
+            hipLaunchKernelGGL(attn_fwd_dma<64>, grid, dim3(kAttnThreads), 0, stream, a);
     }
     return hipGetLastError();
 }
