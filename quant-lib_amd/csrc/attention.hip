@@ -12,10 +12,11 @@
 // chunked prefill), head_dim may be 64 or 128 (the reference's tiles hold 64),
 // rows may be strided, and K/V may live in 16-token pages.
 //
-// Work decomposition.  One workgroup = 4 wavefronts = 128 consecutive queries
-// of one query head; each wavefront owns 32 queries.  Keys stream through LDS
-// in tiles of 64 (double-buffered: the next tile is fetched into registers
-// while the current one is multiplied).  Per tile and wavefront:
+// Work decomposition (prefill).  One workgroup = 4 wavefronts = 128
+// consecutive queries of one query head; each wavefront owns 32 queries.  Keys
+// stream through LDS in tiles of 64, loaded straight from global memory into
+// the other of two LDS stages while the current tile is multiplied.  Per tile
+// and wavefront:
 //   S^T (64 keys x 32 queries) = K . Q^T    -- v_mfma_f32_32x32x16_f16
 //   O^T (d x 32 queries)      += V^T . P^T
 // Computing the transposed products makes every lane own one query column:
@@ -23,8 +24,8 @@
 // the P^T operand of the second product is the lane's own S^T registers
 // narrowed to fp16 (no shuffles).  The contraction order of the keys inside
 // one 16-key MFMA step is permuted identically in both operands, which the
-// sum does not see.  V is stored transposed in LDS (d-major) so the V^T
-// operand is two 8-byte LDS reads per MFMA.
+// sum does not see.  V stays row-major in LDS; the V^T operand is two
+// transposing 8-byte LDS reads per MFMA.
 //
 // Precision: Q, K, V, P in fp16 (exact products), fp32 accumulation and
 // softmax state; p = 2^(s*c - m*c) with c = scale*log2(e) from v_exp_f32, m a
@@ -54,21 +55,6 @@ constexpr int kAttnWaves = 4;
 constexpr int kAttnThreads = kAttnWaves * kWave;   // 256
 constexpr int kBQ = 32 * kAttnWaves;               // 128 queries per workgroup
 constexpr int kBK = 64;                            // keys per tile
-
-template <int HD>
-struct Tile {
-    static constexpr int KS = HD + 8;        // K row stride in LDS (halfs): +16 B breaks bank aliasing
-    static constexpr int VS = kBK + 4;       // V^T row stride (halfs): +8 B
-    static constexpr int K_ELEMS = kBK * KS;
-    static constexpr int V_ELEMS = HD * VS;
-    static constexpr int STAGE = K_ELEMS + V_ELEMS;
-    static constexpr int KCH = HD / 8;       // 16-byte chunks per K/V row
-    static constexpr int KLOADS = kBK * KCH / kAttnThreads;   // K chunks per thread
-    static constexpr int KPT = HD / 32;      // keys per thread in the V loader (4 or 2)
-    static constexpr int VGROUPS = kBK / KPT;                 // key groups (16 or 32)
-    static_assert(KLOADS * kAttnThreads == kBK * KCH, "K tile split");
-    static_assert(VGROUPS * KCH == kAttnThreads, "V tile split");
-};
 
 struct AttnArgs {
     const _Float16* q;
@@ -119,10 +105,14 @@ __device__ __forceinline__ uintptr_t readlane64(uintptr_t x, int l) {
 // results are broadcast with v_readlane.  Each stage's result is consumed one
 // tile later, at a point where the kernel waits for its K/V loads anyway, so the
 // dependent table -> pointer chain never stalls the tile in flight.
+// A null block pointer in device memory: the pointer lookup of a missing table
+// entry reads it, so the lookup is one unconditional load.
+__device__ const _Float16* const kNoBlock = nullptr;
+
 template <bool PAGED, int COUNT>
 struct PagePipe {
     int b = -1;                 // stage 1: table entry of page first + lane%4 (or -1)
-    uintptr_t kp = 0, vp = 0;   // stage 2: block pointers (0 = missing)
+    uintptr_t kp = 0, vp = 0;   // stage 2: block pointers as stored (0 = missing)
 
     __device__ __forceinline__ void entries(const AttnArgs& a, const int32_t* table, int first) {
         if constexpr (PAGED) {
@@ -133,26 +123,27 @@ struct PagePipe {
             b = e;
         }
     }
-    __device__ __forceinline__ void pointers(const AttnArgs& a, int kvh, int hd) {
+    // The loaded pointers are used only by bases(), one tile later: nothing here
+    // consumes them, so no wait for these loads is placed before the next tile's work.
+    __device__ __forceinline__ void pointers(const AttnArgs& a) {
         if constexpr (PAGED) {
-            const size_t head_off = ((size_t)a.layer * QL_PAGE_SIZE * a.n_kv_heads + kvh) * hd;
-            uintptr_t k = 0, v = 0;
-            if (b >= 0 && b < a.n_blocks) {
-                k = reinterpret_cast<uintptr_t>(a.kb[b] + head_off);
-                v = reinterpret_cast<uintptr_t>(a.vb[b] + head_off);
-            }
-            kp = k;
-            vp = v;
+            const bool ok = b >= 0 && b < a.n_blocks;
+            typedef const _Float16* const __attribute__((address_space(1)))* GlobalBlockPtr;
+            kp = reinterpret_cast<uintptr_t>(*(GlobalBlockPtr)(ok ? a.kb + b : &kNoBlock));
+            vp = reinterpret_cast<uintptr_t>(*(GlobalBlockPtr)(ok ? a.vb + b : &kNoBlock));
         }
     }
-    __device__ __forceinline__ Pages bases() const {
+    // page bases: (block, layer, slot 0, KV head kvh)
+    __device__ __forceinline__ Pages bases(const AttnArgs& a, int kvh, int hd) const {
         Pages pg{};
         if constexpr (PAGED) {
+            const uintptr_t head = ((uintptr_t)a.layer * QL_PAGE_SIZE * a.n_kv_heads + kvh) * hd * sizeof(_Float16);
             uintptr_t any = 0;
 #pragma unroll
             for (int q = 0; q < COUNT; ++q) {
-                pg.k[q] = readlane64(kp, q);
-                pg.v[q] = readlane64(vp, q);
+                const uintptr_t k = readlane64(kp, q), v = readlane64(vp, q);
+                pg.k[q] = k ? k + head : 0;
+                pg.v[q] = v ? v + head : 0;
                 any |= pg.k[q] | pg.v[q];
             }
             pg.misaligned = (any & 15) != 0;
@@ -215,129 +206,128 @@ __device__ __forceinline__ half8 load_chunk_unaligned(uintptr_t row, int ch) {
     return r;
 }
 
-template <int HD, bool PAGED>
-struct TileRegs {
-    half8 k[Tile<HD>::KLOADS];
-    half8 v[Tile<HD>::KPT];
-};
-
-// Per-thread constants of the tile loader: which tile key each of the thread's
-// K and V chunks belongs to, the page it lies in, and its byte offset from that
-// page's base (paged) or from the tile's first key row (contiguous).
-template <int HD, bool PAGED>
-struct TilePlan {
-    using T = Tile<HD>;
-    uint32_t k_off[T::KLOADS], v_off[T::KPT];
-    int k_page[T::KLOADS], v_page;
-
-    __device__ __forceinline__ TilePlan(const AttnArgs& a, int kvh) {
-        const int tid = (int)threadIdx.x;
-        const uint32_t row_bytes = PAGED ? (uint32_t)(a.n_kv_heads * HD * sizeof(_Float16))
-                                         : (uint32_t)(a.kv_stride * sizeof(_Float16));
-        const uint32_t head_bytes = PAGED ? 0u : (uint32_t)(kvh * HD * sizeof(_Float16));
-#pragma unroll
-        for (int i = 0; i < T::KLOADS; ++i) {
-            const int key = tid / T::KCH + (kAttnThreads / T::KCH) * i, ch = tid % T::KCH;
-            k_page[i] = key >> 4;
-            k_off[i] = (uint32_t)(PAGED ? (key & 15) : key) * row_bytes + head_bytes + 16u * ch;
-        }
-        const int g = tid % T::VGROUPS, ch = tid / T::VGROUPS;
-        v_page = (g * T::KPT) >> 4;
-#pragma unroll
-        for (int i = 0; i < T::KPT; ++i) {
-            const int key = g * T::KPT + i;
-            v_off[i] = (uint32_t)(PAGED ? (key & 15) : key) * row_bytes + head_bytes + 16u * ch;
-        }
-    }
-};
-
+// v[i & 3] as selects on the index bits (an indexed array read would be placed in
+// scratch memory)
 __device__ __forceinline__ uintptr_t pick4(const uintptr_t* v, int i) {
-    return i == 0 ? v[0] : i == 1 ? v[1] : i == 2 ? v[2] : v[3];
+    const uintptr_t lo = (i & 1) ? v[1] : v[0];
+    const uintptr_t hi = (i & 1) ? v[3] : v[2];
+    return (i & 2) ? hi : lo;
 }
 
-// Fetch key tile [kv0, kv0+64) of this KV head into registers (keys at or
-// beyond kv_len read as zeros; they are masked anyway).  A full tile whose
-// pages are all present and aligned takes the branch-free path; the last
-// tile, holes in the block table and misaligned pages take the checked path.
-template <int HD, bool PAGED>
-__device__ __forceinline__ void fetch_tile(TileRegs<HD, PAGED>& r, const AttnArgs& a,
-                                           const TilePlan<HD, PAGED>& plan, const Pages& pg,
-                                           int kvh, int kv0, int kv_len, uintptr_t dummy) {
-    using T = Tile<HD>;
-    bool clean = kv0 + kBK <= kv_len;
-    if constexpr (PAGED)
-        clean = clean && !pg.misaligned && pg.k[0] && pg.k[1] && pg.k[2] && pg.k[3] && pg.v[0] &&
-                pg.v[1] && pg.v[2] && pg.v[3];
-    if (clean) {   // workgroup-uniform
-        uintptr_t kbase[4], vbase;
-        if constexpr (PAGED) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) kbase[i] = pg.k[i];
-            vbase = pick4(pg.v, plan.v_page);
-        } else {
-            const uintptr_t step = (uintptr_t)kv0 * (uintptr_t)a.kv_stride * sizeof(_Float16);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) kbase[i] = reinterpret_cast<uintptr_t>(a.k) + step;
-            vbase = reinterpret_cast<uintptr_t>(a.v) + step;
-        }
-#pragma unroll
-        for (int i = 0; i < T::KLOADS; ++i) {
-            const uintptr_t kb = PAGED ? pick4(kbase, plan.k_page[i]) : kbase[0];
-            r.k[i] = *(GlobalHalf8Ptr)(kb + plan.k_off[i]);
-        }
-#pragma unroll
-        for (int i = 0; i < T::KPT; ++i) r.v[i] = *(GlobalHalf8Ptr)(vbase + plan.v_off[i]);
-        return;
-    }
-    const int tid = threadIdx.x;
-    uintptr_t krow[T::KLOADS], vrow[T::KPT];
-#pragma unroll
-    for (int i = 0; i < T::KLOADS; ++i) {
-        const int j = kv0 + (tid + kAttnThreads * i) / T::KCH;
-        krow[i] = j < kv_len ? key_row<PAGED>(a, a.k, pg.k, kvh, kv0, j, HD) : 0;
-    }
-    const int g = tid % T::VGROUPS, vch = tid / T::VGROUPS;
-#pragma unroll
-    for (int i = 0; i < T::KPT; ++i) {
-        const int j = kv0 + g * T::KPT + i;
-        vrow[i] = j < kv_len ? key_row<PAGED>(a, a.v, pg.v, kvh, kv0, j, HD) : 0;
-    }
-    if (PAGED && pg.misaligned) {   // workgroup-uniform
-#pragma unroll
-        for (int i = 0; i < T::KLOADS; ++i)
-            r.k[i] = load_chunk_unaligned(krow[i], (tid + kAttnThreads * i) % T::KCH);
-#pragma unroll
-        for (int i = 0; i < T::KPT; ++i) r.v[i] = load_chunk_unaligned(vrow[i], vch);
-        return;
-    }
-#pragma unroll
-    for (int i = 0; i < T::KLOADS; ++i)
-        r.k[i] = load_chunk(krow[i], (tid + kAttnThreads * i) % T::KCH, dummy);
-#pragma unroll
-    for (int i = 0; i < T::KPT; ++i) r.v[i] = load_chunk(vrow[i], vch, dummy);
+// ---- prefill key tiles: global memory straight into LDS ------------------------------------
+//
+// gfx950's global_load_lds_dwordx4: lane l of one load instruction writes its 16
+// bytes at the instruction's (wave-uniform) LDS base + 16*l, so no registers hold
+// a tile in flight and nothing is copied from registers to LDS.  K and V tiles
+// are stored row-major with unpadded rows; the 16-byte chunk c of key row r
+// sits in slot c ^ tile_swz(r), so the fragment reads of 16 consecutive keys
+// spread over all banks.  Keys at or past kv_len, and keys of a page missing
+// from the block table, load a row of zeros (kZeroRow).
+__device__ __attribute__((aligned(16))) _Float16 kZeroRow[128] = {};
+
+template <int HD>
+__device__ __forceinline__ int tile_swz(int r) {
+    return HD == 128 ? (r & 15) : ((r >> 1) & 7);
 }
 
-// Registers -> LDS stage: K row-major [key][d], V transposed [d][key].
+template <int HD>
+struct KvTile {
+    static constexpr int CH = HD / 8;                          // 16-byte chunks per key row
+    static constexpr int ELEMS = kBK * HD;                     // one K (or V) tile, halfs
+    static constexpr int LOADS = kBK * CH / kAttnThreads;      // chunks per thread per tile
+    static constexpr int PAGE_SLOTS = QL_PAGE_SIZE * CH;       // slots of one 16-key page
+    static_assert(LOADS * kAttnThreads == kBK * CH, "tile split");
+    static_assert(PAGE_SLOTS % kWave == 0, "one load instruction stays inside one page");
+    static_assert(HD <= 128, "kZeroRow covers one key row");
+};
+
+// Load i of a lane fills slot (i*4 + wave)*64 + lane of the stage, i.e. key row
+// r = slot / CH, chunk (slot % CH) ^ tile_swz(r).
+__device__ __forceinline__ void lds_load16(const void* src, _Float16* stage, int base_slot) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(stage + base_slot * 8), 16, 0,
+                                     0);
+}
+
+// Paged source addresses of load i of this lane.  The 64 slots of one
+// instruction lie in one 16-key page, page (i*4 + wave)*64 / PAGE_SLOTS of the
+// tile.  CHECKED: keys past kv_len and missing pages read kZeroRow.
+template <int HD, bool CHECKED>
+__device__ __forceinline__ void page_sources(uintptr_t& kg, uintptr_t& vg, const AttnArgs& a, const Pages& pg,
+                                             int kv0, int kv_len, int i, int wave, int lane) {
+    using T = KvTile<HD>;
+    const int first = (i * kAttnWaves + (wave & (kAttnWaves - 1))) * kWave;
+    const int slot = first + lane;
+    const int r = slot / T::CH, c = (slot % T::CH) ^ tile_swz<HD>(r);
+    const int p = first / T::PAGE_SLOTS;
+    const uintptr_t pk = pick4(pg.k, p), pv = pick4(pg.v, p);
+    const uintptr_t off =
+        (uintptr_t)(r & (QL_PAGE_SIZE - 1)) * (uintptr_t)a.n_kv_heads * HD * sizeof(_Float16) + 16u * c;
+    const uintptr_t zero = reinterpret_cast<uintptr_t>(kZeroRow) + 16u * c;
+    const bool ok = kv0 + r < kv_len;
+    kg = !CHECKED || (ok & (pk != 0)) ? pk + off : zero;
+    vg = !CHECKED || (ok & (pv != 0)) ? pv + off : zero;
+}
+
+template <int HD, bool CHECKED>
+__device__ __forceinline__ void load_pages(_Float16* sk, _Float16* sv, const AttnArgs& a, const Pages& pg, int kv0,
+                                           int kv_len, int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < KvTile<HD>::LOADS; ++i) {
+        uintptr_t kg, vg;
+        page_sources<HD, CHECKED>(kg, vg, a, pg, kv0, kv_len, i, wave, lane);
+        const int base = (i * kAttnWaves + wave) * kWave;
+        lds_load16(reinterpret_cast<const void*>(kg), sk, base);
+        lds_load16(reinterpret_cast<const void*>(vg), sv, base);
+    }
+}
+
+// Issue the loads of key tile [kv0, kv0 + 64) of KV head kvh into sk (K) and sv
+// (V).  Paged: a full tile whose pages are all present takes the unchecked
+// path; page pointers that are not 16-byte aligned (caller-provided pools) take
+// element-wise loads and LDS stores.  Every branch is workgroup-uniform.
 template <int HD, bool PAGED>
-__device__ __forceinline__ void stash_tile(const TileRegs<HD, PAGED>& r, _Float16* sk, _Float16* sv) {
-    using T = Tile<HD>;
-    const int tid = threadIdx.x;
+__device__ __forceinline__ void load_tile(_Float16* sk, _Float16* sv, const AttnArgs& a, const Pages& pg,
+                                          int kvh, int kv0, int kv_len, int wave, int lane) {
+    using T = KvTile<HD>;
+    if constexpr (!PAGED) {   // rows 16-byte aligned (checked by the entry points)
 #pragma unroll
-    for (int i = 0; i < T::KLOADS; ++i) {
-        const int idx = tid + kAttnThreads * i;
-        const int key = idx / T::KCH, ch = idx % T::KCH;
-        *reinterpret_cast<half8*>(sk + key * T::KS + ch * 8) = r.k[i];
-    }
-    const int g = tid % T::VGROUPS, ch = tid / T::VGROUPS;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        _Float16* dst = sv + (ch * 8 + e) * T::VS + g * T::KPT;
-        if constexpr (T::KPT == 4) {
-            *reinterpret_cast<half4*>(dst) = half4{r.v[0][e], r.v[1][e], r.v[2][e], r.v[3][e]};
-        } else {
-            *reinterpret_cast<half2v*>(dst) = half2v{r.v[0][e], r.v[1][e]};
+        for (int i = 0; i < T::LOADS; ++i) {
+            const int base = (i * kAttnWaves + wave) * kWave, slot = base + lane;
+            const int r = slot / T::CH, c = (slot % T::CH) ^ tile_swz<HD>(r);
+            const int j = kv0 + r;
+            const size_t off = (size_t)j * (size_t)a.kv_stride + (size_t)kvh * HD + (size_t)c * 8;
+            lds_load16(j < kv_len ? a.k + off : kZeroRow + c * 8, sk, base);
+            lds_load16(j < kv_len ? a.v + off : kZeroRow + c * 8, sv, base);
         }
+    } else if (pg.misaligned) {
+#pragma unroll
+        for (int i = 0; i < T::LOADS; ++i) {
+            uintptr_t kg, vg;
+            page_sources<HD, true>(kg, vg, a, pg, kv0, kv_len, i, wave, lane);
+            const int slot = (i * kAttnWaves + wave) * kWave + lane;
+            *reinterpret_cast<half8*>(sk + slot * 8) = load_chunk_unaligned(kg, 0);
+            *reinterpret_cast<half8*>(sv + slot * 8) = load_chunk_unaligned(vg, 0);
+        }
+    } else if (kv0 + kBK <= kv_len && pg.k[0] && pg.k[1] && pg.k[2] && pg.k[3] && pg.v[0] && pg.v[1] && pg.v[2] &&
+               pg.v[3]) {
+        load_pages<HD, false>(sk, sv, a, pg, kv0, kv_len, wave, lane);
+    } else {
+        load_pages<HD, true>(sk, sv, a, pg, kv0, kv_len, wave, lane);
     }
+}
+
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima): this thread's
+// direct-to-LDS loads have landed.
+__device__ __forceinline__ void wait_tile_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+typedef short short4v __attribute__((ext_vector_type(4)));
+
+// Transposing LDS read (ds_read_b64_tr_b16): in each 16-lane group, lane i
+// receives element i%4 of the 8 bytes addressed by lanes 4e + i/4, e = 0..3.
+__device__ __forceinline__ half4 lds_read_tr4(const _Float16* p) {
+    const short4v r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) short4v*)(p));
+    return __builtin_bit_cast(half4, r);
 }
 
 // Work item of a prefill workgroup: (query head, query tile).  Consecutive
@@ -460,12 +450,20 @@ __device__ __forceinline__ void store_o(const floatx16 (&o)[HD / 32], float l_ru
     }
 }
 
+// One prefill workgroup: 128 queries of one query head against every key they
+// see, in 64-key tiles through two LDS stages.  The stages are two distinct
+// arrays and the tile loop is unrolled by two, so no wait for the loads into
+// one stage is placed before the reads of the other.  Paged K/V: the page bases
+// of tile t+2 are looked up (PagePipe) while tile t is multiplied.
 template <int HD, bool PAGED>
 __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
-    using T = Tile<HD>;
+    using T = KvTile<HD>;
     constexpr int NKK = HD / 16;   // MFMA steps over d for S^T
     constexpr int NDB = HD / 32;   // 32-row blocks of O^T
-    __shared__ _Float16 smem[2 * T::STAGE];
+    __shared__ __attribute__((aligned(16))) _Float16 sk0[T::ELEMS];
+    __shared__ __attribute__((aligned(16))) _Float16 sv0[T::ELEMS];
+    __shared__ __attribute__((aligned(16))) _Float16 sk1[T::ELEMS];
+    __shared__ __attribute__((aligned(16))) _Float16 sv1[T::ELEMS];
 
     int head, qt;
     prefill_item(a, head, qt);
@@ -486,7 +484,9 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
     if (kv_len < 0) kv_len = 0;
 
     const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
+    // paged: a scalar wave index makes load_tile's page choice scalar (the
+    // compiler's register allocation measured best this way for each layout)
+    const int wave = PAGED ? __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave) : (int)threadIdx.x / kWave;
     const int col = lane & 31;   // this lane's query within the wavefront
     const int hh = lane >> 5;    // which 8-wide half of an MFMA k-step the lane feeds
     const int qi = q0 + wave * 32 + col;     // query index within the sequence
@@ -496,187 +496,6 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
 
     // keys this workgroup needs
     int kv_hi = kv_len;
-    if (a.causal) {
-        const int last = pos_base + min(q_len, q0 + kBQ) - 1;
-        kv_hi = min(kv_len, last + 1);
-    }
-    if (kv_hi < 0) kv_hi = 0;
-    const int n_tiles = (kv_hi + kBK - 1) / kBK;
-    const int wave_last_pos = pos_base + min(q0 + wave * 32 + 31, q_len - 1);
-    const bool wave_has_q = q0 + wave * 32 < q_len;
-
-    half8 qf[NKK];
-    load_q_operand<HD>(qf, a.q + (size_t)(q_begin + (q_valid ? qi : 0)) * a.q_stride + (size_t)head * HD,
-                       q_valid, hh);
-
-    floatx16 o[NDB];
-#pragma unroll
-    for (int i = 0; i < NDB; ++i) o[i] = floatx16{};
-    float m_run = -FLT_MAX, l_run = 0.0f;
-    const float cl2 = a.cl2;
-
-    // a valid, aligned address for the loads of missing key rows: this
-    // sequence's first query row
-    const uintptr_t dummy = reinterpret_cast<uintptr_t>(a.q + (size_t)q_begin * a.q_stride);
-    TileRegs<HD, PAGED> regs;
-    const TilePlan<HD, PAGED> plan(a, kvh);
-    constexpr int kTilePages = kBK / QL_PAGE_SIZE;
-    PagePipe<PAGED, kTilePages> pp;
-    Pages pg_next{};
-    if (n_tiles > 0) {
-        pp.entries(a, table, 0);
-        pp.pointers(a, kvh, HD);
-        const Pages pg0 = pp.bases();
-        if (n_tiles > 1) {
-            pp.entries(a, table, kTilePages);
-            pp.pointers(a, kvh, HD);
-            pg_next = pp.bases();
-        }
-        if (n_tiles > 2) pp.entries(a, table, 2 * kTilePages);
-        fetch_tile<HD, PAGED>(regs, a, plan, pg0, kvh, 0, kv_len, dummy);
-        stash_tile<HD, PAGED>(regs, smem, smem + T::K_ELEMS);
-    }
-    __syncthreads();
-
-    for (int t = 0; t < n_tiles; ++t) {
-        const int kv0 = t * kBK;
-        const bool more = t + 1 < n_tiles;
-        const _Float16* sk = smem + (t & 1) * T::STAGE;
-        const _Float16* sv = sk + T::K_ELEMS;
-
-        // a wavefront with no queries, or whose queries all precede this tile,
-        // has nothing to add
-        const bool active = wave_has_q && (!a.causal || kv0 <= wave_last_pos);
-        floatx16 s[2];
-        if (active) {
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                s[kb] = floatx16{};
-                const _Float16* krow = sk + (kb * 32 + col) * T::KS + 8 * hh;
-#pragma unroll
-                for (int kk = 0; kk < NKK; ++kk) {
-                    const half8 kf = *reinterpret_cast<const half8*>(krow + 16 * kk);
-                    s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[kk], s[kb], 0, 0, 0);
-                }
-            }
-        }
-        // The next tile's loads are issued after this tile's score products: issued
-        // before them, the products waited for the loads (measured 4% slower).
-        if (more) fetch_tile<HD, PAGED>(regs, a, plan, pg_next, kvh, kv0 + kBK, kv_len, dummy);
-        if (t + 2 < n_tiles) pp.pointers(a, kvh, HD);                          // tile t+2
-        if (t + 3 < n_tiles) pp.entries(a, table, (t + 3) * kTilePages);       // tile t+3
-        if (active) {
-            // V^T operand from the transposed stage: lane holds V[keys 32*kb + 16*c + 4*hh
-            // + 0..3 and + 8..11][d = 32*db + col]
-            softmax_pv<HD>(s, o, m_run, l_run, cl2, a.causal, kv0, kv_len, qpos, pos_base + q0 + wave * 32, hh,
-                           [&](int db, int kb, int c) {
-                               const _Float16* vrow = sv + (db * 32 + col) * T::VS + 4 * hh + 32 * kb + 16 * c;
-                               const half4 lo = *reinterpret_cast<const half4*>(vrow);
-                               const half4 hi = *reinterpret_cast<const half4*>(vrow + 8);
-                               return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                           });
-        }
-        if (more) stash_tile<HD, PAGED>(regs, smem + ((t + 1) & 1) * T::STAGE,
-                                        smem + ((t + 1) & 1) * T::STAGE + T::K_ELEMS);
-        if (t + 2 < n_tiles) pg_next = pp.bases();
-        __syncthreads();
-    }
-
-    if (!q_valid) return;
-    store_o<HD>(o, l_run, a.out + (size_t)(q_begin + qi) * a.o_stride + (size_t)head * HD, hh);
-}
-
-// ---- prefill over contiguous K/V with direct-to-LDS tile loads ----------------------------
-//
-// The work decomposition and arithmetic of attn_fwd, but the K and V tiles go
-// from global memory straight into LDS (gfx950 global_load_lds_dwordx4: lane l
-// of one load instruction writes its 16 bytes at the instruction's LDS base +
-// 16*l), so no registers hold a tile in flight and nothing is copied from
-// registers to LDS.  Both tiles are stored row-major with unpadded rows; the
-// 16-byte chunk c of key row r sits in slot c ^ dma_swz(r), so the fragment
-// reads of 16 consecutive keys spread over all banks.  The V^T operand comes
-// from the transposing LDS read (ds_read_b64_tr_b16).  Keys at or past kv_len
-// load a row of zeros (kZeroRow).  The two stages are two distinct arrays and
-// the tile loop is unrolled by two, so no wait for the loads into one stage is
-// placed before the reads of the other.  Contiguous K/V only: the pool rows of
-// the paged layout go through attn_fwd.
-__device__ _Float16 kZeroRow[128] = {};
-
-template <int HD>
-__device__ __forceinline__ int dma_swz(int r) {
-    return HD == 128 ? (r & 15) : ((r >> 1) & 7);
-}
-
-template <int HD>
-struct DmaTile {
-    static constexpr int CH = HD / 8;                          // 16-byte chunks per key row
-    static constexpr int ELEMS = kBK * HD;                     // one K (or V) tile, halfs
-    static constexpr int LOADS = kBK * CH / kAttnThreads;      // chunks per thread per tile
-    static_assert(LOADS * kAttnThreads == kBK * CH, "tile split");
-    static_assert(HD <= 128, "kZeroRow covers one key row");
-};
-
-typedef short short4v __attribute__((ext_vector_type(4)));
-
-// Transposing LDS read: in each 16-lane group, lane i receives element i%4 of
-// the 8 bytes addressed by lanes 4e + i/4, e = 0..3.
-__device__ __forceinline__ half4 lds_read_tr4(const _Float16* p) {
-    const short4v r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) short4v*)(p));
-    return __builtin_bit_cast(half4, r);
-}
-
-// Issue the loads of key tile [kv0, kv0 + 64) of KV head kvh into sk (K) and sv (V).
-template <int HD>
-__device__ __forceinline__ void dma_tile(_Float16* sk, _Float16* sv, const AttnArgs& a, int kvh, int kv0,
-                                         int kv_len, int wave, int lane) {
-    using T = DmaTile<HD>;
-#pragma unroll
-    for (int i = 0; i < T::LOADS; ++i) {
-        const int base = (i * kAttnWaves + wave) * kWave;      // first slot of this instruction
-        const int slot = base + lane;
-        const int r = slot / T::CH, c = (slot % T::CH) ^ dma_swz<HD>(r);
-        const int j = kv0 + r;
-        const size_t off = (size_t)j * (size_t)a.kv_stride + (size_t)kvh * HD + (size_t)c * 8;
-        const _Float16* kg = j < kv_len ? a.k + off : kZeroRow + c * 8;
-        const _Float16* vg = j < kv_len ? a.v + off : kZeroRow + c * 8;
-        __builtin_amdgcn_global_load_lds(kg, (__attribute__((address_space(3))) void*)(sk + base * 8), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(vg, (__attribute__((address_space(3))) void*)(sv + base * 8), 16, 0, 0);
-    }
-}
-
-// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima): this thread's
-// direct-to-LDS loads have landed.
-__device__ __forceinline__ void wait_tile_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-
-template <int HD>
-__global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd_dma(AttnArgs a) {
-    using T = DmaTile<HD>;
-    constexpr int NKK = HD / 16;
-    constexpr int NDB = HD / 32;
-    __shared__ __attribute__((aligned(16))) _Float16 sk0[T::ELEMS];
-    __shared__ __attribute__((aligned(16))) _Float16 sv0[T::ELEMS];
-    __shared__ __attribute__((aligned(16))) _Float16 sk1[T::ELEMS];
-    __shared__ __attribute__((aligned(16))) _Float16 sv1[T::ELEMS];
-
-    int head, qt;
-    prefill_item(a, head, qt);
-    const int kvh = (int)(((long long)head * a.n_kv_heads) / a.n_heads);
-    const int q_len = a.q_len;
-    const int kv_len = a.kv_len;
-    const int q0 = qt * kBQ;
-    if (q0 >= q_len) return;   // workgroup-uniform
-
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
-    const int col = lane & 31;
-    const int hh = lane >> 5;
-    const int qi = q0 + wave * 32 + col;
-    const int pos_base = kv_len - q_len;
-    const int qpos = pos_base + qi;
-    const bool q_valid = qi < q_len;
-
-    int kv_hi = kv_len;
     if (a.causal) kv_hi = min(kv_len, pos_base + min(q_len, q0 + kBQ));
     if (kv_hi < 0) kv_hi = 0;
     const int n_tiles = (kv_hi + kBK - 1) / kBK;
@@ -685,13 +504,16 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd_dma(AttnArgs a) {
     const bool wave_has_q = q0 + wave * 32 < q_len;
 
     half8 qf[NKK];
-    load_q_operand<HD>(qf, a.q + (size_t)(q_valid ? qi : 0) * a.q_stride + (size_t)head * HD, q_valid, hh);
+    load_q_operand<HD>(qf, a.q + (size_t)(q_begin + (q_valid ? qi : 0)) * a.q_stride + (size_t)head * HD,
+                       q_valid, hh);
     floatx16 o[NDB];
 #pragma unroll
     for (int i = 0; i < NDB; ++i) o[i] = floatx16{};
     float m_run = -FLT_MAX, l_run = 0.0f;
     const int s16 = lane & 15, grp = (lane >> 4) & 1;
 
+    // S^T = K . Q^T and the online-softmax step of one tile held in (sk, sv); a
+    // wavefront with no queries, or whose queries all precede the tile, skips it
     auto compute = [&](const _Float16* sk, const _Float16* sv, int kv0) {
         if (!(wave_has_q && (!a.causal || kv0 <= wave_last_pos))) return;
         floatx16 s[2];
@@ -700,7 +522,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd_dma(AttnArgs a) {
             s[kb] = floatx16{};
             const int key = kb * 32 + col;
             const _Float16* krow = sk + key * HD;
-            const int sw = dma_swz<HD>(key);
+            const int sw = tile_swz<HD>(key);
 #pragma unroll
             for (int kk = 0; kk < NKK; ++kk) {
                 const half8 kf = *reinterpret_cast<const half8*>(krow + 8 * ((2 * kk + hh) ^ sw));
@@ -714,30 +536,48 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd_dma(AttnArgs a) {
                        [&](int db, int kb, int c) {
                            const int d = 32 * db + 16 * grp + 4 * (s16 & 3);
                            const int r0 = 32 * kb + 16 * c + 4 * hh + (s16 >> 2), r1 = r0 + 8;
-                           const half4 lo = lds_read_tr4(sv + r0 * HD + 8 * ((d >> 3) ^ dma_swz<HD>(r0)) + (d & 7));
-                           const half4 hi = lds_read_tr4(sv + r1 * HD + 8 * ((d >> 3) ^ dma_swz<HD>(r1)) + (d & 7));
+                           const half4 lo = lds_read_tr4(sv + r0 * HD + 8 * ((d >> 3) ^ tile_swz<HD>(r0)) + (d & 7));
+                           const half4 hi = lds_read_tr4(sv + r1 * HD + 8 * ((d >> 3) ^ tile_swz<HD>(r1)) + (d & 7));
                            return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                        });
     };
 
-    if (n_tiles > 0) dma_tile<HD>(sk0, sv0, a, kvh, 0, kv_len, wave, lane);
+    constexpr int kTilePages = kBK / QL_PAGE_SIZE;
+    PagePipe<PAGED, kTilePages> pp;
+    Pages pg_next{};
+    if (n_tiles > 0) {
+        pp.entries(a, table, 0);
+        pp.pointers(a);
+        const Pages pg0 = pp.bases(a, kvh, HD);
+        if (n_tiles > 1) {
+            pp.entries(a, table, kTilePages);
+            pp.pointers(a);
+            pg_next = pp.bases(a, kvh, HD);
+        }
+        if (n_tiles > 2) pp.entries(a, table, 2 * kTilePages);
+        load_tile<HD, PAGED>(sk0, sv0, a, pg0, kvh, 0, kv_len, wave, lane);
+    }
     wait_tile_loads();
     __syncthreads();
-    for (int t = 0; t < n_tiles; t += 2) {
+    // tile t sits in (sk, sv); tile t+1 is loaded into (nk, nv) meanwhile
+    auto step = [&](int t, const _Float16* sk, const _Float16* sv, _Float16* nk, _Float16* nv) {
         const int kv0 = t * kBK;
-        if (t + 1 < n_tiles) dma_tile<HD>(sk1, sv1, a, kvh, kv0 + kBK, kv_len, wave, lane);
-        compute(sk0, sv0, kv0);
+        if (t + 1 < n_tiles) load_tile<HD, PAGED>(nk, nv, a, pg_next, kvh, kv0 + kBK, kv_len, wave, lane);
+        if (t + 2 < n_tiles) pp.pointers(a);                      // tile t+2
+        if (t + 3 < n_tiles) pp.entries(a, table, (t + 3) * kTilePages);   // tile t+3
+        compute(sk, sv, kv0);
+        if (t + 2 < n_tiles) pg_next = pp.bases(a, kvh, HD);
         wait_tile_loads();
         __syncthreads();
+    };
+    for (int t = 0; t < n_tiles; t += 2) {
+        step(t, sk0, sv0, sk1, sv1);
         if (t + 1 >= n_tiles) break;
-        if (t + 2 < n_tiles) dma_tile<HD>(sk0, sv0, a, kvh, kv0 + 2 * kBK, kv_len, wave, lane);
-        compute(sk1, sv1, kv0 + kBK);
-        wait_tile_loads();
-        __syncthreads();
+        step(t + 1, sk1, sv1, sk0, sv0);
     }
 
     if (!q_valid) return;
-    store_o<HD>(o, l_run, a.out + (size_t)qi * a.o_stride + (size_t)head * HD, hh);
+    store_o<HD>(o, l_run, a.out + (size_t)(q_begin + qi) * a.o_stride + (size_t)head * HD, hh);
 }
 
 // ---- decode: one query row per sequence ------------------------------------------------
@@ -1071,12 +911,12 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_decode(AttnArgs a) {
     if (step < n_steps) {
         const int k0 = k_begin + step * kDecStep;
         pp.entries(a, table, page_of(step));
-        pp.pointers(a, kvh, HD);
-        const Pages pg = pp.bases();
+        pp.pointers(a);
+        const Pages pg = pp.bases(a, kvh, HD);
         if (step + kAttnWaves < n_steps) {
             pp.entries(a, table, page_of(step + kAttnWaves));
-            pp.pointers(a, kvh, HD);
-            pg_next = pp.bases();
+            pp.pointers(a);
+            pg_next = pp.bases(a, kvh, HD);
         }
         if (step + 2 * kAttnWaves < n_steps) pp.entries(a, table, page_of(step + 2 * kAttnWaves));
         dec_fetch_kv<HD, PAGED>(kr, vr, a, plan, pg, kvh, k0, k_end, dummy, lane);
@@ -1090,13 +930,13 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_decode(AttnArgs a) {
         dec_stage_k<HD>(kr, sk, lane);   // after the previous step's K reads (in order)
         // page lookups first: issued after the K/V rows, their waits would also
         // wait for the rows
-        if (step + 2 * kAttnWaves < n_steps) pp.pointers(a, kvh, HD);
+        if (step + 2 * kAttnWaves < n_steps) pp.pointers(a);
         if (step + 3 * kAttnWaves < n_steps) pp.entries(a, table, page_of(step + 3 * kAttnWaves));
         if (more) dec_fetch_kv<HD, PAGED>(kr, vr, a, plan, pg_next, kvh, k0 + kStride, k_end, dummy, lane);
         dec_step<HD>(sk, qf, o, st, sv, k0, k_end, lane, cl2);
         if (!more) return false;
         dec_stage_v<HD>(vr, sv, lane);    // after this step's V^T reads (in order)
-        if (step + 2 * kAttnWaves < n_steps) pg_next = pp.bases();
+        if (step + 2 * kAttnWaves < n_steps) pg_next = pp.bases(a, kvh, HD);
         step += kAttnWaves;
         return true;
     };
@@ -1200,16 +1040,10 @@ template <bool PAGED>
 hipError_t launch_attn(const AttnArgs& a, int head_dim, unsigned gx, unsigned gz, hipStream_t stream) {
     QL_CHECK_ARG((long long)gx * a.n_heads <= INT32_MAX);
     const dim3 grid(gx * (unsigned)a.n_heads, 1, gz);
-    if constexpr (PAGED) {
-        if (head_dim == 128)
-            hipLaunchKernelGGL((attn_fwd<128, true>), grid, dim3(kAttnThreads), 0, stream, a);
-        else
-            hipLaunchKernelGGL((attn_fwd<64, true>), grid, dim3(kAttnThreads), 0, stream, a);
-    } else {   // contiguous rows, 16-byte aligned (checked by the callers)
-        if (head_dim == 128)
-            hipLaunchKernelGGL(attn_fwd_dma<128>, grid, dim3(kAttnThreads), 0, stream, a);
-        else
-            hipLaunchKernelGGL(attn_fwd_dma<64>, grid, dim3(kAttnThreads), 0, stream, a);
+    if (head_dim == 128) {
+        hipLaunchKernelGGL((attn_fwd<128, PAGED>), grid, dim3(kAttnThreads), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL((attn_fwd<64, PAGED>), grid, dim3(kAttnThreads), 0, stream, a);
     }
     return hipGetLastError();
 }

@@ -122,13 +122,17 @@ class PagedPool:
     """Device pool of nb blocks [L, 16, HK, d] (K and V), written through
     ql_paged_kv_append_f16 from per-sequence block tables."""
 
-    def __init__(self, nb, L, hkv, d):
+    def __init__(self, nb, L, hkv, d, offset_elems=0):
+        # offset_elems > 0 starts every block that many elements past a 16-byte
+        # boundary (a caller-provided pool with misaligned block pointers)
         self.nb, self.L, self.hkv, self.d = nb, L, hkv, d
         self.blk = L * 16 * hkv * d
-        self.kpool = empty((nb * self.blk,), np.uint16, fill_bits=GUARD_BYTE)
-        self.vpool = empty((nb * self.blk,), np.uint16, fill_bits=GUARD_BYTE)
-        self.kptrs = dev(np.array([self.kpool.ptr + 2 * self.blk * b for b in range(nb)], np.int64))
-        self.vptrs = dev(np.array([self.vpool.ptr + 2 * self.blk * b for b in range(nb)], np.int64))
+        self.kpool = empty((nb * self.blk + offset_elems,), np.uint16, fill_bits=GUARD_BYTE)
+        self.vpool = empty((nb * self.blk + offset_elems,), np.uint16, fill_bits=GUARD_BYTE)
+        self.kptrs = dev(np.array([self.kpool.ptr + 2 * (self.blk * b + offset_elems) for b in range(nb)],
+                                  np.int64))
+        self.vptrs = dev(np.array([self.vpool.ptr + 2 * (self.blk * b + offset_elems) for b in range(nb)],
+                                  np.int64))
 
     def append(self, table, k, v, layer):
         n = k.shape[0]
@@ -219,6 +223,55 @@ def test_paged_attention_skips_bad_rows_and_missing_blocks():
     kz[16:32] = 0
     vz[16:32] = 0
     check_attn(out.get((4, h, d)), orc.attention(q, kz, vz, h, hkv, True, f16=True), v, "holed table")
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_paged_attention_misaligned_block_pointers(d):
+    # block pointers 2 bytes past a 16-byte boundary take the element-wise load
+    # path: prefill and decode give the same bits as over an aligned pool, and
+    # match the oracle (holes in the table still read as zero rows)
+    h, hkv, L, layer = 8, 2, 2, 1
+    ctx, qn = [150, 77, 40], [150, 20, 1]
+    need = [(c + 15) // 16 for c in ctx]
+    nb = sum(need) + 1
+    perm = np.random.default_rng(d).permutation(nb)
+    bt = np.full((len(ctx), max(need) + 1), -1, np.int32)
+    o = 0
+    for s, n in enumerate(need):
+        bt[s, :n] = perm[o:o + n]
+        o += n
+    bt[2, 1] = -1   # sequence 2: keys 16..31 have no block
+    ks = [to_f16_bits(normal(400 + s, (c, hkv, d))) for s, c in enumerate(ctx)]
+    vs = [to_f16_bits(normal(500 + s, (c, hkv, d))) for s, c in enumerate(ctx)]
+    qs = [to_f16_bits(normal(600 + s, (n, h, d))) for s, n in enumerate(qn)]
+    cu = np.concatenate([[0], np.cumsum(qn)]).astype(np.int32)
+    rows = int(cu[-1])
+    dq, dcu, dctx, dbt = dev(np.concatenate(qs)), dev(cu), dev(np.array(ctx, np.int32)), dev(bt)
+    dq1 = dev(np.stack([q[-1] for q in qs]))   # each sequence's last query, for the decode call
+    got = {}
+    for off in (0, 1):
+        pool = PagedPool(nb, L, hkv, d, offset_elems=off)
+        for s in range(len(ctx)):
+            pool.append(bt[s], ks[s], vs[s], layer)
+        out = Out(rows * h * d, np.uint16)
+        ql.call("ql_paged_attention_f16", dq.ptr, out.ptr, h * d, h * d, rows, len(ctx), dcu.ptr,
+                dctx.ptr, max(qn), dbt.ptr, bt.shape[1], pool.kptrs.ptr, pool.vptrs.ptr, nb, layer, L,
+                h, hkv, d, 1, stream())
+        dec = Out(len(ctx) * h * d, np.uint16)
+        ql.call("ql_paged_decode_attention_f16", dq1.ptr, dec.ptr, h * d, h * d, len(ctx), dctx.ptr,
+                max(ctx), dbt.ptr, bt.shape[1], pool.kptrs.ptr, pool.vptrs.ptr, nb, layer, L, h, hkv,
+                d, None, 0, stream())
+        got[off] = (out.get((rows, h, d)), dec.get((len(ctx), h, d)))
+    assert np.array_equal(got[0][0], got[1][0]), "prefill: misaligned pool != aligned pool"
+    assert np.array_equal(got[0][1], got[1][1]), "decode: misaligned pool != aligned pool"
+    for s in range(len(ctx)):
+        k, v = ks[s].copy(), vs[s].copy()
+        if s == 2:
+            k[16:32] = 0
+            v[16:32] = 0
+        want = orc.attention(qs[s], k, v, h, hkv, True, f16=True)
+        check_attn(got[1][0][cu[s]:cu[s + 1]], want, v, f"misaligned pool prefill seq {s}")
+        check_attn(got[1][1][s:s + 1], want[-1:], v, f"misaligned pool decode seq {s}")
 
 
 # ---- C5 shape: 8192-token causal prefill, GQA 32/8, head_dim 128 ---------------------------
