@@ -220,14 +220,25 @@ __device__ __forceinline__ uintptr_t pick4(const uintptr_t* v, int i) {
 // bytes at the instruction's (wave-uniform) LDS base + 16*l, so no registers hold
 // a tile in flight and nothing is copied from registers to LDS.  K and V tiles
 // are stored row-major with unpadded rows; the 16-byte chunk c of key row r
-// sits in slot c ^ tile_swz(r), so the fragment reads of 16 consecutive keys
-// spread over all banks.  Keys at or past kv_len, and keys of a page missing
+// sits in slot c ^ tile_swz(r), so both the K fragment reads and the
+// transposing V reads spread over all banks.  Keys at or past kv_len, and keys of a page missing
 // from the block table, load a row of zeros (kZeroRow).
 __device__ __attribute__((aligned(16))) _Float16 kZeroRow[128] = {};
 
+// Chunk swizzle of key row r: a permutation of the row-number bits that sets the
+// LDS bank group (the 16-byte slot within a 256-byte bank line).  K fragment
+// reads (16 consecutive keys, one chunk each) need 16 (HD 64: 8 per row parity)
+// distinct values over consecutive rows: any bit permutation gives that.  The
+// transposing V reads of one instruction cover rows R + 0..3 (R = 4*hh mod 16)
+// and 4 consecutive chunks (2 per 16-lane group): the row's low two bits go to
+// the slot's high bits and hh to slot bit 1, so each 32-lane half of the
+// instruction, whichever halves the hardware pairs, covers all 64 banks once.
+// (HD 128 rows span one bank line; HD 64 rows two, split by the row parity.)
 template <int HD>
 __device__ __forceinline__ int tile_swz(int r) {
-    return HD == 128 ? (r & 15) : ((r >> 1) & 7);
+    if constexpr (HD == 128) return ((r & 3) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1);
+    const int t = (r >> 1) & 7;   // row pair within 16 rows
+    return ((t & 1) << 2) | (t & 2) | ((t >> 2) & 1);
 }
 
 template <int HD>
