@@ -8,7 +8,12 @@
  *   - returns hipSuccess without launching anything when the problem is empty
  *     (rows == 0, n == 0, n_tokens == 0);
  *   - otherwise enqueues its kernel(s) on `stream` and returns the launch status.
- *     It never synchronises, never allocates and never frees.
+ *     The kernel entry points never synchronise, allocate or free.  Exceptions,
+ *     each stated at its declaration: ql_gemm_f16 creates its per-device
+ *     library context on first use and allocates a 64 MB workspace the first
+ *     time it runs on a given stream (kept until the process ends); the
+ *     setup-time calls (ql_gemm_tune_f16, ql_engine_tune, ql_engine_create*,
+ *     ql_batcher_create, ql_graph_*) allocate, and the tuners synchronise.
  *
  * fp16 tensors are passed as `uint16_t*` holding IEEE-754 binary16 bit patterns
  * (the storage of `__half`).  Buffers must not alias unless an entry point says
@@ -204,6 +209,12 @@ hipError_t ql_paged_slot_mapping(const int32_t* block_table, int n_table, int st
 /* ---- fp16 -> fp32 widening (launch_fp16_to_fp32, kernels/fp16_ops.cu:103-110,149-153) */
 hipError_t ql_f16_to_f32(const uint16_t* src, float* dst, int64_t n, hipStream_t stream);
 
+/* ---- fp32 -> fp16 narrowing, round to nearest even (__float2half): the
+ * fp32_to_fp16_kernel of src/quant_forward.cu:18-21, launched by the fp32 engine's
+ * quantized GEMM bridge (sgemm, src/forward.cu:52-70: narrow A, quantlib FP8 GEMM,
+ * widen C).  Overflow gives +-inf, NaN stays NaN. */
+hipError_t ql_f32_to_f16(const float* src, uint16_t* dst, int64_t n, hipStream_t stream);
+
 /* ---- attention (fp16 I/O, fp32 softmax state, gfx950 matrix cores) ----------------
  * out[i, h, :] = sum_j softmax_j((q[i,h,:] . k[j,g,:]) * scale) v[j,g,:] with
  * g = h * n_kv_heads / n_heads (grouped-query heads, kernels/flash_attention.cu:45),
@@ -346,9 +357,11 @@ hipError_t ql_batcher_pop_finished(ql_batcher* b, ql_finished* ev, int32_t* toke
 
 /* ---- greedy sampling ----------------------------------------------------------------
  * out[r] = the first index of the maximum of row r (logits + r*ld, cols values): the
- * strict-">" scan of argmax_kernel (src/continuous_batch.cu:12-25,
- * src/fp16_forward.cu:259-283), batched over rows.  NaN never wins; a row with no
- * value above -inf gives 0. */
+ * strict-">" scan of argmax_kernel (src/continuous_batch.cu:12-25), batched over
+ * rows, starting from its -1e20f: NaN and values at or below -1e20 never win, and a
+ * row with no value above -1e20 gives 0.  (src/fp16_forward.cu:259-283 starts from
+ * -FLT_MAX; the two agree on every row holding a value above -1e20, which includes
+ * every binary16 row with a finite value.) */
 hipError_t ql_argmax_f32(const float* logits, int rows, int cols, int64_t ld, int32_t* out,
                          hipStream_t stream);
 hipError_t ql_argmax_f16(const uint16_t* logits, int rows, int cols, int64_t ld, int32_t* out,

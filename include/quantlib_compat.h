@@ -71,6 +71,12 @@ void launch_fp16_kvcache_append(__half* k_cache, __half* v_cache, const __half* 
                                 int head_dim, int max_seq, int n_layers,
                                 hipStream_t stream);
 
+/* src/quant_forward.cu:18-21 (fp32_to_fp16_kernel, launched by sgemm at
+ * src/forward.cu:62-64): dst[i] = __float2half(src[i]).  Its partner
+ * fp16_to_fp32_kernel (src/quant_forward.cu:23-26, src/forward.cu:66-67) is
+ * launch_fp16_to_fp32 above. */
+void launch_fp32_to_fp16(const float* src, __half* dst, int n, hipStream_t stream);
+
 /* ---- fp32 contiguous KV cache (include/kv_cache.h:12-36) ------------------- */
 typedef struct {
     float* k_cache; /* [n_layers * max_seq_len * n_heads * head_dim] */
@@ -130,8 +136,11 @@ void paged_kv_free_block(PagedKVCache* cache, int block_idx);
 /* ---- quantlib FP8 (quantlib_src/include/quant_types.h:15-45, quantlib.h:10-43) -----
  * Same types and names; the conversions run the reference's algorithm
  * (QL_FP8_MODE_REFERENCE of quantlib_amd.h) and, like the reference, allocate the
- * QuantMatrix's device buffers (freed by quantlib_free).  quantlib_fp8_gemm with
- * M > 64 dequantizes into a process-wide device buffer that grows on demand. */
+ * QuantMatrix's device buffers (freed by quantlib_free).  quantlib_fp8_gemm keeps
+ * its workspace (split-K partials, or the dequantized weights when M > 64) in a
+ * device buffer per (device, stream) that grows on demand: the first call with
+ * a larger need on a stream allocates (after waiting for that stream), so calls
+ * on different streams never share a buffer. */
 typedef uint8_t fp8_e4m3_t;
 typedef uint8_t fp8_e5m2_t;
 

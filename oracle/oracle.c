@@ -534,13 +534,14 @@ void or_matmul_f16(const uint16_t* x, const uint16_t* w, uint16_t* y, int M, int
 }
 
 /* argmax_kernel (src/continuous_batch.cu:12-25): the first index whose value is
- * strictly greater than all earlier ones; NaN never is; a row without a value
- * above -inf gives 0.
- * Pinned by: numpy argmax (first occurrence) on NaN-free rows; ties, all -inf and
- * NaN rows by closed forms (tests/test_oracle.py::test_argmax_*). */
+ * strictly greater than all earlier ones and than the start value -1e20f (:15);
+ * NaN never is; a row without a value above -1e20f gives 0.
+ * Pinned by: numpy argmax (first occurrence) on NaN-free rows; ties, all -inf,
+ * NaN rows and rows at or below -1e20 by closed forms
+ * (tests/test_oracle.py::test_argmax_*). */
 void or_argmax_f32(const float* x, int rows, int cols, int32_t* out) {
     for (int r = 0; r < rows; ++r) {
-        float best = -INFINITY;
+        float best = -1e20f;
         int32_t idx = 0;
         for (int c = 0; c < cols; ++c) {
             const float v = x[(size_t)r * cols + c];

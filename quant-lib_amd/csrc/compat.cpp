@@ -10,7 +10,9 @@
 
 #include <string.h>
 
+#include <map>
 #include <mutex>
+#include <utility>
 
 #include <hip/hip_runtime_api.h>
 
@@ -92,6 +94,11 @@ void launch_fp16_add(__half* x, const __half* y, int n, hipStream_t stream) {
 // kernels/fp16_ops.cu:149-153
 void launch_fp16_to_fp32(const __half* src, float* dst, int n, hipStream_t stream) {
     (void)ql_f16_to_f32(bits(src), dst, n, stream);
+}
+
+// src/quant_forward.cu:18-21
+void launch_fp32_to_fp16(const float* src, __half* dst, int n, hipStream_t stream) {
+    (void)ql_f32_to_f16(src, bits(dst), n, stream);
 }
 
 // kernels/flash_attention.cu:169-182
@@ -339,9 +346,17 @@ QuantMatrix fp16_to_fp8(const __half* src, int rows, int cols, QuantGranularity 
     return qm;
 }
 
+// quantlib_fp8_gemm's workspace (split-K partials, or the dequantized weights for
+// M > 64): one buffer per (device, stream), grown on demand, so calls on
+// different streams never share one.  The lock is held until the call's kernels
+// are enqueued: a concurrent call on the same stream that grows the buffer waits
+// for the stream before freeing the old one.
+struct Workspace {
+    void* p = nullptr;
+    size_t bytes = 0;
+};
 std::mutex g_ws_mu;
-void* g_ws = nullptr;
-size_t g_ws_bytes = 0;
+std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
 
 }  // namespace
 
@@ -372,22 +387,25 @@ extern "C" void quantlib_fp8_gemm(const __half* A, const QuantMatrix* W, __half*
     if (ql_fp8_gemm_workspace_size(M, N, K, (int)W->params.granularity, W->params.group_size, &need) !=
         hipSuccess)
         return;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return;
+    std::lock_guard<std::mutex> lock(g_ws_mu);
     if (need > 0) {
-        std::lock_guard<std::mutex> lock(g_ws_mu);
-        if (g_ws_bytes < need) {
-            if (g_ws) {
-                (void)hipStreamSynchronize(stream);
-                (void)hipFree(g_ws);
+        Workspace& slot = g_ws[std::make_pair(dev, stream)];
+        if (slot.bytes < need) {
+            if (slot.p) {
+                (void)hipStreamSynchronize(stream);   // earlier calls on this stream still use it
+                (void)hipFree(slot.p);
             }
-            if (hipMalloc(&g_ws, need) != hipSuccess) {
-                g_ws = nullptr;
-                g_ws_bytes = 0;
+            if (hipMalloc(&slot.p, need) != hipSuccess) {
+                slot.p = nullptr;
+                slot.bytes = 0;
                 return;
             }
-            g_ws_bytes = need;
+            slot.bytes = need;
         }
-        ws = g_ws;
-        ws_bytes = g_ws_bytes;
+        ws = slot.p;
+        ws_bytes = slot.bytes;
     }
     (void)ql_fp8_gemm_f16(bits(A), static_cast<const uint8_t*>(W->data), W->params.scales, M, N, K,
                           fp8_format_of(W), (int)W->params.granularity, W->params.group_size,

@@ -1,5 +1,5 @@
 // elementwise.hip -- streaming kernels for gfx950: SwiGLU, residual add,
-// binary16 -> fp32 widening, and the contiguous KV-cache append (a pair of
+// binary16 <-> fp32 conversions, and the contiguous KV-cache append (a pair of
 // copies).
 //
 // Every kernel moves each input once and each output once with 16-byte
@@ -136,6 +136,45 @@ __global__ __launch_bounds__(kBlock) void widen_stream(const _Float16* __restric
         for (long long i = nvec * W + threadIdx.x; i < n; i += kBlock) dst[i] = (float)src[i];
 }
 
+// fp32 -> binary16 narrowing, RNE (src/quant_forward.cu:18-21).  W = 8: each
+// thread reads two adjacent 16-byte vectors and writes one; a wavefront's two
+// loads together cover one contiguous 2 KiB span and its store 1 KiB.
+template <int W>
+__global__ __launch_bounds__(kBlock) void narrow_stream(const float* __restrict__ src,
+                                                        _Float16* __restrict__ dst, long long n) {
+    using VI = Vec<float, (W > 1 ? W / 2 : 1)>;
+    using VO = Vec<_Float16, W>;
+    constexpr int H = W > 1 ? 2 : 1;        // input vectors per output vector
+    constexpr int WI = W / H;
+    const long long nvec = n / W;
+    const long long base = (long long)blockIdx.x * (kBlock * kUnroll) + threadIdx.x;
+    VI r[kUnroll][H];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const long long i = base + (long long)u * kBlock;
+        if (i < nvec) {
+#pragma unroll
+            for (int h = 0; h < H; ++h)
+                r[u][h] = load<(W > 1)>(reinterpret_cast<const VI*>(src) + i * H + h);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const long long i = base + (long long)u * kBlock;
+        if (i < nvec) {
+            VO y;
+#pragma unroll
+            for (int h = 0; h < H; ++h)
+#pragma unroll
+                for (int e = 0; e < WI; ++e) y.v[h * WI + e] = from_f32<_Float16>(r[u][h].v[e]);
+            store<(W > 1)>(reinterpret_cast<VO*>(dst) + i, y);
+        }
+    }
+    if (W > 1 && blockIdx.x == 0)
+        for (long long i = nvec * W + threadIdx.x; i < n; i += kBlock)
+            dst[i] = from_f32<_Float16>(src[i]);
+}
+
 // Two independent copies in one launch (blockIdx.y selects the pair): the K
 // and V halves of a contiguous KV append.  16-byte units with nontemporal
 // access (one unit per thread measured fastest for a pure copy) when all four
@@ -246,6 +285,24 @@ extern "C" hipError_t ql_f16_to_f32(const uint16_t* src, float* dst, int64_t n,
     } else {
         hipLaunchKernelGGL((widen_stream<1>), dim3(qlh::blocks_for(n, (long long)kBlock * kUnroll)),
                            dim3(kBlock), 0, stream, s, dst, (long long)n);
+    }
+    return hipGetLastError();
+}
+
+extern "C" hipError_t ql_f32_to_f16(const float* src, uint16_t* dst, int64_t n,
+                                    hipStream_t stream) {
+    QL_CHECK_ARG(n >= 0);
+    if (n == 0) return hipSuccess;
+    QL_CHECK_ARG(src && dst);
+    _Float16* d = reinterpret_cast<_Float16*>(dst);
+    if (qlh::aligned16(src) && qlh::aligned16(dst)) {
+        const long long nvec = n / 8;
+        const unsigned grid = nvec > 0 ? qlh::blocks_for(nvec, (long long)kBlock * kUnroll) : 1;
+        hipLaunchKernelGGL((narrow_stream<8>), dim3(grid), dim3(kBlock), 0, stream, src, d,
+                           (long long)n);
+    } else {
+        hipLaunchKernelGGL((narrow_stream<1>), dim3(qlh::blocks_for(n, (long long)kBlock * kUnroll)),
+                           dim3(kBlock), 0, stream, src, d, (long long)n);
     }
     return hipGetLastError();
 }

@@ -636,22 +636,10 @@ __global__ __launch_bounds__(kBlock) void splitk_reduce(const float* __restrict_
 // per output per piece with the inverse from the workgroup's LDS table.  The KW
 // partial tiles of a row tile are summed in LDS in wavefront order.
 constexpr int kRowsChunk = 256;
-#ifndef QL_ROWS_STAGES
-#define QL_ROWS_STAGES 2
-#endif
-constexpr int kRowsStages = QL_ROWS_STAGES;   // register ring depth (chunks in flight)
-constexpr int kRowsMaxTokens = 8;              // more tokens: the register path is faster
-#ifndef QL_ROWS_CONTIG
-#define QL_ROWS_CONTIG 1
-#endif
-#ifndef QL_ROWS_OCP_WAVES
-#define QL_ROWS_OCP_WAVES 1024
-#endif
-#ifndef QL_ROWS_REF_WAVES
-#define QL_ROWS_REF_WAVES 2048
-#endif
-constexpr int kRowsOcpWaves = QL_ROWS_OCP_WAVES;   // wavefront budgets of the launch shape
-constexpr int kRowsRefWaves = QL_ROWS_REF_WAVES;
+constexpr int kRowsStages = 2;        // register ring depth (chunks in flight)
+constexpr int kRowsMaxTokens = 8;     // more tokens: the register path is faster
+constexpr int kRowsOcpWaves = 1024;   // wavefront budgets of the launch shape
+constexpr int kRowsRefWaves = 2048;
 constexpr int kRowsTableFloats = 4096;
 constexpr uint32_t kBufferWord3 = 0x00020000u;          // raw buffer, 32-bit dwords (gfx9)
 
@@ -761,17 +749,11 @@ __global__ __launch_bounds__(RW * KW * kWave) void fp8_gemm_rows(SkinnyArgs p) {
     // never used, and the waits count every round's loads exactly); the remaining
     // chunks are computed without refills.
     constexpr int NS = kRowsStages;
-#if QL_ROWS_CONTIG
     // wavefront kp of a row tile takes the kp-th contiguous run of the split's chunks
     constexpr int CS = 1;
     const int per_w = (c_end - c_begin + KW - 1) / KW;
     const int first = c_begin + kp * per_w;   // wave-uniform
     const int w_end = min(c_end, first + per_w);
-#else
-    constexpr int CS = KW;
-    const int first = c_begin + kp;           // wave-uniform
-    const int w_end = c_end;
-#endif
     if (first < w_end) {
         const int n_mine = (w_end - 1 - first) / CS + 1;
         const int last = first + CS * (n_mine - 1);

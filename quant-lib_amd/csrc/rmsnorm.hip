@@ -125,94 +125,62 @@ __global__ __launch_bounds__(WPR <= 4 ? kBlock : kWave * WPR) void rmsnorm_rows(
     }
 }
 
-// Persistent variant: a workgroup of WPR wavefronts walks rows blockIdx.x,
-// blockIdx.x + gridDim.x, ..., prefetching the next row's x (and d) into
-// registers before reducing the current one, so HBM reads overlap the
-// reduction and the stores.  The LDS partials are double-buffered, so one
-// barrier per row suffices.
-template <typename D, int NV, int WPR, bool ADD>
-__global__ __launch_bounds__(kWave * WPR) void rmsnorm_pipe(D* x, const D* __restrict__ d,
-                                                           const D* __restrict__ w,
-                                                           D* __restrict__ out, int rows,
-                                                           int dim, float eps) {
+// One wavefront per row (launched with grid = rows, 64-thread workgroups): the
+// row's NV vectors per lane are loaded, reduced with the wave64 butterfly alone
+// (no LDS, no barrier) and written.  Used below 4096 rows, where one small
+// workgroup per row fills the chip better than row groups.
+template <typename D, int NV, bool ADD>
+__global__ __launch_bounds__(kWave) void rmsnorm_wave(D* x, const D* __restrict__ d,
+                                                     const D* __restrict__ w,
+                                                     D* __restrict__ out, int dim, float eps) {
     constexpr int W = vec16<D>();
-    constexpr int TPR = kWave * WPR;
     using V = Vec<D, W>;
-    __shared__ float red[2][WPR];
     const int rl = threadIdx.x;
     const int nvec = dim / W;
+    const size_t row = blockIdx.x;
     const V* wr = reinterpret_cast<const V*>(w);
-    V wv[NV];
+    const V* xr = reinterpret_cast<const V*>(x + row * dim);
+    const V* dr = reinterpret_cast<const V*>(ADD ? d + row * dim : d);
+    V cx[NV], cd[ADD ? NV : 1], wv[NV];
 #pragma unroll
-    for (int k = 0; k < NV; ++k)
-        if (rl + k * TPR < nvec) wv[k] = wr[rl + k * TPR];
-
-    V cx[NV], cd[ADD ? NV : 1];
-    int row = blockIdx.x;
-    if (row < rows) {
+    for (int k = 0; k < NV; ++k) {
+        const int vi = rl + k * kWave;
+        if (vi < nvec) {
+            cx[k] = load<true>(xr + vi);
+            if constexpr (ADD) cd[k] = load<true>(dr + vi);
+            wv[k] = wr[vi];   // shared by every row: keep it cached
+        }
+    }
+    float ss = 0.0f;
 #pragma unroll
-        for (int k = 0; k < NV; ++k) {
-            const int vi = rl + k * TPR;
-            if (vi < nvec) {
-                cx[k] = load<true>(reinterpret_cast<const V*>(x + (size_t)row * dim) + vi);
-                if constexpr (ADD) cd[k] = load<true>(reinterpret_cast<const V*>(d + (size_t)row * dim) + vi);
+    for (int k = 0; k < NV; ++k) {
+        if (rl + k * kWave < nvec) {
+#pragma unroll
+            for (int e = 0; e < W; ++e) {
+                float a = to_f32(cx[k].v[e]);
+                if constexpr (ADD) {
+                    a = a + to_f32(cd[k].v[e]);
+                    cx[k].v[e] = from_f32<D>(a);
+                    a = to_f32(cx[k].v[e]);
+                }
+                ss = fmaf(a, a, ss);
             }
         }
     }
-    for (int it = 0; row < rows; row += gridDim.x, ++it) {
-        const int nrow = row + gridDim.x;
-        V nx[NV], nd[ADD ? NV : 1];
-        if (nrow < rows) {
+    ss = wave_sum(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+    V* xw = reinterpret_cast<V*>(x + row * dim);
+    V* orow = reinterpret_cast<V*>(out + row * dim);
 #pragma unroll
-            for (int k = 0; k < NV; ++k) {
-                const int vi = rl + k * TPR;
-                if (vi < nvec) {
-                    nx[k] = load<true>(reinterpret_cast<const V*>(x + (size_t)nrow * dim) + vi);
-                    if constexpr (ADD) nd[k] = load<true>(reinterpret_cast<const V*>(d + (size_t)nrow * dim) + vi);
-                }
-            }
-        }
-        float ss = 0.0f;
+    for (int k = 0; k < NV; ++k) {
+        const int vi = rl + k * kWave;
+        if (vi < nvec) {
+            V y;
 #pragma unroll
-        for (int k = 0; k < NV; ++k) {
-            if (rl + k * TPR < nvec) {
-#pragma unroll
-                for (int e = 0; e < W; ++e) {
-                    float a = to_f32(cx[k].v[e]);
-                    if constexpr (ADD) {
-                        a = a + to_f32(cd[k].v[e]);
-                        cx[k].v[e] = from_f32<D>(a);
-                        a = to_f32(cx[k].v[e]);
-                    }
-                    ss = fmaf(a, a, ss);
-                }
-            }
-        }
-        ss = wave_sum(ss);
-        if ((rl & (kWave - 1)) == 0) red[it & 1][rl / kWave] = ss;
-        __syncthreads();
-        ss = 0.0f;
-#pragma unroll
-        for (int i = 0; i < WPR; ++i) ss += red[it & 1][i];
-        const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
-        V* xr = reinterpret_cast<V*>(x + (size_t)row * dim);
-        V* orow = reinterpret_cast<V*>(out + (size_t)row * dim);
-#pragma unroll
-        for (int k = 0; k < NV; ++k) {
-            const int vi = rl + k * TPR;
-            if (vi < nvec) {
-                V y;
-#pragma unroll
-                for (int e = 0; e < W; ++e)
-                    y.v[e] = from_f32<D>((to_f32(cx[k].v[e]) * inv) * to_f32(wv[k].v[e]));
-                if constexpr (ADD) store<true>(xr + vi, cx[k]);
-                store<true>(orow + vi, y);
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < NV; ++k) {
-            cx[k] = nx[k];
-            if constexpr (ADD) cd[k] = nd[k];
+            for (int e = 0; e < W; ++e)
+                y.v[e] = from_f32<D>((to_f32(cx[k].v[e]) * inv) * to_f32(wv[k].v[e]));
+            if constexpr (ADD) store<true>(xw + vi, cx[k]);
+            store<true>(orow + vi, y);
         }
     }
 }
@@ -280,17 +248,17 @@ hipError_t rmsnorm_dispatch(D* x, const D* d, const D* w, D* out, int rows, int 
         // over 512-thread groups when the whole problem is a few tens of MB.
         const unsigned grid = (unsigned)rows;
         if (nvec <= 64)
-            hipLaunchKernelGGL((rmsnorm_pipe<D, 1, 1, ADD>), dim3(grid), dim3(kWave), 0, stream, x,
-                               d, w, out, rows, dim, eps);
+            hipLaunchKernelGGL((rmsnorm_wave<D, 1, ADD>), dim3(grid), dim3(kWave), 0, stream, x,
+                               d, w, out, dim, eps);
         else if (nvec <= 128)
-            hipLaunchKernelGGL((rmsnorm_pipe<D, 2, 1, ADD>), dim3(grid), dim3(kWave), 0, stream, x,
-                               d, w, out, rows, dim, eps);
+            hipLaunchKernelGGL((rmsnorm_wave<D, 2, ADD>), dim3(grid), dim3(kWave), 0, stream, x,
+                               d, w, out, dim, eps);
         else if (nvec <= 256)
-            hipLaunchKernelGGL((rmsnorm_pipe<D, 4, 1, ADD>), dim3(grid), dim3(kWave), 0, stream, x,
-                               d, w, out, rows, dim, eps);
+            hipLaunchKernelGGL((rmsnorm_wave<D, 4, ADD>), dim3(grid), dim3(kWave), 0, stream, x,
+                               d, w, out, dim, eps);
         else
-            hipLaunchKernelGGL((rmsnorm_pipe<D, 8, 1, ADD>), dim3(grid), dim3(kWave), 0, stream, x,
-                               d, w, out, rows, dim, eps);
+            hipLaunchKernelGGL((rmsnorm_wave<D, 8, ADD>), dim3(grid), dim3(kWave), 0, stream, x,
+                               d, w, out, dim, eps);
         return hipGetLastError();
     }
     if (vec_ok) {

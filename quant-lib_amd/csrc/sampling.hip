@@ -1,9 +1,12 @@
 // sampling.hip -- greedy token selection over rows of logits.
 //
-// argmax_kernel (src/continuous_batch.cu:12-25) and argmax_kernel
-// (src/fp16_forward.cu:259-283) pick, for one row, the first index whose value
-// is strictly greater than every earlier one (NaN never compares greater; a row
-// with nothing above the start value gives 0).  Here one workgroup handles one
+// argmax_kernel (src/continuous_batch.cu:12-25) picks, for one row, the first
+// index whose value is strictly greater than every earlier one and than the
+// start value -1e20f (:15); NaN never compares greater, and a row with nothing
+// above -1e20f gives 0.  (The fp16 engine's argmax_kernel,
+// src/fp16_forward.cu:259-283, starts from -FLT_MAX instead: the two agree on
+// every row that holds a value above -1e20f, which every binary16 row with a
+// finite value does.)  Here one workgroup handles one
 // row of a batch: each lane keeps its first strict maximum over a strided pass
 // (16-byte loads when the row allows), then (value, index) pairs are reduced
 // preferring the larger value and, on equal values, the smaller index -- the
@@ -18,6 +21,8 @@ namespace {
 
 using namespace ql;
 
+constexpr float kStart = -1e20f;   // src/continuous_batch.cu:15
+
 __device__ __forceinline__ void better(float& v, int& i, float v2, int i2) {
     if (v2 > v || (v2 == v && i2 < i)) {
         v = v2;
@@ -29,7 +34,7 @@ template <typename D, bool VEC>
 __global__ __launch_bounds__(kBlock) void argmax_rows(const D* __restrict__ x, int cols, int64_t ld,
                                                       int32_t* __restrict__ out) {
     const D* row = x + (size_t)blockIdx.x * (size_t)ld;
-    float best = -INFINITY;
+    float best = kStart;
     int idx = INT_MAX;   // none yet
     if constexpr (VEC) {
         constexpr int W = vec16<D>();
@@ -61,7 +66,7 @@ __global__ __launch_bounds__(kBlock) void argmax_rows(const D* __restrict__ x, i
             }
         }
     }
-    // lanes that saw only -inf / NaN keep (-inf, INT_MAX) and never win a tie
+    // lanes that saw nothing above the start keep (kStart, INT_MAX) and never win a tie
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         const float v2 = __shfl_xor(best, o, kWave);
@@ -78,7 +83,7 @@ __global__ __launch_bounds__(kBlock) void argmax_rows(const D* __restrict__ x, i
     __syncthreads();
     if (threadIdx.x == 0) {
         for (int w = 1; w < kBlock / kWave; ++w) better(best, idx, sv[w], si[w]);
-        out[blockIdx.x] = (idx == INT_MAX || !(best > -INFINITY)) ? 0 : idx;
+        out[blockIdx.x] = idx == INT_MAX ? 0 : idx;
     }
 }
 

@@ -56,6 +56,7 @@ SIGNATURES = {
     "ql_paged_kv_append_f16": [_p, _p, _i, _p, _p, _p, _i, _i, _i, _i, _i, _p],
     "ql_paged_slot_mapping": [_p, _i, _i, _i, _p],
     "ql_f16_to_f32": [_p, _p, _i64, _p],
+    "ql_f32_to_f16": [_p, _p, _i64, _p],
     "ql_flash_attention_f16": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p],
     "ql_attention_f16": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _i64, _i64, _i64, _i, _p],
     "ql_paged_attention_f16": [_p, _p, _i64, _i64, _i, _i, _p, _p, _i, _p, _i, _p, _p, _i, _i, _i,

@@ -24,6 +24,7 @@ COMPAT_MANGLED = {
     "launch_fp16_embed": "_Z17launch_fp16_embedPK6__halfPS_iiP12ihipStream_t",
     "launch_fp16_add": "_Z15launch_fp16_addP6__halfPKS_iP12ihipStream_t",
     "launch_fp16_to_fp32": "_Z19launch_fp16_to_fp32PK6__halfPfiP12ihipStream_t",
+    "launch_fp32_to_fp16": "_Z19launch_fp32_to_fp16PKfP6__halfiP12ihipStream_t",
     "launch_flash_attention": "_Z22launch_flash_attentionPK6__halfS1_S1_PS_iiiiiP12ihipStream_t",
     "add_residual": "_Z12add_residualPfPKfiP12ihipStream_t",
     "launch_embed": "_Z12launch_embedPfPKfiiP12ihipStream_t",
@@ -110,6 +111,9 @@ P = 4096  # a non-null, 16-byte aligned dummy address: never dereferenced on the
     (("ql_paged_kv_append_f16", P, P, 4, P, P, P, 10, 4, 4, 8, 128, None), INVALID),  # layer
     (("ql_paged_kv_append_f16", P, None, 4, P, P, P, 10, 0, 4, 8, 128, None), INVALID),
     (("ql_f16_to_f32", P, P, -1, None), INVALID),
+    (("ql_f32_to_f16", P, P, -1, None), INVALID),
+    (("ql_f32_to_f16", P, None, 5, None), INVALID),
+    (("ql_f32_to_f16", None, None, 0, None), 0),
     # fused RoPE + append: v missing, layer out of range, v stride too small, pos+T > max_seq
     (("ql_rope_paged_kv_append_f16", P, P, None, 4, 8, 2, 64, 512, 128, 128, None, 0, 1e4, 1,
       P, P, 4, P, 0, 2, None), INVALID),

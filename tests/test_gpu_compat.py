@@ -294,3 +294,76 @@ def test_quantlib_fp8_gemm_shim(M):
                           np.abs(f16_bits_to_f32(a)).astype(np.float64) @ np.abs(f16_bits_to_f32(wd)).T)
     assert np.all(np.abs(f16_bits_to_f32(host(out, shape=(M, N))) - f16_bits_to_f32(want)) <= bound)
     qfree(ctypes.byref(qm))
+
+
+def test_quantlib_fp8_gemm_shim_on_two_streams():
+    """Two quantlib_fp8_gemm calls in flight at once on two streams, one on the
+    split-K register path (16 rows) and one on the dequantize path (128 rows):
+    each stream has its own workspace, so both match the oracle.  Repeated so
+    the second round reuses the grown buffers."""
+    to_e4m3 = fn("quantlib_fp16_to_fp8_e4m3", [_p, _i, _i, _i, _i, _p], QuantMatrix)
+    gemm = fn("quantlib_fp8_gemm", [_p, ctypes.POINTER(QuantMatrix), _p, _i, _i, _i, _p])
+    qfree = fn("quantlib_free", [ctypes.POINTER(QuantMatrix)])
+    s2 = ctypes.c_void_p()
+    ql.hip_check(ql.hip().hipStreamCreate(ctypes.byref(s2)), "hipStreamCreate")
+    N, K = 1024, 4096
+    w = to_f16_bits(normal(15, (N, K), K ** -0.5))
+    dw = dev(w)
+    qm = to_e4m3(ptr(dw), N, K, 2, 128, stream())
+    sync()
+    q, sc = orc.fp8_quantize(w, 0, 2, 128, 0)
+    wd = orc.fp8_dequantize(q, sc, 0, 2, 128, 0)
+    cases = []
+    for M, s in ((16, stream()), (128, s2.value)):
+        a = to_f16_bits(normal(16 + M, (M, K)))
+        want = orc.matmul(a, wd)
+        bound = 2.0 ** -10 * (np.abs(f16_bits_to_f32(want)) +
+                              np.abs(f16_bits_to_f32(a)).astype(np.float64) @ np.abs(f16_bits_to_f32(wd)).T)
+        cases.append((M, s, dev(a), empty((M * N,), np.uint16), want, bound))
+    for _ in range(2):
+        for M, s, da, out, _, _ in cases:
+            out.fill_bytes(0xFF)
+        for rep in range(3):      # interleave enqueues on the two streams
+            for M, s, da, out, _, _ in cases:
+                gemm(ptr(da), ctypes.byref(qm), ptr(out), M, N, K, s)
+        ql.hip_check(ql.hip().hipStreamSynchronize(s2.value), "hipStreamSynchronize")
+        sync()
+        for M, s, da, out, want, bound in cases:
+            got = f16_bits_to_f32(host(out, shape=(M, N)))
+            assert np.all(np.abs(got - f16_bits_to_f32(want)) <= bound), M
+    qfree(ctypes.byref(qm))
+
+
+@pytest.mark.parametrize("M", [1, 100])
+def test_fp32_quantized_gemm_bridge(M):
+    """The fp32 engine's quantized GEMM (sgemm, src/forward.cu:52-70) through the
+    shims: launch_fp32_to_fp16 on A, quantlib_fp8_gemm, launch_fp16_to_fp32 on C.
+    The narrowed A is bit-exact (RNE), C within the FP8 GEMM bound, and the widened
+    C is exactly the binary16 C."""
+    to_e4m3 = fn("quantlib_fp16_to_fp8_e4m3", [_p, _i, _i, _i, _i, _p], QuantMatrix)
+    gemm = fn("quantlib_fp8_gemm", [_p, ctypes.POINTER(QuantMatrix), _p, _i, _i, _i, _p])
+    qfree = fn("quantlib_free", [ctypes.POINTER(QuantMatrix)])
+    narrow = fn("launch_fp32_to_fp16", [_p, _p, _i, _p])
+    widen = fn("launch_fp16_to_fp32", [_p, _p, _i, _p])
+    N, K = 512, 1024
+    w = to_f16_bits(normal(25, (N, K), K ** -0.5))
+    a32 = normal(26 + M, (M, K))
+    dw, da32 = dev(w), dev(a32)
+    qm = to_e4m3(ptr(dw), N, K, 2, 128, stream())
+    ha, hc = empty((M * K,), np.uint16), empty((M * N,), np.uint16)
+    c32 = empty((M * N,), np.float32)
+    narrow(ptr(da32), ptr(ha), M * K, stream())
+    gemm(ptr(ha), ctypes.byref(qm), ptr(hc), M, N, K, stream())
+    widen(ptr(hc), ptr(c32), M * N, stream())
+    sync()
+    a16 = orc.f32_to_f16(a32)
+    assert np.array_equal(host(ha, shape=(M, K)), a16)
+    q, sc = orc.fp8_quantize(w, 0, 2, 128, 0)
+    wd = orc.fp8_dequantize(q, sc, 0, 2, 128, 0)
+    want = orc.matmul(a16, wd)
+    bound = 2.0 ** -10 * (np.abs(f16_bits_to_f32(want)) +
+                          np.abs(f16_bits_to_f32(a16)).astype(np.float64) @ np.abs(f16_bits_to_f32(wd)).T)
+    c16 = host(hc, shape=(M, N))
+    assert np.all(np.abs(f16_bits_to_f32(c16) - f16_bits_to_f32(want)) <= bound)
+    assert np.array_equal(host(c32, shape=(M, N)), f16_bits_to_f32(c16))
+    qfree(ctypes.byref(qm))

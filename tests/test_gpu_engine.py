@@ -35,6 +35,13 @@ def test_argmax_matches_oracle(rows, cols, pad, f16):
         x[0, :] = -np.inf
         x[1, :cols // 2] = np.nan
         x[2, 7 % cols] = x[2, (cols - 1)] = 50.0          # tie: first index wins
+    if rows >= 5 and not f16:
+        # the scan's start value -1e20f (src/continuous_batch.cu:15): a row at or
+        # below it gives 0; in the next one the last value is the first above it
+        x[3, :] = -1e20
+        x[3, cols // 3] = -np.inf
+        x[4, :] = -2e20
+        x[4, cols - 1] = -9.9e19
     if f16:
         xb = to_f16_bits(x)
         want = orc.argmax(f16_bits_to_f32(xb)[:, :cols])

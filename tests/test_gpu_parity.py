@@ -49,6 +49,56 @@ def test_rmsnorm_f16(rows, dim):
     check_f16(out.get((rows, dim)), orc.rmsnorm(x, w, 1e-5, f16=True), f"rmsnorm f16 {rows}x{dim}")
 
 
+# At 4096 rows and more the vector path spreads each row over 1..16 wavefronts
+# (the wavefronts-per-row count follows the width), so every instantiation of
+# the many-rows kernel runs here, plain and fused, including the C5 final-norm
+# shape (fp16 8192 x 4096), ragged widths and a row count that leaves a partial
+# workgroup.
+MANY_ROWS_F16 = [(8192, 4096), (4096, 512), (4096, 1024), (4096, 2048), (4097, 1000), (4096, 8192),
+                 (4099, 64)]
+MANY_ROWS_F32 = [(4096, 256), (4096, 512), (4096, 1024), (4096, 2048), (4099, 1000), (4096, 4096),
+                 (4097, 36)]
+
+
+@pytest.mark.parametrize("add", [False, True])
+@pytest.mark.parametrize("rows,dim", MANY_ROWS_F16)
+def test_rmsnorm_f16_many_rows(rows, dim, add):
+    x = _f16(normal(0x51A10061 + dim, (rows, dim)))
+    d = _f16(normal(0x51A10062 + dim, (rows, dim)))
+    w = _f16(uniform(0x51A10063 + dim, dim, 0.5, 1.5))
+    out = Out(rows * dim, np.uint16)
+    dx, dd, dw = dev(x), dev(d), dev(w)
+    if add:
+        ql.call("ql_add_rmsnorm_f16", ptr(dx), ptr(dd), ptr(dw), out.ptr, rows, dim, 1e-5, stream())
+        want_x, want = orc.add_rmsnorm(x, d, w, 1e-5, f16=True)
+        assert np.array_equal(host(dx, shape=(rows, dim)), want_x)
+    else:
+        ql.call("ql_rmsnorm_f16", ptr(dx), ptr(dw), out.ptr, rows, dim, 1e-5, stream())
+        want = orc.rmsnorm(x, w, 1e-5, f16=True)
+        assert np.array_equal(host(dx, shape=(rows, dim)), x)     # input untouched
+    check_f16(out.get((rows, dim)), want, f"{'add_' if add else ''}rmsnorm f16 {rows}x{dim}")
+
+
+@pytest.mark.parametrize("add", [False, True])
+@pytest.mark.parametrize("rows,dim", MANY_ROWS_F32)
+def test_rmsnorm_f32_many_rows(rows, dim, add):
+    x = normal(0x51A10071 + dim, (rows, dim))
+    d = normal(0x51A10072 + dim, (rows, dim))
+    w = uniform(0x51A10073 + dim, dim, 0.5, 1.5)
+    out = Out(rows * dim, np.float32)
+    dx, dd, dw = dev(x), dev(d), dev(w)
+    if add:
+        ql.call("ql_add_rmsnorm_f32", ptr(dx), ptr(dd), ptr(dw), out.ptr, rows, dim, 1e-5, stream())
+        want_x, want = orc.add_rmsnorm(x, d, w, 1e-5)
+        assert np.array_equal(host(dx, shape=(rows, dim)), want_x)
+    else:
+        ql.call("ql_rmsnorm_f32", ptr(dx), ptr(dw), out.ptr, rows, dim, 1e-5, stream())
+        want = orc.rmsnorm(x, w, 1e-5)
+        assert np.array_equal(host(dx, shape=(rows, dim)), x)
+    check_close(out.get((rows, dim)), want, RTOL_F32, ATOL_F32,
+                f"{'add_' if add else ''}rmsnorm f32 {rows}x{dim}")
+
+
 @pytest.mark.parametrize("f16", [False, True])
 def test_rmsnorm_unaligned_pointers(f16):
     rows, dim = 9, 2048
@@ -403,6 +453,31 @@ def test_f16_to_f32_bit_exact(n):
     nan = np.isnan(want)
     assert np.array_equal(np.isnan(got), nan)
     assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+# ---- fp32 -> fp16 (the fp32 engine's quantized GEMM bridge) ------------------------------------
+def _narrow_inputs():
+    h = np.arange(0, 0x7bff, dtype=np.uint16)
+    lo = h.view(np.float16).astype(np.float64)
+    mid = ((lo + (h + 1).view(np.float16).astype(np.float64)) / 2).astype(np.float32)   # ties
+    bits = np.random.default_rng(9).integers(0, 2 ** 32, size=1 << 20, dtype=np.uint64).astype(np.uint32)
+    special = np.array([65504.0, 65519.996, 65520.0, 1e9, 2.0 ** -24, 2.0 ** -25, 2.0 ** -14, -0.0,
+                        np.inf, -np.inf, np.nan], np.float32)
+    return np.concatenate([mid, -mid, np.nextafter(mid, np.float32(0)), bits.view(np.float32), special])
+
+
+@pytest.mark.parametrize("offset,n", [(0, None), (1, 1001), (0, 13)])
+def test_f32_to_f16_bit_exact(offset, n):
+    x = _narrow_inputs()
+    if n is not None:
+        x = x[-n:]
+    out = Out(x.size, np.uint16, offset=offset)
+    dx = dev(x, offset_elems=offset)
+    ql.call("ql_f32_to_f16", ptr(dx), out.ptr, x.size, stream())
+    got, want = out.get(), orc.f32_to_f16(x)
+    nan = np.isnan(x)
+    assert np.all((got[nan] & 0x7c00) == 0x7c00) and np.all((got[nan] & 0x3ff) != 0)
+    assert np.array_equal(got[~nan], want[~nan])
 
 
 # ---- fused RoPE + KV-cache append ----------------------------------------------------------

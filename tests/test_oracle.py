@@ -450,6 +450,11 @@ def test_argmax_first_maximum_and_special_rows():
     nan = np.array([[np.nan, 2.0, np.nan, 5.0, np.nan]], np.float32)
     assert orc.argmax(nan)[0] == 3                      # NaN never wins
     assert orc.argmax(np.full((1, 3), np.nan, np.float32))[0] == 0
+    # the scan starts from -1e20f (src/continuous_batch.cu:15): values at or below
+    # it never win, so such a row gives 0, and the first value above it wins
+    assert orc.argmax(np.array([[-3e20, -1e21, -1e20]], np.float32))[0] == 0
+    assert orc.argmax(np.array([[-3e20, -1e21, -9.9e19, -1e19]], np.float32))[0] == 3
+    assert orc.argmax(np.array([[-1e30, -9.9e19, -1e20]], np.float32))[0] == 1
 
 
 # ---- FP8 codec ----------------------------------------------------------------------------
@@ -526,6 +531,67 @@ def test_fp8_reference_codec_truncates(fmt):
             assert d <= x < d + 2.0 ** (math.floor(math.log2(d)) - mb)
 
 
+def simulate_reference_scale_kernel(xf, group_size, fmax, block=128, warp=32):
+    """compute_scales_fp8 (quantlib_src/kernels/fp8_convert.cu:15-34, launched with
+    one 128-thread block per group at :123/:149) executed thread by thread: each
+    thread folds fmaxf(|x|) over i = tid, tid + blockDim, ... < group_size (and
+    inside the matrix), every warp runs the __shfl_down_sync tree for masks
+    16..1 (lane l reads lane l + mask when that lane is inside the warp, else
+    keeps its own value), and thread 0 writes fp8_max / max, or 1 below 1e-8.
+    Written from the kernel's structure, not from which offsets it sees."""
+    n = xf.size
+    n_groups = -(-n // group_size)
+    out = np.empty(n_groups, np.float32)
+    a = np.abs(xf.astype(np.float32))
+    for grp in range(n_groups):
+        offset = grp * group_size
+        local = np.zeros(block, np.float32)
+        for tid in range(block):
+            i = tid
+            while i < group_size and offset + i < n:
+                local[tid] = np.fmax(local[tid], a[offset + i])
+                i += block
+        for w0 in range(0, block, warp):
+            lanes = local[w0:w0 + warp]
+            mask = warp // 2
+            while mask > 0:
+                src = lanes.copy()                  # every lane reads before any writes
+                for lane in range(warp):
+                    other = src[lane + mask] if lane + mask < warp else src[lane]
+                    lanes[lane] = np.fmax(lanes[lane], other)
+                mask //= 2
+        m = local[0]                                # thread 0 = lane 0 of warp 0
+        out[grp] = np.float32(1.0) if m < np.float32(1e-8) else np.float32(np.float32(fmax) / m)
+    return out
+
+
+@pytest.mark.parametrize("rows,cols,gran,gs", [
+    (3, 1000, 2, 7), (5, 33, 1, 0), (2, 300, 0, 0), (4, 160, 2, 200), (1, 4096, 2, 1000),
+    (6, 96, 2, 40)])
+@pytest.mark.parametrize("fmt", [E4M3, E5M2])
+def test_fp8_reference_scales_match_kernel_simulation(rows, cols, gran, gs, fmt):
+    """Reference-mode scales of the oracle against the thread-level simulation of the
+    reference kernel, on groups shorter and longer than the block, ragged last
+    groups, and inputs whose largest magnitude sits at each offset mod 128 in turn
+    (most of them unseen by the reference's reduction)."""
+    fmax = 448.0 if fmt == E4M3 else 57344.0
+    g = rows * cols if gran == 0 else (cols if gran == 1 else gs)
+    base = to_f16_bits(uniform(rows * cols + gs, (rows, cols), -1.0, 1.0))
+    for spike in list(range(0, 128, 9)) + [None]:
+        x = base.copy()
+        if spike is not None:                # plant a large value at offset spike of each group
+            flat = x.reshape(-1)
+            for start in range(0, flat.size, g):
+                if start + spike < min(flat.size, start + g):
+                    flat[start + spike] = to_f16_bits(np.array([-7.5], np.float32))[0]
+        q, sc = orc.fp8_quantize(x, fmt, gran, gs, REF)
+        want = simulate_reference_scale_kernel(f16_bits_to_f32(x).ravel(), g, fmax)
+        assert np.array_equal(sc, want), (spike, sc[:4], want[:4])
+    # a group of zeros takes the scale 1 (below 1e-8)
+    z = np.zeros((2, 64), np.uint16)
+    assert np.array_equal(orc.fp8_quantize(z, fmt, 1, 0, REF)[1], np.ones(2, np.float32))
+
+
 @pytest.mark.parametrize("mode", [REF, OCP])
 @pytest.mark.parametrize("gran,gs", [(0, 0), (1, 0), (2, 128), (2, 100)])
 def test_fp8_quantize_scales_and_reference_error_bar(mode, gran, gs):
@@ -537,10 +603,13 @@ def test_fp8_quantize_scales_and_reference_error_bar(mode, gran, gs):
         g = 64 * 256 if gran == 0 else (256 if gran == 1 else gs)
         assert sc.size == -(-x.size // g)
         xf = f16_bits_to_f32(x).ravel()
-        for i in range(sc.size):   # the scale rule of each mode
-            grp = np.abs(xf[i * g:(i + 1) * g])
-            seen = grp if mode == OCP else grp[(np.arange(grp.size) % 128) < 32]
-            assert sc[i] == np.float32(np.float32(448.0 if fmt == E4M3 else 57344.0) / np.float32(seen.max()))
+        fmax = 448.0 if fmt == E4M3 else 57344.0
+        if mode == OCP:          # the whole group's max
+            for i in range(sc.size):
+                m = np.abs(xf[i * g:(i + 1) * g]).max()
+                assert sc[i] == np.float32(np.float32(fmax) / np.float32(m))
+        else:                    # the reference kernel, thread by thread
+            assert np.array_equal(sc, simulate_reference_scale_kernel(xf, g, fmax))
         back = f16_bits_to_f32(orc.fp8_dequantize(q, sc, fmt, gran, gs, mode))
         err = float(np.abs(back - f16_bits_to_f32(x)).max())
         assert err < 0.25, err
