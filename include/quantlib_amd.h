@@ -282,6 +282,31 @@ hipError_t ql_paged_decode_attention_f16(const uint16_t* q, uint16_t* out, int64
                                          int head_dim, void* workspace, size_t workspace_bytes,
                                          hipStream_t stream);
 
+/* ql_paged_decode_attention_f16 for callers that cannot allocate (code under HIP
+ * graph capture, serving loops that forbid hipMalloc): no workspace argument and no
+ * allocation.  It runs the key split that ql_paged_decode_workspace_size sizes --
+ * the same kernels and results as ql_paged_decode_attention_f16 given that many
+ * workspace bytes -- with the partials in a library-owned device array of
+ * QL_DECODE_SCRATCH_BYTES per GPU, held until the process ends.  A problem whose
+ * split would need more (possible only with more than 8 query heads per KV head at
+ * head_dim 128 and several hundred sequences) returns hipErrorInvalidValue before
+ * touching the GPU.  Nothing in the array needs clearing: every split writes its
+ * partials before the combine reads them.  Every call on one GPU shares that
+ * GPU's array, so calls that overlap on one GPU (two streams, two host threads)
+ * race; order them on one stream.  The first call on each device looks up the
+ * array's device address (hipGetSymbolAddress); make it outside graph capture.
+ * No counterpart in the reference. */
+#define QL_DECODE_SCRATCH_BYTES (8u << 20)
+hipError_t ql_paged_decode_attention_f16_noalloc(const uint16_t* q, uint16_t* out,
+                                                 int64_t q_row_stride, int64_t out_row_stride,
+                                                 int n_seqs, const int32_t* ctx_lens,
+                                                 int max_ctx_len, const int32_t* block_tables,
+                                                 int max_blocks_per_seq,
+                                                 const uint16_t* const* k_blocks,
+                                                 const uint16_t* const* v_blocks, int n_blocks,
+                                                 int layer, int n_layers, int n_heads,
+                                                 int n_kv_heads, int head_dim, hipStream_t stream);
+
 /* ---- continuous batching over the paged pool (host only, no GPU calls) -------------
  * The bookkeeping of the reference scheduler (scheduler_create / scheduler_add_request
  * / scheduler_step, src/continuous_batch.cu:48-174, include/scheduler.h:6-54) over the

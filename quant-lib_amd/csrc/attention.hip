@@ -42,6 +42,15 @@
 #include <math.h>
 #include <float.h>
 
+#include <mutex>
+
+// Key-split partials of ql_paged_decode_attention_f16_noalloc: a library-owned
+// device array, one copy per GPU, reached through its device address (resolved
+// once per device by hipGetSymbolAddress in decode_scratch()); host code never
+// passes the array's name itself to a kernel or a copy.
+constexpr size_t kDecodeScratchBytes = (size_t)QL_DECODE_SCRATCH_BYTES;
+static __device__ __align__(256) float scratch[kDecodeScratchBytes / sizeof(float)];
+
 namespace {
 
 using namespace ql;
@@ -1205,12 +1214,40 @@ extern "C" hipError_t ql_paged_decode_workspace_size(int n_seqs, int n_heads, in
     return hipSuccess;
 }
 
-extern "C" hipError_t ql_paged_decode_attention_f16(
+namespace {
+
+constexpr int kScratchMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kScratchMaxDevices] = {};
+
+// Device address of `scratch` on the current device, looked up on the first
+// call per device (with that device current) and kept for the process.
+hipError_t decode_scratch(void** addr) {
+    int dev = -1;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kScratchMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_addr[dev]) {
+        void* p = nullptr;
+        const hipError_t r = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (r != hipSuccess) return r;
+        if (!p) return hipErrorInvalidSymbol;
+        g_scratch_addr[dev] = p;
+    }
+    *addr = g_scratch_addr[dev];
+    return hipSuccess;
+}
+
+// Shared body of the split decode entry points.  from_scratch: run exactly the
+// split the workspace query sizes, with its partials in `scratch`, or refuse
+// when they would not fit; otherwise as many splits as `workspace` holds.
+hipError_t paged_decode(
     const uint16_t* q, uint16_t* out, int64_t q_row_stride, int64_t out_row_stride, int n_seqs,
     const int32_t* ctx_lens, int max_ctx_len, const int32_t* block_tables, int max_blocks_per_seq,
     const uint16_t* const* k_blocks, const uint16_t* const* v_blocks, int n_blocks, int layer,
     int n_layers, int n_heads, int n_kv_heads, int head_dim, void* workspace,
-    size_t workspace_bytes, hipStream_t stream) {
+    size_t workspace_bytes, bool from_scratch, hipStream_t stream) {
     QL_CHECK_ARG(n_seqs >= 0 && n_seqs <= 65535 && max_ctx_len >= 0);
     QL_CHECK_ARG(n_heads > 0 && n_kv_heads > 0 && n_kv_heads <= n_heads && n_heads <= 65535);
     QL_CHECK_ARG(head_dim == 64 || head_dim == 128);
@@ -1242,10 +1279,42 @@ extern "C" hipError_t ql_paged_decode_attention_f16(
     a.ctx_lens = ctx_lens;
     a.n_q_rows = n_seqs;
     a.layer = layer;
-    // as many key splits as wanted and the workspace holds (1 = no workspace used)
     int n_split = dec_splits(n_seqs, n_kv_heads, dec_col_chunks(n_heads, n_kv_heads), max_ctx_len);
-    while (n_split > 1 && dec_ws_bytes(n_seqs, n_heads, head_dim, n_split) > workspace_bytes) --n_split;
+    if (from_scratch) {
+        QL_CHECK_ARG(dec_ws_bytes(n_seqs, n_heads, head_dim, n_split) <= kDecodeScratchBytes);
+        if (n_split > 1) {
+            const hipError_t e = decode_scratch(&workspace);
+            if (e != hipSuccess) return e;
+        }
+    } else {
+        // as many key splits as wanted and the workspace holds (1 = no workspace used)
+        while (n_split > 1 && dec_ws_bytes(n_seqs, n_heads, head_dim, n_split) > workspace_bytes) --n_split;
+    }
     a.n_split = n_split;
     a.ws = n_split > 1 ? static_cast<float*>(workspace) : nullptr;
     return launch_decode<true>(a, head_dim, n_seqs, stream);
+}
+
+}  // namespace
+
+extern "C" hipError_t ql_paged_decode_attention_f16(
+    const uint16_t* q, uint16_t* out, int64_t q_row_stride, int64_t out_row_stride, int n_seqs,
+    const int32_t* ctx_lens, int max_ctx_len, const int32_t* block_tables, int max_blocks_per_seq,
+    const uint16_t* const* k_blocks, const uint16_t* const* v_blocks, int n_blocks, int layer,
+    int n_layers, int n_heads, int n_kv_heads, int head_dim, void* workspace,
+    size_t workspace_bytes, hipStream_t stream) {
+    return paged_decode(q, out, q_row_stride, out_row_stride, n_seqs, ctx_lens, max_ctx_len,
+                        block_tables, max_blocks_per_seq, k_blocks, v_blocks, n_blocks, layer,
+                        n_layers, n_heads, n_kv_heads, head_dim, workspace, workspace_bytes, false,
+                        stream);
+}
+
+extern "C" hipError_t ql_paged_decode_attention_f16_noalloc(
+    const uint16_t* q, uint16_t* out, int64_t q_row_stride, int64_t out_row_stride, int n_seqs,
+    const int32_t* ctx_lens, int max_ctx_len, const int32_t* block_tables, int max_blocks_per_seq,
+    const uint16_t* const* k_blocks, const uint16_t* const* v_blocks, int n_blocks, int layer,
+    int n_layers, int n_heads, int n_kv_heads, int head_dim, hipStream_t stream) {
+    return paged_decode(q, out, q_row_stride, out_row_stride, n_seqs, ctx_lens, max_ctx_len,
+                        block_tables, max_blocks_per_seq, k_blocks, v_blocks, n_blocks, layer,
+                        n_layers, n_heads, n_kv_heads, head_dim, nullptr, 0, true, stream);
 }

@@ -94,7 +94,11 @@ SIGNATURES = {
     "ql_engine_logits_f16": [_p, _p, _p, _p, _p, _i, _p, _i, _i, _p, _p, _p],
     "ql_paged_decode_attention_f16": [_p, _p, _i64, _i64, _i, _p, _i, _p, _i, _p, _p, _i, _i, _i,
                                       _i, _i, _i, _p, ctypes.c_size_t, _p],
+    "ql_paged_decode_attention_f16_noalloc": [_p, _p, _i64, _i64, _i, _p, _i, _p, _i, _p, _p, _i,
+                                              _i, _i, _i, _i, _i, _p],
 }
+
+DECODE_SCRATCH_BYTES = 8 << 20   # QL_DECODE_SCRATCH_BYTES
 
 HIP_SUCCESS = 0
 HIP_ERROR_INVALID_VALUE = 1
