@@ -23,7 +23,9 @@ written once) / wall time per step.
 The embedding gather (once per forward, not per layer) is timed separately and
 reported under "kernels".  The roofline entry is for the dominant kernel,
 SwiGLU fp16 [8192 x 14336]: 3 x 8192 x 14336 x 2 B = 704,643,072 B per launch,
-timed with HIP events around each of its launches on the work stream.
+timed after the timed steps in a pass of its own: back-to-back launches on the
+work stream between one pair of HIP events.  The timed steps themselves carry
+no instrumentation: one event pair and a host clock at their edges only.
 
 `--all-configs` times every BASELINE config (C1-C5) one kernel at a time and
 adds the attention that consumes the path's output: causal prefill over the
@@ -67,6 +69,8 @@ BYTES = {
     "embed_f16": 2 * T * D * 2 + 4 * T,                           # read rows; write out; ids
     # Q read+write; K read, write in place, write to cache; V read, write to cache; slots
     "rope_paged_kv_append_f16": 2 * T * HQ * HD * 2 + 5 * T * HKV * HD * 2 + 4 * T,
+    # opt-in variant: rotated K to the cache only (no in-place K write), not in the chain
+    "rope_q_paged_kv_append_f16": 2 * T * HQ * HD * 2 + 4 * T * HKV * HD * 2 + 4 * T,
 }
 COPY_TOKENS = 131072                                              # 256 MiB per K and V
 COPY_ELEMS = COPY_TOKENS * HKV * HD
@@ -84,7 +88,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--breakdown-reps", type=int, default=30)
+    ap.add_argument("--breakdown-reps", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target CPU time of the oracle baseline sample (0 = skip)")
     ap.add_argument("--traffic-file", default=str(ROOT / "profiles" / "pmc_traffic.json"))
@@ -163,6 +167,11 @@ class Chain:
                      HQ * HD, HKV * HD, HKV * HD, None, 0, THETA, self.ql.ROPE_HALF, self.kptrs.ptr,
                      self.vptrs.ptr, self.nb, self.slots.ptr, layer, L_POOL, self.stream)
 
+    def k_rope_q_paged(self, s, layer):
+        self.ql.call("ql_rope_q_paged_kv_append_f16", s["q"].ptr, s["k"].ptr, s["v"].ptr, T, HQ, HKV,
+                     HD, HQ * HD, HKV * HD, HKV * HD, None, 0, THETA, self.ql.ROPE_HALF, self.kptrs.ptr,
+                     self.vptrs.ptr, self.nb, self.slots.ptr, layer, L_POOL, self.stream)
+
     def k_swiglu(self, s):
         self.ql.call("ql_swiglu_f16", s["gate"].ptr, s["up"].ptr, s["out"].ptr, T, F, self.stream)
 
@@ -175,18 +184,14 @@ class Chain:
         self.ql.call("ql_kv_append_f16", self.cp_dst[0].ptr, self.cp_dst[1].ptr, self.cp_src[0].ptr,
                      self.cp_src[1].ptr, 0, 0, COPY_TOKENS, HKV, HD, COPY_TOKENS, 1, self.stream)
 
-    def step(self, ev_swiglu=None):
+    def step(self):
         i = self.step_no
         self.step_no += 1
         s = self.sets[i % NSETS]
         self.k_add_rmsnorm(s, "d1")
         self.k_rope_paged(s, i % L_POOL)
         self.k_add_rmsnorm(s, "d2")
-        if ev_swiglu is not None:
-            ev_swiglu[0].record(self.stream)
         self.k_swiglu(s)
-        if ev_swiglu is not None:
-            ev_swiglu[1].record(self.stream)
 
     def kernel_launcher(self, name):
         return {
@@ -194,6 +199,7 @@ class Chain:
             "rope_f16": lambda i: self.k_rope(self.sets[i % NSETS]),
             "paged_kv_append_f16": lambda i: self.k_paged(self.sets[i % NSETS], i % L_POOL),
             "rope_paged_kv_append_f16": lambda i: self.k_rope_paged(self.sets[i % NSETS], i % L_POOL),
+            "rope_q_paged_kv_append_f16": lambda i: self.k_rope_q_paged(self.sets[i % NSETS], i % L_POOL),
             "swiglu_f16": lambda i: self.k_swiglu(self.sets[i % NSETS]),
             "embed_f16": lambda i: self.k_embed(i),
             "copy_calibration": lambda i: self.k_copy(),
@@ -208,26 +214,57 @@ def percentiles(us):
 
 
 def breakdown(chain, ql, reps):
-    """Average duration of each kernel, HIP events around every launch."""
+    """Duration of each kernel on the work stream, two ways.
+
+    us_mean: `reps` launches back to back (rotating buffer sets) between one
+    pair of HIP events, divided by reps -- the kernel's duration plus the
+    dispatch gap, which is what a rocprofv3 kernel trace averages to within
+    about 1%.  events_per_launch: a second pass with an event pair around
+    every launch (each pair adds the events' own cost, a few us), kept for
+    its spread."""
     out = {}
-    for name in ["add_rmsnorm_f16", "rope_paged_kv_append_f16", "rope_f16", "paged_kv_append_f16",
-                 "swiglu_f16", "embed_f16", "copy_calibration"]:
+    for name in ["add_rmsnorm_f16", "rope_paged_kv_append_f16", "rope_q_paged_kv_append_f16",
+                 "rope_f16", "paged_kv_append_f16", "swiglu_f16", "embed_f16", "copy_calibration"]:
         launch = chain.kernel_launcher(name)
         for i in range(3):
             launch(i)
-        evs = [(ql.Event(), ql.Event()) for _ in range(reps)]
         ql.synchronize()
+        a0, a1 = ql.Event(), ql.Event()
+        a0.record(chain.stream)
+        for i in range(reps):
+            launch(i)
+        a1.record(chain.stream)
+        ql.synchronize()
+        mean = a0.elapsed_ms(a1) * 1e3 / reps
+        evs = [(ql.Event(), ql.Event()) for _ in range(reps)]
         for i, (a, b) in enumerate(evs):
             a.record(chain.stream)
             launch(i)
             b.record(chain.stream)
         ql.synchronize()
         us = sorted(a.elapsed_ms(b) * 1e3 for a, b in evs)
-        mean = sum(us) / len(us)
         gbs = BYTES[name] / (mean * 1e-6) / 1e9
-        out[name] = {"us_mean": round(mean, 2), **percentiles(us), "bytes": BYTES[name],
-                     "GBps": round(gbs, 1), "frac_peak": round(gbs / PEAK_HBM_GBS, 4)}
+        out[name] = {"us_mean": round(mean, 2), "bytes": BYTES[name], "GBps": round(gbs, 1),
+                     "frac_peak": round(gbs / PEAK_HBM_GBS, 4),
+                     "events_per_launch": percentiles(us)}
     return out
+
+
+def host_cpu():
+    """CPU model and the cores this process may run on (the box's share)."""
+    model = "unknown"
+    try:
+        for ln in pathlib.Path("/proc/cpuinfo").read_text().splitlines():
+            if ln.startswith("model name"):
+                model = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    return {"cpu_model": model, "nproc": usable, "os_cpu_count": os.cpu_count()}
 
 
 def cpu_baseline(seconds, threads=1):
@@ -392,10 +429,11 @@ def all_configs(ql, np, reps, only=()):
         time_it(f"softmax_{prec}", "C4 4096x4096 causal", nb, sets_for(nb),
                 lambda xx=xx: (upload(xx), ql.DeviceArray(xx.shape, xx.dtype)),
                 lambda b, prec=prec: ql.call(f"ql_softmax_{prec}", b[0].ptr, b[1].ptr, 4096, 4096, st))
+    rows.append(cpu_softmax_row(np, x4))
     del x4
     # C5: the layer-chain kernels (one launch each, as in the default mode)
     for name in ["embed_f16", "add_rmsnorm_f16", "rope_f16", "paged_kv_append_f16",
-                 "rope_paged_kv_append_f16", "swiglu_f16"]:
+                 "rope_paged_kv_append_f16", "rope_q_paged_kv_append_f16", "swiglu_f16"]:
         launch = chain.kernel_launcher(name)
         for i in range(3):
             launch(i)
@@ -409,11 +447,90 @@ def all_configs(ql, np, reps, only=()):
         gbs = BYTES[name] / (us * 1e-6) / 1e9
         rows.append({"config": "C5 T=8192 llama3-8b", "kernel": name, "bytes": BYTES[name],
                      "us": round(us, 2), "GBps": round(gbs, 1), "frac_peak": round(gbs / PEAK_HBM_GBS, 4)})
+    rows += kvcache_append_rows(ql, np, st)
     rows += attention_rows(ql, np, chain, reps) if want("attention") else []
     rows += layer_rows(ql, np, chain, reps) if want("layer") else []
     del chain
     rows += fp8_rows(ql, np, reps) if want("fp8") else []
     return rows
+
+
+def cpu_softmax_row(np, x):
+    """The reference's only CPU loop on the path, cpu_softmax of
+    tests/test_softmax.cu:19-30 (3 passes, expf, one thread), restated in the
+    oracle as or_softmax_reftest_cpu, on the C4 input; median of 3 runs."""
+    sys.path.insert(0, str(ROOT))
+    import oracle as orc
+    lib = orc.lib()
+    rows_, cols = x.shape
+    xin = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(xin)
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        lib.or_softmax_reftest_cpu(xin.ctypes.data, out.ctypes.data, rows_, cols)
+        ts.append(time.perf_counter() - t0)
+    us = sorted(ts)[1] * 1e6
+    nb = 2 * xin.nbytes
+    info = host_cpu()
+    return {"config": "C4 4096x4096 causal", "bytes": nb, "us": round(us, 1),
+            "GBps": round(nb / (us * 1e-6) / 1e9, 2), "frac_peak": None,
+            "kernel": f"CPU baseline: cpu_softmax (tests/test_softmax.cu:19-30) restated in "
+                      f"oracle/oracle.c, gcc -O2, 1 thread of {info['nproc']} ({info['cpu_model']})"}
+
+
+def kvcache_append_rows(ql, np, st):
+    """The reference's per-token KV-cache benchmark (tests/benchmark_all.cu:265-291,
+    README.md:66-73): an fp32 KVCache of n_layers x 512 positions x 4 kv heads x
+    64, one kvcache_append per layer per token (the drop-in shim of
+    include/quantlib_compat.h, one kernel per call), current_len advanced after
+    each token, 1000 tokens.  The loop is driven from Python through ctypes, so
+    host time per call includes the interpreter's call cost."""
+    from quantlib_amd import lib as _lib
+    p_, i_ = ctypes.c_void_p, ctypes.c_int
+
+    class KVCache(ctypes.Structure):  # include/kv_cache.h:12-20
+        _fields_ = [("k_cache", p_), ("v_cache", p_), ("n_layers", i_), ("max_seq_len", i_),
+                    ("n_heads", i_), ("head_dim", i_), ("current_len", i_)]
+
+    L = _lib()
+    create = L._Z14kvcache_createiiii
+    create.argtypes, create.restype = [i_, i_, i_, i_], ctypes.POINTER(KVCache)
+    append = L._Z14kvcache_appendP7KVCacheiPKfS2_P12ihipStream_t
+    append.argtypes, append.restype = [ctypes.POINTER(KVCache), i_, p_, p_, p_], None
+    free = L._Z12kvcache_freeP7KVCache
+    free.argtypes, free.restype = [ctypes.POINTER(KVCache)], None
+    out = []
+    for n_layers, n_kv, hd in ((4, 4, 64), (8, 4, 64), (16, 4, 64), (32, 4, 64)):
+        cache = create(n_layers, 512, n_kv, hd)
+        if not cache:
+            raise RuntimeError("kvcache_create failed")
+        dk = ql.DeviceArray.from_numpy(np.ones(n_kv * hd, np.float32))
+        dv = ql.DeviceArray.from_numpy(np.ones(n_kv * hd, np.float32))
+        ql.synchronize()
+        reps = 1000
+        a, b = ql.Event(), ql.Event()
+        t0 = time.perf_counter()
+        a.record(st)
+        for _ in range(reps):
+            for layer in range(n_layers):
+                append(cache, layer, dk.ptr, dv.ptr, st)
+            cache.contents.current_len = (cache.contents.current_len + 1) % 256
+        b.record(st)
+        ql.synchronize()
+        host_ms = (time.perf_counter() - t0) * 1e3 / reps
+        ms = a.elapsed_ms(b) / reps
+        nb = 4 * n_layers * n_kv * hd * 4  # per token: read K,V slices, write them, every layer
+        out.append({"config": f"KV cache {n_layers} layers, kv={n_kv}, hd={hd}",
+                    "kernel": "kvcache_append shim, ms per token (reference README.md:66-73: "
+                              "0.2751 / 0.5461 / 1.0679 / 0.7727)",
+                    "bytes": nb, "us": round(ms * 1e3, 2), "ms_per_token": round(ms, 4),
+                    "host_ms_per_token": round(host_ms, 4),
+                    "us_per_append": round(ms * 1e3 / n_layers, 2),
+                    "GBps": round(nb / (ms * 1e-3) / 1e9, 3), "frac_peak": None})
+        free(cache)
+        del dk, dv
+    return out
 
 
 def layer_rows(ql, np, chain, reps):
@@ -749,8 +866,9 @@ def main():
         for r_ in rows:
             extra = (f" ({r_['tflops']:.0f} TFLOP/s, {100 * r_['frac_mfma_peak']:.1f}% of fp16 MFMA peak)"
                      if "tflops" in r_ else "")
+            frac = "-" if r_["frac_peak"] is None else f"{100 * r_['frac_peak']:.1f}"
             print(f"| {r_['config']} | {r_['kernel']}{extra} | {r_['bytes']:,} | {r_['us']:.2f} | "
-                  f"{r_['GBps']:.0f} | {100 * r_['frac_peak']:.1f} |", flush=True)
+                  f"{r_['GBps']:.2f} | {frac} |", flush=True)
         print(json.dumps({"all_configs": rows}), flush=True)
         return
     chain = Chain(ql, np)
@@ -759,25 +877,24 @@ def main():
         chain.step()
     ql.synchronize()
 
-    evs = [(ql.Event(), ql.Event()) for _ in range(args.steps)]
-    ev_steps = [ql.Event() for _ in range(args.steps + 1)]   # step boundaries
-    t_all0, t_all1 = ev_steps[0], ev_steps[-1]
+    # timed region: K steps and nothing else, one event pair at its edges
+    t_all0, t_all1 = ql.Event(), ql.Event()
     ql.synchronize()
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        ev_steps[i].record(chain.stream)
-        chain.step(evs[i])
+    t_all0.record(chain.stream)
+    for _ in range(args.steps):
+        chain.step()
     t_all1.record(chain.stream)
     ql.synchronize()
     wall = time.perf_counter() - t0
 
     ms_per_step = wall / args.steps * 1e3
     ev_ms_per_step = t_all0.elapsed_ms(t_all1) / args.steps
-    sw_all = [a.elapsed_ms(b) * 1e3 for a, b in evs]
-    sw_us = sum(sw_all) / len(sw_all)
-    step_all = [ev_steps[i].elapsed_ms(ev_steps[i + 1]) * 1e3 for i in range(args.steps)]
-    sw_gbs = BYTES["swiglu_f16"] / (sw_us * 1e-6) / 1e9
+    # per-kernel durations, each kernel in its own bracketed pass after the timed region
     kernels = breakdown(chain, ql, args.breakdown_reps)
+    sw = kernels["swiglu_f16"]
+    sw_us = sw["us_mean"]
+    sw_gbs = BYTES["swiglu_f16"] / (sw_us * 1e-6) / 1e9
 
     traffic = None
     tf = pathlib.Path(args.traffic_file)
@@ -787,10 +904,14 @@ def main():
         except (ValueError, AttributeError):
             traffic = None
 
+    cpu_info = host_cpu()
     cpu = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
-    # all host cores, labelled separately (the GPU box's share is 16 cores)
-    n_cores = min(16, os.cpu_count() or 1)
+    # all usable host cores, labelled separately (the GPU box's share is 16 cores)
+    n_cores = min(16, cpu_info["nproc"])
     cpu_all = cpu_baseline(args.cpu_seconds, n_cores) if args.cpu_seconds > 0 and n_cores > 1 else None
+    for c in (cpu, cpu_all):
+        if c is not None:
+            c.update(cpu_info)
 
     chain_gbs = CHAIN_BYTES / (ms_per_step * 1e-3) / 1e9
     line = {
@@ -803,7 +924,6 @@ def main():
         "ms_per_step": round(ms_per_step, 4),
         "us_per_decoder_layer": round(ms_per_step * 1e3, 1),
         "us_per_decoder_layer_events": round(ev_ms_per_step * 1e3, 1),
-        "step_events": percentiles(step_all),
         "frac_peak": round(chain_gbs / PEAK_HBM_GBS, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -821,8 +941,13 @@ def main():
         "roofline": {"kernel": "swiglu_f16 [8192 x 14336]", "bound": "hbm",
                      "achieved": round(sw_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(sw_gbs / PEAK_HBM_GBS, 4), "traffic": traffic,
-                     "algorithmic_bytes": BYTES["swiglu_f16"], "us_per_launch": round(sw_us, 2),
-                     **percentiles(sw_all)},
+                     "traffic_source": "not measured in this run: rocprofv3 --pmc FETCH_SIZE and "
+                                       "WRITE_SIZE of this kernel, copy-calibrated, read from "
+                                       + os.path.relpath(tf, ROOT),
+                     "algorithmic_bytes": BYTES["swiglu_f16"], "us_per_launch": sw_us,
+                     "timing": f"{args.breakdown_reps} back-to-back launches on the work stream "
+                               "between one pair of HIP events, after the timed steps",
+                     "events_per_launch": sw["events_per_launch"]},
         "kernels": kernels,
         "cpu_baseline": cpu,
         "cpu_baseline_all_cores": cpu_all,

@@ -120,6 +120,20 @@ hipError_t ql_rope_paged_kv_append_f16(uint16_t* q, uint16_t* k, const uint16_t*
                                        uint16_t* const* k_blocks, uint16_t* const* v_blocks,
                                        int n_blocks, const int32_t* slot_mapping, int layer,
                                        int n_layers, hipStream_t stream);
+/* As ql_rope_paged_kv_append_f16, except that k is only read: the rotated K rows
+ * go to the paged cache and nowhere else, and the caller's k rows are left as
+ * they were.  For callers that read K only from the cache afterwards, which is
+ * the reference layer's case: attention takes K_full from the cache
+ * (src/fp16_forward.cu:194-209), so its in-place rotated K is never read.  This
+ * saves one write of the K rows. */
+hipError_t ql_rope_q_paged_kv_append_f16(uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                         int n_tokens, int n_heads, int n_kv_heads, int head_dim,
+                                         int64_t q_row_stride, int64_t k_row_stride,
+                                         int64_t v_row_stride, const int32_t* positions,
+                                         int pos_offset, float theta, int pairing,
+                                         uint16_t* const* k_blocks, uint16_t* const* v_blocks,
+                                         int n_blocks, const int32_t* slot_mapping, int layer,
+                                         int n_layers, hipStream_t stream);
 hipError_t ql_rope_kv_append_f16(uint16_t* q, uint16_t* k, const uint16_t* v, int n_tokens,
                                  int n_heads, int n_kv_heads, int head_dim, int64_t q_row_stride,
                                  int64_t k_row_stride, int64_t v_row_stride,

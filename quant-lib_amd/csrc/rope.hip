@@ -80,6 +80,7 @@ struct KvDst {
     const D* v;             // new V rows [n_tokens, v_row_stride]
     long long vs;
     int layer;
+    int skip_k_inplace;     // 1: rotated K goes to the cache only, k is left as read
 };
 
 // Cache row of token t for the current layer (K and V), or nullptr to skip.
@@ -206,7 +207,8 @@ __global__ __launch_bounds__(kBlock) void rope_fast(D* q, D* k, int n_tokens, in
                 ylo.v[2 * e] = from_f32<D>(y0);
                 ylo.v[2 * e + 1] = from_f32<D>(y1);
             }
-            store<true>(reinterpret_cast<V*>(src[u]), ylo);
+            if (!(CACHE != kNoCache && h >= hq && kv.skip_k_inplace))
+                store<true>(reinterpret_cast<V*>(src[u]), ylo);
         } else {
 #pragma unroll
             for (int e = 0; e < PPS; ++e) {
@@ -215,8 +217,10 @@ __global__ __launch_bounds__(kBlock) void rope_fast(D* q, D* k, int n_tokens, in
                 ylo.v[e] = from_f32<D>(y0);
                 yhi.v[e] = from_f32<D>(y1);
             }
-            store<true>(reinterpret_cast<V*>(src[u]), ylo);
-            store<true>(reinterpret_cast<V*>(src[u] + npairs), yhi);
+            if (!(CACHE != kNoCache && h >= hq && kv.skip_k_inplace)) {
+                store<true>(reinterpret_cast<V*>(src[u]), ylo);
+                store<true>(reinterpret_cast<V*>(src[u] + npairs), yhi);
+            }
         }
         if (CACHE != kNoCache && h >= hq && kd) {  // rotated K also goes to the cache
             D* dst = kd + (h - hq) * d + j * W;
@@ -253,8 +257,10 @@ __global__ __launch_bounds__(kBlock) void rope_generic(D* q, D* k, int n_tokens,
                              : k + (long long)t * ks + (long long)(h - hq) * d;
             float y0, y1;
             rotate(to_f32(head[i0]), to_f32(head[i1]), c, s, y0, y1);
-            head[i0] = from_f32<D>(y0);
-            head[i1] = from_f32<D>(y1);
+            if (!(CACHE != kNoCache && h >= hq && kv.skip_k_inplace)) {
+                head[i0] = from_f32<D>(y0);
+                head[i1] = from_f32<D>(y1);
+            }
             if (CACHE != kNoCache && h >= hq && kd) {
                 kd[(h - hq) * d + i0] = from_f32<D>(y0);
                 kd[(h - hq) * d + i1] = from_f32<D>(y1);
@@ -370,7 +376,8 @@ __global__ __launch_bounds__(kBlock) void rope_planes(D* q, D* k, int n_tokens, 
                 ylo.v[2 * e] = from_f32<D>(y0);
                 ylo.v[2 * e + 1] = from_f32<D>(y1);
             }
-            store<true>(reinterpret_cast<V*>(row + off), ylo);
+            if (!(CACHE != kNoCache && plane == 1 && kv.skip_k_inplace))
+                store<true>(reinterpret_cast<V*>(row + off), ylo);
         } else {
 #pragma unroll
             for (int e = 0; e < PPS; ++e) {
@@ -379,8 +386,10 @@ __global__ __launch_bounds__(kBlock) void rope_planes(D* q, D* k, int n_tokens, 
                 ylo.v[e] = from_f32<D>(y0);
                 yhi.v[e] = from_f32<D>(y1);
             }
-            store<true>(reinterpret_cast<V*>(row + off), ylo);
-            store<true>(reinterpret_cast<V*>(row + off + NP), yhi);
+            if (!(CACHE != kNoCache && plane == 1 && kv.skip_k_inplace)) {
+                store<true>(reinterpret_cast<V*>(row + off), ylo);
+                store<true>(reinterpret_cast<V*>(row + off + NP), yhi);
+            }
         }
         if constexpr (CACHE != kNoCache) {
             if (plane == 1 && kd) {
@@ -532,12 +541,14 @@ extern "C" hipError_t ql_rope_f16(uint16_t* q, uint16_t* k, int n_tokens, int n_
         no_cache<_Float16>(), stream);
 }
 
-extern "C" hipError_t ql_rope_paged_kv_append_f16(
-    uint16_t* q, uint16_t* k, const uint16_t* v, int n_tokens, int n_heads, int n_kv_heads,
-    int head_dim, int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
-    const int32_t* positions, int pos_offset, float theta, int pairing,
-    uint16_t* const* k_blocks, uint16_t* const* v_blocks, int n_blocks,
-    const int32_t* slot_mapping, int layer, int n_layers, hipStream_t stream) {
+namespace {
+
+hipError_t rope_paged_entry(uint16_t* q, uint16_t* k, const uint16_t* v, int n_tokens, int n_heads,
+                            int n_kv_heads, int head_dim, int64_t q_row_stride, int64_t k_row_stride,
+                            int64_t v_row_stride, const int32_t* positions, int pos_offset,
+                            float theta, int pairing, uint16_t* const* k_blocks,
+                            uint16_t* const* v_blocks, int n_blocks, const int32_t* slot_mapping,
+                            int layer, int n_layers, bool skip_k_inplace, hipStream_t stream) {
     QL_CHECK_ARG(n_layers > 0 && layer >= 0 && layer < n_layers && n_blocks >= 0);
     QL_CHECK_ARG((long long)n_kv_heads * head_dim <= (1LL << 30));
     QL_CHECK_ARG(n_tokens <= 0 || (k_blocks && v_blocks && slot_mapping));
@@ -549,10 +560,37 @@ extern "C" hipError_t ql_rope_paged_kv_append_f16(
     kv.v = reinterpret_cast<const _Float16*>(v);
     kv.vs = v_row_stride;
     kv.layer = layer;
+    kv.skip_k_inplace = skip_k_inplace ? 1 : 0;
     return rope_dispatch<_Float16, kPagedCache>(
         reinterpret_cast<_Float16*>(q), reinterpret_cast<_Float16*>(k), n_tokens, n_heads,
         n_kv_heads, head_dim, q_row_stride, k_row_stride, positions, pos_offset, theta, pairing,
         kv, stream);
+}
+
+}  // namespace
+
+extern "C" hipError_t ql_rope_paged_kv_append_f16(
+    uint16_t* q, uint16_t* k, const uint16_t* v, int n_tokens, int n_heads, int n_kv_heads,
+    int head_dim, int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
+    const int32_t* positions, int pos_offset, float theta, int pairing,
+    uint16_t* const* k_blocks, uint16_t* const* v_blocks, int n_blocks,
+    const int32_t* slot_mapping, int layer, int n_layers, hipStream_t stream) {
+    return rope_paged_entry(q, k, v, n_tokens, n_heads, n_kv_heads, head_dim, q_row_stride,
+                            k_row_stride, v_row_stride, positions, pos_offset, theta, pairing,
+                            k_blocks, v_blocks, n_blocks, slot_mapping, layer, n_layers, false,
+                            stream);
+}
+
+extern "C" hipError_t ql_rope_q_paged_kv_append_f16(
+    uint16_t* q, const uint16_t* k, const uint16_t* v, int n_tokens, int n_heads, int n_kv_heads,
+    int head_dim, int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
+    const int32_t* positions, int pos_offset, float theta, int pairing,
+    uint16_t* const* k_blocks, uint16_t* const* v_blocks, int n_blocks,
+    const int32_t* slot_mapping, int layer, int n_layers, hipStream_t stream) {
+    return rope_paged_entry(q, const_cast<uint16_t*>(k), v, n_tokens, n_heads, n_kv_heads, head_dim,
+                            q_row_stride, k_row_stride, v_row_stride, positions, pos_offset, theta,
+                            pairing, k_blocks, v_blocks, n_blocks, slot_mapping, layer, n_layers,
+                            true, stream);
 }
 
 template <typename D>

@@ -39,6 +39,8 @@ SIGNATURES = {
     "ql_rope_f16": [_p, _p, _i, _i, _i, _i, _i64, _i64, _p, _i, _f, _i, _p],
     "ql_rope_paged_kv_append_f16": [_p, _p, _p, _i, _i, _i, _i, _i64, _i64, _i64, _p, _i, _f, _i,
                                     _p, _p, _i, _p, _i, _i, _p],
+    "ql_rope_q_paged_kv_append_f16": [_p, _p, _p, _i, _i, _i, _i, _i64, _i64, _i64, _p, _i, _f, _i,
+                                      _p, _p, _i, _p, _i, _i, _p],
     "ql_rope_kv_append_f16": [_p, _p, _p, _i, _i, _i, _i, _i64, _i64, _i64, _p, _i, _f, _i, _p, _p,
                               _i, _i, _i, _i, _p],
     "ql_rope_kv_append_f32": [_p, _p, _p, _i, _i, _i, _i, _i64, _i64, _i64, _p, _i, _f, _i, _p, _p,

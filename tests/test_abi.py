@@ -119,6 +119,10 @@ P = 4096  # a non-null, 16-byte aligned dummy address: never dereferenced on the
       P, P, 4, P, 0, 2, None), INVALID),
     (("ql_rope_paged_kv_append_f16", P, P, P, 4, 8, 2, 64, 512, 128, 128, None, 0, 1e4, 1,
       P, P, 4, P, 2, 2, None), INVALID),
+    (("ql_rope_q_paged_kv_append_f16", P, None, P, 4, 8, 2, 64, 512, 128, 128, None, 0, 1e4, 1,
+      P, P, 4, P, 0, 2, None), INVALID),
+    (("ql_rope_q_paged_kv_append_f16", P, P, P, 4, 8, 2, 64, 512, 128, 128, None, 0, 1e4, 1,
+      P, P, 4, None, 0, 2, None), INVALID),
     (("ql_rope_kv_append_f16", P, P, P, 4, 8, 2, 64, 512, 128, 64, None, 0, 1e4, 1,
       P, P, 0, 0, 16, 2, None), INVALID),
     (("ql_rope_kv_append_f32", P, P, P, 4, 8, 2, 64, 512, 128, 128, None, 0, 1e4, 1,

@@ -490,7 +490,9 @@ def _pool(nb, blk, misalign=0):
 
 @pytest.mark.parametrize("pairing", [ql.ROPE_HALF, ql.ROPE_INTERLEAVED])
 @pytest.mark.parametrize("T,H,HK,d,misalign", [(8192, 32, 8, 128, 0), (37, 4, 2, 64, 0),
-                                               (20, 3, 1, 96, 0), (45, 4, 2, 64, 1)])
+                                               (20, 3, 1, 96, 0), (45, 4, 2, 64, 1),
+                                               (45, 5, 3, 128, 1), (19, 2, 1, 128, 0),
+                                               (33, 6, 2, 128, 0), (5, 120, 8, 128, 0)])
 def test_rope_paged_kv_append_fused(pairing, T, H, HK, d, misalign):
     # One launch == ql_rope_f16 then ql_paged_kv_append_f16, bit for bit; and
     # both agree with the oracle (C5 shape: Q 32x128, K/V 8x128, theta 5e5).
@@ -533,9 +535,39 @@ def test_rope_paged_kv_append_fused(pairing, T, H, HK, d, misalign):
     assert np.array_equal(host(kp1), wk) and np.array_equal(host(vp1), wv)
 
 
+@pytest.mark.parametrize("pairing", [ql.ROPE_HALF, ql.ROPE_INTERLEAVED])
+@pytest.mark.parametrize("T,H,HK,d,misalign", [(8192, 32, 8, 128, 0), (45, 5, 3, 128, 1),
+                                               (37, 4, 2, 64, 0), (20, 3, 1, 96, 0)])
+def test_rope_q_paged_kv_append_leaves_k(pairing, T, H, HK, d, misalign):
+    # ql_rope_q_paged_kv_append_f16: Q and both pools exactly as the fused entry
+    # point writes them; the caller's K rows are read and left unrotated.
+    L, layer, theta = 4, 1, 5e5
+    nb = (T + 15) // 16 + 1
+    blk = L * 16 * HK * d
+    q = _f16(normal(3 * T, (T, H * d)))
+    k = _f16(normal(3 * T + 1, (T, HK * d)))
+    v = _f16(normal(3 * T + 2, (T, HK * d)))
+    order = np.random.default_rng(T).permutation(nb)
+    slots = np.array([order[t // 16] * 16 + t % 16 for t in range(T)], np.int32)
+    dsl, dv = dev(slots), dev(v)
+    outs = []
+    for name in ("ql_rope_paged_kv_append_f16", "ql_rope_q_paged_kv_append_f16"):
+        dq, dk = dev(q), dev(k)
+        kp, kb = _pool(nb, blk, misalign)
+        vp, vb = _pool(nb, blk, misalign)
+        ql.call(name, dq.ptr, dk.ptr, dv.ptr, T, H, HK, d, H * d, HK * d, HK * d, None, 0, theta,
+                pairing, kb.ptr, vb.ptr, nb, dsl.ptr, layer, L, stream())
+        outs.append((host(dq, shape=(T, H * d)), host(dk, shape=(T, HK * d)), host(kp), host(vp)))
+    (q1, k1, kp1, vp1), (q2, k2, kp2, vp2) = outs
+    assert np.array_equal(q1, q2) and np.array_equal(kp1, kp2) and np.array_equal(vp1, vp2)
+    assert np.array_equal(k2, k), "K rows must be left as read"
+    check_f16(k1, orc.rope(k, HK, d, theta, pairing, f16=True), "fused rope k")
+
+
 @pytest.mark.parametrize("f16", [True, False])
 @pytest.mark.parametrize("pairing", [ql.ROPE_HALF, ql.ROPE_INTERLEAVED])
-@pytest.mark.parametrize("T,H,HK,d", [(300, 8, 2, 128), (33, 4, 4, 64), (17, 2, 1, 6)])
+@pytest.mark.parametrize("T,H,HK,d", [(300, 8, 2, 128), (33, 4, 4, 64), (17, 2, 1, 6),
+                                      (29, 3, 3, 64), (31, 7, 1, 128)])
 def test_rope_kv_append_fused_contiguous_from_fused_qkv(f16, pairing, T, H, HK, d):
     # Q, K, V are views into one fused [T, (H + 2*HK)*d] QKV buffer (strided rows);
     # the cache is [L, S, HK, d], tokens written at positions pos..pos+T-1.
