@@ -97,7 +97,7 @@ def parse():
     ap.add_argument("--reps", type=int, default=50, help="launches per config in --all-configs")
     ap.add_argument("--only", default="",
                     help="--all-configs row groups to time, comma-separated: "
-                         "configs, attention, layer, fp8 (default: all)")
+                         "configs, kv, attention, layer, fp8 (default: all)")
     return ap.parse_args()
 
 
@@ -354,8 +354,10 @@ def all_configs(ql, np, reps, only=()):
     st = ql.stream()
     rows = []
     want = lambda group: not only or group in only
+    if want("kv"):
+        rows += kvcache_append_rows(ql, np, st)
     if not want("configs") and not want("attention") and not want("layer"):
-        return fp8_rows(ql, np, reps) if want("fp8") else rows
+        return rows + (fp8_rows(ql, np, reps) if want("fp8") else [])
 
     def sets_for(nbytes):
         return max(2, min(64, -(-(1 << 30) // max(nbytes, 1))))
@@ -433,7 +435,8 @@ def all_configs(ql, np, reps, only=()):
     del x4
     # C5: the layer-chain kernels (one launch each, as in the default mode)
     for name in ["embed_f16", "add_rmsnorm_f16", "rope_f16", "paged_kv_append_f16",
-                 "rope_paged_kv_append_f16", "rope_q_paged_kv_append_f16", "swiglu_f16"]:
+                 "rope_paged_kv_append_f16", "rope_q_paged_kv_append_f16", "swiglu_f16",
+                 "copy_calibration"]:
         launch = chain.kernel_launcher(name)
         for i in range(3):
             launch(i)
@@ -447,7 +450,6 @@ def all_configs(ql, np, reps, only=()):
         gbs = BYTES[name] / (us * 1e-6) / 1e9
         rows.append({"config": "C5 T=8192 llama3-8b", "kernel": name, "bytes": BYTES[name],
                      "us": round(us, 2), "GBps": round(gbs, 1), "frac_peak": round(gbs / PEAK_HBM_GBS, 4)})
-    rows += kvcache_append_rows(ql, np, st)
     rows += attention_rows(ql, np, chain, reps) if want("attention") else []
     rows += layer_rows(ql, np, chain, reps) if want("layer") else []
     del chain

@@ -360,3 +360,99 @@ def test_engine_layers_after_tuning_match_oracle():
             weights, prompts, 3)
     finally:
         ql.call("ql_engine_destroy", eng)
+
+
+# ---- the engine at the benched layer shape ------------------------------------------------
+# Llama-3-8B-shaped layer of fp16_layer_forward (src/fp16_forward.cu:167-223): hidden 4096,
+# 32 query / 8 KV heads of 128, ffn 14336, rotate-half RoPE at theta 5e5.  The oracle GEMMs
+# at these widths take ~0.7 s per 400 M multiply-adds, so every row goes through the QKV
+# product (attention needs all K/V rows) but only sampled rows through attention, the output
+# projection and the MLP.
+C5 = {"DM": 4096, "H": 32, "HK": 8, "HD": 128, "FF": 14336, "THETA": 5e5}
+
+
+def c5_weights(seed):
+    c = C5
+    r = lambda s, shape, scale: to_f16_bits(normal(seed + s, shape, scale))
+    return {"attn_norm": to_f16_bits(np.random.default_rng(seed).uniform(0.5, 1.5, c["DM"]).astype(np.float32)),
+            "wqkv": r(1, ((c["H"] + 2 * c["HK"]) * c["HD"], c["DM"]), c["DM"] ** -0.5),
+            "wo": r(2, (c["DM"], c["H"] * c["HD"]), (c["H"] * c["HD"]) ** -0.5),
+            "ffn_norm": to_f16_bits(np.random.default_rng(seed + 3).uniform(0.5, 1.5, c["DM"]).astype(np.float32)),
+            "w_gate": r(4, (c["FF"], c["DM"]), c["DM"] ** -0.5), "w_up": r(5, (c["FF"], c["DM"]), c["DM"] ** -0.5),
+            "w_down": r(6, (c["DM"], c["FF"]), c["FF"] ** -0.5)}
+
+
+def oracle_layer_rows(x, delta_in, w, plan, hist, rows):
+    """The oracle layer of oracle_layer at the C5 dims, returning the residual
+    stream and MLP output of `rows` only; hist[req] gains every row's K and V."""
+    c = C5
+    H_, HK_, HD_ = c["H"], c["HK"], c["HD"]
+    if delta_in is None:
+        x1, y = x, orc.rmsnorm(x, w["attn_norm"], EPS, f16=True)
+    else:
+        x1, y = orc.add_rmsnorm(x, delta_in, w["attn_norm"], EPS, f16=True)
+    qkv = orc.matmul(y, w["wqkv"])
+    pos = plan["positions"]
+    q = orc.rope(np.ascontiguousarray(qkv[:, :H_ * HD_]), H_, HD_, c["THETA"], PAIR, positions=pos, f16=True)
+    k = orc.rope(np.ascontiguousarray(qkv[:, H_ * HD_:(H_ + HK_) * HD_]), HK_, HD_, c["THETA"], PAIR,
+                 positions=pos, f16=True)
+    v = np.ascontiguousarray(qkv[:, (H_ + HK_) * HD_:])
+    cu = plan["cu_q_lens"]
+    seq_of = np.searchsorted(cu, np.arange(plan["n_rows"]), side="right") - 1
+    before = {}
+    for i, rid in enumerate(plan["req_ids"]):
+        ks, vs = hist.setdefault(int(rid), ([], []))
+        before[i] = len(ks)
+        ks.extend(k[cu[i]:cu[i + 1]])
+        vs.extend(v[cu[i]:cu[i + 1]])
+    attn = np.zeros((len(rows), H_ * HD_), np.uint16)
+    for j, r in enumerate(rows):
+        i = int(seq_of[r])
+        ks, vs = hist[int(plan["req_ids"][i])]
+        n = before[i] + (r - cu[i]) + 1          # keys up to this row's position (causal)
+        kk = np.stack(ks[:n]).reshape(n, HK_, HD_)
+        vv = np.stack(vs[:n]).reshape(n, HK_, HD_)
+        attn[j] = orc.attention(q[r:r + 1].reshape(1, H_, HD_), kk, vv, H_, HK_, True, f16=True).reshape(-1)
+    x2 = orc.add(x1[rows], orc.matmul(attn, w["wo"]), f16=True)
+    y2 = orc.rmsnorm(x2, w["ffn_norm"], EPS, f16=True)
+    mid = orc.swiglu(orc.matmul(y2, w["w_gate"]), orc.matmul(y2, w["w_up"]), f16=True)
+    return x2, orc.matmul(mid, w["w_down"])
+
+
+@pytest.mark.parametrize("prompts", [{0: 64},            # one fresh prompt: contiguous attention
+                                     {0: 40, 1: 24}])    # two prompts: paged prefill attention
+def test_engine_layer_c5_shape_prefill_and_decode(prompts):
+    """One C5-shaped layer (ql_engine_layer_f16) for a prefill step and then an
+    all-decode step (split decode over the paged pool), sampled rows of the
+    residual stream and of the MLP output against the oracle-composed layer."""
+    c = C5
+    w = c5_weights(300)
+    dw = {k: dev(v) for k, v in w.items()}
+    lw = ql.LayerWeights(*(dw[k].ptr for k in ("attn_norm", "wqkv", "wo", "ffn_norm", "w_gate", "w_up",
+                                               "w_down")))
+    dims = ql.LayerDims(c["DM"], c["H"], c["HK"], c["HD"], c["FF"], c["THETA"], EPS, PAIR)
+    eng = ctypes.c_void_p()
+    ql.call("ql_engine_create", ctypes.byref(dims), 64, 4, 256, ctypes.byref(eng))
+    pool = PagedPool(16, 1, c["HK"], c["HD"])
+    b = ql.Batcher(16, 4)
+    for rid, n in prompts.items():
+        b.add(rid, np.arange(n, dtype=np.int32), 4)
+    hist, keep = {}, []
+    try:
+        for step in range(2):
+            plan = b.plan()
+            T = plan["n_rows"]
+            assert (step == 0) == (plan["max_q_len"] > 1)
+            sd = step_device(plan, pool, 1, keep)
+            x = to_f16_bits(normal(900 + step, (T, c["DM"])))
+            dx, dd = dev(x), empty((T * c["DM"],), np.uint16)
+            ql.call("ql_engine_layer_f16", eng, ctypes.byref(lw), 0, dx.ptr, None, dd.ptr, ctypes.byref(sd),
+                    stream())
+            rows = [0, 17, 39, 40, T - 1] if T > 1 else [0]
+            rows = sorted(set(r for r in rows if r < T))
+            wx, wd = oracle_layer_rows(x, None, w, plan, hist, rows)
+            check_layer(host(dx, shape=(T, c["DM"]))[rows], wx, f"C5 step {step} residual")
+            check_layer(host(dd, shape=(T, c["DM"]))[rows], wd, f"C5 step {step} mlp out")
+            b.commit(np.full(plan["n_seqs"], 7, np.int32))
+    finally:
+        ql.call("ql_engine_destroy", eng)
