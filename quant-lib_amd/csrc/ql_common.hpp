@@ -60,6 +60,36 @@ __device__ __forceinline__ void store(V* p, const V& v) {
     }
 }
 
+// 16-byte store with the cache policy "sc1 nt" (device scope, nontemporal):
+// the line is written through to memory rather than left dirty in L2.  Issued
+// as a buffer store, whose instruction carries the policy bits: `base` must be
+// the same for every lane of the wavefront (pass it through uniform() when the
+// compiler cannot see that), `byte_off` is the lane's offset from it (below
+// 4 GiB).  Measured on MI355X with buffers rotated past the MALL, against
+// nontemporal stores: a plain 1-read/1-write stream 6.44 -> 6.55 TB/s, RoPE
+// (which writes back the rows it just read) 2-11% faster; but the row kernels
+// that write fresh buffers were no faster or slower (add+RMSNorm equal,
+// SwiGLU -0.7%, fp16 softmax -5%, a 2048-row RMSNorm -35%), so only RoPE
+// uses it.
+constexpr int kStorePolicy = 16 | 2;   // sc1 | nt
+template <typename V>
+__device__ __forceinline__ void store_wt(const void* base, uint32_t byte_off, const V& v) {
+    static_assert(sizeof(V) == 16, "16-byte stores");
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, -1, 0x00020000);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, (int)byte_off, 0,
+                                           kStorePolicy);
+}
+
+// A pointer that is the same in every lane of the wavefront, made scalar.
+template <typename T>
+__device__ __forceinline__ T* uniform(T* p) {
+    const uint64_t a = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    return reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
+}
+
 __device__ __forceinline__ float to_f32(float x) { return x; }
 __device__ __forceinline__ float to_f32(_Float16 x) { return (float)x; }
 

@@ -313,8 +313,10 @@ __global__ __launch_bounds__(kBlock) void rope_planes(D* q, D* k, int n_tokens, 
     const int h0 = g * hpw;
     const int h1 = min(nh, h0 + hpw);
     const int nslots = (h1 - h0) * S;
-    D* row = plane == 0 ? q + (long long)t * qs
-           : (plane == 1 ? k + (long long)t * ks : const_cast<D*>(kv.v) + (long long)t * kv.vs);
+    // one token per wavefront: the row base is scalar (stores go out as
+    // write-through buffer stores from it)
+    D* row = uniform(plane == 0 ? q + (long long)t * qs
+                     : (plane == 1 ? k + (long long)t * ks : const_cast<D*>(kv.v) + (long long)t * kv.vs));
 
     V lo[MAXU];
     V hi[HALF ? MAXU : 1];
@@ -334,6 +336,8 @@ __global__ __launch_bounds__(kBlock) void rope_planes(D* q, D* k, int n_tokens, 
     if constexpr (CACHE != kNoCache) {
         if (plane != 0) {
             cache_rows<D, CACHE>(kv, t, hk * HD, kd, vd);
+            kd = uniform(kd);
+            vd = uniform(vd);
             cache_aligned = ((reinterpret_cast<uintptr_t>(kd) | reinterpret_cast<uintptr_t>(vd)) & 15) == 0;
         }
         if (plane == 2) {  // V: copy the rows into the cache, no rotation
@@ -342,9 +346,14 @@ __global__ __launch_bounds__(kBlock) void rope_planes(D* q, D* k, int n_tokens, 
                 for (int u = 0; u < MAXU; ++u) {
                     const int sl = lane + u * kWave;
                     if (sl < nslots) {
-                        D* dst = vd + (h0 + sl / S) * HD + j * W;
-                        store_cache<D>(dst, lo[u], cache_aligned);
-                        if constexpr (HALF) store_cache<D>(dst + NP, hi[u], cache_aligned);
+                        const int off = (h0 + sl / S) * HD + j * W;
+                        if (cache_aligned) {
+                            store_wt(vd, (uint32_t)off * sizeof(D), lo[u]);
+                            if constexpr (HALF) store_wt(vd, (uint32_t)(off + NP) * sizeof(D), hi[u]);
+                        } else {
+                            store_cache<D>(vd + off, lo[u], false);
+                            if constexpr (HALF) store_cache<D>(vd + off + NP, hi[u], false);
+                        }
                     }
                 }
             }
@@ -377,7 +386,7 @@ __global__ __launch_bounds__(kBlock) void rope_planes(D* q, D* k, int n_tokens, 
                 ylo.v[2 * e + 1] = from_f32<D>(y1);
             }
             if (!(CACHE != kNoCache && plane == 1 && kv.skip_k_inplace))
-                store<true>(reinterpret_cast<V*>(row + off), ylo);
+                store_wt(row, (uint32_t)off * sizeof(D), ylo);
         } else {
 #pragma unroll
             for (int e = 0; e < PPS; ++e) {
@@ -387,14 +396,19 @@ __global__ __launch_bounds__(kBlock) void rope_planes(D* q, D* k, int n_tokens, 
                 yhi.v[e] = from_f32<D>(y1);
             }
             if (!(CACHE != kNoCache && plane == 1 && kv.skip_k_inplace)) {
-                store<true>(reinterpret_cast<V*>(row + off), ylo);
-                store<true>(reinterpret_cast<V*>(row + off + NP), yhi);
+                store_wt(row, (uint32_t)off * sizeof(D), ylo);
+                store_wt(row, (uint32_t)(off + NP) * sizeof(D), yhi);
             }
         }
         if constexpr (CACHE != kNoCache) {
             if (plane == 1 && kd) {
-                store_cache<D>(kd + off, ylo, cache_aligned);
-                if constexpr (HALF) store_cache<D>(kd + off + NP, yhi, cache_aligned);
+                if (cache_aligned) {
+                    store_wt(kd, (uint32_t)off * sizeof(D), ylo);
+                    if constexpr (HALF) store_wt(kd, (uint32_t)(off + NP) * sizeof(D), yhi);
+                } else {
+                    store_cache<D>(kd + off, ylo, false);
+                    if constexpr (HALF) store_cache<D>(kd + off + NP, yhi, false);
+                }
             }
         }
     }
