@@ -16,7 +16,10 @@ One step = one pass of that chain.  The unfused RoPE and paged-append kernels
 are timed separately under "kernels" for comparison.  Inputs are synthetic (seeded normal values
 made on the host and uploaded once) and resident in HBM before timing.  Three
 device buffer sets (~1 GB each) are rotated step to step so no input is still
-in the 256 MB MALL; the KV append rotates over the 32 pool layers.
+in the 256 MB MALL; the KV append rotates over the 32 pool layers.  The
+single-kernel passes of the smaller kernels rotate more: the RoPE and KV-append
+kernels over 12 sets of Q, K, V (96 MiB each), the embedding gather over 4
+tables (250 MB each) with their own ids.
 value = algorithmic bytes of the chain (each input read once, each output
 written once) / wall time per step.
 
@@ -60,6 +63,14 @@ PEAK_MFMA_F16_TFLOPS = 2500.0  # MI355X dense fp16 matrix peak, TFLOP/s
 T, D, HQ, HKV, HD, F = 8192, 4096, 32, 8, 128, 14336
 VOCAB, THETA, EPS, L_POOL, PAGE = 32000, 5e5, 1e-5, 32, 16
 NSETS = 3
+# single-kernel passes of the RoPE / KV-append kernels rotate over more sets:
+# one set of Q, K, V is 96 MiB, and three would partly stay in the 256 MB MALL
+NROPE = 12
+NTABLES = 4   # embedding tables (250 MB each) rotated by the gather pass
+# warm-up launches of a single-kernel pass: one full rotation of every set it
+# cycles through (buffer sets, tables, the 32 pool layers), so no timed launch
+# is the first to touch a buffer (first touches also pay address translation)
+WARM = 32
 
 BYTES = {
     "add_rmsnorm_f16": 4 * T * D * 2 + 2 * D,                     # read x,d; write x',y; w
@@ -87,7 +98,7 @@ def parse():
                                  formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--breakdown-reps", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target CPU time of the oracle baseline sample (0 = skip)")
@@ -131,15 +142,22 @@ class Chain:
         # paged pool: 512 blocks of [32 layers, 16, 8, 128] fp16 (1 MiB each) per K and V
         self.nb = T // PAGE
         blk = L_POOL * PAGE * HKV * HD
-        self.kpool = ql.DeviceArray((self.nb * blk,), np.uint16)
-        self.vpool = ql.DeviceArray((self.nb * blk,), np.uint16)
+        self.kpool = ql.DeviceArray((self.nb * blk,), np.uint16).fill_bytes(0)
+        self.vpool = ql.DeviceArray((self.nb * blk,), np.uint16).fill_bytes(0)
         self.kptrs = up(np.array([self.kpool.ptr + 2 * blk * b for b in range(self.nb)], np.int64))
         self.vptrs = up(np.array([self.vpool.ptr + 2 * blk * b for b in range(self.nb)], np.int64))
         # fresh-pool block order 0,1,2,... (LIFO allocator of src/paged_kvcache.cu:49-53)
         self.slots = up(np.arange(T, dtype=np.int32))
-        # embedding table and ids (gather timed separately)
-        self.table = up(randn(VOCAB, D))
-        self.ids = up(r.integers(0, VOCAB, size=T).astype(np.int32))
+        # Q, K, V sets for the single-kernel RoPE / append passes (12 x 96 MiB)
+        qh, kh, vh = randn(T, HQ * HD), randn(T, HKV * HD), randn(T, HKV * HD)
+        self.rope_sets = [{"q": up(qh), "k": up(kh), "v": up(vh)} for _ in range(NROPE)]
+        del qh, kh, vh
+        # embedding tables and ids (gather timed separately): each launch gathers
+        # from another table with other ids, so no row is still in the MALL
+        tab = randn(VOCAB, D)
+        self.tables = [up(tab) for _ in range(NTABLES)]
+        del tab
+        self.ids = [up(r.integers(0, VOCAB, size=T).astype(np.int32)) for _ in range(NTABLES)]
         self.emb_out = [ql.DeviceArray((T, D), np.uint16) for _ in range(NSETS)]
         # plain-copy reference: 2 x 256 MiB copied by the contiguous KV-append kernel
         self.cp_src = [ql.DeviceArray((COPY_ELEMS,), np.uint16) for _ in range(2)]
@@ -176,7 +194,7 @@ class Chain:
         self.ql.call("ql_swiglu_f16", s["gate"].ptr, s["up"].ptr, s["out"].ptr, T, F, self.stream)
 
     def k_embed(self, i):
-        self.ql.call("ql_embed_f16", self.table.ptr, self.ids.ptr, T, VOCAB, D,
+        self.ql.call("ql_embed_f16", self.tables[i % NTABLES].ptr, self.ids[i % NTABLES].ptr, T, VOCAB, D,
                      self.emb_out[i % NSETS].ptr, self.stream)
 
     def k_copy(self):
@@ -196,10 +214,11 @@ class Chain:
     def kernel_launcher(self, name):
         return {
             "add_rmsnorm_f16": lambda i: self.k_add_rmsnorm(self.sets[i % NSETS], "d1"),
-            "rope_f16": lambda i: self.k_rope(self.sets[i % NSETS]),
-            "paged_kv_append_f16": lambda i: self.k_paged(self.sets[i % NSETS], i % L_POOL),
-            "rope_paged_kv_append_f16": lambda i: self.k_rope_paged(self.sets[i % NSETS], i % L_POOL),
-            "rope_q_paged_kv_append_f16": lambda i: self.k_rope_q_paged(self.sets[i % NSETS], i % L_POOL),
+            "rope_f16": lambda i: self.k_rope(self.rope_sets[i % NROPE]),
+            "paged_kv_append_f16": lambda i: self.k_paged(self.rope_sets[i % NROPE], i % L_POOL),
+            "rope_paged_kv_append_f16": lambda i: self.k_rope_paged(self.rope_sets[i % NROPE], i % L_POOL),
+            "rope_q_paged_kv_append_f16": lambda i: self.k_rope_q_paged(self.rope_sets[i % NROPE],
+                                                                        i % L_POOL),
             "swiglu_f16": lambda i: self.k_swiglu(self.sets[i % NSETS]),
             "embed_f16": lambda i: self.k_embed(i),
             "copy_calibration": lambda i: self.k_copy(),
@@ -226,7 +245,7 @@ def breakdown(chain, ql, reps):
     for name in ["add_rmsnorm_f16", "rope_paged_kv_append_f16", "rope_q_paged_kv_append_f16",
                  "rope_f16", "paged_kv_append_f16", "swiglu_f16", "embed_f16", "copy_calibration"]:
         launch = chain.kernel_launcher(name)
-        for i in range(3):
+        for i in range(WARM):
             launch(i)
         ql.synchronize()
         a0, a1 = ql.Event(), ql.Event()
@@ -370,7 +389,7 @@ def all_configs(ql, np, reps, only=()):
 
     def time_it(name, cfg, nbytes, nsets, make, launch):
         bufs = [make() for _ in range(nsets)]
-        for i in range(3):
+        for i in range(max(3, nsets)):   # every set once before timing
             launch(bufs[i % nsets])
         ql.synchronize()
         a, b = ql.Event(), ql.Event()
@@ -438,7 +457,7 @@ def all_configs(ql, np, reps, only=()):
                  "rope_paged_kv_append_f16", "rope_q_paged_kv_append_f16", "swiglu_f16",
                  "copy_calibration"]:
         launch = chain.kernel_launcher(name)
-        for i in range(3):
+        for i in range(WARM):
             launch(i)
         ql.synchronize()
         a, b = ql.Event(), ql.Event()
@@ -622,7 +641,7 @@ def layer_rows(ql, np, chain, reps):
             def launch(i, fn=fn, lws=lws):
                 ql.call(fn, eng, ctypes.byref(lws[i % len(lws)]), i % L_POOL, x.ptr,
                         deltas[(i + 1) % 2].ptr if i else None, deltas[i % 2].ptr, ctypes.byref(sd), st)
-            for i in range(3):
+            for i in range(max(3, 2 * len(lws))):   # every weight set before timing
                 launch(i)
             ql.synchronize()
             n = max(6, reps // 10)
@@ -696,7 +715,7 @@ def fp8_rows(ql, np, reps):
         return max(2, -(-(640 << 20) // n_bytes))
 
     def timed(launch, n):
-        for i in range(3):
+        for i in range(n):   # as many warm-up launches as timed ones: every rotated copy once
             launch(i)
         ql.synchronize()
         a, b = ql.Event(), ql.Event()
@@ -778,7 +797,7 @@ def attention_rows(ql, np, chain, reps):
     rows = []
 
     def timed(launch, n):
-        for i in range(3):
+        for i in range(n):   # as many warm-up launches as timed ones: every rotated copy once
             launch(i)
         ql.synchronize()
         a, b = ql.Event(), ql.Event()

@@ -117,19 +117,26 @@ __device__ __forceinline__ uintptr_t readlane64(uintptr_t x, int l) {
 // A null block pointer in device memory: the pointer lookup of a missing table
 // entry reads it, so the lookup is one unconditional load.
 __device__ const _Float16* const kNoBlock = nullptr;
+// Likewise an absent table entry: lanes past the pages wanted (or the table's
+// end) read this instead, so the entry lookup is one unconditional load too.
+__device__ const int32_t kNoEntry = -1;
 
 template <bool PAGED, int COUNT>
 struct PagePipe {
     int b = -1;                 // stage 1: table entry of page first + lane%4 (or -1)
     uintptr_t kp = 0, vp = 0;   // stage 2: block pointers as stored (0 = missing)
 
+    // No branch around the load: with one, the compiler's wait before a later
+    // use of any earlier load could not count the loads issued after it and
+    // would wait for all of them.
     __device__ __forceinline__ void entries(const AttnArgs& a, const int32_t* table, int first) {
         if constexpr (PAGED) {
             const int p = (int)(threadIdx.x & 3);
             const int t = first + p;
-            int e = -1;
-            if (p < COUNT && t < a.max_blocks) e = table[t];
-            b = e;
+            const bool ok = p < COUNT && t < a.max_blocks;
+            typedef const int32_t __attribute__((address_space(1)))* GlobalEntryPtr;
+            const int e = *(GlobalEntryPtr)(ok ? table + t : &kNoEntry);
+            b = ok ? e : -1;
         }
     }
     // The loaded pointers are used only by bases(), one tile later: nothing here
@@ -944,15 +951,20 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_decode(AttnArgs a) {
     }
     // one step: stage its K rows, prefetch the wavefront's next step into the
     // registers, multiply, then stage the next step's V rows
+    // Every load of a step is issued unconditionally (lookups for steps past the
+    // end read valid table entries or the null entry, the last step's prefetch
+    // reads the dummy row): with a branch around any of them the compiler could
+    // not count the loads issued after this step's V rows, and its wait for those
+    // rows would wait for the next step's rows too.
     auto run_step = [&]() -> bool {
         const int k0 = k_begin + step * kDecStep;
         const bool more = step + kAttnWaves < n_steps;
         dec_stage_k<HD>(kr, sk, lane);   // after the previous step's K reads (in order)
         // page lookups first: issued after the K/V rows, their waits would also
         // wait for the rows
-        if (step + 2 * kAttnWaves < n_steps) pp.pointers(a);
-        if (step + 3 * kAttnWaves < n_steps) pp.entries(a, table, page_of(step + 3 * kAttnWaves));
-        if (more) dec_fetch_kv<HD, PAGED>(kr, vr, a, plan, pg_next, kvh, k0 + kStride, k_end, dummy, lane);
+        pp.pointers(a);
+        pp.entries(a, table, page_of(step + 3 * kAttnWaves));
+        dec_fetch_kv<HD, PAGED>(kr, vr, a, plan, pg_next, kvh, k0 + kStride, k_end, dummy, lane);
         dec_step<HD>(sk, qf, o, st, sv, k0, k_end, lane, cl2);
         if (!more) return false;
         dec_stage_v<HD>(vr, sv, lane);    // after this step's V^T reads (in order)

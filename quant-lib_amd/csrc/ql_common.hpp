@@ -81,6 +81,15 @@ __device__ __forceinline__ void store_wt(const void* base, uint32_t byte_off, co
                                            kStorePolicy);
 }
 
+// Read of a table that no kernel of the launch writes (ids, slot maps, block
+// pointers, positions) through the constant address space: at a
+// wavefront-uniform index it is a scalar load, on the counter the vector row
+// loads do not use, so waiting for it does not wait for them.
+template <typename T>
+__device__ __forceinline__ T ld_scalar(const T* p) {
+    return *reinterpret_cast<const __attribute__((address_space(4))) T*>(reinterpret_cast<uintptr_t>(p));
+}
+
 // A pointer that is the same in every lane of the wavefront, made scalar.
 template <typename T>
 __device__ __forceinline__ T* uniform(T* p) {

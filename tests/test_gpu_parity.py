@@ -214,6 +214,30 @@ def test_rope_positions_offset_and_fused_qkv_strides(f16):
     assert np.array_equal(gk[:, 2 * 64:], k[:, 2 * 64:])
 
 
+@pytest.mark.parametrize("pairing", [ql.ROPE_HALF, ql.ROPE_INTERLEAVED])
+@pytest.mark.parametrize("H,HK", [(5, 3), (1, 1), (7, 2), (64, 8)])
+def test_rope_f16_d128_unit_shapes(pairing, H, HK):
+    # binary16 head_dim 128 without a cache runs in 1 KiB units of four head
+    # rows: units that straddle Q and K, idle lanes past the last head, padded
+    # row strides (left untouched) and a positions array
+    T = 37
+    pos = np.random.default_rng(H * 10 + HK).integers(0, 1 << 17, size=T).astype(np.int32)
+    gq, gk, q, k = _rope_case(True, T, H, HK, 128, 5e5, pairing, 240 + H, positions=pos,
+                              q_extra=128, k_extra=8)
+    assert np.array_equal(gq[:, H * 128:], q[:, H * 128:])
+    assert np.array_equal(gk[:, HK * 128:], k[:, HK * 128:])
+    # Q only and K only (the reference's launch_fp16_rope takes one tensor per call)
+    for only_q in (True, False):
+        x = _f16(normal(250 + H + only_q, (T, (H if only_q else HK) * 128)))
+        dx = dev(x)
+        n = H if only_q else HK
+        ql.call("ql_rope_f16", ptr(dx) if only_q else None, None if only_q else ptr(dx), T,
+                H if only_q else 9, HK if not only_q else 9, 128, n * 128, n * 128, None, 3, 5e5,
+                pairing, stream())
+        check_f16(host(dx, shape=(T, n * 128)), orc.rope(x, n, 128, 5e5, pairing, pos_offset=3, f16=True),
+                  f"rope f16 d128 {'q' if only_q else 'k'} only")
+
+
 def test_rope_q_only_and_k_only():
     T, H, d = 64, 4, 64
     q = normal(300, (T, H * d))
@@ -440,6 +464,47 @@ def test_paged_kv_append_unaligned_rows_and_bad_slots():
     orc.paged_kv_append_inplace(wk, wv, (np.arange(nb) * blk).astype(np.int64), slots, kn, vn,
                                 layer, L, H, d)
     assert np.array_equal(host(kpool), wk) and np.array_equal(host(vpool), wv)
+
+
+@pytest.mark.parametrize("T,H,d,misalign", [(7, 8, 128, 0), (9, 1, 64, 0), (13, 16, 128, 0), (5, 32, 128, 0),
+                                             (11, 8, 128, 1), (6, 2, 8, 1), (3, 1, 8, 0)])
+def test_paged_kv_append_token_groups_and_misaligned_blocks(T, H, d, misalign):
+    # token counts that do not fill the last group of four, rows of 64 .. 4096
+    # elements (one, two or four vectors per lane, and the wide-row kernel), and
+    # block pointers 2 bytes past 16-byte alignment (element stores)
+    L, layer = 3, 2
+    nb = (T + 15) // 16 + 2
+    blk = L * 16 * H * d
+    r = np.random.default_rng(T * 100 + H * d + misalign)
+    kn = r.integers(0, 60000, size=(T, H, d)).astype(np.uint16)
+    vn = r.integers(0, 60000, size=(T, H, d)).astype(np.uint16)
+    kpool = empty((nb * blk + 8,), np.uint16, fill_bits=GUARD_BYTE)
+    vpool = empty((nb * blk + 8,), np.uint16, fill_bits=GUARD_BYTE)
+    kptrs = dev(np.array([kpool.ptr + 2 * (misalign + blk * b) for b in range(nb)], np.int64))
+    vptrs = dev(np.array([vpool.ptr + 2 * (misalign + blk * b) for b in range(nb)], np.int64))
+    order = r.permutation(nb)
+    slots = np.array([order[t // 16] * 16 + t % 16 for t in range(T)], np.int32)
+    slots[T // 2] = -1
+    dsl, dkn, dvn = dev(slots), dev(kn), dev(vn)
+    ql.call("ql_paged_kv_append_f16", ptr(kptrs), ptr(vptrs), nb, ptr(dsl), ptr(dkn), ptr(dvn), T,
+            layer, L, H, d, stream())
+    wk = np.full(nb * blk + 8, 0xA5A5, np.uint16)
+    wv = wk.copy()
+    orc.paged_kv_append_inplace(wk, wv, (np.arange(nb) * blk + misalign).astype(np.int64), slots, kn,
+                                vn, layer, L, H, d)
+    assert np.array_equal(host(kpool), wk) and np.array_equal(host(vpool), wv)
+
+
+@pytest.mark.parametrize("f16", [False, True])
+def test_embed_empty_vocab_gives_zero_rows(f16):
+    # vocab 0: every id is out of range, so every row is zeros and no table row is read
+    T, dim = 9, 4096
+    dt = np.uint16 if f16 else np.float32
+    table = dev(np.ones(8, dt))                      # smaller than one row
+    ids = dev(np.arange(T, dtype=np.int32))
+    out = Out(T * dim, dt)
+    ql.call("ql_embed_f16" if f16 else "ql_embed_f32", table.ptr, ids.ptr, T, 0, dim, out.ptr, stream())
+    assert not np.any(out.get((T, dim)))
 
 
 # ---- fp16 -> fp32 ------------------------------------------------------------------------------
