@@ -41,13 +41,15 @@ __global__ __launch_bounds__(WPR <= 4 ? kBlock : kWave * WPR) void rmsnorm_rows(
     const int nvec = dim / W;
     const V* wr = reinterpret_cast<const V*>(w);
 
+    // Every lane loads -- rows past the end re-read row 0, indices past the row
+    // its last vector: a load under a per-lane test makes the compiler wait for
+    // it before issuing the next one, which had put a wait for the (cached)
+    // weight load ahead of every row's HBM loads.  The weight is issued first:
+    // loads complete in order, so the wait for the rows covers it.
     V xv[RPT][NV], wv[NV];
     V dv[ADD ? RPT : 1][ADD ? NV : 1];
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-        const int vi = rl + k * TPR;
-        if (vi < nvec) wv[k] = wr[vi];  // shared by every row: keep it cached
-    }
+    for (int k = 0; k < NV; ++k) wv[k] = wr[min(rl + k * TPR, nvec - 1)];  // cached: shared by every row
 #pragma unroll
     for (int r = 0; r < RPT; ++r) {
         const int row = row0 + r;
@@ -55,16 +57,18 @@ __global__ __launch_bounds__(WPR <= 4 ? kBlock : kWave * WPR) void rmsnorm_rows(
         const V* dr = reinterpret_cast<const V*>(ADD ? d + (size_t)(row < rows ? row : 0) * dim : d);
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
-            const int vi = rl + k * TPR;
-            if (row < rows && vi < nvec) {
-                xv[r][k] = load<NT>(xr + vi);
-                if constexpr (ADD) dv[r][k] = load<NT>(dr + vi);
-            }
+            const int vi = min(rl + k * TPR, nvec - 1);
+            xv[r][k] = load<NT>(xr + vi);
+            if constexpr (ADD) dv[r][k] = load<NT>(dr + vi);
         }
     }
+    __builtin_amdgcn_sched_barrier(0);   // every load issued before any arithmetic
 
     // Values stay in D precision (exact for the rounded sum) to halve the
     // register footprint of binary16 rows; they are widened again for output.
+    // Every lane computes; lanes past the row add fmaf(0, 0, ss) == ss.  (With
+    // the arithmetic under a per-lane test the compiler moved the d loads into
+    // it, behind the wait for x.)
     float ss[RPT];
 #pragma unroll
     for (int r = 0; r < RPT; ++r) {
@@ -73,22 +77,22 @@ __global__ __launch_bounds__(WPR <= 4 ? kBlock : kWave * WPR) void rmsnorm_rows(
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
             const int vi = rl + k * TPR;
-            if (row_ok && vi < nvec) {
+            const bool ok = row_ok && vi < nvec;
 #pragma unroll
-                for (int e = 0; e < W; ++e) {
-                    float a = to_f32(xv[r][k].v[e]);
-                    if constexpr (ADD) {
-                        a = a + to_f32(dv[r][k].v[e]);
-                        xv[r][k].v[e] = from_f32<D>(a);
-                        a = to_f32(xv[r][k].v[e]);
-                    }
-                    ss[r] = fmaf(a, a, ss[r]);
+            for (int e = 0; e < W; ++e) {
+                float a = to_f32(xv[r][k].v[e]);
+                if constexpr (ADD) {
+                    a = a + to_f32(dv[r][k].v[e]);
+                    xv[r][k].v[e] = from_f32<D>(a);
+                    a = to_f32(xv[r][k].v[e]);
                 }
-                // the rounded sum x' is final: store it now, before the
-                // row's reduction (measured 0.7% faster than with y)
-                if constexpr (ADD)
-                    store<NT>(reinterpret_cast<V*>(x + (size_t)(row0 + r) * dim) + vi, xv[r][k]);
+                a = ok ? a : 0.0f;
+                ss[r] = fmaf(a, a, ss[r]);
             }
+            // the rounded sum x' is final: store it now, before the row's
+            // reduction (measured 0.7% faster than with y)
+            if (ADD && ok)
+                store<NT>(reinterpret_cast<V*>(x + (size_t)(row0 + r) * dim) + vi, xv[r][k]);
         }
         ss[r] = wave_sum(ss[r]);
     }
@@ -143,30 +147,32 @@ __global__ __launch_bounds__(kWave) void rmsnorm_wave(D* x, const D* __restrict_
     const V* wr = reinterpret_cast<const V*>(w);
     const V* xr = reinterpret_cast<const V*>(x + row * dim);
     const V* dr = reinterpret_cast<const V*>(ADD ? d + row * dim : d);
+    // every lane loads (indices past the row re-read its last vector), the
+    // shared weight first, as in rmsnorm_rows
     V cx[NV], cd[ADD ? NV : 1], wv[NV];
 #pragma unroll
+    for (int k = 0; k < NV; ++k) wv[k] = wr[min(rl + k * kWave, nvec - 1)];   // cached
+#pragma unroll
     for (int k = 0; k < NV; ++k) {
-        const int vi = rl + k * kWave;
-        if (vi < nvec) {
-            cx[k] = load<true>(xr + vi);
-            if constexpr (ADD) cd[k] = load<true>(dr + vi);
-            wv[k] = wr[vi];   // shared by every row: keep it cached
-        }
+        const int vi = min(rl + k * kWave, nvec - 1);
+        cx[k] = load<true>(xr + vi);
+        if constexpr (ADD) cd[k] = load<true>(dr + vi);
     }
-    float ss = 0.0f;
+    __builtin_amdgcn_sched_barrier(0);   // every load issued before any arithmetic
+    float ss = 0.0f;   // every lane computes; lanes past the row add fmaf(0, 0, ss)
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
-        if (rl + k * kWave < nvec) {
+        const bool ok = rl + k * kWave < nvec;
 #pragma unroll
-            for (int e = 0; e < W; ++e) {
-                float a = to_f32(cx[k].v[e]);
-                if constexpr (ADD) {
-                    a = a + to_f32(cd[k].v[e]);
-                    cx[k].v[e] = from_f32<D>(a);
-                    a = to_f32(cx[k].v[e]);
-                }
-                ss = fmaf(a, a, ss);
+        for (int e = 0; e < W; ++e) {
+            float a = to_f32(cx[k].v[e]);
+            if constexpr (ADD) {
+                a = a + to_f32(cd[k].v[e]);
+                cx[k].v[e] = from_f32<D>(a);
+                a = to_f32(cx[k].v[e]);
             }
+            a = ok ? a : 0.0f;
+            ss = fmaf(a, a, ss);
         }
     }
     ss = wave_sum(ss);

@@ -88,12 +88,12 @@ template <typename D, int CACHE>
 __device__ __forceinline__ void cache_rows(const KvDst<D>& kv, int t, int kvw, D*& kd, D*& vd) {
     kd = vd = nullptr;
     if constexpr (CACHE == kPagedCache) {
-        const int slot = kv.slots[t];
+        const int slot = ld_scalar(kv.slots + t);
         if (slot >= 0 && slot / QL_PAGE_SIZE < kv.n_blocks) {
             const int b = slot / QL_PAGE_SIZE;
             const size_t off = ((size_t)kv.layer * QL_PAGE_SIZE + slot % QL_PAGE_SIZE) * (size_t)kvw;
-            kd = kv.kb[b] + off;
-            vd = kv.vb[b] + off;
+            kd = ld_scalar(kv.kb + b) + off;
+            vd = ld_scalar(kv.vb + b) + off;
         }
     } else if constexpr (CACHE == kContigCache) {
         const size_t off = ((size_t)kv.layer * kv.max_seq + kv.pos0 + t) * (size_t)kvw;
@@ -128,7 +128,9 @@ __global__ __launch_bounds__(kBlock) void rope_fast(D* q, D* k, int n_tokens, in
     using V = Vec<D, W>;
 
     const int lane = threadIdx.x & (kWave - 1);
-    const int t = blockIdx.x * (kBlock / kWave) + (threadIdx.x / kWave);
+    // token index made scalar: its position, slot and block pointers are then
+    // read with scalar loads, whose waits do not wait for the row loads
+    const int t = blockIdx.x * (kBlock / kWave) + __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
     if (t >= n_tokens) return;  // wavefront-uniform; no barriers below
     const int npairs = d >> 1;
     const int S = npairs / PPS;  // slots per head; divides 64
@@ -176,7 +178,7 @@ __global__ __launch_bounds__(kBlock) void rope_fast(D* q, D* k, int n_tokens, in
 
     float c[PPS], s[PPS];
     if (h0 < hrot) {  // wavefront-uniform: this group has heads to rotate
-        const int pos = positions ? positions[t] : pos_offset + t;
+        const int pos = positions ? ld_scalar(positions + t) : pos_offset + t;
         float c_own, s_own;
         trig((float)pos * inv.v[lane % npairs], c_own, s_own);
 #pragma unroll
@@ -240,10 +242,12 @@ __global__ __launch_bounds__(kBlock) void rope_generic(D* q, D* k, int n_tokens,
                                                        int pos_offset, float theta,
                                                        KvDst<D> kv) {
     const int lane = threadIdx.x & (kWave - 1);
-    const int t = blockIdx.x * (kBlock / kWave) + (threadIdx.x / kWave);
+    // token index made scalar: its position, slot and block pointers are then
+    // read with scalar loads, whose waits do not wait for the row loads
+    const int t = blockIdx.x * (kBlock / kWave) + __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
     if (t >= n_tokens) return;
     const int npairs = d >> 1;
-    const int pos = positions ? positions[t] : pos_offset + t;
+    const int pos = positions ? ld_scalar(positions + t) : pos_offset + t;
     D* kd = nullptr;
     D* vd = nullptr;
     if constexpr (CACHE != kNoCache) cache_rows<D, CACHE>(kv, t, hk * d, kd, vd);
@@ -300,7 +304,9 @@ __global__ __launch_bounds__(kBlock) void rope_planes(D* q, D* k, int n_tokens, 
     using V = Vec<D, W>;
 
     const int lane = threadIdx.x & (kWave - 1);
-    const int t = blockIdx.x * (kBlock / kWave) + (threadIdx.x / kWave);
+    // token index made scalar: its position, slot and block pointers are then
+    // read with scalar loads, whose waits do not wait for the row loads
+    const int t = blockIdx.x * (kBlock / kWave) + __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
     if (t >= n_tokens) return;  // wavefront-uniform; no barriers below
     const int j = lane % S;
 
@@ -313,21 +319,27 @@ __global__ __launch_bounds__(kBlock) void rope_planes(D* q, D* k, int n_tokens, 
     const int h0 = g * hpw;
     const int h1 = min(nh, h0 + hpw);
     const int nslots = (h1 - h0) * S;
-    // one token per wavefront: the row base is scalar (stores go out as
-    // write-through buffer stores from it)
-    D* row = uniform(plane == 0 ? q + (long long)t * qs
-                     : (plane == 1 ? k + (long long)t * ks : const_cast<D*>(kv.v) + (long long)t * kv.vs));
+    D* row = plane == 0 ? q + (long long)t * qs
+           : (plane == 1 ? k + (long long)t * ks : const_cast<D*>(kv.v) + (long long)t * kv.vs);
+    // the same row base made scalar for the write-through buffer stores (the
+    // loads keep `row`: a pointer rebuilt from integers would make them FLAT
+    // accesses, which also count against the scalar-load counter)
+    D* const row_s = uniform(row);
 
+    // The per-lane inv_freq read goes first (vector loads retire in issue
+    // order, so the trig's wait for it then does not wait for the rows), and
+    // every lane loads (slots past the group re-read its last chunk): a load
+    // under a per-lane test makes the compiler wait for it before the next.
+    const float inv_l = inv.v[lane % NP];
+    asm volatile("" ::: "memory");   // keep the row loads after it
     V lo[MAXU];
     V hi[HALF ? MAXU : 1];
 #pragma unroll
     for (int u = 0; u < MAXU; ++u) {
-        const int sl = lane + u * kWave;
-        if (sl < nslots) {
-            const V* p = reinterpret_cast<const V*>(row + (h0 + sl / S) * HD + j * W);
-            lo[u] = load<true>(p);
-            if constexpr (HALF) hi[u] = load<true>(reinterpret_cast<const V*>(reinterpret_cast<const D*>(p) + NP));
-        }
+        const int sl = min(lane + u * kWave, nslots - 1);
+        const V* p = reinterpret_cast<const V*>(row + (h0 + sl / S) * HD + j * W);
+        lo[u] = load<true>(p);
+        if constexpr (HALF) hi[u] = load<true>(reinterpret_cast<const V*>(reinterpret_cast<const D*>(p) + NP));
     }
 
     D* kd = nullptr;
@@ -361,9 +373,9 @@ __global__ __launch_bounds__(kBlock) void rope_planes(D* q, D* k, int n_tokens, 
         }
     }
 
-    const int pos = positions ? positions[t] : pos_offset + t;
+    const int pos = positions ? ld_scalar(positions + t) : pos_offset + t;
     float c_own, s_own;
-    trig((float)pos * inv.v[lane % NP], c_own, s_own);
+    trig((float)pos * inv_l, c_own, s_own);
     float c[PPS], s[PPS];
 #pragma unroll
     for (int e = 0; e < PPS; ++e) {
@@ -386,7 +398,7 @@ __global__ __launch_bounds__(kBlock) void rope_planes(D* q, D* k, int n_tokens, 
                 ylo.v[2 * e + 1] = from_f32<D>(y1);
             }
             if (!(CACHE != kNoCache && plane == 1 && kv.skip_k_inplace))
-                store_wt(row, (uint32_t)off * sizeof(D), ylo);
+                store_wt(row_s, (uint32_t)off * sizeof(D), ylo);
         } else {
 #pragma unroll
             for (int e = 0; e < PPS; ++e) {
@@ -396,8 +408,8 @@ __global__ __launch_bounds__(kBlock) void rope_planes(D* q, D* k, int n_tokens, 
                 yhi.v[e] = from_f32<D>(y1);
             }
             if (!(CACHE != kNoCache && plane == 1 && kv.skip_k_inplace)) {
-                store_wt(row, (uint32_t)off * sizeof(D), ylo);
-                store_wt(row, (uint32_t)(off + NP) * sizeof(D), yhi);
+                store_wt(row_s, (uint32_t)off * sizeof(D), ylo);
+                store_wt(row_s, (uint32_t)(off + NP) * sizeof(D), yhi);
             }
         }
         if constexpr (CACHE != kNoCache) {
@@ -498,7 +510,7 @@ __global__ __launch_bounds__(kUnitBlock) void rope_units(_Float16* q, _Float16* 
                                          reinterpret_cast<g_u32x4*>(row[i] + 16 * (size_t)c)));
     }
 
-    const int pos = positions ? positions[t] : pos_offset + t;
+    const int pos = positions ? ld_scalar(positions + t) : pos_offset + t;
     float c_own, s_own;
     trig((float)pos * inv_l, c_own, s_own);
     const int p0 = HALF ? (c & 7) * 8 : c * 4;  // first pair of this lane's chunk

@@ -8,9 +8,10 @@
 // i.e. three reads and two writes.  Here the row lives in registers: one read
 // and one write per element, with nontemporal hints.  WPR wavefronts share a
 // row; each lane holds NV 16-byte vectors, lanes past the row end hold -inf
-// (no effect on max or sum).  When the row is exactly NV*64*WPR vectors
-// (FULL) the loads carry no per-vector bounds test, so all NV of them issue
-// back to back; rows past the end re-read the last row and store nothing.
+// (no effect on max or sum).  Every lane loads -- an index past the row
+// re-reads the row's last vector, masked afterwards -- so all NV loads issue
+// back to back; rows that are exactly NV*64*WPR vectors (FULL) skip the masks;
+// rows past the end re-read the last row and store nothing.
 // The fp16 variant (no reference kernel) is the same fp32 arithmetic with
 // binary16 input and RNE binary16 output.
 #include <float.h>
@@ -47,12 +48,12 @@ __global__ __launch_bounds__(WPR <= 4 ? kBlock : kWave * WPR) void softmax_rows(
     const size_t roff = (size_t)(row_ok ? row : rows - 1) * (size_t)cols;
     const V* src = reinterpret_cast<const V*>(in + roff);
 
+    // every lane loads (an index past the row re-reads its last vector, masked
+    // below): a load under a per-lane test makes the compiler wait for it before
+    // issuing the next one
     V raw[NV];
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-        const int vi = rl + k * TPR;
-        if (FULL || vi < nvec) raw[k] = load<true>(src + vi);
-    }
+    for (int k = 0; k < NV; ++k) raw[k] = load<true>(src + (FULL ? rl + k * TPR : min(rl + k * TPR, nvec - 1)));
 
     float v[NV][W];
     float m = -FLT_MAX;
