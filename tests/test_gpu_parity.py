@@ -508,11 +508,13 @@ def test_embed_empty_vocab_gives_zero_rows(f16):
 
 
 # ---- fp16 -> fp32 ------------------------------------------------------------------------------
-@pytest.mark.parametrize("n", [65536, 32000, 13])
-def test_f16_to_f32_bit_exact(n):
-    h = (np.arange(n, dtype=np.uint32) % 65536).astype(np.uint16)
+# offsets in elements: 0 takes the 8-byte-load path, 4 (8-byte but not 16-byte aligned)
+# too, 1 the per-element path; n = 3 has no whole 4-element vector
+@pytest.mark.parametrize("offset,n", [(0, 65536), (0, 32000), (0, 13), (4, 32003), (1, 1001), (0, 3)])
+def test_f16_to_f32_bit_exact(offset, n):
+    h = (np.arange(n, dtype=np.uint32) * 7 % 65536).astype(np.uint16)
     out = Out(n, np.float32)
-    dh = dev(h)
+    dh = dev(h, offset)
     ql.call("ql_f16_to_f32", ptr(dh), out.ptr, n, stream())
     got, want = out.get(), orc.f16_to_f32(h)
     nan = np.isnan(want)
@@ -531,12 +533,15 @@ def _narrow_inputs():
     return np.concatenate([mid, -mid, np.nextafter(mid, np.float32(0)), bits.view(np.float32), special])
 
 
-@pytest.mark.parametrize("offset,n", [(0, None), (1, 1001), (0, 13)])
-def test_f32_to_f16_bit_exact(offset, n):
+# (input offset, n, output offset) in elements: 16-byte-aligned input with an
+# 8-byte-aligned output takes the vector path, offset 1 the per-element path
+@pytest.mark.parametrize("offset,n,out_offset", [(0, None, 0), (1, 1001, 1), (0, 13, 0), (0, 4099, 4),
+                                                 (4, 2001, 4), (0, 3, 0)])
+def test_f32_to_f16_bit_exact(offset, n, out_offset):
     x = _narrow_inputs()
     if n is not None:
         x = x[-n:]
-    out = Out(x.size, np.uint16, offset=offset)
+    out = Out(x.size, np.uint16, offset=out_offset)
     dx = dev(x, offset_elems=offset)
     ql.call("ql_f32_to_f16", ptr(dx), out.ptr, x.size, stream())
     got, want = out.get(), orc.f32_to_f16(x)
