@@ -13,7 +13,8 @@ and attention excluded:
   4. SwiGLU                             gate, up [8192,14336] -> out
 
 One step = one pass of that chain.  The unfused RoPE and paged-append kernels
-are timed separately under "kernels" for comparison.  Inputs are synthetic (seeded normal values
+are timed separately under "kernels" for comparison, each kernel beside a plain
+copy of its byte count (copy_same_bytes, vs_copy).  Inputs are synthetic (seeded normal values
 made on the host and uploaded once) and resident in HBM before timing.  Three
 device buffer sets (~1 GB each) are rotated step to step so no input is still
 in the 256 MB MALL; the KV append rotates over the 32 pool layers.  The
@@ -202,6 +203,19 @@ class Chain:
         self.ql.call("ql_kv_append_f16", self.cp_dst[0].ptr, self.cp_dst[1].ptr, self.cp_src[0].ptr,
                      self.cp_src[1].ptr, 0, 0, COPY_TOKENS, HKV, HD, COPY_TOKENS, 1, self.stream)
 
+    def k_copy_bytes(self, nbytes, i):
+        """A plain copy moving `nbytes` in all (half read, half written) with the
+        same kernel as k_copy, at offsets that rotate through the 2 x 256 MiB
+        source and destination pool so a small copy is not served from the MALL."""
+        tokens = max(1, nbytes // (8 * HKV * HD))      # 2 KiB read + 2 KiB written per token, K and V
+        elems = tokens * HKV * HD
+        nrot = max(1, COPY_ELEMS // elems)
+        off = 2 * (i % nrot) * elems                   # bytes
+        self.ql.call("ql_kv_append_f16", self.cp_dst[0].ptr + off, self.cp_dst[1].ptr + off,
+                     self.cp_src[0].ptr + off, self.cp_src[1].ptr + off, 0, 0, tokens, HKV, HD, tokens, 1,
+                     self.stream)
+        return 8 * elems                               # bytes moved: K and V, 2 B each, read and written
+
     def step(self):
         i = self.step_no
         self.step_no += 1
@@ -240,11 +254,15 @@ def breakdown(chain, ql, reps):
     dispatch gap, which is what a rocprofv3 kernel trace averages to within
     about 1%.  events_per_launch: a second pass with an event pair around
     every launch (each pair adds the events' own cost, a few us), kept for
-    its spread."""
-    out = {}
-    for name in ["add_rmsnorm_f16", "rope_paged_kv_append_f16", "rope_q_paged_kv_append_f16",
-                 "rope_f16", "paged_kv_append_f16", "swiglu_f16", "embed_f16", "copy_calibration"]:
-        launch = chain.kernel_launcher(name)
+    its spread.
+
+    copy_same_bytes: the plain copy of copy_calibration, resized to move the
+    kernel's algorithmic bytes (half read, half written) and timed the same way.
+    A launch carries a fixed cost (ramp-up and drain, ~2 us) besides its
+    bytes, so a 67 MB copy runs at ~5.3 TB/s and a 1 GB one at ~6.5-6.7: the
+    copy of the same size is the kernel's practical ceiling, and vs_copy =
+    copy us / kernel us (1.0 = as fast as a copy of its bytes)."""
+    def back_to_back(launch):
         for i in range(WARM):
             launch(i)
         ql.synchronize()
@@ -254,7 +272,13 @@ def breakdown(chain, ql, reps):
             launch(i)
         a1.record(chain.stream)
         ql.synchronize()
-        mean = a0.elapsed_ms(a1) * 1e3 / reps
+        return a0.elapsed_ms(a1) * 1e3 / reps
+
+    out = {}
+    for name in ["add_rmsnorm_f16", "rope_paged_kv_append_f16", "rope_q_paged_kv_append_f16",
+                 "rope_f16", "paged_kv_append_f16", "swiglu_f16", "embed_f16", "copy_calibration"]:
+        launch = chain.kernel_launcher(name)
+        mean = back_to_back(launch)
         evs = [(ql.Event(), ql.Event()) for _ in range(reps)]
         for i, (a, b) in enumerate(evs):
             a.record(chain.stream)
@@ -266,6 +290,12 @@ def breakdown(chain, ql, reps):
         out[name] = {"us_mean": round(mean, 2), "bytes": BYTES[name], "GBps": round(gbs, 1),
                      "frac_peak": round(gbs / PEAK_HBM_GBS, 4),
                      "events_per_launch": percentiles(us)}
+        if name != "copy_calibration":
+            moved = chain.k_copy_bytes(BYTES[name], 0)
+            cp = back_to_back(lambda i: chain.k_copy_bytes(BYTES[name], i))
+            out[name]["copy_same_bytes"] = {"bytes": moved, "us_mean": round(cp, 2),
+                                            "GBps": round(moved / (cp * 1e-6) / 1e9, 1)}
+            out[name]["vs_copy"] = round(cp * BYTES[name] / moved / mean, 3)
     return out
 
 
