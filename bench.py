@@ -26,8 +26,8 @@ written once) / wall time per step.  128 untimed steps (~30 ms) come first, and
 every single-kernel pass starts after ~30 ms of untimed device work: the clocks
 take ~20 ms of sustained load to ramp up.
 
-The embedding gather (once per forward, not per layer) is timed separately and
-reported under "kernels".  The roofline entry is for the dominant kernel,
+The embedding gather and the final RMSNorm (once per forward, not per layer)
+are timed separately and reported under "kernels".  The roofline entry is for the dominant kernel,
 SwiGLU fp16 [8192 x 14336]: 3 x 8192 x 14336 x 2 B = 704,643,072 B per launch,
 timed after the timed steps in a pass of its own: back-to-back launches on the
 work stream between one pair of HIP events.  The timed steps themselves carry
@@ -77,6 +77,7 @@ WARM = 32
 
 BYTES = {
     "add_rmsnorm_f16": 4 * T * D * 2 + 2 * D,                     # read x,d; write x',y; w
+    "rmsnorm_f16": 2 * T * D * 2 + 2 * D,                         # final norm: read x; write y; w
     "rope_f16": 2 * T * (HQ + HKV) * HD * 2,                      # in-place read+write Q,K
     "paged_kv_append_f16": 4 * T * HKV * HD * 2 + 4 * T,          # read K,V; write K,V; slots
     "swiglu_f16": 3 * T * F * 2,                                  # read gate,up; write out
@@ -177,6 +178,9 @@ class Chain:
         self.ql.call("ql_add_rmsnorm_f16", s["x"].ptr, s[which].ptr, w.ptr, s["y"].ptr, T, D, EPS,
                      self.stream)
 
+    def k_rmsnorm(self, s):
+        self.ql.call("ql_rmsnorm_f16", s["x"].ptr, self.w_ffn.ptr, s["y"].ptr, T, D, EPS, self.stream)
+
     def k_rope(self, s):
         self.ql.call("ql_rope_f16", s["q"].ptr, s["k"].ptr, T, HQ, HKV, HD, HQ * HD, HKV * HD, None,
                      0, THETA, self.ql.ROPE_HALF, self.stream)
@@ -232,6 +236,7 @@ class Chain:
     def kernel_launcher(self, name):
         return {
             "add_rmsnorm_f16": lambda i: self.k_add_rmsnorm(self.sets[i % NSETS], "d1"),
+            "rmsnorm_f16": lambda i: self.k_rmsnorm(self.sets[i % NSETS]),
             "rope_f16": lambda i: self.k_rope(self.rope_sets[i % NROPE]),
             "paged_kv_append_f16": lambda i: self.k_paged(self.rope_sets[i % NROPE], i % L_POOL),
             "rope_paged_kv_append_f16": lambda i: self.k_rope_paged(self.rope_sets[i % NROPE], i % L_POOL),
@@ -300,7 +305,8 @@ def breakdown(chain, ql, reps):
 
     out = {}
     for name in ["add_rmsnorm_f16", "rope_paged_kv_append_f16", "rope_q_paged_kv_append_f16",
-                 "rope_f16", "paged_kv_append_f16", "swiglu_f16", "embed_f16", "copy_calibration"]:
+                 "rope_f16", "paged_kv_append_f16", "swiglu_f16", "embed_f16", "rmsnorm_f16",
+                 "copy_calibration"]:
         launch = chain.kernel_launcher(name)
         mean = back_to_back(launch)
         evs = [(ql.Event(), ql.Event()) for _ in range(reps)]
@@ -508,7 +514,7 @@ def all_configs(ql, np, reps, only=()):
     rows.append(cpu_softmax_row(np, x4))
     del x4
     # C5: the layer-chain kernels (one launch each, as in the default mode)
-    for name in ["embed_f16", "add_rmsnorm_f16", "rope_f16", "paged_kv_append_f16",
+    for name in ["embed_f16", "add_rmsnorm_f16", "rmsnorm_f16", "rope_f16", "paged_kv_append_f16",
                  "rope_paged_kv_append_f16", "rope_q_paged_kv_append_f16", "swiglu_f16",
                  "copy_calibration"]:
         launch = chain.kernel_launcher(name)

@@ -125,7 +125,11 @@ __global__ __launch_bounds__(WPR <= 4 ? kBlock : kWave * WPR) void rmsnorm_rows(
 #pragma unroll
                 for (int e = 0; e < W; ++e)
                     y.v[e] = from_f32<D>((to_f32(xv[r][k].v[e]) * inv) * to_f32(wv[k].v[e]));
-                store<NT>(orow + vi, y);
+                // plain RMSNorm writes y through (sc1 nt): 25.8 -> 24.3 us at
+                // 8192 x 4096 binary16 on MI355X; with the fused add it measured
+                // no faster (x' and y both 0.5% either way), so it keeps NT
+                if constexpr (!ADD && NT) store_wt(uniform(orow), (uint32_t)vi * (uint32_t)sizeof(V), y);
+                else store<NT>(orow + vi, y);
             }
         }
     }
@@ -269,10 +273,22 @@ hipError_t rmsnorm_dispatch(D* x, const D* d, const D* w, D* out, int rows, int 
                                d, w, out, dim, eps);
         return hipGetLastError();
     }
+    if (vec_ok && !ADD && nvec > 64 && nvec <= 1024) {
+        // Plain RMSNorm reads one row, not two: two 16-byte vectors per lane
+        // over half the wavefronts keep as many bytes in flight per lane as the
+        // fused kernel's x and d.  Measured on MI355X (8192 rows, rotating
+        // buffers): binary16 4096 wide 24.3 -> 23.1 us, 8192 wide 52.2 -> 44.6,
+        // 1024 wide 7.8 -> 6.8; fp32 4096 wide 51.6 -> 44.4; 2048 wide equal.
+        if (nvec <= 128) return launch_fast<D, 2, 1, ADD>(x, d, w, out, rows, dim, eps, stream);
+        if (nvec <= 256) return launch_fast<D, 2, 2, ADD>(x, d, w, out, rows, dim, eps, stream);
+        if (nvec <= 512) return launch_fast<D, 2, 4, ADD>(x, d, w, out, rows, dim, eps, stream);
+        return launch_fast<D, 2, 8, ADD>(x, d, w, out, rows, dim, eps, stream);
+    }
     if (vec_ok) {
         // Spread a row over as many wavefronts as it has 64-vector chunks (up
-        // to 16): one 16-byte vector per lane measured fastest (more waves in
-        // flight, shorter reduction tails).
+        // to 16): one 16-byte vector per lane measured fastest for the fused
+        // add (more waves in flight, shorter reduction tails; two vectors per
+        // lane 0.1-1.9% slower at 1024-8192 wide).
         if (nvec <= 64) return launch_fast<D, 1, 1, ADD>(x, d, w, out, rows, dim, eps, stream);
         if (nvec <= 128) return launch_fast<D, 1, 2, ADD>(x, d, w, out, rows, dim, eps, stream);
         if (nvec <= 256) return launch_fast<D, 1, 4, ADD>(x, d, w, out, rows, dim, eps, stream);
