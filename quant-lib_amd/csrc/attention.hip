@@ -168,24 +168,6 @@ struct PagePipe {
     }
 };
 
-// Address of key row j (its d values are contiguous) for this KV head, or 0
-// when the key has no backing block.  kv0 = first key of the tile j is in.
-template <bool PAGED>
-__device__ __forceinline__ uintptr_t key_row(const AttnArgs& a, const _Float16* base,
-                                             const uintptr_t* pages, int kvh, int kv0, int j,
-                                             int hd) {
-    if constexpr (PAGED) {
-        const int p = (j - kv0) >> 4;
-        const uintptr_t pb = p == 0 ? pages[0] : p == 1 ? pages[1] : p == 2 ? pages[2] : pages[3];
-        const uintptr_t row_bytes = (uintptr_t)a.n_kv_heads * hd * sizeof(_Float16);
-        return pb ? pb + (uintptr_t)(j & (QL_PAGE_SIZE - 1)) * row_bytes : 0;
-    } else {
-        (void)pages;
-        (void)kv0;
-        return reinterpret_cast<uintptr_t>(base + (size_t)j * a.kv_stride + (size_t)kvh * hd);
-    }
-}
-
 typedef const __attribute__((address_space(1))) half8* GlobalHalf8Ptr;
 typedef uint32_t u32x4g __attribute__((ext_vector_type(4)));
 typedef const __attribute__((address_space(1))) u32x4g* GlobalU4Ptr;
@@ -195,20 +177,9 @@ __device__ __forceinline__ half8 load_nt16(uintptr_t p) {
     return __builtin_bit_cast(half8, __builtin_nontemporal_load((GlobalU4Ptr)p));
 }
 
-// 16 bytes of chunk ch of a key row (row == 0: missing key -> zeros).  Loads
-// always target a valid address (dummy stands in for a missing row) and the
-// value is selected afterwards, so there are no branches; loads are issued in
-// the global address space so they count only against the vector memory
-// counter (LDS waits do not wait for them).
-__device__ __forceinline__ half8 load_chunk(uintptr_t row, int ch, uintptr_t dummy) {
-    const bool ok = row != 0;
-    const uintptr_t src = (ok ? row : dummy) + 16 * (uintptr_t)ch;
-    const half8 x = *(GlobalHalf8Ptr)src;
-    return ok ? x : half8{};
-}
-
-// The same for page pointers that are not 16-byte aligned (caller-provided
-// pools): element-wise loads.  Used for a whole tile, chosen once per tile.
+// 16 bytes of chunk ch of a key row (row == 0: missing key -> zeros) for page
+// pointers that are not 16-byte aligned (caller-provided pools): element-wise
+// loads.  Used for a whole tile, chosen once per tile.
 __device__ __forceinline__ half8 load_chunk_unaligned(uintptr_t row, int ch) {
     half8 r{};
     if (row != 0) {
@@ -645,9 +616,14 @@ struct Dec {
         kAttnWaves * WAVE_V * 2 > PART * 4 ? kAttnWaves * WAVE_V * 2 : PART * 4;
 };
 
+// Rows of one step as loaded: chunk lane%CH of keys KPL*(lane/CH) + i.  A key
+// with no backing row (past the split's end, or its page missing from the block
+// table) was loaded from the dummy row and is zeroed when staged; on a page that
+// is not 16-byte aligned every row was, and staging re-reads the rows element by
+// element (dec_rows says which, from the step's first key and its pages).
 template <int HD>
 struct DecK {
-    half8 k[Dec<HD>::KPL];   // rows as loaded: chunk lane%CH of keys KPL*(lane/CH) + i
+    half8 k[Dec<HD>::KPL];
 };
 template <int HD>
 struct DecV {
@@ -663,41 +639,29 @@ struct DecPlan {
     uint32_t row_bytes;   // uniform
     uint32_t v_off;       // the lane's first key; key i adds i * row_bytes
     int v_page;
+    int key;              // the lane's first key in the step
 
     __device__ __forceinline__ DecPlan(const AttnArgs& a, int kvh, int lane) {
         row_bytes = PAGED ? (uint32_t)(a.n_kv_heads * HD * sizeof(_Float16))
                           : (uint32_t)(a.kv_stride * sizeof(_Float16));
         const uint32_t head_bytes = PAGED ? 0u : (uint32_t)(kvh * HD * sizeof(_Float16));
         const int ch = lane % T::CH, kg = lane / T::CH;
-        const int key = T::KPL * kg;   // its KPL keys stay inside one page
+        key = T::KPL * kg;   // its KPL keys stay inside one page
         v_page = key >> 4;
         v_off = (uint32_t)(PAGED ? (key & 15) : key) * row_bytes + head_bytes + 16u * ch;
     }
 };
 
-// A full 32-key step whose two pages are present and aligned: no checks.
-template <bool PAGED>
-__device__ __forceinline__ bool dec_clean(const Pages& pg, int k0, int k_end) {
-    bool clean = k0 + kDecStep <= k_end;
-    if constexpr (PAGED) clean = clean && !pg.misaligned && pg.k[0] && pg.k[1] && pg.v[0] && pg.v[1];
-    return clean;
-}
-
-// K rows of a step that is not clean (last step, holes in the table, misaligned
-// pages): lane owns chunk lane%CH of keys k0 + KPL*(lane/CH) + i, checked loads.
-template <int HD, bool PAGED>
-__device__ __forceinline__ void dec_fetch_k_checked(DecK<HD>& r, const AttnArgs& a, const Pages& pg,
-                                                    int kvh, int k0, int k_end, uintptr_t dummy,
-                                                    int lane) {
-    using T = Dec<HD>;
-    const int ch = lane % T::CH, kg = lane / T::CH;
-    const bool unaligned = PAGED && pg.misaligned;   // wavefront-uniform
+// The 16 bytes at p for a page pointer that is not 16-byte aligned (caller-
+// provided pools): element-wise loads in the global address space (generic
+// loads would also count against the LDS counter).
+__device__ __forceinline__ half8 load8_unaligned(uintptr_t p) {
+    const __attribute__((address_space(1))) _Float16* e =
+        reinterpret_cast<const __attribute__((address_space(1))) _Float16*>(p);
+    half8 r;
 #pragma unroll
-    for (int i = 0; i < T::KPL; ++i) {
-        const int j = k0 + T::KPL * kg + i;
-        const uintptr_t row = j < k_end ? key_row<PAGED>(a, a.k, pg.k, kvh, k0, j, HD) : 0;
-        r.k[i] = unaligned ? load_chunk_unaligned(row, ch) : load_chunk(row, ch, dummy);
-    }
+    for (int i = 0; i < 8; ++i) r[i] = e[i];
+    return r;
 }
 
 // K stage: row `key` holds its 16-byte chunk c in slot kt_slot(key, c).  Fragment
@@ -709,10 +673,54 @@ __device__ __forceinline__ int kt_slot(int key, int c) {
     return HD == 128 ? (c ^ (key & 15)) : (c ^ ((key >> 1) & 7));
 }
 
-template <int HD>
-__device__ __forceinline__ void dec_stage_k(const DecK<HD>& r, _Float16* sk, int lane) {
+// A step whose 32 keys all exist on present, aligned pages: nothing to zero or
+// re-read at staging.
+template <bool PAGED>
+__device__ __forceinline__ bool dec_full(const uintptr_t* pages, bool misaligned, int k0, int k_end) {
+    bool full = k0 + kDecStep <= k_end;
+    if constexpr (PAGED) full = full && !misaligned && pages[0] && pages[1];
+    return full;
+}
+
+// The lane's chunk of its first key in the step at k0 (0 = no page), and which
+// of its KPL keys have a row (bit i).
+template <int HD, bool PAGED>
+__device__ __forceinline__ uintptr_t dec_rows(const AttnArgs& a, const DecPlan<HD, PAGED>& plan,
+                                              const uintptr_t* pages, const _Float16* base, int k0,
+                                              int k_end, uint32_t& live) {
+    using T = Dec<HD>;
+    uintptr_t b;
+    if constexpr (PAGED) {
+        (void)base;
+        b = plan.v_page == 0 ? pages[0] : pages[1];
+    } else {
+        (void)pages;
+        b = reinterpret_cast<uintptr_t>(base) + (uintptr_t)k0 * (uintptr_t)a.kv_stride * sizeof(_Float16);
+    }
+    const int n_in = k_end - (k0 + plan.key);
+    uint32_t in = 0;
+#pragma unroll
+    for (int i = 0; i < T::KPL; ++i) in |= (uint32_t)(i < n_in) << i;
+    live = b ? in : 0u;
+    return b ? b + plan.v_off : 0;
+}
+
+template <int HD, bool PAGED>
+__device__ __forceinline__ void dec_stage_k(DecK<HD>& r, _Float16* sk, const AttnArgs& a,
+                                            const DecPlan<HD, PAGED>& plan, const Pages& pg, int k0,
+                                            int k_end, int lane) {
     using T = Dec<HD>;
     const int ch = lane % T::CH, kg = lane / T::CH;
+    if (!dec_full<PAGED>(pg.k, pg.misaligned, k0, k_end)) {   // wavefront-uniform
+        uint32_t live;
+        const uintptr_t row = dec_rows<HD, PAGED>(a, plan, pg.k, a.k, k0, k_end, live);
+#pragma unroll
+        for (int i = 0; i < T::KPL; ++i) {
+            if (PAGED && pg.misaligned && ((live >> i) & 1))
+                r.k[i] = load8_unaligned(row + (uintptr_t)i * plan.row_bytes);
+            if (!((live >> i) & 1)) r.k[i] = half8{};
+        }
+    }
 #pragma unroll
     for (int i = 0; i < T::KPL; ++i) {
         const int key = T::KPL * kg + i;
@@ -720,52 +728,38 @@ __device__ __forceinline__ void dec_stage_k(const DecK<HD>& r, _Float16* sk, int
     }
 }
 
-// V rows of a step that is not clean, as the K rows.
-template <int HD, bool PAGED>
-__device__ __forceinline__ void dec_fetch_v_checked(DecV<HD>& r, const AttnArgs& a, const Pages& pg,
-                                                    int kvh, int k0, int k_end, uintptr_t dummy,
-                                                    int lane) {
-    using T = Dec<HD>;
-    const int ch = lane % T::CH, kg = lane / T::CH;
-    const bool unaligned = PAGED && pg.misaligned;   // wavefront-uniform
-#pragma unroll
-    for (int i = 0; i < T::KPL; ++i) {
-        const int j = k0 + T::KPL * kg + i;
-        const uintptr_t row = j < k_end ? key_row<PAGED>(a, a.v, pg.v, kvh, k0, j, HD) : 0;
-        r.v[i] = unaligned ? load_chunk_unaligned(row, ch) : load_chunk(row, ch, dummy);
-    }
-}
-
-// K and V rows of one step: lane owns chunk lane%CH of keys k0 + KPL*(lane/CH) + i.
-// A clean step issues all 2*KPL loads back to back, nontemporal (each row is
-// read by one workgroup), in one straight-line block: with the K and V paths as
-// separate branches the compiler waited for the K loads before issuing the V
-// loads.
+// K and V rows of one step.  Every step issues the same 2*KPL loads, back to
+// back and nontemporal (each row is read by one workgroup), with no branch:
+// a lane whose page is missing or misaligned reads its chunk of the dummy row
+// KPL times; keys past the end read a row that exists (the rest of their page,
+// or for contiguous K/V the last key's row), and staging zeroes or re-reads
+// them.  (With the checked loads of the last step and of missing pages as a
+// separate branch, the compiler's wait before the first product of every step,
+// at the join of the two paths, waited for 13 of the 16 rows just issued for
+// the next step.)
 template <int HD, bool PAGED>
 __device__ __forceinline__ void dec_fetch_kv(DecK<HD>& rk, DecV<HD>& rv, const AttnArgs& a,
-                                             const DecPlan<HD, PAGED>& plan, const Pages& pg, int kvh,
+                                             const DecPlan<HD, PAGED>& plan, const Pages& pg,
                                              int k0, int k_end, uintptr_t dummy, int lane) {
     using T = Dec<HD>;
-    if (dec_clean<PAGED>(pg, k0, k_end)) {   // wavefront-uniform
-        uintptr_t kbase, vbase;
-        if constexpr (PAGED) {
-            kbase = plan.v_page == 0 ? pg.k[0] : pg.k[1];
-            vbase = plan.v_page == 0 ? pg.v[0] : pg.v[1];
-        } else {
-            const uintptr_t step = (uintptr_t)k0 * (uintptr_t)a.kv_stride * sizeof(_Float16);
-            kbase = reinterpret_cast<uintptr_t>(a.k) + step;
-            vbase = reinterpret_cast<uintptr_t>(a.v) + step;
-        }
+    uint32_t klive, vlive;
+    const uintptr_t krow = dec_rows<HD, PAGED>(a, plan, pg.k, a.k, k0, k_end, klive);
+    const uintptr_t vrow = dec_rows<HD, PAGED>(a, plan, pg.v, a.v, k0, k_end, vlive);
+    const bool mis = PAGED && pg.misaligned;
+    const int n_in = k_end - (k0 + plan.key);
+    // rows a lane may read: all KPL of its page (paged), up to the last key (contiguous)
+    const int last = PAGED ? T::KPL - 1 : (n_in > 0 ? min(n_in, T::KPL) - 1 : 0);
+    const bool kok = krow != 0 && !mis && (PAGED || n_in > 0);
+    const bool vok = vrow != 0 && !mis && (PAGED || n_in > 0);
+    const uintptr_t dchunk = dummy + 16u * (uint32_t)(lane % T::CH);
+    const uintptr_t kb = kok ? krow : dchunk, vb = vok ? vrow : dchunk;
+    const uint32_t ks = kok ? plan.row_bytes : 0u, vs = vok ? plan.row_bytes : 0u;
+    (void)klive;
+    (void)vlive;
 #pragma unroll
-        for (int i = 0; i < T::KPL; ++i)
-            rk.k[i] = load_nt16(kbase + plan.v_off + (uintptr_t)i * plan.row_bytes);
+    for (int i = 0; i < T::KPL; ++i) rk.k[i] = load_nt16(kb + (uintptr_t)((uint32_t)min(i, last) * ks));
 #pragma unroll
-        for (int i = 0; i < T::KPL; ++i)
-            rv.v[i] = load_nt16(vbase + plan.v_off + (uintptr_t)i * plan.row_bytes);
-        return;
-    }
-    dec_fetch_k_checked<HD, PAGED>(rk, a, pg, kvh, k0, k_end, dummy, lane);
-    dec_fetch_v_checked<HD, PAGED>(rv, a, pg, kvh, k0, k_end, dummy, lane);
+    for (int i = 0; i < T::KPL; ++i) rv.v[i] = load_nt16(vb + (uintptr_t)((uint32_t)min(i, last) * vs));
 }
 
 // V^T stage: row d, keys KPL*kg + i.  The 8-byte unit u (4 keys) of row r is
@@ -774,10 +768,22 @@ __device__ __forceinline__ void dec_fetch_kv(DecK<HD>& rk, DecV<HD>& rv, const A
 // per 16 lanes.
 __device__ __forceinline__ int vt_unit(int r, int u) { return u ^ ((r >> 4) & 7); }
 
-template <int HD>
-__device__ __forceinline__ void dec_stage_v(const DecV<HD>& r, _Float16* sv, int lane) {
+template <int HD, bool PAGED>
+__device__ __forceinline__ void dec_stage_v(DecV<HD>& r, _Float16* sv, const AttnArgs& a,
+                                            const DecPlan<HD, PAGED>& plan, const Pages& pg, int k0,
+                                            int k_end, int lane) {
     using T = Dec<HD>;
     const int ch = lane % T::CH, kg = lane / T::CH;
+    if (!dec_full<PAGED>(pg.v, pg.misaligned, k0, k_end)) {   // wavefront-uniform
+        uint32_t live;
+        const uintptr_t row = dec_rows<HD, PAGED>(a, plan, pg.v, a.v, k0, k_end, live);
+#pragma unroll
+        for (int i = 0; i < T::KPL; ++i) {
+            if (PAGED && pg.misaligned && ((live >> i) & 1))
+                r.v[i] = load8_unaligned(row + (uintptr_t)i * plan.row_bytes);
+            if (!((live >> i) & 1)) r.v[i] = half8{};
+        }
+    }
 #pragma unroll
     for (int i = 0; i < T::KPL; i += 4)
 #pragma unroll
@@ -934,20 +940,22 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_decode(AttnArgs a) {
     PagePipe<PAGED, kStepPages> pp;
     int step = wave;
     Pages pg_next{};
+    Pages pg_k{};   // pages of the K rows in kr
     auto page_of = [&](int sidx) { return (k_begin + sidx * kDecStep) >> 4; };
     if (step < n_steps) {
         const int k0 = k_begin + step * kDecStep;
         pp.entries(a, table, page_of(step));
         pp.pointers(a);
         const Pages pg = pp.bases(a, kvh, HD);
+        pg_k = pg;
         if (step + kAttnWaves < n_steps) {
             pp.entries(a, table, page_of(step + kAttnWaves));
             pp.pointers(a);
             pg_next = pp.bases(a, kvh, HD);
         }
         if (step + 2 * kAttnWaves < n_steps) pp.entries(a, table, page_of(step + 2 * kAttnWaves));
-        dec_fetch_kv<HD, PAGED>(kr, vr, a, plan, pg, kvh, k0, k_end, dummy, lane);
-        dec_stage_v<HD>(vr, sv, lane);
+        dec_fetch_kv<HD, PAGED>(kr, vr, a, plan, pg, k0, k_end, dummy, lane);
+        dec_stage_v<HD, PAGED>(vr, sv, a, plan, pg, k0, k_end, lane);
     }
     // one step: stage its K rows, prefetch the wavefront's next step into the
     // registers, multiply, then stage the next step's V rows
@@ -959,15 +967,16 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_decode(AttnArgs a) {
     auto run_step = [&]() -> bool {
         const int k0 = k_begin + step * kDecStep;
         const bool more = step + kAttnWaves < n_steps;
-        dec_stage_k<HD>(kr, sk, lane);   // after the previous step's K reads (in order)
+        dec_stage_k<HD, PAGED>(kr, sk, a, plan, pg_k, k0, k_end, lane);   // after the previous step's K reads (in order)
         // page lookups first: issued after the K/V rows, their waits would also
         // wait for the rows
         pp.pointers(a);
         pp.entries(a, table, page_of(step + 3 * kAttnWaves));
-        dec_fetch_kv<HD, PAGED>(kr, vr, a, plan, pg_next, kvh, k0 + kStride, k_end, dummy, lane);
+        dec_fetch_kv<HD, PAGED>(kr, vr, a, plan, pg_next, k0 + kStride, k_end, dummy, lane);
         dec_step<HD>(sk, qf, o, st, sv, k0, k_end, lane, cl2);
         if (!more) return false;
-        dec_stage_v<HD>(vr, sv, lane);    // after this step's V^T reads (in order)
+        dec_stage_v<HD, PAGED>(vr, sv, a, plan, pg_next, k0 + kStride, k_end, lane);    // after this step's V^T reads (in order)
+        pg_k = pg_next;
         if (step + 2 * kAttnWaves < n_steps) pg_next = pp.bases(a, kvh, HD);
         step += kAttnWaves;
         return true;
