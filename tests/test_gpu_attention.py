@@ -369,6 +369,39 @@ def test_paged_decode_splits_and_one_pass_agree_with_oracle(h, hkv, d):
     assert np.array_equal(out.get((S, h, d)), results["one pass"])
 
 
+@pytest.mark.parametrize("h,hkv,d", [(32, 8, 128), (8, 2, 64)])
+@pytest.mark.parametrize("split", [False, True])
+def test_paged_decode_holed_tables(h, hkv, d, split):
+    # decode steps over block tables with a hole (-1) and a block index past the
+    # pool: the keys of those pages read as zero rows (score 0, value 0), as in
+    # the prefill kernel; ragged context lengths end steps inside a page
+    ctx = [75, 40, 130]
+    L, layer = 2, 1
+    pool, bt, ks, vs, q = _decode_setup(ctx, h, hkv, d, L, layer, 0x51A100A0)
+    bt = bt.copy()
+    bt[0, 1] = -1
+    bt[2, 3] = pool.nb + 5
+    kz, vz = [k.copy() for k in ks], [v.copy() for v in vs]
+    kz[0][16:32] = 0
+    vz[0][16:32] = 0
+    kz[2][48:64] = 0
+    vz[2][48:64] = 0
+    S = len(ctx)
+    dq, dctx, dbt = dev(q), dev(np.array(ctx, np.int32)), dev(bt)
+    size = ctypes.c_size_t()
+    ql.call("ql_paged_decode_workspace_size", S, h, hkv, d, max(ctx), ctypes.addressof(size))
+    nbytes = size.value if split else 0
+    ws = empty((max(nbytes, 1),), np.uint8, fill_bits=0x7F) if nbytes else None
+    out = Out(S * h * d, np.uint16)
+    ql.call("ql_paged_decode_attention_f16", dq.ptr, out.ptr, h * d, h * d, S, dctx.ptr, max(ctx),
+            dbt.ptr, bt.shape[1], pool.kptrs.ptr, pool.vptrs.ptr, pool.nb, layer, L, h, hkv, d,
+            ws.ptr if ws else None, nbytes, stream())
+    got = out.get((S, h, d))
+    for s in range(S):
+        want = orc.attention(q[s:s + 1], kz[s], vz[s], h, hkv, True, f16=True)
+        check_attn(got[s:s + 1], want, vs[s], f"holed decode seq {s} ctx {ctx[s]} split {split}")
+
+
 def test_paged_decode_batch_c5_heads_long_context():
     # 16 sequences x 4096-token contexts, Llama-3-8B heads, split over the workspace
     S, C, h, hkv, d, L, layer = 16, 4096, 32, 8, 128, 2, 1
