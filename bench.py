@@ -33,7 +33,8 @@ timed after the timed steps in a pass of its own: back-to-back launches on the
 work stream between one pair of HIP events.  The timed steps themselves carry
 no instrumentation: one event pair and a host clock at their edges only.
 
-`--all-configs` times every BASELINE config (C1-C5) one kernel at a time and
+`--all-configs` times every BASELINE config (C1-C5) one kernel at a time, each
+beside a plain copy of its byte count, and
 adds the attention that consumes the path's output: causal prefill over the
 8192 tokens (contiguous, and over the paged pool the chain writes), reported in
 TFLOP/s against the dense fp16 matrix peak, and paged decode (64 sequences x
@@ -461,8 +462,23 @@ def all_configs(ql, np, reps, only=()):
         us = a.elapsed_ms(b) * 1e3 / reps
         gbs = nbytes / (us * 1e-6) / 1e9
         rows.append({"config": cfg, "kernel": name, "bytes": nbytes, "us": round(us, 2),
-                     "GBps": round(gbs, 1), "frac_peak": round(gbs / PEAK_HBM_GBS, 4)})
+                     "GBps": round(gbs, 1), "frac_peak": round(gbs / PEAK_HBM_GBS, 4),
+                     **copy_same(nbytes, us)})
         del bufs
+
+    def copy_same(nbytes, us):
+        """A plain copy of the row's byte count, timed the same way (see breakdown)."""
+        moved = chain.k_copy_bytes(nbytes, 0)
+        for i in range(WARM):
+            chain.k_copy_bytes(nbytes, i)
+        ql.synchronize()
+        a, b = ql.Event(), ql.Event()
+        a.record(st)
+        for i in range(reps):
+            chain.k_copy_bytes(nbytes, i)
+        b.record(st)
+        cp = a.elapsed_ms(b) * 1e3 / reps
+        return {"copy_same_bytes_us": round(cp, 2), "vs_copy": round(cp * nbytes / moved / us, 3)}
 
     def randn(*shape, clip=None, sigma=1.0):
         x = r.standard_normal(size=shape, dtype=np.float32) * np.float32(sigma)
@@ -530,7 +546,8 @@ def all_configs(ql, np, reps, only=()):
         us = a.elapsed_ms(b) * 1e3 / reps
         gbs = BYTES[name] / (us * 1e-6) / 1e9
         rows.append({"config": "C5 T=8192 llama3-8b", "kernel": name, "bytes": BYTES[name],
-                     "us": round(us, 2), "GBps": round(gbs, 1), "frac_peak": round(gbs / PEAK_HBM_GBS, 4)})
+                     "us": round(us, 2), "GBps": round(gbs, 1), "frac_peak": round(gbs / PEAK_HBM_GBS, 4),
+                     **(copy_same(BYTES[name], us) if name != "copy_calibration" else {})})
     rows += attention_rows(ql, np, chain, reps) if want("attention") else []
     rows += layer_rows(ql, np, chain, reps) if want("layer") else []
     del chain
@@ -948,14 +965,15 @@ def main():
         sys.exit(1)
     if args.all_configs:
         rows = all_configs(ql, np, args.reps, tuple(g for g in args.only.split(",") if g))
-        print("| config | kernel | algorithmic bytes | us per launch | GB/s | % of 8 TB/s |")
-        print("|---|---|---|---|---|---|")
+        print("| config | kernel | algorithmic bytes | us per launch | GB/s | % of 8 TB/s | vs a copy of the same bytes |")
+        print("|---|---|---|---|---|---|---|")
         for r_ in rows:
             extra = (f" ({r_['tflops']:.0f} TFLOP/s, {100 * r_['frac_mfma_peak']:.1f}% of fp16 MFMA peak)"
                      if "tflops" in r_ else "")
             frac = "-" if r_["frac_peak"] is None else f"{100 * r_['frac_peak']:.1f}"
+            vs = f"{r_['vs_copy']:.3f} (copy {r_['copy_same_bytes_us']:.2f} us)" if "vs_copy" in r_ else "-"
             print(f"| {r_['config']} | {r_['kernel']}{extra} | {r_['bytes']:,} | {r_['us']:.2f} | "
-                  f"{r_['GBps']:.2f} | {frac} |", flush=True)
+                  f"{r_['GBps']:.2f} | {frac} | {vs} |", flush=True)
         print(json.dumps({"all_configs": rows}), flush=True)
         return
     chain = Chain(ql, np)
