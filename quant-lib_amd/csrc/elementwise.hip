@@ -47,11 +47,12 @@ struct AddOp {
 
 // out[i] = op(a[i], b[i]) over n elements; out may alias a (in-place add).
 // BS threads per workgroup, U vectors per thread, NT = nontemporal loads and
-// stores.  Measured on MI355X (C5 SwiGLU, 705 MB, buffers rotated past the
-// MALL): one 16-byte vector per thread with nontemporal access streams
-// fastest; unrolling further lowers occupancy without adding useful bytes in
-// flight, and 128-thread workgroups stream a 2-read/1-write mix ~3% faster
-// than 256-thread ones.
+// stores.  Measured on MI355X (buffers rotated past the MALL, clocks warm):
+// one 16-byte vector per thread with nontemporal access streams fastest
+// (unrolling further lowers occupancy without adding useful bytes in flight),
+// and one-wavefront workgroups beat 128- and 256-thread ones at every size
+// tried: C5 SwiGLU (705 MB) 0.6-3.7%, 8192 x 4096 fp16 3%, the 512 x 5632
+// configs 6-7%, the residual add 1-3%.
 template <typename D, int W, int U, bool NT, typename Op, int BS = kBlock>
 __global__ __launch_bounds__(BS) void binary_stream(const D* a, const D* b, D* out,
                                                     long long n) {
@@ -91,7 +92,7 @@ __global__ __launch_bounds__(BS) void binary_stream(const D* a, const D* b, D* o
 }
 
 constexpr int kStreamU = 1;
-constexpr int kStreamBlock = 128;
+constexpr int kStreamBlock = 64;
 
 template <typename D, typename Op>
 hipError_t launch_binary(const D* a, const D* b, D* out, long long n, hipStream_t stream) {
