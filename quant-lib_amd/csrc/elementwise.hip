@@ -147,24 +147,25 @@ __global__ __launch_bounds__(kBlock) void widen_stream(const _Float16* __restric
 // fp32 -> binary16 narrowing, RNE (src/quant_forward.cu:18-21).  W = 4: 16-byte
 // loads and 8-byte stores (a wavefront's load covers 1 KiB, its store 512 B);
 // measured 6.34 TB/s on MI355X (64 Mi elements) against 6.06 for two 16-byte
-// loads and one 16-byte store per lane.
-template <int W>
-__global__ __launch_bounds__(kBlock) void narrow_stream(const float* __restrict__ src,
+// loads and one 16-byte store per lane; one-wavefront workgroups (BS = 64)
+// a further 2.8%.
+template <int W, int BS = kBlock>
+__global__ __launch_bounds__(BS) void narrow_stream(const float* __restrict__ src,
                                                         _Float16* __restrict__ dst, long long n) {
     using VI = Vec<float, W>;
     using VO = Vec<_Float16, W>;
     const long long nvec = n / W;
-    const long long base = (long long)blockIdx.x * (kBlock * kUnroll) + threadIdx.x;
+    const long long base = (long long)blockIdx.x * (BS * kUnroll) + threadIdx.x;
     VI r[kUnroll];   // every thread loads, as binary_stream
     if (nvec > 0) {
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u)
-            r[u] = load<(W > 1)>(reinterpret_cast<const VI*>(src) + min(base + (long long)u * kBlock, nvec - 1));
+            r[u] = load<(W > 1)>(reinterpret_cast<const VI*>(src) + min(base + (long long)u * BS, nvec - 1));
         __builtin_amdgcn_sched_barrier(0);   // every load issued before any arithmetic
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-        const long long i = base + (long long)u * kBlock;
+        const long long i = base + (long long)u * BS;
         if (i < nvec) {
             VO y;
 #pragma unroll
@@ -173,16 +174,17 @@ __global__ __launch_bounds__(kBlock) void narrow_stream(const float* __restrict_
         }
     }
     if (W > 1 && blockIdx.x == 0)
-        for (long long i = nvec * W + threadIdx.x; i < n; i += kBlock)
+        for (long long i = nvec * W + threadIdx.x; i < n; i += BS)
             dst[i] = from_f32<_Float16>(src[i]);
 }
 
 // Two independent copies in one launch (blockIdx.y selects the pair): the K
 // and V halves of a contiguous KV append.  16-byte units with nontemporal
-// access (one unit per thread measured fastest for a pure copy) when all four
+// access (one unit per thread measured fastest for a pure copy; one-wavefront
+// workgroups 8% faster than 256-thread ones at C5, 2 x 16 MiB) when all four
 // pointers and the byte count allow it, else element-sized units.
-template <int UNIT, int U, bool NT>
-__global__ __launch_bounds__(kBlock) void copy_pair(char* __restrict__ d0,
+template <int UNIT, int U, bool NT, int BS = kBlock>
+__global__ __launch_bounds__(BS) void copy_pair(char* __restrict__ d0,
                                                     const char* __restrict__ s0,
                                                     char* __restrict__ d1,
                                                     const char* __restrict__ s1,
@@ -191,16 +193,16 @@ __global__ __launch_bounds__(kBlock) void copy_pair(char* __restrict__ d0,
     char* dst = blockIdx.y == 0 ? d0 : d1;
     const char* src = blockIdx.y == 0 ? s0 : s1;
     const long long nvec = nbytes / UNIT;
-    const long long base = (long long)blockIdx.x * (kBlock * U) + threadIdx.x;
+    const long long base = (long long)blockIdx.x * (BS * U) + threadIdx.x;
     V r[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const long long i = base + (long long)u * kBlock;
+        const long long i = base + (long long)u * BS;
         if (i < nvec) r[u] = load<NT>(reinterpret_cast<const V*>(src) + i);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const long long i = base + (long long)u * kBlock;
+        const long long i = base + (long long)u * BS;
         if (i < nvec) store<NT>(reinterpret_cast<V*>(dst) + i, r[u]);
     }
 }
@@ -224,8 +226,8 @@ hipError_t kv_append_dispatch(D* kc, D* vc, const D* kn, const D* vn, int layer,
     const bool vec_ok = qlh::aligned16(d0) && qlh::aligned16(d1) && qlh::aligned16(s0) &&
                         qlh::aligned16(s1) && nbytes % 16 == 0;
     if (vec_ok) {
-        hipLaunchKernelGGL((copy_pair<16, 1, true>), dim3(qlh::blocks_for(nbytes / 16, kBlock), 2),
-                           dim3(kBlock), 0, stream, d0, s0, d1, s1, nbytes);
+        hipLaunchKernelGGL((copy_pair<16, 1, true, kWave>), dim3(qlh::blocks_for(nbytes / 16, kWave), 2),
+                           dim3(kWave), 0, stream, d0, s0, d1, s1, nbytes);
     } else {
         constexpr int U = (int)sizeof(D);
         hipLaunchKernelGGL((copy_pair<U, kUnroll, false>),
@@ -299,8 +301,8 @@ extern "C" hipError_t ql_f32_to_f16(const float* src, uint16_t* dst, int64_t n,
     _Float16* d = reinterpret_cast<_Float16*>(dst);
     if (qlh::aligned16(src) && ((uintptr_t)dst & 7u) == 0) {
         const long long nvec = n / 4;
-        const unsigned grid = nvec > 0 ? qlh::blocks_for(nvec, (long long)kBlock * kUnroll) : 1;
-        hipLaunchKernelGGL((narrow_stream<4>), dim3(grid), dim3(kBlock), 0, stream, src, d,
+        const unsigned grid = nvec > 0 ? qlh::blocks_for(nvec, (long long)kWave * kUnroll) : 1;
+        hipLaunchKernelGGL((narrow_stream<4, kWave>), dim3(grid), dim3(kWave), 0, stream, src, d,
                            (long long)n);
     } else {
         hipLaunchKernelGGL((narrow_stream<1>), dim3(qlh::blocks_for(n, (long long)kBlock * kUnroll)),
