@@ -1120,14 +1120,20 @@ hipError_t launch_decode(const AttnArgs& a, int head_dim, int n_seqs, hipStream_
     QL_CHECK_ARG((long long)a.n_split * n_cg <= INT32_MAX);
     const dim3 grid((unsigned)(a.n_split * n_cg), (unsigned)a.n_kv_heads, (unsigned)n_seqs);
     const dim3 cgrid((unsigned)a.n_heads, (unsigned)n_seqs);
+    // the contiguous-cache decode (one sequence) always runs unsplit
+    if (!PAGED && a.n_split != 1) return hipErrorInvalidValue;
     if (head_dim == 128) {
         hipLaunchKernelGGL((attn_decode<128, PAGED>), grid, dim3(kAttnThreads), 0, stream, a);
-        if (a.n_split > 1)
-            hipLaunchKernelGGL((attn_decode_combine<128, PAGED>), cgrid, dim3(kMaxSplits), 0, stream, a);
+        if constexpr (PAGED) {
+            if (a.n_split > 1)
+                hipLaunchKernelGGL((attn_decode_combine<128, PAGED>), cgrid, dim3(kMaxSplits), 0, stream, a);
+        }
     } else {
         hipLaunchKernelGGL((attn_decode<64, PAGED>), grid, dim3(kAttnThreads), 0, stream, a);
-        if (a.n_split > 1)
-            hipLaunchKernelGGL((attn_decode_combine<64, PAGED>), cgrid, dim3(kMaxSplits), 0, stream, a);
+        if constexpr (PAGED) {
+            if (a.n_split > 1)
+                hipLaunchKernelGGL((attn_decode_combine<64, PAGED>), cgrid, dim3(kMaxSplits), 0, stream, a);
+        }
     }
     return hipGetLastError();
 }

@@ -897,7 +897,14 @@ void launch_skinny_rs(const SkinnyArgs& a, int kind, dim3 grid, hipStream_t st) 
     switch (kind) {
     case kScaleTensor: hipLaunchKernelGGL((fp8_gemm_skinny<FMT, MODE, MT, R, kScaleTensor>), grid, block, 0, st, a); break;
     case kScaleRow: hipLaunchKernelGGL((fp8_gemm_skinny<FMT, MODE, MT, R, kScaleRow>), grid, block, 0, st, a); break;
-    case kScaleGroupFold: hipLaunchKernelGGL((fp8_gemm_skinny<FMT, MODE, MT, R, kScaleGroupFold>), grid, block, 0, st, a); break;
+    case kScaleGroupFold:
+        // scale_kind() folds only for up to 2 token tiles and not for reference-mode
+        // E5M2; elsewhere the LDS-table kernel, which covers every folded case, runs
+        if constexpr (MT <= 2 && !(FMT == QL_FP8_E5M2 && MODE == QL_FP8_MODE_REFERENCE))
+            hipLaunchKernelGGL((fp8_gemm_skinny<FMT, MODE, MT, R, kScaleGroupFold>), grid, block, 0, st, a);
+        else
+            hipLaunchKernelGGL((fp8_gemm_skinny<FMT, MODE, MT, R, kScaleGroupLds>), grid, block, 0, st, a);
+        break;
     case kScaleGroupLds: hipLaunchKernelGGL((fp8_gemm_skinny<FMT, MODE, MT, R, kScaleGroupLds>), grid, block, 0, st, a); break;
     case kScaleGroup: hipLaunchKernelGGL((fp8_gemm_skinny<FMT, MODE, MT, R, kScaleGroup>), grid, block, 0, st, a); break;
     default: hipLaunchKernelGGL((fp8_gemm_skinny<FMT, MODE, MT, R, kScaleAny>), grid, block, 0, st, a); break;
@@ -1176,9 +1183,17 @@ extern "C" hipError_t ql_fp8_gemm_f16(const uint16_t* A, const uint8_t* W, const
         a.groups_per_row = K % g.gs == 0 ? (int)(K / g.gs) : 0;
         a.g_step = (int)(256 / g.gs);
         a.r_step = (int)(256 % g.gs);
-        if (rkind >= 0)
-            QL_FP8_DISPATCH(format, mode, launch_rows, a, pl, rkind, stream);
-        else
+        if (rkind >= 0) {
+            // rows_kind() keeps reference-mode E5M2 on the register path
+            if (format == QL_FP8_E4M3 && mode == QL_FP8_MODE_REFERENCE)
+                launch_rows<QL_FP8_E4M3, QL_FP8_MODE_REFERENCE>(a, pl, rkind, stream);
+            else if (format == QL_FP8_E4M3)
+                launch_rows<QL_FP8_E4M3, QL_FP8_MODE_OCP>(a, pl, rkind, stream);
+            else if (mode == QL_FP8_MODE_OCP)
+                launch_rows<QL_FP8_E5M2, QL_FP8_MODE_OCP>(a, pl, rkind, stream);
+            else
+                return hipErrorInvalidValue;
+        } else
             QL_FP8_DISPATCH(format, mode, launch_skinny, a, pl, scale_kind(g, K, pl, format, mode), stream);
         if (pl.splits > 1) {
             const long long mn = (long long)M * N;

@@ -273,27 +273,30 @@ hipError_t rmsnorm_dispatch(D* x, const D* d, const D* w, D* out, int rows, int 
                                d, w, out, dim, eps);
         return hipGetLastError();
     }
-    if (vec_ok && !ADD && nvec > 64 && nvec <= 1024) {
-        // Plain RMSNorm reads one row, not two: two 16-byte vectors per lane
-        // over half the wavefronts keep as many bytes in flight per lane as the
-        // fused kernel's x and d.  Measured on MI355X (8192 rows, rotating
-        // buffers): binary16 4096 wide 24.3 -> 23.1 us, 8192 wide 52.2 -> 44.6,
-        // 1024 wide 7.8 -> 6.8; fp32 4096 wide 51.6 -> 44.4; 2048 wide equal.
-        if (nvec <= 128) return launch_fast<D, 2, 1, ADD>(x, d, w, out, rows, dim, eps, stream);
-        if (nvec <= 256) return launch_fast<D, 2, 2, ADD>(x, d, w, out, rows, dim, eps, stream);
-        if (nvec <= 512) return launch_fast<D, 2, 4, ADD>(x, d, w, out, rows, dim, eps, stream);
-        return launch_fast<D, 2, 8, ADD>(x, d, w, out, rows, dim, eps, stream);
-    }
     if (vec_ok) {
-        // Spread a row over as many wavefronts as it has 64-vector chunks (up
-        // to 16): one 16-byte vector per lane measured fastest for the fused
-        // add (more waves in flight, shorter reduction tails; two vectors per
-        // lane 0.1-1.9% slower at 1024-8192 wide).
         if (nvec <= 64) return launch_fast<D, 1, 1, ADD>(x, d, w, out, rows, dim, eps, stream);
-        if (nvec <= 128) return launch_fast<D, 1, 2, ADD>(x, d, w, out, rows, dim, eps, stream);
-        if (nvec <= 256) return launch_fast<D, 1, 4, ADD>(x, d, w, out, rows, dim, eps, stream);
-        if (nvec <= 512) return launch_fast<D, 1, 8, ADD>(x, d, w, out, rows, dim, eps, stream);
-        if (nvec <= 1024) return launch_fast<D, 1, 16, ADD>(x, d, w, out, rows, dim, eps, stream);
+        if constexpr (!ADD) {
+            // Plain RMSNorm reads one row, not two: two 16-byte vectors per
+            // lane over half the wavefronts keep as many bytes in flight per
+            // lane as the fused kernel's x and d.  Measured on MI355X (8192
+            // rows, rotating buffers): binary16 4096 wide 24.3 -> 23.1 us, 8192
+            // wide 52.2 -> 44.6, 1024 wide 7.8 -> 6.8; fp32 4096 wide 51.6 ->
+            // 44.4; 2048 wide equal.
+            if (nvec <= 128) return launch_fast<D, 2, 1, ADD>(x, d, w, out, rows, dim, eps, stream);
+            if (nvec <= 256) return launch_fast<D, 2, 2, ADD>(x, d, w, out, rows, dim, eps, stream);
+            if (nvec <= 512) return launch_fast<D, 2, 4, ADD>(x, d, w, out, rows, dim, eps, stream);
+            if (nvec <= 1024) return launch_fast<D, 2, 8, ADD>(x, d, w, out, rows, dim, eps, stream);
+        } else {
+            // The fused add: a row over as many wavefronts as it has 64-vector
+            // chunks (up to 16), one 16-byte vector per lane (more waves in
+            // flight, shorter reduction tails; two vectors per lane measured
+            // 0.1-1.9% slower at 1024-8192 wide).
+            if (nvec <= 128) return launch_fast<D, 1, 2, ADD>(x, d, w, out, rows, dim, eps, stream);
+            if (nvec <= 256) return launch_fast<D, 1, 4, ADD>(x, d, w, out, rows, dim, eps, stream);
+            if (nvec <= 512) return launch_fast<D, 1, 8, ADD>(x, d, w, out, rows, dim, eps, stream);
+            if (nvec <= 1024) return launch_fast<D, 1, 16, ADD>(x, d, w, out, rows, dim, eps, stream);
+        }
+        // wider rows, both: 16 wavefronts, 2-8 vectors per lane
         if (nvec <= 2048) return launch_fast<D, 2, 16, ADD>(x, d, w, out, rows, dim, eps, stream);
         if (nvec <= 4096) return launch_fast<D, 4, 16, ADD>(x, d, w, out, rows, dim, eps, stream);
         if (nvec <= 8192) return launch_fast<D, 8, 16, ADD>(x, d, w, out, rows, dim, eps, stream);

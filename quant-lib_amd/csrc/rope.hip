@@ -584,12 +584,17 @@ hipError_t launch_planes_hd(int d, int pairing, D* q, D* k, int n_tokens, int hq
                             long long qs, long long ks, const int32_t* positions, int pos_offset,
                             const InvFreq& inv, const KvDst<D>& kv, hipStream_t stream) {
     if (d == 128) {
-        if (pairing == QL_ROPE_HALF)
-            return launch_planes<D, QL_ROPE_HALF, 128, CACHE>(q, k, n_tokens, hq, hk, qs, ks,
-                                                              positions, pos_offset, inv, kv, stream);
-        return launch_planes<D, QL_ROPE_INTERLEAVED, 128, CACHE>(q, k, n_tokens, hq, hk, qs, ks,
-                                                                 positions, pos_offset, inv, kv,
-                                                                 stream);
+        if constexpr (CACHE == kNoCache && sizeof(D) == 2) {
+            return hipErrorInvalidValue;   // binary16 head_dim 128 without a cache runs rope_units
+        } else {
+            if (pairing == QL_ROPE_HALF)
+                return launch_planes<D, QL_ROPE_HALF, 128, CACHE>(q, k, n_tokens, hq, hk, qs, ks,
+                                                                  positions, pos_offset, inv, kv,
+                                                                  stream);
+            return launch_planes<D, QL_ROPE_INTERLEAVED, 128, CACHE>(q, k, n_tokens, hq, hk, qs,
+                                                                     ks, positions, pos_offset,
+                                                                     inv, kv, stream);
+        }
     }
     if (pairing == QL_ROPE_HALF)
         return launch_planes<D, QL_ROPE_HALF, 64, CACHE>(q, k, n_tokens, hq, hk, qs, ks, positions,

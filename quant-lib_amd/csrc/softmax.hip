@@ -172,22 +172,22 @@ hipError_t softmax_dispatch(const D* in, D* out, int rows, int cols, hipStream_t
     constexpr int W = vec16<D>();
     const bool vec_ok = cols % W == 0 && qlh::aligned16(in) && qlh::aligned16(out);
     const int nvec = cols / W;
-    if (vec_ok && sizeof(D) == 2 && nvec <= 512) {
-        // binary16 rows up to 4096 wide: one wavefront per row, up to eight
-        // 16-byte vectors per lane, four rows per workgroup (C4 fp16: 11.6 us
-        // against 14.2 us for four wavefronts of two vectors per row).
-        if (nvec <= 64) return launch_fast<D, 1, 1>(in, out, rows, cols, stream);
-        if (nvec <= 128) return launch_fast<D, 2, 1>(in, out, rows, cols, stream);
-        if (nvec <= 256) return launch_fast<D, 4, 1>(in, out, rows, cols, stream);
-        return launch_fast<D, 8, 1>(in, out, rows, cols, stream);
-    }
     if (vec_ok) {
-        // Two 16-byte vectors per lane, as many wavefronts per row as that
-        // needs (up to 16): measured fastest at C4 fp32.
         if (nvec <= 64) return launch_fast<D, 1, 1>(in, out, rows, cols, stream);
         if (nvec <= 128) return launch_fast<D, 2, 1>(in, out, rows, cols, stream);
-        if (nvec <= 256) return launch_fast<D, 2, 2>(in, out, rows, cols, stream);
-        if (nvec <= 512) return launch_fast<D, 2, 4>(in, out, rows, cols, stream);
+        if constexpr (sizeof(D) == 2) {
+            // binary16 rows up to 4096 wide: one wavefront per row, up to eight
+            // 16-byte vectors per lane, four rows per workgroup (C4 fp16: 11.6
+            // us against 14.2 us for four wavefronts of two vectors per row).
+            if (nvec <= 256) return launch_fast<D, 4, 1>(in, out, rows, cols, stream);
+            if (nvec <= 512) return launch_fast<D, 8, 1>(in, out, rows, cols, stream);
+        } else {
+            // Two 16-byte vectors per lane, as many wavefronts per row as that
+            // needs: measured fastest at C4 fp32.
+            if (nvec <= 256) return launch_fast<D, 2, 2>(in, out, rows, cols, stream);
+            if (nvec <= 512) return launch_fast<D, 2, 4>(in, out, rows, cols, stream);
+        }
+        // wider rows, both: 8-16 wavefronts per row, 2-16 vectors per lane
         if (nvec <= 1024) return launch_fast<D, 2, 8>(in, out, rows, cols, stream);
         if (nvec <= 2048) return launch_fast<D, 2, 16>(in, out, rows, cols, stream);
         if (nvec <= 4096) return launch_fast<D, 4, 16>(in, out, rows, cols, stream);

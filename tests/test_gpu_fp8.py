@@ -196,6 +196,50 @@ def test_fp8_gemm_matches_oracle(mode, fmt, M, N, K, gran, gs):
         check_gemm(got, exact, f"fp8 gemm {M}x{N}x{K} workspace {workspace}")
 
 
+# Shapes that select every launch variant of the FP8-weight GEMM's two register
+# paths, run in all four format/mode pairs by the test below (ids name them):
+# - register path, more than 8 tokens (or reference-mode E5M2): token tiles
+#   MT = 1, 2, 4 (12, 24, 48 tokens) x row tiles per workgroup R = 4, 2, 1
+#   (N = 128, 96, 80: 8, 6, 5 row tiles) x scale handling: per tensor, per row,
+#   folded groups of 64 (MT <= 2; four token tiles take the LDS table), an LDS
+#   table of groups of 32, groups of 48 that do not divide K (general index),
+#   and groups of 16 over K = 8192, whose table only fits LDS once K is split
+#   (the "none" workspace run keeps it whole);
+# - whole-row path (at most 8 tokens, K a multiple of 256): row tiles x
+#   wavefronts per tile (4,1) (2,1) (1,1) at K = 256, (2,2) (1,2) at K = 1024,
+#   (1,4) at 2048 and (1,8) at 4096, each per tensor, per row and with folded
+#   groups.
+def _plan_cases():
+    cases = []
+    scales = [("tensor", ql.QUANT_PER_TENSOR, 0, 256), ("row", ql.QUANT_PER_CHANNEL, 0, 256),
+              ("fold64", ql.QUANT_PER_GROUP, 64, 256), ("lds32", ql.QUANT_PER_GROUP, 32, 256),
+              ("any48", ql.QUANT_PER_GROUP, 48, 256), ("table16", ql.QUANT_PER_GROUP, 16, 8192)]
+    for mt, M in ((1, 12), (2, 24), (4, 48)):
+        for r, N in ((4, 128), (2, 96), (1, 80)):
+            for tag, gran, gs, K in scales:
+                cases.append(pytest.param(M, N, K, gran, gs, id=f"regs-mt{mt}-r{r}-{tag}"))
+    for (rw, kw), N, K in (((4, 1), 128, 256), ((2, 1), 96, 256), ((1, 1), 80, 256),
+                           ((2, 2), 96, 1024), ((1, 2), 80, 1024), ((1, 4), 80, 2048),
+                           ((1, 8), 80, 4096)):
+        for tag, gran, gs in (("tensor", ql.QUANT_PER_TENSOR, 0), ("row", ql.QUANT_PER_CHANNEL, 0),
+                              ("fold64", ql.QUANT_PER_GROUP, 64)):
+            cases.append(pytest.param(3, N, K, gran, gs, id=f"rows-rw{rw}-kw{kw}-{tag}"))
+    return cases
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("M,N,K,gran,gs", _plan_cases())
+def test_fp8_gemm_launch_variants(mode, fmt, M, N, K, gran, gs):
+    a = to_f16_bits(normal(3 * M + N + K, (M, K)))
+    w = to_f16_bits(normal(5 * N + K + gs, (N, K), K ** -0.5))
+    q, sc = orc.fp8_quantize(w, fmt, gran, gs, mode)
+    exact = gemm_exact(a, orc.fp8_dequantize(q, sc, fmt, gran, gs, mode))
+    for workspace in ("query", "none"):
+        got = gpu_fp8_gemm(a, q, sc, M, N, K, fmt, gran, gs, mode, workspace)
+        check_gemm(got, exact, f"fp8 gemm {M}x{N}x{K} gran {gran} gs {gs} workspace {workspace}")
+
+
 @pytest.mark.parametrize("a_scale", [1.0, 2.0 ** -12])
 @pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize("fmt", FMTS)

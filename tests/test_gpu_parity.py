@@ -99,6 +99,43 @@ def test_rmsnorm_f32_many_rows(rows, dim, add):
                 f"{'add_' if add else ''}rmsnorm f32 {rows}x{dim}")
 
 
+# Widths that select the remaining vector-path variants (fewer than 4096 rows):
+# one-wavefront rows of 4 vectors per lane (binary16 1032-2048 wide, fp32
+# fused 516-1024) and 2 (fp32 fused 260-512); 16-wavefront rows of 2, 4 or 8
+# vectors per lane for the fused add (binary16 8200-16384 and 32776-65536 wide,
+# fp32 4100-8192, 8196-16384 and 16388-32768).
+VARIANT_WIDTHS = [(True, False, 50, 2048), (True, True, 50, 2048), (True, True, 9, 1536),
+                  (True, True, 3, 12288), (True, True, 2, 65536), (False, True, 7, 512),
+                  (False, True, 5, 1000), (False, True, 3, 8192), (False, True, 2, 16384),
+                  (False, True, 2, 32768)]
+
+
+@pytest.mark.parametrize("f16,add,rows,dim", VARIANT_WIDTHS)
+def test_rmsnorm_variant_widths(f16, add, rows, dim):
+    x = normal(0x51A10081 + dim, (rows, dim))
+    d = normal(0x51A10082 + dim, (rows, dim))
+    w = uniform(0x51A10083 + dim, dim, 0.5, 1.5)
+    if f16:
+        x, d, w = _f16(x), _f16(d), _f16(w)
+    dt = np.uint16 if f16 else np.float32
+    out = Out(rows * dim, dt)
+    dx, dd, dw = dev(x), dev(d), dev(w)
+    sfx = "f16" if f16 else "f32"
+    if add:
+        ql.call(f"ql_add_rmsnorm_{sfx}", ptr(dx), ptr(dd), ptr(dw), out.ptr, rows, dim, 1e-5,
+                stream())
+        want_x, want = orc.add_rmsnorm(x, d, w, 1e-5, f16=f16)
+        assert np.array_equal(host(dx, shape=(rows, dim)), want_x)
+    else:
+        ql.call(f"ql_rmsnorm_{sfx}", ptr(dx), ptr(dw), out.ptr, rows, dim, 1e-5, stream())
+        want = orc.rmsnorm(x, w, 1e-5, f16=f16)
+    tag = f"{'add_' if add else ''}rmsnorm {sfx} {rows}x{dim}"
+    if f16:
+        check_f16(out.get((rows, dim)), want, tag)
+    else:
+        check_close(out.get((rows, dim)), want, RTOL_F32, ATOL_F32, tag)
+
+
 @pytest.mark.parametrize("f16", [False, True])
 def test_rmsnorm_unaligned_pointers(f16):
     rows, dim = 9, 2048
@@ -145,12 +182,14 @@ def test_add_rmsnorm_f32(rows, dim):
     check_close(out.get((rows, dim)), want, RTOL_F32, ATOL_F32, f"add_rmsnorm f32 {rows}x{dim}")
 
 
-@pytest.mark.parametrize("f16,n", [(False, 1 << 20), (True, 1 << 20), (False, 1001), (True, 1003)])
-def test_residual_add(f16, n):
+# offset 1: x and d not 16-byte aligned, the element-wise kernel
+@pytest.mark.parametrize("f16,n,offset", [(False, 1 << 20, 0), (True, 1 << 20, 0), (False, 1001, 0),
+                                          (True, 1003, 0), (False, 4099, 1), (True, 4101, 1)])
+def test_residual_add(f16, n, offset):
     x, d = normal(44, n), normal(45, n)
     if f16:
         x, d = _f16(x), _f16(d)
-    dx, dd = dev(x), dev(d)
+    dx, dd = dev(x, offset), dev(d, offset)
     ql.call("ql_add_f16" if f16 else "ql_add_f32", ptr(dx), ptr(dd), n, stream())
     assert np.array_equal(host(dx), orc.add(x, d, f16=f16))
 
@@ -333,8 +372,16 @@ def test_softmax_reference_test_thresholds():
 
 
 @pytest.mark.parametrize("f16", [False, True])
+# Besides ragged and generic widths, every vector-path variant, exactly filled
+# and with a partial last pass: binary16 512, 1024, 1536, 2048, 3000 (one
+# wavefront, 1-8 vectors per lane), 6000 (8 wavefronts), 12000, 16384, 32768,
+# 40000, 131072 (16 wavefronts, 2-16 vectors); fp32 512, 1024, 1500, 3000, 6000,
+# 12000, 16384, 32768, 40000 (1-16 wavefronts, 2-16 vectors).
 @pytest.mark.parametrize("rows,cols", [(5, 1), (7, 8), (9, 256), (6, 1000), (3, 8192), (3, 20000),
-                                       (2, 65536), (2, 70000), (4, 4097), (1, 3)])
+                                       (2, 65536), (2, 70000), (4, 4097), (1, 3), (5, 512),
+                                       (5, 1024), (5, 1500), (5, 1536), (5, 2048), (4, 3000),
+                                       (4, 6000), (3, 12000), (3, 16384), (2, 32768), (2, 40000),
+                                       (2, 131072)])
 def test_softmax_widths(f16, rows, cols):
     x = normal(500 + cols, (rows, cols), sigma=2.0)
     if cols > 3:
@@ -562,7 +609,8 @@ def _pool(nb, blk, misalign=0):
 @pytest.mark.parametrize("T,H,HK,d,misalign", [(8192, 32, 8, 128, 0), (37, 4, 2, 64, 0),
                                                (20, 3, 1, 96, 0), (45, 4, 2, 64, 1),
                                                (45, 5, 3, 128, 1), (19, 2, 1, 128, 0),
-                                               (33, 6, 2, 128, 0), (5, 120, 8, 128, 0)])
+                                               (33, 6, 2, 128, 0), (5, 120, 8, 128, 0),
+                                               (21, 4, 2, 32, 0), (21, 4, 2, 32, 1)])
 def test_rope_paged_kv_append_fused(pairing, T, H, HK, d, misalign):
     # One launch == ql_rope_f16 then ql_paged_kv_append_f16, bit for bit; and
     # both agree with the oracle (C5 shape: Q 32x128, K/V 8x128, theta 5e5).
@@ -637,7 +685,7 @@ def test_rope_q_paged_kv_append_leaves_k(pairing, T, H, HK, d, misalign):
 @pytest.mark.parametrize("f16", [True, False])
 @pytest.mark.parametrize("pairing", [ql.ROPE_HALF, ql.ROPE_INTERLEAVED])
 @pytest.mark.parametrize("T,H,HK,d", [(300, 8, 2, 128), (33, 4, 4, 64), (17, 2, 1, 6),
-                                      (29, 3, 3, 64), (31, 7, 1, 128)])
+                                      (29, 3, 3, 64), (31, 7, 1, 128), (23, 4, 2, 32)])
 def test_rope_kv_append_fused_contiguous_from_fused_qkv(f16, pairing, T, H, HK, d):
     # Q, K, V are views into one fused [T, (H + 2*HK)*d] QKV buffer (strided rows);
     # the cache is [L, S, HK, d], tokens written at positions pos..pos+T-1.
