@@ -161,6 +161,47 @@ def test_fp16_shims_match_oracle():
     assert np.array_equal(host(vc, shape=(L, S, H, d)), wv)
 
 
+class FP16KVCache(ctypes.Structure):  # src/fp16_forward.cu:115-120
+    _fields_ = [("k_cache", _p), ("v_cache", _p), ("n_layers", _i), ("max_seq", _i),
+                ("n_kv_heads", _i), ("head_dim", _i), ("current_len", _i)]
+
+
+def test_fp16_kvcache_create_append_free():
+    # the fp16 layer's cache lifecycle (src/fp16_forward.cu:122-145, appends as at
+    # :194-199): create, one launch_fp16_kvcache_append per layer per token at
+    # position current_len, read the written rows back, free
+    create = fn("fp16_kvcache_create", [_i, _i, _i, _i], ctypes.POINTER(FP16KVCache))
+    free = fn("fp16_kvcache_free", [ctypes.POINTER(FP16KVCache)])
+    append = fn("launch_fp16_kvcache_append", [_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p])
+    L, S, H, d, T = 3, 40, 8, 128, 5
+    assert not create(0, S, H, d) and not create(L, S, H, -1)
+    c = create(L, S, H, d)
+    assert c
+    try:
+        cc = c.contents
+        assert (cc.n_layers, cc.max_seq, cc.n_kv_heads, cc.head_dim, cc.current_len) == (L, S, H, d, 0)
+        kn = to_f16_bits(normal(30, (T, L, H, d)))
+        vn = to_f16_bits(normal(31, (T, L, H, d)))
+        for t in range(T):
+            for layer in range(L):
+                dk, dv = dev(kn[t, layer]), dev(vn[t, layer])
+                append(cc.k_cache, cc.v_cache, ptr(dk), ptr(dv), layer, cc.current_len, H, d, S, L,
+                       stream())
+                sync()
+            cc.current_len += 1
+        row = H * d * 2
+        for layer in range(L):
+            for t in range(T):
+                gk, gv = np.empty(H * d, np.uint16), np.empty(H * d, np.uint16)
+                off = ((layer * S) + t) * row
+                d2h(gk.ctypes.data, cc.k_cache + off, row)
+                d2h(gv.ctypes.data, cc.v_cache + off, row)
+                assert np.array_equal(gk, kn[t, layer].reshape(-1))
+                assert np.array_equal(gv, vn[t, layer].reshape(-1))
+    finally:
+        free(c)
+
+
 def test_fp32_shims_match_oracle():
     s = stream()
     rows, dim = 3, 2048
