@@ -269,6 +269,27 @@ def heat(ql, stream, ms=30.0):
     ql.synchronize()
 
 
+def warm_on(ql, stream, launch, ms=60.0):
+    """About `ms` of untimed launches of the workload itself before a timed pass
+    of a matrix-core-bound kernel.  Under sustained matrix-core load the clocks
+    go through a transient: a kernel trace of the C5 prefill attention shows
+    ~630 us for the first launches, ~800 us around the fifth (after 30 ms of
+    copies), then a slow settle to a steady 605-660 us (box to box) after
+    ~40 ms; timed inside that window it read 700 us.  The launch count is
+    sized from the second launch (the first one also loads the code object)."""
+    launch(0)
+    ql.synchronize()
+    a, b = ql.Event(), ql.Event()
+    a.record(stream)
+    launch(1)
+    b.record(stream)
+    ql.synchronize()
+    per_ms = max(a.elapsed_ms(b), 1e-3)
+    for i in range(2, int(ms / per_ms) + 2):
+        launch(i)
+    ql.synchronize()
+
+
 def percentiles(us):
     """Median, p10 and p90 of a list of durations (us)."""
     v = sorted(us)
@@ -720,7 +741,10 @@ def layer_rows(ql, np, chain, reps):
             def launch(i, fn=fn, lws=lws):
                 ql.call(fn, eng, ctypes.byref(lws[i % len(lws)]), i % L_POOL, x.ptr,
                         deltas[(i + 1) % 2].ptr if i else None, deltas[i % 2].ptr, ctypes.byref(sd), st)
-            heat(ql, st)
+            if q_len > 1:
+                warm_on(ql, st, launch)   # prefill layers are matrix-core bound
+            else:
+                heat(ql, st)
             for i in range(max(3, 2 * len(lws))):   # every weight set before timing
                 launch(i)
             ql.synchronize()
@@ -878,11 +902,14 @@ def attention_rows(ql, np, chain, reps):
     st = chain.stream
     rows = []
 
-    def timed(launch, n):
-        heat(ql, st)
-        for i in range(n):   # as many warm-up launches as timed ones: every rotated copy once
-            launch(i)
-        ql.synchronize()
+    def timed(launch, n, compute_bound=False):
+        if compute_bound:
+            warm_on(ql, st, launch)   # matrix-core bound: warm on the kernel itself
+        else:
+            heat(ql, st)
+            for i in range(n):   # as many warm-up launches as timed ones: every rotated copy once
+                launch(i)
+            ql.synchronize()
         a, b = ql.Event(), ql.Event()
         a.record(st)
         for i in range(n):
@@ -899,9 +926,10 @@ def attention_rows(ql, np, chain, reps):
     cu, ctx, table = up(np.array([0, T], np.int32)), up(np.array([T], np.int32)), \
         up(np.arange(chain.nb, dtype=np.int32))
     n_att = max(3, reps // 10)
+    n_pre = max(20, reps // 2)   # prefill: ~15 ms timed after the warm-up on the kernel
     us = timed(lambda i: ql.call("ql_flash_attention_f16", chain.sets[i % NSETS]["q"].ptr,
                                  chain.sets[i % NSETS]["k"].ptr, chain.sets[i % NSETS]["v"].ptr,
-                                 out[i % 2].ptr, T, HQ, HKV, HD, 1, st), n_att)
+                                 out[i % 2].ptr, T, HQ, HKV, HD, 1, st), n_pre, compute_bound=True)
     rows.append({"config": "C5 attention prefill T=8192 causal", "kernel": "flash_attention_f16",
                  "bytes": io, "us": round(us, 2), "GBps": round(io / (us * 1e-6) / 1e9, 1),
                  "frac_peak": round(io / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
@@ -910,7 +938,7 @@ def attention_rows(ql, np, chain, reps):
     us = timed(lambda i: ql.call("ql_paged_attention_f16", chain.sets[i % NSETS]["q"].ptr,
                                  out[i % 2].ptr, HQ * HD, HQ * HD, T, 1, cu.ptr, ctx.ptr, T, table.ptr,
                                  chain.nb, chain.kptrs.ptr, chain.vptrs.ptr, chain.nb, i % L_POOL,
-                                 L_POOL, HQ, HKV, HD, 1, st), n_att)
+                                 L_POOL, HQ, HKV, HD, 1, st), n_pre, compute_bound=True)
     rows.append({"config": "C5 attention prefill T=8192 causal", "kernel": "paged_attention_f16",
                  "bytes": io, "us": round(us, 2), "GBps": round(io / (us * 1e-6) / 1e9, 1),
                  "frac_peak": round(io / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),

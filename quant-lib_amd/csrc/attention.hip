@@ -65,6 +65,29 @@ constexpr int kAttnThreads = kAttnWaves * kWave;   // 256
 constexpr int kBQ = 32 * kAttnWaves;               // 128 queries per workgroup
 constexpr int kBK = 64;                            // keys per tile
 
+// Pair reductions across lanes l and l ^ 32 (l ^ 16) without an LDS round
+// trip: gfx950's v_permlane32_swap (v_permlane16_swap) applied to a value and
+// itself hands every lane both values of its pair, the lower half's first, so
+// both lanes of a pair compute the same bits (__shfl_xor compiled to
+// ds_bpermute plus a wait on every outstanding LDS read; measured 2-3% of the
+// prefill kernel, bit-identical).
+__device__ __forceinline__ float max_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float max_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 struct AttnArgs {
     const _Float16* q;
     _Float16* out;
@@ -387,7 +410,7 @@ __device__ __forceinline__ void softmax_pv(floatx16 (&s)[2], floatx16 (&o)[HD / 
         for (int i = 2; i < 8; ++i) mq[c] = fmaxf(mq[c], s[c >> 1][8 * (c & 1) + i]);
     }
     float mt = fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]));
-    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+    mt = max_xor32(mt);
     // Rescale only when some query's max grew by more than 2^8 in the
     // exponent: until then the stale offset keeps p <= 256 (exact
     // enough in binary16) and O/l is unchanged, since the offset cancels.
@@ -434,7 +457,7 @@ __device__ __forceinline__ void softmax_pv(floatx16 (&s)[2], floatx16 (&o)[HD / 
 // O = O^T / l for the lane's query (both 8-key halves of the sum combined).
 template <int HD>
 __device__ __forceinline__ void store_o(const floatx16 (&o)[HD / 32], float l_run, _Float16* orow, int hh) {
-    const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
+    const float l_tot = sum_xor32(l_run);
     const float inv_den = 1.0f / (l_tot + 1e-8f);
 #pragma unroll
     for (int db = 0; db < HD / 32; ++db) {
@@ -829,8 +852,7 @@ __device__ __forceinline__ void dec_step(const _Float16* sk, const half8* qf, fl
             }
             mt = fmaxf(mt, sc[kb][i]);
         }
-    mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
-    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+    mt = max_xor32(max_xor16(mt));
     const float m_cand = fmaxf(st.m_run, mt);
     if (__any((m_cand - st.m_run) * cl2 > 8.0f)) {
         const float alpha = __builtin_amdgcn_exp2f((st.m_run - m_cand) * cl2);
@@ -985,8 +1007,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_decode(AttnArgs a) {
         if (!run_step()) break;
 
     // merge the wavefronts: the 4 lanes of a column share m_run, so their sums add
-    float l_tot = st.l_run + __shfl_xor(st.l_run, 16, kWave);
-    l_tot += __shfl_xor(l_tot, 32, kWave);
+    const float l_tot = sum_xor32(sum_xor16(st.l_run));
     __syncthreads();   // every wavefront is done with its V^T staging
     float* part = reinterpret_cast<float*>(smem_raw);   // [wave][column][HD + 2]
     {
