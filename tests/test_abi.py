@@ -229,3 +229,19 @@ def test_paged_slot_mapping_host_helper():
     assert ql.raw("ql_paged_slot_mapping", ctypes.addressof(table), 3, 40, 10, ctypes.addressof(slots)) == INVALID
     bad = (ctypes.c_int32 * 2)(3, -1)
     assert ql.raw("ql_paged_slot_mapping", ctypes.addressof(bad), 2, 10, 10, ctypes.addressof(slots)) == INVALID
+
+
+def test_dropin_caller_builds_and_links():
+    """tests/dropin/caller.cpp calls the reference-named launchers, caches and
+    quantlib functions through quantlib_compat.h alone and links against the
+    built library: every name it uses resolves (the GPU run is in
+    tests/test_gpu_compat.py)."""
+    d = ROOT / "tests" / "dropin"
+    subprocess.run(["make", "-B", "-C", str(d)], check=True, capture_output=True, text=True)
+    undefined = subprocess.run(["nm", "-u", "-C", str(d / "caller")], check=True, capture_output=True,
+                               text=True).stdout
+    linked = subprocess.run(["nm", "-D", "--defined-only", "-C", str(ql.LIB_PATH)], check=True,
+                            capture_output=True, text=True).stdout
+    for name in ("launch_rmsnorm", "launch_rope", "launch_flash_attention", "kvcache_append",
+                 "paged_kv_create", "quantlib_fp8_to_fp16", "launch_fp16_kvcache_append"):
+        assert name in undefined and name in linked, name

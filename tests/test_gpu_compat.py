@@ -1,6 +1,7 @@
 """The reference's own tests, rerun against the drop-in shims that keep the
 reference's names and signatures (include/quantlib_compat.h), on the GPU."""
 import ctypes
+import pathlib
 
 import numpy as np
 import pytest
@@ -408,3 +409,14 @@ def test_fp32_quantized_gemm_bridge(M):
     assert np.all(np.abs(f16_bits_to_f32(c16) - f16_bits_to_f32(want)) <= bound)
     assert np.array_equal(host(c32, shape=(M, N)), f16_bits_to_f32(c16))
     qfree(ctypes.byref(qm))
+
+
+def test_dropin_caller_program_runs():
+    """The C++ caller of tests/dropin/caller.cpp (reference-style call sites,
+    linked against libquantlib_amd.so, built by build()) run as a child process:
+    every closed-form check it makes passes."""
+    import subprocess
+    exe = pathlib.Path(__file__).resolve().parent / "dropin" / "caller"
+    assert exe.exists(), f"{exe} is not built: run __graft_entry__.build() (make -C tests/dropin)"
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and "dropin caller: ok" in r.stdout, r.stdout + r.stderr
