@@ -115,7 +115,7 @@ def parse():
     ap.add_argument("--reps", type=int, default=50, help="launches per config in --all-configs")
     ap.add_argument("--only", default="",
                     help="--all-configs row groups to time, comma-separated: "
-                         "configs, kv, attention, layer, fp8 (default: all)")
+                         "configs, refbench, kv, attention, layer, fp8 (default: all)")
     return ap.parse_args()
 
 
@@ -455,6 +455,8 @@ def all_configs(ql, np, reps, only=()):
     st = ql.stream()
     rows = []
     want = lambda group: not only or group in only
+    if want("refbench"):
+        rows += refbench_rows(ql, np, st)
     if want("kv"):
         rows += kvcache_append_rows(ql, np, st)
     if not want("configs") and not want("attention") and not want("layer"):
@@ -598,6 +600,76 @@ def cpu_softmax_row(np, x):
             "GBps": round(nb / (us * 1e-6) / 1e9, 2), "frac_peak": None,
             "kernel": f"CPU baseline: cpu_softmax (tests/test_softmax.cu:19-30) restated in "
                       f"oracle/oracle.c, gcc -O2, 1 thread of {info['nproc']} ({info['cpu_model']})"}
+
+
+def refbench_rows(ql, np, st):
+    """The reference's own kernel benchmark (tests/benchmark_all.cu:89-262) on
+    this build, the reference's way: the drop-in shims of include/quantlib_compat.h
+    (launch_softmax, launch_rmsnorm, launch_rope, launch_swiglu), one untimed
+    launch, then `reps` back-to-back launches on the same buffers between one
+    event pair (500 / 1000 / 1000 / 5000, as there).  Inputs are seeded N(0,1)
+    (the reference times uninitialised buffers); ~30 ms of copies warm the clocks
+    before each shape.  Published times: RTX 2060 Max-Q, README.md:25-64.
+    Bytes: this repo's algorithmic model (each input read once, each output
+    written once); the reference's own GB/s counts RMSNorm's x twice."""
+    from quantlib_amd import lib as _lib
+    p_, i_, f_ = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+    L = _lib()
+    softmax = L._Z14launch_softmaxPKfPfiiP12ihipStream_t
+    softmax.argtypes, softmax.restype = [p_, p_, i_, i_, p_], None
+    rmsnorm = L._Z14launch_rmsnormPKfS0_PfiifP12ihipStream_t
+    rmsnorm.argtypes, rmsnorm.restype = [p_, p_, p_, i_, i_, f_, p_], None
+    rope = L._Z11launch_ropePfiiifP12ihipStream_t
+    rope.argtypes, rope.restype = [p_, i_, i_, i_, f_, p_], None
+    swiglu = L._Z13launch_swigluPKfS0_PfiiP12ihipStream_t
+    swiglu.argtypes, swiglu.restype = [p_, p_, p_, i_, i_, p_], None
+    r = np.random.default_rng(17)
+    up = lambda *shape: ql.DeviceArray.from_numpy(r.standard_normal(shape, dtype=np.float32))
+    out = []
+
+    def timed(launch, reps):
+        heat(ql, st)
+        launch()
+        ql.synchronize()
+        a, b = ql.Event(), ql.Event()
+        a.record(st)
+        for _ in range(reps):
+            launch()
+        b.record(st)
+        ql.synchronize()
+        return a.elapsed_ms(b) * 1e3 / reps
+
+    def row(what, shape, nbytes, us, ref_ms, where):
+        out.append({"config": f"reference benchmark ({where}) {shape}",
+                    "kernel": f"{what} (reference RTX 2060: {ref_ms * 1e3:.1f} us; {ref_ms * 1e3 / us:.1f}x faster)",
+                    "bytes": nbytes, "us": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                    "frac_peak": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+                    "reference_us": round(ref_ms * 1e3, 1), "speedup_vs_reference": round(ref_ms * 1e3 / us, 1)})
+
+    for n, ref_ms in ((512, 0.0136), (1024, 0.0377), (2048, 0.1430), (4096, 0.6598)):
+        x, y = up(n, n), ql.DeviceArray((n, n), np.float32)
+        us = timed(lambda: softmax(x.ptr, y.ptr, n, n, st), 500)
+        row("launch_softmax", f"{n}x{n}", 2 * n * n * 4, us, ref_ms, "tests/benchmark_all.cu:89-118")
+        del x, y
+    for dim, ref_ms in ((512, 0.0390), (1024, 0.0755), (2048, 0.1494), (4096, 0.3757)):
+        x, w, y = up(2048, dim), up(dim), ql.DeviceArray((2048, dim), np.float32)
+        us = timed(lambda: rmsnorm(x.ptr, w.ptr, y.ptr, 2048, dim, 1e-5, st), 1000)
+        row("launch_rmsnorm", f"2048x{dim}", 2 * 2048 * dim * 4 + dim * 4, us, ref_ms,
+            "tests/benchmark_all.cu:121-153")
+        del x, w, y
+    for seq, ref_ms in ((128, 0.0113), (512, 0.0729), (1024, 0.1429), (2048, 0.2842)):
+        x = up(seq, 32 * 128)
+        us = timed(lambda: rope(x.ptr, seq, 32, 128, 1e4, st), 1000)
+        row("launch_rope (32 heads x 128, in place)", f"seq {seq}", 2 * seq * 32 * 128 * 4, us, ref_ms,
+            "tests/benchmark_all.cu:190-222")
+        del x
+    for rows_, ref_ms in ((1, 0.0339), (32, 0.0110), (128, 0.0377), (512, 0.1434)):
+        g, u, o = up(rows_, 5632), up(rows_, 5632), ql.DeviceArray((rows_, 5632), np.float32)
+        us = timed(lambda: swiglu(g.ptr, u.ptr, o.ptr, rows_, 5632, st), 5000)
+        row("launch_swiglu", f"{rows_}x5632", 3 * rows_ * 5632 * 4, us, ref_ms,
+            "tests/benchmark_all.cu:225-262")
+        del g, u, o
+    return out
 
 
 def kvcache_append_rows(ql, np, st):
