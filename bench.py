@@ -1046,6 +1046,30 @@ def attention_rows(ql, np, chain, reps):
                      "us": round(us, 2), "GBps": round(gbs, 1), "frac_peak": round(gbs / PEAK_HBM_GBS, 4),
                      "splits_workspace_bytes": size.value})
         del kpool, vpool, ws
+    # decode over the contiguous cache of the reference's fp16 layer (one sequence,
+    # src/fp16_forward.cu:202-209): the single pass of ql_attention_f16 against the
+    # key split of ql_decode_attention_f16; K/V rows [8192, 8 x 128], 4 rotating copies
+    C = 8192
+    kvs = [(up(r.standard_normal((C, HKV * HD), dtype=np.float32).astype(np.float16).view(np.uint16)),
+            up(r.standard_normal((C, HKV * HD), dtype=np.float32).astype(np.float16).view(np.uint16)))
+           for _ in range(4)]
+    q = up(r.standard_normal((1, HQ * HD), dtype=np.float32).astype(np.float16).view(np.uint16))
+    o = ql.DeviceArray((1, HQ * HD), np.uint16)
+    size = ctypes.c_size_t()
+    ql.call("ql_decode_attention_workspace_size", HQ, HKV, HD, C, ctypes.addressof(size))
+    ws = ql.DeviceArray((max(size.value, 16),), np.uint8)
+    nbytes = C * HKV * HD * 2 * 2 + 2 * HQ * HD * 2
+    for label, fn in (("attention_f16 (q_len 1, one pass)",
+                       lambda i: ql.call("ql_attention_f16", q.ptr, kvs[i % 4][0].ptr, kvs[i % 4][1].ptr, o.ptr,
+                                         1, C, HQ, HKV, HD, HQ * HD, HKV * HD, HQ * HD, 1, st)),
+                      ("decode_attention_f16 (key split + combine)",
+                       lambda i: ql.call("ql_decode_attention_f16", q.ptr, kvs[i % 4][0].ptr, kvs[i % 4][1].ptr,
+                                         o.ptr, C, HQ, HKV, HD, HKV * HD, ws.ptr, size.value, st))):
+        us = timed(fn, max(3, reps // 5))
+        gbs = nbytes / (us * 1e-6) / 1e9
+        rows.append({"config": f"decode 1 seq x {C} ctx (contiguous cache)", "kernel": label, "bytes": nbytes,
+                     "us": round(us, 2), "GBps": round(gbs, 1), "frac_peak": round(gbs / PEAK_HBM_GBS, 4)})
+    del kvs, ws
     return rows
 
 

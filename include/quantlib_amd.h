@@ -254,6 +254,24 @@ hipError_t ql_attention_f16(const uint16_t* q, const uint16_t* k, const uint16_t
                             int head_dim, int64_t q_row_stride, int64_t kv_row_stride,
                             int64_t out_row_stride, int causal, hipStream_t stream);
 
+/* Decode against the contiguous cache with the keys split over workgroups: the one
+ * query row q / out ([n_heads, head_dim]) of the token at position kv_len - 1
+ * against K/V rows 0 .. kv_len-1 (row stride kv_row_stride elements) -- the
+ * decode call of src/fp16_forward.cu:202-209 (launch_flash_attention over the
+ * layer's K_full/V_full with ctx_len keys) with its query count stated.  Same
+ * kernel as ql_attention_f16 with q_len = 1; with the
+ * ql_decode_attention_workspace_size() bytes the keys are split over more
+ * workgroups (fp32 partials in the workspace, then a combine kernel), a smaller
+ * or NULL workspace uses fewer splits (down to ql_attention_f16's single pass).
+ * Results for a given workspace size are deterministic; calls that share a
+ * workspace must be ordered on one stream. */
+hipError_t ql_decode_attention_workspace_size(int n_heads, int n_kv_heads, int head_dim,
+                                              int kv_len, size_t* bytes);
+hipError_t ql_decode_attention_f16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                   uint16_t* out, int kv_len, int n_heads, int n_kv_heads,
+                                   int head_dim, int64_t kv_row_stride, void* workspace,
+                                   size_t workspace_bytes, hipStream_t stream);
+
 /* Attention over the paged KV cache (pool layout of src/paged_kvcache.cu:26-46, the
  * layout ql_paged_kv_append_f16 writes), for n_seqs sequences at once.  Device
  * arrays: cu_q_lens[n_seqs+1] (sequence s owns query rows cu_q_lens[s] ..

@@ -1141,20 +1141,14 @@ hipError_t launch_decode(const AttnArgs& a, int head_dim, int n_seqs, hipStream_
     QL_CHECK_ARG((long long)a.n_split * n_cg <= INT32_MAX);
     const dim3 grid((unsigned)(a.n_split * n_cg), (unsigned)a.n_kv_heads, (unsigned)n_seqs);
     const dim3 cgrid((unsigned)a.n_heads, (unsigned)n_seqs);
-    // the contiguous-cache decode (one sequence) always runs unsplit
-    if (!PAGED && a.n_split != 1) return hipErrorInvalidValue;
     if (head_dim == 128) {
         hipLaunchKernelGGL((attn_decode<128, PAGED>), grid, dim3(kAttnThreads), 0, stream, a);
-        if constexpr (PAGED) {
-            if (a.n_split > 1)
-                hipLaunchKernelGGL((attn_decode_combine<128, PAGED>), cgrid, dim3(kMaxSplits), 0, stream, a);
-        }
+        if (a.n_split > 1)
+            hipLaunchKernelGGL((attn_decode_combine<128, PAGED>), cgrid, dim3(kMaxSplits), 0, stream, a);
     } else {
         hipLaunchKernelGGL((attn_decode<64, PAGED>), grid, dim3(kAttnThreads), 0, stream, a);
-        if constexpr (PAGED) {
-            if (a.n_split > 1)
-                hipLaunchKernelGGL((attn_decode_combine<64, PAGED>), cgrid, dim3(kMaxSplits), 0, stream, a);
-        }
+        if (a.n_split > 1)
+            hipLaunchKernelGGL((attn_decode_combine<64, PAGED>), cgrid, dim3(kMaxSplits), 0, stream, a);
     }
     return hipGetLastError();
 }
@@ -1260,6 +1254,52 @@ extern "C" hipError_t ql_paged_decode_workspace_size(int n_seqs, int n_heads, in
     const int n_split = dec_splits(n_seqs, n_kv_heads, dec_col_chunks(n_heads, n_kv_heads), max_ctx_len);
     *bytes = dec_ws_bytes(n_seqs, n_heads, head_dim, n_split);
     return hipSuccess;
+}
+
+extern "C" hipError_t ql_decode_attention_workspace_size(int n_heads, int n_kv_heads, int head_dim,
+                                                         int kv_len, size_t* bytes) {
+    QL_CHECK_ARG(bytes && n_heads > 0 && n_kv_heads > 0 && n_kv_heads <= n_heads);
+    QL_CHECK_ARG((head_dim == 64 || head_dim == 128) && kv_len >= 0);
+    const int n_split = dec_splits(1, n_kv_heads, dec_col_chunks(n_heads, n_kv_heads), kv_len);
+    *bytes = dec_ws_bytes(1, n_heads, head_dim, n_split);
+    return hipSuccess;
+}
+
+extern "C" hipError_t ql_decode_attention_f16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                              uint16_t* out, int kv_len, int n_heads, int n_kv_heads,
+                                              int head_dim, int64_t kv_row_stride, void* workspace,
+                                              size_t workspace_bytes, hipStream_t stream) {
+    QL_CHECK_ARG(kv_len >= 0 && n_heads > 0 && n_kv_heads > 0);
+    QL_CHECK_ARG(n_kv_heads <= n_heads && n_heads <= 65535);
+    QL_CHECK_ARG(head_dim == 64 || head_dim == 128);
+    QL_CHECK_ARG(kv_row_stride >= (int64_t)n_kv_heads * head_dim);
+    QL_CHECK_ARG(kv_row_stride < (int64_t)1 << 24);   // as ql_attention_f16
+    QL_CHECK_ARG(workspace_bytes == 0 || workspace);
+    QL_CHECK_ARG(q && out && (kv_len == 0 || (k && v)));
+    const int64_t qs = (int64_t)n_heads * head_dim;
+    QL_CHECK_ARG(aligned_rows(q, qs) && aligned_rows(out, qs));
+    QL_CHECK_ARG(kv_len == 0 || (aligned_rows(k, kv_row_stride) && aligned_rows(v, kv_row_stride)));
+    AttnArgs a{};
+    a.q = reinterpret_cast<const _Float16*>(q);
+    a.out = reinterpret_cast<_Float16*>(out);
+    a.q_stride = qs;
+    a.o_stride = qs;
+    a.n_heads = n_heads;
+    a.n_kv_heads = n_kv_heads;
+    a.cl2 = scale_log2e(head_dim);
+    a.causal = 1;
+    a.q_len = 1;
+    a.kv_len = kv_len;
+    a.k = reinterpret_cast<const _Float16*>(k);
+    a.v = reinterpret_cast<const _Float16*>(v);
+    a.kv_stride = kv_row_stride;
+    // as many key splits as wanted and the workspace holds (1 = no workspace used)
+    int n_split = dec_splits(1, n_kv_heads, dec_col_chunks(n_heads, n_kv_heads), kv_len);
+    while (n_split > 1 && dec_ws_bytes(1, n_heads, head_dim, n_split) > workspace_bytes) --n_split;
+    QL_CHECK_ARG(n_split == 1 || qlh::aligned16(workspace));
+    a.n_split = n_split;
+    a.ws = n_split > 1 ? static_cast<float*>(workspace) : nullptr;
+    return launch_decode<false>(a, head_dim, 1, stream);
 }
 
 namespace {

@@ -61,6 +61,8 @@ SIGNATURES = {
     "ql_f32_to_f16": [_p, _p, _i64, _p],
     "ql_flash_attention_f16": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p],
     "ql_attention_f16": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _i64, _i64, _i64, _i, _p],
+    "ql_decode_attention_workspace_size": [_i, _i, _i, _i, _p],
+    "ql_decode_attention_f16": [_p, _p, _p, _p, _i, _i, _i, _i, _i64, _p, ctypes.c_size_t, _p],
     "ql_paged_attention_f16": [_p, _p, _i64, _i64, _i, _i, _p, _p, _i, _p, _i, _p, _p, _i, _i, _i,
                                _i, _i, _i, _i, _p],
     "ql_paged_decode_workspace_size": [_i, _i, _i, _i, _i, _p],

@@ -200,6 +200,16 @@ def test_decode_workspace_size_host_query():
     assert size.value == 0
 
 
+def test_contiguous_decode_workspace_size_host_query():
+    size = ctypes.c_size_t()
+    for h, hkv, d, kv, splits in ((32, 8, 128, 8192, 32), (32, 8, 128, 100, 1), (8, 2, 64, 4096, 16)):
+        assert ql.raw("ql_decode_attention_workspace_size", h, hkv, d, kv, ctypes.byref(size)) == 0
+        assert size.value == (0 if splits == 1 else h * splits * (d + 2) * 4), (h, hkv, d, kv, size.value)
+    assert ql.raw("ql_decode_attention_workspace_size", 32, 8, 96, 100, ctypes.byref(size)) == INVALID
+    assert ql.raw("ql_decode_attention_f16", P, P, P, P, 10, 32, 8, 128, 8 * 128 - 8, None, 0, None) == INVALID
+    assert ql.raw("ql_decode_attention_f16", P, P, P, P, 10, 32, 8, 128, 8 * 128, None, 64, None) == INVALID
+
+
 def test_fp8_gemm_workspace_size_host_query():
     size = ctypes.c_size_t(123)
     q = lambda *a: ql.raw("ql_fp8_gemm_workspace_size", *a, ctypes.addressof(size))

@@ -316,6 +316,56 @@ def test_decode_contiguous_gqa_groups(h, hkv, d, kv_len):
                f"decode h={h}/{hkv} d={d} kv={kv_len}")
 
 
+@pytest.mark.parametrize("h,hkv,d", [(32, 8, 128), (8, 2, 64), (32, 1, 128), (6, 4, 64)])
+@pytest.mark.parametrize("kv_len,row_pad", [(1, 0), (300, 0), (1000, 8), (8192, 0), (4097, 16)])
+def test_contiguous_decode_key_split(h, hkv, d, kv_len, row_pad):
+    """ql_decode_attention_f16: with the queried workspace the keys are split over
+    workgroups (then combined); against the oracle, bit-identical to the paged split
+    decode over the same keys (identity block table, same workspace size), and with
+    no workspace bit-identical to ql_attention_f16's single pass.  row_pad: K/V rows
+    strided past n_kv_heads*d."""
+    q, k, v = qkv(kv_len + 7 * h + d, 1, kv_len, h, hkv, d, 2.0)
+    stride = hkv * d + row_pad
+    kp = np.zeros((kv_len, stride), np.uint16)
+    vp = np.zeros((kv_len, stride), np.uint16)
+    kp[:, :hkv * d] = k.reshape(kv_len, -1)
+    vp[:, :hkv * d] = v.reshape(kv_len, -1)
+    dq, dk, dv = dev(q), dev(kp), dev(vp)
+    size = ctypes.c_size_t()
+    ql.call("ql_decode_attention_workspace_size", h, hkv, d, kv_len, ctypes.addressof(size))
+    ws = empty((max(size.value, 16),), np.uint8, fill_bits=0x7F)
+    split = Out(h * d, np.uint16)
+    ql.call("ql_decode_attention_f16", ptr(dq), ptr(dk), ptr(dv), split.ptr, kv_len, h, hkv, d, stride,
+            ws.ptr if size.value else None, size.value, stream())
+    got = split.get((1, h, d))
+    check_attn(got, orc.attention(q, k, v, h, hkv, True, f16=True), v,
+               f"split decode h={h}/{hkv} d={d} kv={kv_len}")
+    # no workspace: the single pass of ql_attention_f16
+    one, ref1 = Out(h * d, np.uint16), Out(h * d, np.uint16)
+    ql.call("ql_decode_attention_f16", ptr(dq), ptr(dk), ptr(dv), one.ptr, kv_len, h, hkv, d, stride,
+            None, 0, stream())
+    ql.call("ql_attention_f16", ptr(dq), ptr(dk), ptr(dv), ref1.ptr, 1, kv_len, h, hkv, d, h * d, stride,
+            h * d, 1, stream())
+    assert np.array_equal(one.get(), ref1.get())
+    # the paged split decode over the same keys (blocks in order) runs the same split
+    L, layer = 2, 1
+    nbs = (kv_len + 15) // 16
+    pool = PagedPool(nbs, L, hkv, d)
+    bt = np.arange(nbs, dtype=np.int32)
+    pool.append(bt, k, v, layer)
+    psize = ctypes.c_size_t()
+    ql.call("ql_paged_decode_workspace_size", 1, h, hkv, d, kv_len, ctypes.addressof(psize))
+    assert psize.value == size.value
+    pws = empty((max(psize.value, 16),), np.uint8, fill_bits=0x7F)
+    paged = Out(h * d, np.uint16)
+    dctx, dbt = dev(np.array([kv_len], np.int32)), dev(bt)
+    ql.call("ql_paged_decode_attention_f16", ptr(dq), paged.ptr, h * d, h * d, 1,
+            dctx.ptr, kv_len, dbt.ptr, nbs, pool.kptrs.ptr,
+            pool.vptrs.ptr, pool.nb, layer, L, h, hkv, d, pws.ptr if psize.value else None, psize.value,
+            stream())
+    assert np.array_equal(paged.get((1, h, d)), got)
+
+
 def _decode_setup(ctx, h, hkv, d, L, layer, seed):
     r = np.random.default_rng(seed)
     need = [(c + 15) // 16 for c in ctx]
