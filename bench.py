@@ -43,7 +43,12 @@ on the K/V rows, and one whole decoder layer through the engine (hipBLASLt
 GEMMs + the fused kernels + attention) for that prefill and those decode steps,
 on fp16 weights and on FP8 weights (the reference's quantized forward; the
 decode steps also as a 32-layer step captured in one HIP graph), plus the
-FP8-weight GEMM at decode row counts against the fp16 GEMM and the FP8 codec.
+FP8-weight GEMM at decode row counts against the fp16 GEMM and the FP8 codec,
+the decode of one sequence over the contiguous cache (one pass and key split),
+and the reference's own kernel benchmark (tests/benchmark_all.cu: its shapes,
+its timing method, through the drop-in shims) beside its published times.
+Matrix-core-bound passes warm up for ~60 ms on their own kernel rather than on
+copies (the clocks need it after a memory-bound pass).
 
 Device memory, the stream and events come from libamdhip64 through the
 library's own binding (quant-lib_amd/quantlib_amd.py); no framework runtime is
