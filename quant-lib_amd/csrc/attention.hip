@@ -116,11 +116,11 @@ struct AttnArgs {
     float* ws;                     // [n_seqs, n_heads, n_split, head_dim + 2] partials
 };
 
-// Page bases of up to 4 consecutive 16-key pages: the address of (block,
-// layer, slot 0, this KV head) for K and V, or 0 where the table entry is
-// missing or out of range.  The lookups use VECTOR loads whose results are
-// broadcast with v_readlane: scalar loads would share the LDS wait counter, so
-// every LDS wait would also wait for the lookup.
+// Page bases of the consecutive 16-key pages of one decode step (up to 4): the
+// address of (block, layer, slot 0, this KV head) for K and V, or 0 where the
+// table entry is missing or out of range.  The lookups use VECTOR loads whose
+// results are broadcast with v_readlane: scalar loads would share the LDS wait
+// counter, so every LDS wait would also wait for the lookup.
 struct Pages {
     uintptr_t k[4], v[4];
     bool misaligned;
@@ -134,9 +134,9 @@ __device__ __forceinline__ uintptr_t readlane64(uintptr_t x, int l) {
 
 // Three-stage lookup of the page bases of COUNT consecutive pages: (1) lane p
 // loads table entry first+p, (2) it loads the two block pointers, (3) the
-// results are broadcast with v_readlane.  Each stage's result is consumed one
-// tile later, at a point where the kernel waits for its K/V loads anyway, so the
-// dependent table -> pointer chain never stalls the tile in flight.
+// results are broadcast with v_readlane (decode).  Each stage's result is
+// consumed one step later, at a point where the kernel waits for its K/V loads
+// anyway, so the dependent table -> pointer chain never stalls the step in flight.
 // A null block pointer in device memory: the pointer lookup of a missing table
 // entry reads it, so the lookup is one unconditional load.
 __device__ const _Float16* const kNoBlock = nullptr;
@@ -191,6 +191,39 @@ struct PagePipe {
     }
 };
 
+// Lookup of the base of this wavefront's page of a prefill tile: (1) the table
+// entry, (2) the two block pointers, (3) the head offset; each stage's result is
+// consumed one tile later, where the kernel waits for its K/V loads anyway.
+// Every lane loads the same addresses, so the results stay in the wavefront's
+// own registers.
+template <bool PAGED>
+struct WavePagePipe {
+    int b = -1;
+    uintptr_t kp = 0, vp = 0;
+
+    __device__ __forceinline__ void entry(const AttnArgs& a, const int32_t* table, int t) {
+        if constexpr (PAGED) {
+            typedef const int32_t __attribute__((address_space(1)))* GlobalEntryPtr;
+            b = *(GlobalEntryPtr)(t < a.max_blocks ? table + t : &kNoEntry);
+        }
+    }
+    __device__ __forceinline__ void pointers(const AttnArgs& a) {
+        if constexpr (PAGED) {
+            const bool ok = b >= 0 && b < a.n_blocks;
+            typedef const _Float16* const __attribute__((address_space(1)))* GlobalBlockPtr;
+            kp = reinterpret_cast<uintptr_t>(*(GlobalBlockPtr)(ok ? a.kb + b : &kNoBlock));
+            vp = reinterpret_cast<uintptr_t>(*(GlobalBlockPtr)(ok ? a.vb + b : &kNoBlock));
+        }
+    }
+    __device__ __forceinline__ void bases(const AttnArgs& a, int kvh, int hd, uintptr_t& k, uintptr_t& v) const {
+        if constexpr (PAGED) {
+            const uintptr_t head = ((uintptr_t)a.layer * QL_PAGE_SIZE * a.n_kv_heads + kvh) * hd * sizeof(_Float16);
+            k = kp ? kp + head : 0;
+            v = vp ? vp + head : 0;
+        }
+    }
+};
+
 typedef const __attribute__((address_space(1))) half8* GlobalHalf8Ptr;
 typedef uint32_t u32x4g __attribute__((ext_vector_type(4)));
 typedef const __attribute__((address_space(1))) u32x4g* GlobalU4Ptr;
@@ -202,7 +235,7 @@ __device__ __forceinline__ half8 load_nt16(uintptr_t p) {
 
 // 16 bytes of chunk ch of a key row (row == 0: missing key -> zeros) for page
 // pointers that are not 16-byte aligned (caller-provided pools): element-wise
-// loads.  Used for a whole tile, chosen once per tile.
+// loads.  Used for a whole page, chosen once per wavefront.
 __device__ __forceinline__ half8 load_chunk_unaligned(uintptr_t row, int ch) {
     half8 r{};
     if (row != 0) {
@@ -214,14 +247,6 @@ __device__ __forceinline__ half8 load_chunk_unaligned(uintptr_t row, int ch) {
         for (int i = 0; i < 8; ++i) r[i] = e[i];
     }
     return r;
-}
-
-// v[i & 3] as selects on the index bits (an indexed array read would be placed in
-// scratch memory)
-__device__ __forceinline__ uintptr_t pick4(const uintptr_t* v, int i) {
-    const uintptr_t lo = (i & 1) ? v[1] : v[0];
-    const uintptr_t hi = (i & 1) ? v[3] : v[2];
-    return (i & 2) ? hi : lo;
 }
 
 // ---- prefill key tiles: global memory straight into LDS ------------------------------------
@@ -269,46 +294,42 @@ __device__ __forceinline__ void lds_load16(const void* src, _Float16* stage, int
                                      0);
 }
 
-// Paged source addresses of load i of this lane.  The 64 slots of one
-// instruction lie in one 16-key page, page (i*4 + wave)*64 / PAGE_SLOTS of the
-// tile.  CHECKED: keys past kv_len and missing pages read kZeroRow.
+// Paged tiles: wavefront w loads page w of the tile (key rows 16w .. 16w+15)
+// with its LOADS instructions, so each wavefront needs the base of one page
+// only and keeps it in its own registers.  Load i of a lane fills slot
+// (w*LOADS + i)*64 + lane, i.e. key row r = slot / CH, chunk (slot % CH) ^
+// tile_swz(r), row r % 16 of the page.  CHECKED: keys past kv_len and a missing
+// page read kZeroRow.
 template <int HD, bool CHECKED>
-__device__ __forceinline__ void page_sources(uintptr_t& kg, uintptr_t& vg, const AttnArgs& a, const Pages& pg,
-                                             int kv0, int kv_len, int i, int wave, int lane) {
+__device__ __forceinline__ void load_wave_page(_Float16* sk, _Float16* sv, const AttnArgs& a, uintptr_t pk,
+                                               uintptr_t pv, int kv0, int kv_len, int wave, int lane) {
     using T = KvTile<HD>;
-    const int first = (i * kAttnWaves + (wave & (kAttnWaves - 1))) * kWave;
-    const int slot = first + lane;
-    const int r = slot / T::CH, c = (slot % T::CH) ^ tile_swz<HD>(r);
-    const int p = first / T::PAGE_SLOTS;
-    const uintptr_t pk = pick4(pg.k, p), pv = pick4(pg.v, p);
-    const uintptr_t off =
-        (uintptr_t)(r & (QL_PAGE_SIZE - 1)) * (uintptr_t)a.n_kv_heads * HD * sizeof(_Float16) + 16u * c;
-    const uintptr_t zero = reinterpret_cast<uintptr_t>(kZeroRow) + 16u * c;
-    const bool ok = kv0 + r < kv_len;
-    kg = !CHECKED || (ok & (pk != 0)) ? pk + off : zero;
-    vg = !CHECKED || (ok & (pv != 0)) ? pv + off : zero;
-}
-
-template <int HD, bool CHECKED>
-__device__ __forceinline__ void load_pages(_Float16* sk, _Float16* sv, const AttnArgs& a, const Pages& pg, int kv0,
-                                           int kv_len, int wave, int lane) {
 #pragma unroll
-    for (int i = 0; i < KvTile<HD>::LOADS; ++i) {
-        uintptr_t kg, vg;
-        page_sources<HD, CHECKED>(kg, vg, a, pg, kv0, kv_len, i, wave, lane);
-        const int base = (i * kAttnWaves + wave) * kWave;
+    for (int i = 0; i < T::LOADS; ++i) {
+        const int base = (wave * T::LOADS + i) * kWave, slot = base + lane;
+        const int r = slot / T::CH, c = (slot % T::CH) ^ tile_swz<HD>(r);
+        const uintptr_t off =
+            (uintptr_t)(r & (QL_PAGE_SIZE - 1)) * (uintptr_t)a.n_kv_heads * HD * sizeof(_Float16) + 16u * c;
+        uintptr_t kg = pk + off, vg = pv + off;
+        if constexpr (CHECKED) {
+            const uintptr_t zero = reinterpret_cast<uintptr_t>(kZeroRow) + 16u * c;
+            const bool ok = kv0 + r < kv_len;
+            kg = ok && pk != 0 ? kg : zero;
+            vg = ok && pv != 0 ? vg : zero;
+        }
         lds_load16(reinterpret_cast<const void*>(kg), sk, base);
         lds_load16(reinterpret_cast<const void*>(vg), sv, base);
     }
 }
 
 // Issue the loads of key tile [kv0, kv0 + 64) of KV head kvh into sk (K) and sv
-// (V).  Paged: a full tile whose pages are all present takes the unchecked
-// path; page pointers that are not 16-byte aligned (caller-provided pools) take
-// element-wise loads and LDS stores.  Every branch is workgroup-uniform.
+// (V).  Paged: pk / pv are the bases of this wavefront's page (0: missing); a
+// full page takes the unchecked path, page bases that are not 16-byte aligned
+// (caller-provided pools) element-wise loads and LDS stores.  Each branch is
+// uniform over the wavefront.
 template <int HD, bool PAGED>
-__device__ __forceinline__ void load_tile(_Float16* sk, _Float16* sv, const AttnArgs& a, const Pages& pg,
-                                          int kvh, int kv0, int kv_len, int wave, int lane) {
+__device__ __forceinline__ void load_tile(_Float16* sk, _Float16* sv, const AttnArgs& a, uintptr_t pk,
+                                          uintptr_t pv, int kvh, int kv0, int kv_len, int wave, int lane) {
     using T = KvTile<HD>;
     if constexpr (!PAGED) {   // rows 16-byte aligned (checked by the entry points)
 #pragma unroll
@@ -320,20 +341,22 @@ __device__ __forceinline__ void load_tile(_Float16* sk, _Float16* sv, const Attn
             lds_load16(j < kv_len ? a.k + off : kZeroRow + c * 8, sk, base);
             lds_load16(j < kv_len ? a.v + off : kZeroRow + c * 8, sv, base);
         }
-    } else if (pg.misaligned) {
+    } else if (((pk | pv) & 15) != 0) {
 #pragma unroll
         for (int i = 0; i < T::LOADS; ++i) {
-            uintptr_t kg, vg;
-            page_sources<HD, true>(kg, vg, a, pg, kv0, kv_len, i, wave, lane);
-            const int slot = (i * kAttnWaves + wave) * kWave + lane;
-            *reinterpret_cast<half8*>(sk + slot * 8) = load_chunk_unaligned(kg, 0);
-            *reinterpret_cast<half8*>(sv + slot * 8) = load_chunk_unaligned(vg, 0);
+            const int slot = (wave * T::LOADS + i) * kWave + lane;
+            const int r = slot / T::CH, c = (slot % T::CH) ^ tile_swz<HD>(r);
+            const uintptr_t off =
+                (uintptr_t)(r & (QL_PAGE_SIZE - 1)) * (uintptr_t)a.n_kv_heads * HD * sizeof(_Float16) + 16u * c;
+            const uintptr_t zero = reinterpret_cast<uintptr_t>(kZeroRow) + 16u * c;
+            const bool ok = kv0 + r < kv_len;
+            *reinterpret_cast<half8*>(sk + slot * 8) = load_chunk_unaligned(ok && pk != 0 ? pk + off : zero, 0);
+            *reinterpret_cast<half8*>(sv + slot * 8) = load_chunk_unaligned(ok && pv != 0 ? pv + off : zero, 0);
         }
-    } else if (kv0 + kBK <= kv_len && pg.k[0] && pg.k[1] && pg.k[2] && pg.k[3] && pg.v[0] && pg.v[1] && pg.v[2] &&
-               pg.v[3]) {
-        load_pages<HD, false>(sk, sv, a, pg, kv0, kv_len, wave, lane);
+    } else if (kv0 + (wave + 1) * QL_PAGE_SIZE <= kv_len && pk != 0 && pv != 0) {
+        load_wave_page<HD, false>(sk, sv, a, pk, pv, kv0, kv_len, wave, lane);
     } else {
-        load_pages<HD, true>(sk, sv, a, pg, kv0, kv_len, wave, lane);
+        load_wave_page<HD, true>(sk, sv, a, pk, pv, kv0, kv_len, wave, lane);
     }
 }
 
@@ -474,8 +497,9 @@ __device__ __forceinline__ void store_o(const floatx16 (&o)[HD / 32], float l_ru
 // One prefill workgroup: 128 queries of one query head against every key they
 // see, in 64-key tiles through two LDS stages.  The stages are two distinct
 // arrays and the tile loop is unrolled by two, so no wait for the loads into
-// one stage is placed before the reads of the other.  Paged K/V: the page bases
-// of tile t+2 are looked up (PagePipe) while tile t is multiplied.
+// one stage is placed before the reads of the other.  Paged K/V: wavefront w
+// loads page w of each tile, and the base of its page of tile t+2 is looked up
+// (WavePagePipe) while tile t is multiplied.
 template <int HD, bool PAGED>
 __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
     using T = KvTile<HD>;
@@ -564,30 +588,33 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
     };
 
     constexpr int kTilePages = kBK / QL_PAGE_SIZE;
-    PagePipe<PAGED, kTilePages> pp;
-    Pages pg_next{};
+    static_assert(kTilePages == kAttnWaves && KvTile<HD>::PAGE_SLOTS == KvTile<HD>::LOADS * kWave,
+                  "one page per wavefront");
+    WavePagePipe<PAGED> pp;
+    uintptr_t pgk = 0, pgv = 0;   // this wavefront's page of the next tile (paged)
     if (n_tiles > 0) {
-        pp.entries(a, table, 0);
+        uintptr_t k0 = 0, v0 = 0;
+        pp.entry(a, table, wave);
         pp.pointers(a);
-        const Pages pg0 = pp.bases(a, kvh, HD);
+        pp.bases(a, kvh, HD, k0, v0);
         if (n_tiles > 1) {
-            pp.entries(a, table, kTilePages);
+            pp.entry(a, table, kTilePages + wave);
             pp.pointers(a);
-            pg_next = pp.bases(a, kvh, HD);
+            pp.bases(a, kvh, HD, pgk, pgv);
         }
-        if (n_tiles > 2) pp.entries(a, table, 2 * kTilePages);
-        load_tile<HD, PAGED>(sk0, sv0, a, pg0, kvh, 0, kv_len, wave, lane);
+        if (n_tiles > 2) pp.entry(a, table, 2 * kTilePages + wave);
+        load_tile<HD, PAGED>(sk0, sv0, a, k0, v0, kvh, 0, kv_len, wave, lane);
     }
     wait_tile_loads();
     __syncthreads();
     // tile t sits in (sk, sv); tile t+1 is loaded into (nk, nv) meanwhile
     auto step = [&](int t, const _Float16* sk, const _Float16* sv, _Float16* nk, _Float16* nv) {
         const int kv0 = t * kBK;
-        if (t + 1 < n_tiles) load_tile<HD, PAGED>(nk, nv, a, pg_next, kvh, kv0 + kBK, kv_len, wave, lane);
-        if (t + 2 < n_tiles) pp.pointers(a);                      // tile t+2
-        if (t + 3 < n_tiles) pp.entries(a, table, (t + 3) * kTilePages);   // tile t+3
+        if (t + 1 < n_tiles) load_tile<HD, PAGED>(nk, nv, a, pgk, pgv, kvh, kv0 + kBK, kv_len, wave, lane);
+        if (t + 2 < n_tiles) pp.pointers(a);                                    // tile t+2
+        if (t + 3 < n_tiles) pp.entry(a, table, (t + 3) * kTilePages + wave);   // tile t+3
         compute(sk, sv, kv0);
-        if (t + 2 < n_tiles) pg_next = pp.bases(a, kvh, HD);
+        if (t + 2 < n_tiles) pp.bases(a, kvh, HD, pgk, pgv);
         wait_tile_loads();
         __syncthreads();
     };
