@@ -191,20 +191,36 @@ struct PagePipe {
     }
 };
 
+// A zero held in a vector register that the compiler cannot see through.  A
+// load whose address is uniform over the wavefront has its result moved to
+// scalar registers right after it is issued, which waits for that load and for
+// every load issued before it; offset by this zero, the lookups below keep
+// their results in vector registers until bases() moves them, after the tile's
+// products.
+__device__ __forceinline__ int divergent_zero() {
+    int z;
+    asm("v_mov_b32 %0, 0" : "=v"(z));
+    return z;
+}
+
 // Lookup of the base of this wavefront's page of a prefill tile: (1) the table
 // entry, (2) the two block pointers, (3) the head offset; each stage's result is
 // consumed one tile later, where the kernel waits for its K/V loads anyway.
-// Every lane loads the same addresses, so the results stay in the wavefront's
-// own registers.
+// Every lane loads the same addresses; bases() moves the result to scalar
+// registers.
 template <bool PAGED>
 struct WavePagePipe {
     int b = -1;
     uintptr_t kp = 0, vp = 0;
+    int z = 0;
 
+    __device__ __forceinline__ void init() {
+        if constexpr (PAGED) z = divergent_zero();
+    }
     __device__ __forceinline__ void entry(const AttnArgs& a, const int32_t* table, int t) {
         if constexpr (PAGED) {
             typedef const int32_t __attribute__((address_space(1)))* GlobalEntryPtr;
-            b = *(GlobalEntryPtr)(t < a.max_blocks ? table + t : &kNoEntry);
+            b = *(GlobalEntryPtr)((t < a.max_blocks ? table + t : &kNoEntry) + z);
         }
     }
     __device__ __forceinline__ void pointers(const AttnArgs& a) {
@@ -218,8 +234,9 @@ struct WavePagePipe {
     __device__ __forceinline__ void bases(const AttnArgs& a, int kvh, int hd, uintptr_t& k, uintptr_t& v) const {
         if constexpr (PAGED) {
             const uintptr_t head = ((uintptr_t)a.layer * QL_PAGE_SIZE * a.n_kv_heads + kvh) * hd * sizeof(_Float16);
-            k = kp ? kp + head : 0;
-            v = vp ? vp + head : 0;
+            const uintptr_t ks = readlane64(kp, 0), vs = readlane64(vp, 0);
+            k = ks ? ks + head : 0;
+            v = vs ? vs + head : 0;
         }
     }
 };
@@ -591,6 +608,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
     static_assert(kTilePages == kAttnWaves && KvTile<HD>::PAGE_SLOTS == KvTile<HD>::LOADS * kWave,
                   "one page per wavefront");
     WavePagePipe<PAGED> pp;
+    pp.init();
     uintptr_t pgk = 0, pgv = 0;   // this wavefront's page of the next tile (paged)
     if (n_tiles > 0) {
         uintptr_t k0 = 0, v0 = 0;
