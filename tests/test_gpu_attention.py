@@ -226,6 +226,33 @@ def test_paged_attention_skips_bad_rows_and_missing_blocks():
 
 
 @pytest.mark.parametrize("d", [64, 128])
+def test_paged_prefill_tile_with_one_missing_page(d):
+    # 200-token causal prefill over 13 permuted blocks whose table misses page 5
+    # (keys 80..95, the second page of the second 64-key tile): in that tile one
+    # wavefront's page takes the checked loads and reads zero rows while the
+    # other three load their pages unchecked; the last tile is partial (keys
+    # 192..199).  Oracle: the same attention with K/V rows 80..95 zeroed.
+    h, hkv, L, layer, n = 8, 2, 2, 1, 200
+    pool = PagedPool(16, L, hkv, d)
+    k = to_f16_bits(normal(71 + d, (n, hkv, d)))
+    v = to_f16_bits(normal(72 + d, (n, hkv, d)))
+    table = np.random.default_rng(d).permutation(16)[:13].astype(np.int32)
+    pool.append(table, k, v, layer)
+    bt = table.copy()
+    bt[5] = -1
+    q = to_f16_bits(normal(73 + d, (n, h, d)))
+    dq, dcu, dctx, dbt = dev(q), dev(np.array([0, n], np.int32)), dev(np.array([n], np.int32)), dev(bt[None, :])
+    out = Out(n * h * d, np.uint16)
+    ql.call("ql_paged_attention_f16", dq.ptr, out.ptr, h * d, h * d, n, 1, dcu.ptr, dctx.ptr, n,
+            dbt.ptr, 13, pool.kptrs.ptr, pool.vptrs.ptr, 16, layer, L, h, hkv, d, 1, stream())
+    kz, vz = k.copy(), v.copy()
+    kz[80:96] = 0
+    vz[80:96] = 0
+    check_attn(out.get((n, h, d)), orc.attention(q, kz, vz, h, hkv, True, f16=True), v,
+               f"d={d} tile with one missing page")
+
+
+@pytest.mark.parametrize("d", [64, 128])
 def test_paged_attention_misaligned_block_pointers(d):
     # block pointers 2 bytes past a 16-byte boundary take the element-wise load
     # path: prefill and decode give the same bits as over an aligned pool, and
