@@ -233,12 +233,15 @@ hipError_t ql_f32_to_f16(const float* src, uint16_t* dst, int64_t n, hipStream_t
  * out[i, h, :] = sum_j softmax_j((q[i,h,:] . k[j,g,:]) * scale) v[j,g,:] with
  * g = h * n_kv_heads / n_heads (grouped-query heads, kernels/flash_attention.cu:45),
  * scale = 1/sqrtf(head_dim) (:173), normalised as O / (l + 1e-8) (:161).  Causal:
- * key j is visible to query i when j <= its position.  head_dim must be 64 or 128;
- * rows 16-byte aligned (strides multiples of 8 elements). */
+ * key j is visible to query i when j <= its position.  head_dim 64 and 128 run on
+ * the matrix cores and need rows 16-byte aligned (strides multiples of 8 elements);
+ * every other head_dim from 1 to 64 (the reference kernel's range) runs a vector-ALU
+ * kernel at any row alignment, with fp32 probabilities, in one pass (the workspace
+ * sizes below are 0 for it).  Other head_dims are rejected. */
 
 /* Replaces launch_flash_attention (kernels/flash_attention.cu:169-182): Q, out
  * [seq_len, n_heads, head_dim]; K, V [seq_len, n_kv_heads, head_dim], query i at
- * position i.  (The reference's tiles hold head_dim <= 64 only.) */
+ * position i.  (The reference's tiles hold head_dim <= 64 only; 128 is an extension.) */
 hipError_t ql_flash_attention_f16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                   uint16_t* out, int seq_len, int n_heads, int n_kv_heads,
                                   int head_dim, int causal, hipStream_t stream);

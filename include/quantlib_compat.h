@@ -55,10 +55,17 @@ void launch_fp16_embed(const __half* table, __half* out, int token_id, int hidde
 void launch_fp16_add(__half* x, const __half* y, int n, hipStream_t stream);
 /* kernels/fp16_ops.cu:149 */
 void launch_fp16_to_fp32(const __half* src, float* dst, int n, hipStream_t stream);
-/* kernels/flash_attention.cu:169-182 (head_dim 64 or 128; see ql_flash_attention_f16) */
+/* kernels/flash_attention.cu:169-182 (head_dim 1..64, the reference's range, or 128;
+ * see ql_flash_attention_f16) */
 void launch_flash_attention(const __half* Q, const __half* K, const __half* V, __half* Out,
                             int seq_len, int n_heads, int n_kv_heads, int head_dim, int causal,
                             hipStream_t stream);
+/* src/fp16_forward.cu:285-297: the index of the largest of logits[0 .. vocab_size)
+ * (the first such index), copied to the host; the call synchronises the stream and,
+ * like the reference, allocates and frees a 4-byte device buffer.  Where the
+ * reference would exit (a failed HIP call) it returns -1; vocab_size <= 0 gives 0,
+ * as the reference's empty scan does. */
+int fp16_greedy_sample(const float* logits, int vocab_size, hipStream_t stream);
 
 /* ---- inline kernels of src/forward.cu / src/fp16_forward.cu given launchers ---- */
 /* src/forward.cu:128-135 (add_residual_kernel + its static launcher) */

@@ -9,8 +9,9 @@
 // masked when causal (:106); the softmax is the online (running max, running
 // sum) form and the output is O / (l + 1e-8) (:161).  Generalisations: the
 // queries may be the last q_len positions of a longer context (decode and
-// chunked prefill), head_dim may be 64 or 128 (the reference's tiles hold 64),
-// rows may be strided, and K/V may live in 16-token pages.
+// chunked prefill), head_dim may be 64 or 128 on the matrix cores (the
+// reference's tiles hold 64) and any other value up to 64 on a vector-ALU
+// kernel (attn_small), rows may be strided, and K/V may live in 16-token pages.
 //
 // Work decomposition (prefill).  One workgroup = 4 wavefronts = 128
 // consecutive queries of one query head; each wavefront owns 32 queries.  Keys
@@ -114,6 +115,7 @@ struct AttnArgs {
     // decode (one query row per sequence)
     int n_split;                   // key splits per (sequence, KV head)
     float* ws;                     // [n_seqs, n_heads, n_split, head_dim + 2] partials
+    int hd;                        // head_dim (read by attn_small only)
 };
 
 // Page bases of the consecutive 16-key pages of one decode step (up to 4): the
@@ -1138,6 +1140,150 @@ __global__ __launch_bounds__(kMaxSplits) void attn_decode_combine(AttnArgs a) {
     }
 }
 
+// ---- any other head_dim up to 64 ------------------------------------------------------
+//
+// The reference kernel's tiles hold head_dim <= 64 and take any such value
+// (kernels/flash_attention.cu:25-27,64-66); the matrix-core kernels above take
+// 64 and 128 with 16-byte rows.  This kernel covers the rest of that range, 1 ..
+// 63, at any row alignment: one workgroup = 256 consecutive queries of one
+// query head, one query per lane.  Key tiles of 64 rows are staged through LDS
+// as binary16, zero-padded to HDP (16, 32 or 64) columns, one element per load
+// (no alignment assumed), and every lane reads the same LDS row (a broadcast).
+// A lane keeps its query, running max, running sum and output row in
+// registers; scores, probabilities and sums are fp32 (the probabilities are
+// not rounded to binary16 as in the matrix-core kernels).  Masking, the GQA
+// map, the paged lookups (a missing page reads as zero keys), the sequence
+// checks and O / (l + 1e-8) are those of attn_fwd and attn_decode.
+constexpr int kSmallThreads = 256;
+constexpr int kSmallBK = 64;   // keys per LDS tile
+constexpr int kSmallSub = 32;  // keys per online-softmax update (bounds the score registers)
+
+template <int HDP, bool PAGED>
+__global__ __launch_bounds__(kSmallThreads) void attn_small(AttnArgs a) {
+    static_assert(HDP % 8 == 0 && HDP <= 64, "LDS rows are read 8 halfs at a time");
+    __shared__ __attribute__((aligned(16))) _Float16 sk[kSmallBK * HDP];
+    __shared__ __attribute__((aligned(16))) _Float16 sv[kSmallBK * HDP];
+    const int hd = a.hd;
+    const int head = (int)blockIdx.x % a.n_heads, qt = (int)blockIdx.x / a.n_heads;
+    const int kvh = (int)(((long long)head * a.n_kv_heads) / a.n_heads);
+    int q_begin = 0, q_len = a.q_len, kv_len = a.kv_len;
+    const int32_t* table = nullptr;
+    if constexpr (PAGED) {
+        const int s = blockIdx.z;
+        if (a.cu_q) {
+            q_begin = a.cu_q[s];
+            q_len = a.cu_q[s + 1] - q_begin;
+        } else {   // decode: sequence s owns query row s
+            q_begin = s;
+            q_len = 1;
+        }
+        kv_len = a.ctx_lens[s];
+        if (q_begin < 0 || q_len <= 0 || q_begin + q_len > a.n_q_rows) return;   // workgroup-uniform
+        if (kv_len > a.max_blocks * QL_PAGE_SIZE) kv_len = a.max_blocks * QL_PAGE_SIZE;
+        table = a.block_tables + (size_t)s * a.max_blocks;
+    }
+    if (kv_len < 0) kv_len = 0;
+    const int q0 = qt * kSmallThreads;
+    if (q0 >= q_len) return;   // workgroup-uniform
+
+    const int tid = threadIdx.x;
+    const int qi = q0 + tid;
+    const bool q_valid = qi < q_len;
+    const int pos_base = kv_len - q_len;   // absolute position of query 0
+    // keys this workgroup needs, and the last key this lane's query sees
+    int kv_hi = kv_len;
+    if (a.causal) kv_hi = min(kv_len, pos_base + min(q_len, q0 + kSmallThreads));
+    const int last = a.causal ? min(pos_base + qi, kv_len - 1) : kv_len - 1;
+
+    float q[HDP], o[HDP];
+    {
+        const _Float16* qrow = a.q + (size_t)(q_begin + (q_valid ? qi : 0)) * a.q_stride + (size_t)head * hd;
+#pragma unroll
+        for (int d = 0; d < HDP; ++d) {
+            q[d] = q_valid && d < hd ? (float)qrow[d] : 0.0f;
+            o[d] = 0.0f;
+        }
+    }
+    float m_run = -INFINITY, l_run = 0.0f;
+    const float cl2 = a.cl2;
+
+    for (int kv0 = 0; kv0 < kv_hi; kv0 += kSmallBK) {
+        __syncthreads();   // every lane has read the previous tile
+        for (int i = tid; i < kSmallBK * HDP; i += kSmallThreads) {
+            const int r = i / HDP, c = i % HDP, key = kv0 + r;
+            _Float16 kx = 0, vx = 0;
+            if (c < hd && key < kv_len) {
+                const _Float16* kp = nullptr;
+                const _Float16* vp = nullptr;
+                if constexpr (PAGED) {
+                    const int b = table[key / QL_PAGE_SIZE];
+                    if (b >= 0 && b < a.n_blocks) {
+                        const size_t off =
+                            (((size_t)a.layer * QL_PAGE_SIZE + key % QL_PAGE_SIZE) * a.n_kv_heads + kvh) * hd + c;
+                        const _Float16* kb = a.kb[b];
+                        const _Float16* vb = a.vb[b];
+                        kp = kb ? kb + off : nullptr;
+                        vp = vb ? vb + off : nullptr;
+                    }
+                } else {
+                    const size_t off = (size_t)key * a.kv_stride + (size_t)kvh * hd + c;
+                    kp = a.k + off;
+                    vp = a.v + off;
+                }
+                if (kp) kx = *kp;
+                if (vp) vx = *vp;
+            }
+            sk[i] = kx;
+            sv[i] = vx;
+        }
+        __syncthreads();
+        if (!q_valid) continue;
+#pragma unroll 1
+        for (int j0 = kv0; j0 < kv0 + kSmallBK && j0 <= last; j0 += kSmallSub) {
+            const _Float16* kt = sk + (j0 - kv0) * HDP;
+            const _Float16* vt = sv + (j0 - kv0) * HDP;
+            float s[kSmallSub];
+            float m_sub = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < kSmallSub; ++j) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int c = 0; c < HDP / 8; ++c) {
+                    const half8 k8 = *reinterpret_cast<const half8*>(kt + j * HDP + 8 * c);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc = fmaf(q[8 * c + e], (float)k8[e], acc);
+                }
+                s[j] = j0 + j <= last ? acc : -INFINITY;
+                m_sub = fmaxf(m_sub, s[j]);
+            }
+            // m_sub is finite: key j0 <= last is visible
+            const float m_new = fmaxf(m_run, m_sub);
+            const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * cl2);   // 0 on the first update
+            l_run *= alpha;
+#pragma unroll
+            for (int d = 0; d < HDP; ++d) o[d] *= alpha;
+#pragma unroll
+            for (int j = 0; j < kSmallSub; ++j) {
+                const float p = __builtin_amdgcn_exp2f((s[j] - m_new) * cl2);   // 0 for masked keys
+                l_run += p;
+#pragma unroll
+                for (int c = 0; c < HDP / 8; ++c) {
+                    const half8 v8 = *reinterpret_cast<const half8*>(vt + j * HDP + 8 * c);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) o[8 * c + e] = fmaf(p, (float)v8[e], o[8 * c + e]);
+                }
+            }
+            m_run = m_new;
+        }
+    }
+    if (!q_valid) return;
+    const float inv_den = 1.0f / (l_run + 1e-8f);
+    _Float16* orow = a.out + (size_t)(q_begin + qi) * a.o_stride + (size_t)head * hd;
+#pragma unroll
+    for (int d = 0; d < HDP; ++d)
+        if (d < hd) orow[d] = from_f32<_Float16>(o[d] * inv_den);
+}
+
 float scale_log2e(int head_dim) {
     const float scale = 1.0f / sqrtf((float)head_dim);   // the reference's scale, fp32
     return (float)((double)scale * 1.4426950408889634);
@@ -1157,6 +1303,26 @@ hipError_t launch_attn(const AttnArgs& a, int head_dim, unsigned gx, unsigned gz
 
 bool aligned_rows(const void* p, int64_t stride) {
     return qlh::aligned16(p) && stride % 8 == 0;
+}
+
+// head_dim 64 and 128 run the matrix-core kernels; every other value up to 64
+// (the reference kernel's range) runs attn_small.
+bool mfma_hd(int head_dim) { return head_dim == 64 || head_dim == 128; }
+bool valid_hd(int head_dim) { return head_dim == 128 || (head_dim >= 1 && head_dim <= 64); }
+
+// attn_small over n_seqs sequences of at most max_q_len queries (grid z = n_seqs).
+template <bool PAGED>
+hipError_t launch_small(const AttnArgs& a, int max_q_len, unsigned n_seqs, hipStream_t stream) {
+    const long long gx = (long long)qlh::blocks_for(max_q_len, kSmallThreads) * a.n_heads;
+    QL_CHECK_ARG(gx <= INT32_MAX && n_seqs <= 65535);
+    const dim3 grid((unsigned)gx, 1, n_seqs);
+    if (a.hd <= 16)
+        hipLaunchKernelGGL((attn_small<16, PAGED>), grid, dim3(kSmallThreads), 0, stream, a);
+    else if (a.hd <= 32)
+        hipLaunchKernelGGL((attn_small<32, PAGED>), grid, dim3(kSmallThreads), 0, stream, a);
+    else
+        hipLaunchKernelGGL((attn_small<64, PAGED>), grid, dim3(kSmallThreads), 0, stream, a);
+    return hipGetLastError();
 }
 
 // Decode launch shape: chunks of <= 16 query heads per KV head, and key splits
@@ -1207,15 +1373,17 @@ extern "C" hipError_t ql_attention_f16(const uint16_t* q, const uint16_t* k, con
                                        hipStream_t stream) {
     QL_CHECK_ARG(q_len >= 0 && kv_len >= 0 && n_heads > 0 && n_kv_heads > 0);
     QL_CHECK_ARG(n_kv_heads <= n_heads && n_heads <= 65535);
-    QL_CHECK_ARG(head_dim == 64 || head_dim == 128);
+    QL_CHECK_ARG(valid_hd(head_dim));
     QL_CHECK_ARG(q_row_stride >= (int64_t)n_heads * head_dim);
     QL_CHECK_ARG(out_row_stride >= (int64_t)n_heads * head_dim);
     QL_CHECK_ARG(kv_row_stride >= (int64_t)n_kv_heads * head_dim);
     QL_CHECK_ARG(kv_row_stride < (int64_t)1 << 24);   // 64 key rows span < 4 GiB (32-bit offsets)
     if (q_len == 0) return hipSuccess;
     QL_CHECK_ARG(q && out && (kv_len == 0 || (k && v)));
-    QL_CHECK_ARG(aligned_rows(q, q_row_stride) && aligned_rows(out, out_row_stride));
-    QL_CHECK_ARG(kv_len == 0 || (aligned_rows(k, kv_row_stride) && aligned_rows(v, kv_row_stride)));
+    if (mfma_hd(head_dim)) {
+        QL_CHECK_ARG(aligned_rows(q, q_row_stride) && aligned_rows(out, out_row_stride));
+        QL_CHECK_ARG(kv_len == 0 || (aligned_rows(k, kv_row_stride) && aligned_rows(v, kv_row_stride)));
+    }
     AttnArgs a{};
     a.q = reinterpret_cast<const _Float16*>(q);
     a.out = reinterpret_cast<_Float16*>(out);
@@ -1230,6 +1398,8 @@ extern "C" hipError_t ql_attention_f16(const uint16_t* q, const uint16_t* k, con
     a.k = reinterpret_cast<const _Float16*>(k);
     a.v = reinterpret_cast<const _Float16*>(v);
     a.kv_stride = kv_row_stride;
+    a.hd = head_dim;
+    if (!mfma_hd(head_dim)) return launch_small<false>(a, q_len, 1, stream);
     if (q_len == 1) {   // decode: the query heads of a KV head share one pass over K/V
         a.n_split = 1;
         return launch_decode<false>(a, head_dim, 1, stream);
@@ -1255,7 +1425,7 @@ extern "C" hipError_t ql_paged_attention_f16(
     int n_kv_heads, int head_dim, int causal, hipStream_t stream) {
     QL_CHECK_ARG(n_seqs >= 0 && n_seqs <= 65535 && max_q_len >= 0 && n_q_rows >= 0);
     QL_CHECK_ARG(n_heads > 0 && n_kv_heads > 0 && n_kv_heads <= n_heads && n_heads <= 65535);
-    QL_CHECK_ARG(head_dim == 64 || head_dim == 128);
+    QL_CHECK_ARG(valid_hd(head_dim));
     QL_CHECK_ARG(n_layers > 0 && layer >= 0 && layer < n_layers);
     QL_CHECK_ARG(max_blocks_per_seq >= 0 && max_blocks_per_seq <= (INT32_MAX / QL_PAGE_SIZE));
     QL_CHECK_ARG(n_blocks >= 0);
@@ -1264,7 +1434,7 @@ extern "C" hipError_t ql_paged_attention_f16(
     if (n_seqs == 0 || max_q_len == 0 || n_q_rows == 0) return hipSuccess;
     QL_CHECK_ARG(q && out && cu_q_lens && ctx_lens);
     QL_CHECK_ARG(max_blocks_per_seq == 0 || (block_tables && k_blocks && v_blocks));
-    QL_CHECK_ARG(aligned_rows(q, q_row_stride) && aligned_rows(out, out_row_stride));
+    if (mfma_hd(head_dim)) QL_CHECK_ARG(aligned_rows(q, q_row_stride) && aligned_rows(out, out_row_stride));
     AttnArgs a{};
     a.q = reinterpret_cast<const _Float16*>(q);
     a.out = reinterpret_cast<_Float16*>(out);
@@ -1283,6 +1453,8 @@ extern "C" hipError_t ql_paged_attention_f16(
     a.ctx_lens = ctx_lens;
     a.n_q_rows = n_q_rows;
     a.layer = layer;
+    a.hd = head_dim;
+    if (!mfma_hd(head_dim)) return launch_small<true>(a, max_q_len, (unsigned)n_seqs, stream);
     if (max_q_len == 1) {   // every sequence decodes one token
         a.n_split = 1;
         return launch_decode<true>(a, head_dim, n_seqs, stream);
@@ -1293,9 +1465,9 @@ extern "C" hipError_t ql_paged_attention_f16(
 extern "C" hipError_t ql_paged_decode_workspace_size(int n_seqs, int n_heads, int n_kv_heads,
                                                      int head_dim, int max_ctx_len, size_t* bytes) {
     QL_CHECK_ARG(bytes && n_seqs >= 0 && n_heads > 0 && n_kv_heads > 0 && n_kv_heads <= n_heads);
-    QL_CHECK_ARG((head_dim == 64 || head_dim == 128) && max_ctx_len >= 0);
+    QL_CHECK_ARG(valid_hd(head_dim) && max_ctx_len >= 0);
     *bytes = 0;
-    if (n_seqs == 0) return hipSuccess;
+    if (n_seqs == 0 || !mfma_hd(head_dim)) return hipSuccess;   // attn_small: one pass, no workspace
     const int n_split = dec_splits(n_seqs, n_kv_heads, dec_col_chunks(n_heads, n_kv_heads), max_ctx_len);
     *bytes = dec_ws_bytes(n_seqs, n_heads, head_dim, n_split);
     return hipSuccess;
@@ -1304,7 +1476,9 @@ extern "C" hipError_t ql_paged_decode_workspace_size(int n_seqs, int n_heads, in
 extern "C" hipError_t ql_decode_attention_workspace_size(int n_heads, int n_kv_heads, int head_dim,
                                                          int kv_len, size_t* bytes) {
     QL_CHECK_ARG(bytes && n_heads > 0 && n_kv_heads > 0 && n_kv_heads <= n_heads);
-    QL_CHECK_ARG((head_dim == 64 || head_dim == 128) && kv_len >= 0);
+    QL_CHECK_ARG(valid_hd(head_dim) && kv_len >= 0);
+    *bytes = 0;
+    if (!mfma_hd(head_dim)) return hipSuccess;   // attn_small: one pass, no workspace
     const int n_split = dec_splits(1, n_kv_heads, dec_col_chunks(n_heads, n_kv_heads), kv_len);
     *bytes = dec_ws_bytes(1, n_heads, head_dim, n_split);
     return hipSuccess;
@@ -1316,14 +1490,16 @@ extern "C" hipError_t ql_decode_attention_f16(const uint16_t* q, const uint16_t*
                                               size_t workspace_bytes, hipStream_t stream) {
     QL_CHECK_ARG(kv_len >= 0 && n_heads > 0 && n_kv_heads > 0);
     QL_CHECK_ARG(n_kv_heads <= n_heads && n_heads <= 65535);
-    QL_CHECK_ARG(head_dim == 64 || head_dim == 128);
+    QL_CHECK_ARG(valid_hd(head_dim));
     QL_CHECK_ARG(kv_row_stride >= (int64_t)n_kv_heads * head_dim);
     QL_CHECK_ARG(kv_row_stride < (int64_t)1 << 24);   // as ql_attention_f16
     QL_CHECK_ARG(workspace_bytes == 0 || workspace);
     QL_CHECK_ARG(q && out && (kv_len == 0 || (k && v)));
     const int64_t qs = (int64_t)n_heads * head_dim;
-    QL_CHECK_ARG(aligned_rows(q, qs) && aligned_rows(out, qs));
-    QL_CHECK_ARG(kv_len == 0 || (aligned_rows(k, kv_row_stride) && aligned_rows(v, kv_row_stride)));
+    if (mfma_hd(head_dim)) {
+        QL_CHECK_ARG(aligned_rows(q, qs) && aligned_rows(out, qs));
+        QL_CHECK_ARG(kv_len == 0 || (aligned_rows(k, kv_row_stride) && aligned_rows(v, kv_row_stride)));
+    }
     AttnArgs a{};
     a.q = reinterpret_cast<const _Float16*>(q);
     a.out = reinterpret_cast<_Float16*>(out);
@@ -1338,6 +1514,8 @@ extern "C" hipError_t ql_decode_attention_f16(const uint16_t* q, const uint16_t*
     a.k = reinterpret_cast<const _Float16*>(k);
     a.v = reinterpret_cast<const _Float16*>(v);
     a.kv_stride = kv_row_stride;
+    a.hd = head_dim;
+    if (!mfma_hd(head_dim)) return launch_small<false>(a, 1, 1, stream);
     // as many key splits as wanted and the workspace holds (1 = no workspace used)
     int n_split = dec_splits(1, n_kv_heads, dec_col_chunks(n_heads, n_kv_heads), kv_len);
     while (n_split > 1 && dec_ws_bytes(1, n_heads, head_dim, n_split) > workspace_bytes) --n_split;
@@ -1353,17 +1531,24 @@ constexpr int kScratchMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_addr[kScratchMaxDevices] = {};
 
-// Device address of `scratch` on the current device, looked up on the first
-// call per device (with that device current) and kept for the process.
-hipError_t decode_scratch(void** addr) {
+// Device address of `scratch` on the device of `stream` (the current device
+// for the null stream), where the kernels reading it run: looked up on the
+// first call per device, with that device made current for the lookup, and
+// kept for the process.
+hipError_t decode_scratch(hipStream_t stream, void** addr) {
     int dev = -1;
-    const hipError_t e = hipGetDevice(&dev);
+    const hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
     if (e != hipSuccess) return e;
     if (dev < 0 || dev >= kScratchMaxDevices) return hipErrorInvalidDevice;
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (!g_scratch_addr[dev]) {
+        int cur = -1;
+        hipError_t r = hipGetDevice(&cur);
+        if (r != hipSuccess) return r;
+        if (cur != dev && (r = hipSetDevice(dev)) != hipSuccess) return r;
         void* p = nullptr;
-        const hipError_t r = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        r = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (cur != dev) (void)hipSetDevice(cur);
         if (r != hipSuccess) return r;
         if (!p) return hipErrorInvalidSymbol;
         g_scratch_addr[dev] = p;
@@ -1383,7 +1568,7 @@ hipError_t paged_decode(
     size_t workspace_bytes, bool from_scratch, hipStream_t stream) {
     QL_CHECK_ARG(n_seqs >= 0 && n_seqs <= 65535 && max_ctx_len >= 0);
     QL_CHECK_ARG(n_heads > 0 && n_kv_heads > 0 && n_kv_heads <= n_heads && n_heads <= 65535);
-    QL_CHECK_ARG(head_dim == 64 || head_dim == 128);
+    QL_CHECK_ARG(valid_hd(head_dim));
     QL_CHECK_ARG(n_layers > 0 && layer >= 0 && layer < n_layers);
     QL_CHECK_ARG(max_blocks_per_seq >= 0 && max_blocks_per_seq <= (INT32_MAX / QL_PAGE_SIZE));
     QL_CHECK_ARG(n_blocks >= 0);
@@ -1393,7 +1578,7 @@ hipError_t paged_decode(
     if (n_seqs == 0) return hipSuccess;
     QL_CHECK_ARG(q && out && ctx_lens);
     QL_CHECK_ARG(max_blocks_per_seq == 0 || (block_tables && k_blocks && v_blocks));
-    QL_CHECK_ARG(aligned_rows(q, q_row_stride) && aligned_rows(out, out_row_stride));
+    if (mfma_hd(head_dim)) QL_CHECK_ARG(aligned_rows(q, q_row_stride) && aligned_rows(out, out_row_stride));
     AttnArgs a{};
     a.q = reinterpret_cast<const _Float16*>(q);
     a.out = reinterpret_cast<_Float16*>(out);
@@ -1412,11 +1597,13 @@ hipError_t paged_decode(
     a.ctx_lens = ctx_lens;
     a.n_q_rows = n_seqs;
     a.layer = layer;
+    a.hd = head_dim;
+    if (!mfma_hd(head_dim)) return launch_small<true>(a, 1, (unsigned)n_seqs, stream);   // no split
     int n_split = dec_splits(n_seqs, n_kv_heads, dec_col_chunks(n_heads, n_kv_heads), max_ctx_len);
     if (from_scratch) {
         QL_CHECK_ARG(dec_ws_bytes(n_seqs, n_heads, head_dim, n_split) <= kDecodeScratchBytes);
         if (n_split > 1) {
-            const hipError_t e = decode_scratch(&workspace);
+            const hipError_t e = decode_scratch(stream, &workspace);
             if (e != hipSuccess) return e;
         }
     } else {

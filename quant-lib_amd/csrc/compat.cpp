@@ -11,6 +11,8 @@
 #include <string.h>
 
 #include <map>
+#include <cstdlib>
+#include <memory>
 #include <mutex>
 #include <utility>
 
@@ -107,6 +109,24 @@ void launch_flash_attention(const __half* Q, const __half* K, const __half* V, _
                             hipStream_t stream) {
     (void)ql_flash_attention_f16(bits(Q), bits(K), bits(V), bits(Out), seq_len, n_heads,
                                  n_kv_heads, head_dim, causal, stream);
+}
+
+// src/fp16_forward.cu:285-297 (argmax_kernel :259-283 on one block, then a
+// synchronous copy of the index).  The reference's block reduction merges warp
+// maxima with atomicMax on the float bits read as int, which orders negative
+// maxima backwards and lets tied warps race; ql_argmax_f32 returns the first
+// index of the true maximum.
+int fp16_greedy_sample(const float* logits, int vocab_size, hipStream_t stream) {
+    if (vocab_size <= 0) return 0;
+    int32_t* d_out = nullptr;
+    if (hipMalloc(reinterpret_cast<void**>(&d_out), sizeof(int32_t)) != hipSuccess) return -1;
+    int32_t result = -1;
+    hipError_t e = ql_argmax_f32(logits, 1, vocab_size, vocab_size, d_out, stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(&result, d_out, sizeof(result), hipMemcpyDeviceToHost, stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
+    (void)hipFree(d_out);
+    return e == hipSuccess ? (int)result : -1;
 }
 
 // src/forward.cu:128-135
@@ -347,16 +367,53 @@ QuantMatrix fp16_to_fp8(const __half* src, int rows, int cols, QuantGranularity 
 }
 
 // quantlib_fp8_gemm's workspace (split-K partials, or the dequantized weights for
-// M > 64): one buffer per (device, stream), grown on demand, so calls on
-// different streams never share one.  The lock is held until the call's kernels
-// are enqueued: a concurrent call on the same stream that grows the buffer waits
-// for the stream before freeing the old one.
+// M > 64): one buffer per (device of the stream, stream), grown on demand, so
+// calls on different streams never share one.  Each buffer has its own lock,
+// held until the call's kernels are enqueued: a concurrent call on the same
+// stream that grows the buffer waits for the stream before freeing the old one,
+// while calls on other streams go on.  g_ws_mu guards only the map, whose
+// entries are never removed before exit (so a Workspace stays where it is);
+// the buffers are freed at process exit (free_workspaces, registered with
+// atexit after the HIP runtime has loaded, so it runs before the runtime's
+// own teardown).
 struct Workspace {
+    std::mutex mu;
     void* p = nullptr;
     size_t bytes = 0;
 };
 std::mutex g_ws_mu;
-std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+std::map<std::pair<int, hipStream_t>, std::unique_ptr<Workspace>> g_ws;
+bool g_ws_atexit = false;
+
+void free_workspaces() {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    for (auto& kv : g_ws) {
+        if (kv.second->p) {
+            int cur = -1;
+            if (hipGetDevice(&cur) == hipSuccess && cur != kv.first.first) (void)hipSetDevice(kv.first.first);
+            (void)hipFree(kv.second->p);
+            if (cur >= 0 && cur != kv.first.first) (void)hipSetDevice(cur);
+            kv.second->p = nullptr;
+            kv.second->bytes = 0;
+        }
+    }
+}
+
+// The device a stream belongs to (the current device for the null stream).
+hipError_t stream_device(hipStream_t stream, int* dev) {
+    if (stream == nullptr) return hipGetDevice(dev);
+    return hipStreamGetDevice(stream, dev);
+}
+
+Workspace* workspace_for(int dev, hipStream_t stream) {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    if (!g_ws_atexit) {
+        g_ws_atexit = std::atexit(free_workspaces) == 0;
+    }
+    std::unique_ptr<Workspace>& w = g_ws[std::make_pair(dev, stream)];
+    if (!w) w.reset(new Workspace);
+    return w.get();
+}
 
 }  // namespace
 
@@ -387,29 +444,40 @@ extern "C" void quantlib_fp8_gemm(const __half* A, const QuantMatrix* W, __half*
     if (ql_fp8_gemm_workspace_size(M, N, K, (int)W->params.granularity, W->params.group_size, &need) !=
         hipSuccess)
         return;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return;
-    std::lock_guard<std::mutex> lock(g_ws_mu);
-    if (need > 0) {
-        Workspace& slot = g_ws[std::make_pair(dev, stream)];
-        if (slot.bytes < need) {
-            if (slot.p) {
-                (void)hipStreamSynchronize(stream);   // earlier calls on this stream still use it
-                (void)hipFree(slot.p);
-            }
-            if (hipMalloc(&slot.p, need) != hipSuccess) {
-                slot.p = nullptr;
-                slot.bytes = 0;
-                return;
-            }
-            slot.bytes = need;
-        }
-        ws = slot.p;
-        ws_bytes = slot.bytes;
+    auto run = [&]() {
+        (void)ql_fp8_gemm_f16(bits(A), static_cast<const uint8_t*>(W->data), W->params.scales, M, N, K,
+                              fp8_format_of(W), (int)W->params.granularity, W->params.group_size,
+                              QL_FP8_MODE_REFERENCE, bits(C), ws, ws_bytes, stream);
+    };
+    if (need == 0) {   // no workspace: nothing shared, no lock
+        run();
+        return;
     }
-    (void)ql_fp8_gemm_f16(bits(A), static_cast<const uint8_t*>(W->data), W->params.scales, M, N, K,
-                          fp8_format_of(W), (int)W->params.granularity, W->params.group_size,
-                          QL_FP8_MODE_REFERENCE, bits(C), ws, ws_bytes, stream);
+    int dev = 0;
+    if (stream_device(stream, &dev) != hipSuccess) return;
+    Workspace& slot = *workspace_for(dev, stream);
+    std::lock_guard<std::mutex> lock(slot.mu);
+    if (slot.bytes < need) {
+        // allocate on the stream's device, whatever device is current
+        int cur = -1;
+        if (hipGetDevice(&cur) != hipSuccess) return;
+        if (cur != dev && hipSetDevice(dev) != hipSuccess) return;
+        if (slot.p) {
+            (void)hipStreamSynchronize(stream);   // earlier calls on this stream still use it
+            (void)hipFree(slot.p);
+        }
+        const hipError_t e = hipMalloc(&slot.p, need);
+        if (cur != dev) (void)hipSetDevice(cur);
+        if (e != hipSuccess) {
+            slot.p = nullptr;
+            slot.bytes = 0;
+            return;
+        }
+        slot.bytes = need;
+    }
+    ws = slot.p;
+    ws_bytes = slot.bytes;
+    run();
 }
 
 extern "C" void quantlib_free(QuantMatrix* qm) {

@@ -183,8 +183,9 @@ int main() {
     }
 
     // kernels/flash_attention.cu:169: causal, query 0 sees only key 0, so O[0] = V[0]
-    {
-        const int seq = 2, d = 64;
+    // (head_dim 64, the reference's tile width, and 32, which its tiles also take)
+    for (const int d : {64, 32}) {
+        const int seq = 2;
         std::vector<float> qf(seq * d), kf(seq * d), vf(seq * d);
         for (int i = 0; i < seq * d; ++i) {
             qf[i] = 0.01f * (float)(i % 7);
@@ -208,6 +209,15 @@ int main() {
         bool ok = true;
         for (int i = 0; i < d; ++i) ok = ok && of[i] == vf[i];
         expect(ok, "launch_flash_attention");
+    }
+
+    // src/fp16_forward.cu:285-297: greedy sample of fp32 logits peaking at index 777
+    {
+        const int vocab = 32000;
+        std::vector<float> lg(vocab);
+        for (int i = 0; i < vocab; ++i) lg[i] = -0.001f * (float)((i - 777) * (i - 777));
+        const int tok = fp16_greedy_sample(upload(lg), vocab, stream);
+        expect(tok == 777, "fp16_greedy_sample");
     }
 
     // quantlib_src/include/quantlib.h:10-21: E4M3 per-channel round trip of exact values

@@ -26,6 +26,7 @@ COMPAT_MANGLED = {
     "launch_fp16_to_fp32": "_Z19launch_fp16_to_fp32PK6__halfPfiP12ihipStream_t",
     "launch_fp32_to_fp16": "_Z19launch_fp32_to_fp16PKfP6__halfiP12ihipStream_t",
     "launch_flash_attention": "_Z22launch_flash_attentionPK6__halfS1_S1_PS_iiiiiP12ihipStream_t",
+    "fp16_greedy_sample": "_Z18fp16_greedy_samplePKfiP12ihipStream_t",
     "add_residual": "_Z12add_residualPfPKfiP12ihipStream_t",
     "launch_embed": "_Z12launch_embedPfPKfiiP12ihipStream_t",
     "launch_fp16_kvcache_append": "_Z26launch_fp16_kvcache_appendP6__halfS0_PKS_S2_iiiiiiP12ihipStream_t",
@@ -131,6 +132,9 @@ P = 4096  # a non-null, 16-byte aligned dummy address: never dereferenced on the
       P, P, 0, 3, 16, 2, None), 0),
     # attention: head_dim 96 unsupported, kv heads > heads, empty problem
     (("ql_flash_attention_f16", P, P, P, P, 4, 8, 2, 96, 1, None), INVALID),
+    (("ql_flash_attention_f16", P, P, P, P, 4, 8, 2, 0, 1, None), INVALID),
+    (("ql_flash_attention_f16", P, P, P, P, 4, 8, 2, 65, 1, None), INVALID),
+    (("ql_flash_attention_f16", P, P, P, P, 4, 8, 2, 129, 1, None), INVALID),
     (("ql_flash_attention_f16", P, P, P, P, 4, 2, 8, 64, 1, None), INVALID),
     (("ql_flash_attention_f16", None, None, None, None, 0, 8, 2, 64, 1, None), 0),
     # q stride too small, stride not a multiple of 8, misaligned base, missing K
@@ -206,6 +210,14 @@ def test_contiguous_decode_workspace_size_host_query():
         assert ql.raw("ql_decode_attention_workspace_size", h, hkv, d, kv, ctypes.byref(size)) == 0
         assert size.value == (0 if splits == 1 else h * splits * (d + 2) * 4), (h, hkv, d, kv, size.value)
     assert ql.raw("ql_decode_attention_workspace_size", 32, 8, 96, 100, ctypes.byref(size)) == INVALID
+    # head_dims below 64 other than 64 run one pass without a workspace
+    for d in (8, 32, 48, 63):
+        size.value = 123
+        assert ql.raw("ql_decode_attention_workspace_size", 32, 8, d, 8192, ctypes.byref(size)) == 0
+        assert size.value == 0
+        size.value = 123
+        assert ql.raw("ql_paged_decode_workspace_size", 1, 32, 8, d, 8192, ctypes.byref(size)) == 0
+        assert size.value == 0
     assert ql.raw("ql_decode_attention_f16", P, P, P, P, 10, 32, 8, 128, 8 * 128 - 8, None, 0, None) == INVALID
     assert ql.raw("ql_decode_attention_f16", P, P, P, P, 10, 32, 8, 128, 8 * 128, None, 64, None) == INVALID
 

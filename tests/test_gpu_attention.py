@@ -91,6 +91,139 @@ def test_launch_flash_attention_shim_tinyllama_shape():
     check_attn(g1, orc.attention(q, k, v, h, hkv, True, f16=True), v, "launch_flash_attention")
 
 
+# ---- head_dims below 64 (the reference kernel's range; the vector-ALU kernel) ---------------
+# The reference's launch_flash_attention takes any head_dim <= 64
+# (kernels/flash_attention.cu:25-27,64-66); 64 and 128 run on the matrix cores,
+# every other value on attn_small, whose probabilities stay fp32 (tighter than
+# the bound above).  The shim and the C ABI must give the same bits.
+@pytest.mark.parametrize("seq,h,hkv,d,causal", [
+    (1, 4, 2, 32, 1), (77, 32, 4, 32, 1), (300, 8, 2, 48, 1), (129, 6, 3, 40, 0),
+    (513, 4, 4, 16, 1), (65, 2, 1, 8, 1), (100, 3, 1, 63, 0), (257, 4, 2, 1, 1), (64, 4, 1, 33, 1)])
+def test_flash_attention_small_head_dims(seq, h, hkv, d, causal):
+    f = getattr(ql.lib(), COMPAT_MANGLED["launch_flash_attention"])
+    f.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int] * 5 + [ctypes.c_void_p]
+    f.restype = None
+    q, k, v = qkv(seq * 11 + d, seq, seq, h, hkv, d)
+    dq, dk, dv = dev(q), dev(k), dev(v)
+    o1, o2 = Out(seq * h * d, np.uint16), Out(seq * h * d, np.uint16)
+    f(ptr(dq), ptr(dk), ptr(dv), o1.ptr, seq, h, hkv, d, causal, stream())
+    ql.call("ql_flash_attention_f16", ptr(dq), ptr(dk), ptr(dv), o2.ptr, seq, h, hkv, d, causal,
+            stream())
+    g1 = o1.get((seq, h, d))
+    assert np.array_equal(g1, o2.get((seq, h, d)))
+    check_attn(g1, orc.attention(q, k, v, h, hkv, bool(causal), f16=True), v,
+               f"head_dim {d} seq={seq} h={h}/{hkv}")
+
+
+def test_flash_attention_small_head_dim_reference_test_inputs():
+    # tests/test_attention.cu's srand(99) U(-0.5,0.5) inputs and 1e-3 bar at head_dim 32
+    seq, h, d = 128, 8, 32
+    q, k, v = orc.reftest_attention_inputs(seq, h, d, 99)
+    qb, kb, vb = to_f16_bits(q), to_f16_bits(k), to_f16_bits(v)
+    out = Out(seq * h * d, np.uint16)
+    dq, dk, dv = dev(qb), dev(kb), dev(vb)
+    ql.call("ql_flash_attention_f16", ptr(dq), ptr(dk), ptr(dv), out.ptr, seq, h, h, d, 0, stream())
+    got = out.get((seq, h, d))
+    err = float(np.abs(f16_bits_to_f32(got) - orc.attention_reftest_cpu(q, k, v, h)).max())
+    assert err < 1e-3, err
+
+
+@pytest.mark.parametrize("q_len,kv_len,causal", [(1, 1000, 1), (5, 77, 1), (130, 333, 0), (3, 0, 1)])
+def test_attention_small_head_dim_strided_unaligned(q_len, kv_len, causal):
+    # head_dim 40 with row strides that are not multiples of 8 elements and base
+    # pointers 2 bytes past a 16-byte boundary; out padding stays untouched
+    h, hkv, d = 6, 2, 40
+    qrow, kvrow, orow = h * d + 3, hkv * d + 5, h * d + 7
+    qbuf = to_f16_bits(normal(q_len + 5, (q_len * qrow + 1,)))
+    kbuf = to_f16_bits(normal(kv_len + 6, (max(kv_len, 1) * kvrow + 1,)))
+    vbuf = to_f16_bits(normal(kv_len + 7, (max(kv_len, 1) * kvrow + 1,)))
+    dq, dk, dv = dev(qbuf), dev(kbuf), dev(vbuf)
+    out = Out(q_len * orow + 1, np.uint16)
+    ql.call("ql_attention_f16", ptr(dq) + 2, ptr(dk) + 2, ptr(dv) + 2, out.ptr + 2, q_len, kv_len, h, hkv,
+            d, qrow, kvrow, orow, causal, stream())
+    got = out.get()
+    body = got[1:].reshape(q_len, orow)
+    assert got[0] == np.frombuffer(bytes([GUARD_BYTE] * 2), np.uint16)[0]
+    assert np.all(body[:, h * d:].view(np.uint8) == GUARD_BYTE), "padding columns written"
+    q = qbuf[1:].reshape(q_len, qrow)[:, :h * d].reshape(q_len, h, d)
+    k = kbuf[1:1 + kv_len * kvrow].reshape(kv_len, kvrow)[:, :hkv * d].reshape(kv_len, hkv, d)
+    v = vbuf[1:1 + kv_len * kvrow].reshape(kv_len, kvrow)[:, :hkv * d].reshape(kv_len, hkv, d)
+    want = orc.attention(np.ascontiguousarray(q), np.ascontiguousarray(k), np.ascontiguousarray(v), h, hkv,
+                         bool(causal), f16=True)
+    check_attn(body[:, :h * d].reshape(q_len, h, d), want, v, f"head_dim 40 q={q_len} kv={kv_len}")
+
+
+@pytest.mark.parametrize("d", [32, 48])
+def test_paged_attention_small_head_dims(d):
+    # prefill, decode and a chunk over permuted blocks with a hole in one table,
+    # through ql_paged_attention_f16, then every sequence decoding through both
+    # paged decode entry points (one pass, no workspace at these head_dims)
+    h, hkv, L, layer = 8, 2, 3, 2
+    ctx, qn = [150, 70, 33], [150, 1, 9]
+    need = [(c + 15) // 16 for c in ctx]
+    nb = sum(need) + 2
+    perm = np.random.default_rng(d).permutation(nb)
+    max_blocks = max(need) + 1
+    bt = np.full((3, max_blocks), -1, np.int32)
+    o = 0
+    for s, n in enumerate(need):
+        bt[s, :n] = perm[o:o + n]
+        o += n
+    pool = PagedPool(nb, L, hkv, d)
+    ks, vs, qs = [], [], []
+    for s, c in enumerate(ctx):
+        ks.append(to_f16_bits(normal(400 + s + d, (c, hkv, d))))
+        vs.append(to_f16_bits(normal(500 + s + d, (c, hkv, d))))
+        pool.append(bt[s], ks[s], vs[s], layer)
+        qs.append(to_f16_bits(normal(600 + s + d, (qn[s], h, d))))
+    bt[0, 3] = -1          # sequence 0: keys 48..63 read as zero rows
+    kz, vz = [k.copy() for k in ks], [v.copy() for v in vs]
+    kz[0][48:64] = 0
+    vz[0][48:64] = 0
+    cu = np.concatenate([[0], np.cumsum(qn)]).astype(np.int32)
+    rows = int(cu[-1])
+    dq, dcu, dctx, dbt = dev(np.concatenate(qs)), dev(cu), dev(np.array(ctx, np.int32)), dev(bt)
+    out = Out(rows * h * d, np.uint16)
+    ql.call("ql_paged_attention_f16", dq.ptr, out.ptr, h * d, h * d, rows, 3, dcu.ptr, dctx.ptr, max(qn),
+            dbt.ptr, max_blocks, pool.kptrs.ptr, pool.vptrs.ptr, nb, layer, L, h, hkv, d, 1, stream())
+    got = out.get((rows, h, d))
+    for s in range(3):
+        check_attn(got[cu[s]:cu[s + 1]], orc.attention(qs[s], kz[s], vz[s], h, hkv, True, f16=True), vs[s],
+                   f"paged head_dim {d} sequence {s}")
+    # decode: one query per sequence (row s), against all ctx[s] keys
+    qd = to_f16_bits(normal(700 + d, (3, h, d)))
+    dqd = dev(qd)
+    size = ctypes.c_size_t(1)
+    ql.call("ql_paged_decode_workspace_size", 3, h, hkv, d, max(ctx), ctypes.addressof(size))
+    assert size.value == 0
+    o1, o2 = Out(3 * h * d, np.uint16), Out(3 * h * d, np.uint16)
+    ql.call("ql_paged_decode_attention_f16", dqd.ptr, o1.ptr, h * d, h * d, 3, dctx.ptr, max(ctx), dbt.ptr,
+            max_blocks, pool.kptrs.ptr, pool.vptrs.ptr, nb, layer, L, h, hkv, d, None, 0, stream())
+    ql.call("ql_paged_decode_attention_f16_noalloc", dqd.ptr, o2.ptr, h * d, h * d, 3, dctx.ptr, max(ctx),
+            dbt.ptr, max_blocks, pool.kptrs.ptr, pool.vptrs.ptr, nb, layer, L, h, hkv, d, stream())
+    g1 = o1.get((3, h, d))
+    assert np.array_equal(g1, o2.get((3, h, d)))
+    for s in range(3):
+        check_attn(g1[s:s + 1], orc.attention(qd[s:s + 1], kz[s], vz[s], h, hkv, True, f16=True), vs[s],
+                   f"paged decode head_dim {d} sequence {s}")
+
+
+def test_contiguous_decode_small_head_dim():
+    # ql_decode_attention_f16 at head_dim 32 (no workspace needed) equals
+    # ql_attention_f16 with one query, and the oracle
+    h, hkv, d, kv = 16, 4, 32, 3000
+    q, k, v = qkv(31, 1, kv, h, hkv, d)
+    dq, dk, dv = dev(q), dev(k), dev(v)
+    o1, o2 = Out(h * d, np.uint16), Out(h * d, np.uint16)
+    ql.call("ql_decode_attention_f16", dq.ptr, dk.ptr, dv.ptr, o1.ptr, kv, h, hkv, d, hkv * d, None, 0,
+            stream())
+    ql.call("ql_attention_f16", dq.ptr, dk.ptr, dv.ptr, o2.ptr, 1, kv, h, hkv, d, h * d, hkv * d, h * d, 1,
+            stream())
+    g1 = o1.get((1, h, d))
+    assert np.array_equal(g1, o2.get((1, h, d)))
+    check_attn(g1, orc.attention(q, k, v, h, hkv, True, f16=True), v, "decode head_dim 32")
+
+
 # ---- decode / chunked prefill over a contiguous cache, strided rows -----------------------
 @pytest.mark.parametrize("q_len,kv_len", [(1, 1), (1, 1000), (5, 77), (130, 333), (64, 64),
                                           (3, 0)])

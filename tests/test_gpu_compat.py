@@ -374,6 +374,9 @@ def test_quantlib_fp8_gemm_shim_on_two_streams():
             got = f16_bits_to_f32(host(out, shape=(M, N)))
             assert np.all(np.abs(got - f16_bits_to_f32(want)) <= bound), M
     qfree(ctypes.byref(qm))
+    h = ql.hip()
+    h.hipStreamDestroy.argtypes, h.hipStreamDestroy.restype = [_p], ctypes.c_int
+    ql.hip_check(h.hipStreamDestroy(s2.value), "hipStreamDestroy")
 
 
 @pytest.mark.parametrize("M", [1, 100])
@@ -409,6 +412,27 @@ def test_fp32_quantized_gemm_bridge(M):
     assert np.all(np.abs(f16_bits_to_f32(c16) - f16_bits_to_f32(want)) <= bound)
     assert np.array_equal(host(c32, shape=(M, N)), f16_bits_to_f32(c16))
     qfree(ctypes.byref(qm))
+
+
+@pytest.mark.parametrize("vocab", [1, 255, 32000, 128256])
+def test_fp16_greedy_sample_shim(vocab):
+    # src/fp16_forward.cu:285-297: the index of the largest logit, as a host int.
+    # Logits come from binary16 (the engine widens them), so ties are likely at
+    # this vocab size; the first index of the maximum is the answer (the
+    # reference's own tie order depends on a race between its warps).
+    f = fn("fp16_greedy_sample", [_p, _i, _p], _i)
+    r = np.random.default_rng(vocab)
+    for trial in range(3):
+        x = f16_bits_to_f32(to_f16_bits(r.standard_normal(vocab).astype(np.float32) * 3.0))
+        if trial == 1:
+            x[r.integers(0, vocab, size=min(vocab, 4))] = x.max()   # planted ties
+        if trial == 2:
+            x = -np.abs(x) - 1.0                                    # every logit negative
+        d = dev(x.astype(np.float32))
+        got = f(d.ptr, vocab, stream())
+        assert got == int(np.argmax(x)), (vocab, trial, got, int(np.argmax(x)))
+        assert got == int(orc.argmax(x[None, :])[0])
+    assert f(None, 0, stream()) == 0   # empty scan: index 0, no launch
 
 
 def test_dropin_caller_program_runs():
