@@ -22,9 +22,10 @@ single-kernel passes of the smaller kernels rotate more: the RoPE and KV-append
 kernels over 12 sets of Q, K, V (96 MiB each), the embedding gather over 4
 tables (250 MB each) with their own ids.
 value = algorithmic bytes of the chain (each input read once, each output
-written once) / wall time per step.  128 untimed steps (~30 ms) come first, and
-every single-kernel pass starts after ~30 ms of untimed device work: the clocks
-take ~20 ms of sustained load to ramp up.
+written once) / wall time per step.  Before the timed steps, whatever --warmup
+asks, ~30 ms of copies and then >= 30 ms of chain steps run untimed (the
+clocks take ~20 ms of sustained load to ramp up), then the --warmup steps; every
+single-kernel pass starts after ~30 ms of untimed device work as well.
 
 The embedding gather and the final RMSNorm (once per forward, not per layer)
 are timed separately and reported under "kernels".  The roofline entry is for the dominant kernel,
@@ -80,6 +81,9 @@ NTABLES = 4   # embedding tables (250 MB each) rotated by the gather pass
 # cycles through (buffer sets, tables, the 32 pool layers), so no timed launch
 # is the first to touch a buffer (first touches also pay address translation)
 WARM = 32
+# untimed device work before the timed steps, whatever --warmup says: half
+# copies, half chain steps (the clocks ramp over ~20 ms of sustained load)
+CLOCK_WARMUP_MS = 60.0
 
 BYTES = {
     "add_rmsnorm_f16": 4 * T * D * 2 + 2 * D,                     # read x,d; write x',y; w
@@ -108,9 +112,8 @@ def parse():
                                  formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    # untimed steps: a kernel trace of this bench shows the step time settle
-    # (236 -> 229 us) only after ~20 ms of sustained load, as the clocks ramp
-    ap.add_argument("--warmup", type=int, default=128)
+    # untimed steps after the time-based clock warm-up (CLOCK_WARMUP_MS)
+    ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--breakdown-reps", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target CPU time of the oracle baseline sample (0 = skip)")
@@ -290,9 +293,11 @@ def warm_on(ql, stream, launch, ms=60.0):
     b.record(stream)
     ql.synchronize()
     per_ms = max(a.elapsed_ms(b), 1e-3)
-    for i in range(2, int(ms / per_ms) + 2):
+    n = int(ms / per_ms) + 2
+    for i in range(2, n):
         launch(i)
     ql.synchronize()
+    return n
 
 
 def percentiles(us):
@@ -319,6 +324,7 @@ def breakdown(chain, ql, reps):
     copy of the same size is the kernel's practical ceiling, and vs_copy =
     copy us / kernel us (1.0 = as fast as a copy of its bytes)."""
     def back_to_back(launch):
+        heat(ql, chain.stream)   # every pass starts on ramped clocks
         for i in range(WARM):
             launch(i)
         ql.synchronize()
@@ -1107,6 +1113,11 @@ def main():
         return
     chain = Chain(ql, np)
 
+    # clock warm-up by time, independent of --warmup: the clocks need ~20 ms of
+    # sustained load to ramp (a kernel trace shows the step settle from 236 to
+    # ~230 us), so ~30 ms of copies and then >= 30 ms of chain steps run first
+    heat(ql, chain.stream, CLOCK_WARMUP_MS / 2)
+    warm_steps = warm_on(ql, chain.stream, lambda i: chain.step(), CLOCK_WARMUP_MS / 2)
     for _ in range(args.warmup):
         chain.step()
     ql.synchronize()
@@ -1155,6 +1166,9 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "clock_warmup_ms": CLOCK_WARMUP_MS,
+        "clock_warmup": f"{CLOCK_WARMUP_MS / 2:.0f} ms of copies, then {warm_steps} untimed chain steps "
+                        f"(>= {CLOCK_WARMUP_MS / 2:.0f} ms), then the --warmup steps",
         "ms_per_step": round(ms_per_step, 4),
         "us_per_decoder_layer": round(ms_per_step * 1e3, 1),
         "us_per_decoder_layer_events": round(ev_ms_per_step * 1e3, 1),
