@@ -580,18 +580,61 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
     // wavefront with no queries, or whose queries all precede the tile, skips it
     auto compute = [&](const _Float16* sk, const _Float16* sv, int kv0) {
         if (!(wave_has_q && (!a.causal || kv0 <= wave_last_pos))) return;
+        // the two 32-key blocks' products in turn, each step's K fragments read
+        // ahead of its products (PF steps ahead; with them read just before, every
+        // product waited for an LDS round trip): HD 128 prefetches two steps, in an
+        // order pinned by scheduling groups (the compiler otherwise sinks the reads
+        // back); HD 64 one step, which keeps its occupancy at 3 wavefronts per SIMD.
+        // Measured on MI355X, bit-identical: C5 prefill 591 -> 580 us, 4096 tokens
+        // at HD 64 102 -> 98 us.
+        constexpr int PF = HD == 128 ? 2 : 1;
         floatx16 s[2];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            s[kb] = floatx16{};
-            const int key = kb * 32 + col;
-            const _Float16* krow = sk + key * HD;
-            const int sw = tile_swz<HD>(key);
+        const _Float16* krow0 = sk + col * HD;
+        const _Float16* krow1 = sk + (32 + col) * HD;
+        const int sw0 = tile_swz<HD>(col), sw1 = tile_swz<HD>(32 + col);
+        auto kfrag = [&](const _Float16* krow, int sw, int kk) {
+            return *reinterpret_cast<const half8*>(krow + 8 * ((2 * kk + hh) ^ sw));
+        };
+        s[0] = floatx16{};
+        s[1] = floatx16{};
+        if constexpr (PF == 1) {
+            half8 ka = kfrag(krow0, sw0, 0), kb = kfrag(krow1, sw1, 0);
 #pragma unroll
             for (int kk = 0; kk < NKK; ++kk) {
-                const half8 kf = *reinterpret_cast<const half8*>(krow + 8 * ((2 * kk + hh) ^ sw));
-                s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[kk], s[kb], 0, 0, 0);
+                half8 na{}, nb{};
+                if (kk + 1 < NKK) {
+                    na = kfrag(krow0, sw0, kk + 1);
+                    nb = kfrag(krow1, sw1, kk + 1);
+                }
+                s[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qf[kk], s[0], 0, 0, 0);
+                s[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kb, qf[kk], s[1], 0, 0, 0);
+                ka = na;
+                kb = nb;
             }
+        } else {
+            half8 ka[NKK], kb2[NKK];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int kk = 0; kk < PF; ++kk) {
+                ka[kk] = kfrag(krow0, sw0, kk);
+                kb2[kk] = kfrag(krow1, sw1, kk);
+            }
+#pragma unroll
+            for (int kk = 0; kk < NKK; ++kk) {
+                if (kk + PF < NKK) {
+                    ka[kk + PF] = kfrag(krow0, sw0, kk + PF);
+                    kb2[kk + PF] = kfrag(krow1, sw1, kk + PF);
+                }
+                s[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[kk], qf[kk], s[0], 0, 0, 0);
+                s[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kb2[kk], qf[kk], s[1], 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, 2 * PF, 0);   // DS reads of the first steps
+#pragma unroll
+            for (int kk = 0; kk < NKK; ++kk) {
+                if (kk + PF < NKK) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // DS reads
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);                       // MFMA
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
         // V^T operand: lane s16 of its 16-lane group addresses V[key r][d .. d+3] with
         // key r = 32*kb + 16*c + 4*hh + s16/4 (+8 for the upper half) and
