@@ -360,6 +360,7 @@ __device__ __forceinline__ void dequant16(uint4 codes, float inv, half8& lo, hal
 
 struct SkinnyArgs {
     const char* A;        // byte views: every offset below 2^32 (checked on the host)
+                          // (packed_a: the fragment-major copy of the token rows)
     const char* W;
     const float* scales;
     _Float16* C;
@@ -369,7 +370,37 @@ struct SkinnyArgs {
     long long gs;         // group length in elements
     int groups_per_row;   // K / gs (kScaleGroup)
     int g_step, r_step;   // 256 / gs, 256 % gs: a wavefront's next chunk starts 256 k on
+    int packed_a;         // register path: A holds the token fragments fragment-major
 };
+
+// Fragment-major token layout of the register path (more than 32 tokens): the
+// fragment of chunk c (64 k), token tile t and half h is 64 lanes x 16 bytes,
+// lane l = 16*kq + j holding A[16t + j][64c + 16kq + 8h .. +7] (zeros past the
+// last token), so each fragment load reads one contiguous 1 KiB (8 whole cache
+// lines) instead of 16 half-used lines of the row-major rows.
+constexpr uint32_t kPackFrag = 64u * 16u;   // bytes per fragment
+
+__host__ __device__ constexpr size_t packed_a_bytes(int K, int mt) {
+    return (size_t)(K / 64) * (size_t)mt * 2u * kPackFrag;
+}
+
+// One thread per 16-byte fragment slot (written in order, so the stores coalesce).
+__global__ __launch_bounds__(kBlock) void pack_tokens(const _Float16* __restrict__ A, uint4* __restrict__ P,
+                                                      int M, int K, int MT) {
+    const long long i = (long long)blockIdx.x * kBlock + threadIdx.x;
+    const long long total = (long long)(K / 64) * MT * 2 * kWave;
+    if (i >= total) return;
+    const int lane = (int)(i & (kWave - 1));
+    const long long f = i / kWave;             // (c * MT + t) * 2 + h
+    const int h = (int)(f & 1);
+    const long long ct = f >> 1;
+    const int t = (int)(ct % MT), c = (int)(ct / MT);
+    const int j = lane & 15, kq = lane >> 4;
+    const int row = 16 * t + j;
+    uint4 v = {0u, 0u, 0u, 0u};
+    if (row < M) v = *reinterpret_cast<const uint4*>(A + (size_t)row * K + 64 * c + 16 * kq + 8 * h);
+    P[i] = v;
+}
 
 template <int MT, int R>
 struct SkStage {
@@ -412,10 +443,14 @@ __device__ __forceinline__ void sk_load(SkStage<MT, R>& st, const SkinnyArgs& p,
     const uint32_t k = (uint32_t)c * 64u;
 #pragma unroll
     for (int r = 0; r < R; ++r) st.w[r] = *reinterpret_cast<const uint4*>(p.W + (woff[r] + k));
+    // row-major rows: the chunk is 128 bytes on, the second half 16; fragment-major:
+    // MT * 2 fragments on, the second half one fragment
+    const uint32_t a_c = p.packed_a ? (uint32_t)c * (uint32_t)(MT * 2) * kPackFrag : 2u * k;
+    const uint32_t a_h = p.packed_a ? kPackFrag : 16u;
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
-        st.a[t][0] = *reinterpret_cast<const half8*>(p.A + (aoff[t] + 2u * k));
-        st.a[t][1] = *reinterpret_cast<const half8*>(p.A + (aoff[t] + 2u * k + 16u));
+        st.a[t][0] = *reinterpret_cast<const half8*>(p.A + (aoff[t] + a_c));
+        st.a[t][1] = *reinterpret_cast<const half8*>(p.A + (aoff[t] + a_c + a_h));
     }
     if constexpr (SK == kScaleGroupFold || SK == kScaleGroupLds || SK == kScaleGroup) {
         const int g = min(gc.g, gc.g_last);
@@ -507,7 +542,9 @@ __global__ __launch_bounds__(kGemmWaves * kWave) void fp8_gemm_skinny(SkinnyArgs
     }
     uint32_t aoff[MT];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) aoff[t] = 2u * ((uint32_t)min(16 * t + (lane & 15), p.M - 1) * (uint32_t)p.K + 16u * kq);
+    for (int t = 0; t < MT; ++t)
+        aoff[t] = p.packed_a ? (uint32_t)(2 * t) * kPackFrag + 16u * (uint32_t)lane
+                             : 2u * ((uint32_t)min(16 * t + (lane & 15), p.M - 1) * (uint32_t)p.K + 16u * kq);
     floatx4 acc[R][MT];
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -851,6 +888,8 @@ void launch_dequantize(const uint8_t* q, const Geom& g, const float* s, _Float16
 // two at 96, four at 64.)
 constexpr int kSkinnyTargetWgs = 256;
 
+inline size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
 struct SkinnyPlan {
     int mt, r, splits, chunks_per_split;
     int rw = 0, kw = 0;   // whole-row path: row tiles per workgroup, wavefronts per row tile
@@ -1144,6 +1183,7 @@ extern "C" hipError_t ql_fp8_gemm_workspace_size(int M, int N, int K, int granul
             for (int mode : {QL_FP8_MODE_REFERENCE, QL_FP8_MODE_OCP})
                 splits = std::max(splits, (size_t)rows_plan(M, N, K, mode, SIZE_MAX).splits);
         *bytes = splits > 1 ? splits * (size_t)M * (size_t)N * sizeof(float) : 0;
+        if (pl.mt == 4) *bytes = align256(*bytes) + packed_a_bytes(K, pl.mt);   // fragment-major tokens
     } else {
         *bytes = (size_t)N * (size_t)K * sizeof(uint16_t);
     }
@@ -1169,8 +1209,27 @@ extern "C" hipError_t ql_fp8_gemm_f16(const uint16_t* A, const uint8_t* W, const
             rkind = -1;
             pl = skinny_plan(M, N, K, ws);
         }
+        // more than 32 tokens (four token tiles) on the register path: the token
+        // rows are copied fragment-major after the split partials, when the
+        // workspace holds both.  Measured on MI355X, bit-identical, weights
+        // streamed from HBM: 64 rows x gate/up (14336 x 4096) 35.4 -> 31.4 us
+        // (E4M3 groups of 128, reference codec) and 32.9 -> 28.7 us (per channel,
+        // OCP), down (4096 x 14336) 34.8 -> 33.2 and 33.1 -> 31.1 us; at 32 rows
+        // the copy's launch cost more than it saved (+3-4%).
+        const size_t part_bytes = pl.splits > 1 ? (size_t)pl.splits * (size_t)M * (size_t)N * sizeof(float) : 0;
+        const bool pack = rkind < 0 && pl.mt == 4 && ws_ok &&
+                          align256(part_bytes) + packed_a_bytes(K, pl.mt) <= workspace_bytes;
         SkinnyArgs a;
         a.A = reinterpret_cast<const char*>(A);
+        a.packed_a = 0;
+        if (pack) {
+            char* pa = static_cast<char*>(workspace) + align256(part_bytes);
+            const long long slots = (long long)(K / 64) * pl.mt * 2 * kWave;
+            hipLaunchKernelGGL(pack_tokens, dim3(qlh::blocks_for(slots, kBlock)), dim3(kBlock), 0, stream,
+                               reinterpret_cast<const _Float16*>(A), reinterpret_cast<uint4*>(pa), M, K, pl.mt);
+            a.A = pa;
+            a.packed_a = 1;
+        }
         a.W = reinterpret_cast<const char*>(W);
         a.scales = scales;
         a.C = reinterpret_cast<_Float16*>(C);

@@ -225,13 +225,18 @@ def test_contiguous_decode_workspace_size_host_query():
 def test_fp8_gemm_workspace_size_host_query():
     size = ctypes.c_size_t(123)
     q = lambda *a: ql.raw("ql_fp8_gemm_workspace_size", *a, ctypes.addressof(size))
+    # more than 32 tokens: after the split partials (256-byte aligned), the token
+    # rows fragment-major, K/64 chunks x 4 token tiles x 2 fragments of 1 KiB
+    packed = lambda K, mt: (K // 64) * mt * 2 * 1024
     # 4096 x 14336 weights: 64 row blocks of 64 rows, four K-splits of fp32 partials
-    assert q(64, 4096, 14336, 1, 0) == 0 and size.value == 4 * 64 * 4096 * 4
+    assert q(64, 4096, 14336, 1, 0) == 0 and size.value == 4 * 64 * 4096 * 4 + packed(14336, 4)
     assert q(1, 4096, 14336, 2, 128) == 0 and size.value == 4 * 1 * 4096 * 4
     assert q(16, 6144, 4096, 0, 0) == 0 and size.value == 2 * 16 * 6144 * 4      # 96 blocks: two
-    # enough row blocks (224 of 64 rows): no split, no workspace
+    # enough row blocks (224 of 64 rows): no split; packed tokens only past 32 tokens
     assert q(1, 14336, 4096, 2, 128) == 0 and size.value == 0
-    assert q(64, 14336, 4096, 0, 0) == 0 and size.value == 0
+    assert q(64, 14336, 4096, 0, 0) == 0 and size.value == packed(4096, 4)
+    assert q(33, 14336, 4096, 0, 0) == 0 and size.value == packed(4096, 4)
+    assert q(32, 14336, 4096, 0, 0) == 0 and size.value == 0
     # K too short to split (two chunks per wavefront)
     assert q(16, 1024, 512, 2, 128) == 0 and size.value == 0
     # more than 64 rows, or a shape the register path does not take: dequantized copy
