@@ -580,14 +580,16 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
     // wavefront with no queries, or whose queries all precede the tile, skips it
     auto compute = [&](const _Float16* sk, const _Float16* sv, int kv0) {
         if (!(wave_has_q && (!a.causal || kv0 <= wave_last_pos))) return;
-        // the two 32-key blocks' products in turn, each step's K fragments read
-        // ahead of its products (PF steps ahead; with them read just before, every
-        // product waited for an LDS round trip): HD 128 prefetches two steps, in an
-        // order pinned by scheduling groups (the compiler otherwise sinks the reads
-        // back); HD 64 one step, which keeps its occupancy at 3 wavefronts per SIMD.
-        // Measured on MI355X, bit-identical: C5 prefill 591 -> 580 us, 4096 tokens
-        // at HD 64 102 -> 98 us.
-        constexpr int PF = HD == 128 ? 2 : 1;
+        // Contiguous K/V: the two 32-key blocks' products in turn, each step's K
+        // fragments read ahead of its products (PF steps ahead; with them read just
+        // before, every product waited for an LDS round trip): HD 128 prefetches two
+        // steps, in an order pinned by scheduling groups (the compiler otherwise
+        // sinks the reads back); HD 64 one step, which keeps its occupancy at 3
+        // wavefronts per SIMD.  Measured on MI355X, same process, bit-identical:
+        // C5 prefill 592.7 -> 577.7 us (611.5 -> 600.8 on a slower box), 4096
+        // tokens at HD 64 101.8 -> 97.4 us.  The paged kernel measured no gain
+        // (635.9 -> 639.7 us) and keeps the plain loop (PF = 0).
+        constexpr int PF = PAGED ? 0 : (HD == 128 ? 2 : 1);
         floatx16 s[2];
         const _Float16* krow0 = sk + col * HD;
         const _Float16* krow1 = sk + (32 + col) * HD;
@@ -597,7 +599,16 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
         };
         s[0] = floatx16{};
         s[1] = floatx16{};
-        if constexpr (PF == 1) {
+        if constexpr (PF == 0) {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const _Float16* krow = kb ? krow1 : krow0;
+                const int sw = kb ? sw1 : sw0;
+#pragma unroll
+                for (int kk = 0; kk < NKK; ++kk)
+                    s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kfrag(krow, sw, kk), qf[kk], s[kb], 0, 0, 0);
+            }
+        } else if constexpr (PF == 1) {
             half8 ka = kfrag(krow0, sw0, 0), kb = kfrag(krow1, sw1, 0);
 #pragma unroll
             for (int kk = 0; kk < NKK; ++kk) {
