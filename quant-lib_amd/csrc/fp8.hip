@@ -366,7 +366,7 @@ struct SkinnyArgs {
     _Float16* C;
     float* part;          // [splits][M][N] fp32 partials (splits > 1)
     int M, N, K;
-    int chunks_per_split;
+    int chunks_per_split; // in the kernel's chunks (64 codes; 128 wide, 256 whole-row)
     long long gs;         // group length in elements
     int groups_per_row;   // K / gs (kScaleGroup)
     int g_step, r_step;   // 256 / gs, 256 % gs: a wavefront's next chunk starts 256 k on
@@ -620,6 +620,238 @@ __global__ __launch_bounds__(kGemmWaves * kWave) void fp8_gemm_skinny(SkinnyArgs
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 part[wave][16 * r + 4 * kq + i][16 * t + (lane & 15)] = kFold ? acc[r][t][i] * rs[i] : acc[r][t][i];
+    }
+    __syncthreads();
+    const int m_end = min(p.M, MC);
+    for (int e = threadIdx.x; e < NR * m_end; e += kGemmWaves * kWave) {
+        const int m = e / NR, nn = e % NR;
+        float s = part[0][nn][m];
+#pragma unroll
+        for (int w = 1; w < kGemmWaves; ++w) s += part[w][nn][m];
+        const size_t o = (size_t)m * p.N + n0 + nn;
+        if (gridDim.y == 1) p.C[o] = from_f32<_Float16>(s);
+        else p.part[(size_t)blockIdx.y * p.M * p.N + o] = s;
+    }
+}
+
+// ---- four token tiles from the fragment-major copy: whole-line weight loads ------------
+// Workgroup (4 wavefronts) = 64 weight rows x 64 tokens over one K-split's range of
+// 128-k chunks; wavefront w takes chunks w, w+4, ...  Per chunk each weight load
+// instruction covers 8 complete 128-byte row lines (lane l: row 8i + l/8, bytes
+// 16*(l%8)), so a load touches 8 lines instead of 16 half-used ones; the chunk is
+// re-laid through a wavefront-private 8 KB LDS tile (16-byte slots XOR-swizzled by
+// row, conflict-free for both the writes and the fragment reads; one wavefront's
+// LDS operations complete in order, so no barrier) into the register path's
+// fragments: for row tile r and 64-k half s, lane (j = l%16, kq = l/16) takes slot
+// 4s + kq of row 16r + j, i.e. codes 64s + 16kq .. +15 of the chunk, matching the
+// token fragments of 64-k chunk 2c + s.  Scales: per tensor / per row applied to
+// the sums (for reference-mode E5M2, per row to the weights); per group from the
+// workgroup's LDS table of inverses -- for groups of a multiple of 64 codes one
+// multiply-add per output per group-chunk on the sums of decoded codes (not
+// reference-mode E5M2), else per weight.  The fp32 summation order differs from
+// the register kernel's (another split of K over the wavefronts), not the bound.
+constexpr int kWideChunk = 128;
+constexpr int kWideStages = 2;
+constexpr int kWideTileU4 = 64 * 8;    // 16-byte slots per wavefront tile
+constexpr int kWideTableFloats = 4096;
+
+struct WideStage {
+    u32x4 w[8];
+    half8 a[2][4][2];   // 64-k half s, token tile t, fragment half h
+};
+
+// slot of (row, 16-byte column) in a wavefront tile: rows of 128 bytes, the column
+// XORed with (row ^ row/8) % 8 -- distinct over any 8 consecutive rows and over
+// the even and the odd rows of any 16
+__device__ __forceinline__ int wide_slot(int row, int col) {
+    return row * 8 + (col ^ ((row ^ (row >> 3)) & 7));
+}
+
+__device__ __forceinline__ void wide_load_w(WideStage& st, const SkinnyArgs& p, const uint32_t (&woff)[8], int c) {
+    const uint32_t kb = (uint32_t)c * kWideChunk;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) st.w[i] = *reinterpret_cast<const u32x4*>(p.W + (woff[i] + kb));
+}
+
+// chunk c is 64-k chunks 2c and 2c + 1: 16 KB of fragments from byte c * 16 KB
+__device__ __forceinline__ void wide_load_a(WideStage& st, const SkinnyArgs& p, uint32_t lane16, int c) {
+    const uint32_t base = (uint32_t)c * (2u * 4u * 2u * kPackFrag) + lane16;
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                st.a[s][t][h] = *reinterpret_cast<const half8*>(p.A + base + (uint32_t)((s * 4 + t) * 2 + h) * kPackFrag);
+}
+
+template <int FMT, int MODE, int SK>
+__global__ __launch_bounds__(kGemmWaves * kWave) void fp8_gemm_wide(SkinnyArgs p) {
+    constexpr int NR = 64, MC = 64;
+    constexpr bool kFold = fold_scale<FMT, MODE, SK>();
+    static_assert(SK == kScaleTensor || SK == kScaleRow || SK == kScaleGroupFold || SK == kScaleGroupLds,
+                  "wide kernel scale kinds");
+    const int lane = threadIdx.x & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int j = lane & 15, kq = lane >> 4;
+    const int n0 = blockIdx.x * NR;
+    const int n_chunks = p.K / kWideChunk;
+    const int c_begin = blockIdx.y * p.chunks_per_split;
+    const int c_end = min(n_chunks, c_begin + p.chunks_per_split);
+    uint32_t woff[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) woff[i] = (uint32_t)(n0 + 8 * i + (lane >> 3)) * (uint32_t)p.K + 16u * (lane & 7);
+    float inv_fixed[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        inv_fixed[r] = 1.0f;
+        if constexpr (SK <= kScaleRow && !kFold) inv_fixed[r] = 1.0f / scale_at<SK>(p, n0 + 16 * r + j, 0);
+    }
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[r][t] = floatx4{};
+
+    // LDS: the wavefront tiles and the inverse-scale table ([NR][ng], GroupLds; the
+    // host checks NR * ng <= kWideTableFloats) during the loop, then the partial tiles
+    constexpr int kTileFloats = kGemmWaves * kWideTileU4 * 4;
+    constexpr int kLoopFloats = kTileFloats + (SK >= kScaleGroupFold ? kWideTableFloats : 0);
+    constexpr int kPartFloats = kGemmWaves * NR * (MC + 1);
+    __shared__ __align__(16) float smem[kLoopFloats > kPartFloats ? kLoopFloats : kPartFloats];
+    u32x4* tile = reinterpret_cast<u32x4*>(smem) + wave * kWideTileU4;
+    const float* table = smem + kTileFloats;
+    int g0 = 0, ng = 0;
+    if constexpr (SK == kScaleGroupLds || SK == kScaleGroupFold) {
+        const int gs = (int)p.gs;
+        g0 = c_begin * kWideChunk / gs;
+        ng = (c_end * kWideChunk - 1) / gs + 1 - g0;
+        for (int i = threadIdx.x; i < NR * ng; i += kGemmWaves * kWave) {
+            int rr, gg;
+            if constexpr (SK == kScaleGroupFold) {   // group-major: a lane's 4 rows are adjacent
+                gg = i / NR;
+                rr = i - gg * NR;
+            } else {
+                rr = i / ng;
+                gg = i - rr * ng;
+            }
+            smem[kTileFloats + i] = 1.0f / p.scales[(n0 + rr) * p.groups_per_row + g0 + gg];
+        }
+        __syncthreads();
+    }
+    int wslot[8], rslot[4][2];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) wslot[i] = wide_slot(8 * i + (lane >> 3), lane & 7);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int s = 0; s < 2; ++s) rslot[r][s] = wide_slot(16 * r + j, 4 * s + kq);
+    const uint32_t lane16 = 16u * (uint32_t)lane;
+
+    auto step = [&](WideStage& st, int c, int c_next, auto load) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) tile[wslot[i]] = st.w[i];
+        if constexpr (decltype(load)::value) wide_load_w(st, p, woff, c_next);
+        // orders the compiler only: one wavefront's LDS operations execute in order
+        __builtin_amdgcn_wave_barrier();
+        u32x4 codes[4][2];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int s = 0; s < 2; ++s) codes[r][s] = tile[rslot[r][s]];
+        __builtin_amdgcn_wave_barrier();
+        if constexpr (SK == kScaleGroupFold) {
+            // the products of decoded codes per group (the chunk, or each 64-k half
+            // for groups of 64), then one multiply-add per output by the inverse
+            // scale of its weight row (lane rows 16r + 4*kq + i)
+            const bool halves = (int)p.gs % kWideChunk != 0;   // uniform
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                floatx4 part[4];
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    half8 wlo, whi;
+                    const u32x4 cv = codes[r][s];
+                    dequant16<FMT, MODE, false>(uint4{cv[0], cv[1], cv[2], cv[3]}, 1.0f, wlo, whi);
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        part[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wlo, st.a[s][t][0], s == 0 ? floatx4{} : part[t], 0, 0, 0);
+                        part[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(whi, st.a[s][t][1], part[t], 0, 0, 0);
+                    }
+                    if (s == 1 || halves) {
+                        const int g = (c * kWideChunk + 64 * s) / (int)p.gs - g0;
+                        const float4 inv = *reinterpret_cast<const float4*>(table + g * NR + 16 * r + 4 * kq);
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) {
+                            acc[r][t][0] = fmaf(part[t][0], inv.x, acc[r][t][0]);
+                            acc[r][t][1] = fmaf(part[t][1], inv.y, acc[r][t][1]);
+                            acc[r][t][2] = fmaf(part[t][2], inv.z, acc[r][t][2]);
+                            acc[r][t][3] = fmaf(part[t][3], inv.w, acc[r][t][3]);
+                            part[t] = floatx4{};
+                        }
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    // per-weight scale: the lane's row 16r + j, group of its 16 codes
+                    float inv = inv_fixed[r];
+                    if constexpr (SK == kScaleGroupLds)
+                        inv = table[(16 * r + j) * ng + (c * kWideChunk + 64 * s + 16 * kq) / (int)p.gs - g0];
+                    half8 wlo, whi;
+                    const u32x4 cv = codes[r][s];
+                    dequant16<FMT, MODE, !kFold>(uint4{cv[0], cv[1], cv[2], cv[3]}, inv, wlo, whi);
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        acc[r][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wlo, st.a[s][t][0], acc[r][t], 0, 0, 0);
+                        acc[r][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(whi, st.a[s][t][1], acc[r][t], 0, 0, 0);
+                    }
+                }
+        }
+        if constexpr (decltype(load)::value) wide_load_a(st, p, lane16, c_next);
+    };
+    // ring of NS stages: stage s holds the wavefront's chunks s, s + NS, ... (4 apart
+    // in K).  Whole rounds refill every stage (loads past the last chunk repeat it:
+    // in bounds, never used, and the waits count every round's loads exactly); the
+    // remaining chunks are computed without refills.
+    constexpr int NS = kWideStages, CS = kGemmWaves;
+    const int first = c_begin + wave;   // wave-uniform
+    if (first < c_end) {
+        const int n_mine = (c_end - 1 - first) / CS + 1;
+        const int last = first + CS * (n_mine - 1);
+        WideStage st[NS];
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            wide_load_w(st[s], p, woff, min(first + CS * s, last));
+            wide_load_a(st[s], p, lane16, min(first + CS * s, last));
+        }
+        const int rounds = n_mine / NS;
+        int c = first;
+        for (int rd = 0; rd < rounds; ++rd) {
+#pragma unroll
+            for (int s = 0; s < NS; ++s, c += CS) step(st[s], c, min(c + CS * NS, last), std::true_type{});
+        }
+#pragma unroll
+        for (int s = 0; s < NS - 1; ++s, c += CS)
+            if (s < n_mine - rounds * NS) step(st[s], c, 0, std::false_type{});
+    }
+    __syncthreads();   // the tiles' and the table's space is reused below
+    // lane holds C^T[16r + 4*(lane/16) + i][16t + lane%16]; sum the four wavefronts
+    float (*part)[NR][MC + 1] = reinterpret_cast<float (*)[NR][MC + 1]>(smem);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        float rs[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+        if constexpr (kFold) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) rs[i] = 1.0f / scale_at<SK>(p, n0 + 16 * r + 4 * kq + i, 0);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                part[wave][16 * r + 4 * kq + i][16 * t + j] = kFold ? acc[r][t][i] * rs[i] : acc[r][t][i];
     }
     __syncthreads();
     const int m_end = min(p.M, MC);
@@ -965,6 +1197,38 @@ void launch_skinny(const SkinnyArgs& a, const SkinnyPlan& pl, int kind, hipStrea
     else launch_skinny_mt<FMT, MODE, 4>(a, pl, kind, grid, st);
 }
 
+// The wide kernel's K-splits: the register plan's split count over 128-k chunks
+// (never more splits, so the workspace covers the partials); scale kinds per
+// tensor, per row and per group from the LDS table when every split's groups fit.
+// Returns the scale kind, or -1 for the register kernel.
+int wide_kind(const Geom& g, int K, const SkinnyPlan& pl, int kind, bool fold_ok, int& cps, int& splits) {
+    if (pl.mt != 4 || pl.r != 4 || K % kWideChunk) return -1;
+    if (kind != kScaleTensor && kind != kScaleRow && kind != kScaleGroupLds) return -1;
+    // groups of a multiple of 64 codes: chunk sums of decoded codes, scaled per group
+    // (not reference-mode E5M2, whose codes can decode beyond the binary16 range)
+    if (kind == kScaleGroupLds && g.gs % 64 == 0 && fold_ok) kind = kScaleGroupFold;
+    const int n = K / kWideChunk;
+    cps = (n + pl.splits - 1) / pl.splits;
+    splits = (n + cps - 1) / cps;
+    if (kind >= kScaleGroupFold)
+        for (int s = 0; s < splits; ++s) {
+            const int cb = s * cps, ce = std::min(n, cb + cps);
+            const long long ngs = (ce * (long long)kWideChunk - 1) / g.gs + 1 - cb * (long long)kWideChunk / g.gs;
+            if (64 * ngs > kWideTableFloats) return -1;
+        }
+    return kind;
+}
+
+template <int FMT, int MODE>
+void launch_wide(const SkinnyArgs& a, int kind, int splits, hipStream_t st) {
+    const dim3 grid((unsigned)(a.N / 64), (unsigned)splits), block(kGemmWaves * kWave);
+    if (kind == kScaleTensor) hipLaunchKernelGGL((fp8_gemm_wide<FMT, MODE, kScaleTensor>), grid, block, 0, st, a);
+    else if (kind == kScaleRow) hipLaunchKernelGGL((fp8_gemm_wide<FMT, MODE, kScaleRow>), grid, block, 0, st, a);
+    else if (kind == kScaleGroupLds) hipLaunchKernelGGL((fp8_gemm_wide<FMT, MODE, kScaleGroupLds>), grid, block, 0, st, a);
+    else if constexpr (!(FMT == QL_FP8_E5M2 && MODE == QL_FP8_MODE_REFERENCE))
+        hipLaunchKernelGGL((fp8_gemm_wide<FMT, MODE, kScaleGroupFold>), grid, block, 0, st, a);
+}
+
 // Whole-row path for one token tile: chunks of 256 codes, scales per tensor, per
 // row or per group of a multiple of 64 codes dividing K (the group table of a split
 // must fit LDS).  It multiplies decoded codes and scales the sums, so
@@ -1211,11 +1475,14 @@ extern "C" hipError_t ql_fp8_gemm_f16(const uint16_t* A, const uint8_t* W, const
         }
         // more than 32 tokens (four token tiles) on the register path: the token
         // rows are copied fragment-major after the split partials, when the
-        // workspace holds both.  Measured on MI355X, bit-identical, weights
-        // streamed from HBM: 64 rows x gate/up (14336 x 4096) 35.4 -> 31.4 us
-        // (E4M3 groups of 128, reference codec) and 32.9 -> 28.7 us (per channel,
-        // OCP), down (4096 x 14336) 34.8 -> 33.2 and 33.1 -> 31.1 us; at 32 rows
-        // the copy's launch cost more than it saved (+3-4%).
+        // workspace holds both, and the whole-line kernel reads them where it
+        // applies.  Measured on MI355X, weights streamed from HBM, 64 rows x
+        // gate/up (14336 x 4096) / down (4096 x 14336), us per call: register
+        // kernel on row-major tokens 35.2 / 34.9 (E4M3 groups of 128, codes
+        // checked clean) and 32.8 / 32.6 (per channel, OCP); with the copy
+        // 31.3 / 32.9 and 28.1 / 31.5; whole-line kernel 26.1 / 28.9 and
+        // 24.9 / 28.5 (the fp16 library GEMM: 26.5 / 29.7).  At 32 rows the
+        // copy's launch cost more than it saved (+3-4%).
         const size_t part_bytes = pl.splits > 1 ? (size_t)pl.splits * (size_t)M * (size_t)N * sizeof(float) : 0;
         const bool pack = rkind < 0 && pl.mt == 4 && ws_ok &&
                           align256(part_bytes) + packed_a_bytes(K, pl.mt) <= workspace_bytes;
@@ -1252,8 +1519,18 @@ extern "C" hipError_t ql_fp8_gemm_f16(const uint16_t* A, const uint8_t* W, const
                 launch_rows<QL_FP8_E5M2, QL_FP8_MODE_OCP>(a, pl, rkind, stream);
             else
                 return hipErrorInvalidValue;
-        } else
-            QL_FP8_DISPATCH(format, mode, launch_skinny, a, pl, scale_kind(g, K, pl, format, mode), stream);
+        } else {
+            const int kind = scale_kind(g, K, pl, format, mode);
+            int cps = 0, wsplits = 0;
+            const bool fold_ok = !(format == QL_FP8_E5M2 && mode == QL_FP8_MODE_REFERENCE);
+            const int wk = pack ? wide_kind(g, K, pl, kind, fold_ok, cps, wsplits) : -1;
+            if (wk >= 0) {
+                a.chunks_per_split = cps;
+                pl.splits = wsplits;
+                QL_FP8_DISPATCH(format, mode, launch_wide, a, wk, wsplits, stream);
+            } else
+                QL_FP8_DISPATCH(format, mode, launch_skinny, a, pl, kind, stream);
+        }
         if (pl.splits > 1) {
             const long long mn = (long long)M * N;
             hipLaunchKernelGGL(splitk_reduce, dim3(qlh::blocks_for(mn / 4, kBlock)), dim3(kBlock), 0, stream,
