@@ -634,7 +634,7 @@ __global__ __launch_bounds__(kGemmWaves * kWave) void fp8_gemm_skinny(SkinnyArgs
     }
 }
 
-// ---- four token tiles from the fragment-major copy: whole-line weight loads ------------
+// ---- four token tiles (33-64 tokens): whole-line loads ---------------------------------
 // Workgroup (4 wavefronts) = 64 weight rows x 64 tokens over one K-split's range of
 // 128-k chunks; wavefront w takes chunks w, w+4, ...  Per chunk each weight load
 // instruction covers 8 complete 128-byte row lines (lane l: row 8i + l/8, bytes
@@ -644,20 +644,39 @@ __global__ __launch_bounds__(kGemmWaves * kWave) void fp8_gemm_skinny(SkinnyArgs
 // LDS operations complete in order, so no barrier) into the register path's
 // fragments: for row tile r and 64-k half s, lane (j = l%16, kq = l/16) takes slot
 // 4s + kq of row 16r + j, i.e. codes 64s + 16kq .. +15 of the chunk, matching the
-// token fragments of 64-k chunk 2c + s.  Scales: per tensor / per row applied to
-// the sums (for reference-mode E5M2, per row to the weights); per group from the
-// workgroup's LDS table of inverses -- for groups of a multiple of 64 codes one
-// multiply-add per output per group-chunk on the sums of decoded codes (not
-// reference-mode E5M2), else per weight.  The fp32 summation order differs from
-// the register kernel's (another split of K over the wavefronts), not the bound.
+// token fragments of 64-k chunk 2c + s.  Tokens (TS, fixed per scale kind by
+// wide_token_stages from measurements): TS = 0 loads the fragments from the
+// fragment-major copy; TS = 1, 2 read the token rows themselves, 4 rows x 256
+// bytes per instruction, re-laid through a second wavefront tile (16 KB, column
+// XORed with row % 16) with 1 or 2 chunks of them in registers.  Scales: per
+// tensor / per row applied to the sums (for reference-mode E5M2, per row to the
+// weights); per group from the workgroup's LDS table of inverses -- for groups of
+// a multiple of 64 codes one multiply-add per output per group-chunk on the sums
+// of decoded codes (not reference-mode E5M2), else per weight.  The fp32 summation
+// order differs from the register kernel's (another split of K over the
+// wavefronts), not the bound; TS does not change it.
 constexpr int kWideChunk = 128;
 constexpr int kWideStages = 2;
-constexpr int kWideTileU4 = 64 * 8;    // 16-byte slots per wavefront tile
+constexpr int kWideTileU4 = 64 * 8;    // 16-byte slots per wavefront weight tile
+constexpr int kWideTokU4 = 64 * 16;    // 16-byte slots per wavefront token tile
 constexpr int kWideTableFloats = 4096;
 
+// token staging per (decode mode, scale kind): measured on MI355X at 48 and 64
+// tokens x 14336 x 4096 and 4096 x 14336 (us per call, copy / 1 / 2 stages):
+// per channel 25.2 / 24.7 / 23.8 and 27.5 / 26.3 / 24.9; groups of 128, OCP decode
+// 26.2 / 25.5 / 26.6 and 29.0 / 28.0 / 28.2; reference decode 28.2 / 30.5 / 37.2
+// and 30.1 / 32.0 / 36.5 (the two direct forms need more registers than that
+// instance has without spilling)
+__host__ __device__ constexpr int wide_token_stages(int mode, int sk) {
+    return sk <= kScaleRow ? 2 : (sk == kScaleGroupFold && mode == QL_FP8_MODE_OCP ? 1 : 0);
+}
+
+template <int TS>
 struct WideStage {
     u32x4 w[8];
-    half8 a[2][4][2];   // 64-k half s, token tile t, fragment half h
+    // TS 0: fragments [64-k half s][token tile t][half h]; TS 2: raw row segments
+    // (instruction i: rows 4i .. 4i+3); TS 1 keeps one set outside the ring
+    std::conditional_t<TS == 0, half8[2][4][2], std::conditional_t<TS == 2, u32x4[16], u32x4[1]>> a;
 };
 
 // slot of (row, 16-byte column) in a wavefront tile: rows of 128 bytes, the column
@@ -667,14 +686,15 @@ __device__ __forceinline__ int wide_slot(int row, int col) {
     return row * 8 + (col ^ ((row ^ (row >> 3)) & 7));
 }
 
-__device__ __forceinline__ void wide_load_w(WideStage& st, const SkinnyArgs& p, const uint32_t (&woff)[8], int c) {
+template <int TS>
+__device__ __forceinline__ void wide_load_w(WideStage<TS>& st, const SkinnyArgs& p, const uint32_t (&woff)[8], int c) {
     const uint32_t kb = (uint32_t)c * kWideChunk;
 #pragma unroll
     for (int i = 0; i < 8; ++i) st.w[i] = *reinterpret_cast<const u32x4*>(p.W + (woff[i] + kb));
 }
 
-// chunk c is 64-k chunks 2c and 2c + 1: 16 KB of fragments from byte c * 16 KB
-__device__ __forceinline__ void wide_load_a(WideStage& st, const SkinnyArgs& p, uint32_t lane16, int c) {
+// copy: chunk c is 64-k chunks 2c and 2c + 1, 16 KB of fragments from byte c * 16 KB
+__device__ __forceinline__ void wide_load_frags(half8 (&a)[2][4][2], const SkinnyArgs& p, uint32_t lane16, int c) {
     const uint32_t base = (uint32_t)c * (2u * 4u * 2u * kPackFrag) + lane16;
 #pragma unroll
     for (int s = 0; s < 2; ++s)
@@ -682,12 +702,22 @@ __device__ __forceinline__ void wide_load_a(WideStage& st, const SkinnyArgs& p, 
         for (int t = 0; t < 4; ++t)
 #pragma unroll
             for (int h = 0; h < 2; ++h)
-                st.a[s][t][h] = *reinterpret_cast<const half8*>(p.A + base + (uint32_t)((s * 4 + t) * 2 + h) * kPackFrag);
+                a[s][t][h] = *reinterpret_cast<const half8*>(p.A + base + (uint32_t)((s * 4 + t) * 2 + h) * kPackFrag);
+}
+
+// token rows: the chunk's 256 bytes of each row, lane l of instruction i reading
+// row 4i + l/16 (rows past M repeat row M - 1: in bounds, and their products only
+// reach outputs that are never written), bytes 16*(l%16) of the chunk
+__device__ __forceinline__ void wide_load_rows(u32x4 (&a)[16], const SkinnyArgs& p, const uint32_t (&aoff)[16], int c) {
+    const uint32_t kb = (uint32_t)c * (2u * kWideChunk);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) a[i] = *reinterpret_cast<const u32x4*>(p.A + (aoff[i] + kb));
 }
 
 template <int FMT, int MODE, int SK>
 __global__ __launch_bounds__(kGemmWaves * kWave) void fp8_gemm_wide(SkinnyArgs p) {
     constexpr int NR = 64, MC = 64;
+    constexpr int TS = wide_token_stages(MODE, SK);
     constexpr bool kFold = fold_scale<FMT, MODE, SK>();
     static_assert(SK == kScaleTensor || SK == kScaleRow || SK == kScaleGroupFold || SK == kScaleGroupLds,
                   "wide kernel scale kinds");
@@ -700,6 +730,10 @@ __global__ __launch_bounds__(kGemmWaves * kWave) void fp8_gemm_wide(SkinnyArgs p
     uint32_t woff[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) woff[i] = (uint32_t)(n0 + 8 * i + (lane >> 3)) * (uint32_t)p.K + 16u * (lane & 7);
+    uint32_t aoff[16];   // TS > 0: token row segments
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        aoff[i] = 2u * (uint32_t)min(4 * i + (lane >> 4), p.M - 1) * (uint32_t)p.K + 16u * (lane & 15);
     float inv_fixed[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -714,11 +748,12 @@ __global__ __launch_bounds__(kGemmWaves * kWave) void fp8_gemm_wide(SkinnyArgs p
 
     // LDS: the wavefront tiles and the inverse-scale table ([NR][ng], GroupLds; the
     // host checks NR * ng <= kWideTableFloats) during the loop, then the partial tiles
-    constexpr int kTileFloats = kGemmWaves * kWideTileU4 * 4;
+    constexpr int kTileFloats = kGemmWaves * (kWideTileU4 + (TS > 0 ? kWideTokU4 : 0)) * 4;
     constexpr int kLoopFloats = kTileFloats + (SK >= kScaleGroupFold ? kWideTableFloats : 0);
     constexpr int kPartFloats = kGemmWaves * NR * (MC + 1);
     __shared__ __align__(16) float smem[kLoopFloats > kPartFloats ? kLoopFloats : kPartFloats];
     u32x4* tile = reinterpret_cast<u32x4*>(smem) + wave * kWideTileU4;
+    u32x4* ttile = reinterpret_cast<u32x4*>(smem) + kGemmWaves * kWideTileU4 + wave * kWideTokU4;   // TS > 0
     const float* table = smem + kTileFloats;
     int g0 = 0, ng = 0;
     if constexpr (SK == kScaleGroupLds || SK == kScaleGroupFold) {
@@ -746,11 +781,28 @@ __global__ __launch_bounds__(kGemmWaves * kWave) void fp8_gemm_wide(SkinnyArgs p
 #pragma unroll
         for (int s = 0; s < 2; ++s) rslot[r][s] = wide_slot(16 * r + j, 4 * s + kq);
     const uint32_t lane16 = 16u * (uint32_t)lane;
+    // token tile: row 4i + l/16 of instruction i, 16-byte column l%16 XORed with row % 16
+    int twslot[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) twslot[i] = (4 * i + (lane >> 4)) * 16 + ((lane & 15) ^ ((4 * i + (lane >> 4)) & 15));
+    u32x4 tk[16];   // TS = 1: the next chunk's token rows
 
-    auto step = [&](WideStage& st, int c, int c_next, auto load) __attribute__((always_inline)) {
+    // one chunk from stage st; with LOAD, the stage is refilled with chunk c_next
+    // (weights and token rows as soon as they are in LDS, fragments after the
+    // products); TS = 1 refills tk with chunk c_tok
+    auto step = [&](WideStage<TS>& st, int c, int c_next, int c_tok, auto load) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) tile[wslot[i]] = st.w[i];
         if constexpr (decltype(load)::value) wide_load_w(st, p, woff, c_next);
+        if constexpr (TS == 1) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) ttile[twslot[i]] = tk[i];
+            wide_load_rows(tk, p, aoff, c_tok);
+        } else if constexpr (TS == 2) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) ttile[twslot[i]] = st.a[i];
+            if constexpr (decltype(load)::value) wide_load_rows(st.a, p, aoff, c_next);
+        }
         // orders the compiler only: one wavefront's LDS operations execute in order
         __builtin_amdgcn_wave_barrier();
         u32x4 codes[4][2];
@@ -758,7 +810,23 @@ __global__ __launch_bounds__(kGemmWaves * kWave) void fp8_gemm_wide(SkinnyArgs p
         for (int r = 0; r < 4; ++r)
 #pragma unroll
             for (int s = 0; s < 2; ++s) codes[r][s] = tile[rslot[r][s]];
+        // token fragment (s, t, h): lane (j, kq) holds k = 64s + 16kq + 8h .. +7 of
+        // token 16t + j, i.e. column 8s + 2kq + h of its row in the tile
+        half8 frag[2][4][2];
+        if constexpr (TS > 0) {
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+                        frag[s][t][h] = __builtin_bit_cast(half8, ttile[(16 * t + j) * 16 + ((8 * s + 2 * kq + h) ^ j)]);
+        }
         __builtin_amdgcn_wave_barrier();
+        auto fr = [&](int s_, int t_, int h_) __attribute__((always_inline)) -> const half8& {
+            if constexpr (TS == 0) return st.a[s_][t_][h_];
+            else return frag[s_][t_][h_];
+        };
         if constexpr (SK == kScaleGroupFold) {
             // the products of decoded codes per group (the chunk, or each 64-k half
             // for groups of 64), then one multiply-add per output by the inverse
@@ -774,8 +842,8 @@ __global__ __launch_bounds__(kGemmWaves * kWave) void fp8_gemm_wide(SkinnyArgs p
                     dequant16<FMT, MODE, false>(uint4{cv[0], cv[1], cv[2], cv[3]}, 1.0f, wlo, whi);
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
-                        part[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wlo, st.a[s][t][0], s == 0 ? floatx4{} : part[t], 0, 0, 0);
-                        part[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(whi, st.a[s][t][1], part[t], 0, 0, 0);
+                        part[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wlo, fr(s, t, 0), s == 0 ? floatx4{} : part[t], 0, 0, 0);
+                        part[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(whi, fr(s, t, 1), part[t], 0, 0, 0);
                     }
                     if (s == 1 || halves) {
                         const int g = (c * kWideChunk + 64 * s) / (int)p.gs - g0;
@@ -805,37 +873,44 @@ __global__ __launch_bounds__(kGemmWaves * kWave) void fp8_gemm_wide(SkinnyArgs p
                     dequant16<FMT, MODE, !kFold>(uint4{cv[0], cv[1], cv[2], cv[3]}, inv, wlo, whi);
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
-                        acc[r][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wlo, st.a[s][t][0], acc[r][t], 0, 0, 0);
-                        acc[r][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(whi, st.a[s][t][1], acc[r][t], 0, 0, 0);
+                        acc[r][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wlo, fr(s, t, 0), acc[r][t], 0, 0, 0);
+                        acc[r][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(whi, fr(s, t, 1), acc[r][t], 0, 0, 0);
                     }
                 }
         }
-        if constexpr (decltype(load)::value) wide_load_a(st, p, lane16, c_next);
+        if constexpr (TS == 0) {
+            if constexpr (decltype(load)::value) wide_load_frags(st.a, p, lane16, c_next);
+        }
     };
     // ring of NS stages: stage s holds the wavefront's chunks s, s + NS, ... (4 apart
     // in K).  Whole rounds refill every stage (loads past the last chunk repeat it:
     // in bounds, never used, and the waits count every round's loads exactly); the
-    // remaining chunks are computed without refills.
+    // remaining chunks are computed without refills, except TS = 1's token rows,
+    // loaded one chunk ahead in every step (the last step's repeat the last chunk).
     constexpr int NS = kWideStages, CS = kGemmWaves;
     const int first = c_begin + wave;   // wave-uniform
     if (first < c_end) {
         const int n_mine = (c_end - 1 - first) / CS + 1;
         const int last = first + CS * (n_mine - 1);
-        WideStage st[NS];
+        WideStage<TS> st[NS];
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
             wide_load_w(st[s], p, woff, min(first + CS * s, last));
-            wide_load_a(st[s], p, lane16, min(first + CS * s, last));
+            if constexpr (TS == 0) wide_load_frags(st[s].a, p, lane16, min(first + CS * s, last));
+            if constexpr (TS == 2) wide_load_rows(st[s].a, p, aoff, min(first + CS * s, last));
+            if constexpr (TS == 1)
+                if (s == 0) wide_load_rows(tk, p, aoff, first);
         }
         const int rounds = n_mine / NS;
         int c = first;
         for (int rd = 0; rd < rounds; ++rd) {
 #pragma unroll
-            for (int s = 0; s < NS; ++s, c += CS) step(st[s], c, min(c + CS * NS, last), std::true_type{});
+            for (int s = 0; s < NS; ++s, c += CS)
+                step(st[s], c, min(c + CS * NS, last), min(c + CS, last), std::true_type{});
         }
 #pragma unroll
         for (int s = 0; s < NS - 1; ++s, c += CS)
-            if (s < n_mine - rounds * NS) step(st[s], c, 0, std::false_type{});
+            if (s < n_mine - rounds * NS) step(st[s], c, 0, min(c + CS, last), std::false_type{});
     }
     __syncthreads();   // the tiles' and the table's space is reused below
     // lane holds C^T[16r + 4*(lane/16) + i][16t + lane%16]; sum the four wavefronts
@@ -1484,8 +1559,19 @@ extern "C" hipError_t ql_fp8_gemm_f16(const uint16_t* A, const uint8_t* W, const
         // 24.9 / 28.5 (the fp16 library GEMM: 26.5 / 29.7).  At 32 rows the
         // copy's launch cost more than it saved (+3-4%).
         const size_t part_bytes = pl.splits > 1 ? (size_t)pl.splits * (size_t)M * (size_t)N * sizeof(float) : 0;
-        const bool pack = rkind < 0 && pl.mt == 4 && ws_ok &&
-                          align256(part_bytes) + packed_a_bytes(K, pl.mt) <= workspace_bytes;
+        const bool pack_fits = rkind < 0 && pl.mt == 4 && ws_ok &&
+                               align256(part_bytes) + packed_a_bytes(K, pl.mt) <= workspace_bytes;
+        // the whole-line kernel where it applies, reading the token rows itself or
+        // (wide_token_stages 0) the copy; else the register kernel, on the copy when
+        // the workspace holds it
+        int kind = -1, wk = -1, cps = 0, wsplits = 0;
+        if (rkind < 0) {
+            kind = scale_kind(g, K, pl, format, mode);
+            const bool fold_ok = !(format == QL_FP8_E5M2 && mode == QL_FP8_MODE_REFERENCE);
+            wk = wide_kind(g, K, pl, kind, fold_ok, cps, wsplits);
+            if (wk >= 0 && wide_token_stages(mode, wk) == 0 && !pack_fits) wk = -1;
+        }
+        const bool pack = pack_fits && (wk < 0 || wide_token_stages(mode, wk) == 0);
         SkinnyArgs a;
         a.A = reinterpret_cast<const char*>(A);
         a.packed_a = 0;
@@ -1520,10 +1606,6 @@ extern "C" hipError_t ql_fp8_gemm_f16(const uint16_t* A, const uint8_t* W, const
             else
                 return hipErrorInvalidValue;
         } else {
-            const int kind = scale_kind(g, K, pl, format, mode);
-            int cps = 0, wsplits = 0;
-            const bool fold_ok = !(format == QL_FP8_E5M2 && mode == QL_FP8_MODE_REFERENCE);
-            const int wk = pack ? wide_kind(g, K, pl, kind, fold_ok, cps, wsplits) : -1;
             if (wk >= 0) {
                 a.chunks_per_split = cps;
                 pl.splits = wsplits;

@@ -14,7 +14,9 @@ binary16, which can move a weight by one binary16 step (2^-11 relative), or,
 for per-tensor and per-row scales and for groups of a multiple of 64,
 multiplies the fp32 sums of the exactly decoded codes by 1/scale, which skips
 the weight rounding altogether (at most 2^-11 relative from the oracle's
-rounded weights)."""
+rounded weights).  The same bound covers every launch shape (the split of K
+over wavefronts and workgroups, hence the fp32 summation order, differs
+between the whole-row, register and whole-line kernels)."""
 import ctypes
 
 import numpy as np
@@ -238,6 +240,36 @@ def test_fp8_gemm_launch_variants(mode, fmt, M, N, K, gran, gs):
     for workspace in ("query", "none"):
         got = gpu_fp8_gemm(a, q, sc, M, N, K, fmt, gran, gs, mode, workspace)
         check_gemm(got, exact, f"fp8 gemm {M}x{N}x{K} gran {gran} gs {gs} workspace {workspace}")
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("M,N,K,gran,gs", [
+    (64, 1024, 4096, ql.QUANT_PER_GROUP, 128),    # 16 row blocks, 8 K-splits, folded groups
+    (48, 512, 2048, ql.QUANT_PER_CHANNEL, 0),     # 8 row blocks, 4 K-splits
+    (40, 256, 8192, ql.QUANT_PER_GROUP, 32)])     # 16 K-splits, per-weight group scales
+def test_fp8_gemm_reused_workspace(mode, fmt, M, N, K, gran, gs):
+    """33-64 tokens with K-splits (the token copy and the fp32 partials share the
+    workspace): calls that reuse one workspace, first filled with arbitrary bytes
+    and then holding the call before's partials and copy, repeat the result bit for
+    bit (the splits are summed in split order)."""
+    a = to_f16_bits(normal(M + 3 * N + K, (M, K)))
+    w = to_f16_bits(normal(N + K + gs, (N, K), K ** -0.5))
+    q, sc = orc.fp8_quantize(w, fmt, gran, gs, mode)
+    exact = gemm_exact(a, orc.fp8_dequantize(q, sc, fmt, gran, gs, mode))
+    size = ctypes.c_size_t()
+    ql.call("ql_fp8_gemm_workspace_size", M, N, K, gran, gs, ctypes.byref(size))
+    da, dq, ds = dev(a), dev(q), dev(sc)
+    ws = dev(np.full(size.value, 0xA5, np.uint8))
+    outs = []
+    for _ in range(3):
+        out = empty((M * N,), np.uint16)
+        ql.call("ql_fp8_gemm_f16", da.ptr, dq.ptr, ds.ptr, M, N, K, fmt, gran, gs, mode, out.ptr,
+                ws.ptr, size.value, stream())
+        outs.append(host(out, shape=(M, N)).copy())
+    check_gemm(outs[0], exact, f"fp8 gemm {M}x{N}x{K} gran {gran} gs {gs}")
+    for i, o in enumerate(outs[1:], 1):
+        assert same_f16(o, outs[0]), f"call {i} differs"
 
 
 @pytest.mark.parametrize("a_scale", [1.0, 2.0 ** -12])
