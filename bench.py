@@ -903,16 +903,22 @@ def fp8_rows(ql, np, reps):
         return max(2, -(-(640 << 20) // n_bytes))
 
     def timed(launch, n):
+        # at least 30 launches per pass (a 10-launch pass moved by up to 60% between
+        # runs at 15-30 us per launch), the median of three passes
+        n = max(n, 30)
         heat(ql, st)
         for i in range(n):   # as many warm-up launches as timed ones: every rotated copy once
             launch(i)
         ql.synchronize()
-        a, b = ql.Event(), ql.Event()
-        a.record(st)
-        for i in range(n):
-            launch(i + 3)
-        b.record(st)
-        return a.elapsed_ms(b) * 1e3 / n
+        passes = []
+        for _ in range(3):
+            a, b = ql.Event(), ql.Event()
+            a.record(st)
+            for i in range(n):
+                launch(i + 3)
+            b.record(st)
+            passes.append(a.elapsed_ms(b) * 1e3 / n)
+        return sorted(passes)[1]
 
     for N, K, what in ((F, D, "gate/up 14336x4096"), (D, F, "down 4096x14336")):
         w16 = (r.standard_normal((N, K), dtype=np.float32) * np.float32(K ** -0.5)).astype(np.float16)
