@@ -1150,6 +1150,128 @@ __global__ __launch_bounds__(RW * KW * kWave) void fp8_gemm_rows(SkinnyArgs p) {
     }
 }
 
+// ---- one or two tokens: contiguous row streams -----------------------------------------
+// At most kVecMaxTokens tokens the GEMM is a stream of the weight matrix, and the
+// shape of that stream decides its speed: measured on MI355X, a wavefront
+// reading its own contiguous region 1 KiB per instruction moves a 58.7 MB matrix
+// in 10-11 us (5.3-6.0 TB/s), while row tiles read as 256-byte pieces of 16 rows
+// 4 KiB apart (the whole-row kernel's shape, every row of the matrix in flight
+// at once) take 15-18 us even with no arithmetic.  So wavefront w takes rows
+// [w*rpw, (w+1)*rpw) -- one contiguous region -- row by row: instruction j of a
+// row reads its bytes 1024j .. 1024j+1023, lane l the 16 codes at k = 1024j + 16l
+// (lanes past K load the row's first 16 bytes, to stay in bounds, and drop their
+// sums: an inf code there times a padding zero would be NaN).  Loads run
+// kVecStages instructions ahead through a register ring, unconditionally (past
+// the end they repeat the last one), each with the lane's scale.  The token rows
+// sit in LDS (zero-padded to whole instructions); each lane decodes its 16 codes
+// to binary16 pairs and multiplies them with v_dot2_f32_f16 (exact products,
+// fp32 sums), and at each row's end the 64 lane sums are added by a butterfly.
+// Scales: per tensor / per row applied to the row's sum, per group (the lane's
+// 16 codes lie in one group) to each lane's 16-code sum; reference-mode E5M2
+// scales each weight (its exponent-31 codes exceed the binary16 range).
+constexpr int kVecMaxTokens = 2;
+constexpr int kVecStages = 4;
+constexpr int kVecThreads = 512;      // 8 wavefronts per workgroup share the token rows
+constexpr int kVecTargetWaves = 2048;
+constexpr int kVecMaxTokBytes = 64 * 1024;
+
+// Sum over the wavefront: DPP adds within each row of 16 lanes (xor 1, xor 2, then
+// the mirrored quads and halves), then the four row sums read as scalars.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));  // quad_perm 1,0,3,2
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));  // quad_perm 2,3,0,1
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, true)); // row_half_mirror
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, true)); // row_mirror
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
+template <int FMT, int MODE, int SK, int M>
+__global__ __launch_bounds__(kVecThreads) void fp8_gemv(SkinnyArgs p, int rpw, int J) {
+    constexpr bool kScaled = !fold_scale<FMT, MODE, SK == kScaleGroupFold ? kScaleRow : SK>();
+    extern __shared__ __align__(16) _Float16 tok[];   // [M][J * 1024]
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * (kVecThreads / kWave) + threadIdx.x / kWave));
+    const int KP = J * 1024;   // padded row length of the token tile
+    for (int i = threadIdx.x * 8; i < M * KP; i += kVecThreads * 8) {
+        const int m = i / KP, k = i - m * KP;
+        half8 v = half8{};
+        if (k < p.K) v = *reinterpret_cast<const half8*>(reinterpret_cast<const _Float16*>(p.A) + (size_t)m * p.K + k);
+        *reinterpret_cast<half8*>(tok + i) = v;
+    }
+    __syncthreads();
+    const int r0 = wave * rpw, r1 = min(p.N, r0 + rpw);
+    if (r0 >= r1) return;   // wavefront-uniform, after the only barrier
+    const int S = (r1 - r0) * J;
+    // instruction (row, j): bytes 1024 j + 16 lane of the row; the fetch cursor runs
+    // kVecStages instructions ahead of the compute cursor and stops at the last one
+    int f_row = r0, f_j = 0, f_left = S;   // next instruction to load
+    auto fetch = [&](u32x4& v, float& sc) __attribute__((always_inline)) {
+        const int k = 1024 * f_j + 16 * lane;
+        v = *reinterpret_cast<const u32x4*>(p.W + (size_t)f_row * p.K + (k < p.K ? k : 0));
+        if constexpr (SK == kScaleTensor) sc = p.scales[0];
+        else if constexpr (SK == kScaleRow) sc = p.scales[f_row];
+        else sc = p.scales[f_row * p.groups_per_row + (int)((unsigned)min(k, p.K - 1) / (unsigned)p.gs)];
+        if (f_left > 1) {   // uniform
+            --f_left;
+            if (++f_j == J) {
+                f_j = 0;
+                ++f_row;
+            }
+        }
+    };
+    u32x4 v[kVecStages];
+    float sc[kVecStages];
+#pragma unroll
+    for (int u = 0; u < kVecStages; ++u) fetch(v[u], sc[u]);
+    float acc[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[m] = 0.0f;
+    int c_row = r0, c_j = 0;
+    for (int s0 = 0; s0 < S; s0 += kVecStages) {
+#pragma unroll
+        for (int u = 0; u < kVecStages; ++u) {
+            if (s0 + u < S) {   // uniform
+                const int k = 1024 * c_j + 16 * lane;
+                // v_rcp_f32 (1 ulp) for the per-instruction inverses
+                const float inv = kScaled || SK == kScaleGroupFold ? __builtin_amdgcn_rcpf(sc[u]) : 1.0f;
+                half8 lo, hi;
+                dequant16<FMT, MODE, kScaled>(uint4{v[u][0], v[u][1], v[u][2], v[u][3]}, inv, lo, hi);
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const half8 a0 = *reinterpret_cast<const half8*>(tok + m * KP + k);
+                    const half8 a1 = *reinterpret_cast<const half8*>(tok + m * KP + k + 8);
+                    float part = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 8; e += 2) {
+                        part = __builtin_amdgcn_fdot2(half2v{lo[e], lo[e + 1]}, half2v{a0[e], a0[e + 1]}, part, false);
+                        part = __builtin_amdgcn_fdot2(half2v{hi[e], hi[e + 1]}, half2v{a1[e], a1[e + 1]}, part, false);
+                    }
+                    part = k < p.K ? part : 0.0f;   // past K: padding zeros times codes not of this row's tail
+                    if constexpr (SK == kScaleGroupFold && !kScaled) acc[m] = fmaf(part, inv, acc[m]);
+                    else acc[m] += part;
+                }
+                if (++c_j == J) {   // the row's last instruction (uniform)
+#pragma unroll
+                    for (int m = 0; m < M; ++m) {
+                        float t = wave_sum_dpp(acc[m]);
+                        if constexpr (!kScaled && SK != kScaleGroupFold) t *= 1.0f / sc[u];
+                        if (lane == 0) p.C[(size_t)m * p.N + c_row] = from_f32<_Float16>(t);
+                        acc[m] = 0.0f;
+                    }
+                    c_j = 0;
+                    ++c_row;
+                }
+            }
+            // refill with the next instruction (the last one repeated past the end)
+            fetch(v[u], sc[u]);
+        }
+    }
+}
+
 // ---- host helpers ----------------------------------------------------------------------
 bool geom_for(int rows, int cols, int gran, int group_size, Geom& g) {
     if (rows < 0 || cols < 0) return false;
@@ -1302,6 +1424,40 @@ void launch_wide(const SkinnyArgs& a, int kind, int splits, hipStream_t st) {
     else if (kind == kScaleGroupLds) hipLaunchKernelGGL((fp8_gemm_wide<FMT, MODE, kScaleGroupLds>), grid, block, 0, st, a);
     else if constexpr (!(FMT == QL_FP8_E5M2 && MODE == QL_FP8_MODE_REFERENCE))
         hipLaunchKernelGGL((fp8_gemm_wide<FMT, MODE, kScaleGroupFold>), grid, block, 0, st, a);
+}
+
+// The contiguous-stream kernel's scale kind (kScaleGroupFold: groups folded per
+// lane, kScaleGroupLds: reference-mode E5M2 groups, scaled per weight), or -1.
+int gemv_kind(const Geom& g, int M, int K, int format, int mode, int& J) {
+    J = (K + 1023) / 1024;
+    if (M < 1 || M > kVecMaxTokens || K % 16 || (size_t)M * (size_t)J * 1024u * 2u > (size_t)kVecMaxTokBytes)
+        return -1;
+    if (g.n_groups == 1) return kScaleTensor;
+    if (g.gs == K) return kScaleRow;
+    if (K % g.gs || g.gs % 16) return -1;
+    return format == QL_FP8_E5M2 && mode == QL_FP8_MODE_REFERENCE ? kScaleGroupLds : kScaleGroupFold;
+}
+
+template <int FMT, int MODE, int SK>
+void launch_gemv_sk(const SkinnyArgs& a, int J, hipStream_t st) {
+    const int rpw = std::max(1, (a.N + kVecTargetWaves - 1) / kVecTargetWaves);
+    const int waves = (a.N + rpw - 1) / rpw;
+    const dim3 grid((unsigned)((waves + kVecThreads / kWave - 1) / (kVecThreads / kWave))), block(kVecThreads);
+    const size_t lds = (size_t)a.M * (size_t)J * 1024u * sizeof(_Float16);
+    if (a.M == 1) hipLaunchKernelGGL((fp8_gemv<FMT, MODE, SK, 1>), grid, block, lds, st, a, rpw, J);
+    else hipLaunchKernelGGL((fp8_gemv<FMT, MODE, SK, 2>), grid, block, lds, st, a, rpw, J);
+}
+
+// (gemv_kind gives groups kScaleGroupLds exactly for reference-mode E5M2, so each
+// format/mode pair instantiates one group kind)
+template <int FMT, int MODE>
+void launch_gemv(const SkinnyArgs& a, int kind, int J, hipStream_t st) {
+    if (kind == kScaleTensor) launch_gemv_sk<FMT, MODE, kScaleTensor>(a, J, st);
+    else if (kind == kScaleRow) launch_gemv_sk<FMT, MODE, kScaleRow>(a, J, st);
+    else if constexpr (FMT == QL_FP8_E5M2 && MODE == QL_FP8_MODE_REFERENCE)
+        launch_gemv_sk<FMT, MODE, kScaleGroupLds>(a, J, st);
+    else
+        launch_gemv_sk<FMT, MODE, kScaleGroupFold>(a, J, st);
 }
 
 // Whole-row path for one token tile: chunks of 256 codes, scales per tensor, per
@@ -1539,6 +1695,22 @@ extern "C" hipError_t ql_fp8_gemm_f16(const uint16_t* A, const uint8_t* W, const
     if (M == 0 || N == 0) return hipSuccess;
     QL_CHECK_ARG(A && W && scales && C && K > 0);
     mode = decode_mode(mode);
+    int gemv_j = 0;
+    const int gkind = gemv_kind(g, M, K, format, mode, gemv_j);
+    if (gkind >= 0 && qlh::aligned16(A) && qlh::aligned16(W)) {
+        SkinnyArgs a{};
+        a.A = reinterpret_cast<const char*>(A);
+        a.W = reinterpret_cast<const char*>(W);
+        a.scales = scales;
+        a.C = reinterpret_cast<_Float16*>(C);
+        a.M = M;
+        a.N = N;
+        a.K = K;
+        a.gs = g.gs;
+        a.groups_per_row = K % g.gs == 0 ? (int)(K / g.gs) : 0;
+        QL_FP8_DISPATCH(format, mode, launch_gemv, a, gkind, gemv_j, stream);
+        return hipGetLastError();
+    }
     if (skinny_ok(M, N, K, g) && qlh::aligned16(A) && qlh::aligned16(W)) {
         const bool ws_ok = workspace && qlh::aligned16(workspace) && ((uintptr_t)C & 7) == 0;
         const size_t ws = ws_ok ? workspace_bytes : 0;

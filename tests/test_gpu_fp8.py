@@ -242,6 +242,78 @@ def test_fp8_gemm_launch_variants(mode, fmt, M, N, K, gran, gs):
         check_gemm(got, exact, f"fp8 gemm {M}x{N}x{K} gran {gran} gs {gs} workspace {workspace}")
 
 
+# One or two tokens with K a multiple of 16 take the contiguous-stream kernel: each
+# wavefront walks its own run of rows, 1 KiB of a row per load instruction.  The
+# shapes cover rows per wavefront 1-3 (N up to 2048 wavefronts, then more rows
+# each), a last wavefront with fewer rows, N not a multiple of 16, rows of less
+# than one instruction and a last instruction with 1, 4 or 40 live lanes, every
+# scale kind (per tensor, per row, groups of 16, 48 and 128, which each lane's 16
+# codes never straddle), and the largest token tile (two rows of 16384 codes:
+# 64 KiB of LDS); K = 16400 at two tokens is past it and takes the other path.
+STREAM_CASES = [
+    (1, 100, 1040, ql.QUANT_PER_GROUP, 16), (2, 4100, 64, ql.QUANT_PER_CHANNEL, 0),
+    (2, 300, 1536, ql.QUANT_PER_GROUP, 48), (1, 2049, 2048, ql.QUANT_PER_TENSOR, 0),
+    (2, 64, 16384, ql.QUANT_PER_GROUP, 128), (1, 6000, 1664, ql.QUANT_PER_GROUP, 128),
+    (2, 64, 16400, ql.QUANT_PER_GROUP, 16), (1, 512, 4096, ql.QUANT_PER_CHANNEL, 0)]
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("M,N,K,gran,gs", STREAM_CASES)
+def test_fp8_gemm_stream_path(mode, fmt, M, N, K, gran, gs):
+    a = to_f16_bits(normal(2 * M + N + K, (M, K)))
+    w = to_f16_bits(normal(3 * N + K + gs, (N, K), K ** -0.5))
+    q, sc = orc.fp8_quantize(w, fmt, gran, gs, mode)
+    exact = gemm_exact(a, orc.fp8_dequantize(q, sc, fmt, gran, gs, mode))
+    # the stream kernel needs no workspace; the path past its token tile does here
+    stream_path = M * -(-K // 1024) * 2048 <= 65536
+    for workspace in ("query",) + (("none",) if stream_path else ()):
+        got = gpu_fp8_gemm(a, q, sc, M, N, K, fmt, gran, gs, mode, workspace)
+        check_gemm(got, exact, f"fp8 gemm {M}x{N}x{K} gran {gran} gs {gs} workspace {workspace}")
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("M,K", [(1, 1040), (2, 1040), (1, 64), (2, 4096)])
+def test_fp8_gemm_stream_path_nonfinite_codes(fmt, M, K):
+    """OCP inf and NaN codes in the first 16 codes of a row, the bytes that the
+    stream kernel's lanes past K load (and must not use) when K is not a multiple
+    of 1024: an infinite weight gives the same-signed infinite output, a NaN weight
+    a NaN output, and the other rows are unaffected."""
+    N = 256
+    rng = np.random.default_rng(11 + M + K + fmt)
+    codes = np.arange(256, dtype=np.uint8)
+    bad = (codes & 0x7F) == 0x7F if fmt == ql.FP8_E4M3 else (codes & 0x7C) == 0x7C
+    q = rng.choice(codes[~bad], size=(N, K)).astype(np.uint8)
+    sc = rng.uniform(2.0, 8.0, N).astype(np.float32)
+    nan_code = 0x7F if fmt == ql.FP8_E4M3 else 0x7E
+    planted = {}
+    for r in range(0, N, 7):
+        kind = r // 7 % 3
+        if fmt == ql.FP8_E4M3 and kind < 2:
+            continue                                      # E4M3 (OCP) has no infinity
+        col = int(rng.integers(0, min(K, 16)))
+        q[r, col] = (0x7C, 0xFC, nan_code)[kind]
+        planted[r] = (col, kind)
+    a = to_f16_bits(normal(M + 3, (M, K)))
+    af = f16_bits_to_f32(a)
+    for r, (col, kind) in planted.items():
+        a[:, col] = to_f16_bits(np.where(af[:, col] < 0, -1.0, 1.0).astype(np.float32))
+    w_deq = orc.fp8_dequantize(q, sc, fmt, ql.QUANT_PER_CHANNEL, 0, ql.FP8_MODE_OCP)
+    af, wf = f16_bits_to_f32(a).astype(np.float64), f16_bits_to_f32(w_deq).astype(np.float64)
+    with np.errstate(invalid="ignore", over="ignore"):
+        s = af @ wf.T
+    got = f16_bits_to_f32(gpu_fp8_gemm(a, q, sc, M, N, K, fmt, ql.QUANT_PER_CHANNEL, 0, ql.FP8_MODE_OCP,
+                                       "query")).astype(np.float64)
+    rows = np.array(sorted(planted))
+    assert not np.isfinite(s[:, rows]).any()
+    np.testing.assert_array_equal(np.isnan(got[:, rows]), np.isnan(s[:, rows]))
+    fin = ~np.isnan(s[:, rows])
+    np.testing.assert_array_equal(got[:, rows][fin], s[:, rows][fin])
+    rest = np.setdiff1d(np.arange(N), rows)
+    sub = gemm_exact(a, w_deq[rest])
+    check_gemm(to_f16_bits(got[:, rest].astype(np.float32)), sub, f"fp8 gemm {M}x{N}x{K} unplanted rows")
+
+
 @pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("M,N,K,gran,gs", [
