@@ -193,17 +193,11 @@ struct PagePipe {
     }
 };
 
-// A zero held in a vector register that the compiler cannot see through.  A
-// load whose address is uniform over the wavefront has its result moved to
-// scalar registers right after it is issued, which waits for that load and for
-// every load issued before it; offset by this zero, the lookups below keep
-// their results in vector registers until bases() moves them, after the tile's
-// products.
-__device__ __forceinline__ int divergent_zero() {
-    int z;
-    asm("v_mov_b32 %0, 0" : "=v"(z));
-    return z;
-}
+// The page lookups below are offset by divergent_zero(): a load whose address
+// is uniform over the wavefront has its result moved to scalar registers right
+// after it is issued, which waits for that load and for every load issued
+// before it; offset by the zero, the lookups keep their results in vector
+// registers until bases() moves them, after the tile's products.
 
 // Lookup of the base of this wavefront's page of a prefill tile: (1) the table
 // entry, (2) the two block pointers, (3) the head offset; each stage's result is

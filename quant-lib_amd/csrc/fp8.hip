@@ -1196,24 +1196,19 @@ __global__ __launch_bounds__(kVecThreads) void fp8_gemv(SkinnyArgs p, int rpw, i
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * (kVecThreads / kWave) + threadIdx.x / kWave));
     const int KP = J * 1024;   // padded row length of the token tile
-    for (int i = threadIdx.x * 8; i < M * KP; i += kVecThreads * 8) {
-        const int m = i / KP, k = i - m * KP;
-        half8 v = half8{};
-        if (k < p.K) v = *reinterpret_cast<const half8*>(reinterpret_cast<const _Float16*>(p.A) + (size_t)m * p.K + k);
-        *reinterpret_cast<half8*>(tok + i) = v;
-    }
-    __syncthreads();
     const int r0 = wave * rpw, r1 = min(p.N, r0 + rpw);
-    if (r0 >= r1) return;   // wavefront-uniform, after the only barrier
     const int S = (r1 - r0) * J;
     // instruction (row, j): bytes 1024 j + 16 lane of the row; the fetch cursor runs
     // kVecStages instructions ahead of the compute cursor and stops at the last one
-    int f_row = r0, f_j = 0, f_left = S;   // next instruction to load
+    // (wavefronts past the last row load row N-1's first instruction, unused)
+    int f_row = min(r0, p.N - 1), f_j = 0, f_left = S;   // next instruction to load
     auto fetch = [&](u32x4& v, float& sc) __attribute__((always_inline)) {
         const int k = 1024 * f_j + 16 * lane;
         v = *reinterpret_cast<const u32x4*>(p.W + (size_t)f_row * p.K + (k < p.K ? k : 0));
-        if constexpr (SK == kScaleTensor) sc = p.scales[0];
-        else if constexpr (SK == kScaleRow) sc = p.scales[f_row];
+        // vector loads (divergent_zero): as scalar loads, the wait for each
+        // instruction's LDS token reads would wait for them too
+        if constexpr (SK == kScaleTensor) sc = p.scales[divergent_zero()];
+        else if constexpr (SK == kScaleRow) sc = p.scales[f_row + divergent_zero()];
         else sc = p.scales[f_row * p.groups_per_row + (int)((unsigned)min(k, p.K - 1) / (unsigned)p.gs)];
         if (f_left > 1) {   // uniform
             --f_left;
@@ -1223,10 +1218,33 @@ __global__ __launch_bounds__(kVecThreads) void fp8_gemv(SkinnyArgs p, int rpw, i
             }
         }
     };
+    // token rows: loads issued first, then the wavefront's first weight loads (they
+    // do not depend on the tokens), then the LDS stores; the barrier waits for the
+    // LDS stores only, so the weight loads stay in flight across it
+    constexpr int kTokIters = kVecMaxTokBytes / (kVecThreads * 16);
+    half8 tv[kTokIters];
+#pragma unroll
+    for (int it = 0; it < kTokIters; ++it) {
+        const int i = (it * kVecThreads + (int)threadIdx.x) * 8;
+        const int m = i / KP, k = i - m * KP;
+        const bool ok = i < M * KP && k < p.K;
+        tv[it] = *reinterpret_cast<const half8*>(reinterpret_cast<const _Float16*>(p.A) +
+                                                 (ok ? (size_t)m * p.K + k : 0));
+        tv[it] = ok ? tv[it] : half8{};
+    }
     u32x4 v[kVecStages];
     float sc[kVecStages];
 #pragma unroll
     for (int u = 0; u < kVecStages; ++u) fetch(v[u], sc[u]);
+#pragma unroll
+    for (int it = 0; it < kTokIters; ++it) {
+        const int i = (it * kVecThreads + (int)threadIdx.x) * 8;
+        if (i < M * KP) *reinterpret_cast<half8*>(tok + i) = tv[it];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    if (r0 >= r1) return;   // wavefront-uniform, after the only barrier
     float acc[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[m] = 0.0f;

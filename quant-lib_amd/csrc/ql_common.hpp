@@ -90,6 +90,18 @@ __device__ __forceinline__ T ld_scalar(const T* p) {
     return *reinterpret_cast<const __attribute__((address_space(4))) T*>(reinterpret_cast<uintptr_t>(p));
 }
 
+// A zero held in a vector register that the compiler cannot see through.  A
+// load whose address is uniform over the wavefront becomes a scalar load (or has
+// its result moved to scalar registers right after it is issued); scalar loads
+// share their wait counter with LDS accesses, so every wait for an LDS read would
+// also wait for them.  Offset by this zero, the load stays a vector load on the
+// vector memory counter.
+__device__ __forceinline__ int divergent_zero() {
+    int z;
+    asm("v_mov_b32 %0, 0" : "=v"(z));
+    return z;
+}
+
 // A pointer that is the same in every lane of the wavefront, made scalar.
 template <typename T>
 __device__ __forceinline__ T* uniform(T* p) {

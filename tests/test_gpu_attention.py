@@ -153,7 +153,7 @@ def test_attention_small_head_dim_strided_unaligned(q_len, kv_len, causal):
     check_attn(body[:, :h * d].reshape(q_len, h, d), want, v, f"head_dim 40 q={q_len} kv={kv_len}")
 
 
-@pytest.mark.parametrize("d", [32, 48])
+@pytest.mark.parametrize("d", [16, 32, 48])
 def test_paged_attention_small_head_dims(d):
     # prefill, decode and a chunk over permuted blocks with a hole in one table,
     # through ql_paged_attention_f16, then every sequence decoding through both

@@ -207,6 +207,8 @@ def test_fp8_gemm_matches_oracle(mode, fmt, M, N, K, gran, gs):
 #   table of groups of 32, groups of 48 that do not divide K (general index),
 #   and groups of 16 over K = 8192, whose table only fits LDS once K is split
 #   (the "none" workspace run keeps it whole);
+#   (with four token tiles and four row tiles the whole-line kernel takes K a
+#   multiple of 128, so the register kernel's cases there use K = 320);
 # - whole-row path (at most 8 tokens, K a multiple of 256): row tiles x
 #   wavefronts per tile (4,1) (2,1) (1,1) at K = 256, (2,2) (1,2) at K = 1024,
 #   (1,4) at 2048 and (1,8) at 4096, each per tensor, per row and with folded
@@ -226,6 +228,11 @@ def _plan_cases():
         for tag, gran, gs in (("tensor", ql.QUANT_PER_TENSOR, 0), ("row", ql.QUANT_PER_CHANNEL, 0),
                               ("fold64", ql.QUANT_PER_GROUP, 64)):
             cases.append(pytest.param(3, N, K, gran, gs, id=f"rows-rw{rw}-kw{kw}-{tag}"))
+    # four token tiles and four row tiles with K not a multiple of 128: the
+    # whole-line kernel does not apply, so per-tensor and per-row scales stay on
+    # the register kernel
+    for tag, gran in (("tensor", ql.QUANT_PER_TENSOR), ("row", ql.QUANT_PER_CHANNEL)):
+        cases.append(pytest.param(48, 128, 320, gran, 0, id=f"regs-mt4-r4-{tag}-k320"))
     return cases
 
 
