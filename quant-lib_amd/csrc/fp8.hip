@@ -1156,8 +1156,8 @@ __global__ __launch_bounds__(RW * KW * kWave) void fp8_gemm_rows(SkinnyArgs p) {
 // reading its own contiguous region 1 KiB per instruction moves a 58.7 MB matrix
 // in 10-11 us (5.3-6.0 TB/s), while row tiles read as 256-byte pieces of 16 rows
 // 4 KiB apart (the whole-row kernel's shape, every row of the matrix in flight
-// at once) take 15-18 us even with no arithmetic.  So wavefront w takes rows
-// [w*rpw, (w+1)*rpw) -- one contiguous region -- row by row: instruction j of a
+// at once) take 15-18 us even with no arithmetic.  So wavefront w of W takes rows
+// [w*N/W, (w+1)*N/W) -- one contiguous region -- row by row: instruction j of a
 // row reads its bytes 1024j .. 1024j+1023, lane l the 16 codes at k = 1024j + 16l
 // (lanes past K load the row's first 16 bytes, to stay in bounds, and drop their
 // sums: an inf code there times a padding zero would be NaN).  Loads run
@@ -1190,13 +1190,16 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
 }
 
 template <int FMT, int MODE, int SK, int M>
-__global__ __launch_bounds__(kVecThreads) void fp8_gemv(SkinnyArgs p, int rpw, int J) {
+__global__ __launch_bounds__(kVecThreads) void fp8_gemv(SkinnyArgs p, int W, int J) {
     constexpr bool kScaled = !fold_scale<FMT, MODE, SK == kScaleGroupFold ? kScaleRow : SK>();
     extern __shared__ __align__(16) _Float16 tok[];   // [M][J * 1024]
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * (kVecThreads / kWave) + threadIdx.x / kWave));
     const int KP = J * 1024;   // padded row length of the token tile
-    const int r0 = wave * rpw, r1 = min(p.N, r0 + rpw);
+    // rows split evenly over the W wavefronts (W <= N); the grid's last workgroup
+    // may hold wavefronts past W, which get none
+    const int r0 = (int)min((long long)p.N, (long long)wave * p.N / W);
+    const int r1 = (int)min((long long)p.N, (long long)(wave + 1) * p.N / W);
     const int S = (r1 - r0) * J;
     // instruction (row, j): bytes 1024 j + 16 lane of the row; the fetch cursor runs
     // kVecStages instructions ahead of the compute cursor and stops at the last one
@@ -1458,12 +1461,11 @@ int gemv_kind(const Geom& g, int M, int K, int format, int mode, int& J) {
 
 template <int FMT, int MODE, int SK>
 void launch_gemv_sk(const SkinnyArgs& a, int J, hipStream_t st) {
-    const int rpw = std::max(1, (a.N + kVecTargetWaves - 1) / kVecTargetWaves);
-    const int waves = (a.N + rpw - 1) / rpw;
+    const int waves = std::min(a.N, kVecTargetWaves);
     const dim3 grid((unsigned)((waves + kVecThreads / kWave - 1) / (kVecThreads / kWave))), block(kVecThreads);
     const size_t lds = (size_t)a.M * (size_t)J * 1024u * sizeof(_Float16);
-    if (a.M == 1) hipLaunchKernelGGL((fp8_gemv<FMT, MODE, SK, 1>), grid, block, lds, st, a, rpw, J);
-    else hipLaunchKernelGGL((fp8_gemv<FMT, MODE, SK, 2>), grid, block, lds, st, a, rpw, J);
+    if (a.M == 1) hipLaunchKernelGGL((fp8_gemv<FMT, MODE, SK, 1>), grid, block, lds, st, a, waves, J);
+    else hipLaunchKernelGGL((fp8_gemv<FMT, MODE, SK, 2>), grid, block, lds, st, a, waves, J);
 }
 
 // (gemv_kind gives groups kScaleGroupLds exactly for reference-mode E5M2, so each

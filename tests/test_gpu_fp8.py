@@ -251,8 +251,8 @@ def test_fp8_gemm_launch_variants(mode, fmt, M, N, K, gran, gs):
 
 # One or two tokens with K a multiple of 16 take the contiguous-stream kernel: each
 # wavefront walks its own run of rows, 1 KiB of a row per load instruction.  The
-# shapes cover rows per wavefront 1-3 (N up to 2048 wavefronts, then more rows
-# each), a last wavefront with fewer rows, N not a multiple of 16, rows of less
+# shapes cover 1-3 rows per wavefront (N split evenly over at most 2048
+# wavefronts, so runs of two lengths), N not a multiple of 16, rows of less
 # than one instruction and a last instruction with 1, 4 or 40 live lanes, every
 # scale kind (per tensor, per row, groups of 16, 48 and 128, which each lane's 16
 # codes never straddle), and the largest token tile (two rows of 16384 codes:
