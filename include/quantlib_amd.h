@@ -495,7 +495,10 @@ hipError_t ql_fp8_dequantize(const uint8_t* src, const float* scales, int rows, 
 hipError_t ql_fp8_count_ref_special(const uint8_t* codes, size_t n, int format,
                                     unsigned long long* count, hipStream_t stream);
 /* C[M, N] = A[M, K] (dequant W[N, K])^T, fp32 accumulation, fp16 out
- * (quantlib_src/kernels/fp8_gemm.cu:34-139, quantlib_fp8_gemm).  M <= 64 with
+ * (quantlib_src/kernels/fp8_gemm.cu:34-139, quantlib_fp8_gemm).  M <= 2 with
+ * K % 16 == 0, M * ceil(K / 1024) <= 32, scales per tensor, per row or in groups of
+ * a multiple of 16 dividing K, and 16-byte aligned A and W streams W as contiguous
+ * runs of rows (no matrix cores, no workspace used).  Otherwise M <= 64 with
  * N % 16 == 0, K % 64 == 0, 16 | group length and 16-byte aligned A and W streams W
  * once and dequantizes in registers (multiplying by 1/scale); there the workspace
  * is optional and, when it holds ql_fp8_gemm_workspace_size bytes (16-byte aligned,

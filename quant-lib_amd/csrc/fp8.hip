@@ -1212,7 +1212,7 @@ __global__ __launch_bounds__(kVecThreads) void fp8_gemv(SkinnyArgs p, int W, int
         // instruction's LDS token reads would wait for them too
         if constexpr (SK == kScaleTensor) sc = p.scales[divergent_zero()];
         else if constexpr (SK == kScaleRow) sc = p.scales[f_row + divergent_zero()];
-        else sc = p.scales[f_row * p.groups_per_row + (int)((unsigned)min(k, p.K - 1) / (unsigned)p.gs)];
+        else sc = p.scales[(size_t)f_row * (size_t)p.groups_per_row + (unsigned)min(k, p.K - 1) / (unsigned)p.gs];
         if (f_left > 1) {   // uniform
             --f_left;
             if (++f_j == J) {
