@@ -25,6 +25,8 @@
 // 16-byte-per-lane span, streamed with nontemporal hints.
 #include <math.h>
 
+#include <algorithm>
+
 #include "ql_common.hpp"
 #include "quantlib_amd.h"
 
@@ -284,17 +286,22 @@ inline bool rows_aligned16(const void* p, int64_t stride_bytes) {
     return !p || (qlh::aligned16(p) && stride_bytes % 16 == 0);
 }
 
-// Plane kernel for the common head sizes (HD = 64 or 128, compile time):
-// blockIdx.y selects the plane -- Q, K or (fused variants) V -- and a group of
-// its heads, so every branch on the head type is uniform over the workgroup and
+// Plane kernel for the common head sizes (HD = 64 or 128, compile time): each
+// workgroup takes one plane -- Q, K or (fused variants) V -- and a group of its
+// heads, so every branch on the head type is uniform over the workgroup and
 // all address arithmetic is shifts.  V planes only copy into the cache and
-// skip the trig.  Groups: gq over Q, gk over K, gk over V.
+// skip the trig.  Groups: gq over Q, gk over K, gk over V.  Grid: mix == 0 puts
+// the plane groups along blockIdx.y (each plane streams its own buffer); mix > 0
+// is one row of workgroups in which every `mix` token blocks of one plane group
+// are followed by the same token blocks of the next group, so Q, K and V rows
+// that interleave in one buffer (a fused QKV projection's output) are read
+// together.
 template <typename D, int PAIRING, int HD, int MAXU, int CACHE>
 __global__ __launch_bounds__(kBlock) void rope_planes(D* q, D* k, int n_tokens, int hq, int hk,
                                                       long long qs, long long ks,
                                                       const int32_t* __restrict__ positions,
                                                       int pos_offset, InvFreq inv, int gq, int gk,
-                                                      int hpw_q, int hpw_k, KvDst<D> kv) {
+                                                      int hpw_q, int hpw_k, KvDst<D> kv, int mix) {
     constexpr int W = vec16<D>();
     constexpr bool HALF = PAIRING == QL_ROPE_HALF;
     constexpr int NP = HD / 2;                                  // pairs per head
@@ -306,12 +313,18 @@ __global__ __launch_bounds__(kBlock) void rope_planes(D* q, D* k, int n_tokens, 
     const int lane = threadIdx.x & (kWave - 1);
     // token index made scalar: its position, slot and block pointers are then
     // read with scalar loads, whose waits do not wait for the row loads
-    const int t = blockIdx.x * (kBlock / kWave) + __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
+    int tb = (int)blockIdx.x, gy = (int)blockIdx.y;   // token block, plane group
+    if (mix > 0) {
+        const int span = (gq + gk + (CACHE != kNoCache ? gk : 0)) * mix;
+        const int c = tb / span, r = tb - c * span;
+        gy = r / mix;
+        tb = c * mix + (r - gy * mix);
+    }
+    const int t = tb * (kBlock / kWave) + __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
     if (t >= n_tokens) return;  // wavefront-uniform; no barriers below
     const int j = lane % S;
 
     // plane and head range of this workgroup (uniform)
-    const int gy = blockIdx.y;
     const int plane = gy < gq ? 0 : (gy < gq + gk ? 1 : 2);    // 0 Q, 1 K, 2 V
     const int g = plane == 0 ? gy : (plane == 1 ? gy - gq : gy - gq - gk);
     const int hpw = plane == 0 ? hpw_q : hpw_k;
@@ -560,7 +573,7 @@ __global__ __launch_bounds__(kUnitBlock) void rope_units(_Float16* q, _Float16* 
 template <typename D, int PAIRING, int HD, int CACHE>
 hipError_t launch_planes(D* q, D* k, int n_tokens, int hq, int hk, long long qs, long long ks,
                          const int32_t* positions, int pos_offset, const InvFreq& inv,
-                         const KvDst<D>& kv, hipStream_t stream) {
+                         const KvDst<D>& kv, int mix, hipStream_t stream) {
     constexpr int W = vec16<D>();
     constexpr int S = (HD / 2) / (PAIRING == QL_ROPE_HALF ? W : W / 2);
     // a rotate-half slot is two 16-byte chunks, an interleaved slot one: keep
@@ -573,34 +586,60 @@ hipError_t launch_planes(D* q, D* k, int n_tokens, int hq, int hk, long long qs,
     const int gk = hk > 0 ? (hk + hpw_k - 1) / hpw_k : 0;
     const int gy = gq + gk + (CACHE != kNoCache ? gk : 0);
     const unsigned gx = qlh::blocks_for(n_tokens, kBlock / kWave);
-    hipLaunchKernelGGL((rope_planes<D, PAIRING, HD, MAXU, CACHE>), dim3(gx, gy), dim3(kBlock), 0,
-                       stream, q, k, n_tokens, hq, hk, qs, ks, positions, pos_offset, inv, gq, gk,
-                       hpw_q, hpw_k, kv);
+    dim3 grid(gx, gy);
+    if (mix > 0) {
+        const long long n = ((long long)gx + mix - 1) / mix * mix * gy;
+        QL_CHECK_ARG(n <= 0x7fffffffLL);
+        grid = dim3((unsigned)n, 1);
+    }
+    hipLaunchKernelGGL((rope_planes<D, PAIRING, HD, MAXU, CACHE>), grid, dim3(kBlock), 0, stream, q, k,
+                       n_tokens, hq, hk, qs, ks, positions, pos_offset, inv, gq, gk, hpw_q, hpw_k, kv, mix);
     return hipGetLastError();
 }
 
 template <typename D, int CACHE>
 hipError_t launch_planes_hd(int d, int pairing, D* q, D* k, int n_tokens, int hq, int hk,
                             long long qs, long long ks, const int32_t* positions, int pos_offset,
-                            const InvFreq& inv, const KvDst<D>& kv, hipStream_t stream) {
+                            const InvFreq& inv, const KvDst<D>& kv, int mix, hipStream_t stream) {
     if (d == 128) {
         if constexpr (CACHE == kNoCache && sizeof(D) == 2) {
             return hipErrorInvalidValue;   // binary16 head_dim 128 without a cache runs rope_units
         } else {
             if (pairing == QL_ROPE_HALF)
                 return launch_planes<D, QL_ROPE_HALF, 128, CACHE>(q, k, n_tokens, hq, hk, qs, ks,
-                                                                  positions, pos_offset, inv, kv,
+                                                                  positions, pos_offset, inv, kv, mix,
                                                                   stream);
             return launch_planes<D, QL_ROPE_INTERLEAVED, 128, CACHE>(q, k, n_tokens, hq, hk, qs,
                                                                      ks, positions, pos_offset,
-                                                                     inv, kv, stream);
+                                                                     inv, kv, mix, stream);
         }
     }
     if (pairing == QL_ROPE_HALF)
         return launch_planes<D, QL_ROPE_HALF, 64, CACHE>(q, k, n_tokens, hq, hk, qs, ks, positions,
-                                                         pos_offset, inv, kv, stream);
+                                                         pos_offset, inv, kv, mix, stream);
     return launch_planes<D, QL_ROPE_INTERLEAVED, 64, CACHE>(q, k, n_tokens, hq, hk, qs, ks,
-                                                            positions, pos_offset, inv, kv, stream);
+                                                            positions, pos_offset, inv, kv, mix, stream);
+}
+
+// Token blocks per plane group of the plane kernel's interleaved grid (mix > 0),
+// used when the Q, K (and V) rows interleave in one buffer: equal row strides and
+// every plane's first row inside one row's span, as in a fused QKV projection's
+// output.  Measured on MI355X, fused RoPE + paged append at 8192 tokens, Q 32 and
+// K 8 heads of 128 in 12 KiB QKV rows: planes along y 43.1 us, interleaved every
+// 1 / 4 / 16 token blocks 39.0 / 38.2 / 37.8 us; on separate Q, K, V buffers the
+// planes along y stay faster (36.0 against 36.7-37.6 us).  Bit-identical either way.
+constexpr int kRopeMixBlocks = 16;
+
+template <typename D>
+int rope_mix(const D* q, const D* k, const D* v, long long qs, long long ks, long long vs) {
+    if (!q || !k || qs != ks || (v && vs != qs)) return 0;
+    uintptr_t lo = reinterpret_cast<uintptr_t>(q), hi = lo;
+    for (const D* p : {k, v}) {
+        if (!p) continue;
+        lo = std::min(lo, reinterpret_cast<uintptr_t>(p));
+        hi = std::max(hi, reinterpret_cast<uintptr_t>(p));
+    }
+    return hi - lo < (uintptr_t)qs * sizeof(D) ? kRopeMixBlocks : 0;
 }
 
 constexpr int kRopeMaxU = 4;        // chunks (or chunk pairs) per lane
@@ -656,9 +695,12 @@ hipError_t rope_dispatch(D* q, D* k, int n_tokens, int hq, int hk, int d, int64_
                 return hipGetLastError();
             }
         }
-        if (d == 64 || d == 128)
+        if (d == 64 || d == 128) {
+            const int mix = rope_mix<D>(hq ? q : nullptr, hk ? k : nullptr, CACHE != kNoCache ? kv.v : nullptr,
+                                        (long long)qs, (long long)ks, kv.vs);
             return launch_planes_hd<D, CACHE>(d, pairing, q, k, n_tokens, hq, hk, (long long)qs,
-                                              (long long)ks, positions, pos_offset, inv, kv, stream);
+                                              (long long)ks, positions, pos_offset, inv, kv, mix, stream);
+        }
         // Heads per wavefront: at most 64*kRopeMaxU chunks per wavefront, and
         // split further while tokens alone give fewer than kRopeTargetWaves.
         const int htot = hq + hk + (CACHE != kNoCache ? hk : 0);

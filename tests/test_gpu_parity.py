@@ -682,6 +682,78 @@ def test_rope_q_paged_kv_append_leaves_k(pairing, T, H, HK, d, misalign):
     check_f16(k1, orc.rope(k, HK, d, theta, pairing, f16=True), "fused rope k")
 
 
+# Q, K and V rows that interleave in one buffer (a fused QKV projection's output)
+# run the plane kernel on an interleaved grid (every 16 token blocks of one plane
+# group, then the same blocks of the next group); separate buffers keep the planes
+# along the grid's y.  Both mappings must give the same bits: each case runs the
+# entry point on views of one fused [T, (H + 2*HK)*d] buffer and on contiguous
+# copies of the three planes, then checks the fused result against the oracle.
+# T covers a partial last token block and a partial last group of 16 blocks.
+@pytest.mark.parametrize("pairing", [ql.ROPE_HALF, ql.ROPE_INTERLEAVED])
+@pytest.mark.parametrize("entry,T,H,HK,d", [
+    ("paged", 8192, 32, 8, 128), ("paged", 77, 4, 2, 64), ("paged", 300, 8, 2, 128), ("paged", 1, 4, 1, 128),
+    ("paged_q", 301, 8, 2, 128), ("paged_q", 65, 6, 2, 64),
+    ("f32", 300, 8, 2, 128), ("f32", 77, 5, 5, 64), ("f16", 130, 8, 4, 64)])
+def test_rope_on_fused_qkv_rows_matches_separate_buffers(entry, pairing, T, H, HK, d):
+    L, layer, theta = 3, 1, 5e5
+    row = (H + 2 * HK) * d
+    f16 = entry != "f32"
+    qkv = normal(T + d + H, (T, row))
+    if f16:
+        qkv = _f16(qkv)
+    dt = np.uint16 if f16 else np.float32
+    esz = np.dtype(dt).itemsize
+    planes = [np.ascontiguousarray(qkv[:, a:b]) for a, b in ((0, H * d), (H * d, (H + HK) * d), ((H + HK) * d, row))]
+    nb = (T + 15) // 16 + 1
+    blk = L * 16 * HK * d
+    slots = np.array([(nb - 1 - t // 16) * 16 + t % 16 for t in range(T)], np.int32)
+    dsl = dev(slots)
+    outs = []
+    for fused in (True, False):
+        if fused:
+            base = dev(qkv)
+            qp, kp, vp = base.ptr, base.ptr + H * d * esz, base.ptr + (H + HK) * d * esz
+            qs = ks = vs = row
+        else:
+            bufs = [dev(x) for x in planes]
+            qp, kp, vp = (b.ptr for b in bufs)
+            qs, ks, vs = H * d, HK * d, HK * d
+        pools = []
+        if entry.startswith("paged"):
+            kpool, kb = _pool(nb, blk)
+            vpool, vb = _pool(nb, blk)
+            pools = [kpool, vpool]
+            name = "ql_rope_paged_kv_append_f16" if entry == "paged" else "ql_rope_q_paged_kv_append_f16"
+            ql.call(name, qp, kp, vp, T, H, HK, d, qs, ks, vs, None, 0, theta, pairing, kb.ptr, vb.ptr, nb,
+                    dsl.ptr, layer, L, stream())
+        else:
+            ql.call("ql_rope_f16" if f16 else "ql_rope_f32", qp, kp, T, H, HK, d, qs, ks, None, 0, theta,
+                    pairing, stream())
+        if fused:
+            got = host(base, shape=(T, row))
+            res = [got[:, :H * d], got[:, H * d:(H + HK) * d], got[:, (H + HK) * d:]]
+        else:
+            res = [host(b, shape=x.shape) for b, x in zip(bufs, planes)]
+        outs.append([np.ascontiguousarray(x) for x in res] + [host(pp) for pp in pools])
+    for i, (a, b) in enumerate(zip(*outs)):
+        assert np.array_equal(a, b), f"output {i} differs between the fused and the separate layout"
+    q_got, k_got, v_got = outs[0][:3]
+    assert np.array_equal(v_got, planes[2])   # V is read, never written
+    wq = orc.rope(planes[0], H, d, theta, pairing, f16=f16)
+    if f16:
+        check_f16(q_got, wq, "rope q on fused rows")
+    else:
+        check_abs(q_got, wq, ATOL_ROPE_F32, "rope q on fused rows")
+    if entry == "paged_q":
+        assert np.array_equal(k_got, planes[1]), "K rows must be left as read"
+    else:
+        wk = orc.rope(planes[1], HK, d, theta, pairing, f16=f16)
+        if f16:
+            check_f16(k_got, wk, "rope k on fused rows")
+        else:
+            check_abs(k_got, wk, ATOL_ROPE_F32, "rope k on fused rows")
+
+
 @pytest.mark.parametrize("f16", [True, False])
 @pytest.mark.parametrize("pairing", [ql.ROPE_HALF, ql.ROPE_INTERLEAVED])
 @pytest.mark.parametrize("T,H,HK,d", [(300, 8, 2, 128), (33, 4, 4, 64), (17, 2, 1, 6),
