@@ -59,6 +59,8 @@ _SIGS = {
     "or_fp8_quantize": ([_p, _i, _i, _i, _i, _i, _i, _p, _p], None),
     "or_fp8_dequantize": ([_p, _p, _i, _i, _i, _i, _i, _i, _p], None),
     "or_reftest_fp8_inputs": ([_p, _i64, ctypes.c_uint], None),
+    "or_reftest_gemm_inputs": ([_p, _i64, _p, _i64, ctypes.c_uint], None),
+    "or_gemm_reftest_cpu": ([_p, _p, _p, _i, _i, _i], None),
 }
 
 _lib = None
@@ -311,3 +313,21 @@ def reftest_fp8_inputs(rows: int, cols: int, seed: int = 1) -> np.ndarray:
     out = np.empty((rows, cols), np.float32)
     lib().or_reftest_fp8_inputs(_ptr(out), out.size, seed)
     return out
+
+
+def reftest_gemm_inputs(M: int, N: int, K: int, seed: int = 7):
+    """quantlib_src/tests/test_gemm.cu:38-52: (A [M, K], W [N, K]) fp32, before rounding."""
+    a = np.empty((M, K), np.float32)
+    w = np.empty((N, K), np.float32)
+    lib().or_reftest_gemm_inputs(_ptr(a), a.size, _ptr(w), w.size, seed)
+    return a, w
+
+
+def gemm_reftest_cpu(a, w) -> np.ndarray:
+    """quantlib_src/tests/test_gemm.cu:17-27 on binary16 A [M, K], W [N, K]: fp32 C [M, N]."""
+    a, w = _u16(a), _u16(w)
+    M, K = a.shape
+    N = w.shape[0]
+    c = np.empty((M, N), np.float32)
+    lib().or_gemm_reftest_cpu(_ptr(a), _ptr(w), _ptr(c), M, N, K)
+    return c

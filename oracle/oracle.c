@@ -700,3 +700,29 @@ void or_reftest_fp8_inputs(float* out, int64_t n, unsigned seed) {
     srand(seed);
     for (int64_t i = 0; i < n; ++i) out[i] = ((float)rand() / RAND_MAX) * 2.0f - 1.0f;
 }
+
+/* Inputs of quantlib_src/tests/test_gemm.cu:38-52 (srand(seed), then A [M x K] and
+ * W [N x K] in that order): v = ((float)rand() / RAND_MAX) * 0.2f - 0.1f, in fp32
+ * (the caller rounds them to binary16, as __float2half does).
+ * Pinned by: glibc rand() called through ctypes (tests/test_oracle.py). */
+void or_reftest_gemm_inputs(float* a, int64_t na, float* w, int64_t nw, unsigned seed) {
+    srand(seed);
+    for (int64_t i = 0; i < na; ++i) a[i] = ((float)rand() / RAND_MAX) * 0.2f - 0.1f;
+    for (int64_t i = 0; i < nw; ++i) w[i] = ((float)rand() / RAND_MAX) * 0.2f - 0.1f;
+}
+
+/* The CPU check of quantlib_src/tests/test_gemm.cu:17-27: C[m, n] = sum over k in
+ * order of f(A[m, k]) * f(W[n, k]), fp32 products and sums (f = binary16 -> fp32).
+ * Pinned by: numpy float64 matmul within the fp32 sum's rounding bound, and exact
+ * small-integer cases (tests/test_oracle.py). */
+void or_gemm_reftest_cpu(const uint16_t* a, const uint16_t* w, float* c, int M, int N, int K) {
+    for (int m = 0; m < M; ++m)
+        for (int n = 0; n < N; ++n) {
+            float s = 0.0f;
+            for (int k = 0; k < K; ++k) {
+                const float p = or_f16_to_f32(a[(size_t)m * K + k]) * or_f16_to_f32(w[(size_t)n * K + k]);
+                s = s + p;
+            }
+            c[(size_t)m * N + n] = s;
+        }
+}

@@ -116,6 +116,8 @@ void or_fp8_dequantize(const uint8_t* src, const float* scales, int rows, int co
 
 /* Inputs of quantlib_src/tests/test_fp8.cu:27-29. */
 void or_reftest_fp8_inputs(float* out, int64_t n, unsigned seed);
+void or_reftest_gemm_inputs(float* a, int64_t na, float* w, int64_t nw, unsigned seed);
+void or_gemm_reftest_cpu(const uint16_t* a, const uint16_t* w, float* c, int M, int N, int K);
 
 #ifdef __cplusplus
 }

@@ -316,6 +316,40 @@ def test_reference_fp8_test_via_quantlib_shims():
         assert qm.data is None and qm.params.scales is None
 
 
+def test_reference_gemm_test_via_quantlib_shims():
+    # quantlib_src/tests/test_gemm.cu:29-85: A [32 x 64] and W [64 x 64] from srand(7)
+    # U(-0.1, 0.1), W quantized E4M3 in groups of 64 (quantlib_fp16_to_fp8_e4m3),
+    # C = quantlib_fp8_gemm; its bar: max abs error < 1.0 against its fp32 CPU GEMM
+    # of the unquantized weights.  Tighter here: the same against the product of the
+    # dequantized weights within the GEMM bound, and the quantization error alone
+    # explains the distance to the unquantized product.
+    to_e4m3 = fn("quantlib_fp16_to_fp8_e4m3", [_p, _i, _i, _i, _i, _p], QuantMatrix)
+    gemm = fn("quantlib_fp8_gemm", [_p, ctypes.POINTER(QuantMatrix), _p, _i, _i, _i, _p])
+    qfree = fn("quantlib_free", [ctypes.POINTER(QuantMatrix)])
+    M, N, K = 32, 64, 64
+    a32, w32 = orc.reftest_gemm_inputs(M, N, K, 7)
+    a, w = to_f16_bits(a32), to_f16_bits(w32)
+    da, dw = dev(a), dev(w)
+    qm = to_e4m3(ptr(dw), N, K, 2, 64, stream())
+    out = empty((M * N,), np.uint16)
+    gemm(ptr(da), ctypes.byref(qm), ptr(out), M, N, K, stream())
+    sync()
+    got = f16_bits_to_f32(host(out, shape=(M, N))).astype(np.float64)
+    ref = orc.gemm_reftest_cpu(a, w).astype(np.float64)
+    err = float(np.abs(got - ref).max())
+    assert err < 1.0, err
+    q, sc = orc.fp8_quantize(w, 0, 2, 64, 0)
+    wd = orc.fp8_dequantize(q, sc, 0, 2, 64, 0)
+    af, wdf = f16_bits_to_f32(a).astype(np.float64), f16_bits_to_f32(wd).astype(np.float64)
+    s = af @ wdf.T
+    bound = 2.0 ** -10 * (np.abs(s) + np.abs(af) @ np.abs(wdf).T)
+    assert np.all(np.abs(got - s) <= bound)
+    wf = f16_bits_to_f32(w).astype(np.float64)
+    qerr = np.abs(af) @ np.abs(wdf - wf).T
+    assert np.all(np.abs(got - ref) <= qerr + bound + K * 2.0 ** -23 * (np.abs(af) @ np.abs(wf).T))
+    qfree(ctypes.byref(qm))
+
+
 @pytest.mark.parametrize("M", [16, 128])
 def test_quantlib_fp8_gemm_shim(M):
     to_e4m3 = fn("quantlib_fp16_to_fp8_e4m3", [_p, _i, _i, _i, _i, _p], QuantMatrix)

@@ -239,6 +239,30 @@ def test_softmax_passes_reference_test():
     assert np.max(np.abs(got.astype(np.float64).sum(axis=1) - 1.0)) < 1e-5
 
 
+def test_gemm_reference_test_inputs_and_cpu_loop():
+    # quantlib_src/tests/test_gemm.cu:17-52: srand(7), then A [32 x 64] and W [64 x 64],
+    # each element ((float)rand() / RAND_MAX) * 0.2f - 0.1f in fp32 arithmetic
+    M, N, K = 32, 64, 64
+    a, w = orc.reftest_gemm_inputs(M, N, K, 7)
+    libc = __import__("ctypes").CDLL(None)
+    libc.srand(7)
+    r = np.array([libc.rand() for _ in range(M * K + N * K)], np.int64)
+    want = (r.astype(np.float32) / np.float32(2147483647)) * np.float32(0.2) - np.float32(0.1)
+    assert np.array_equal(a.ravel(), want[:M * K]) and np.array_equal(w.ravel(), want[M * K:])
+    # its CPU check: fp32 products summed in k order, within the fp32 sum's rounding
+    # bound of the float64 product; exact where every partial sum is exact
+    ah, wh = to_f16_bits(a), to_f16_bits(w)
+    c = orc.gemm_reftest_cpu(ah, wh)
+    af, wf = f16_bits_to_f32(ah).astype(np.float64), f16_bits_to_f32(wh).astype(np.float64)
+    c64 = af @ wf.T
+    assert np.all(np.abs(c - c64) <= K * 2.0 ** -23 * (np.abs(af) @ np.abs(wf).T))
+    assert float(np.abs(c - c64).max()) > 0        # the fp32 loop rounds: not the float64 product
+    ints_a = to_f16_bits(np.array([[1, 2, 3], [-4, 5, 6]], np.float32))
+    ints_w = to_f16_bits(np.array([[7, -8, 9], [1, 1, 1], [0, 2, -1]], np.float32))
+    np.testing.assert_array_equal(orc.gemm_reftest_cpu(ints_a, ints_w),
+                                  np.array([[18, 6, 1], [-14, 7, 4]], np.float32))
+
+
 def test_softmax_matches_scipy_and_shift():
     x = normal(40, (64, 1000), sigma=2.0)
     got = orc.softmax(x)
