@@ -61,6 +61,7 @@ _SIGS = {
     "or_reftest_fp8_inputs": ([_p, _i64, ctypes.c_uint], None),
     "or_reftest_gemm_inputs": ([_p, _i64, _p, _i64, ctypes.c_uint], None),
     "or_gemm_reftest_cpu": ([_p, _p, _p, _i, _i, _i], None),
+    "or_check_recip_division": ([], ctypes.c_longlong),
 }
 
 _lib = None
@@ -331,3 +332,9 @@ def gemm_reftest_cpu(a, w) -> np.ndarray:
     c = np.empty((M, N), np.float32)
     lib().or_gemm_reftest_cpu(_ptr(a), _ptr(w), _ptr(c), M, N, K)
     return c
+
+
+def check_recip_division() -> int:
+    """Mismatches of the reciprocal-and-correction division against fp32 division over
+    one binade of divisors and every FP8 mantissa (0 expected)."""
+    return int(lib().or_check_recip_division())

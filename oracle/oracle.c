@@ -726,3 +726,28 @@ void or_gemm_reftest_cpu(const uint16_t* a, const uint16_t* w, float* c, int M, 
             c[(size_t)m * N + n] = s;
         }
 }
+
+/* Not a restatement of the reference: an exhaustive check of the division the
+ * GPU dequantizer uses in place of fp32 division (decoded FP8 value d over the
+ * group's scale s): r = RN(1/s) once per group, then per element q0 = RN(d*r),
+ * e = RN(d - s*q0) (one fma, exact), q = RN(q0 + e*r) (one fma).  Returns how many
+ * (s, d) pairs give q != RN(d/s) over every fp32 s in [1, 2) and every d = +-(1 +
+ * m/16), m = 0..15 (every FP8 mantissa).  In the normal range every step scales
+ * exactly with s and d by powers of two, so this binade covers all normal cases. */
+long long or_check_recip_division(void) {
+    long long bad = 0;
+    for (uint32_t bits = 0x3f800000u; bits < 0x40000000u; ++bits) {
+        float s;
+        memcpy(&s, &bits, 4);
+        const float r = 1.0f / s;
+        for (int m = 0; m < 16; ++m)
+            for (int sg = -1; sg <= 1; sg += 2) {
+                const float d = (float)sg * (1.0f + (float)m / 16.0f);
+                const float q0 = d * r;
+                const float e = fmaf(-q0, s, d);
+                const float q = fmaf(e, r, q0);
+                if (q != d / s) ++bad;
+            }
+    }
+    return bad;
+}

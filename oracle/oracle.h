@@ -118,6 +118,7 @@ void or_fp8_dequantize(const uint8_t* src, const float* scales, int rows, int co
 void or_reftest_fp8_inputs(float* out, int64_t n, unsigned seed);
 void or_reftest_gemm_inputs(float* a, int64_t na, float* w, int64_t nw, unsigned seed);
 void or_gemm_reftest_cpu(const uint16_t* a, const uint16_t* w, float* c, int M, int N, int K);
+long long or_check_recip_division(void);
 
 #ifdef __cplusplus
 }

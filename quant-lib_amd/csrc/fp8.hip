@@ -197,6 +197,25 @@ __global__ void finalize_scales(float* __restrict__ s, int n, float fmax) {
 }
 
 // ---- quantize / dequantize ------------------------------------------------------------
+// 8 elements times their group's scale -> 8 codes
+template <int FMT, int MODE>
+__device__ __forceinline__ u32x2 encode8(const Vec<_Float16, 8>& v, float s) {
+    uint32_t w[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        float f[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) f[e] = (float)v.v[4 * h + e] * s;
+        if constexpr (MODE == QL_FP8_MODE_REFERENCE) {
+            w[h] = enc_ref<FMT>(f[0]) | (enc_ref<FMT>(f[1]) << 8) | (enc_ref<FMT>(f[2]) << 16) |
+                   (enc_ref<FMT>(f[3]) << 24);
+        } else {
+            w[h] = enc_ocp2<FMT>(f[0], f[1]) | (enc_ocp2<FMT>(f[2], f[3]) << 16);
+        }
+    }
+    return u32x2{w[0], w[1]};
+}
+
 // VEC: 8 elements per thread (n % 8 == 0, gs % 8 == 0, aligned); else one element.
 template <int FMT, int MODE, bool VEC>
 __global__ __launch_bounds__(kBlock) void quantize_kernel(const _Float16* __restrict__ x, Geom g,
@@ -206,21 +225,7 @@ __global__ __launch_bounds__(kBlock) void quantize_kernel(const _Float16* __rest
     if constexpr (VEC) {
         if (t * 8 >= g.n) return;
         const Vec<_Float16, 8> v = load<true>(reinterpret_cast<const Vec<_Float16, 8>*>(x) + t);
-        const float s = scales[(t * 8) / g.gs];
-        uint32_t w[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            float f[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) f[e] = (float)v.v[4 * h + e] * s;
-            if constexpr (MODE == QL_FP8_MODE_REFERENCE) {
-                w[h] = enc_ref<FMT>(f[0]) | (enc_ref<FMT>(f[1]) << 8) | (enc_ref<FMT>(f[2]) << 16) |
-                       (enc_ref<FMT>(f[3]) << 24);
-            } else {
-                w[h] = enc_ocp2<FMT>(f[0], f[1]) | (enc_ocp2<FMT>(f[2], f[3]) << 16);
-            }
-        }
-        store<true>(reinterpret_cast<u32x2*>(q) + t, u32x2{w[0], w[1]});
+        store<true>(reinterpret_cast<u32x2*>(q) + t, encode8<FMT, MODE>(v, scales[(t * 8) / g.gs]));
     } else {
         if (t >= g.n) return;
         const float f = (float)x[t] * scales[t / g.gs];
@@ -228,10 +233,113 @@ __global__ __launch_bounds__(kBlock) void quantize_kernel(const _Float16* __rest
     }
 }
 
+// Scales and codes in one pass for groups of GL*8 elements (GL = 2..64 lanes, a
+// power of two; n % 8 == 0, 16-byte aligned x, 8-byte aligned q): the layout of
+// absmax_vec -- each lane loads its 8 elements with one 16-byte load, the GL
+// lanes of a group reduce the group's max -- and then every lane computes the
+// group's scale exactly as finalize_scales does (fmax / max, 1 below 1e-8) and
+// encodes its 8 elements from the registers it loaded, so x is read once instead
+// of twice.  One lane per group stores the scale.
+constexpr int kQuantIters = 4;   // spans of 64 vectors per wavefront (2, 4, 8, 16 measured: 4 best)
+
+template <int FMT, int MODE, int GL>
+__global__ __launch_bounds__(kBlock) void quantize_groups(const _Float16* __restrict__ x, Geom g,
+                                                          float* __restrict__ scales, uint8_t* __restrict__ q) {
+    constexpr float kMax = fp8_max(FMT);
+    const int lane = threadIdx.x & (kWave - 1);
+    const long long n_vec = g.n / 8;
+    const long long w0 = ((long long)blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave) * kQuantIters * kWave;
+    Vec<_Float16, 8> h[kQuantIters];
+#pragma unroll
+    for (int it = 0; it < kQuantIters; ++it) {   // every load first
+        const long long v = w0 + (long long)it * kWave + lane;
+        h[it] = load<true>(reinterpret_cast<const Vec<_Float16, 8>*>(x) + (v < n_vec ? v : 0));
+    }
+#pragma unroll
+    for (int it = 0; it < kQuantIters; ++it) {
+        const long long v = w0 + (long long)it * kWave + lane;
+        const long long off = (v * 8) % (8 * GL);                 // offset inside the group
+        float m = 0.0f;   // lanes past the end (their load repeated vector 0) add nothing
+        if (v < n_vec && seen(MODE, off)) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf((float)h[it].v[e]));
+        }
+#pragma unroll
+        for (int o = 1; o < GL; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
+        const float sc = m < 1e-8f ? 1.0f : kMax / m;
+        if (v < n_vec) {
+            if ((lane & (GL - 1)) == 0) scales[v / GL] = sc;
+            store<true>(reinterpret_cast<u32x2*>(q) + v, encode8<FMT, MODE>(h[it], sc));
+        }
+    }
+}
+
 template <int FMT, int MODE>
 __device__ __forceinline__ float decode1(uint32_t q) {
     if constexpr (MODE == QL_FP8_MODE_REFERENCE) return dec_ref<FMT>(q);
     else return dec_ocp2<FMT>(q)[0];
+}
+
+// d / s for a decoded code d: with r = RN(1/s) and s in [2^-90, 2^90] (every step
+// normal: |d| lies in [2^-16, 2^17]), q0 = d * r plus one fma correction is RN(d / s)
+// exactly (exhaustive over a binade of s and every FP8 mantissa on the CPU; every
+// step scales exactly by powers of two).  Zeros, infinities and NaNs take q0
+// (signed zeros keep their sign).  Callers outside that range of s divide.
+__device__ __forceinline__ bool recip_ok(float s) { return s >= 0x1p-90f && s <= 0x1p90f; }
+__device__ __forceinline__ float div_by_recip(float d, float s, float r) {
+    const float q0 = d * r;
+    const float q1 = fmaf(fmaf(-q0, s, d), r, q0);
+    return d != 0.0f && __builtin_isfinite(d) ? q1 : q0;
+}
+
+// the four codes of w, decoded
+template <int FMT, int MODE>
+__device__ __forceinline__ void decode4(uint32_t w, float (&d)[4]) {
+    if constexpr (MODE == QL_FP8_MODE_REFERENCE) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) d[e] = dec_ref<FMT>((w >> (8 * e)) & 0xFFu);
+    } else {
+        const float2v lo = dec_ocp2<FMT>(w), hi = dec_ocp2<FMT, true>(w);
+        d[0] = lo[0];
+        d[1] = lo[1];
+        d[2] = hi[0];
+        d[3] = hi[1];
+    }
+}
+
+// 16 codes per thread (n % 16 == 0, gs % 16 == 0, 16-byte aligned codes and output):
+// one 16-byte load, the group's scale and its reciprocal once, two 16-byte stores.
+template <int FMT, int MODE>
+__global__ __launch_bounds__(kBlock) void dequantize16(const uint8_t* __restrict__ q, Geom g,
+                                                       const float* __restrict__ scales,
+                                                       _Float16* __restrict__ y) {
+    const long long t = (long long)blockIdx.x * kBlock + threadIdx.x;
+    if (t * 16 >= g.n) return;
+    const u32x4 w = load<true>(reinterpret_cast<const u32x4*>(q) + t);
+    const long long e0 = t * 16;
+    const long long gi = g.n <= 0xFFFFFFFFLL ? (long long)((uint32_t)e0 / (uint32_t)g.gs) : e0 / g.gs;
+    const float s = scales[gi];
+    Vec<_Float16, 8> out[2];
+    if (recip_ok(s)) {
+        const float r = 1.0f / s;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float d[4];
+            decode4<FMT, MODE>(w[j], d);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) out[j >> 1].v[4 * (j & 1) + e] = from_f32<_Float16>(div_by_recip(d[e], s, r));
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float d[4];
+            decode4<FMT, MODE>(w[j], d);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) out[j >> 1].v[4 * (j & 1) + e] = from_f32<_Float16>(d[e] / s);
+        }
+    }
+    store<true>(reinterpret_cast<Vec<_Float16, 8>*>(y) + 2 * t, out[0]);
+    store<true>(reinterpret_cast<Vec<_Float16, 8>*>(y) + 2 * t + 1, out[1]);
 }
 
 template <int FMT, int MODE, bool VEC>
@@ -244,10 +352,15 @@ __global__ __launch_bounds__(kBlock) void dequantize_kernel(const uint8_t* __res
         const u32x2 w = load<true>(reinterpret_cast<const u32x2*>(q) + t);
         const float s = scales[(t * 8) / g.gs];
         Vec<_Float16, 8> out;
+        if (recip_ok(s)) {
+            const float r = 1.0f / s;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const uint32_t code = (w[e >> 2] >> (8 * (e & 3))) & 0xFFu;
-            out.v[e] = from_f32<_Float16>(decode1<FMT, MODE>(code) / s);
+            for (int e = 0; e < 8; ++e)
+                out.v[e] = from_f32<_Float16>(div_by_recip(decode1<FMT, MODE>((w[e >> 2] >> (8 * (e & 3))) & 0xFFu), s, r));
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                out.v[e] = from_f32<_Float16>(decode1<FMT, MODE>((w[e >> 2] >> (8 * (e & 3))) & 0xFFu) / s);
         }
         store<true>(reinterpret_cast<Vec<_Float16, 8>*>(y) + t, out);
     } else {
@@ -1308,6 +1421,19 @@ bool geom_for(int rows, int cols, int gran, int group_size, Geom& g) {
 }
 
 template <int FMT, int MODE>
+void launch_quantize_groups(const _Float16* x, const Geom& g, float* s, uint8_t* q, hipStream_t st) {
+    const dim3 grid(qlh::blocks_for(g.n / 8, (long long)kQuantIters * kBlock)), block(kBlock);
+    switch (g.gs) {
+    case 16: hipLaunchKernelGGL((quantize_groups<FMT, MODE, 2>), grid, block, 0, st, x, g, s, q); break;
+    case 32: hipLaunchKernelGGL((quantize_groups<FMT, MODE, 4>), grid, block, 0, st, x, g, s, q); break;
+    case 64: hipLaunchKernelGGL((quantize_groups<FMT, MODE, 8>), grid, block, 0, st, x, g, s, q); break;
+    case 128: hipLaunchKernelGGL((quantize_groups<FMT, MODE, 16>), grid, block, 0, st, x, g, s, q); break;
+    case 256: hipLaunchKernelGGL((quantize_groups<FMT, MODE, 32>), grid, block, 0, st, x, g, s, q); break;
+    default: hipLaunchKernelGGL((quantize_groups<FMT, MODE, 64>), grid, block, 0, st, x, g, s, q); break;
+    }
+}
+
+template <int FMT, int MODE>
 void launch_quantize(const _Float16* x, const Geom& g, const float* s, uint8_t* q, bool vec,
                      hipStream_t st) {
     if (vec)
@@ -1321,7 +1447,10 @@ void launch_quantize(const _Float16* x, const Geom& g, const float* s, uint8_t* 
 template <int FMT, int MODE>
 void launch_dequantize(const uint8_t* q, const Geom& g, const float* s, _Float16* y, bool vec,
                        hipStream_t st) {
-    if (vec)
+    if (vec && g.n % 16 == 0 && g.gs % 16 == 0 && qlh::aligned16(q))
+        hipLaunchKernelGGL((dequantize16<FMT, MODE>), dim3(qlh::blocks_for(g.n / 16, kBlock)), dim3(kBlock), 0,
+                           st, q, g, s, y);
+    else if (vec)
         hipLaunchKernelGGL((dequantize_kernel<FMT, MODE, true>), dim3(qlh::blocks_for(g.n / 8, kBlock)),
                            dim3(kBlock), 0, st, q, g, s, y);
     else
@@ -1660,6 +1789,12 @@ extern "C" hipError_t ql_fp8_quantize(const uint16_t* src, int rows, int cols, i
     QL_CHECK_ARG(fmt_mode_ok(format, mode) && geom_for(rows, cols, granularity, group_size, g));
     if (g.n == 0) return hipSuccess;
     QL_CHECK_ARG(dst);
+    if (src && scales && g.n % 8 == 0 && qlh::aligned16(src) && ((uintptr_t)dst & 7) == 0 && g.gs >= 16 &&
+        g.gs <= 512 && (g.gs & (g.gs - 1)) == 0) {   // one pass: scales and codes together
+        QL_FP8_DISPATCH(format, mode, launch_quantize_groups, reinterpret_cast<const _Float16*>(src), g, scales,
+                        dst, stream);
+        return hipGetLastError();
+    }
     const hipError_t e = ql_fp8_scales(src, rows, cols, format, granularity, group_size, mode, scales, stream);
     if (e != hipSuccess) return e;
     const bool vec = g.n % 8 == 0 && g.gs % 8 == 0 && qlh::aligned16(src) && ((uintptr_t)dst & 7) == 0;

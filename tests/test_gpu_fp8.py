@@ -68,9 +68,12 @@ def same_f16(a, b):
     (1024, 1024, ql.QUANT_PER_CHANNEL, 0), (1024, 1024, ql.QUANT_PER_TENSOR, 0),
     (64, 256, ql.QUANT_PER_GROUP, 100), (3, 1000, ql.QUANT_PER_GROUP, 7), (5, 33, ql.QUANT_PER_CHANNEL, 0),
     (4096, 4096, ql.QUANT_PER_TENSOR, 0),       # one group larger than a wavefront pass
-    # power-of-two groups take the vector scales pass: every lane count, a partial last group
+    # power-of-two groups take the one-pass kernel (scales and codes from one read of x,
+    # ql_fp8_scales' vector pass for the scales alone): every lane count
     (16, 512, ql.QUANT_PER_GROUP, 16), (5, 96, ql.QUANT_PER_GROUP, 32), (7, 64, ql.QUANT_PER_GROUP, 64),
-    (8, 1024, ql.QUANT_PER_GROUP, 256), (16, 512, ql.QUANT_PER_GROUP, 512), (3, 200, ql.QUANT_PER_GROUP, 128)])
+    (8, 1024, ql.QUANT_PER_GROUP, 256), (16, 512, ql.QUANT_PER_GROUP, 512), (3, 200, ql.QUANT_PER_GROUP, 128),
+    # ... and a partial last group (fewer lanes than the group spans)
+    (3, 1000, ql.QUANT_PER_GROUP, 512), (5, 24, ql.QUANT_PER_GROUP, 16), (1, 8, ql.QUANT_PER_GROUP, 64)])
 def test_fp8_codec_bit_exact(mode, fmt, rows, cols, gran, gs):
     x = to_f16_bits(uniform(rows + cols + gs, (rows, cols), -1.0, 1.0) *
                     np.float32(1.0 if fmt == ql.FP8_E4M3 else 300.0))
@@ -101,6 +104,28 @@ def test_fp8_encode_every_half_and_decode_every_code(mode, fmt):
     ones = np.ones(8, np.float32)
     assert same_f16(gpu_dequantize(codes, ones, fmt, ql.QUANT_PER_GROUP, 32, mode),
                     orc.fp8_dequantize(codes, ones, fmt, ql.QUANT_PER_GROUP, 32, mode))
+
+
+@pytest.mark.parametrize("gs", [32, 8])
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("fmt", FMTS)
+def test_fp8_dequantize_any_scale_bit_exact(mode, fmt, gs):
+    # every code under log-uniform scales from 2^-100 to 2^100 (the dequantizer divides
+    # by a corrected reciprocal for scales in [2^-90, 2^90] and by fp32 division
+    # outside), plus scales at and just past those limits: bit for bit the oracle's
+    # binary16(decode / scale), NaN for NaN.  Groups of 32 take the 16-codes-per-thread
+    # kernel, groups of 8 the 8-codes one.
+    rng = np.random.default_rng(40 + 2 * fmt + mode)
+    n_grp = 2048
+    edges = np.array([2.0 ** -90, 2.0 ** 90, np.nextafter(np.float32(2.0 ** -90), 0),
+                      np.nextafter(np.float32(2.0 ** 90), np.float32(np.inf)), 1.0, 3.0, 448.0, 1e-8], np.float32)
+    sc = np.concatenate([edges, np.exp2(rng.uniform(-100, 100, n_grp - edges.size))]).astype(np.float32)
+    codes = np.resize(np.arange(256, dtype=np.uint8), (n_grp, 256))
+    codes = np.ascontiguousarray(rng.permuted(codes, axis=1)).reshape(n_grp * 256 // gs, gs)
+    scg = np.repeat(sc, 256 // gs)          # one row per group, each group's scale
+    got = gpu_dequantize(codes, scg, fmt, ql.QUANT_PER_GROUP, gs, mode)
+    want = orc.fp8_dequantize(codes, scg, fmt, ql.QUANT_PER_GROUP, gs, mode)
+    assert same_f16(got, want), int((got != want).sum())
 
 
 def gemm_exact(a, w_deq):

@@ -616,6 +616,14 @@ def test_fp8_reference_scales_match_kernel_simulation(rows, cols, gran, gs, fmt)
     assert np.array_equal(orc.fp8_quantize(z, fmt, 1, 0, REF)[1], np.ones(2, np.float32))
 
 
+def test_dequantize_division_by_corrected_reciprocal_is_exact():
+    # The GPU dequantizer divides each decoded code d by its group's scale s as
+    # q0 = d * RN(1/s), then one fma correction; exhaustively equal to RN(d / s) for
+    # every fp32 s in [1, 2) and every FP8 mantissa, both signs (and hence, by exact
+    # power-of-two scaling, over the normal range the kernel uses it for)
+    assert orc.check_recip_division() == 0
+
+
 @pytest.mark.parametrize("mode", [REF, OCP])
 @pytest.mark.parametrize("gran,gs", [(0, 0), (1, 0), (2, 128), (2, 100)])
 def test_fp8_quantize_scales_and_reference_error_bar(mode, gran, gs):
