@@ -274,6 +274,49 @@ __global__ __launch_bounds__(kBlock) void quantize_groups(const _Float16* __rest
     }
 }
 
+// Scales and codes in one pass for any group length that is a multiple of 8, up to
+// 16384 (per-channel rows, large or odd groups; n % 8 == 0, 16-byte aligned x, 8-byte
+// aligned q): one wavefront per group holds the group in registers (NV 16-byte
+// vectors per lane: 8, 16 or 32, the fewest that hold it), reduces its max, computes
+// the scale as finalize_scales does and encodes from the registers: x is read once,
+// with 16-byte loads.
+constexpr int kWaveGroupVecs = 32;
+
+template <int FMT, int MODE, int NV>
+__global__ __launch_bounds__(kBlock) void quantize_wave_groups(const _Float16* __restrict__ x, Geom g,
+                                                               float* __restrict__ scales,
+                                                               uint8_t* __restrict__ q) {
+    constexpr float kMax = fp8_max(FMT);
+    const int lane = threadIdx.x & (kWave - 1);
+    const long long grp = (long long)blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
+    if (grp >= g.n_groups) return;   // wavefront-uniform
+    const long long base = grp * g.gs;
+    const int nv = (int)(min(g.gs, g.n - base) / 8);   // vectors of this group
+    const Vec<_Float16, 8>* xv = reinterpret_cast<const Vec<_Float16, 8>*>(x + base);
+    Vec<_Float16, 8> h[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+        if (j * kWave < nv) h[j] = load<true>(xv + min(j * kWave + lane, nv - 1));   // uniform test
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int i = j * kWave + lane;
+        if (i < nv && seen(MODE, (long long)i * 8)) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf((float)h[j].v[e]));
+        }
+    }
+    m = wave_max(m);
+    const float sc = m < 1e-8f ? 1.0f : kMax / m;
+    if (lane == 0) scales[grp] = sc;
+    u32x2* qv = reinterpret_cast<u32x2*>(q + base);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int i = j * kWave + lane;
+        if (i < nv) store<true>(qv + i, encode8<FMT, MODE>(h[j], sc));
+    }
+}
+
 template <int FMT, int MODE>
 __device__ __forceinline__ float decode1(uint32_t q) {
     if constexpr (MODE == QL_FP8_MODE_REFERENCE) return dec_ref<FMT>(q);
@@ -1434,6 +1477,15 @@ void launch_quantize_groups(const _Float16* x, const Geom& g, float* s, uint8_t*
 }
 
 template <int FMT, int MODE>
+void launch_quantize_wave_groups(const _Float16* x, const Geom& g, float* s, uint8_t* q, hipStream_t st) {
+    const dim3 grid(qlh::blocks_for(g.n_groups, kBlock / kWave)), block(kBlock);
+    if (g.gs <= 8 * kWave * 8) hipLaunchKernelGGL((quantize_wave_groups<FMT, MODE, 8>), grid, block, 0, st, x, g, s, q);
+    else if (g.gs <= 8 * kWave * 16)
+        hipLaunchKernelGGL((quantize_wave_groups<FMT, MODE, 16>), grid, block, 0, st, x, g, s, q);
+    else hipLaunchKernelGGL((quantize_wave_groups<FMT, MODE, 32>), grid, block, 0, st, x, g, s, q);
+}
+
+template <int FMT, int MODE>
 void launch_quantize(const _Float16* x, const Geom& g, const float* s, uint8_t* q, bool vec,
                      hipStream_t st) {
     if (vec)
@@ -1793,6 +1845,12 @@ extern "C" hipError_t ql_fp8_quantize(const uint16_t* src, int rows, int cols, i
         g.gs <= 512 && (g.gs & (g.gs - 1)) == 0) {   // one pass: scales and codes together
         QL_FP8_DISPATCH(format, mode, launch_quantize_groups, reinterpret_cast<const _Float16*>(src), g, scales,
                         dst, stream);
+        return hipGetLastError();
+    }
+    if (src && scales && g.n % 8 == 0 && g.gs % 8 == 0 && g.gs <= 8LL * kWave * kWaveGroupVecs &&
+        qlh::aligned16(src) && ((uintptr_t)dst & 7) == 0) {   // one wavefront per group, one pass
+        QL_FP8_DISPATCH(format, mode, launch_quantize_wave_groups, reinterpret_cast<const _Float16*>(src), g,
+                        scales, dst, stream);
         return hipGetLastError();
     }
     const hipError_t e = ql_fp8_scales(src, rows, cols, format, granularity, group_size, mode, scales, stream);

@@ -73,7 +73,12 @@ def same_f16(a, b):
     (16, 512, ql.QUANT_PER_GROUP, 16), (5, 96, ql.QUANT_PER_GROUP, 32), (7, 64, ql.QUANT_PER_GROUP, 64),
     (8, 1024, ql.QUANT_PER_GROUP, 256), (16, 512, ql.QUANT_PER_GROUP, 512), (3, 200, ql.QUANT_PER_GROUP, 128),
     # ... and a partial last group (fewer lanes than the group spans)
-    (3, 1000, ql.QUANT_PER_GROUP, 512), (5, 24, ql.QUANT_PER_GROUP, 16), (1, 8, ql.QUANT_PER_GROUP, 64)])
+    (3, 1000, ql.QUANT_PER_GROUP, 512), (5, 24, ql.QUANT_PER_GROUP, 16), (1, 8, ql.QUANT_PER_GROUP, 64),
+    # other multiples of 8 up to 16384 take the one-wavefront-per-group pass: up to 8,
+    # 16 and 32 vectors per lane, per-channel rows, partial last groups
+    (5, 1000, ql.QUANT_PER_GROUP, 200), (3, 1000, ql.QUANT_PER_GROUP, 1992), (7, 3000, ql.QUANT_PER_GROUP, 4104),
+    (4, 8192, ql.QUANT_PER_CHANNEL, 0), (6, 14336, ql.QUANT_PER_CHANNEL, 0), (2, 16384, ql.QUANT_PER_GROUP, 16384),
+    (9, 48, ql.QUANT_PER_GROUP, 48)])
 def test_fp8_codec_bit_exact(mode, fmt, rows, cols, gran, gs):
     x = to_f16_bits(uniform(rows + cols + gs, (rows, cols), -1.0, 1.0) *
                     np.float32(1.0 if fmt == ql.FP8_E4M3 else 300.0))
