@@ -982,14 +982,19 @@ def fp8_rows(ql, np, reps):
     nsets = len(xs)
     qs = [(ql.DeviceArray((N * K,), np.uint8), ql.DeviceArray((N * K // 128,), np.float32)) for _ in range(nsets)]
     for mode, mname in ((ql.FP8_MODE_REFERENCE, "reference codec"), (ql.FP8_MODE_OCP, "OCP")):
-        us = timed(lambda i: ql.call("ql_fp8_quantize", xs[i % nsets].ptr, N, K, ql.FP8_E4M3,
-                                     ql.QUANT_PER_GROUP, 128, mode, qs[i % nsets][0].ptr, qs[i % nsets][1].ptr, st),
-                   max(6, reps // 5))
+        # per tensor reads the matrix twice (its one scale first): 5 bytes an element
+        for gran, gs, glabel, n_sc in ((ql.QUANT_PER_GROUP, 128, "g128", N * K // 128),
+                                       (ql.QUANT_PER_CHANNEL, 0, "per channel", N),
+                                       (ql.QUANT_PER_TENSOR, 0, "per tensor", 1)):
+            us = timed(lambda i: ql.call("ql_fp8_quantize", xs[i % nsets].ptr, N, K, ql.FP8_E4M3, gran, gs, mode,
+                                         qs[i % nsets][0].ptr, qs[i % nsets][1].ptr, st),
+                       max(6, reps // 5))
+            nbytes = 3 * N * K + 4 * n_sc
+            gbs = nbytes / (us * 1e-6) / 1e9
+            rows.append({"config": f"FP8 quantize 14336x4096 e4m3 {glabel}, {mname}", "kernel": "fp8_quantize",
+                         "bytes": nbytes, "us": round(us, 2), "GBps": round(gbs, 1),
+                         "frac_peak": round(gbs / PEAK_HBM_GBS, 4)})
         nbytes = 3 * N * K + 4 * N * K // 128
-        gbs = nbytes / (us * 1e-6) / 1e9
-        rows.append({"config": f"FP8 quantize 14336x4096 e4m3 g128, {mname}", "kernel": "fp8_quantize",
-                     "bytes": nbytes, "us": round(us, 2), "GBps": round(gbs, 1),
-                     "frac_peak": round(gbs / PEAK_HBM_GBS, 4)})
         us = timed(lambda i: ql.call("ql_fp8_dequantize", qs[i % nsets][0].ptr, qs[i % nsets][1].ptr, N, K,
                                      ql.FP8_E4M3, ql.QUANT_PER_GROUP, 128, mode, xs[(i + 1) % nsets].ptr, st),
                    max(6, reps // 5))

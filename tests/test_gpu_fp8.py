@@ -91,6 +91,27 @@ def test_fp8_codec_bit_exact(mode, fmt, rows, cols, gran, gs):
 
 @pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("rows,cols,gran,gs,offset", [
+    (64, 256, ql.QUANT_PER_GROUP, 128, 0),       # power-of-two groups, 16-byte loads
+    (5, 1000, ql.QUANT_PER_GROUP, 200, 0),       # one wavefront per group, scales only
+    (4, 14336, ql.QUANT_PER_CHANNEL, 0, 0), (3, 8200, ql.QUANT_PER_CHANNEL, 0, 0),
+    (5, 1000, ql.QUANT_PER_GROUP, 200, 1),       # unaligned source: element loads
+    (3, 1000, ql.QUANT_PER_GROUP, 7, 0),
+    (1024, 1024, ql.QUANT_PER_TENSOR, 0, 0),     # groups over many workgroups, 16-byte loads
+    (4096, 4096, ql.QUANT_PER_TENSOR, 0, 0), (2, 20000, ql.QUANT_PER_CHANNEL, 0, 0),
+    (3, 9001, ql.QUANT_PER_CHANNEL, 0, 0),       # ... element loads (n % 8 != 0)
+    (1024, 1024, ql.QUANT_PER_TENSOR, 0, 3)])
+def test_fp8_scales_entry_bit_exact(mode, fmt, rows, cols, gran, gs, offset):
+    # ql_fp8_scales alone, over each of its passes: the oracle's scales bit for bit
+    x = to_f16_bits(uniform(7 * rows + cols + gs, (rows, cols), -1.0, 1.0) * np.float32(3.0))
+    ns = n_scales(rows, cols, gran, gs)
+    sc = empty((ns,), np.float32, fill_bits=0xFF)
+    ql.call("ql_fp8_scales", dev(x, offset).ptr, rows, cols, fmt, gran, gs, mode, sc.ptr, stream())
+    assert np.array_equal(host(sc), orc.fp8_quantize(x, fmt, gran, gs, mode)[1])
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("fmt", FMTS)
 def test_fp8_encode_every_half_and_decode_every_code(mode, fmt):
     # groups of 32 whose first element is fmax: scale == 1, so codes = encode(x) for
     # every binary16 value up to fmax (both modes see all 32 offsets)
