@@ -92,9 +92,11 @@ def test_fp8_codec_bit_exact(mode, fmt, rows, cols, gran, gs):
 @pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("rows,cols,gran,gs,offset", [
-    (64, 256, ql.QUANT_PER_GROUP, 128, 0),       # power-of-two groups, 16-byte loads
-    (5, 1000, ql.QUANT_PER_GROUP, 200, 0),       # one wavefront per group, scales only
-    (4, 14336, ql.QUANT_PER_CHANNEL, 0, 0), (3, 8200, ql.QUANT_PER_CHANNEL, 0, 0),
+    (64, 256, ql.QUANT_PER_GROUP, 128, 0),       # power-of-two groups, 16-byte loads: every lane count
+    (16, 512, ql.QUANT_PER_GROUP, 16, 0), (5, 96, ql.QUANT_PER_GROUP, 32, 0), (7, 64, ql.QUANT_PER_GROUP, 64, 0),
+    (8, 1024, ql.QUANT_PER_GROUP, 256, 0), (16, 512, ql.QUANT_PER_GROUP, 512, 0), (3, 200, ql.QUANT_PER_GROUP, 128, 0),
+    (5, 1000, ql.QUANT_PER_GROUP, 200, 0),       # one wavefront per group, scales only: 8, 16, 32 vectors a lane
+    (3, 6000, ql.QUANT_PER_CHANNEL, 0, 0), (4, 14336, ql.QUANT_PER_CHANNEL, 0, 0), (3, 8200, ql.QUANT_PER_CHANNEL, 0, 0),
     (5, 1000, ql.QUANT_PER_GROUP, 200, 1),       # unaligned source: element loads
     (3, 1000, ql.QUANT_PER_GROUP, 7, 0),
     (1024, 1024, ql.QUANT_PER_TENSOR, 0, 0),     # groups over many workgroups, 16-byte loads
