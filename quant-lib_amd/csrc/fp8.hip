@@ -132,7 +132,7 @@ __global__ __launch_bounds__(kBlock) void absmax_wave(const _Float16* __restrict
     if (lane == 0) mx[grp] = m;
 }
 
-// groups of GL*8 elements (GL = 2..64 lanes, a power of two), n % 8 == 0, 16-byte
+// groups of GL*8 elements (GL = 1..64 lanes, a power of two), n % 8 == 0, 16-byte
 // aligned: each lane reads 8 consecutive elements with one 16-byte load, the GL
 // lanes of a group (a group starts at a lane multiple of GL, since every
 // wavefront starts at a multiple of 64 vectors) reduce with shuffles, and each
@@ -282,7 +282,7 @@ __global__ __launch_bounds__(kBlock) void quantize_kernel(const _Float16* __rest
     }
 }
 
-// Scales and codes in one pass for groups of GL*8 elements (GL = 2..64 lanes, a
+// Scales and codes in one pass for groups of GL*8 elements (GL = 1..64 lanes, a
 // power of two; n % 8 == 0, 16-byte aligned x, 8-byte aligned q): the layout of
 // absmax_vec -- each lane loads its 8 elements with one 16-byte load, the GL
 // lanes of a group reduce the group's max -- and then every lane computes the
@@ -319,6 +319,51 @@ __global__ __launch_bounds__(kBlock) void quantize_groups(const _Float16* __rest
         if (v < n_vec) {
             if ((lane & (GL - 1)) == 0) scales[v / GL] = sc;
             store<true>(reinterpret_cast<u32x2*>(q) + v, encode8<FMT, MODE>(h[it], sc));
+        }
+    }
+}
+
+// Scales and codes in one pass for short groups of V 16-byte vectors, V = 3..31 not a
+// power of two (n % 8 == 0, 16-byte aligned x, 8-byte aligned q): a wavefront span is
+// P = 64 / V whole groups in lanes [0, P*V) -- lane l holds vector l % V of group
+// l / V -- so each load instruction reads P*V consecutive vectors.  A group's max is
+// a segmented reduction (each step a lane takes the max of the lane o places up when
+// that lane is in its group, o = 1, 2, 4, ...), which leaves it in the group's first
+// lane, read back by the others.  kQuantIters spans per wavefront.  ENCODE false:
+// scales only.
+template <int FMT, int MODE, bool ENCODE>
+__global__ __launch_bounds__(kBlock) void quantize_segments(const _Float16* __restrict__ x, Geom g, int V, int P,
+                                                            float* __restrict__ scales, uint8_t* __restrict__ q) {
+    constexpr float kMax = fp8_max(FMT);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int seg = lane / V, first = seg * V, idx = lane - first;
+    const bool in_span = seg < P;
+    const long long n_vec = g.n / 8;
+    const long long sp0 = ((long long)blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave) * kQuantIters;
+    Vec<_Float16, 8> h[kQuantIters];
+#pragma unroll
+    for (int it = 0; it < kQuantIters; ++it) {   // every load first
+        const long long v = (sp0 + it) * P * V + lane;
+        h[it] = load<true>(reinterpret_cast<const Vec<_Float16, 8>*>(x) + (in_span && v < n_vec ? v : 0));
+    }
+#pragma unroll
+    for (int it = 0; it < kQuantIters; ++it) {
+        const long long v = (sp0 + it) * P * V + lane;
+        const bool ok = in_span && v < n_vec;
+        float m = 0.0f;
+        if (ok && seen(MODE, (long long)idx * 8)) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf((float)h[it].v[e]));
+        }
+        for (int o = 1; o < V; o <<= 1) {   // uniform trip count
+            const float t = __shfl(m, min(lane + o, kWave - 1), kWave);
+            if (idx + o < V) m = fmaxf(m, t);
+        }
+        m = __shfl(m, first, kWave);
+        const float sc = m < 1e-8f ? 1.0f : kMax / m;
+        if (ok) {
+            if (idx == 0) scales[(sp0 + it) * P + seg] = sc;
+            if constexpr (ENCODE) store<true>(reinterpret_cast<u32x2*>(q) + v, encode8<FMT, MODE>(h[it], sc));
         }
     }
 }
@@ -1518,6 +1563,7 @@ template <int FMT, int MODE>
 void launch_quantize_groups(const _Float16* x, const Geom& g, float* s, uint8_t* q, hipStream_t st) {
     const dim3 grid(qlh::blocks_for(g.n / 8, (long long)kQuantIters * kBlock)), block(kBlock);
     switch (g.gs) {
+    case 8: hipLaunchKernelGGL((quantize_groups<FMT, MODE, 1>), grid, block, 0, st, x, g, s, q); break;
     case 16: hipLaunchKernelGGL((quantize_groups<FMT, MODE, 2>), grid, block, 0, st, x, g, s, q); break;
     case 32: hipLaunchKernelGGL((quantize_groups<FMT, MODE, 4>), grid, block, 0, st, x, g, s, q); break;
     case 64: hipLaunchKernelGGL((quantize_groups<FMT, MODE, 8>), grid, block, 0, st, x, g, s, q); break;
@@ -1545,6 +1591,16 @@ void launch_quantize_wave_groups(const _Float16* x, const Geom& g, float* s, uin
     } else {
         hipLaunchKernelGGL((quantize_wave_groups<FMT, MODE, 32>), grid, block, 0, st, x, g, s, q);
     }
+}
+
+// q == nullptr: scales only (ql_fp8_scales)
+template <int FMT, int MODE>
+void launch_quantize_segments(const _Float16* x, const Geom& g, float* s, uint8_t* q, hipStream_t st) {
+    const int V = (int)(g.gs / 8), P = kWave / V;
+    const long long spans = (g.n_groups + P - 1) / P;
+    const dim3 grid(qlh::blocks_for(spans, (long long)kQuantIters * (kBlock / kWave))), block(kBlock);
+    if (q) hipLaunchKernelGGL((quantize_segments<FMT, MODE, true>), grid, block, 0, st, x, g, V, P, s, q);
+    else hipLaunchKernelGGL((quantize_segments<FMT, MODE, false>), grid, block, 0, st, x, g, V, P, s, q);
 }
 
 template <int FMT, int MODE>
@@ -1869,9 +1925,10 @@ extern "C" hipError_t ql_fp8_scales(const uint16_t* src, int rows, int cols, int
     const _Float16* x = reinterpret_cast<const _Float16*>(src);
     const unsigned sblocks = qlh::blocks_for(g.n_groups, kBlock);
     const bool vec = g.n % 8 == 0 && qlh::aligned16(src);
-    if (vec && (g.gs == 16 || g.gs == 32 || g.gs == 64 || g.gs == 128 || g.gs == 256 || g.gs == 512)) {
+    if (vec && (g.gs == 8 || g.gs == 16 || g.gs == 32 || g.gs == 64 || g.gs == 128 || g.gs == 256 || g.gs == 512)) {
         const unsigned blocks = qlh::blocks_for(g.n / 8, (long long)kAbsIters * kBlock);
         switch (g.gs) {
+        case 8: hipLaunchKernelGGL(absmax_vec<1>, dim3(blocks), dim3(kBlock), 0, stream, x, g, mode, scales); break;
         case 16: hipLaunchKernelGGL(absmax_vec<2>, dim3(blocks), dim3(kBlock), 0, stream, x, g, mode, scales); break;
         case 32: hipLaunchKernelGGL(absmax_vec<4>, dim3(blocks), dim3(kBlock), 0, stream, x, g, mode, scales); break;
         case 64: hipLaunchKernelGGL(absmax_vec<8>, dim3(blocks), dim3(kBlock), 0, stream, x, g, mode, scales); break;
@@ -1879,6 +1936,10 @@ extern "C" hipError_t ql_fp8_scales(const uint16_t* src, int rows, int cols, int
         case 256: hipLaunchKernelGGL(absmax_vec<32>, dim3(blocks), dim3(kBlock), 0, stream, x, g, mode, scales); break;
         default: hipLaunchKernelGGL(absmax_vec<64>, dim3(blocks), dim3(kBlock), 0, stream, x, g, mode, scales); break;
         }
+    } else if (vec && g.gs % 8 == 0 && g.gs < 8 * 32) {
+        // several short groups per wavefront; it writes the final scales itself
+        QL_FP8_DISPATCH(format, mode, launch_quantize_segments, x, g, scales, nullptr, stream);
+        return hipGetLastError();
     } else if (vec && g.gs % 8 == 0 && g.gs <= 8LL * kWave * kWaveGroupVecs) {
         // one wavefront per group in registers; it writes the final scales itself
         QL_FP8_DISPATCH(format, mode, launch_quantize_wave_groups, x, g, scales, nullptr, stream);
@@ -1916,9 +1977,15 @@ extern "C" hipError_t ql_fp8_quantize(const uint16_t* src, int rows, int cols, i
     QL_CHECK_ARG(fmt_mode_ok(format, mode) && geom_for(rows, cols, granularity, group_size, g));
     if (g.n == 0) return hipSuccess;
     QL_CHECK_ARG(dst);
-    if (src && scales && g.n % 8 == 0 && qlh::aligned16(src) && ((uintptr_t)dst & 7) == 0 && g.gs >= 16 &&
+    if (src && scales && g.n % 8 == 0 && qlh::aligned16(src) && ((uintptr_t)dst & 7) == 0 && g.gs >= 8 &&
         g.gs <= 512 && (g.gs & (g.gs - 1)) == 0) {   // one pass: scales and codes together
         QL_FP8_DISPATCH(format, mode, launch_quantize_groups, reinterpret_cast<const _Float16*>(src), g, scales,
+                        dst, stream);
+        return hipGetLastError();
+    }
+    if (src && scales && g.n % 8 == 0 && g.gs % 8 == 0 && g.gs < 8 * 32 && qlh::aligned16(src) &&
+        ((uintptr_t)dst & 7) == 0) {   // several short groups per wavefront, one pass
+        QL_FP8_DISPATCH(format, mode, launch_quantize_segments, reinterpret_cast<const _Float16*>(src), g, scales,
                         dst, stream);
         return hipGetLastError();
     }

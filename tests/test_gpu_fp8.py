@@ -74,8 +74,12 @@ def same_f16(a, b):
     (8, 1024, ql.QUANT_PER_GROUP, 256), (16, 512, ql.QUANT_PER_GROUP, 512), (3, 200, ql.QUANT_PER_GROUP, 128),
     # ... and a partial last group (fewer lanes than the group spans)
     (3, 1000, ql.QUANT_PER_GROUP, 512), (5, 24, ql.QUANT_PER_GROUP, 16), (1, 8, ql.QUANT_PER_GROUP, 64),
-    # other multiples of 8 up to 16384 take the one-wavefront-per-group pass: up to 8,
-    # 16 and 32 vectors per lane, per-channel rows, partial last groups
+    (16, 64, ql.QUANT_PER_GROUP, 8), (3, 40, ql.QUANT_PER_GROUP, 8),   # groups of 8: one lane each
+    # other multiples of 8 below 256: 64 / V whole groups of V vectors per wavefront span
+    (7, 96, ql.QUANT_PER_GROUP, 24), (5, 120, ql.QUANT_PER_GROUP, 40), (6, 744, ql.QUANT_PER_GROUP, 248),
+    (3, 200, ql.QUANT_PER_GROUP, 56), (64, 960, ql.QUANT_PER_GROUP, 24), (33, 1000, ql.QUANT_PER_GROUP, 200),
+    # other multiples of 8 from 256 to 16384 take the one-wavefront-per-group pass: up
+    # to 8, 16 and 32 vectors per lane, per-channel rows, partial last groups
     (5, 1000, ql.QUANT_PER_GROUP, 200), (3, 1000, ql.QUANT_PER_GROUP, 1992), (7, 3000, ql.QUANT_PER_GROUP, 4104),
     (4, 8192, ql.QUANT_PER_CHANNEL, 0), (6, 14336, ql.QUANT_PER_CHANNEL, 0), (2, 16384, ql.QUANT_PER_GROUP, 16384),
     (9, 48, ql.QUANT_PER_GROUP, 48)])
@@ -94,8 +98,11 @@ def test_fp8_codec_bit_exact(mode, fmt, rows, cols, gran, gs):
 @pytest.mark.parametrize("rows,cols,gran,gs,offset", [
     (64, 256, ql.QUANT_PER_GROUP, 128, 0),       # power-of-two groups, 16-byte loads: every lane count
     (16, 512, ql.QUANT_PER_GROUP, 16, 0), (5, 96, ql.QUANT_PER_GROUP, 32, 0), (7, 64, ql.QUANT_PER_GROUP, 64, 0),
+    (3, 40, ql.QUANT_PER_GROUP, 8, 0),
     (8, 1024, ql.QUANT_PER_GROUP, 256, 0), (16, 512, ql.QUANT_PER_GROUP, 512, 0), (3, 200, ql.QUANT_PER_GROUP, 128, 0),
-    (5, 1000, ql.QUANT_PER_GROUP, 200, 0),       # one wavefront per group, scales only: 8, 16, 32 vectors a lane
+    (7, 96, ql.QUANT_PER_GROUP, 24, 0), (3, 200, ql.QUANT_PER_GROUP, 56, 0),   # several short groups a wavefront
+    (5, 1000, ql.QUANT_PER_GROUP, 200, 0), (64, 960, ql.QUANT_PER_GROUP, 24, 0),
+    (3, 2000, ql.QUANT_PER_GROUP, 400, 0),       # one wavefront per group, scales only: 8, 16, 32 vectors a lane
     (3, 6000, ql.QUANT_PER_CHANNEL, 0, 0), (4, 14336, ql.QUANT_PER_CHANNEL, 0, 0), (3, 8200, ql.QUANT_PER_CHANNEL, 0, 0),
     (5, 1000, ql.QUANT_PER_GROUP, 200, 1),       # unaligned source: element loads
     (3, 1000, ql.QUANT_PER_GROUP, 7, 0),
