@@ -231,6 +231,21 @@ __global__ __launch_bounds__(kBlock) void absmax_blocks_vec(const _Float16* __re
     }
 }
 
+// groups of at most 64 elements that are not a multiple of 8 (so groups start inside
+// 16-byte vectors): one thread per group reads its elements, and writes the final
+// scale (fmax / max, 1 below 1e-8) itself
+__global__ __launch_bounds__(kBlock) void absmax_thread(const _Float16* __restrict__ x, Geom g, int mode,
+                                                        float fmax, float* __restrict__ scales) {
+    const long long grp = (long long)blockIdx.x * kBlock + threadIdx.x;
+    if (grp >= g.n_groups) return;
+    const long long base = grp * g.gs;
+    const int len = (int)min(g.gs, g.n - base);
+    float m = 0.0f;
+    for (int i = 0; i < len; ++i)
+        if (seen(mode, i)) m = fmaxf(m, fabsf((float)x[base + i]));
+    scales[grp] = m < 1e-8f ? 1.0f : fmax / m;
+}
+
 __global__ void fill_zero(float* __restrict__ p, int n) {
     const int i = blockIdx.x * kBlock + threadIdx.x;
     if (i < n) p[i] = 0.0f;
@@ -245,15 +260,18 @@ __global__ void finalize_scales(float* __restrict__ s, int n, float fmax) {
 }
 
 // ---- quantize / dequantize ------------------------------------------------------------
-// 8 elements times their group's scale -> 8 codes
-template <int FMT, int MODE>
-__device__ __forceinline__ u32x2 encode8(const Vec<_Float16, 8>& v, float s) {
+// 8 elements times their group's scale -> 8 codes (s: one float, or one per element)
+template <int FMT, int MODE, typename S = float>
+__device__ __forceinline__ u32x2 encode8(const Vec<_Float16, 8>& v, const S& s) {
     uint32_t w[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         float f[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) f[e] = (float)v.v[4 * h + e] * s;
+        for (int e = 0; e < 4; ++e) {
+            if constexpr (std::is_same_v<S, float>) f[e] = (float)v.v[4 * h + e] * s;
+            else f[e] = (float)v.v[4 * h + e] * s[4 * h + e];
+        }
         if constexpr (MODE == QL_FP8_MODE_REFERENCE) {
             w[h] = enc_ref<FMT>(f[0]) | (enc_ref<FMT>(f[1]) << 8) | (enc_ref<FMT>(f[2]) << 16) |
                    (enc_ref<FMT>(f[3]) << 24);
@@ -264,7 +282,27 @@ __device__ __forceinline__ u32x2 encode8(const Vec<_Float16, 8>& v, float s) {
     return u32x2{w[0], w[1]};
 }
 
-// VEC: 8 elements per thread (n % 8 == 0, gs % 8 == 0, aligned); else one element.
+// The scales of the 8 elements from e0 (a multiple of 8): groups that are not a
+// multiple of 8 long start inside vectors.  From g0 = e0 / gs and r0 = e0 - g0 * gs,
+// element e is in group g0 + (r0 + e) / gs: g0 or g0 + 1 when gs >= 8 (two scale
+// loads, the second clamped to the last group), up to 8 groups below 8.
+__device__ __forceinline__ void scales8(const float* __restrict__ scales, const Geom& g, long long e0,
+                                        float (&s)[8]) {
+    const long long g0 = g.n_groups == 1 ? 0 : e0 / g.gs;   // per tensor: no 64-bit division
+    const long long r0 = e0 - g0 * g.gs;                     // < gs
+    if (g.gs >= 8) {
+        const float s0 = scales[g0];
+        const float s1 = scales[min(g0 + 1, (long long)g.n_groups - 1)];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s[e] = r0 + e < g.gs ? s0 : s1;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s[e] = scales[g0 + (r0 + e) / g.gs];
+    }
+}
+
+// VEC: 8 elements per thread (n % 8 == 0, 16-byte aligned x, 8-byte aligned q; groups
+// of a multiple of 8 take one scale per thread, others scales8); else one element.
 template <int FMT, int MODE, bool VEC>
 __global__ __launch_bounds__(kBlock) void quantize_kernel(const _Float16* __restrict__ x, Geom g,
                                                           const float* __restrict__ scales,
@@ -273,8 +311,14 @@ __global__ __launch_bounds__(kBlock) void quantize_kernel(const _Float16* __rest
     if constexpr (VEC) {
         if (t * 8 >= g.n) return;
         const Vec<_Float16, 8> v = load<true>(reinterpret_cast<const Vec<_Float16, 8>*>(x) + t);
-        const long long gi = g.n_groups == 1 ? 0 : (t * 8) / g.gs;   // per tensor: no 64-bit division
-        store<true>(reinterpret_cast<u32x2*>(q) + t, encode8<FMT, MODE>(v, scales[gi]));
+        if (g.gs % 8 == 0) {   // uniform
+            const long long gi = g.n_groups == 1 ? 0 : (t * 8) / g.gs;   // per tensor: no 64-bit division
+            store<true>(reinterpret_cast<u32x2*>(q) + t, encode8<FMT, MODE>(v, scales[gi]));
+        } else {
+            float s8[8];
+            scales8(scales, g, t * 8, s8);
+            store<true>(reinterpret_cast<u32x2*>(q) + t, encode8<FMT, MODE>(v, s8));
+        }
     } else {
         if (t >= g.n) return;
         const float f = (float)x[t] * scales[t / g.gs];
@@ -489,8 +533,36 @@ __global__ __launch_bounds__(kBlock) void dequantize_kernel(const uint8_t* __res
     if constexpr (VEC) {
         if (t * 8 >= g.n) return;
         const u32x2 w = load<true>(reinterpret_cast<const u32x2*>(q) + t);
-        const float s = scales[(t * 8) / g.gs];
         Vec<_Float16, 8> out;
+        if (g.gs % 8) {   // uniform: groups start inside vectors
+            float s8[8];
+            scales8(scales, g, t * 8, s8);
+            bool ok = true;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ok = ok && recip_ok(s8[e]);
+            if (ok) {   // both forms give RN(d / s); at most 2 distinct scales when gs >= 8
+                float r8[8];
+                if (g.gs >= 8) {   // s8 holds the scales of at most two groups, in order
+                    const float ra = 1.0f / s8[0], rb = 1.0f / s8[7];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) r8[e] = s8[e] == s8[0] ? ra : rb;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) r8[e] = 1.0f / s8[e];
+                }
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    out.v[e] = from_f32<_Float16>(
+                        div_by_recip(decode1<FMT, MODE>((w[e >> 2] >> (8 * (e & 3))) & 0xFFu), s8[e], r8[e]));
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    out.v[e] = from_f32<_Float16>(decode1<FMT, MODE>((w[e >> 2] >> (8 * (e & 3))) & 0xFFu) / s8[e]);
+            }
+            store<true>(reinterpret_cast<Vec<_Float16, 8>*>(y) + t, out);
+            return;
+        }
+        const float s = scales[(t * 8) / g.gs];
         if (recip_ok(s)) {
             const float r = 1.0f / s;
 #pragma unroll
@@ -1944,6 +2016,10 @@ extern "C" hipError_t ql_fp8_scales(const uint16_t* src, int rows, int cols, int
         // one wavefront per group in registers; it writes the final scales itself
         QL_FP8_DISPATCH(format, mode, launch_quantize_wave_groups, x, g, scales, nullptr, stream);
         return hipGetLastError();
+    } else if (g.gs <= 64 && g.gs % 8) {
+        hipLaunchKernelGGL(absmax_thread, dim3(sblocks), dim3(kBlock), 0, stream, x, g, mode, fp8_max(format),
+                           scales);
+        return hipGetLastError();
     } else if (g.gs <= 8192) {
         hipLaunchKernelGGL(absmax_wave, dim3(qlh::blocks_for(g.n_groups, kBlock / kWave)), dim3(kBlock),
                            0, stream, x, g, mode, scales);
@@ -1997,7 +2073,7 @@ extern "C" hipError_t ql_fp8_quantize(const uint16_t* src, int rows, int cols, i
     }
     const hipError_t e = ql_fp8_scales(src, rows, cols, format, granularity, group_size, mode, scales, stream);
     if (e != hipSuccess) return e;
-    const bool vec = g.n % 8 == 0 && g.gs % 8 == 0 && qlh::aligned16(src) && ((uintptr_t)dst & 7) == 0;
+    const bool vec = g.n % 8 == 0 && qlh::aligned16(src) && ((uintptr_t)dst & 7) == 0;
     QL_FP8_DISPATCH(format, mode, launch_quantize, reinterpret_cast<const _Float16*>(src), g, scales,
                     dst, vec, stream);
     return hipGetLastError();
@@ -2012,7 +2088,7 @@ extern "C" hipError_t ql_fp8_dequantize(const uint8_t* src, const float* scales,
     QL_CHECK_ARG(src && scales && dst);
     // the reference's decoder throughout (its +0 for code 0x80 included): cheap here
     if (mode == QL_FP8_MODE_REFERENCE_CLEAN) mode = QL_FP8_MODE_REFERENCE;
-    const bool vec = g.n % 8 == 0 && g.gs % 8 == 0 && qlh::aligned16(dst) && ((uintptr_t)src & 7) == 0;
+    const bool vec = g.n % 8 == 0 && qlh::aligned16(dst) && ((uintptr_t)src & 7) == 0;
     QL_FP8_DISPATCH(format, mode, launch_dequantize, src, g, scales, reinterpret_cast<_Float16*>(dst),
                     vec, stream);
     return hipGetLastError();

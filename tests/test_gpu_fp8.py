@@ -24,7 +24,7 @@ import pytest
 
 import oracle as orc
 import quantlib_amd as ql
-from helpers import dev, empty, f16_bits_to_f32, host, normal, stream, to_f16_bits, uniform
+from helpers import Out, dev, empty, f16_bits_to_f32, host, normal, stream, to_f16_bits, uniform
 
 pytestmark = pytest.mark.gpu
 
@@ -39,20 +39,21 @@ def n_scales(rows, cols, gran, gs):
 
 
 def gpu_quantize(x, fmt, gran, gs, mode):
+    # codes and scales between guard bands: a write past either fails the test
     rows, cols = x.shape
-    q = empty((rows * cols,), np.uint8)
-    sc = empty((max(n_scales(rows, cols, gran, gs), 1),), np.float32)
+    q = Out(rows * cols, np.uint8, offset=8)
+    sc = Out(n_scales(rows, cols, gran, gs), np.float32)
     dx = dev(x)
     ql.call("ql_fp8_quantize", dx.ptr, rows, cols, fmt, gran, gs, mode, q.ptr, sc.ptr, stream())
-    return host(q, shape=(rows, cols)), host(sc)[:n_scales(rows, cols, gran, gs)]
+    return q.get(shape=(rows, cols)), sc.get()
 
 
 def gpu_dequantize(q, sc, fmt, gran, gs, mode):
     rows, cols = q.shape
-    out = empty((rows * cols,), np.uint16)
+    out = Out(rows * cols, np.uint16, offset=8)
     dq, ds = dev(q), dev(sc)
     ql.call("ql_fp8_dequantize", dq.ptr, ds.ptr, rows, cols, fmt, gran, gs, mode, out.ptr, stream())
-    return host(out, shape=(rows, cols))
+    return out.get(shape=(rows, cols))
 
 
 def same_f16(a, b):
@@ -82,7 +83,12 @@ def same_f16(a, b):
     # to 8, 16 and 32 vectors per lane, per-channel rows, partial last groups
     (5, 1000, ql.QUANT_PER_GROUP, 200), (3, 1000, ql.QUANT_PER_GROUP, 1992), (7, 3000, ql.QUANT_PER_GROUP, 4104),
     (4, 8192, ql.QUANT_PER_CHANNEL, 0), (6, 14336, ql.QUANT_PER_CHANNEL, 0), (2, 16384, ql.QUANT_PER_GROUP, 16384),
-    (9, 48, ql.QUANT_PER_GROUP, 48)])
+    (9, 48, ql.QUANT_PER_GROUP, 48),
+    # lengths that are not a multiple of 8 (groups start inside 16-byte vectors): one
+    # thread per group up to 64 for the scales, then 8 elements per thread with each
+    # element's own group scale, also below 8
+    (16, 360, ql.QUANT_PER_GROUP, 36), (8, 1000, ql.QUANT_PER_GROUP, 3), (4, 1000, ql.QUANT_PER_GROUP, 1),
+    (6, 64, ql.QUANT_PER_GROUP, 65), (2, 4096, ql.QUANT_PER_GROUP, 63), (7, 1000, ql.QUANT_PER_CHANNEL, 0)])
 def test_fp8_codec_bit_exact(mode, fmt, rows, cols, gran, gs):
     x = to_f16_bits(uniform(rows + cols + gs, (rows, cols), -1.0, 1.0) *
                     np.float32(1.0 if fmt == ql.FP8_E4M3 else 300.0))
@@ -105,7 +111,8 @@ def test_fp8_codec_bit_exact(mode, fmt, rows, cols, gran, gs):
     (3, 2000, ql.QUANT_PER_GROUP, 400, 0),       # one wavefront per group, scales only: 8, 16, 32 vectors a lane
     (3, 6000, ql.QUANT_PER_CHANNEL, 0, 0), (4, 14336, ql.QUANT_PER_CHANNEL, 0, 0), (3, 8200, ql.QUANT_PER_CHANNEL, 0, 0),
     (5, 1000, ql.QUANT_PER_GROUP, 200, 1),       # unaligned source: element loads
-    (3, 1000, ql.QUANT_PER_GROUP, 7, 0),
+    (3, 1000, ql.QUANT_PER_GROUP, 7, 0), (8, 1000, ql.QUANT_PER_GROUP, 3, 0),   # one thread per group
+    (16, 360, ql.QUANT_PER_GROUP, 36, 0), (4, 1000, ql.QUANT_PER_GROUP, 36, 1), (2, 4096, ql.QUANT_PER_GROUP, 63, 0),
     (1024, 1024, ql.QUANT_PER_TENSOR, 0, 0),     # groups over many workgroups, 16-byte loads
     (4096, 4096, ql.QUANT_PER_TENSOR, 0, 0), (2, 20000, ql.QUANT_PER_CHANNEL, 0, 0),
     (3, 9001, ql.QUANT_PER_CHANNEL, 0, 0),       # ... element loads (n % 8 != 0)
