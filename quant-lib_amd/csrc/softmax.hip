@@ -31,7 +31,13 @@ __device__ __forceinline__ float softmax_exp(float y) {
     else return exp_f32_fast(y);
 }
 
-template <typename D, int NV, int WPR, bool FULL>
+// ANY: rows of any length, whose starts need not be 16-byte aligned (in and out at
+// the same offset modulo 16): a row's vectors are the aligned 16-byte vectors that
+// cover it, the first starting p elements before the row; elements outside the row
+// count as -inf, and the first and last vectors, shared with the neighbouring rows,
+// are stored element by element.  (An aligned 16-byte vector never crosses a page,
+// so the covering loads stay within mapped memory.)
+template <typename D, int NV, int WPR, bool FULL, bool ANY = false>
 __global__ __launch_bounds__(WPR <= 4 ? kBlock : kWave * WPR) void softmax_rows(
     const D* __restrict__ in, D* __restrict__ out, int rows, int cols) {
     constexpr int W = vec16<D>();
@@ -44,9 +50,10 @@ __global__ __launch_bounds__(WPR <= 4 ? kBlock : kWave * WPR) void softmax_rows(
     const int row = blockIdx.x * RPB + tid / TPR;
     const int rl = tid % TPR;
     const bool row_ok = row < rows;
-    const int nvec = cols / W;
     const size_t roff = (size_t)(row_ok ? row : rows - 1) * (size_t)cols;
-    const V* src = reinterpret_cast<const V*>(in + roff);
+    const int p = ANY ? (int)((reinterpret_cast<uintptr_t>(in + roff) & 15) / sizeof(D)) : 0;
+    const int nvec = ANY ? (p + cols + W - 1) / W : cols / W;
+    const V* src = reinterpret_cast<const V*>(in + roff - p);
 
     // every lane loads (an index past the row re-reads its last vector, masked
     // below): a load under a per-lane test makes the compiler wait for it before
@@ -62,10 +69,14 @@ __global__ __launch_bounds__(WPR <= 4 ? kBlock : kWave * WPR) void softmax_rows(
         const int vi = rl + k * TPR;
         const bool ok = FULL || vi < nvec;
 #pragma unroll
-        for (int e = 0; e < W; ++e) {
-            v[k][e] = ok ? to_f32(raw[k].v[e]) : -INFINITY;
-            m = fmaxf(m, v[k][e]);
+        for (int e = 0; e < W; ++e) v[k][e] = ok ? to_f32(raw[k].v[e]) : -INFINITY;
+        if (ANY && ok && (vi * W < p || vi * W + W - p > cols)) {   // the row's first or last vector
+#pragma unroll
+            for (int e = 0; e < W; ++e)
+                if (vi * W + e - p < 0 || vi * W + e - p >= cols) v[k][e] = -INFINITY;
         }
+#pragma unroll
+        for (int e = 0; e < W; ++e) m = fmaxf(m, v[k][e]);
     }
     m = wave_max(m);
     if constexpr (WPR > 1) {
@@ -100,7 +111,7 @@ __global__ __launch_bounds__(WPR <= 4 ? kBlock : kWave * WPR) void softmax_rows(
     const float inv = 1.0f / s;
 
     if (!row_ok) return;
-    V* dst = reinterpret_cast<V*>(out + roff);
+    V* dst = reinterpret_cast<V*>(out + roff - p);
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
         const int vi = rl + k * TPR;
@@ -108,7 +119,14 @@ __global__ __launch_bounds__(WPR <= 4 ? kBlock : kWave * WPR) void softmax_rows(
             V y;
 #pragma unroll
             for (int e = 0; e < W; ++e) y.v[e] = from_f32<D>(v[k][e] * inv);
-            store<true>(dst + vi, y);
+            if (!ANY || (vi * W >= p && vi * W + W - p <= cols)) {
+                store<true>(dst + vi, y);
+            } else {   // a vector shared with a neighbouring row: this row's elements only
+                D* d = out + roff - p + (size_t)vi * W;
+#pragma unroll
+                for (int e = 0; e < W; ++e)
+                    if (vi * W + e - p >= 0 && vi * W + e - p < cols) d[e] = y.v[e];
+            }
         }
     }
 }
@@ -149,12 +167,15 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_generic(const D* __restri
         out[roff + c] = from_f32<D>(softmax_exp<D>(to_f32(in[roff + c]) - m) * inv);
 }
 
-template <typename D, int NV, int WPR>
+template <typename D, int NV, int WPR, bool ANY = false>
 hipError_t launch_fast(const D* in, D* out, int rows, int cols, hipStream_t stream) {
     constexpr int BLOCK = WPR <= 4 ? kBlock : kWave * WPR;
     constexpr int RPB = BLOCK / (kWave * WPR);
     const dim3 grid(qlh::blocks_for(rows, RPB));
-    if (cols / vec16<D>() == NV * kWave * WPR)
+    if constexpr (ANY)
+        hipLaunchKernelGGL((softmax_rows<D, NV, WPR, false, true>), grid, dim3(BLOCK), 0, stream, in,
+                           out, rows, cols);
+    else if (cols / vec16<D>() == NV * kWave * WPR)
         hipLaunchKernelGGL((softmax_rows<D, NV, WPR, true>), grid, dim3(BLOCK), 0, stream, in,
                            out, rows, cols);
     else
@@ -171,6 +192,32 @@ hipError_t softmax_dispatch(const D* in, D* out, int rows, int cols, hipStream_t
     QL_CHECK_ARG(in && out);
     constexpr int W = vec16<D>();
     const bool vec_ok = cols % W == 0 && qlh::aligned16(in) && qlh::aligned16(out);
+    // other lengths or element-aligned pointers: the covering aligned vectors of each
+    // row, when in and out share their offset mod 16
+    const bool any = !vec_ok && (reinterpret_cast<uintptr_t>(in) & (sizeof(D) - 1)) == 0 &&
+                     ((reinterpret_cast<uintptr_t>(in) - reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+    if (any) {   // at most (cols + 2W - 2) / W covering vectors
+        const int nv = (cols + 2 * W - 2) / W;
+        if (nv <= 64) return launch_fast<D, 1, 1, true>(in, out, rows, cols, stream);
+        if (nv <= 128) return launch_fast<D, 2, 1, true>(in, out, rows, cols, stream);
+        if constexpr (sizeof(D) == 2) {
+            if (nv <= 256) return launch_fast<D, 4, 1, true>(in, out, rows, cols, stream);
+            if (nv <= 512) return launch_fast<D, 8, 1, true>(in, out, rows, cols, stream);
+            if (nv <= 576) return launch_fast<D, 9, 1, true>(in, out, rows, cols, stream);
+        } else {
+            if (nv <= 256) return launch_fast<D, 2, 2, true>(in, out, rows, cols, stream);
+            if (nv <= 512) return launch_fast<D, 2, 4, true>(in, out, rows, cols, stream);
+        }
+        if (nv <= 1024) return launch_fast<D, 2, 8, true>(in, out, rows, cols, stream);
+        if (nv <= 1536) return launch_fast<D, 3, 8, true>(in, out, rows, cols, stream);
+        if (nv <= 2048) return launch_fast<D, 2, 16, true>(in, out, rows, cols, stream);
+        if (nv <= 3072) return launch_fast<D, 3, 16, true>(in, out, rows, cols, stream);
+        if (nv <= 4096) return launch_fast<D, 4, 16, true>(in, out, rows, cols, stream);
+        if (nv <= 6144) return launch_fast<D, 6, 16, true>(in, out, rows, cols, stream);
+        if (nv <= 8192) return launch_fast<D, 8, 16, true>(in, out, rows, cols, stream);
+        if (nv <= 12288) return launch_fast<D, 12, 16, true>(in, out, rows, cols, stream);
+        if (nv <= 16384) return launch_fast<D, 16, 16, true>(in, out, rows, cols, stream);
+    }
     const int nvec = cols / W;
     if (vec_ok) {
         if (nvec <= 64) return launch_fast<D, 1, 1>(in, out, rows, cols, stream);

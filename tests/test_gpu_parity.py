@@ -398,6 +398,49 @@ def test_softmax_widths(f16, rows, cols):
         check_close(out.get((rows, cols)), want, RTOL_F32, ATOL_F32, f"softmax f32 {rows}x{cols}")
 
 
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("rows,cols,in_off,out_off", [
+    (100, 3, 0, 0), (33, 7, 1, 1), (17, 33, 3, 3), (9, 1001, 0, 0), (9, 1001, 5, 5), (6, 4095, 2, 2),
+    (5, 4097, 0, 0), (3, 16383, 1, 1), (3, 32001, 0, 0), (2, 50257, 7, 7), (4, 1024, 1, 1),
+    (5, 1001, 1, 0), (5, 1001, 0, 3)])   # last two: in and out at different offsets mod 16
+def test_softmax_rows_at_any_offset(f16, rows, cols, in_off, out_off):
+    # Rows whose starts are not 16-byte aligned (lengths not a multiple of a vector,
+    # or offset pointers) take the covering aligned vectors of each row, storing the
+    # vectors shared with a neighbouring row element by element; in and out at
+    # different offsets take the block-per-row loop.  Guard bands catch stray writes.
+    x = normal(900 + cols + in_off, (rows, cols), sigma=2.0)
+    if cols > 3:
+        x[-1, -3:] = -np.inf
+    if f16:
+        x = _f16(x)
+    out = Out(rows * cols, np.uint16 if f16 else np.float32, offset=out_off)
+    dx = dev(x, in_off)
+    ql.call("ql_softmax_f16" if f16 else "ql_softmax_f32", ptr(dx), out.ptr, rows, cols, stream())
+    want = orc.softmax(x, f16=f16)
+    if f16:
+        check_f16(out.get((rows, cols)), want, f"softmax f16 {rows}x{cols} +{in_off}/+{out_off}")
+    else:
+        check_close(out.get((rows, cols)), want, RTOL_F32, ATOL_F32, f"softmax f32 {rows}x{cols} +{in_off}/+{out_off}")
+
+
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("rows,cols,off", [(9, 1001, 0), (6, 4095, 3), (40, 5, 1)])
+def test_softmax_in_place_rows_at_any_offset(f16, rows, cols, off):
+    # in place: a row's covering loads read neighbouring rows' elements, which their
+    # own workgroups may already have overwritten; those are never used
+    x = normal(950 + cols, (rows, cols), sigma=2.0)
+    if f16:
+        x = _f16(x)
+    d = dev(x, off)
+    ql.call("ql_softmax_f16" if f16 else "ql_softmax_f32", ptr(d), ptr(d), rows, cols, stream())
+    got = host(d, shape=(rows, cols))
+    want = orc.softmax(x, f16=f16)
+    if f16:
+        check_f16(got, want, f"in-place softmax f16 {rows}x{cols}")
+    else:
+        check_close(got, want, RTOL_F32, ATOL_F32, f"in-place softmax f32 {rows}x{cols}")
+
+
 @pytest.mark.parametrize("cols", [256, 1001])
 def test_softmax_fully_masked_row_is_nan_like_reference(cols):
     x = normal(77, (3, cols))
