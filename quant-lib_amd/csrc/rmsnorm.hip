@@ -13,8 +13,9 @@
 // one contiguous 1 KiB span).  x (and d) are read once and y (and x') written
 // once: 2 (4 fused) row transfers per row, the HBM minimum, with nontemporal
 // hints on the streamed rows and ordinary (cached) loads of the shared weight.
-// Rows too wide for registers, or unaligned layouts, take a block-per-row loop
-// that re-reads x.
+// Other lengths and offsets hold the row's covering aligned vectors in registers;
+// rows too wide for registers, or x, d and out at different offsets modulo 16,
+// take a block-per-row loop that re-reads x.
 #include "ql_common.hpp"
 #include "quantlib_amd.h"
 
@@ -197,6 +198,156 @@ __global__ __launch_bounds__(kWave) void rmsnorm_wave(D* x, const D* __restrict_
     }
 }
 
+// Elements S .. S + W - 1 of the concatenation a:b.
+template <int S, typename V>
+__device__ __forceinline__ V take(const V& a, const V& b) {
+    constexpr int W = sizeof(V) / sizeof(a.v[0]);
+    V r;
+#pragma unroll
+    for (int e = 0; e < W; ++e) r.v[e] = e + S < W ? a.v[e + S] : b.v[e + S - W];
+    return r;
+}
+
+// take<s>(a, b) for a wavefront-uniform s in [0, W)
+template <typename V>
+__device__ __forceinline__ V take_at(int s, const V& a, const V& b) {
+    constexpr int W = sizeof(V) / sizeof(a.v[0]);
+    switch (s) {
+    case 0: return a;
+    case 1: return take<1>(a, b);
+    case 2: return take<2>(a, b);
+    case 3: return take<3>(a, b);
+    default:
+        if constexpr (W > 4) {
+            switch (s) {
+            case 4: return take<4>(a, b);
+            case 5: return take<5>(a, b);
+            case 6: return take<6>(a, b);
+            default: return take<7>(a, b);
+            }
+        }
+        return a;
+    }
+}
+
+// Rows of any length whose starts need not be 16-byte aligned (x, d and out at one
+// offset modulo 16): WPR wavefronts per row, each lane NV of the aligned 16-byte
+// vectors that cover the row, the first starting p elements before it.  Elements
+// outside the row add nothing to the sum and are not written: the row's first and
+// last vectors, shared with the neighbouring rows, are stored element by element.
+// The weights of a vector's columns c0 .. c0 + W - 1 are two aligned vectors of w
+// (w at its own offset pw) shifted by s = (pw + c0) mod W, which is the same for
+// every vector of a row; the first and last pair are clamped to w's covering
+// vectors, which changes only weights of columns outside the row.  (An aligned
+// 16-byte vector never crosses a page, so the covering loads stay within mapped
+// memory.)
+// One row per workgroup of blockDim.x = 64 * wpr threads (wpr <= 16, chosen by the
+// host as the fewest wavefronts whose NV vectors per lane cover the row, so few
+// lanes sit idle and as many rows as fit stay in flight per CU).
+constexpr int kAnyMaxWaves = 16;
+
+template <typename D, int NV, bool ADD>
+__global__ __launch_bounds__(kWave * kAnyMaxWaves) void rmsnorm_any(
+    D* x, const D* __restrict__ d, const D* __restrict__ w, D* __restrict__ out, int rows, int dim,
+    float eps) {
+    constexpr int W = vec16<D>();
+    using V = Vec<D, W>;
+
+    const int tid = threadIdx.x;
+    const int TPR = blockDim.x;
+    const int row = blockIdx.x;
+    const int rl = tid;
+    const bool row_ok = true;
+    (void)rows;
+    const size_t roff = (size_t)row * (size_t)dim;
+    const int p = (int)((reinterpret_cast<uintptr_t>(x + roff) & 15) / sizeof(D));
+    const int nvec = (p + dim + W - 1) / W;
+    const V* xr = reinterpret_cast<const V*>(x + roff - p);
+    const V* dr = reinterpret_cast<const V*>(ADD ? d + roff - p : d);
+
+    const int pw = (int)((reinterpret_cast<uintptr_t>(w) & 15) / sizeof(D));
+    const V* wa = reinterpret_cast<const V*>(w - pw);
+    const int wlast = (pw + dim - 1) / W;   // w's last covering vector
+    const int sh = (pw - p + W) % W;
+    V xv[NV], dv[ADD ? NV : 1], w0[NV], w1[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {   // the shared weight first (cached), then the row
+        const int ja = (pw + min(rl + k * TPR, nvec - 1) * W - p + W) / W - 1;   // floor, >= -1
+        w0[k] = wa[min(max(ja, 0), wlast)];
+        w1[k] = wa[min(ja + 1, wlast)];
+    }
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int vi = min(rl + k * TPR, nvec - 1);
+        xv[k] = load<true>(xr + vi);
+        if constexpr (ADD) dv[k] = load<true>(dr + vi);
+    }
+    __builtin_amdgcn_sched_barrier(0);   // every load issued before any arithmetic
+    V wv[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) wv[k] = take_at(sh, w0[k], w1[k]);
+
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int vi = rl + k * TPR;
+#pragma unroll
+        for (int e = 0; e < W; ++e) {
+            float a = to_f32(xv[k].v[e]);
+            if constexpr (ADD) {
+                a = a + to_f32(dv[k].v[e]);
+                xv[k].v[e] = from_f32<D>(a);
+                a = to_f32(xv[k].v[e]);
+            }
+            const int c = vi * W + e - p;
+            a = c >= 0 && c < dim ? a : 0.0f;   // vectors past the row: c >= dim
+            ss = fmaf(a, a, ss);
+        }
+    }
+    ss = wave_sum(ss);
+    const int wpr = TPR / kWave;   // uniform
+    if (wpr > 1) {
+        __shared__ float red[kAnyMaxWaves];
+        if ((tid & (kWave - 1)) == 0) red[tid / kWave] = ss;
+        __syncthreads();
+        ss = 0.0f;
+        for (int i = 0; i < wpr; ++i) ss += red[i];
+    }
+    if (!row_ok) return;
+    const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int vi = rl + k * TPR;
+        if (vi < nvec) {
+            V y;
+#pragma unroll
+            for (int e = 0; e < W; ++e) y.v[e] = from_f32<D>((to_f32(xv[k].v[e]) * inv) * to_f32(wv[k].v[e]));
+            if (vi * W >= p && vi * W + W - p <= dim) {
+                if constexpr (ADD) store<true>(reinterpret_cast<V*>(x + roff - p) + vi, xv[k]);
+                store<true>(reinterpret_cast<V*>(out + roff - p) + vi, y);
+            } else {   // shared with a neighbouring row: this row's elements only
+#pragma unroll
+                for (int e = 0; e < W; ++e) {
+                    const int c = vi * W + e - p;
+                    if (c >= 0 && c < dim) {
+                        if constexpr (ADD) x[roff + c] = xv[k].v[e];
+                        out[roff + c] = y.v[e];
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <typename D, int NV, bool ADD>
+hipError_t launch_any(D* x, const D* d, const D* w, D* out, int rows, int nv, int dim, float eps,
+                      hipStream_t stream) {
+    const int wpr = (nv + NV * kWave - 1) / (NV * kWave);   // <= kAnyMaxWaves by the caller's choice of NV
+    hipLaunchKernelGGL((rmsnorm_any<D, NV, ADD>), dim3((unsigned)rows), dim3(kWave * wpr), 0, stream, x, d, w,
+                       out, rows, dim, eps);
+    return hipGetLastError();
+}
+
 // Block-per-row loop for any dim / alignment.  Same arithmetic; x' is written
 // in the first pass and re-read by the same thread in the second.
 template <typename D, bool ADD>
@@ -300,6 +451,20 @@ hipError_t rmsnorm_dispatch(D* x, const D* d, const D* w, D* out, int rows, int 
         if (nvec <= 2048) return launch_fast<D, 2, 16, ADD>(x, d, w, out, rows, dim, eps, stream);
         if (nvec <= 4096) return launch_fast<D, 4, 16, ADD>(x, d, w, out, rows, dim, eps, stream);
         if (nvec <= 8192) return launch_fast<D, 8, 16, ADD>(x, d, w, out, rows, dim, eps, stream);
+    }
+    // other lengths or offsets: the covering aligned vectors of each row, when x, d and
+    // out share their offset mod 16 (at most (dim + 2W - 2) / W vectors a row).  As on
+    // the aligned path, the fused add takes one vector per lane and plain RMSNorm two,
+    // over as many wavefronts as cover the row (up to 16), then 2-8 over 16.
+    const uintptr_t xa = reinterpret_cast<uintptr_t>(x);
+    const bool any = (xa & (sizeof(D) - 1)) == 0 && ((xa - reinterpret_cast<uintptr_t>(out)) & 15) == 0 &&
+                     (!ADD || ((xa - reinterpret_cast<uintptr_t>(d)) & 15) == 0);
+    const int nv = (dim + 2 * W - 2) / W;
+    if (any) {
+        if (nv <= (ADD ? 1024 : 64)) return launch_any<D, 1, ADD>(x, d, w, out, rows, nv, dim, eps, stream);
+        if (nv <= 2048) return launch_any<D, 2, ADD>(x, d, w, out, rows, nv, dim, eps, stream);
+        if (nv <= 4096) return launch_any<D, 4, ADD>(x, d, w, out, rows, nv, dim, eps, stream);
+        if (nv <= 8192) return launch_any<D, 8, ADD>(x, d, w, out, rows, nv, dim, eps, stream);
     }
     hipLaunchKernelGGL((rmsnorm_rows_generic<D, ADD>), dim3((unsigned)rows), dim3(kBlock), 0,
                        stream, x, d, w, out, rows, dim, eps);

@@ -136,6 +136,82 @@ def test_rmsnorm_variant_widths(f16, add, rows, dim):
         check_close(out.get((rows, dim)), want, RTOL_F32, ATOL_F32, tag)
 
 
+# Lengths that are not a multiple of a 16-byte vector, or rows at an offset: each row
+# holds the aligned vectors that cover it (1 vector per lane over 1-16 wavefronts,
+# then 2, 4, 8 per lane over 16), the vectors shared with a neighbouring row stored
+# element by element.  One width per variant for each type, plain and fused; x, d
+# and out at one offset mod 16 (and, last, at different offsets: the block-per-row
+# loop).  Outputs between guard bands.
+ANY_WIDTHS_F16 = [33, 1001, 2001, 4001, 4095, 10001, 30001, 65001]
+ANY_WIDTHS_F32 = [33, 501, 1001, 2001, 4001, 8001, 16001, 32001]
+
+
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("add", [False, True])
+@pytest.mark.parametrize("wi", range(8))
+@pytest.mark.parametrize("off", [0, 3])
+def test_rmsnorm_rows_at_any_offset(f16, add, wi, off):
+    dim = (ANY_WIDTHS_F16 if f16 else ANY_WIDTHS_F32)[wi]
+    rows = 5 if dim > 4096 else 37
+    x = normal(0x51A10091 + dim + off, (rows, dim))
+    d = normal(0x51A10092 + dim, (rows, dim))
+    w = uniform(0x51A10093 + dim, dim, 0.5, 1.5)
+    if f16:
+        x, d, w = _f16(x), _f16(d), _f16(w)
+    dt = np.uint16 if f16 else np.float32
+    out = Out(rows * dim, dt, offset=off)
+    dx, dd, dw = dev(x, off), dev(d, off), dev(w, 1)
+    sfx = "f16" if f16 else "f32"
+    tag = f"{'add_' if add else ''}rmsnorm {sfx} {rows}x{dim} +{off}"
+    if add:
+        ql.call(f"ql_add_rmsnorm_{sfx}", ptr(dx), ptr(dd), ptr(dw), out.ptr, rows, dim, 1e-5, stream())
+        want_x, want = orc.add_rmsnorm(x, d, w, 1e-5, f16=f16)
+        assert np.array_equal(host(dx, shape=(rows, dim)), want_x), tag
+    else:
+        ql.call(f"ql_rmsnorm_{sfx}", ptr(dx), ptr(dw), out.ptr, rows, dim, 1e-5, stream())
+        want = orc.rmsnorm(x, w, 1e-5, f16=f16)
+        assert np.array_equal(host(dx, shape=(rows, dim)), x), tag
+    if f16:
+        check_f16(out.get((rows, dim)), want, tag)
+    else:
+        check_close(out.get((rows, dim)), want, RTOL_F32, ATOL_F32, tag)
+
+
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("add,x_off,d_off,out_off,inplace", [
+    (False, 1, 0, 1, True), (False, 6, 0, 6, True), (True, 2, 2, 0, False), (False, 1, 0, 0, False),
+    (True, 0, 3, 0, False)])
+def test_rmsnorm_any_in_place_and_mixed_offsets(f16, add, x_off, d_off, out_off, inplace):
+    # plain RMSNorm in place (out = x, as the reference's two-pass kernel allows): a
+    # row's covering loads read neighbouring rows' elements, which their own
+    # workgroups may have overwritten already and which are never used; x, d and
+    # out at different offsets mod 16 take the block-per-row loop
+    rows, dim = 4097, 1001
+    x = normal(0x51A100A1 + x_off, (rows, dim))
+    d = normal(0x51A100A2, (rows, dim))
+    w = uniform(0x51A100A3, dim, 0.5, 1.5)
+    if f16:
+        x, d, w = _f16(x), _f16(d), _f16(w)
+    dt = np.uint16 if f16 else np.float32
+    sfx = "f16" if f16 else "f32"
+    dx, dd, dw = dev(x, x_off), dev(d, d_off), dev(w)
+    out = None if inplace else Out(rows * dim, dt, offset=out_off)
+    optr = ptr(dx) if inplace else out.ptr
+    if add:
+        ql.call(f"ql_add_rmsnorm_{sfx}", ptr(dx), ptr(dd), ptr(dw), optr, rows, dim, 1e-5, stream())
+        want_x, want = orc.add_rmsnorm(x, d, w, 1e-5, f16=f16)
+    else:
+        ql.call(f"ql_rmsnorm_{sfx}", ptr(dx), ptr(dw), optr, rows, dim, 1e-5, stream())
+        want_x, want = x, orc.rmsnorm(x, w, 1e-5, f16=f16)
+    got = host(dx, shape=(rows, dim)) if inplace else out.get((rows, dim))
+    if not inplace:
+        assert np.array_equal(host(dx, shape=(rows, dim)), want_x)
+    if f16:
+        check_f16(got, want, f"rmsnorm f16 in place={inplace}")
+    else:
+        check_close(got, want, RTOL_F32, ATOL_F32, f"rmsnorm f32 in place={inplace}")
+
+
 @pytest.mark.parametrize("f16", [False, True])
 def test_rmsnorm_unaligned_pointers(f16):
     rows, dim = 9, 2048
