@@ -14,8 +14,8 @@
 //   y0  = fma(x0, c, -(x1*s)),  y1 = fma(x0, s, x1*c)
 // Pairing: interleaved (2i, 2i+1) as the reference, or rotate-half (i, i+d/2).
 //
-// Fast path (d/2 <= 64 pairs, 16-byte aligned rows, head chunks that tile a
-// wavefront): inv_freq is computed once per call on the host (the same libm
+// Fast path (d/2 <= 64 pairs, 16-byte aligned rows; a wavefront pass takes as many
+// whole heads' 16-byte chunks as fit its 64 lanes): inv_freq is computed once per call on the host (the same libm
 // pow the CPU restatement uses) and passed by value.  One wavefront serves a
 // (token, group of heads): every lane first issues the loads of all 16-byte
 // chunks it owns (at most MAXU, or MAXU pairs of chunks for rotate-half), then
@@ -135,13 +135,14 @@ __global__ __launch_bounds__(kBlock) void rope_fast(D* q, D* k, int n_tokens, in
     const int t = blockIdx.x * (kBlock / kWave) + __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
     if (t >= n_tokens) return;  // wavefront-uniform; no barriers below
     const int npairs = d >> 1;
-    const int S = npairs / PPS;  // slots per head; divides 64
+    const int S = npairs / PPS;        // slots per head (<= 64)
+    const int SPW = (kWave / S) * S;   // slots per wavefront pass: whole heads, lanes past it idle
     const int j = lane % S;
     const int hrot = hq + hk;                          // heads that rotate
     const int htot = hrot + (CACHE != kNoCache ? hk : 0);
     const int h0 = blockIdx.y * heads_per_wave;
     const int h1 = min(htot, h0 + heads_per_wave);
-    const int nslots = (h1 - h0) * S;  // <= 64 * MAXU (host guarantees)
+    const int nslots = (h1 - h0) * S;  // <= SPW * MAXU (host guarantees)
     D* qt = q ? q + (long long)t * qs : nullptr;
     D* kt = k ? k + (long long)t * ks : nullptr;
     const D* vt = CACHE != kNoCache ? kv.v + (long long)t * kv.vs : nullptr;
@@ -160,10 +161,10 @@ __global__ __launch_bounds__(kBlock) void rope_fast(D* q, D* k, int n_tokens, in
     int hs[MAXU];
 #pragma unroll
     for (int u = 0; u < MAXU; ++u) {
-        const int sl = lane + u * kWave;
+        const int sl = lane + u * SPW;
         src[u] = nullptr;
         hs[u] = -1;
-        if (sl < nslots) {
+        if (lane < SPW && sl < nslots) {
             const int h = h0 + sl / S;
             hs[u] = h;
             // Selected as integer addresses: the equivalent nested pointer
@@ -666,7 +667,7 @@ hipError_t rope_dispatch(D* q, D* k, int n_tokens, int hq, int hk, int d, int64_
     const int npairs = d / 2;
     const int pps = pairing == QL_ROPE_INTERLEAVED ? W / 2 : W;
     const int slots = npairs % pps == 0 ? npairs / pps : 0;
-    const bool tile_ok = npairs <= 64 && slots > 0 && 64 % slots == 0;
+    const bool tile_ok = npairs <= 64 && slots > 0;
     bool align_ok = rows_aligned16(q, qs * (int64_t)sizeof(D)) &&
                     rows_aligned16(k, ks * (int64_t)sizeof(D)) && (d * (int)sizeof(D)) % 16 == 0;
     if (CACHE != kNoCache) align_ok = align_ok && rows_aligned16(kv.v, kv.vs * (int64_t)sizeof(D));
@@ -704,7 +705,7 @@ hipError_t rope_dispatch(D* q, D* k, int n_tokens, int hq, int hk, int d, int64_
         // Heads per wavefront: at most 64*kRopeMaxU chunks per wavefront, and
         // split further while tokens alone give fewer than kRopeTargetWaves.
         const int htot = hq + hk + (CACHE != kNoCache ? hk : 0);
-        const int hcap = (kWave * kRopeMaxU) / slots;
+        const int hcap = (kWave / slots) * kRopeMaxU;   // whole heads per wavefront pass
         int groups = (kRopeTargetWaves + n_tokens - 1) / n_tokens;
         groups = groups < 1 ? 1 : (groups > htot ? htot : groups);
         int hpw = (htot + groups - 1) / groups;

@@ -312,10 +312,20 @@ def test_rope_f16_c5(pairing):
 
 
 @pytest.mark.parametrize("f16", [False, True])
-@pytest.mark.parametrize("d", [2, 8, 16, 32, 96, 128, 256, 2048])
+@pytest.mark.parametrize("d", [2, 8, 16, 24, 32, 40, 48, 80, 96, 112, 120, 128, 256, 2048])
 def test_rope_head_dims(f16, d):
     for pairing in (ql.ROPE_INTERLEAVED, ql.ROPE_HALF):
         _rope_case(f16, 37, 3, 1, d, 1e4, pairing, 100 + d)
+
+
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("d", [24, 40, 48, 80, 96, 112])
+def test_rope_head_dims_many_heads(f16, d):
+    # head chunks that do not tile a wavefront: each pass takes the whole heads that
+    # fit its 64 lanes (the rest idle), several passes per wavefront, several
+    # wavefronts per token
+    for pairing in (ql.ROPE_INTERLEAVED, ql.ROPE_HALF):
+        _rope_case(f16, 29, 40, 8, d, 5e5, pairing, 300 + d)
 
 
 @pytest.mark.parametrize("f16", [False, True])
