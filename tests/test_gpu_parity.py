@@ -509,6 +509,28 @@ def test_softmax_rows_at_any_offset(f16, rows, cols, in_off, out_off):
         check_close(out.get((rows, cols)), want, RTOL_F32, ATOL_F32, f"softmax f32 {rows}x{cols} +{in_off}/+{out_off}")
 
 
+ANY_COLS_F16 = [33, 1001, 2001, 4001, 4095, 8001, 12001, 16001, 24001, 32001, 49001, 65001, 98001, 131001]
+ANY_COLS_F32 = [33, 501, 1001, 2001, 4001, 6001, 8001, 12001, 16001, 24001, 32001, 49001, 65001]
+
+
+@pytest.mark.parametrize("f16,cols", [(True, c) for c in ANY_COLS_F16] + [(False, c) for c in ANY_COLS_F32])
+def test_softmax_any_length_every_variant(f16, cols):
+    # one length per launch shape of the covering-vector path (vectors per lane x
+    # wavefronts per row), so each runs under a check
+    rows = 3
+    x = normal(960 + cols, (rows, cols), sigma=2.0)
+    if f16:
+        x = _f16(x)
+    out = Out(rows * cols, np.uint16 if f16 else np.float32)
+    dx = dev(x)
+    ql.call("ql_softmax_f16" if f16 else "ql_softmax_f32", ptr(dx), out.ptr, rows, cols, stream())
+    want = orc.softmax(x, f16=f16)
+    if f16:
+        check_f16(out.get((rows, cols)), want, f"softmax f16 {rows}x{cols}")
+    else:
+        check_close(out.get((rows, cols)), want, RTOL_F32, ATOL_F32, f"softmax f32 {rows}x{cols}")
+
+
 @pytest.mark.parametrize("f16", [False, True])
 @pytest.mark.parametrize("rows,cols,off", [(9, 1001, 0), (6, 4095, 3), (40, 5, 1)])
 def test_softmax_in_place_rows_at_any_offset(f16, rows, cols, off):
@@ -739,7 +761,8 @@ def _pool(nb, blk, misalign=0):
                                                (20, 3, 1, 96, 0), (45, 4, 2, 64, 1),
                                                (45, 5, 3, 128, 1), (19, 2, 1, 128, 0),
                                                (33, 6, 2, 128, 0), (5, 120, 8, 128, 0),
-                                               (21, 4, 2, 32, 0), (21, 4, 2, 32, 1)])
+                                               (21, 4, 2, 32, 0), (21, 4, 2, 32, 1),
+                                               (13, 3, 1, 6, 0), (9, 2, 2, 256, 0)])   # per-pair loop
 def test_rope_paged_kv_append_fused(pairing, T, H, HK, d, misalign):
     # One launch == ql_rope_f16 then ql_paged_kv_append_f16, bit for bit; and
     # both agree with the oracle (C5 shape: Q 32x128, K/V 8x128, theta 5e5).
