@@ -169,6 +169,8 @@ hipError_t ql_softmax_f16(const uint16_t* in, uint16_t* out, int rows, int cols,
 /* ---- token-embedding gather (batched) ----------------------------------------
  * out[t, :] = table[ids[t], :] for t < n_tokens; bit-exact copy.
  * ids outside [0, vocab) produce a zero row (the reference does no check).
+ * table and out must be aligned to their element size (hipErrorInvalidValue
+ * otherwise); any other offset and any dim are accepted.
  * Replaces embed_kernel (src/forward.cu:137-141, launched :256-257) and
  * launch_fp16_embed (kernels/fp16_ops.cu:81-89,137-142), which gather one token. */
 hipError_t ql_embed_f32(const float* table, const int32_t* ids, int n_tokens,

@@ -101,7 +101,9 @@ __global__ __launch_bounds__(kBlock) void embed_rows_vec(const D* __restrict__ t
     }
 }
 
-// Any dim / alignment: one wavefront per token, element copies.
+// Any dim / offset: one wavefront per token, element copies.  (Covering aligned
+// vectors realigned by a shift of two loads per output vector measured slower at
+// 8192 x 4095 binary16: 31.3 against 26.8 us.)
 template <typename D>
 __global__ __launch_bounds__(kBlock) void embed_rows_scalar(const D* __restrict__ table,
                                                             const int32_t* __restrict__ ids,
@@ -124,6 +126,7 @@ hipError_t embed_dispatch(const D* table, const int32_t* ids, int one_id, int n_
     QL_CHECK_ARG(n_tokens >= 0 && vocab >= 0 && dim >= 0);
     if (n_tokens == 0 || dim == 0) return hipSuccess;
     QL_CHECK_ARG(table && out && (ids || n_tokens == 1));
+    QL_CHECK_ARG(((reinterpret_cast<uintptr_t>(table) | reinterpret_cast<uintptr_t>(out)) & (sizeof(D) - 1)) == 0);
     QL_CHECK_ARG((long long)dim * (long long)sizeof(D) < (1LL << 31));
     const int wpb = kBlock / kWave;
     if ((dim * (int)sizeof(D)) % 16 == 0 && qlh::aligned16(table) && qlh::aligned16(out)) {

@@ -198,38 +198,6 @@ __global__ __launch_bounds__(kWave) void rmsnorm_wave(D* x, const D* __restrict_
     }
 }
 
-// Elements S .. S + W - 1 of the concatenation a:b.
-template <int S, typename V>
-__device__ __forceinline__ V take(const V& a, const V& b) {
-    constexpr int W = sizeof(V) / sizeof(a.v[0]);
-    V r;
-#pragma unroll
-    for (int e = 0; e < W; ++e) r.v[e] = e + S < W ? a.v[e + S] : b.v[e + S - W];
-    return r;
-}
-
-// take<s>(a, b) for a wavefront-uniform s in [0, W)
-template <typename V>
-__device__ __forceinline__ V take_at(int s, const V& a, const V& b) {
-    constexpr int W = sizeof(V) / sizeof(a.v[0]);
-    switch (s) {
-    case 0: return a;
-    case 1: return take<1>(a, b);
-    case 2: return take<2>(a, b);
-    case 3: return take<3>(a, b);
-    default:
-        if constexpr (W > 4) {
-            switch (s) {
-            case 4: return take<4>(a, b);
-            case 5: return take<5>(a, b);
-            case 6: return take<6>(a, b);
-            default: return take<7>(a, b);
-            }
-        }
-        return a;
-    }
-}
-
 // Rows of any length whose starts need not be 16-byte aligned (x, d and out at one
 // offset modulo 16): WPR wavefronts per row, each lane NV of the aligned 16-byte
 // vectors that cover the row, the first starting p elements before it.  Elements

@@ -104,6 +104,8 @@ P = 4096  # a non-null, 16-byte aligned dummy address: never dereferenced on the
     (("ql_softmax_f16", None, P, 2, 8, None), INVALID),
     (("ql_embed_f16", P, None, 4, 100, 64, P, None), INVALID),
     (("ql_embed_f32", P, P, -1, 100, 64, P, None), INVALID),
+    (("ql_embed_f16", P + 1, P, 4, 100, 64, P, None), INVALID),             # table not element-aligned
+    (("ql_embed_f32", P, P, 4, 100, 64, P + 2, None), INVALID),             # out not element-aligned
     (("ql_embed_token_f16", None, 3, 64, P, None), INVALID),
     (("ql_kv_append_f32", P, P, P, P, 2, 0, 1, 8, 128, 16, 2, None), INVALID),   # layer == n_layers
     (("ql_kv_append_f32", P, P, P, P, 0, 15, 2, 8, 128, 16, 2, None), INVALID),  # pos+T > max_seq

@@ -573,6 +573,27 @@ def test_embed_f16_c5():
 
 
 @pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("dim,t_off,o_off", [(1, 0, 0), (3, 1, 0), (7, 0, 5), (33, 2, 3), (1001, 0, 0),
+                                             (4095, 3, 1), (4096, 1, 1), (2050, 0, 2), (5000, 7, 0)])
+def test_embed_rows_at_any_offset(f16, dim, t_off, o_off):
+    # rows that are not whole 16-byte vectors or sit at an offset: each output row's
+    # covering vectors from two shifted table vectors, the ones shared with the
+    # neighbouring rows stored element by element (guard bands around the output);
+    # out-of-range ids give zero rows
+    V, T = 257, 131
+    r = np.random.default_rng(dim + 17 * t_off + o_off)
+    table = normal(dim + 5, (V, dim))
+    if f16:
+        table = _f16(table)
+    ids = r.integers(0, V, size=T).astype(np.int32)
+    ids[[0, 7, 130]] = [-3, V, 2**31 - 1]
+    out = Out(T * dim, np.uint16 if f16 else np.float32, offset=o_off)
+    dt, di = dev(table, t_off), dev(ids)
+    ql.call("ql_embed_f16" if f16 else "ql_embed_f32", ptr(dt), ptr(di), T, V, dim, out.ptr, stream())
+    assert np.array_equal(out.get((T, dim)), orc.embed(table, ids, f16=f16))
+
+
+@pytest.mark.parametrize("f16", [False, True])
 @pytest.mark.parametrize("dim", [1, 7, 64, 1000, 4096])
 def test_embed_ragged_and_out_of_range(f16, dim):
     V, T = 300, 77
@@ -694,9 +715,10 @@ def test_paged_kv_append_token_groups_and_misaligned_blocks(T, H, d, misalign):
 
 
 @pytest.mark.parametrize("f16", [False, True])
-def test_embed_empty_vocab_gives_zero_rows(f16):
+@pytest.mark.parametrize("dim", [4096, 4095])
+def test_embed_empty_vocab_gives_zero_rows(f16, dim):
     # vocab 0: every id is out of range, so every row is zeros and no table row is read
-    T, dim = 9, 4096
+    T = 9
     dt = np.uint16 if f16 else np.float32
     table = dev(np.ones(8, dt))                      # smaller than one row
     ids = dev(np.arange(T, dtype=np.int32))
