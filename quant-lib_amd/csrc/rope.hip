@@ -14,7 +14,7 @@
 //   y0  = fma(x0, c, -(x1*s)),  y1 = fma(x0, s, x1*c)
 // Pairing: interleaved (2i, 2i+1) as the reference, or rotate-half (i, i+d/2).
 //
-// Fast path (d/2 <= 64 pairs, 16-byte aligned rows; a wavefront pass takes as many
+// Fast path (d/2 <= 128 pairs, 16-byte aligned rows; a wavefront pass takes as many
 // whole heads' 16-byte chunks as fit its 64 lanes): inv_freq is computed once per call on the host (the same libm
 // pow the CPU restatement uses) and passed by value.  One wavefront serves a
 // (token, group of heads): every lane first issues the loads of all 16-byte
@@ -34,9 +34,11 @@ namespace {
 
 using namespace ql;
 
-struct InvFreq {
-    float v[64];
+template <int N>
+struct InvFreqN {
+    float v[N];
 };
+using InvFreq = InvFreqN<64>;   // up to 64 pairs (head_dim 128)
 
 // inv_freq of pair i, host side, in the order of kernels/rope.cu:35.
 float host_inv_freq(int pair, int d, float theta) {
@@ -118,11 +120,13 @@ __device__ __forceinline__ void store_cache(D* dst, const V& v, bool aligned) {
 
 // Heads of a token, in order: hq Q heads, hk K heads, then (fused variants)
 // hk V heads that are copied to the cache unrotated.
-template <typename D, int PAIRING, int MAXU, int CACHE>
+// NP: the pairs the inv_freq table holds (64, or 128 for head_dim up to 256: each
+// lane then evaluates the angles of pairs lane and lane + 64).
+template <typename D, int PAIRING, int MAXU, int CACHE, int NP = 64>
 __global__ __launch_bounds__(kBlock) void rope_fast(D* q, D* k, int n_tokens, int hq, int hk,
                                                     int d, long long qs, long long ks,
                                                     const int32_t* __restrict__ positions,
-                                                    int pos_offset, InvFreq inv,
+                                                    int pos_offset, InvFreqN<NP> inv,
                                                     int heads_per_wave, KvDst<D> kv) {
     constexpr int W = vec16<D>();
     constexpr int PPS = PAIRING == QL_ROPE_INTERLEAVED ? W / 2 : W;  // pairs per slot
@@ -184,10 +188,23 @@ __global__ __launch_bounds__(kBlock) void rope_fast(D* q, D* k, int n_tokens, in
         const int pos = positions ? ld_scalar(positions + t) : pos_offset + t;
         float c_own, s_own;
         trig((float)pos * inv.v[lane % npairs], c_own, s_own);
+        if constexpr (NP == 64) {
 #pragma unroll
-        for (int e = 0; e < PPS; ++e) {
-            c[e] = __shfl(c_own, j * PPS + e, kWave);
-            s[e] = __shfl(s_own, j * PPS + e, kWave);
+            for (int e = 0; e < PPS; ++e) {
+                c[e] = __shfl(c_own, j * PPS + e, kWave);
+                s[e] = __shfl(s_own, j * PPS + e, kWave);
+            }
+        } else {   // pairs 64 .. npairs - 1 from the second angle
+            float c_hi, s_hi;
+            trig((float)pos * inv.v[64 + lane % (npairs - 64)], c_hi, s_hi);
+#pragma unroll
+            for (int e = 0; e < PPS; ++e) {
+                const int pi = j * PPS + e;
+                const float cl = __shfl(c_own, pi & 63, kWave), sl = __shfl(s_own, pi & 63, kWave);
+                const float ch = __shfl(c_hi, pi & 63, kWave), sh = __shfl(s_hi, pi & 63, kWave);
+                c[e] = pi < 64 ? cl : ch;
+                s[e] = pi < 64 ? sl : sh;
+            }
         }
     }
 
@@ -646,6 +663,31 @@ int rope_mix(const D* q, const D* k, const D* v, long long qs, long long ks, lon
 constexpr int kRopeMaxU = 4;        // chunks (or chunk pairs) per lane
 constexpr int kRopeTargetWaves = 16384;
 
+// rope_fast's launch: heads per wavefront at most kRopeMaxU passes of the whole heads
+// that fit 64 lanes, split further while tokens alone give fewer than
+// kRopeTargetWaves wavefronts.
+template <typename D, int CACHE, int NP>
+hipError_t launch_fast_heads(D* q, D* k, int n_tokens, int hq, int hk, int d, int64_t qs, int64_t ks,
+                             const int32_t* positions, int pos_offset, const InvFreqN<NP>& inv, int pairing,
+                             int slots, unsigned gx, const KvDst<D>& kv, hipStream_t stream) {
+    const int htot = hq + hk + (CACHE != kNoCache ? hk : 0);
+    const int hcap = (kWave / slots) * kRopeMaxU;   // whole heads per wavefront pass
+    int groups = (kRopeTargetWaves + n_tokens - 1) / n_tokens;
+    groups = groups < 1 ? 1 : (groups > htot ? htot : groups);
+    int hpw = (htot + groups - 1) / groups;
+    hpw = hpw > hcap ? hcap : hpw;
+    groups = (htot + hpw - 1) / hpw;
+    if (pairing == QL_ROPE_INTERLEAVED)
+        hipLaunchKernelGGL((rope_fast<D, QL_ROPE_INTERLEAVED, kRopeMaxU, CACHE, NP>), dim3(gx, groups),
+                           dim3(kBlock), 0, stream, q, k, n_tokens, hq, hk, d, (long long)qs, (long long)ks,
+                           positions, pos_offset, inv, hpw, kv);
+    else
+        hipLaunchKernelGGL((rope_fast<D, QL_ROPE_HALF, kRopeMaxU, CACHE, NP>), dim3(gx, groups), dim3(kBlock), 0,
+                           stream, q, k, n_tokens, hq, hk, d, (long long)qs, (long long)ks, positions, pos_offset,
+                           inv, hpw, kv);
+    return hipGetLastError();
+}
+
 template <typename D, int CACHE>
 hipError_t rope_dispatch(D* q, D* k, int n_tokens, int hq, int hk, int d, int64_t qs,
                          int64_t ks, const int32_t* positions, int pos_offset, float theta,
@@ -667,7 +709,7 @@ hipError_t rope_dispatch(D* q, D* k, int n_tokens, int hq, int hk, int d, int64_
     const int npairs = d / 2;
     const int pps = pairing == QL_ROPE_INTERLEAVED ? W / 2 : W;
     const int slots = npairs % pps == 0 ? npairs / pps : 0;
-    const bool tile_ok = npairs <= 64 && slots > 0;
+    const bool tile_ok = npairs <= 128 && slots > 0;
     bool align_ok = rows_aligned16(q, qs * (int64_t)sizeof(D)) &&
                     rows_aligned16(k, ks * (int64_t)sizeof(D)) && (d * (int)sizeof(D)) % 16 == 0;
     if (CACHE != kNoCache) align_ok = align_ok && rows_aligned16(kv.v, kv.vs * (int64_t)sizeof(D));
@@ -678,6 +720,12 @@ hipError_t rope_dispatch(D* q, D* k, int n_tokens, int hq, int hk, int d, int64_
     if (tile_ok && align_ok) {
         InvFreq inv;
         for (int i = 0; i < 64; ++i) inv.v[i] = i < npairs ? host_inv_freq(i, d, theta) : 0.0f;
+        if (npairs > 64) {   // head_dim 130 .. 256: the vector path with a 128-pair table
+            InvFreqN<128> inv2;
+            for (int i = 0; i < 128; ++i) inv2.v[i] = i < npairs ? host_inv_freq(i, d, theta) : 0.0f;
+            return launch_fast_heads<D, CACHE, 128>(q, k, n_tokens, hq, hk, d, qs, ks, positions, pos_offset,
+                                                    inv2, pairing, slots, gx, kv, stream);
+        }
         if constexpr (CACHE == kNoCache && sizeof(D) == 2) {
             if (d == 128) {
                 const int units = (hq + hk + 3) / 4;
@@ -702,24 +750,8 @@ hipError_t rope_dispatch(D* q, D* k, int n_tokens, int hq, int hk, int d, int64_
             return launch_planes_hd<D, CACHE>(d, pairing, q, k, n_tokens, hq, hk, (long long)qs,
                                               (long long)ks, positions, pos_offset, inv, kv, mix, stream);
         }
-        // Heads per wavefront: at most 64*kRopeMaxU chunks per wavefront, and
-        // split further while tokens alone give fewer than kRopeTargetWaves.
-        const int htot = hq + hk + (CACHE != kNoCache ? hk : 0);
-        const int hcap = (kWave / slots) * kRopeMaxU;   // whole heads per wavefront pass
-        int groups = (kRopeTargetWaves + n_tokens - 1) / n_tokens;
-        groups = groups < 1 ? 1 : (groups > htot ? htot : groups);
-        int hpw = (htot + groups - 1) / groups;
-        hpw = hpw > hcap ? hcap : hpw;
-        groups = (htot + hpw - 1) / hpw;
-        if (pairing == QL_ROPE_INTERLEAVED)
-            hipLaunchKernelGGL((rope_fast<D, QL_ROPE_INTERLEAVED, kRopeMaxU, CACHE>),
-                               dim3(gx, groups), dim3(kBlock), 0, stream, q, k, n_tokens, hq, hk,
-                               d, (long long)qs, (long long)ks, positions, pos_offset, inv, hpw,
-                               kv);
-        else
-            hipLaunchKernelGGL((rope_fast<D, QL_ROPE_HALF, kRopeMaxU, CACHE>), dim3(gx, groups),
-                               dim3(kBlock), 0, stream, q, k, n_tokens, hq, hk, d, (long long)qs,
-                               (long long)ks, positions, pos_offset, inv, hpw, kv);
+        return launch_fast_heads<D, CACHE, 64>(q, k, n_tokens, hq, hk, d, qs, ks, positions, pos_offset, inv,
+                                               pairing, slots, gx, kv, stream);
     } else {
         if (pairing == QL_ROPE_INTERLEAVED)
             hipLaunchKernelGGL((rope_generic<D, QL_ROPE_INTERLEAVED, CACHE>), dim3(gx),

@@ -312,14 +312,14 @@ def test_rope_f16_c5(pairing):
 
 
 @pytest.mark.parametrize("f16", [False, True])
-@pytest.mark.parametrize("d", [2, 8, 16, 24, 32, 40, 48, 80, 96, 112, 120, 128, 256, 2048])
+@pytest.mark.parametrize("d", [2, 8, 16, 24, 32, 40, 48, 80, 96, 112, 120, 128, 136, 192, 256, 264, 2048])
 def test_rope_head_dims(f16, d):
     for pairing in (ql.ROPE_INTERLEAVED, ql.ROPE_HALF):
         _rope_case(f16, 37, 3, 1, d, 1e4, pairing, 100 + d)
 
 
 @pytest.mark.parametrize("f16", [False, True])
-@pytest.mark.parametrize("d", [24, 40, 48, 80, 96, 112])
+@pytest.mark.parametrize("d", [24, 40, 48, 80, 96, 112, 192, 256])
 def test_rope_head_dims_many_heads(f16, d):
     # head chunks that do not tile a wavefront: each pass takes the whole heads that
     # fit its 64 lanes (the rest idle), several passes per wavefront, several
@@ -931,7 +931,7 @@ def test_rope_on_fused_qkv_rows_matches_separate_buffers(entry, pairing, T, H, H
 @pytest.mark.parametrize("f16", [True, False])
 @pytest.mark.parametrize("pairing", [ql.ROPE_HALF, ql.ROPE_INTERLEAVED])
 @pytest.mark.parametrize("T,H,HK,d", [(300, 8, 2, 128), (33, 4, 4, 64), (17, 2, 1, 6),
-                                      (29, 3, 3, 64), (31, 7, 1, 128), (23, 4, 2, 32)])
+                                      (29, 3, 3, 64), (31, 7, 1, 128), (23, 4, 2, 32), (11, 2, 1, 256)])
 def test_rope_kv_append_fused_contiguous_from_fused_qkv(f16, pairing, T, H, HK, d):
     # Q, K, V are views into one fused [T, (H + 2*HK)*d] QKV buffer (strided rows);
     # the cache is [L, S, HK, d], tokens written at positions pos..pos+T-1.
