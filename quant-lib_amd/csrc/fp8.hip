@@ -198,6 +198,9 @@ __host__ __device__ inline long long seen_vectors(int mode, long long nv) {
     return mode == QL_FP8_MODE_OCP ? nv : (nv / 16) * 4 + (nv % 16 < 4 ? nv % 16 : 4);
 }
 
+// PARTIAL: workgroup b of group g writes its max to mx[g * gridDim.x + b] instead
+// (no atomics, nothing to clear first); reduce_partials then finishes the scales.
+template <bool PARTIAL = false>
 __global__ __launch_bounds__(kBlock) void absmax_blocks_vec(const _Float16* __restrict__ x, Geom g,
                                                             int mode, float* __restrict__ mx) {
     const long long grp = blockIdx.y;
@@ -227,7 +230,24 @@ __global__ __launch_bounds__(kBlock) void absmax_blocks_vec(const _Float16* __re
     __syncthreads();
     if (threadIdx.x == 0) {
         for (int w = 1; w < kBlock / kWave; ++w) m = fmaxf(m, part[w]);
-        atomicMax(reinterpret_cast<unsigned int*>(mx) + grp, __float_as_uint(m));
+        if constexpr (PARTIAL) mx[grp * gridDim.x + blockIdx.x] = m;
+        else atomicMax(reinterpret_cast<unsigned int*>(mx) + grp, __float_as_uint(m));
+    }
+}
+
+// one workgroup per group: the max of its nb partial maxima -> the group's scale
+__global__ __launch_bounds__(kBlock) void reduce_partials(const float* __restrict__ part, int nb, float fmax,
+                                                          float* __restrict__ scales) {
+    const int grp = blockIdx.x;
+    float m = 0.0f;
+    for (int b = threadIdx.x; b < nb; b += kBlock) m = fmaxf(m, part[(size_t)grp * nb + b]);
+    m = wave_max(m);
+    __shared__ float red[kBlock / kWave];
+    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < kBlock / kWave; ++w) m = fmaxf(m, red[w]);
+        scales[grp] = m < 1e-8f ? 1.0f : fmax / m;
     }
 }
 
@@ -2031,7 +2051,7 @@ extern "C" hipError_t ql_fp8_scales(const uint16_t* src, int rows, int cols, int
             // at most kAbsBlocks workgroups in all, each looping over its share
             const long long want = qlh::blocks_for(seen_vectors(mode, g.gs / 8), (long long)kBlock * kBlockIters);
             const unsigned bx = (unsigned)std::max(1LL, std::min(want, kAbsBlocks / g.n_groups));
-            hipLaunchKernelGGL(absmax_blocks_vec, dim3(bx, (unsigned)g.n_groups), dim3(kBlock), 0, stream, x,
+            hipLaunchKernelGGL(absmax_blocks_vec<false>, dim3(bx, (unsigned)g.n_groups), dim3(kBlock), 0, stream, x,
                                g, mode, scales);
         } else {
             const long long per = 16LL * kBlock;
@@ -2069,6 +2089,24 @@ extern "C" hipError_t ql_fp8_quantize(const uint16_t* src, int rows, int cols, i
         qlh::aligned16(src) && ((uintptr_t)dst & 7) == 0) {   // one wavefront per group, one pass
         QL_FP8_DISPATCH(format, mode, launch_quantize_wave_groups, reinterpret_cast<const _Float16*>(src), g,
                         scales, dst, stream);
+        return hipGetLastError();
+    }
+    if (src && scales && g.n % 8 == 0 && g.gs % 8 == 0 && g.gs > 8LL * kWave * kWaveGroupVecs &&
+        g.n_groups <= 65535 && qlh::aligned16(src) && ((uintptr_t)dst & 7) == 0) {
+        // groups too large for one wavefront (per tensor): the workgroups' maxima go to
+        // the front of dst (at most kAbsBlocks floats, or one per group; n > 16384
+        // bytes), one workgroup per group reduces them into the scale, then the codes
+        // overwrite them
+        const long long want =
+            qlh::blocks_for(seen_vectors(mode, g.gs / 8), (long long)kBlock * kBlockIters);
+        const unsigned bx = (unsigned)std::max(1LL, std::min(want, kAbsBlocks / g.n_groups));
+        float* part = reinterpret_cast<float*>(dst);
+        hipLaunchKernelGGL(absmax_blocks_vec<true>, dim3(bx, (unsigned)g.n_groups), dim3(kBlock), 0, stream,
+                           reinterpret_cast<const _Float16*>(src), g, mode, part);
+        hipLaunchKernelGGL(reduce_partials, dim3((unsigned)g.n_groups), dim3(kBlock), 0, stream, part, (int)bx,
+                           fp8_max(format), scales);
+        QL_FP8_DISPATCH(format, mode, launch_quantize, reinterpret_cast<const _Float16*>(src), g, scales, dst,
+                        true, stream);
         return hipGetLastError();
     }
     const hipError_t e = ql_fp8_scales(src, rows, cols, format, granularity, group_size, mode, scales, stream);

@@ -216,17 +216,14 @@ constexpr int kAnyMaxWaves = 16;
 
 template <typename D, int NV, bool ADD>
 __global__ __launch_bounds__(kWave * kAnyMaxWaves) void rmsnorm_any(
-    D* x, const D* __restrict__ d, const D* __restrict__ w, D* __restrict__ out, int rows, int dim,
-    float eps) {
+    D* x, const D* __restrict__ d, const D* __restrict__ w, D* __restrict__ out, int dim, float eps) {
     constexpr int W = vec16<D>();
     using V = Vec<D, W>;
 
     const int tid = threadIdx.x;
     const int TPR = blockDim.x;
-    const int row = blockIdx.x;
+    const int row = blockIdx.x;   // grid.x == rows
     const int rl = tid;
-    const bool row_ok = true;
-    (void)rows;
     const size_t roff = (size_t)row * (size_t)dim;
     const int p = (int)((reinterpret_cast<uintptr_t>(x + roff) & 15) / sizeof(D));
     const int nvec = (p + dim + W - 1) / W;
@@ -281,7 +278,6 @@ __global__ __launch_bounds__(kWave * kAnyMaxWaves) void rmsnorm_any(
         ss = 0.0f;
         for (int i = 0; i < wpr; ++i) ss += red[i];
     }
-    if (!row_ok) return;
     const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
@@ -312,7 +308,7 @@ hipError_t launch_any(D* x, const D* d, const D* w, D* out, int rows, int nv, in
                       hipStream_t stream) {
     const int wpr = (nv + NV * kWave - 1) / (NV * kWave);   // <= kAnyMaxWaves by the caller's choice of NV
     hipLaunchKernelGGL((rmsnorm_any<D, NV, ADD>), dim3((unsigned)rows), dim3(kWave * wpr), 0, stream, x, d, w,
-                       out, rows, dim, eps);
+                       out, dim, eps);
     return hipGetLastError();
 }
 

@@ -69,6 +69,8 @@ def same_f16(a, b):
     (1024, 1024, ql.QUANT_PER_CHANNEL, 0), (1024, 1024, ql.QUANT_PER_TENSOR, 0),
     (64, 256, ql.QUANT_PER_GROUP, 100), (3, 1000, ql.QUANT_PER_GROUP, 7), (5, 33, ql.QUANT_PER_CHANNEL, 0),
     (4096, 4096, ql.QUANT_PER_TENSOR, 0),       # one group larger than a wavefront pass
+    # groups beyond one wavefront: workgroup maxima in the code buffer, reduced per group
+    (3, 20000, ql.QUANT_PER_CHANNEL, 0), (5, 9000, ql.QUANT_PER_GROUP, 20000), (3, 6000, ql.QUANT_PER_TENSOR, 0),
     # power-of-two groups take the one-pass kernel (scales and codes from one read of x,
     # ql_fp8_scales' vector pass for the scales alone): every lane count
     (16, 512, ql.QUANT_PER_GROUP, 16), (5, 96, ql.QUANT_PER_GROUP, 32), (7, 64, ql.QUANT_PER_GROUP, 64),
