@@ -123,3 +123,59 @@ def test_rope_f16_beyond_2_31_elements():
                                                       pos_offset=r0, f16=True), f"rope q {r0}..{r1}")
         check_f16(_rows(dk, r0, r1, HK * HD), orc.rope(k[sel], HK, HD, 5e5, ql.ROPE_HALF,
                                                        pos_offset=r0, f16=True), f"rope k {r0}..{r1}")
+
+
+def test_softmax_and_add_rmsnorm_f16_odd_width_beyond_2_31_elements():
+    # rows of 4095 binary16 elements start at every offset mod 16: the covering-vector
+    # paths, with row offsets past 2^31 elements
+    C = 4095
+    rows = E31 // C + 130
+    x = normal(0x5AA, (TILE, C), sigma=2.0)
+    xh = to_f16_bits(x)
+    dx = _tiled(xh, rows)
+    out = ql.DeviceArray((rows * C,), np.uint16)
+    ql.call("ql_softmax_f16", dx.ptr, out.ptr, rows, C, stream())
+    synchronize()
+    want = orc.softmax(xh, f16=True)
+    for r0, r1 in _windows(rows, C):
+        check_f16(_rows(out, r0, r1, C), want[np.arange(r0, r1) % TILE], f"softmax rows {r0}..{r1}")
+    del out
+    d = to_f16_bits(normal(0x5AB, (TILE, C)))
+    w = to_f16_bits(uniform(0x5AC, C, 0.5, 1.5))
+    dd, dw = _tiled(d, rows), dev(w)
+    y = ql.DeviceArray((rows * C,), np.uint16)
+    ql.call("ql_add_rmsnorm_f16", dx.ptr, dd.ptr, dw.ptr, y.ptr, rows, C, 1e-5, stream())
+    synchronize()
+    wx, wy = orc.add_rmsnorm(xh, d, w, 1e-5, f16=True)
+    for r0, r1 in _windows(rows, C):
+        sel = np.arange(r0, r1) % TILE
+        assert np.array_equal(_rows(dx, r0, r1, C), wx[sel]), f"x' rows {r0}..{r1}"
+        check_f16(_rows(y, r0, r1, C), wy[sel], f"add_rmsnorm rows {r0}..{r1}")
+
+
+@pytest.mark.parametrize("mode", [ql.FP8_MODE_REFERENCE, ql.FP8_MODE_OCP])
+def test_fp8_per_tensor_quantize_and_dequantize_beyond_2_31_elements(mode):
+    # one scale over more than 2^31 elements (workgroup maxima reduced in the code
+    # buffer), then the codes and the dequantized rows in windows around element
+    # 2^31: the tiled tensor has the tile's max (the reference mode's max sees the
+    # same offsets mod 128, the rows being 4096 wide), so the tile quantized alone
+    # gives the expected scale and codes
+    C = 4096
+    rows = E31 // C + 130
+    x = to_f16_bits(uniform(0x5AD, (TILE, C), -3.0, 3.0))
+    dx = _tiled(x, rows)
+    q = ql.DeviceArray((rows * C,), np.uint8)
+    sc = ql.DeviceArray((1,), np.float32)
+    ql.call("ql_fp8_quantize", dx.ptr, rows, C, ql.FP8_E4M3, ql.QUANT_PER_TENSOR, 0, mode, q.ptr, sc.ptr, stream())
+    synchronize()
+    q_want, sc_want = orc.fp8_quantize(x, ql.FP8_E4M3, ql.QUANT_PER_TENSOR, 0, mode)
+    assert np.array_equal(sc.numpy(), sc_want)
+    for r0, r1 in _windows(rows, C):
+        assert np.array_equal(_rows(q, r0, r1, C), q_want[np.arange(r0, r1) % TILE]), f"codes rows {r0}..{r1}"
+    del dx
+    y = ql.DeviceArray((rows * C,), np.uint16)
+    ql.call("ql_fp8_dequantize", q.ptr, sc.ptr, rows, C, ql.FP8_E4M3, ql.QUANT_PER_TENSOR, 0, mode, y.ptr, stream())
+    synchronize()
+    y_want = orc.fp8_dequantize(q_want, sc_want, ql.FP8_E4M3, ql.QUANT_PER_TENSOR, 0, mode)
+    for r0, r1 in _windows(rows, C):
+        assert np.array_equal(_rows(y, r0, r1, C), y_want[np.arange(r0, r1) % TILE]), f"dequant rows {r0}..{r1}"
