@@ -53,9 +53,11 @@ struct AddOp {
 // and one-wavefront workgroups beat 128- and 256-thread ones at every size
 // tried: C5 SwiGLU (705 MB) 0.6-3.7%, 8192 x 4096 fp16 3%, the 512 x 5632
 // configs 6-7%, the residual add 1-3%.
+// head > 0: the pointers were advanced past `head` (< BS) leading elements to a
+// 16- or 128-byte boundary (all three share that offset); block 0 also computes those.
 template <typename D, int W, int U, bool NT, typename Op, int BS = kBlock>
 __global__ __launch_bounds__(BS) void binary_stream(const D* a, const D* b, D* out,
-                                                    long long n) {
+                                                    long long n, int head = 0) {
     using V = Vec<D, W>;
     const long long nvec = n / W;
     const long long base = (long long)blockIdx.x * (BS * U) + threadIdx.x;
@@ -88,6 +90,10 @@ __global__ __launch_bounds__(BS) void binary_stream(const D* a, const D* b, D* o
     if (W > 1 && blockIdx.x == 0) {
         for (long long i = nvec * W + threadIdx.x; i < n; i += BS)
             out[i] = from_f32<D>(Op::template apply<D>(to_f32(a[i]), to_f32(b[i])));
+        if ((int)threadIdx.x < head) {
+            const long long i = (long long)threadIdx.x - head;
+            out[i] = from_f32<D>(Op::template apply<D>(to_f32(a[i]), to_f32(b[i])));
+        }
     }
 }
 
@@ -97,13 +103,23 @@ constexpr int kStreamBlock = 64;
 template <typename D, typename Op>
 hipError_t launch_binary(const D* a, const D* b, D* out, long long n, hipStream_t stream) {
     constexpr int W = vec16<D>();
-    const bool vec_ok = qlh::aligned16(a) && qlh::aligned16(b) && qlh::aligned16(out);
-    if (vec_ok) {
-        const long long nvec = n / W;
+    const uintptr_t pa = reinterpret_cast<uintptr_t>(a);
+    // a, b and out at one element-aligned offset mod 16: the leading elements up to
+    // the next 128-byte boundary (16-byte when the offsets differ mod 128) go to
+    // block 0, the rest streams as aligned vectors.  A stream whose wavefront spans
+    // straddle 128-byte lines runs ~20% slower (C5 SwiGLU at a 2-byte offset:
+    // 126.5 us against 103.4 aligned).
+    const uintptr_t db = pa - reinterpret_cast<uintptr_t>(b), dout = pa - reinterpret_cast<uintptr_t>(out);
+    const bool same = (pa & (sizeof(D) - 1)) == 0 && (db & 15) == 0 && (dout & 15) == 0;
+    const uintptr_t line = ((db | dout) & 127) == 0 ? 128 : 16;
+    const int head = same ? (int)(((line - (pa & (line - 1))) & (line - 1)) / sizeof(D)) : 0;
+    if (same && n > head) {
+        const long long nb = n - head;
+        const long long nvec = nb / W;
         const unsigned grid =
             nvec > 0 ? qlh::blocks_for(nvec, (long long)kStreamBlock * kStreamU) : 1;
         hipLaunchKernelGGL((binary_stream<D, W, kStreamU, true, Op, kStreamBlock>), dim3(grid),
-                           dim3(kStreamBlock), 0, stream, a, b, out, n);
+                           dim3(kStreamBlock), 0, stream, a + head, b + head, out + head, nb, head);
     } else {
         const unsigned grid = qlh::blocks_for(n, (long long)kBlock * kUnroll);
         hipLaunchKernelGGL((binary_stream<D, 1, kUnroll, false, Op>), dim3(grid), dim3(kBlock), 0,

@@ -258,9 +258,11 @@ def test_add_rmsnorm_f32(rows, dim):
     check_close(out.get((rows, dim)), want, RTOL_F32, ATOL_F32, f"add_rmsnorm f32 {rows}x{dim}")
 
 
-# offset 1: x and d not 16-byte aligned, the element-wise kernel
+# offsets: x and d not 16-byte aligned (at one offset: leading elements in block 0,
+# then aligned vectors; fewer elements than that: the element-wise kernel)
 @pytest.mark.parametrize("f16,n,offset", [(False, 1 << 20, 0), (True, 1 << 20, 0), (False, 1001, 0),
-                                          (True, 1003, 0), (False, 4099, 1), (True, 4101, 1)])
+                                          (True, 1003, 0), (False, 4099, 1), (True, 4101, 1),
+                                          (True, 4101, 6), (False, 2, 3)])
 def test_residual_add(f16, n, offset):
     x, d = normal(44, n), normal(45, n)
     if f16:
@@ -421,6 +423,26 @@ def test_swiglu_unaligned_and_extremes(f16):
         check_f16(got, want, "swiglu f16 extremes")
     else:
         check_close(got, want, RTOL_F32, ATOL_F32, "swiglu f32 extremes")
+
+
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("n,off", [(4099, 1), (4099, 3), (24581, 7), (3, 1), (9, 5), (1 << 20, 2)])
+def test_swiglu_at_a_shared_offset(f16, n, off):
+    # gate, up and out at one offset mod 16: the elements up to the next 16-byte
+    # boundary go to block 0, the rest streams as aligned vectors (n at most that
+    # many elements: the element-wise kernel); guard bands around the output
+    g = normal(62 + off, n, clip=8.0)
+    u = normal(63 + off, n)
+    if f16:
+        g, u = _f16(g), _f16(u)
+    out = Out(n, np.uint16 if f16 else np.float32, offset=off)
+    dg, du = dev(g, offset_elems=off), dev(u, offset_elems=off)
+    ql.call("ql_swiglu_f16" if f16 else "ql_swiglu_f32", ptr(dg), ptr(du), out.ptr, 1, n, stream())
+    want = orc.swiglu(g, u, f16=f16)
+    if f16:
+        check_f16(out.get(), want, f"swiglu f16 n={n} +{off}")
+    else:
+        check_close(out.get(), want, RTOL_F32, ATOL_F32, f"swiglu f32 n={n} +{off}")
 
 
 # ---- softmax -----------------------------------------------------------------------------------
