@@ -440,38 +440,53 @@ __global__ __launch_bounds__(kBlock) void quantize_segments(const _Float16* __re
 // with 16-byte loads.
 constexpr int kWaveGroupVecs = 32;
 
-template <int FMT, int MODE, int NV, bool ENCODE = true>
-__global__ __launch_bounds__(kBlock) void quantize_wave_groups(const _Float16* __restrict__ x, Geom g,
-                                                               float* __restrict__ scales,
-                                                               uint8_t* __restrict__ q) {
+// WPG > 1: one group per workgroup of WPG wavefronts (groups of more than 4096
+// elements), wavefront w holding vectors j*64*WPG + 64*w + lane, the wavefronts'
+// maxima combined through LDS: a row of 14336 per channel otherwise leaves one
+// wavefront per row holding 32 vectors a lane, too few wavefronts to fill the chip
+// for a 4096-row matrix.
+template <int FMT, int MODE, int NV, bool ENCODE = true, int WPG = 1>
+__global__ __launch_bounds__(WPG == 1 ? kBlock : kWave * WPG) void quantize_wave_groups(
+    const _Float16* __restrict__ x, Geom g, float* __restrict__ scales, uint8_t* __restrict__ q) {
     constexpr float kMax = fp8_max(FMT);
+    constexpr int kSpan = kWave * WPG;   // vectors per j
     const int lane = threadIdx.x & (kWave - 1);
-    const long long grp = (long long)blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
-    if (grp >= g.n_groups) return;   // wavefront-uniform
+    const int wv = WPG == 1 ? 0 : (int)(threadIdx.x / kWave);
+    const long long grp = WPG == 1 ? (long long)blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave
+                                   : (long long)blockIdx.x;
+    if (grp >= g.n_groups) return;   // wavefront-uniform (workgroup-uniform for WPG > 1)
     const long long base = grp * g.gs;
     const int nv = (int)(min(g.gs, g.n - base) / 8);   // vectors of this group
     const Vec<_Float16, 8>* xv = reinterpret_cast<const Vec<_Float16, 8>*>(x + base);
+    const int off = kWave * wv + lane;   // this lane's vector inside each span
     Vec<_Float16, 8> h[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j)
-        if (j * kWave < nv) h[j] = load<true>(xv + min(j * kWave + lane, nv - 1));   // uniform test
+        if (j * kSpan < nv) h[j] = load<true>(xv + min(j * kSpan + off, nv - 1));   // uniform test
     float m = 0.0f;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        const int i = j * kWave + lane;
+        const int i = j * kSpan + off;
         if (i < nv && seen(MODE, (long long)i * 8)) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf((float)h[j].v[e]));
         }
     }
     m = wave_max(m);
+    if constexpr (WPG > 1) {
+        __shared__ float red[WPG];
+        if (lane == 0) red[wv] = m;
+        __syncthreads();
+#pragma unroll
+        for (int w = 0; w < WPG; ++w) m = fmaxf(m, red[w]);
+    }
     const float sc = m < 1e-8f ? 1.0f : kMax / m;
-    if (lane == 0) scales[grp] = sc;
+    if (lane == 0 && wv == 0) scales[grp] = sc;
     if constexpr (ENCODE) {
         u32x2* qv = reinterpret_cast<u32x2*>(q + base);
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
-            const int i = j * kWave + lane;
+            const int i = j * kSpan + off;
             if (i < nv) store<true>(qv + i, encode8<FMT, MODE>(h[j], sc));
         }
     }
@@ -1665,23 +1680,27 @@ void launch_quantize_groups(const _Float16* x, const Geom& g, float* s, uint8_t*
     }
 }
 
-// q == nullptr: scales only (ql_fp8_scales)
+// q == nullptr: scales only (ql_fp8_scales).  Groups up to 4096 elements: one
+// wavefront each; longer ones 2 or 4 wavefronts of 8 vectors a lane.
 template <int FMT, int MODE>
 void launch_quantize_wave_groups(const _Float16* x, const Geom& g, float* s, uint8_t* q, hipStream_t st) {
     const dim3 grid(qlh::blocks_for(g.n_groups, kBlock / kWave)), block(kBlock);
+    const dim3 grid1((unsigned)g.n_groups);
     if (!q) {
         if (g.gs <= 8 * kWave * 8)
             hipLaunchKernelGGL((quantize_wave_groups<FMT, MODE, 8, false>), grid, block, 0, st, x, g, s, q);
         else if (g.gs <= 8 * kWave * 16)
-            hipLaunchKernelGGL((quantize_wave_groups<FMT, MODE, 16, false>), grid, block, 0, st, x, g, s, q);
+            hipLaunchKernelGGL((quantize_wave_groups<FMT, MODE, 8, false, 2>), grid1, dim3(2 * kWave), 0, st, x, g,
+                               s, q);
         else
-            hipLaunchKernelGGL((quantize_wave_groups<FMT, MODE, 32, false>), grid, block, 0, st, x, g, s, q);
+            hipLaunchKernelGGL((quantize_wave_groups<FMT, MODE, 8, false, 4>), grid1, dim3(4 * kWave), 0, st, x, g,
+                               s, q);
     } else if (g.gs <= 8 * kWave * 8) {
         hipLaunchKernelGGL((quantize_wave_groups<FMT, MODE, 8>), grid, block, 0, st, x, g, s, q);
     } else if (g.gs <= 8 * kWave * 16) {
-        hipLaunchKernelGGL((quantize_wave_groups<FMT, MODE, 16>), grid, block, 0, st, x, g, s, q);
+        hipLaunchKernelGGL((quantize_wave_groups<FMT, MODE, 8, true, 2>), grid1, dim3(2 * kWave), 0, st, x, g, s, q);
     } else {
-        hipLaunchKernelGGL((quantize_wave_groups<FMT, MODE, 32>), grid, block, 0, st, x, g, s, q);
+        hipLaunchKernelGGL((quantize_wave_groups<FMT, MODE, 8, true, 4>), grid1, dim3(4 * kWave), 0, st, x, g, s, q);
     }
 }
 
