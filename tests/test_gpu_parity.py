@@ -259,15 +259,17 @@ def test_add_rmsnorm_f32(rows, dim):
 
 
 # offsets: x and d not 16-byte aligned (at one offset: leading elements in block 0,
-# then aligned vectors; fewer elements than that: the element-wise kernel)
-@pytest.mark.parametrize("f16,n,offset", [(False, 1 << 20, 0), (True, 1 << 20, 0), (False, 1001, 0),
-                                          (True, 1003, 0), (False, 4099, 1), (True, 4101, 1),
-                                          (True, 4101, 6), (False, 2, 3)])
-def test_residual_add(f16, n, offset):
+# then aligned vectors; fewer elements than that, or different offsets: the
+# element-wise kernel)
+@pytest.mark.parametrize("f16,n,offset,d_offset", [(False, 1 << 20, 0, 0), (True, 1 << 20, 0, 0), (False, 1001, 0, 0),
+                                                   (True, 1003, 0, 0), (False, 4099, 1, 1), (True, 4101, 1, 1),
+                                                   (True, 4101, 6, 6), (False, 2, 3, 3), (True, 4101, 1, 2),
+                                                   (False, 4099, 0, 1)])
+def test_residual_add(f16, n, offset, d_offset):
     x, d = normal(44, n), normal(45, n)
     if f16:
         x, d = _f16(x), _f16(d)
-    dx, dd = dev(x, offset), dev(d, offset)
+    dx, dd = dev(x, offset), dev(d, d_offset)
     ql.call("ql_add_f16" if f16 else "ql_add_f32", ptr(dx), ptr(dd), n, stream())
     assert np.array_equal(host(dx), orc.add(x, d, f16=f16))
 
