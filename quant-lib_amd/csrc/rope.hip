@@ -163,24 +163,25 @@ __global__ __launch_bounds__(kBlock) void rope_fast(D* q, D* k, int n_tokens, in
     V hi[HALF ? MAXU : 1];
     D* src[MAXU];
     int hs[MAXU];
+    // Every lane loads (slots past the group, and idle lanes, re-read the group's last
+    // slot's row, in bounds): a load under a per-lane test makes the compiler wait for
+    // it before issuing the next one.
 #pragma unroll
     for (int u = 0; u < MAXU; ++u) {
         const int sl = lane + u * SPW;
-        src[u] = nullptr;
-        hs[u] = -1;
-        if (lane < SPW && sl < nslots) {
-            const int h = h0 + sl / S;
-            hs[u] = h;
-            // Selected as integer addresses: the equivalent nested pointer
-            // select crashes this toolchain's optimizer.
-            const uintptr_t head =
-                h < hq ? reinterpret_cast<uintptr_t>(qt) + sizeof(D) * (size_t)h * d
-                       : (h < hrot ? reinterpret_cast<uintptr_t>(kt) + sizeof(D) * (size_t)(h - hq) * d
-                                   : reinterpret_cast<uintptr_t>(vt) + sizeof(D) * (size_t)(h - hrot) * d);
-            src[u] = reinterpret_cast<D*>(head) + j * W;
-            lo[u] = load<true>(reinterpret_cast<const V*>(src[u]));
-            if constexpr (HALF) hi[u] = load<true>(reinterpret_cast<const V*>(src[u] + npairs));
-        }
+        const bool valid = lane < SPW && sl < nslots;
+        const int h = h0 + min(sl, nslots - 1) / S;
+        // Selected as integer addresses: the equivalent nested pointer
+        // select crashes this toolchain's optimizer.
+        const uintptr_t head =
+            h < hq ? reinterpret_cast<uintptr_t>(qt) + sizeof(D) * (size_t)h * d
+                   : (h < hrot ? reinterpret_cast<uintptr_t>(kt) + sizeof(D) * (size_t)(h - hq) * d
+                               : reinterpret_cast<uintptr_t>(vt) + sizeof(D) * (size_t)(h - hrot) * d);
+        D* const p = reinterpret_cast<D*>(head) + j * W;
+        lo[u] = load<true>(reinterpret_cast<const V*>(p));
+        if constexpr (HALF) hi[u] = load<true>(reinterpret_cast<const V*>(p + npairs));
+        src[u] = valid ? p : nullptr;
+        hs[u] = valid ? h : -1;
     }
 
     float c[PPS], s[PPS];
