@@ -115,7 +115,7 @@ struct AttnArgs {
     // decode (one query row per sequence)
     int n_split;                   // key splits per (sequence, KV head)
     float* ws;                     // [n_seqs, n_heads, n_split, head_dim + 2] partials
-    int hd;                        // head_dim (read by attn_small only)
+    int hd;                        // head_dim (read by attn_small and the narrow prefill)
 };
 
 // Page bases of the consecutive 16-key pages of one decode step (up to 4): the
@@ -340,19 +340,24 @@ __device__ __forceinline__ void load_wave_page(_Float16* sk, _Float16* sv, const
 // full page takes the unchecked path, page bases that are not 16-byte aligned
 // (caller-provided pools) element-wise loads and LDS stores.  Each branch is
 // uniform over the wavefront.
-template <int HD, bool PAGED>
+// NARROW (contiguous, HD 64): heads of a.hd < 64 elements (a multiple of 8); the
+// 16-byte chunks past a.hd load the zero row, so the tile holds the heads
+// zero-padded to 64.
+template <int HD, bool PAGED, bool NARROW = false>
 __device__ __forceinline__ void load_tile(_Float16* sk, _Float16* sv, const AttnArgs& a, uintptr_t pk,
                                           uintptr_t pv, int kvh, int kv0, int kv_len, int wave, int lane) {
     using T = KvTile<HD>;
     if constexpr (!PAGED) {   // rows 16-byte aligned (checked by the entry points)
+        const int hd = NARROW ? a.hd : HD;
 #pragma unroll
         for (int i = 0; i < T::LOADS; ++i) {
             const int base = (i * kAttnWaves + wave) * kWave, slot = base + lane;
             const int r = slot / T::CH, c = (slot % T::CH) ^ tile_swz<HD>(r);
             const int j = kv0 + r;
-            const size_t off = (size_t)j * (size_t)a.kv_stride + (size_t)kvh * HD + (size_t)c * 8;
-            lds_load16(j < kv_len ? a.k + off : kZeroRow + c * 8, sk, base);
-            lds_load16(j < kv_len ? a.v + off : kZeroRow + c * 8, sv, base);
+            const size_t off = (size_t)j * (size_t)a.kv_stride + (size_t)kvh * hd + (size_t)c * 8;
+            const bool ok = j < kv_len && (!NARROW || c * 8 < hd);
+            lds_load16(ok ? a.k + off : kZeroRow + c * 8, sk, base);
+            lds_load16(ok ? a.v + off : kZeroRow + c * 8, sv, base);
         }
     } else if (((pk | pv) & 15) != 0) {
 #pragma unroll
@@ -408,10 +413,11 @@ __device__ __forceinline__ void prefill_item(const AttnArgs& a, int& head, int& 
 
 // Q^T operand: lane holds Q[query][d = 16*kk + 8*hh + 0..7] (zeros past the last query).
 template <int HD>
-__device__ __forceinline__ void load_q_operand(half8 (&qf)[HD / 16], const _Float16* qrow, bool valid, int hh) {
+__device__ __forceinline__ void load_q_operand(half8 (&qf)[HD / 16], const _Float16* qrow, bool valid, int hh,
+                                               int hd = HD) {
 #pragma unroll
     for (int kk = 0; kk < HD / 16; ++kk)
-        qf[kk] = valid ? *reinterpret_cast<const half8*>(qrow + 16 * kk + 8 * hh) : half8{};
+        qf[kk] = valid && 16 * kk + 8 * hh < hd ? *reinterpret_cast<const half8*>(qrow + 16 * kk + 8 * hh) : half8{};
 }
 
 // One wavefront's online-softmax step over a 64-key tile, given its scores
@@ -492,7 +498,8 @@ __device__ __forceinline__ void softmax_pv(floatx16 (&s)[2], floatx16 (&o)[HD / 
 
 // O = O^T / l for the lane's query (both 8-key halves of the sum combined).
 template <int HD>
-__device__ __forceinline__ void store_o(const floatx16 (&o)[HD / 32], float l_run, _Float16* orow, int hh) {
+__device__ __forceinline__ void store_o(const floatx16 (&o)[HD / 32], float l_run, _Float16* orow, int hh,
+                                        int hd = HD) {
     const float l_tot = sum_xor32(l_run);
     const float inv_den = 1.0f / (l_tot + 1e-8f);
 #pragma unroll
@@ -502,7 +509,8 @@ __device__ __forceinline__ void store_o(const floatx16 (&o)[HD / 32], float l_ru
             half4 r;
 #pragma unroll
             for (int e = 0; e < 4; ++e) r[e] = from_f32<_Float16>(o[db][4 * g + e] * inv_den);
-            *reinterpret_cast<half4*>(orow + db * 32 + 8 * g + 4 * hh) = r;
+            if (db * 32 + 8 * g + 4 * hh < hd)   // narrow heads (a multiple of 8): whole 4-element runs
+                *reinterpret_cast<half4*>(orow + db * 32 + 8 * g + 4 * hh) = r;
         }
     }
 }
@@ -513,7 +521,7 @@ __device__ __forceinline__ void store_o(const floatx16 (&o)[HD / 32], float l_ru
 // one stage is placed before the reads of the other.  Paged K/V: wavefront w
 // loads page w of each tile, and the base of its page of tile t+2 is looked up
 // (WavePagePipe) while tile t is multiplied.
-template <int HD, bool PAGED>
+template <int HD, bool PAGED, bool NARROW = false>
 __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
     using T = KvTile<HD>;
     constexpr int NKK = HD / 16;   // MFMA steps over d for S^T
@@ -562,8 +570,9 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
     const bool wave_has_q = q0 + wave * 32 < q_len;
 
     half8 qf[NKK];
-    load_q_operand<HD>(qf, a.q + (size_t)(q_begin + (q_valid ? qi : 0)) * a.q_stride + (size_t)head * HD,
-                       q_valid, hh);
+    const int hd = NARROW ? a.hd : HD;   // the heads' width in memory
+    load_q_operand<HD>(qf, a.q + (size_t)(q_begin + (q_valid ? qi : 0)) * a.q_stride + (size_t)head * hd,
+                       q_valid, hh, hd);
     floatx16 o[NDB];
 #pragma unroll
     for (int i = 0; i < NDB; ++i) o[i] = floatx16{};
@@ -671,14 +680,14 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
             pp.bases(a, kvh, HD, pgk, pgv);
         }
         if (n_tiles > 2) pp.entry(a, table, 2 * kTilePages + wave);
-        load_tile<HD, PAGED>(sk0, sv0, a, k0, v0, kvh, 0, kv_len, wave, lane);
+        load_tile<HD, PAGED, NARROW>(sk0, sv0, a, k0, v0, kvh, 0, kv_len, wave, lane);
     }
     wait_tile_loads();
     __syncthreads();
     // tile t sits in (sk, sv); tile t+1 is loaded into (nk, nv) meanwhile
     auto step = [&](int t, const _Float16* sk, const _Float16* sv, _Float16* nk, _Float16* nv) {
         const int kv0 = t * kBK;
-        if (t + 1 < n_tiles) load_tile<HD, PAGED>(nk, nv, a, pgk, pgv, kvh, kv0 + kBK, kv_len, wave, lane);
+        if (t + 1 < n_tiles) load_tile<HD, PAGED, NARROW>(nk, nv, a, pgk, pgv, kvh, kv0 + kBK, kv_len, wave, lane);
         if (t + 2 < n_tiles) pp.pointers(a);                                    // tile t+2
         if (t + 3 < n_tiles) pp.entry(a, table, (t + 3) * kTilePages + wave);   // tile t+3
         compute(sk, sv, kv0);
@@ -693,7 +702,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
     }
 
     if (!q_valid) return;
-    store_o<HD>(o, l_run, a.out + (size_t)(q_begin + qi) * a.o_stride + (size_t)head * HD, hh);
+    store_o<HD>(o, l_run, a.out + (size_t)(q_begin + qi) * a.o_stride + (size_t)head * hd, hh, hd);
 }
 
 // ---- decode: one query row per sequence ------------------------------------------------
@@ -1343,8 +1352,12 @@ hipError_t launch_attn(const AttnArgs& a, int head_dim, unsigned gx, unsigned gz
     const dim3 grid(gx * (unsigned)a.n_heads, 1, gz);
     if (head_dim == 128) {
         hipLaunchKernelGGL((attn_fwd<128, PAGED>), grid, dim3(kAttnThreads), 0, stream, a);
-    } else {
+    } else if (head_dim == 64) {
         hipLaunchKernelGGL((attn_fwd<64, PAGED>), grid, dim3(kAttnThreads), 0, stream, a);
+    } else if constexpr (!PAGED) {   // narrow heads, zero-padded to 64 in the tiles
+        hipLaunchKernelGGL((attn_fwd<64, false, true>), grid, dim3(kAttnThreads), 0, stream, a);
+    } else {
+        return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
@@ -1353,8 +1366,9 @@ bool aligned_rows(const void* p, int64_t stride) {
     return qlh::aligned16(p) && stride % 8 == 0;
 }
 
-// head_dim 64 and 128 run the matrix-core kernels; every other value up to 64
-// (the reference kernel's range) runs attn_small.
+// head_dim 64 and 128 run the matrix-core kernels, as does a prefill over narrower
+// heads of a multiple of 8 (zero-padded to 64 in the tiles); every other value up to
+// 64 (the reference kernel's range) runs attn_small.
 bool mfma_hd(int head_dim) { return head_dim == 64 || head_dim == 128; }
 bool valid_hd(int head_dim) { return head_dim == 128 || (head_dim >= 1 && head_dim <= 64); }
 
@@ -1432,6 +1446,11 @@ extern "C" hipError_t ql_attention_f16(const uint16_t* q, const uint16_t* k, con
         QL_CHECK_ARG(aligned_rows(q, q_row_stride) && aligned_rows(out, out_row_stride));
         QL_CHECK_ARG(kv_len == 0 || (aligned_rows(k, kv_row_stride) && aligned_rows(v, kv_row_stride)));
     }
+    // narrow heads (a multiple of 8 below 64) with 16-byte aligned rows: the
+    // head_dim-64 matrix-core kernel with the heads zero-padded in its tiles
+    const bool narrow = head_dim < 64 && head_dim % 8 == 0 && q_len > 1 && aligned_rows(q, q_row_stride) &&
+                        aligned_rows(out, out_row_stride) &&
+                        (kv_len == 0 || (aligned_rows(k, kv_row_stride) && aligned_rows(v, kv_row_stride)));
     AttnArgs a{};
     a.q = reinterpret_cast<const _Float16*>(q);
     a.out = reinterpret_cast<_Float16*>(out);
@@ -1447,6 +1466,7 @@ extern "C" hipError_t ql_attention_f16(const uint16_t* q, const uint16_t* k, con
     a.v = reinterpret_cast<const _Float16*>(v);
     a.kv_stride = kv_row_stride;
     a.hd = head_dim;
+    if (narrow) return launch_attn<false>(a, head_dim, qlh::blocks_for(q_len, kBQ), 1, stream);
     if (!mfma_hd(head_dim)) return launch_small<false>(a, q_len, 1, stream);
     if (q_len == 1) {   // decode: the query heads of a KV head share one pass over K/V
         a.n_split = 1;

@@ -91,14 +91,16 @@ def test_launch_flash_attention_shim_tinyllama_shape():
     check_attn(g1, orc.attention(q, k, v, h, hkv, True, f16=True), v, "launch_flash_attention")
 
 
-# ---- head_dims below 64 (the reference kernel's range; the vector-ALU kernel) ---------------
+# ---- head_dims below 64 (the reference kernel's range) ---------------------------------------
 # The reference's launch_flash_attention takes any head_dim <= 64
-# (kernels/flash_attention.cu:25-27,64-66); 64 and 128 run on the matrix cores,
-# every other value on attn_small, whose probabilities stay fp32 (tighter than
-# the bound above).  The shim and the C ABI must give the same bits.
+# (kernels/flash_attention.cu:25-27,64-66); 64 and 128 run on the matrix cores, and
+# so does a prefill over heads of a multiple of 8 (zero-padded to 64 in the tiles);
+# every other value, and one-query calls, run attn_small, whose probabilities stay
+# fp32 (tighter than the bound above).  The shim and the C ABI must give the same bits.
 @pytest.mark.parametrize("seq,h,hkv,d,causal", [
     (1, 4, 2, 32, 1), (77, 32, 4, 32, 1), (300, 8, 2, 48, 1), (129, 6, 3, 40, 0),
-    (513, 4, 4, 16, 1), (65, 2, 1, 8, 1), (100, 3, 1, 63, 0), (257, 4, 2, 1, 1), (64, 4, 1, 33, 1)])
+    (513, 4, 4, 16, 1), (65, 2, 1, 8, 1), (100, 3, 1, 63, 0), (257, 4, 2, 1, 1), (64, 4, 1, 33, 1),
+    (200, 6, 2, 24, 1), (131, 4, 4, 56, 0), (1000, 8, 1, 32, 1), (2, 3, 3, 8, 0)])
 def test_flash_attention_small_head_dims(seq, h, hkv, d, causal):
     f = getattr(ql.lib(), COMPAT_MANGLED["launch_flash_attention"])
     f.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int] * 5 + [ctypes.c_void_p]
