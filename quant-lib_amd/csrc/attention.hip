@@ -768,10 +768,12 @@ struct DecPlan {
     int v_page;
     int key;              // the lane's first key in the step
 
-    __device__ __forceinline__ DecPlan(const AttnArgs& a, int kvh, int lane) {
+    // hd: the heads' width in memory (HD, or a narrower contiguous head, decode
+    // with the chunks past it zero)
+    __device__ __forceinline__ DecPlan(const AttnArgs& a, int kvh, int lane, int hd = HD) {
         row_bytes = PAGED ? (uint32_t)(a.n_kv_heads * HD * sizeof(_Float16))
                           : (uint32_t)(a.kv_stride * sizeof(_Float16));
-        const uint32_t head_bytes = PAGED ? 0u : (uint32_t)(kvh * HD * sizeof(_Float16));
+        const uint32_t head_bytes = PAGED ? 0u : (uint32_t)(kvh * hd * sizeof(_Float16));
         const int ch = lane % T::CH, kg = lane / T::CH;
         key = T::KPL * kg;   // its KPL keys stay inside one page
         v_page = key >> 4;
@@ -864,10 +866,12 @@ __device__ __forceinline__ void dec_stage_k(DecK<HD>& r, _Float16* sk, const Att
 // separate branch, the compiler's wait before the first product of every step,
 // at the join of the two paths, waited for 13 of the 16 rows just issued for
 // the next step.)
-template <int HD, bool PAGED>
+// NARROW (contiguous HD 64, heads of hd < 64): lanes whose chunk lies past the
+// head read the zero row instead, so the staged K and V are the heads zero-padded.
+template <int HD, bool PAGED, bool NARROW = false>
 __device__ __forceinline__ void dec_fetch_kv(DecK<HD>& rk, DecV<HD>& rv, const AttnArgs& a,
                                              const DecPlan<HD, PAGED>& plan, const Pages& pg,
-                                             int k0, int k_end, uintptr_t dummy, int lane) {
+                                             int k0, int k_end, uintptr_t dummy, int lane, int hd = HD) {
     using T = Dec<HD>;
     uint32_t klive, vlive;
     const uintptr_t krow = dec_rows<HD, PAGED>(a, plan, pg.k, a.k, k0, k_end, klive);
@@ -878,9 +882,11 @@ __device__ __forceinline__ void dec_fetch_kv(DecK<HD>& rk, DecV<HD>& rv, const A
     const int last = PAGED ? T::KPL - 1 : (n_in > 0 ? min(n_in, T::KPL) - 1 : 0);
     const bool kok = krow != 0 && !mis && (PAGED || n_in > 0);
     const bool vok = vrow != 0 && !mis && (PAGED || n_in > 0);
-    const uintptr_t dchunk = dummy + 16u * (uint32_t)(lane % T::CH);
-    const uintptr_t kb = kok ? krow : dchunk, vb = vok ? vrow : dchunk;
-    const uint32_t ks = kok ? plan.row_bytes : 0u, vs = vok ? plan.row_bytes : 0u;
+    const bool pad = NARROW && (lane % T::CH) * 8 >= hd;
+    const uintptr_t dchunk = pad ? reinterpret_cast<uintptr_t>(kZeroRow) + 16u * (uint32_t)(lane % T::CH)
+                                 : dummy + 16u * (uint32_t)(lane % T::CH);
+    const uintptr_t kb = kok && !pad ? krow : dchunk, vb = vok && !pad ? vrow : dchunk;
+    const uint32_t ks = kok && !pad ? plan.row_bytes : 0u, vs = vok && !pad ? plan.row_bytes : 0u;
     (void)klive;
     (void)vlive;
 #pragma unroll
@@ -1012,7 +1018,9 @@ __device__ __forceinline__ bool dec_sequence(const AttnArgs& a, int s, int& q_ro
     return true;
 }
 
-template <int HD, bool PAGED>
+// NARROW: contiguous K/V with heads of a.hd < 64 (a multiple of 8) on the HD 64
+// kernel, zero-padded, one key split.
+template <int HD, bool PAGED, bool NARROW = false>
 __global__ __launch_bounds__(kAttnThreads, 2) void attn_decode(AttnArgs a) {
     using T = Dec<HD>;
     __shared__ __attribute__((aligned(16))) char smem_raw[T::SMEM_BYTES];
@@ -1037,12 +1045,14 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_decode(AttnArgs a) {
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int col = lane & 15, hq = lane >> 4;
     const bool col_ok = col < G;
+    const int hd = NARROW ? a.hd : HD;   // the heads' width in memory
     half8 qf[T::NKK];
     {
-        const _Float16* qrow = a.q + (size_t)q_row * a.q_stride + (size_t)(hb + (col_ok ? col : 0)) * HD;
+        const _Float16* qrow = a.q + (size_t)q_row * a.q_stride + (size_t)(hb + (col_ok ? col : 0)) * hd;
 #pragma unroll
         for (int kk = 0; kk < T::NKK; ++kk)
-            qf[kk] = col_ok ? *reinterpret_cast<const half8*>(qrow + 32 * kk + 8 * hq) : half8{};
+            qf[kk] = col_ok && 32 * kk + 8 * hq < hd ? *reinterpret_cast<const half8*>(qrow + 32 * kk + 8 * hq)
+                                                     : half8{};
     }
     floatx4 o[T::NDB];
 #pragma unroll
@@ -1062,7 +1072,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_decode(AttnArgs a) {
     constexpr int kStepPages = kDecStep / QL_PAGE_SIZE;
     DecK<HD> kr;
     DecV<HD> vr;
-    const DecPlan<HD, PAGED> plan(a, kvh, lane);
+    const DecPlan<HD, PAGED> plan(a, kvh, lane, hd);
     PagePipe<PAGED, kStepPages> pp;
     int step = wave;
     Pages pg_next{};
@@ -1080,7 +1090,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_decode(AttnArgs a) {
             pg_next = pp.bases(a, kvh, HD);
         }
         if (step + 2 * kAttnWaves < n_steps) pp.entries(a, table, page_of(step + 2 * kAttnWaves));
-        dec_fetch_kv<HD, PAGED>(kr, vr, a, plan, pg, k0, k_end, dummy, lane);
+        dec_fetch_kv<HD, PAGED, NARROW>(kr, vr, a, plan, pg, k0, k_end, dummy, lane, hd);
         dec_stage_v<HD, PAGED>(vr, sv, a, plan, pg, k0, k_end, lane);
     }
     // one step: stage its K rows, prefetch the wavefront's next step into the
@@ -1098,7 +1108,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_decode(AttnArgs a) {
         // wait for the rows
         pp.pointers(a);
         pp.entries(a, table, page_of(step + 3 * kAttnWaves));
-        dec_fetch_kv<HD, PAGED>(kr, vr, a, plan, pg_next, k0 + kStride, k_end, dummy, lane);
+        dec_fetch_kv<HD, PAGED, NARROW>(kr, vr, a, plan, pg_next, k0 + kStride, k_end, dummy, lane, hd);
         dec_step<HD>(sk, qf, o, st, sv, k0, k_end, lane, cl2);
         if (!more) return false;
         dec_stage_v<HD, PAGED>(vr, sv, a, plan, pg_next, k0 + kStride, k_end, lane);    // after this step's V^T reads (in order)
@@ -1140,8 +1150,9 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_decode(AttnArgs a) {
             lsum = fmaf(f, pp[HD + 1], lsum);
         }
         const int h = hb + c;
-        if (a.n_split == 1) {
-            a.out[(size_t)q_row * a.o_stride + (size_t)h * HD + d] = from_f32<_Float16>(acc / (lsum + 1e-8f));
+        if (NARROW || a.n_split == 1) {   // narrow heads: one split, columns past the head dropped
+            if (d < hd)
+                a.out[(size_t)q_row * a.o_stride + (size_t)h * hd + d] = from_f32<_Float16>(acc / (lsum + 1e-8f));
         } else {
             float* w = a.ws + (((size_t)s * a.n_heads + h) * a.n_split + sp) * (HD + 2);
             w[d] = acc;
@@ -1418,10 +1429,15 @@ hipError_t launch_decode(const AttnArgs& a, int head_dim, int n_seqs, hipStream_
         hipLaunchKernelGGL((attn_decode<128, PAGED>), grid, dim3(kAttnThreads), 0, stream, a);
         if (a.n_split > 1)
             hipLaunchKernelGGL((attn_decode_combine<128, PAGED>), cgrid, dim3(kMaxSplits), 0, stream, a);
-    } else {
+    } else if (head_dim == 64) {
         hipLaunchKernelGGL((attn_decode<64, PAGED>), grid, dim3(kAttnThreads), 0, stream, a);
         if (a.n_split > 1)
             hipLaunchKernelGGL((attn_decode_combine<64, PAGED>), cgrid, dim3(kMaxSplits), 0, stream, a);
+    } else if constexpr (!PAGED) {   // narrow heads: one split (the caller sets n_split = 1)
+        QL_CHECK_ARG(a.n_split == 1);
+        hipLaunchKernelGGL((attn_decode<64, false, true>), grid, dim3(kAttnThreads), 0, stream, a);
+    } else {
+        return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
@@ -1448,7 +1464,7 @@ extern "C" hipError_t ql_attention_f16(const uint16_t* q, const uint16_t* k, con
     }
     // narrow heads (a multiple of 8 below 64) with 16-byte aligned rows: the
     // head_dim-64 matrix-core kernel with the heads zero-padded in its tiles
-    const bool narrow = head_dim < 64 && head_dim % 8 == 0 && q_len > 1 && aligned_rows(q, q_row_stride) &&
+    const bool narrow = head_dim < 64 && head_dim % 8 == 0 && aligned_rows(q, q_row_stride) &&
                         aligned_rows(out, out_row_stride) &&
                         (kv_len == 0 || (aligned_rows(k, kv_row_stride) && aligned_rows(v, kv_row_stride)));
     AttnArgs a{};
@@ -1466,8 +1482,8 @@ extern "C" hipError_t ql_attention_f16(const uint16_t* q, const uint16_t* k, con
     a.v = reinterpret_cast<const _Float16*>(v);
     a.kv_stride = kv_row_stride;
     a.hd = head_dim;
-    if (narrow) return launch_attn<false>(a, head_dim, qlh::blocks_for(q_len, kBQ), 1, stream);
-    if (!mfma_hd(head_dim)) return launch_small<false>(a, q_len, 1, stream);
+    if (narrow && q_len > 1) return launch_attn<false>(a, head_dim, qlh::blocks_for(q_len, kBQ), 1, stream);
+    if (!mfma_hd(head_dim) && !narrow) return launch_small<false>(a, q_len, 1, stream);
     if (q_len == 1) {   // decode: the query heads of a KV head share one pass over K/V
         a.n_split = 1;
         return launch_decode<false>(a, head_dim, 1, stream);
@@ -1583,6 +1599,11 @@ extern "C" hipError_t ql_decode_attention_f16(const uint16_t* q, const uint16_t*
     a.v = reinterpret_cast<const _Float16*>(v);
     a.kv_stride = kv_row_stride;
     a.hd = head_dim;
+    if (head_dim < 64 && head_dim % 8 == 0 && aligned_rows(q, qs) && aligned_rows(out, qs) &&
+        (kv_len == 0 || (aligned_rows(k, kv_row_stride) && aligned_rows(v, kv_row_stride)))) {
+        a.n_split = 1;   // narrow heads on the head_dim-64 kernel, zero-padded: one pass, no workspace
+        return launch_decode<false>(a, head_dim, 1, stream);
+    }
     if (!mfma_hd(head_dim)) return launch_small<false>(a, 1, 1, stream);
     // as many key splits as wanted and the workspace holds (1 = no workspace used)
     int n_split = dec_splits(1, n_kv_heads, dec_col_chunks(n_heads, n_kv_heads), kv_len);

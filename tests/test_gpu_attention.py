@@ -210,10 +210,12 @@ def test_paged_attention_small_head_dims(d):
                    f"paged decode head_dim {d} sequence {s}")
 
 
-def test_contiguous_decode_small_head_dim():
-    # ql_decode_attention_f16 at head_dim 32 (no workspace needed) equals
-    # ql_attention_f16 with one query, and the oracle
-    h, hkv, d, kv = 16, 4, 32, 3000
+@pytest.mark.parametrize("h,hkv,d,kv", [(16, 4, 32, 3000), (8, 8, 8, 65), (32, 8, 16, 1), (6, 2, 24, 500),
+                                        (12, 3, 40, 4097), (4, 1, 48, 33), (20, 4, 56, 2000), (16, 4, 36, 700)])
+def test_contiguous_decode_small_head_dim(h, hkv, d, kv):
+    # ql_decode_attention_f16 (no workspace needed) equals ql_attention_f16 with one
+    # query, and the oracle: heads of a multiple of 8 on the head_dim-64 decode
+    # kernel, zero-padded; 36 on attn_small
     q, k, v = qkv(31, 1, kv, h, hkv, d)
     dq, dk, dv = dev(q), dev(k), dev(v)
     o1, o2 = Out(h * d, np.uint16), Out(h * d, np.uint16)
@@ -223,7 +225,7 @@ def test_contiguous_decode_small_head_dim():
             stream())
     g1 = o1.get((1, h, d))
     assert np.array_equal(g1, o2.get((1, h, d)))
-    check_attn(g1, orc.attention(q, k, v, h, hkv, True, f16=True), v, "decode head_dim 32")
+    check_attn(g1, orc.attention(q, k, v, h, hkv, True, f16=True), v, f"decode head_dim {d} kv={kv}")
 
 
 # ---- decode / chunked prefill over a contiguous cache, strided rows -----------------------
