@@ -100,7 +100,7 @@ def test_launch_flash_attention_shim_tinyllama_shape():
 @pytest.mark.parametrize("seq,h,hkv,d,causal", [
     (1, 4, 2, 32, 1), (77, 32, 4, 32, 1), (300, 8, 2, 48, 1), (129, 6, 3, 40, 0),
     (513, 4, 4, 16, 1), (65, 2, 1, 8, 1), (100, 3, 1, 63, 0), (257, 4, 2, 1, 1), (64, 4, 1, 33, 1),
-    (200, 6, 2, 24, 1), (131, 4, 4, 56, 0), (1000, 8, 1, 32, 1), (2, 3, 3, 8, 0)])
+    (200, 6, 2, 24, 1), (131, 4, 4, 56, 0), (1000, 8, 1, 32, 1), (2, 3, 3, 8, 0), (90, 4, 2, 20, 1)])
 def test_flash_attention_small_head_dims(seq, h, hkv, d, causal):
     f = getattr(ql.lib(), COMPAT_MANGLED["launch_flash_attention"])
     f.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int] * 5 + [ctypes.c_void_p]
