@@ -313,20 +313,21 @@ __device__ __forceinline__ void lds_load16(const void* src, _Float16* stage, int
 // (w*LOADS + i)*64 + lane, i.e. key row r = slot / CH, chunk (slot % CH) ^
 // tile_swz(r), row r % 16 of the page.  CHECKED: keys past kv_len and a missing
 // page read kZeroRow.
-template <int HD, bool CHECKED>
+template <int HD, bool CHECKED, bool NARROW = false>
 __device__ __forceinline__ void load_wave_page(_Float16* sk, _Float16* sv, const AttnArgs& a, uintptr_t pk,
                                                uintptr_t pv, int kv0, int kv_len, int wave, int lane) {
     using T = KvTile<HD>;
+    const int hd = NARROW ? a.hd : HD;
 #pragma unroll
     for (int i = 0; i < T::LOADS; ++i) {
         const int base = (wave * T::LOADS + i) * kWave, slot = base + lane;
         const int r = slot / T::CH, c = (slot % T::CH) ^ tile_swz<HD>(r);
         const uintptr_t off =
-            (uintptr_t)(r & (QL_PAGE_SIZE - 1)) * (uintptr_t)a.n_kv_heads * HD * sizeof(_Float16) + 16u * c;
+            (uintptr_t)(r & (QL_PAGE_SIZE - 1)) * (uintptr_t)a.n_kv_heads * hd * sizeof(_Float16) + 16u * c;
         uintptr_t kg = pk + off, vg = pv + off;
-        if constexpr (CHECKED) {
+        if constexpr (CHECKED || NARROW) {
             const uintptr_t zero = reinterpret_cast<uintptr_t>(kZeroRow) + 16u * c;
-            const bool ok = kv0 + r < kv_len;
+            const bool ok = (!CHECKED || kv0 + r < kv_len) && (!NARROW || c * 8 < hd);
             kg = ok && pk != 0 ? kg : zero;
             vg = ok && pv != 0 ? vg : zero;
         }
@@ -340,9 +341,8 @@ __device__ __forceinline__ void load_wave_page(_Float16* sk, _Float16* sv, const
 // full page takes the unchecked path, page bases that are not 16-byte aligned
 // (caller-provided pools) element-wise loads and LDS stores.  Each branch is
 // uniform over the wavefront.
-// NARROW (contiguous, HD 64): heads of a.hd < 64 elements (a multiple of 8); the
-// 16-byte chunks past a.hd load the zero row, so the tile holds the heads
-// zero-padded to 64.
+// NARROW (HD 64): heads of a.hd < 64 elements (a multiple of 8); the 16-byte
+// chunks past a.hd load the zero row, so the tile holds the heads zero-padded to 64.
 template <int HD, bool PAGED, bool NARROW = false>
 __device__ __forceinline__ void load_tile(_Float16* sk, _Float16* sv, const AttnArgs& a, uintptr_t pk,
                                           uintptr_t pv, int kvh, int kv0, int kv_len, int wave, int lane) {
@@ -360,21 +360,22 @@ __device__ __forceinline__ void load_tile(_Float16* sk, _Float16* sv, const Attn
             lds_load16(ok ? a.v + off : kZeroRow + c * 8, sv, base);
         }
     } else if (((pk | pv) & 15) != 0) {
+        const int hd = NARROW ? a.hd : HD;
 #pragma unroll
         for (int i = 0; i < T::LOADS; ++i) {
             const int slot = (wave * T::LOADS + i) * kWave + lane;
             const int r = slot / T::CH, c = (slot % T::CH) ^ tile_swz<HD>(r);
             const uintptr_t off =
-                (uintptr_t)(r & (QL_PAGE_SIZE - 1)) * (uintptr_t)a.n_kv_heads * HD * sizeof(_Float16) + 16u * c;
+                (uintptr_t)(r & (QL_PAGE_SIZE - 1)) * (uintptr_t)a.n_kv_heads * hd * sizeof(_Float16) + 16u * c;
             const uintptr_t zero = reinterpret_cast<uintptr_t>(kZeroRow) + 16u * c;
-            const bool ok = kv0 + r < kv_len;
+            const bool ok = kv0 + r < kv_len && (!NARROW || c * 8 < hd);
             *reinterpret_cast<half8*>(sk + slot * 8) = load_chunk_unaligned(ok && pk != 0 ? pk + off : zero, 0);
             *reinterpret_cast<half8*>(sv + slot * 8) = load_chunk_unaligned(ok && pv != 0 ? pv + off : zero, 0);
         }
     } else if (kv0 + (wave + 1) * QL_PAGE_SIZE <= kv_len && pk != 0 && pv != 0) {
-        load_wave_page<HD, false>(sk, sv, a, pk, pv, kv0, kv_len, wave, lane);
+        load_wave_page<HD, false, NARROW>(sk, sv, a, pk, pv, kv0, kv_len, wave, lane);
     } else {
-        load_wave_page<HD, true>(sk, sv, a, pk, pv, kv0, kv_len, wave, lane);
+        load_wave_page<HD, true, NARROW>(sk, sv, a, pk, pv, kv0, kv_len, wave, lane);
     }
 }
 
@@ -673,11 +674,11 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
         uintptr_t k0 = 0, v0 = 0;
         pp.entry(a, table, wave);
         pp.pointers(a);
-        pp.bases(a, kvh, HD, k0, v0);
+        pp.bases(a, kvh, hd, k0, v0);
         if (n_tiles > 1) {
             pp.entry(a, table, kTilePages + wave);
             pp.pointers(a);
-            pp.bases(a, kvh, HD, pgk, pgv);
+            pp.bases(a, kvh, hd, pgk, pgv);
         }
         if (n_tiles > 2) pp.entry(a, table, 2 * kTilePages + wave);
         load_tile<HD, PAGED, NARROW>(sk0, sv0, a, k0, v0, kvh, 0, kv_len, wave, lane);
@@ -691,7 +692,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd(AttnArgs a) {
         if (t + 2 < n_tiles) pp.pointers(a);                                    // tile t+2
         if (t + 3 < n_tiles) pp.entry(a, table, (t + 3) * kTilePages + wave);   // tile t+3
         compute(sk, sv, kv0);
-        if (t + 2 < n_tiles) pp.bases(a, kvh, HD, pgk, pgv);
+        if (t + 2 < n_tiles) pp.bases(a, kvh, hd, pgk, pgv);
         wait_tile_loads();
         __syncthreads();
     };
@@ -771,7 +772,7 @@ struct DecPlan {
     // hd: the heads' width in memory (HD, or a narrower contiguous head, decode
     // with the chunks past it zero)
     __device__ __forceinline__ DecPlan(const AttnArgs& a, int kvh, int lane, int hd = HD) {
-        row_bytes = PAGED ? (uint32_t)(a.n_kv_heads * HD * sizeof(_Float16))
+        row_bytes = PAGED ? (uint32_t)(a.n_kv_heads * hd * sizeof(_Float16))
                           : (uint32_t)(a.kv_stride * sizeof(_Float16));
         const uint32_t head_bytes = PAGED ? 0u : (uint32_t)(kvh * hd * sizeof(_Float16));
         const int ch = lane % T::CH, kg = lane / T::CH;
@@ -837,7 +838,7 @@ __device__ __forceinline__ uintptr_t dec_rows(const AttnArgs& a, const DecPlan<H
 template <int HD, bool PAGED>
 __device__ __forceinline__ void dec_stage_k(DecK<HD>& r, _Float16* sk, const AttnArgs& a,
                                             const DecPlan<HD, PAGED>& plan, const Pages& pg, int k0,
-                                            int k_end, int lane) {
+                                            int k_end, int lane, int hd = HD) {
     using T = Dec<HD>;
     const int ch = lane % T::CH, kg = lane / T::CH;
     if (!dec_full<PAGED>(pg.k, pg.misaligned, k0, k_end)) {   // wavefront-uniform
@@ -845,7 +846,7 @@ __device__ __forceinline__ void dec_stage_k(DecK<HD>& r, _Float16* sk, const Att
         const uintptr_t row = dec_rows<HD, PAGED>(a, plan, pg.k, a.k, k0, k_end, live);
 #pragma unroll
         for (int i = 0; i < T::KPL; ++i) {
-            if (PAGED && pg.misaligned && ((live >> i) & 1))
+            if (PAGED && pg.misaligned && ((live >> i) & 1) && ch * 8 < hd)   // chunks past a narrow head stay zero
                 r.k[i] = load8_unaligned(row + (uintptr_t)i * plan.row_bytes);
             if (!((live >> i) & 1)) r.k[i] = half8{};
         }
@@ -904,7 +905,7 @@ __device__ __forceinline__ int vt_unit(int r, int u) { return u ^ ((r >> 4) & 7)
 template <int HD, bool PAGED>
 __device__ __forceinline__ void dec_stage_v(DecV<HD>& r, _Float16* sv, const AttnArgs& a,
                                             const DecPlan<HD, PAGED>& plan, const Pages& pg, int k0,
-                                            int k_end, int lane) {
+                                            int k_end, int lane, int hd = HD) {
     using T = Dec<HD>;
     const int ch = lane % T::CH, kg = lane / T::CH;
     if (!dec_full<PAGED>(pg.v, pg.misaligned, k0, k_end)) {   // wavefront-uniform
@@ -912,7 +913,7 @@ __device__ __forceinline__ void dec_stage_v(DecV<HD>& r, _Float16* sv, const Att
         const uintptr_t row = dec_rows<HD, PAGED>(a, plan, pg.v, a.v, k0, k_end, live);
 #pragma unroll
         for (int i = 0; i < T::KPL; ++i) {
-            if (PAGED && pg.misaligned && ((live >> i) & 1))
+            if (PAGED && pg.misaligned && ((live >> i) & 1) && ch * 8 < hd)   // chunks past a narrow head stay zero
                 r.v[i] = load8_unaligned(row + (uintptr_t)i * plan.row_bytes);
             if (!((live >> i) & 1)) r.v[i] = half8{};
         }
@@ -1082,16 +1083,16 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_decode(AttnArgs a) {
         const int k0 = k_begin + step * kDecStep;
         pp.entries(a, table, page_of(step));
         pp.pointers(a);
-        const Pages pg = pp.bases(a, kvh, HD);
+        const Pages pg = pp.bases(a, kvh, hd);
         pg_k = pg;
         if (step + kAttnWaves < n_steps) {
             pp.entries(a, table, page_of(step + kAttnWaves));
             pp.pointers(a);
-            pg_next = pp.bases(a, kvh, HD);
+            pg_next = pp.bases(a, kvh, hd);
         }
         if (step + 2 * kAttnWaves < n_steps) pp.entries(a, table, page_of(step + 2 * kAttnWaves));
         dec_fetch_kv<HD, PAGED, NARROW>(kr, vr, a, plan, pg, k0, k_end, dummy, lane, hd);
-        dec_stage_v<HD, PAGED>(vr, sv, a, plan, pg, k0, k_end, lane);
+        dec_stage_v<HD, PAGED>(vr, sv, a, plan, pg, k0, k_end, lane, hd);
     }
     // one step: stage its K rows, prefetch the wavefront's next step into the
     // registers, multiply, then stage the next step's V rows
@@ -1103,7 +1104,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_decode(AttnArgs a) {
     auto run_step = [&]() -> bool {
         const int k0 = k_begin + step * kDecStep;
         const bool more = step + kAttnWaves < n_steps;
-        dec_stage_k<HD, PAGED>(kr, sk, a, plan, pg_k, k0, k_end, lane);   // after the previous step's K reads (in order)
+        dec_stage_k<HD, PAGED>(kr, sk, a, plan, pg_k, k0, k_end, lane, hd);   // after the previous step's K reads (in order)
         // page lookups first: issued after the K/V rows, their waits would also
         // wait for the rows
         pp.pointers(a);
@@ -1111,9 +1112,9 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_decode(AttnArgs a) {
         dec_fetch_kv<HD, PAGED, NARROW>(kr, vr, a, plan, pg_next, k0 + kStride, k_end, dummy, lane, hd);
         dec_step<HD>(sk, qf, o, st, sv, k0, k_end, lane, cl2);
         if (!more) return false;
-        dec_stage_v<HD, PAGED>(vr, sv, a, plan, pg_next, k0 + kStride, k_end, lane);    // after this step's V^T reads (in order)
+        dec_stage_v<HD, PAGED>(vr, sv, a, plan, pg_next, k0 + kStride, k_end, lane, hd);    // after this step's V^T reads (in order)
         pg_k = pg_next;
-        if (step + 2 * kAttnWaves < n_steps) pg_next = pp.bases(a, kvh, HD);
+        if (step + 2 * kAttnWaves < n_steps) pg_next = pp.bases(a, kvh, hd);
         step += kAttnWaves;
         return true;
     };
@@ -1365,10 +1366,8 @@ hipError_t launch_attn(const AttnArgs& a, int head_dim, unsigned gx, unsigned gz
         hipLaunchKernelGGL((attn_fwd<128, PAGED>), grid, dim3(kAttnThreads), 0, stream, a);
     } else if (head_dim == 64) {
         hipLaunchKernelGGL((attn_fwd<64, PAGED>), grid, dim3(kAttnThreads), 0, stream, a);
-    } else if constexpr (!PAGED) {   // narrow heads, zero-padded to 64 in the tiles
-        hipLaunchKernelGGL((attn_fwd<64, false, true>), grid, dim3(kAttnThreads), 0, stream, a);
-    } else {
-        return hipErrorInvalidValue;
+    } else {   // narrow heads, zero-padded to 64 in the tiles
+        hipLaunchKernelGGL((attn_fwd<64, PAGED, true>), grid, dim3(kAttnThreads), 0, stream, a);
     }
     return hipGetLastError();
 }
@@ -1381,6 +1380,7 @@ bool aligned_rows(const void* p, int64_t stride) {
 // heads of a multiple of 8 (zero-padded to 64 in the tiles); every other value up to
 // 64 (the reference kernel's range) runs attn_small.
 bool mfma_hd(int head_dim) { return head_dim == 64 || head_dim == 128; }
+bool narrow_hd(int head_dim) { return head_dim < 64 && head_dim % 8 == 0; }
 bool valid_hd(int head_dim) { return head_dim == 128 || (head_dim >= 1 && head_dim <= 64); }
 
 // attn_small over n_seqs sequences of at most max_q_len queries (grid z = n_seqs).
@@ -1433,11 +1433,9 @@ hipError_t launch_decode(const AttnArgs& a, int head_dim, int n_seqs, hipStream_
         hipLaunchKernelGGL((attn_decode<64, PAGED>), grid, dim3(kAttnThreads), 0, stream, a);
         if (a.n_split > 1)
             hipLaunchKernelGGL((attn_decode_combine<64, PAGED>), cgrid, dim3(kMaxSplits), 0, stream, a);
-    } else if constexpr (!PAGED) {   // narrow heads: one split (the caller sets n_split = 1)
+    } else {   // narrow heads: one split (the caller sets n_split = 1)
         QL_CHECK_ARG(a.n_split == 1);
-        hipLaunchKernelGGL((attn_decode<64, false, true>), grid, dim3(kAttnThreads), 0, stream, a);
-    } else {
-        return hipErrorInvalidValue;
+        hipLaunchKernelGGL((attn_decode<64, PAGED, true>), grid, dim3(kAttnThreads), 0, stream, a);
     }
     return hipGetLastError();
 }
@@ -1464,7 +1462,7 @@ extern "C" hipError_t ql_attention_f16(const uint16_t* q, const uint16_t* k, con
     }
     // narrow heads (a multiple of 8 below 64) with 16-byte aligned rows: the
     // head_dim-64 matrix-core kernel with the heads zero-padded in its tiles
-    const bool narrow = head_dim < 64 && head_dim % 8 == 0 && aligned_rows(q, q_row_stride) &&
+    const bool narrow = narrow_hd(head_dim) && aligned_rows(q, q_row_stride) &&
                         aligned_rows(out, out_row_stride) &&
                         (kv_len == 0 || (aligned_rows(k, kv_row_stride) && aligned_rows(v, kv_row_stride)));
     AttnArgs a{};
@@ -1538,7 +1536,10 @@ extern "C" hipError_t ql_paged_attention_f16(
     a.n_q_rows = n_q_rows;
     a.layer = layer;
     a.hd = head_dim;
-    if (!mfma_hd(head_dim)) return launch_small<true>(a, max_q_len, (unsigned)n_seqs, stream);
+    // narrow heads (a multiple of 8 below 64) with aligned rows: the head_dim-64
+    // kernels, zero-padded (the decode in one key split)
+    const bool narrow = narrow_hd(head_dim) && aligned_rows(q, q_row_stride) && aligned_rows(out, out_row_stride);
+    if (!mfma_hd(head_dim) && !narrow) return launch_small<true>(a, max_q_len, (unsigned)n_seqs, stream);
     if (max_q_len == 1) {   // every sequence decodes one token
         a.n_split = 1;
         return launch_decode<true>(a, head_dim, n_seqs, stream);
@@ -1599,7 +1600,7 @@ extern "C" hipError_t ql_decode_attention_f16(const uint16_t* q, const uint16_t*
     a.v = reinterpret_cast<const _Float16*>(v);
     a.kv_stride = kv_row_stride;
     a.hd = head_dim;
-    if (head_dim < 64 && head_dim % 8 == 0 && aligned_rows(q, qs) && aligned_rows(out, qs) &&
+    if (narrow_hd(head_dim) && aligned_rows(q, qs) && aligned_rows(out, qs) &&
         (kv_len == 0 || (aligned_rows(k, kv_row_stride) && aligned_rows(v, kv_row_stride)))) {
         a.n_split = 1;   // narrow heads on the head_dim-64 kernel, zero-padded: one pass, no workspace
         return launch_decode<false>(a, head_dim, 1, stream);
@@ -1687,6 +1688,10 @@ hipError_t paged_decode(
     a.n_q_rows = n_seqs;
     a.layer = layer;
     a.hd = head_dim;
+    if (narrow_hd(head_dim) && aligned_rows(q, q_row_stride) && aligned_rows(out, out_row_stride)) {
+        a.n_split = 1;   // narrow heads on the head_dim-64 kernel, zero-padded: one pass, no workspace
+        return launch_decode<true>(a, head_dim, n_seqs, stream);
+    }
     if (!mfma_hd(head_dim)) return launch_small<true>(a, 1, (unsigned)n_seqs, stream);   // no split
     int n_split = dec_splits(n_seqs, n_kv_heads, dec_col_chunks(n_heads, n_kv_heads), max_ctx_len);
     if (from_scratch) {

@@ -155,7 +155,7 @@ def test_attention_small_head_dim_strided_unaligned(q_len, kv_len, causal):
     check_attn(body[:, :h * d].reshape(q_len, h, d), want, v, f"head_dim 40 q={q_len} kv={kv_len}")
 
 
-@pytest.mark.parametrize("d", [16, 32, 48])
+@pytest.mark.parametrize("d", [16, 32, 48, 8, 56, 12, 20, 36])
 def test_paged_attention_small_head_dims(d):
     # prefill, decode and a chunk over permuted blocks with a hole in one table,
     # through ql_paged_attention_f16, then every sequence decoding through both
@@ -362,7 +362,7 @@ def test_paged_attention_skips_bad_rows_and_missing_blocks():
     check_attn(out.get((4, h, d)), orc.attention(q, kz, vz, h, hkv, True, f16=True), v, "holed table")
 
 
-@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("d", [64, 128, 32])
 def test_paged_prefill_tile_with_one_missing_page(d):
     # 200-token causal prefill over 13 permuted blocks whose table misses page 5
     # (keys 80..95, the second page of the second 64-key tile): in that tile one
@@ -389,7 +389,7 @@ def test_paged_prefill_tile_with_one_missing_page(d):
                f"d={d} tile with one missing page")
 
 
-@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("d", [64, 128, 24])
 def test_paged_attention_misaligned_block_pointers(d):
     # block pointers 2 bytes past a 16-byte boundary take the element-wise load
     # path: prefill and decode give the same bits as over an aligned pool, and
