@@ -14,13 +14,21 @@
 // converted by gfx950's v_cvt_pk_fp8_f32 / v_cvt_pk_bf8_f32 (round to nearest
 // even, subnormals) after saturating to +-fmax; decode by v_cvt_f32_fp8/bf8.
 //
+// Codec kernels: groups of 8..512 elements (powers of two) and other multiples of 8
+// below 256 quantize in one pass with several groups per wavefront; longer groups up
+// to 16384 in one pass with one wavefront (or a workgroup of 2-4) per group held in
+// registers; larger groups (per tensor) reduce workgroup maxima, then encode; lengths
+// that are not a multiple of 8 take a scales pass and 8 elements per thread, each
+// with its own group's scale.
+//
 // GEMM (quantlib_src/kernels/fp8_gemm.cu:34-139): C[M,N] = A[M,K] W'[N,K]^T with
-// W' the dequantized weights in binary16 and fp32 accumulation.  For few rows
-// (decode, M <= 64) the weights are streamed once, dequantized in registers and
-// fed to v_mfma_f32_16x16x32_f16 (C^T = W' A^T: 16 weight rows x up to 64 tokens
-// per workgroup, K split over its 4 wavefronts and summed in LDS); the in-register
-// dequant multiplies by 1/scale.  Larger M dequantizes into a workspace with the
-// codec and runs the fp16 library GEMM.
+// W' the dequantized weights in binary16 and fp32 accumulation.  For few rows the
+// weights are streamed once and dequantized in registers: 1-2 rows as a stream of
+// whole weight rows (v_dot2_f32_f16, no matrix cores), up to 8 rows by whole-row
+// loads into v_mfma_f32_16x16x32_f16, 33-64 rows by whole 128-byte lines re-laid
+// through LDS (C^T = W' A^T, K split over wavefronts and summed in LDS); the
+// in-register dequant multiplies by 1/scale or scales the fp32 sums.  Larger M
+// dequantizes into a workspace with the codec and runs the fp16 library GEMM.
 #include "ql_common.hpp"
 #include <type_traits>
 #include "quantlib_amd.h"
