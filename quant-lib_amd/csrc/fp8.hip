@@ -25,7 +25,8 @@
 // W' the dequantized weights in binary16 and fp32 accumulation.  For few rows the
 // weights are streamed once and dequantized in registers: 1-2 rows as a stream of
 // whole weight rows (v_dot2_f32_f16, no matrix cores), up to 8 rows by whole-row
-// loads into v_mfma_f32_16x16x32_f16, 33-64 rows by whole 128-byte lines re-laid
+// loads into v_mfma_f32_16x16x32_f16, up to 32 rows by the register kernel (each
+// lane 16 codes of a row per chunk), 33-64 rows by whole 128-byte lines re-laid
 // through LDS (C^T = W' A^T, K split over wavefronts and summed in LDS); the
 // in-register dequant multiplies by 1/scale or scales the fp32 sums.  Larger M
 // dequantizes into a workspace with the codec and runs the fp16 library GEMM.
