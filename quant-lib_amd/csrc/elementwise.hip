@@ -132,9 +132,11 @@ hipError_t launch_binary(const D* a, const D* b, D* out, long long n, hipStream_
 // loads and 16-byte stores, so a wavefront's store covers one contiguous 1 KiB
 // (16-byte loads and 32-byte stores per lane measured 4.6 TB/s against 6.2 on
 // MI355X, 64 Mi elements).
+// head > 0: src and dst were advanced past `head` (< kBlock) leading elements to
+// aligned addresses; block 0 also converts those.
 template <int W>
 __global__ __launch_bounds__(kBlock) void widen_stream(const _Float16* __restrict__ src,
-                                                       float* __restrict__ dst, long long n) {
+                                                       float* __restrict__ dst, long long n, int head = 0) {
     using VI = Vec<_Float16, W>;
     using VO = Vec<float, W>;
     const long long nvec = n / W;
@@ -156,8 +158,10 @@ __global__ __launch_bounds__(kBlock) void widen_stream(const _Float16* __restric
             store<(W > 1)>(reinterpret_cast<VO*>(dst) + i, y);
         }
     }
-    if (W > 1 && blockIdx.x == 0)
+    if (W > 1 && blockIdx.x == 0) {
         for (long long i = nvec * W + threadIdx.x; i < n; i += kBlock) dst[i] = (float)src[i];
+        if ((int)threadIdx.x < head) dst[(int)threadIdx.x - head] = (float)src[(int)threadIdx.x - head];
+    }
 }
 
 // fp32 -> binary16 narrowing, RNE (src/quant_forward.cu:18-21).  W = 4: 16-byte
@@ -165,9 +169,10 @@ __global__ __launch_bounds__(kBlock) void widen_stream(const _Float16* __restric
 // measured 6.34 TB/s on MI355X (64 Mi elements) against 6.06 for two 16-byte
 // loads and one 16-byte store per lane; one-wavefront workgroups (BS = 64)
 // a further 2.8%.
+// head: as widen_stream (< BS)
 template <int W, int BS = kBlock>
 __global__ __launch_bounds__(BS) void narrow_stream(const float* __restrict__ src,
-                                                        _Float16* __restrict__ dst, long long n) {
+                                                        _Float16* __restrict__ dst, long long n, int head = 0) {
     using VI = Vec<float, W>;
     using VO = Vec<_Float16, W>;
     const long long nvec = n / W;
@@ -189,9 +194,11 @@ __global__ __launch_bounds__(BS) void narrow_stream(const float* __restrict__ sr
             store<(W > 1)>(reinterpret_cast<VO*>(dst) + i, y);
         }
     }
-    if (W > 1 && blockIdx.x == 0)
-        for (long long i = nvec * W + threadIdx.x; i < n; i += BS)
-            dst[i] = from_f32<_Float16>(src[i]);
+    if (W > 1 && blockIdx.x == 0) {
+        for (long long i = nvec * W + threadIdx.x; i < n; i += BS) dst[i] = from_f32<_Float16>(src[i]);
+        if ((int)threadIdx.x < head)
+            dst[(int)threadIdx.x - head] = from_f32<_Float16>(src[(int)threadIdx.x - head]);
+    }
 }
 
 // Two independent copies in one launch (blockIdx.y selects the pair): the K
@@ -297,11 +304,20 @@ extern "C" hipError_t ql_f16_to_f32(const uint16_t* src, float* dst, int64_t n,
     if (n == 0) return hipSuccess;
     QL_CHECK_ARG(src && dst);
     const _Float16* s = reinterpret_cast<const _Float16*>(src);
-    if (((uintptr_t)src & 7u) == 0 && qlh::aligned16(dst)) {
+    // src and dst at one element offset mod 32 elements (element-aligned): the leading
+    // elements up to dst's next 128-byte boundary (src's 64-byte one) go to block 0
+    const uintptr_t ps = (uintptr_t)src, pd = (uintptr_t)dst;
+    const int head = (ps & 1) == 0 && (pd & 3) == 0 && (((ps >> 1) - (pd >> 2)) & 31) == 0
+                         ? (int)(((128 - (pd & 127)) & 127) / 4) : -1;
+    if (head >= 0 && n > head) {
+        const long long nb = n - head, nvec = nb / 4;
+        const unsigned grid = nvec > 0 ? qlh::blocks_for(nvec, (long long)kBlock * kUnroll) : 1;
+        hipLaunchKernelGGL((widen_stream<4>), dim3(grid), dim3(kBlock), 0, stream, s + head, dst + head, nb, head);
+    } else if ((ps & 7u) == 0 && qlh::aligned16(dst)) {
         const long long nvec = n / 4;
         const unsigned grid = nvec > 0 ? qlh::blocks_for(nvec, (long long)kBlock * kUnroll) : 1;
         hipLaunchKernelGGL((widen_stream<4>), dim3(grid), dim3(kBlock), 0, stream, s, dst,
-                           (long long)n);
+                           (long long)n, 0);
     } else {
         hipLaunchKernelGGL((widen_stream<1>), dim3(qlh::blocks_for(n, (long long)kBlock * kUnroll)),
                            dim3(kBlock), 0, stream, s, dst, (long long)n);
@@ -315,11 +331,20 @@ extern "C" hipError_t ql_f32_to_f16(const float* src, uint16_t* dst, int64_t n,
     if (n == 0) return hipSuccess;
     QL_CHECK_ARG(src && dst);
     _Float16* d = reinterpret_cast<_Float16*>(dst);
-    if (qlh::aligned16(src) && ((uintptr_t)dst & 7u) == 0) {
+    // as ql_f16_to_f32, src (fp32) advanced to its next 128-byte boundary
+    const uintptr_t ps = (uintptr_t)src, pd = (uintptr_t)dst;
+    const int head = (ps & 3) == 0 && (pd & 1) == 0 && (((ps >> 2) - (pd >> 1)) & 31) == 0
+                         ? (int)(((128 - (ps & 127)) & 127) / 4) : -1;
+    if (head >= 0 && n > head) {
+        const long long nb = n - head, nvec = nb / 4;
+        const unsigned grid = nvec > 0 ? qlh::blocks_for(nvec, (long long)kWave * kUnroll) : 1;
+        hipLaunchKernelGGL((narrow_stream<4, kWave>), dim3(grid), dim3(kWave), 0, stream, src + head, d + head, nb,
+                           head);
+    } else if (qlh::aligned16(src) && (pd & 7u) == 0) {
         const long long nvec = n / 4;
         const unsigned grid = nvec > 0 ? qlh::blocks_for(nvec, (long long)kWave * kUnroll) : 1;
         hipLaunchKernelGGL((narrow_stream<4, kWave>), dim3(grid), dim3(kWave), 0, stream, src, d,
-                           (long long)n);
+                           (long long)n, 0);
     } else {
         hipLaunchKernelGGL((narrow_stream<1>), dim3(qlh::blocks_for(n, (long long)kBlock * kUnroll)),
                            dim3(kBlock), 0, stream, src, d, (long long)n);

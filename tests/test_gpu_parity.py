@@ -752,12 +752,17 @@ def test_embed_empty_vocab_gives_zero_rows(f16, dim):
 
 
 # ---- fp16 -> fp32 ------------------------------------------------------------------------------
-# offsets in elements: 0 takes the 8-byte-load path, 4 (8-byte but not 16-byte aligned)
-# too, 1 the per-element path; n = 3 has no whole 4-element vector
-@pytest.mark.parametrize("offset,n", [(0, 65536), (0, 32000), (0, 13), (4, 32003), (1, 1001), (0, 3)])
-def test_f16_to_f32_bit_exact(offset, n):
+# offsets in elements (input, output): 0 takes the 8-byte-load path, 4 (8-byte but not
+# 16-byte aligned) too, 1 against 0 the per-element path; one offset for both: the
+# leading elements up to the output's next 128-byte boundary in block 0, then
+# vectors (fewer elements than that: the per-element path); n = 3 has no whole
+# 4-element vector
+@pytest.mark.parametrize("offset,n,out_offset", [(0, 65536, 0), (0, 32000, 0), (0, 13, 0), (4, 32003, 0),
+                                                 (1, 1001, 0), (0, 3, 0), (1, 1001, 1), (17, 5000, 17),
+                                                 (3, 20, 3), (5, 70001, 5)])
+def test_f16_to_f32_bit_exact(offset, n, out_offset):
     h = (np.arange(n, dtype=np.uint32) * 7 % 65536).astype(np.uint16)
-    out = Out(n, np.float32)
+    out = Out(n, np.float32, offset=out_offset)
     dh = dev(h, offset)
     ql.call("ql_f16_to_f32", ptr(dh), out.ptr, n, stream())
     got, want = out.get(), orc.f16_to_f32(h)
@@ -778,9 +783,12 @@ def _narrow_inputs():
 
 
 # (input offset, n, output offset) in elements: 16-byte-aligned input with an
-# 8-byte-aligned output takes the vector path, offset 1 the per-element path
+# 8-byte-aligned output takes the vector path; one offset for both the leading
+# elements up to the input's next 128-byte boundary in block 0, then vectors;
+# different offsets otherwise the per-element path
 @pytest.mark.parametrize("offset,n,out_offset", [(0, None, 0), (1, 1001, 1), (0, 13, 0), (0, 4099, 4),
-                                                 (4, 2001, 4), (0, 3, 0)])
+                                                 (4, 2001, 4), (0, 3, 0), (31, 70001, 31), (2, 10, 2),
+                                                 (1, 1001, 0)])
 def test_f32_to_f16_bit_exact(offset, n, out_offset):
     x = _narrow_inputs()
     if n is not None:
