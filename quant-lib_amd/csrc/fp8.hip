@@ -171,11 +171,19 @@ __global__ __launch_bounds__(kBlock) void absmax_vec(const _Float16* __restrict_
     }
 }
 
+// Groups of the block-strided kernels along grid y (at most 65535) and z.
+constexpr unsigned kGroupsY = 65535;
+inline dim3 group_grid(unsigned bx, int n_groups) {
+    const unsigned gy = (unsigned)std::min<long long>(n_groups, kGroupsY);
+    return dim3(bx, gy, (unsigned)(((long long)n_groups + kGroupsY - 1) / kGroupsY));
+}
+
 // large groups: blocks stride their group and combine with an atomic max on the
 // bit pattern (non-negative floats order like their bits); mx pre-zeroed
 __global__ __launch_bounds__(kBlock) void absmax_blocks(const _Float16* __restrict__ x, Geom g,
                                                         int mode, float* __restrict__ mx) {
-    const long long grp = blockIdx.y;
+    const long long grp = (long long)blockIdx.z * kGroupsY + blockIdx.y;   // grid y x z covers the groups
+    if (grp >= g.n_groups) return;   // workgroup-uniform, before any barrier
     const long long base = grp * g.gs;
     const long long len = min(g.gs, g.n - base);
     float m = 0.0f;
@@ -212,7 +220,8 @@ __host__ __device__ inline long long seen_vectors(int mode, long long nv) {
 template <bool PARTIAL = false>
 __global__ __launch_bounds__(kBlock) void absmax_blocks_vec(const _Float16* __restrict__ x, Geom g,
                                                             int mode, float* __restrict__ mx) {
-    const long long grp = blockIdx.y;
+    const long long grp = (long long)blockIdx.z * kGroupsY + blockIdx.y;   // grid y x z covers the groups
+    if (grp >= g.n_groups) return;   // workgroup-uniform, before any barrier
     const long long base = grp * g.gs;
     const long long nt = seen_vectors(mode, min(g.gs, g.n - base) / 8);
     const Vec<_Float16, 8>* xv = reinterpret_cast<const Vec<_Float16, 8>*>(x + base);
@@ -2072,20 +2081,19 @@ extern "C" hipError_t ql_fp8_scales(const uint16_t* src, int rows, int cols, int
         hipLaunchKernelGGL(absmax_wave, dim3(qlh::blocks_for(g.n_groups, kBlock / kWave)), dim3(kBlock),
                            0, stream, x, g, mode, scales);
     } else {
-        QL_CHECK_ARG(g.n_groups <= 65535);
         hipLaunchKernelGGL(fill_zero, dim3(sblocks), dim3(kBlock), 0, stream, scales, g.n_groups);
         if (vec && g.gs % 8 == 0) {
             // workgroups of one group end in atomics on one address, which serialize:
             // at most kAbsBlocks workgroups in all, each looping over its share
             const long long want = qlh::blocks_for(seen_vectors(mode, g.gs / 8), (long long)kBlock * kBlockIters);
             const unsigned bx = (unsigned)std::max(1LL, std::min(want, kAbsBlocks / g.n_groups));
-            hipLaunchKernelGGL(absmax_blocks_vec<false>, dim3(bx, (unsigned)g.n_groups), dim3(kBlock), 0, stream, x,
+            hipLaunchKernelGGL(absmax_blocks_vec<false>, group_grid(bx, g.n_groups), dim3(kBlock), 0, stream, x,
                                g, mode, scales);
         } else {
             const long long per = 16LL * kBlock;
             unsigned bx = (unsigned)((g.gs + per - 1) / per);
             if (bx > 1024) bx = 1024;
-            hipLaunchKernelGGL(absmax_blocks, dim3(bx, (unsigned)g.n_groups), dim3(kBlock), 0, stream, x, g,
+            hipLaunchKernelGGL(absmax_blocks, group_grid(bx, g.n_groups), dim3(kBlock), 0, stream, x, g,
                                mode, scales);
         }
     }
@@ -2120,7 +2128,7 @@ extern "C" hipError_t ql_fp8_quantize(const uint16_t* src, int rows, int cols, i
         return hipGetLastError();
     }
     if (src && scales && g.n % 8 == 0 && g.gs % 8 == 0 && g.gs > 8LL * kWave * kWaveGroupVecs &&
-        g.n_groups <= 65535 && qlh::aligned16(src) && ((uintptr_t)dst & 7) == 0) {
+        qlh::aligned16(src) && ((uintptr_t)dst & 7) == 0) {
         // groups too large for one wavefront (per tensor): the workgroups' maxima go to
         // the front of dst (at most kAbsBlocks floats, or one per group; n > 16384
         // bytes), one workgroup per group reduces them into the scale, then the codes
@@ -2129,7 +2137,7 @@ extern "C" hipError_t ql_fp8_quantize(const uint16_t* src, int rows, int cols, i
             qlh::blocks_for(seen_vectors(mode, g.gs / 8), (long long)kBlock * kBlockIters);
         const unsigned bx = (unsigned)std::max(1LL, std::min(want, kAbsBlocks / g.n_groups));
         float* part = reinterpret_cast<float*>(dst);
-        hipLaunchKernelGGL(absmax_blocks_vec<true>, dim3(bx, (unsigned)g.n_groups), dim3(kBlock), 0, stream,
+        hipLaunchKernelGGL(absmax_blocks_vec<true>, group_grid(bx, g.n_groups), dim3(kBlock), 0, stream,
                            reinterpret_cast<const _Float16*>(src), g, mode, part);
         hipLaunchKernelGGL(reduce_partials, dim3((unsigned)g.n_groups), dim3(kBlock), 0, stream, part, (int)bx,
                            fp8_max(format), scales);

@@ -179,3 +179,26 @@ def test_fp8_per_tensor_quantize_and_dequantize_beyond_2_31_elements(mode):
     y_want = orc.fp8_dequantize(q_want, sc_want, ql.FP8_E4M3, ql.QUANT_PER_TENSOR, 0, mode)
     for r0, r1 in _windows(rows, C):
         assert np.array_equal(_rows(y, r0, r1, C), y_want[np.arange(r0, r1) % TILE]), f"dequant rows {r0}..{r1}"
+
+
+@pytest.mark.parametrize("mode", [ql.FP8_MODE_REFERENCE, ql.FP8_MODE_OCP])
+def test_fp8_quantize_more_groups_than_a_grid_dimension(mode):
+    # per channel with rows longer than one wavefront's group (16392 > 16384) and
+    # more rows than grid y holds (65535): the block-strided maxima take grid z too
+    C = 16392
+    rows = 65535 + 101
+    x = to_f16_bits(uniform(0x5AE, (TILE, C), -2.0, 2.0))
+    dx = _tiled(x, rows)
+    q = ql.DeviceArray((rows * C,), np.uint8)
+    sc = ql.DeviceArray((rows,), np.float32)
+    ql.call("ql_fp8_quantize", dx.ptr, rows, C, ql.FP8_E4M3, ql.QUANT_PER_CHANNEL, 0, mode, q.ptr, sc.ptr, stream())
+    synchronize()
+    q_want, sc_want = orc.fp8_quantize(x, ql.FP8_E4M3, ql.QUANT_PER_CHANNEL, 0, mode)
+    assert np.array_equal(sc.numpy(), sc_want[np.arange(rows) % TILE])
+    for r0, r1 in [(0, 4), (65533, 65539), (rows - 4, rows)]:
+        assert np.array_equal(_rows(q, r0, r1, C), q_want[np.arange(r0, r1) % TILE]), f"codes rows {r0}..{r1}"
+    # the scales entry alone (block-strided maxima with atomics, then finalized)
+    sc2 = ql.DeviceArray((rows,), np.float32)
+    ql.call("ql_fp8_scales", dx.ptr, rows, C, ql.FP8_E4M3, ql.QUANT_PER_CHANNEL, 0, mode, sc2.ptr, stream())
+    synchronize()
+    assert np.array_equal(sc2.numpy(), sc_want[np.arange(rows) % TILE])
